@@ -1,0 +1,332 @@
+"""S-X8 hot-path benchmark on one MI355X: decode GEMV sweep (headline), fused prefill
+GEMM at M = 2048, embedding gather, plus the CPU dequant+GEMV baseline.
+
+Headline (BASELINE.json metric, configs[1]): one step = the M = 1 decode GEMV of every
+linear of one synthetic Qwen3-4B-class layer (q 4096x2560, k/v 1024x2560,
+o 2560x4096, gate/up 9728x2560, down 2560x9728), weights N(0, 0.02) per seed quantized
+to S-X8 with 1% degenerate blocks, x ~ N(0, 1) fp16.  `value` = packed-weight bytes
+(30 B per 32 weights) of the step / step time, in GB/s.  Inputs are resident in HBM
+before timing; the step cycles through --copies distinct copies of the layer (>1 GB in
+total by default) so the 256 MB Infinity Cache cannot serve repeats.
+
+Timing: a GPU delay kernel is queued first so the host enqueues the whole timed
+region ahead of the GPU; each GEMV is bracketed by HIP events on the launch stream
+(torch's current stream, which the kernels are launched on), giving the per-launch
+kernel durations of the roofline; start/end events bracket the K steps.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "sx8-quantization_amd")
+sys.path.insert(0, PKG)
+
+LAYER = [  # (name, N, K)
+    ("q_proj", 4096, 2560), ("k_proj", 1024, 2560), ("v_proj", 1024, 2560),
+    ("o_proj", 2560, 4096), ("gate_proj", 9728, 2560), ("up_proj", 9728, 2560),
+    ("down_proj", 2560, 9728),
+]
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, vendor figure
+
+
+def packed_bytes(N, K):
+    return N * ((K + 31) // 32) * 30
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--copies", type=int, default=12, help="distinct layer copies (cold cache)")
+    ap.add_argument("--hdr-bytes", type=int, default=6, choices=[6, 8])
+    ap.add_argument("--prefill-m", type=int, default=2048)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|embed")
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gpu_delay(torch, ms):
+    """Queue roughly `ms` of GPU work so the host can enqueue a timed region ahead of
+    the GPU (a bounded clock spin; falls back to large fills)."""
+    try:
+        torch.cuda._sleep(int(ms * 2.0e6))
+    except Exception:
+        buf = torch.empty(64 << 20, dtype=torch.float32, device="cuda")
+        for _ in range(max(1, int(ms / 0.1))):
+            buf.fill_(1.0)
+
+
+def build_layer(torch, dev, hdr_bytes):
+    from prepare_v44 import to_v44_device
+    from quantize_sx8 import quantize_tensor
+    layer = []
+    for i, (name, N, K) in enumerate(LAYER):
+        seed = 1000 + i
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        W = (torch.randn(N, K, generator=g) * 0.02).half()
+        qt, bi = quantize_tensor(W, device=dev, degenerate_frac=0.01, seed=seed + 1)
+        hdr, lvl, bas, sca = to_v44_device(qt, bi, hdr_aligned=(hdr_bytes == 8), device=dev)
+        layer.append({"name": name, "N": N, "K": K, "n_cb": qt["n_cb"], "qt": qt, "bi": bi,
+                      "hdr": hdr, "lvl": lvl, "bas": bas, "sca": sca})
+        log(f"quantized {name} {N}x{K}")
+    return layer
+
+
+def bench_gemv(torch, L, layer, args):
+    import ctypes
+    dev = torch.device("cuda:0")
+    R = max(1, args.copies)
+    copies = [[(t["hdr"].clone(), t["lvl"].clone()) for t in layer] for _ in range(R)]
+    copies[0] = [(t["hdr"], t["lvl"]) for t in layer]
+    g = torch.Generator(device="cpu").manual_seed(2)
+    xs = {K: torch.randn(K, generator=g).half().to(dev) for K in {t["K"] for t in layer}}
+    ys = [torch.empty(t["N"], dtype=torch.float32, device=dev) for t in layer]
+    zs = [torch.empty(t["n_cb"], 2, dtype=torch.float32, device=dev) for t in layer]
+    st = L.stream(dev)
+    calls = []
+    for r in range(R):
+        step = []
+        for i, t in enumerate(layer):
+            h, lv = copies[r][i]
+            step.append((L.ptr(xs[t["K"]]), L.ptr(h), L.ptr(lv), args.hdr_bytes, L.ptr(t["bas"]),
+                         L.ptr(t["sca"]), ctypes.c_void_p(None), L.ptr(zs[i]), t["N"], t["n_cb"],
+                         L.ptr(ys[i]), st))
+        calls.append(step)
+    fn = L.lib().sx8_gemv
+    step_bytes = sum(packed_bytes(t["N"], t["K"]) for t in layer)
+    log(f"gemv: {R} copies x {step_bytes / 1e6:.1f} MB = {R * step_bytes / 1e9:.2f} GB resident")
+
+    def run_step(s, evs=None):
+        for i, a in enumerate(calls[s % R]):
+            if evs is not None:
+                evs[2 * i].record()
+            rc = fn(*a)
+            if rc != 0:
+                raise RuntimeError(L.lib().sx8_last_error().decode())
+            if evs is not None:
+                evs[2 * i + 1].record()
+
+    for s in range(args.warmup):
+        run_step(s)
+    torch.cuda.synchronize()
+
+    K = args.steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * len(layer))] for _ in range(K)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    gpu_delay(torch, 50)                     # keep the GPU busy while the host enqueues
+    start.record()
+    for s in range(K):
+        run_step(s, evs[s])
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    per_shape_ms = [0.0] * len(layer)
+    for s in range(K):
+        for i in range(len(layer)):
+            per_shape_ms[i] += evs[s][2 * i].elapsed_time(evs[s][2 * i + 1])
+    kern_ms = sum(per_shape_ms)
+    out = {
+        "ms_per_step": total_ms / K,
+        "value_gbs": step_bytes * K / (total_ms * 1e-3) / 1e9,
+        "kernel_ms_total": kern_ms,
+        "launches": K * len(layer),
+        "avg_launch_us": kern_ms * 1e3 / (K * len(layer)),
+        "bytes_per_launch": step_bytes / len(layer),
+        "achieved_gbs": step_bytes * K / (kern_ms * 1e-3) / 1e9,
+        "per_shape": {t["name"]: {
+            "us": per_shape_ms[i] * 1e3 / K,
+            "gbs": packed_bytes(t["N"], t["K"]) / (per_shape_ms[i] * 1e-3 / K) / 1e9}
+            for i, t in enumerate(layer)},
+        "step_bytes": step_bytes,
+    }
+    return out
+
+
+def bench_prefill(torch, L, layer, args):
+    dev = torch.device("cuda:0")
+    M = args.prefill_m
+    g = torch.Generator(device="cpu").manual_seed(12)
+    xs = {K: torch.randn(M, K, generator=g).half().to(dev) for K in {t["K"] for t in layer}}
+    ys = [torch.empty(M, t["N"], dtype=torch.float32, device=dev) for t in layer]
+    st = L.stream(dev)
+    fn = L.lib().sx8_gemm_prefill
+
+    def one(i, t):
+        rc = fn(L.ptr(xs[t["K"]]), M, t["K"], t["K"], L.ptr(t["hdr"]), L.ptr(t["lvl"]),
+                args.hdr_bytes, L.ptr(t["bas"]), L.ptr(t["sca"]), t["N"], t["n_cb"],
+                L.ptr(ys[i]), st)
+        if rc != 0:
+            raise RuntimeError(L.lib().sx8_last_error().decode())
+
+    for i, t in enumerate(layer):
+        one(i, t)
+    torch.cuda.synchronize()
+    reps = 5
+    res = {}
+    tot_flop, tot_ms = 0.0, 0.0
+    for i, t in enumerate(layer):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        gpu_delay(torch, 10)
+        a.record()
+        for _ in range(reps):
+            one(i, t)
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / reps
+        flop = 2.0 * M * t["N"] * t["K"]
+        res[t["name"]] = {"us": ms * 1e3, "tflops": flop / (ms * 1e-3) / 1e12}
+        tot_flop += flop
+        tot_ms += ms
+        log(f"prefill {t['name']} M={M}: {ms * 1e3:.1f} us {res[t['name']]['tflops']:.1f} TFLOP/s")
+    return {"M": M, "tflops": tot_flop / (tot_ms * 1e-3) / 1e12, "per_shape": res,
+            "frac_of_mfma_peak": tot_flop / (tot_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS}
+
+
+def bench_embed(torch, L, layer, args):
+    """Row gather of 512 ids from the largest layer matrix (gate_proj, 9728 rows)."""
+    dev = torch.device("cuda:0")
+    t = max(layer, key=lambda t: t["N"])
+    g = torch.Generator(device="cpu").manual_seed(3)
+    ids = torch.randint(0, t["N"], (512,), generator=g).to(dev)
+    out = torch.empty(512, t["K"], dtype=torch.float16, device=dev)
+    st = L.stream(dev)
+    args_ = (L.ptr(ids), 512, L.ptr(t["hdr"]), L.ptr(t["lvl"]), args.hdr_bytes, L.ptr(t["bas"]),
+             L.ptr(t["sca"]), t["K"], t["N"], t["n_cb"], L.ptr(out), st)
+    fn = L.lib().sx8_embed_gather
+    fn(*args_)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gpu_delay(torch, 10)
+    a.record()
+    for _ in range(20):
+        fn(*args_)
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / 20
+    rd = 512 * t["n_cb"] * 30
+    wr = 512 * t["K"] * 2
+    return {"table": f"{t['N']}x{t['K']}", "ids": 512, "us": us, "gbs": (rd + wr) / (us * 1e-6) / 1e9}
+
+
+def cpu_baseline(layer, seconds):
+    """The oracle's C restatement (R64 dequant to fp16 + fp32 GEMV, OpenMP) on the host,
+    over as many layer shapes as fit in about `seconds`."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+    O.build()
+    lib = O.lib()
+    threads = int(lib.sx8o_num_threads())
+    done_bytes, t_dq, t_gv, names = 0, 0.0, 0.0, []
+    rng = np.random.default_rng(2)
+    for t in layer:
+        qt, bi = t["qt"], t["bi"]
+        n_blk, dmin, dmax, cfg, cof, hi, lo = O._fields(qt)
+        data, sc = O._bases(bi)
+        w16 = np.empty(n_blk * 32, dtype=np.uint16)
+        x = rng.standard_normal(t["K"]).astype(np.float16).view(np.uint16)
+        y = np.empty(t["N"], dtype=np.float32)
+        t0 = time.perf_counter()
+        lib.sx8o_dequant_r64(n_blk, qt["n_cb"], O._ptr(dmin), O._ptr(dmax), O._ptr(cfg),
+                             O._ptr(cof), O._ptr(hi), O._ptr(lo), O._ptr(data), O._ptr(sc), 1,
+                             O._ptr(w16), None)
+        t1 = time.perf_counter()
+        lib.sx8o_gemv_f32(t["N"], t["K"], qt["n_cb"] * 32, O._ptr(w16), O._ptr(x), O._ptr(y))
+        t2 = time.perf_counter()
+        t_dq += t1 - t0
+        t_gv += t2 - t1
+        done_bytes += packed_bytes(t["N"], t["K"])
+        names.append(t["name"])
+        if t_dq + t_gv > seconds:
+            break
+    tot = t_dq + t_gv
+    return {"value": done_bytes / tot / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"R64 dequant + fp32 GEMV of {len(names)} layer shapes "
+                      f"({','.join(names)}; {done_bytes / 1e6:.1f} MB packed) "
+                      f"in {tot:.1f} s (dequant {t_dq:.1f} s, GEMV {t_gv:.1f} s)"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
+              "multi-GPU path (see DESIGN.md, 'sharding')", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import _sx8lib as L
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    L.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t0 = time.time()
+    layer = build_layer(torch, dev, args.hdr_bytes)
+    log(f"setup {time.time() - t0:.1f}s")
+    res = {}
+    if args.only in ("", "gemv"):
+        res["gemv"] = bench_gemv(torch, L, layer, args)
+        log("gemv", json.dumps(res["gemv"]))
+    if args.only in ("", "prefill") and not args.no_prefill:
+        res["prefill"] = bench_prefill(torch, L, layer, args)
+    if args.only in ("", "embed"):
+        res["embed"] = bench_embed(torch, L, layer, args)
+        log("embed", json.dumps(res["embed"]))
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(layer, args.cpu_seconds)
+        log("cpu", json.dumps(cpu))
+    gv = res.get("gemv", {})
+    line = {
+        "metric": "S-X8 decode GEMV GB/s (packed weights) @M=1, Qwen3-4B-class layer sweep",
+        "value": round(gv.get("value_gbs", 0.0), 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gv.get("ms_per_step", 0.0), 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 accumulate over fp16 activations x S-X8 (u8) weights",
+        "data": "synthetic: N(0,0.02) weights quantized to S-X8 v4.3 (1% degenerate blocks), x~N(0,1)",
+        "config": {
+            "workload": "decode GEMV M=1 over one Qwen3-4B-class layer (q,k,v,o,gate,up,down), "
+                        f"{args.copies} distinct copies rotated (cold cache), hdr_bytes={args.hdr_bytes}",
+            "shapes": {n: f"{N}x{K}" for n, N, K in LAYER},
+            "step_bytes": gv.get("step_bytes"),
+            "per_shape": gv.get("per_shape"),
+            "frac_of_hbm_peak": round(gv.get("value_gbs", 0.0) / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "kernel": "k_gemv<6,false> (sx8_gemv)" if args.hdr_bytes == 6 else "k_gemv<8,false>",
+            "bound": "hbm",
+            "achieved": round(gv.get("achieved_gbs", 0.0), 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gv.get("achieved_gbs", 0.0) / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(gv.get("avg_launch_us", 0.0), 3),
+            "bytes_per_launch": gv.get("bytes_per_launch"),
+        },
+        "cpu_baseline": cpu,
+        "prefill": res.get("prefill"),
+        "embed": res.get("embed"),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,128 @@
+/*
+ * sx8_hip.h -- C ABI of libsx8_hip.so, the MI355X (gfx950) implementation of the
+ * S-X8 v4.3 weight-dequantization hot path.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer on the current HIP device unless stated.
+ *   - fp16 tensors are passed as uint16_t bit patterns; no HIP or torch types appear
+ *     in the signatures except the stream, passed as an opaque void* (a hipStream_t;
+ *     NULL means the legacy default stream).
+ *   - Every entry point enqueues work on `stream`, never synchronises the device and
+ *     returns SX8_OK or an error code; sx8_last_error() then holds a message.
+ *   - Argument checks (null pointers, sizes, hdr_bytes, alignment) happen on the
+ *     host before any launch, so an invalid call never reaches the GPU.
+ *
+ * Block layouts (reference paths are relative to the reference repository):
+ *   split arrays, pkl/container order ("n-major", bid = n*n_cb + kb):
+ *       dmin/dmax fp16 (n_blk), config u8 (n_blk), coeff u8 (n_blk),
+ *       levels_hi u8 (n_blk*16), levels_lo u8 (n_blk*8)
+ *       -- scripts/sx8_container_v43.py:30-35, scripts/kernel_sx8_v43.py:14-51
+ *   v4.4 kb-major (bid = kb*N + n): hdr u8 (n_blk, hdr_bytes in {6,8}) =
+ *       dmin|dmax|config|coeff(|pad), levels u8 (n_blk, 24) = qh[16]|ql[8]
+ *       -- scripts/prepare_v44.py:35-79
+ *   kb-major split arrays (the fused-WMMA form, scripts/integrate_fused.py:46-58):
+ *       the split arrays above re-ordered to bid = kb*N + n.
+ *   PCA side tables: basis f32 (n_cb, 64) = [b0 | b1], scales f32 (n_cb, 2).
+ */
+#ifndef SX8_HIP_H
+#define SX8_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SX8_ABI_VERSION 1
+
+#define SX8_OK 0
+#define SX8_ERR_INVALID 1      /* bad argument (null pointer, size, hdr_bytes, alignment) */
+#define SX8_ERR_HIP 2          /* HIP runtime error (launch or allocation) */
+#define SX8_ERR_UNSUPPORTED 3  /* shape outside what the kernels support */
+
+/* ABI version of the loaded library (SX8_ABI_VERSION at build time). */
+int32_t sx8_abi_version(void);
+
+/* Message for the last error returned on the calling thread ("" if none). */
+const char* sx8_last_error(void);
+
+/* Canonical R64 dequant to fp16, split arrays in pkl order.
+ * Replaces kernel_sx8_v43.decode_tensor_gpu_fast (scripts/kernel_sx8_v43.py:109-145)
+ * and its numba kernel sx8_v43_kernel (:14-51).  out is (out_f, in_f) row-major fp16;
+ * columns in_f .. n_cb*32-1 of the padded block grid are dropped.  Bit-exact. */
+int32_t sx8_dequant_f16(const uint16_t* dmin, const uint16_t* dmax, const uint8_t* config,
+                        const uint8_t* coeff, const uint8_t* levels_hi,
+                        const uint8_t* levels_lo, const float* basis, const float* scales,
+                        int64_t out_f, int64_t in_f, int64_t n_cb, uint16_t* out,
+                        void* stream);
+
+/* R64 dequant of selected rows from the v4.4 kb-major layout:
+ *   out[t, :] = W16[ids[t], :]  for t < T (ids int64; ids outside [0, N) leave row t
+ *   unwritten).  ids == NULL means ids[t] = t with T = N (whole-tensor dequant).
+ * Replaces sx8_embed_v44 (cuda/sx8_embed_v44.cu:80-94, kernel :21-78), which computed
+ * the rows in float32; this one is bit-exact to the canonical dequant.
+ * out is (T, K) row-major fp16. */
+int32_t sx8_embed_gather(const int64_t* ids, int64_t T, const uint8_t* hdr,
+                         const uint8_t* levels, int32_t hdr_bytes, const float* basis,
+                         const float* scales, int64_t K, int64_t N, int64_t n_cb,
+                         uint16_t* out, void* stream);
+
+/* PCA precompute Z[m, kb, j] = scales[kb, j] * sum_t X[m, kb*32+t] * basis[kb, 32j+t]
+ * for m < M, in float32 with the reference's summation tree.
+ * Replaces compute_z44 (cuda/sx8_decode1_v3.cu:185-195, kernel :44-65) for M = 1 and
+ * compute_z44_batch (cuda/sx8_gemm_compact.cu:157-169, kernel :28-50) for M > 1.
+ * X is (M, ldx) fp16 with ldx >= n_cb*32.  Z is (M, n_cb, 2) float32. */
+int32_t sx8_compute_z(const uint16_t* X, int64_t M, int64_t ldx, const float* basis,
+                      const float* scales, int64_t n_cb, float* Z, void* stream);
+
+/* M = 1 decode GEMV on the v4.4 layout: Y[n] = sum_k X[k] W[n, k], float32 result.
+ * If Z_in != NULL it is used as the PCA precompute (n_cb, 2) (the two-launch form,
+ * decode1_v44 at cuda/sx8_decode1_v3.cu:197-221); otherwise Z is computed inside the
+ * launch from basis/scales and, when Z_out != NULL, also written there (the combined
+ * form, decode1_v44_combined at :223-246).  X holds n_cb*32 fp16 values.
+ * Tolerance against the float64 yardstick: max|dY| / max|Y| <= 1e-3. */
+int32_t sx8_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels,
+                 int32_t hdr_bytes, const float* basis, const float* scales,
+                 const float* Z_in, float* Z_out, int64_t N, int64_t n_cb, float* Y,
+                 void* stream);
+
+/* Prefill GEMM Y (M, N) float32 = X (M, ldx) fp16 . W^T on the v4.4 layout.
+ * Each weight tile is dequantized with R64 (bit-exact fp16) into MFMA operands and
+ * accumulated in float32 (v_mfma_f32_16x16x32_f16).  Columns k >= K of X are never
+ * read; the kernel zero-fills the padded tail of the last K block.
+ * Replaces gemm_compact (cuda/sx8_gemm_compact.cu:171-194, kernel :55-152) together
+ * with its Z precompute: the PCA term is applied per weight instead. */
+int32_t sx8_gemm_prefill(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
+                         const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
+                         const float* basis, const float* scales, int64_t N, int64_t n_cb,
+                         float* Y, void* stream);
+
+/* Same GEMM from kb-major split arrays (dmin/dmax fp16, config, coeff, hi (n_blk*16),
+ * lo (n_blk*8), all in bid = kb*N + n order).
+ * Replaces fused_forward (cuda/sx8_fused_wmma.cu:134-154, kernel :11-132). */
+int32_t sx8_gemm_prefill_split(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
+                               const uint16_t* dmin, const uint16_t* dmax,
+                               const uint8_t* config, const uint8_t* coeff,
+                               const uint8_t* hi, const uint8_t* lo, const float* basis,
+                               const float* scales, int64_t N, int64_t n_cb, float* Y,
+                               void* stream);
+
+/* Output-side PCA GEMM: Y[m, n] += sum_kb c0(kb,n) Z[m,kb,0] + c1(kb,n) Z[m,kb,1],
+ * c0/c1 the signed nibbles of the coeff byte in the v4.4 header.  Together with
+ * sx8_gemm_prefill_core it forms the reference's gemm_compact(X, hdr, levels, Z, ...)
+ * contract (cuda/sx8_gemm_compact.cu:171-194), whose PCA term comes from a
+ * caller-supplied Z. */
+int32_t sx8_gemm_pca_z(const float* Z, int64_t M, const uint8_t* hdr, int32_t hdr_bytes,
+                       int64_t N, int64_t n_cb, float* Y, void* stream);
+
+/* Prefill GEMM of the PCA-free core weights (rlo + step*lv, R64 without the two PCA
+ * terms), used with sx8_gemm_pca_z for the caller-supplied-Z contract. */
+int32_t sx8_gemm_prefill_core(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
+                              const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
+                              int64_t N, int64_t n_cb, float* Y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SX8_HIP_H */

@@ -1,0 +1,138 @@
+"""ctypes binding of libsx8_hip.so, the gfx950 HIP library behind every wrapper here.
+
+The library is built in-tree (``build()`` drives hipcc) and loaded from this
+directory, or from the path in the SX8_HIP_LIB environment variable.  There is no
+fallback: if the library cannot be loaded, every GPU entry point raises
+RuntimeError.  The C signatures are declared in include/sx8_hip.h.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+import threading
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+CSRC_DIR = os.path.join(PKG_DIR, "csrc")
+INCLUDE_DIR = os.path.join(REPO_DIR, "include")
+LIB_NAME = "libsx8_hip.so"
+LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+SOURCES = ["sx8_abi.hip", "sx8_dequant.hip", "sx8_gemv.hip", "sx8_gemm.hip"]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# hipcc flags: gfx950 only, no packed-fp32 instruction selection (those forms have
+# given silent wrong results on the target pool), IEEE denormals, no fast-math.
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fno-fast-math", "-fno-gpu-flush-denormals-to-zero",
+    "-Wall", "-Wno-unused-function",
+]
+
+# (name, restype, argtypes) for every exported symbol of include/sx8_hip.h
+_P = ctypes.c_void_p
+_I32, _I64 = ctypes.c_int32, ctypes.c_int64
+SIGNATURES = [
+    ("sx8_abi_version", _I32, []),
+    ("sx8_last_error", ctypes.c_char_p, []),
+    ("sx8_dequant_f16", _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P]),
+    ("sx8_embed_gather", _I32, [_P, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _P, _P]),
+    ("sx8_compute_z", _I32, [_P, _I64, _I64, _P, _P, _I64, _P, _P]),
+    ("sx8_gemv", _I32, [_P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _P, _P]),
+    ("sx8_gemm_prefill", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P]),
+    ("sx8_gemm_prefill_split", _I32,
+     [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P]),
+    ("sx8_gemm_pca_z", _I32, [_P, _I64, _P, _I32, _I64, _I64, _P, _P]),
+    ("sx8_gemm_prefill_core", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _I64, _I64, _P, _P]),
+]
+ABI_VERSION = 1
+
+_lib = None
+_lock = threading.Lock()
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every HIP source into LIB_PATH with hipcc for gfx950 (always rebuilds)."""
+    srcs = [os.path.join(CSRC_DIR, s) for s in SOURCES]
+    tmp = LIB_PATH + ".tmp"
+    cmd = [HIPCC, *HIP_FLAGS, "-I", CSRC_DIR, "-I", INCLUDE_DIR, "-o", tmp, *srcs]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + res.stdout + res.stderr)
+    if verbose:
+        print(res.stderr)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+def lib_path() -> str:
+    return os.environ.get("SX8_HIP_LIB", LIB_PATH)
+
+
+def lib():
+    """Load the HIP library once; raise RuntimeError if it is missing or stale."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            path = lib_path()
+            if not os.path.exists(path):
+                raise RuntimeError(f"S-X8 HIP library not found at {path}; run "
+                                   "__graft_entry__.build() (or _sx8lib.build()) first")
+            L = ctypes.CDLL(path)
+            for name, res, args in SIGNATURES:
+                fn = getattr(L, name)
+                fn.restype = res
+                fn.argtypes = args
+            if L.sx8_abi_version() != ABI_VERSION:
+                raise RuntimeError(f"{path}: ABI version {L.sx8_abi_version()} != {ABI_VERSION}")
+            _lib = L
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point and raise RuntimeError with the library's message on error."""
+    L = lib()
+    rc = getattr(L, name)(*args)
+    if rc != 0:
+        msg = L.sx8_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed (code {rc}): {msg}")
+
+
+def ptr(t) -> ctypes.c_void_p:
+    """Device pointer of a torch tensor (None -> NULL)."""
+    if t is None:
+        return ctypes.c_void_p(None)
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream(device=None) -> ctypes.c_void_p:
+    """The current torch stream on `device` as a hipStream_t."""
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def as_device(a, np_dtype, device):
+    """numpy array / torch tensor -> contiguous 1-D torch tensor of np_dtype on device.
+    A device tensor of the right dtype is used as is (no copy)."""
+    import numpy as np
+    import torch
+    tdt = {np.uint8: torch.uint8, np.uint16: torch.int16, np.float16: torch.float16,
+           np.float32: torch.float32, np.int64: torch.int64}[np_dtype]
+    if isinstance(a, torch.Tensor):
+        t = a.reshape(-1)
+        if t.dtype != tdt:
+            if np_dtype is np.uint16 and t.dtype == torch.float16:
+                t = t.view(torch.int16)
+            else:
+                t = t.to(tdt)
+        return t.to(device).contiguous()
+    arr = np.ascontiguousarray(np.asarray(a).reshape(-1))
+    if np_dtype is np.uint16 and arr.dtype == np.float16:
+        arr = arr.view(np.uint16)
+    arr = arr.astype(np_dtype, copy=False)
+    if np_dtype is np.uint16:
+        arr = arr.view(np.int16)
+    return torch.from_numpy(arr).to(device)

@@ -1,0 +1,114 @@
+// sx8_device.h -- device-side building blocks shared by the S-X8 HIP kernels (gfx950).
+//
+// S-X8 v4.3 block (docs/SX8_FLASH_V4_3_SPEC.md:13-25 in the reference): 32 weights of
+// one row in 30 bytes -- dmin fp16, dmax fp16, config u8 (4 x 2-bit range strategy),
+// 16 B of high nibbles, 8 B of low quads, coeff u8 (two signed 4-bit PCA coefficients).
+//
+// Two decode recipes live here:
+//   * R64 (sx8_r64_subblock): the canonical dequant of scripts/kernel_sx8_v43.py:14-51
+//     under Numba typing -- binary32 hi-lo, binary64 everywhere else, binary32 store,
+//     RNE to fp16.  Every kernel that hands fp16 weights to a caller or to the MFMA
+//     units uses it, so those weights are bit-identical to the canonical dequant.
+//   * the fp32 GEMV decode in sx8_gemv.hip, which only feeds an fp32 dot product
+//     (tolerance 1e-3 relative, scripts/sx8_decode1_v3.py:131-133).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 sx8_half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 sx8_half2 __attribute__((ext_vector_type(2)));
+typedef float sx8_float4 __attribute__((ext_vector_type(4)));
+
+// fp16 bit pattern (low 16 bits) -> float, exact.
+__device__ __forceinline__ float sx8_h2f(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
+}
+
+__device__ __forceinline__ int sx8_sext4(uint32_t v) {
+    return (int)((v & 0xFu) ^ 0x8u) - 8;      // 0..7 -> 0..7, 8..15 -> -8..-1
+}
+
+// 6-bit level of weight i (0..7) of a sub-block, from its 4 hi-nibble bytes H (weight i
+// at bits 4i) and its 2 lo-quad bytes P (weight i at bits 8*(i>>2) + 6 - 2*(i&3)).
+// This is kernel_sx8_v43.py:23-25 restricted to one sub-block.
+__device__ __forceinline__ uint32_t sx8_level(uint32_t H, uint32_t P, int i) {
+    uint32_t nib = (H >> (4 * i)) & 0xFu;
+    uint32_t qua = (P >> (8 * (i >> 2) + 6 - 2 * (i & 3))) & 0x3u;
+    return (nib << 2) | qua;
+}
+
+// R64 decode of one 8-weight sub-block `sb` of a block.  lo_f/hi_f are the fp16
+// endpoints widened to float, b0/b1 the sub-block's slice of the two PCA bases and
+// s0/s1 the scales, all widened to double (exact).  Writes the 8 fp16 results as
+// four packed dwords, weight 2j in the low half of out[j].
+//
+// Arithmetic (kernel_sx8_v43.py:28-51):
+//   q    = (double)(hi_f - lo_f) * 0.25          binary32 subtract, exact scale
+//   rlo, rhi by strategy s                        exact in binary64 (<= 43 bits)
+//   step = (rhi - rlo) * 0.015873, floored at 1e-10 (NaN passes the floor)
+//   w    = fma(step, lv, rlo)                     NVVM contracts this mul+add
+//   w    = fma((1.0*c0)*s0, b0, w), then c1/s1/b1 (the products are exact)
+//   out  = fp16(float(w))                          two RNE conversions
+// kPca = false drops the two PCA terms (the "core" weights rlo + step*lv), used when
+// the PCA term is applied at the GEMM output from a caller-supplied Z.
+template <bool kPca = true>
+__device__ __forceinline__ void sx8_r64_subblock(float lo_f, float hi_f, uint32_t cfg,
+                                                 uint32_t coeff, int sb, uint32_t H,
+                                                 uint32_t P, const double* b0,
+                                                 const double* b1, double s0, double s1,
+                                                 uint32_t out[4]) {
+#pragma clang fp contract(off)
+    const float d32 = hi_f - lo_f;
+    const double q = (double)d32 * 0.25;
+    const double lo64 = (double)lo_f, hi64 = (double)hi_f;
+    const uint32_t s = (cfg >> (2 * sb)) & 3u;
+    double rlo, rhi;
+    if (s == 0u)      { rlo = lo64;     rhi = hi64; }
+    else if (s == 1u) { rlo = lo64;     rhi = lo64 + q; }
+    else if (s == 2u) { rlo = hi64 - q; rhi = hi64; }
+    else              { rlo = lo64 + q; rhi = hi64 - q; }
+    double step = (rhi - rlo) * 0.015873;
+    if (step < 1e-10) step = 1e-10;
+    const double p0 = (1.0 * (double)sx8_sext4(coeff)) * s0;
+    const double p1 = (1.0 * (double)sx8_sext4(coeff >> 4)) * s1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float f[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int i = 2 * j + e;
+            double w = __builtin_fma(step, (double)sx8_level(H, P, i), rlo);
+            if constexpr (kPca) {
+                w = __builtin_fma(p0, b0[i], w);
+                w = __builtin_fma(p1, b1[i], w);
+            }
+            f[e] = (float)w;
+        }
+        sx8_half2 h;
+        h.x = (_Float16)f[0];
+        h.y = (_Float16)f[1];
+        out[j] = __builtin_bit_cast(uint32_t, h);
+    }
+}
+
+// Load helpers for the kb-major v4.4 header row of block `bid` (HB = 6 or 8 bytes):
+// dmin fp16 | dmax fp16 | config | coeff (| pad).  6-byte rows are only 2-byte aligned.
+template <int HB>
+__device__ __forceinline__ void sx8_load_hdr(const uint8_t* __restrict__ hdr, int64_t bid,
+                                             uint32_t& d0, uint32_t& d1, uint32_t& cfg,
+                                             uint32_t& coeff) {
+    if constexpr (HB == 8) {
+        const uint2 v = *reinterpret_cast<const uint2*>(hdr + bid * 8);
+        d0 = v.x & 0xFFFFu;
+        d1 = v.x >> 16;
+        cfg = v.y & 0xFFu;
+        coeff = (v.y >> 8) & 0xFFu;
+    } else {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(hdr + bid * 6);
+        d0 = h[0];
+        d1 = h[1];
+        const uint32_t cc = h[2];
+        cfg = cc & 0xFFu;
+        coeff = cc >> 8;
+    }
+}

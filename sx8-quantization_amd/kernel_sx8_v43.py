@@ -1,0 +1,91 @@
+"""Canonical S-X8 v4.3 full-tensor dequant on the GPU.
+
+Interface of scripts/kernel_sx8_v43.py (reference): ``decode_tensor_gpu`` and
+``decode_tensor_gpu_fast`` (:54-145).  The numba kernel sx8_v43_kernel (:14-51) is
+replaced by sx8_dequant_f16 in libsx8_hip.so, which computes the same recipe (R64:
+binary32 hi-lo, binary64 range/step/level/PCA arithmetic, binary32 store, RNE to fp16)
+and writes fp16 directly, so the results are bit-identical and no float32 staging
+buffer or device synchronisation is needed.  The work is enqueued on the current
+torch stream.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import _sx8lib as _L
+
+DEV = torch.device("cuda")
+N_BASES = 2
+BYTES_PER_BLOCK = 30  # 2+2+1+16+8+1
+
+# Kept for callers that clear the reference's float32 staging pool; this
+# implementation needs no staging buffer, so the pool stays empty.
+_BUFFER_POOL = {}
+_BUFFER_POOL_ORDER = []
+_BUFFER_POOL_MAX = 3
+
+
+def _get_buffer(n):
+    """float32 device buffer of at least n elements (pool of the reference API)."""
+    n_round = (n + 4095) & ~4095
+    for k in _BUFFER_POOL_ORDER:
+        if k >= n_round:
+            _BUFFER_POOL_ORDER.remove(k)
+            _BUFFER_POOL_ORDER.append(k)
+            return _BUFFER_POOL[k]
+    if len(_BUFFER_POOL_ORDER) >= _BUFFER_POOL_MAX:
+        del _BUFFER_POOL[_BUFFER_POOL_ORDER.pop(0)]
+    buf = torch.empty(n_round, dtype=torch.float32, device=DEV)
+    _BUFFER_POOL[n_round] = buf
+    _BUFFER_POOL_ORDER.append(n_round)
+    return buf
+
+
+def _dequant_into(qt, bases_info, out, device):
+    out_f, in_f = qt["shape"]
+    n_cb = int(qt["n_cb"])
+    if int(qt["n_blocks"]) != out_f * n_cb:
+        raise ValueError(f"n_blocks {qt['n_blocks']} != out_f*n_cb {out_f * n_cb}")
+    dm = _L.as_device(qt["dmin"], np.uint16, device)
+    dx = _L.as_device(qt["dmax"], np.uint16, device)
+    cf = _L.as_device(qt["config"], np.uint8, device)
+    co = _L.as_device(qt["coeff"], np.uint8, device)
+    hi = _L.as_device(qt["levels_hi"], np.uint8, device)
+    lo = _L.as_device(qt["levels_lo"], np.uint8, device)
+    bs = _L.as_device(bases_info["data"], np.float32, device)
+    sc = _L.as_device(bases_info["scales"], np.float32, device)
+    if bs.numel() != n_cb * 64 or sc.numel() != n_cb * 2:
+        raise ValueError("bases_info does not match n_cb")
+    _L.call("sx8_dequant_f16", _L.ptr(dm), _L.ptr(dx), _L.ptr(cf), _L.ptr(co), _L.ptr(hi),
+            _L.ptr(lo), _L.ptr(bs), _L.ptr(sc), out_f, in_f, n_cb, _L.ptr(out),
+            _L.stream(device))
+    return out
+
+
+def decode_tensor_gpu_fast(qt, bases_info, out=None):
+    """S-X8 v4.3 -> fp16 CUDA tensor (out_f, in_f), reshaped to orig_shape when it
+    differs.  If `out` is given it must be an fp16 CUDA tensor of shape (out_f, in_f);
+    it is filled and returned.  Raises ValueError on a shape mismatch."""
+    out_f, in_f = qt["shape"]
+    if out is not None:
+        if tuple(out.shape) != (out_f, in_f):
+            raise ValueError(f"out shape {tuple(out.shape)} != {(out_f, in_f)}")
+        if out.dtype != torch.float16 or not out.is_cuda:
+            raise ValueError("out must be a CUDA float16 tensor")
+        if out.is_contiguous():
+            return _dequant_into(qt, bases_info, out, out.device)
+        out.copy_(_dequant_into(qt, bases_info, torch.empty_like(out, memory_format=torch.contiguous_format), out.device))
+        return out
+    W = torch.empty((out_f, in_f), dtype=torch.float16, device=DEV)
+    _dequant_into(qt, bases_info, W, DEV)
+    orig = qt.get("orig_shape")
+    if orig is not None and tuple(orig) != (out_f, in_f):
+        W = W.reshape(orig)
+    return W
+
+
+def decode_tensor_gpu(qt, bases_info):
+    """Same values as decode_tensor_gpu_fast (the reference version went through a
+    host copy; this one stays on the device)."""
+    return decode_tensor_gpu_fast(qt, bases_info)

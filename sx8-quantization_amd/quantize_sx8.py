@@ -1,0 +1,169 @@
+"""S-X8 v4.3 quantizer in torch (CPU or GPU): fp16 weight -> (qt, bases_info).
+
+Restates the per-tensor path of scripts/quantize_qwen35_4b_sx8_v43_gpu.py in the
+reference, which runs at module import time and cannot be imported:
+  * ``v6_encode_6bit``   -- v6_encode_6bit_gpu (:22-47): per 8-weight sub-block, four
+    candidate ranges, 6-bit levels by round-half-even, lowest MSE wins (strict <).
+  * ``pca_correct``      -- pca_correct_gpu (:75-142): per K block (kb), 4 PCA bases
+    of the V6 residual, coefficients quantized to signed 4 bits with scale
+    median(|c|)/3; the first two are kept (1 coeff byte, 2 bases, 2 scales).
+  * ``pack_levels_6bit`` -- :148-167.
+  * ``quantize_tensor``  -- the tensor loop of :235-282 and the dict layout of
+    :383-395.
+
+Two deliberate differences, both outside bit-level parity (the reference's own
+results there depend on its CUDA reduction order and LAPACK build):
+  * the sub-block MSE sums the eight squared errors left to right, then divides
+    by 8 (torch.mean's order is unspecified);
+  * ``pca_method="gram"`` (the default on GPU) takes the bases from an eigen-
+    decomposition of the 32 x 32 Gram matrix E^T E in float64 instead of an SVD of E;
+    both give the leading right singular vectors up to sign.  Signs are fixed so
+    the largest-magnitude component is positive.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+B = 32
+L63 = 63
+N_BASES = 4
+
+
+def v6_encode_6bit(blocks: torch.Tensor):
+    """blocks (n, 32) float32 -> levels (n,32) u8, dmin f32, dmax f32, config (n,) int32."""
+    n = blocks.shape[0]
+    sub = blocks.reshape(n, 4, 8)
+    dmin = blocks.min(dim=1).values
+    dmax = blocks.max(dim=1).values
+    d = (dmax - dmin).clamp(min=1e-10)
+    q = d / 4.0
+    slo = [dmin, dmin, dmax - q, dmin + q]
+    shi = [dmax, dmin + q, dmax, dmax - q]
+    best_mse = torch.full((n, 4), float("inf"), device=blocks.device)
+    best_lev = torch.zeros(n, 4, 8, dtype=torch.int32, device=blocks.device)
+    best_str = torch.zeros(n, 4, dtype=torch.int32, device=blocks.device)
+    for ri in range(4):
+        lo = slo[ri][:, None, None]
+        hi = shi[ri][:, None, None]
+        step = ((hi - lo) / L63).clamp(min=1e-10)
+        cand = ((sub - lo) / step).round().clamp(0, L63).int()
+        rec = lo + step * cand.float()
+        sq = (sub - rec) ** 2
+        acc = sq[..., 0]
+        for j in range(1, 8):
+            acc = acc + sq[..., j]
+        mse = acc / 8.0
+        better = mse < best_mse
+        best_mse = torch.where(better, mse, best_mse)
+        best_lev = torch.where(better.unsqueeze(-1), cand, best_lev)
+        best_str = torch.where(better, torch.full_like(best_str, ri), best_str)
+    config = best_str[:, 0] | (best_str[:, 1] << 2) | (best_str[:, 2] << 4) | (best_str[:, 3] << 6)
+    return best_lev.to(torch.uint8).reshape(n, 32), dmin, dmax, config
+
+
+def _bases_gram(err: torch.Tensor, k: int) -> torch.Tensor:
+    """Top-k right singular vectors of err (rows, 32) via eigh of the Gram matrix."""
+    e64 = err.double()
+    g = e64.T @ e64
+    w, v = torch.linalg.eigh(g)                 # ascending eigenvalues
+    basis = v[:, torch.argsort(w, descending=True)[:k]].T.contiguous()
+    idx = basis.abs().argmax(dim=1)
+    sign = torch.sign(basis.gather(1, idx[:, None]))
+    sign[sign == 0] = 1
+    return (basis * sign).float()
+
+
+def pca_correct(levels, dmin, dmax, config, blocks, n_cb, pca_method="svd"):
+    """Per-kb PCA post-correction; returns coeff (n_blk,1) u8, data (n_cb,64) f32,
+    scales (n_cb,2) f32 (numpy, on the host)."""
+    dev = blocks.device
+    n_blk = blocks.shape[0]
+    n_rows = n_blk // n_cb
+    d = (dmax - dmin).clamp(min=1e-10)
+    Q = d / 4.0
+    lo_j = torch.stack([dmin, dmin, dmax - Q, dmin + Q], dim=0)
+    st_j = torch.stack([d / L63, Q / L63, Q / L63, (d - 2 * Q).clamp(min=1e-10) / L63], dim=0)
+    lv_f = levels.float()
+    coeff = torch.zeros(n_blk, dtype=torch.uint8, device=dev)
+    data = np.zeros((n_cb, 64), dtype=np.float32)
+    scales = np.zeros((n_cb, 2), dtype=np.float32)
+    if n_rows < 4:
+        return coeff.cpu().numpy().reshape(n_blk, 1), data, scales
+    rec = torch.empty(n_blk, 32, dtype=torch.float32, device=dev)
+    cfg = config.long()
+    ar = torch.arange(n_blk, device=dev)
+    for sb in range(4):
+        st = (cfg >> (sb * 2)) & 3
+        lo_sb = lo_j[st, ar]
+        step_sb = st_j[st, ar]
+        rec[:, sb * 8:(sb + 1) * 8] = lo_sb[:, None] + step_sb[:, None] * lv_f[:, sb * 8:(sb + 1) * 8]
+    err_all = (blocks - rec).reshape(n_rows, n_cb, 32)
+    for cb in range(n_cb):
+        err = err_all[:, cb, :].contiguous()
+        if pca_method == "gram":
+            basis = _bases_gram(err, N_BASES)
+        else:
+            _, _, vh = torch.linalg.svd(err, full_matrices=False)
+            basis = vh[:N_BASES]
+        craw = basis @ err.T
+        sc = (torch.median(craw.abs(), dim=1).values / 3.0).clamp(min=1e-10)
+        cq = (craw / sc[:, None]).round().clamp(-8, 7).to(torch.int8)
+        byte0 = (cq[0].view(torch.uint8) & 0xF) | ((cq[1].view(torch.uint8) & 0xF) << 4)
+        coeff.view(n_rows, n_cb)[:, cb] = byte0
+        data[cb] = basis[:2].reshape(-1).cpu().numpy()
+        scales[cb] = sc[:2].cpu().numpy()
+    return coeff.cpu().numpy().reshape(n_blk, 1), data, scales
+
+
+def pack_levels_6bit(levels: np.ndarray):
+    """(n_blk, 32) u8 levels -> (levels_hi (n_blk*16,), levels_lo (n_blk*8,))."""
+    lv = np.asarray(levels, dtype=np.uint8)
+    hi4 = (lv & 0x3F) >> 2
+    lo2 = lv & 0x03
+    flat = hi4.reshape(-1)
+    packed_hi = ((flat[0::2] & 0xF) | ((flat[1::2] << 4) & 0xF0)).astype(np.uint8)
+    g = lo2.reshape(-1, 4)
+    packed_lo = (((g[:, 0] & 3) << 6) | ((g[:, 1] & 3) << 4) | ((g[:, 2] & 3) << 2) | (g[:, 3] & 3)).astype(np.uint8)
+    return packed_hi, packed_lo
+
+
+def quantize_tensor(W, device=None, pca_method=None, degenerate_frac=0.0, seed=None):
+    """Quantize an fp16/fp32 (out_f, in_f) weight to S-X8 v4.3.
+
+    ``degenerate_frac`` > 0 forces that fraction of blocks (chosen with ``seed``) to
+    be constant (every weight equal to the block's first weight), which exercises the
+    step = 1e-10 floor (dmin == dmax) exactly as the measurement plan asks.
+    Returns (qt, bases_info) with numpy arrays, in the reference's pkl layout.
+    """
+    W = torch.as_tensor(W)
+    if device is None:
+        device = W.device
+    if pca_method is None:
+        pca_method = "gram" if torch.device(device).type == "cuda" else "svd"
+    Wd = W.to(device=device, dtype=torch.float16).float()
+    out_f, in_f = Wd.shape
+    n_cb = (in_f + B - 1) // B
+    pad = n_cb * B - in_f
+    if pad:
+        Wd = torch.nn.functional.pad(Wd, (0, pad))
+    blocks = Wd.reshape(out_f * n_cb, B).contiguous()
+    if degenerate_frac > 0:
+        g = torch.Generator(device="cpu")
+        g.manual_seed(int(seed or 0))
+        n_deg = int(round(degenerate_frac * blocks.shape[0]))
+        idx = torch.randperm(blocks.shape[0], generator=g)[:n_deg].to(device)
+        blocks[idx] = blocks[idx, :1].expand(-1, B)
+    lv, dmin, dmax, cfg = v6_encode_6bit(blocks)
+    coeff, data, scales = pca_correct(lv, dmin, dmax, cfg, blocks, n_cb, pca_method)
+    lv_np = lv.cpu().numpy()
+    hi, lo = pack_levels_6bit(lv_np)
+    qt = {
+        "shape": (out_f, in_f), "orig_shape": (out_f, in_f),
+        "n_blocks": out_f * n_cb, "n_cb": n_cb,
+        "dmin": dmin.cpu().numpy().astype(np.float16),
+        "dmax": dmax.cpu().numpy().astype(np.float16),
+        "config": cfg.cpu().numpy().astype(np.uint8),
+        "levels_hi": hi, "levels_lo": lo, "coeff": coeff,
+    }
+    return qt, {"n_cb": n_cb, "data": data, "scales": scales}

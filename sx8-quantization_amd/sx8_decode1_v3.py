@@ -1,0 +1,119 @@
+"""M = 1 decode GEMV on the kb-major v4.4 layout (the decode path of SX8LinearV44).
+
+Interface of scripts/sx8_decode1_v3.py (reference): ``_ext()`` (an object with
+``compute_z44``, ``decode1_v44`` and ``decode1_v44_combined``), ``make_tensors_v44``,
+``best_split_k``, the ``_BUF``/``_buf`` output pools and ``decode1_v44``.
+The CUDA extension is replaced by libsx8_hip.so (sx8_compute_z / sx8_gemv); the
+combined entry point computes Z inside the GEMV launch (one launch instead of two)
+and still writes it to the caller's Z buffer.
+"""
+from __future__ import annotations
+
+import torch
+
+import _sx8lib as _L
+
+DEV = torch.device("cuda")
+
+
+def _x_for_kernel(X, n_cb):
+    """fp16 (K,) activation as the kernel needs it: contiguous, 16-byte aligned and
+    zero-padded to n_cb*32 values (the reference read past K instead)."""
+    Xc = X.reshape(-1).contiguous().half()
+    Kp = n_cb * 32
+    if Xc.numel() < Kp or Xc.data_ptr() % 16:
+        Xp = torch.zeros(Kp, dtype=torch.float16, device=Xc.device)
+        Xp[:min(Kp, Xc.numel())] = Xc[:Kp]
+        Xc = Xp
+    return Xc
+
+
+class _Ext:
+    """Drop-in for the reference's load_inline module (sx8_decode1_v3.py:33-54)."""
+
+    @staticmethod
+    def compute_z44(X, basis, scales, n_cb, out=None):
+        n_cb = int(n_cb)
+        Xc = _x_for_kernel(X, n_cb)
+        if out is None:
+            out = torch.empty(n_cb, 2, dtype=torch.float32, device=Xc.device)
+        _L.call("sx8_compute_z", _L.ptr(Xc), 1, n_cb * 32, _L.ptr(basis.contiguous()),
+                _L.ptr(scales.contiguous()), n_cb, _L.ptr(out), _L.stream(Xc.device))
+        return out
+
+    @staticmethod
+    def decode1_v44(X, hdr, levels, Z, n_cb, hdr_bytes, split_k=1, out=None):
+        """GEMV with a precomputed Z; split_k is accepted and ignored (as upstream)."""
+        n_cb = int(n_cb)
+        N = hdr.size(0) // n_cb
+        Xc = _x_for_kernel(X, n_cb)
+        if out is None:
+            out = torch.empty(N, dtype=torch.float32, device=Xc.device)
+        _L.call("sx8_gemv", _L.ptr(Xc), _L.ptr(hdr), _L.ptr(levels), int(hdr_bytes), None, None,
+                _L.ptr(Z.contiguous()), None, N, n_cb, _L.ptr(out), _L.stream(Xc.device))
+        return out
+
+    @staticmethod
+    def decode1_v44_combined(X, hdr, levels, basis, scales, n_cb, hdr_bytes, Z, out):
+        n_cb = int(n_cb)
+        N = hdr.size(0) // n_cb
+        Xc = _x_for_kernel(X, n_cb)
+        _L.call("sx8_gemv", _L.ptr(Xc), _L.ptr(hdr), _L.ptr(levels), int(hdr_bytes),
+                _L.ptr(basis.contiguous()), _L.ptr(scales.contiguous()), None, _L.ptr(Z), N,
+                n_cb, _L.ptr(out), _L.stream(Xc.device))
+        return out
+
+
+_cached = None
+
+
+def _ext():
+    global _cached
+    if _cached is None:
+        _L.lib()          # fail loudly here if the HIP library is missing
+        _cached = _Ext()
+    return _cached
+
+
+def make_tensors_v44(qt, bases_info, hdr_aligned=False):
+    """v4.4 kb-major tensors on the current device: hdr (n_blk, 6|8) u8,
+    levels (n_blk, 24) u8, bases (n_cb, 64) f32, scales (n_cb, 2) f32."""
+    from prepare_v44 import to_v44_device
+    return to_v44_device(qt, bases_info, hdr_aligned=hdr_aligned, device=DEV)
+
+
+def best_split_k(N, n_cb):
+    """The reference's split heuristic (sx8_decode1_v3.py:69-77).  Its result is
+    accepted by decode1_v44 and ignored, as upstream; the HIP GEMV picks its own
+    K split from the shape and the CU count."""
+    n_blocks = (N + 63) // 64
+    want = 540
+    sk = max(1, (want + n_blocks - 1) // n_blocks)
+    return min(sk, 16)
+
+
+_BUF = {}
+
+
+def _buf(key, shape):
+    b = _BUF.get(key)
+    if b is None or b.shape != tuple(shape) or b.device != DEV:
+        b = torch.empty(*shape, dtype=torch.float32, device=DEV)
+        _BUF[key] = b
+    return b
+
+
+def decode1_v44(X, qt, bases_info, hdr_t=None, lvl_t=None, bas_t=None, sca_t=None,
+                hdr_bytes=6, split_k=1):
+    """Y = W . X for X (K,) fp16 -> (Y float32 (N,), (hdr_t, lvl_t, bas_t, sca_t)).
+    Y is a pooled buffer keyed by N: the next call with the same N overwrites it."""
+    if hdr_t is None:
+        hdr_t, lvl_t, bas_t, sca_t = make_tensors_v44(qt, bases_info,
+                                                      hdr_aligned=(hdr_bytes == 8))
+    n_cb = qt["n_cb"]
+    N = qt["shape"][0]
+    ext = _ext()
+    Z = _buf(("Z", n_cb), (n_cb, 2))
+    Y = _buf(("Y", N), (N,))
+    ext.decode1_v44_combined(X, hdr_t, lvl_t, bas_t, sca_t, n_cb, hdr_bytes, Z, Y)
+    return Y, (hdr_t, lvl_t, bas_t, sca_t)

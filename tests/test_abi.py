@@ -1,0 +1,75 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol that
+include/sx8_hip.h declares, and rejects bad arguments on the host (before any HIP
+call) with an error code and a message.  No kernel is launched here."""
+import ctypes
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "sx8_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int32_t|const char\*)\s+(sx8_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_abi():
+    names = _declared()
+    assert "sx8_gemv" in names and "sx8_gemm_prefill" in names and "sx8_embed_gather" in names
+    assert len(names) >= 10
+
+
+def test_library_exports_every_declared_symbol(hiplib):
+    import _sx8lib
+    for name in _declared():
+        assert hasattr(hiplib, name), name
+    assert sorted(n for n, _, _ in _sx8lib.SIGNATURES) == _declared()
+    assert hiplib.sx8_abi_version() == _sx8lib.ABI_VERSION
+
+
+NULL = ctypes.c_void_p(None)
+
+
+def _err(lib):
+    return lib.sx8_last_error().decode()
+
+
+def test_invalid_arguments_rejected_on_host(hiplib):
+    L = hiplib
+    p = ctypes.c_void_p(4096)   # never dereferenced: validation fails first
+    # null pointers
+    assert L.sx8_gemv(NULL, p, p, 6, p, p, NULL, NULL, 64, 2, p, NULL) == 1
+    assert "null" in _err(L)
+    # hdr_bytes outside {6, 8}
+    assert L.sx8_gemv(p, p, p, 7, p, p, NULL, NULL, 64, 2, p, NULL) == 1
+    assert "hdr_bytes" in _err(L)
+    # misaligned X (needs 16 bytes)
+    assert L.sx8_gemv(ctypes.c_void_p(4098), p, p, 6, p, p, NULL, NULL, 64, 2, p, NULL) == 1
+    assert "misaligned" in _err(L)
+    # inconsistent K / n_cb
+    assert L.sx8_dequant_f16(p, p, p, p, p, p, p, p, 4, 100, 2, p, NULL) == 1
+    assert "bad shape" in _err(L)
+    assert L.sx8_gemm_prefill(p, 4, 64, 64, p, p, 6, p, p, 0, 2, p, NULL) == 1
+    assert L.sx8_gemm_prefill(p, 4, 32, 64, p, p, 6, p, p, 64, 2, p, NULL) == 1   # ldx < K
+    assert L.sx8_embed_gather(p, 4, p, p, 5, p, p, 64, 10, 2, p, NULL) == 1
+    assert L.sx8_compute_z(p, 1, 16, p, p, 1, p, NULL) == 1                      # ldx < 32
+    assert L.sx8_gemm_pca_z(NULL, 1, p, 6, 64, 2, p, NULL) == 1
+
+
+def test_wrapper_raises_runtime_error(hiplib):
+    import _sx8lib
+    with pytest.raises(RuntimeError, match="hdr_bytes"):
+        _sx8lib.call("sx8_gemv", ctypes.c_void_p(4096), ctypes.c_void_p(4096),
+                     ctypes.c_void_p(4096), 9, ctypes.c_void_p(4096), ctypes.c_void_p(4096),
+                     NULL, NULL, 64, 2, ctypes.c_void_p(4096), NULL)
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    import _sx8lib
+    monkeypatch.setattr(_sx8lib, "_lib", None)
+    monkeypatch.setenv("SX8_HIP_LIB", str(tmp_path / "nope.so"))
+    with pytest.raises(RuntimeError, match="not found"):
+        _sx8lib.lib()

@@ -1,0 +1,301 @@
+"""GPU parity of the HIP hot path against the CPU oracle (run with -m gpu).
+
+Bars:
+  * dequantized fp16 weights (full-tensor dequant, embedding rows, and the MFMA
+    operand tiles of the prefill GEMM) are bit-exact to the canonical R64 dequant,
+    including the degenerate-block step = 1e-10 floor;
+  * GEMV / GEMM outputs are within max|dY| / max|Y_ref| <= 1e-3 of the float64-
+    accumulated X . W16^T (the reference's metric, sx8_fused_wmma.py:132).
+"""
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+SHAPES_4B = {  # name: (N, K)  -- BASELINE.json configs[1]
+    "q_proj": (4096, 2560), "k_proj": (1024, 2560), "o_proj": (2560, 4096),
+    "gate_proj": (9728, 2560), "down_proj": (2560, 9728),
+}
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _golden_qt(prefix):
+    g = np.load(os.path.join(HERE, "golden", "sx8_golden.npz"))
+    out_f, in_f, n_cb = (int(v) for v in g[prefix + "shape"])
+    qt = {"shape": (out_f, in_f), "orig_shape": (out_f, in_f), "n_blocks": out_f * n_cb,
+          "n_cb": n_cb}
+    for k in ("dmin", "dmax", "config", "levels_hi", "levels_lo", "coeff"):
+        qt[k] = g[prefix + k]
+    bi = {"n_cb": n_cb, "data": g[prefix + "basis"], "scales": g[prefix + "scales"]}
+    return qt, bi, g[prefix + "w16"].reshape(out_f, in_f)
+
+
+_QCACHE = {}
+
+
+def _quantized(N, K, seed, cuda, degenerate=0.01):
+    """Seeded N(0, 0.02) fp16 weight, quantized with 1% degenerate blocks."""
+    key = (N, K, seed, degenerate)
+    if key not in _QCACHE:
+        import torch
+        from quantize_sx8 import quantize_tensor
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        W = (torch.randn(N, K, generator=g) * 0.02).half()
+        _QCACHE[key] = quantize_tensor(W, device=cuda, degenerate_frac=degenerate, seed=seed + 1)
+    return _QCACHE[key]
+
+
+def _x(M, K, seed):
+    import torch
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return torch.randn(M, K, generator=g).half()
+
+
+# ------------------------------------------------------------------------ dequant
+
+@pytest.mark.parametrize("prefix", ["fuzz_", "q_"])
+def test_dequant_matches_golden(hiplib, cuda, prefix):
+    import torch
+    from kernel_sx8_v43 import decode_tensor_gpu_fast
+    qt, bi, w16 = _golden_qt(prefix)
+    _say("dequant golden", prefix, qt["shape"])
+    W = decode_tensor_gpu_fast(qt, bi)
+    torch.cuda.synchronize()
+    assert np.array_equal(W.cpu().numpy().view(np.uint16), w16)
+    out = torch.empty(qt["shape"], dtype=torch.float16, device=cuda)
+    assert decode_tensor_gpu_fast(qt, bi, out=out) is out
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), w16)
+    with pytest.raises(ValueError):
+        decode_tensor_gpu_fast(qt, bi, out=torch.empty(3, 3, dtype=torch.float16, device=cuda))
+
+
+@pytest.mark.parametrize("N,K", [(2560, 2560), (1024, 2560), (300, 80), (64, 4096)])
+def test_dequant_quantized_bit_exact(hiplib, oracle, cuda, N, K):
+    from kernel_sx8_v43 import decode_tensor_gpu_fast
+    qt, bi = _quantized(N, K, 0 if (N, K) == (2560, 2560) else N + K, cuda)
+    _say("dequant quantized", N, K)
+    got = decode_tensor_gpu_fast(qt, bi).cpu().numpy().view(np.uint16)
+    exp = oracle.dequant_r64(qt, bi).view(np.uint16)
+    assert np.array_equal(got, exp)
+    # the 1% degenerate blocks decode to their constant value
+    dm = np.asarray(qt["dmin"]).view(np.uint16)
+    dx = np.asarray(qt["dmax"]).view(np.uint16)
+    deg = np.nonzero(dm == dx)[0]
+    assert deg.size > 0
+    n_cb = qt["n_cb"]
+    for bid in deg[:50]:
+        n, kb = divmod(int(bid), n_cb)
+        cols = got[n, kb * 32:min(K, kb * 32 + 32)]
+        v = dm[bid] if dm[bid] != 0x8000 else 0
+        assert np.all(cols == v)
+
+
+# ---------------------------------------------------------------------- embedding
+
+@pytest.mark.parametrize("hdr_bytes", [6, 8])
+def test_embed_gather_bit_exact(hiplib, oracle, cuda, hdr_bytes):
+    import torch
+    from sx8_decode1_v3 import make_tensors_v44
+    from sx8_embed_v44 import SX8EmbeddingV44, ext
+    N, K = 3000, 2560
+    qt, bi = _quantized(N, K, 77, cuda)
+    _say("embed", hdr_bytes)
+    W = oracle.dequant_r64(qt, bi).view(np.uint16)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    ids = torch.randint(0, N, (512,), generator=g)
+    ids[7], ids[100], ids[511] = -1, N, N + 12          # out of range: rows untouched
+    hdr, lvl, bas, sca = make_tensors_v44(qt, bi, hdr_aligned=(hdr_bytes == 8))
+    out = torch.full((512, K), 7.0, dtype=torch.float16, device=cuda)
+    ext().sx8_embed_v44(ids.to(cuda), hdr, lvl, bas, sca, K, N, qt["n_cb"], out)
+    got = out.cpu().numpy().view(np.uint16)
+    idn = ids.numpy()
+    ok = (idn >= 0) & (idn < N)
+    assert np.array_equal(got[ok], W[idn[ok]])
+    assert np.all(got[~ok] == np.float16(7.0).view(np.uint16))
+    emb = SX8EmbeddingV44(qt, bi, hdr_bytes=hdr_bytes)
+    ids2 = torch.randint(0, N, (4, 33), generator=g).to(cuda)
+    e = emb(ids2)
+    assert e.shape == (4, 33, K)
+    assert np.array_equal(e.cpu().numpy().view(np.uint16).reshape(-1, K), W[ids2.cpu().numpy().reshape(-1)])
+
+
+def test_embed_ragged_k(hiplib, oracle, cuda):
+    import torch
+    from sx8_embed_v44 import SX8EmbeddingV44
+    qt, bi = _quantized(257, 80, 9, cuda)              # K = 80: last block half used
+    W = oracle.dequant_r64(qt, bi).view(np.uint16)
+    ids = torch.tensor([0, 256, 3, 3, 128], device=cuda)
+    e = SX8EmbeddingV44(qt, bi)(ids)
+    assert np.array_equal(e.cpu().numpy().view(np.uint16), W[ids.cpu().numpy()])
+
+
+# --------------------------------------------------------------------------- GEMV
+
+GEMV_CASES = [("cpu_config", 2560, 2560, 0)] + [
+    (k, n, kk, 1000 + i) for i, (k, (n, kk)) in enumerate(SHAPES_4B.items())] + [
+    ("odd_N", 1000, 2560, 7), ("tiny", 65, 96, 8), ("ragged_K", 200, 80, 9)]
+
+
+@pytest.mark.parametrize("hdr_bytes", [6, 8])
+@pytest.mark.parametrize("name,N,K,seed", GEMV_CASES)
+def test_gemv_within_1e3(hiplib, oracle, cuda, name, N, K, seed, hdr_bytes):
+    import torch
+    from sx8_decode1_v3 import _ext, decode1_v44, make_tensors_v44
+    qt, bi = _quantized(N, K, seed, cuda)
+    _say("gemv", name, N, K, hdr_bytes)
+    x = _x(1, K, seed + 2)[0]
+    W = oracle.dequant_r64(qt, bi)
+    y_ref = oracle.gemm_f64(x.numpy()[None], W)[0]
+    t = make_tensors_v44(qt, bi, hdr_aligned=(hdr_bytes == 8))
+    Y, _ = decode1_v44(x.to(cuda), qt, bi, *t, hdr_bytes=hdr_bytes)
+    y = Y.cpu().numpy().astype(np.float64)
+    rel = oracle.rel_err(y, y_ref)
+    _say("   rel", rel)
+    assert rel <= 1e-3
+    # the two-launch form (Z precomputed) gives the same numbers
+    ext = _ext()
+    Z = ext.compute_z44(x.to(cuda), t[2], t[3], qt["n_cb"])
+    Y2 = ext.decode1_v44(x.to(cuda), t[0], t[1], Z, qt["n_cb"], hdr_bytes, 1)
+    assert torch.equal(Y2.cpu(), Y.cpu())
+    # Z equals the reference's float32 warp tree bit for bit
+    zref = oracle.z44_f32_tree(x.numpy(), bi)[0]
+    assert np.array_equal(Z.cpu().numpy(), zref)
+
+
+def test_gemv_deterministic_and_pool(hiplib, cuda):
+    import torch
+    from sx8_decode1_v3 import decode1_v44, make_tensors_v44
+    qt, bi = _quantized(1024, 2560, 1001, cuda)      # split-K path (few column tiles)
+    t = make_tensors_v44(qt, bi)
+    x = _x(1, 2560, 3)[0].to(cuda)
+    first = decode1_v44(x, qt, bi, *t)[0].clone()
+    for _ in range(20):
+        y, _ = decode1_v44(x, qt, bi, *t)
+        assert torch.equal(y, first)
+    # pooled output: same N -> same buffer, overwritten by the next call
+    y2, _ = decode1_v44(x * 2, qt, bi, *t)
+    assert y2.data_ptr() == y.data_ptr()
+
+
+# -------------------------------------------------------------------------- GEMM
+
+PREFILL_CASES = [
+    ("q_proj", 4096, 2560, 128), ("k_proj", 1024, 2560, 512), ("down", 2560, 9728, 130),
+    ("odd", 1000, 2560, 7), ("tiny", 64, 96, 1), ("ragged_K", 300, 80, 33),
+]
+
+
+@pytest.mark.parametrize("name,N,K,M", PREFILL_CASES)
+def test_prefill_gemm(hiplib, oracle, cuda, name, N, K, M):
+    import torch
+    from sx8_decode1_v3 import make_tensors_v44
+    from sx8_gemm_compact import _ext, gemm_sx8_compact
+    from sx8_fused_wmma import gemm_sx8_wmma_cached, make_tensors, to_kbmajor
+    qt, bi = _quantized(N, K, N * 3 + K, cuda)
+    _say("prefill", name, N, K, M)
+    X = _x(M, K, 11)
+    W = oracle.dequant_r64(qt, bi)
+    Y_ref = oracle.gemm_f64(X.numpy(), W)
+    t = make_tensors_v44(qt, bi)
+    Y = gemm_sx8_compact(X.to(cuda), qt, bi, *t)
+    rel = oracle.rel_err(Y.cpu().numpy(), Y_ref)
+    _say("   rel", rel)
+    assert rel <= 1e-3
+    # bit-exact operands: the GEMM matches fp32 accumulation over the exact fp16 W
+    Y32 = X.float() @ torch.from_numpy(W.astype(np.float32)).T
+    assert oracle.rel_err(Y.cpu().numpy(), Y32.numpy()) <= 2e-6
+    # the split-array (fused-WMMA) contract runs the same kernel: identical output
+    kbm, _ = to_kbmajor(qt, bi)
+    Yw = gemm_sx8_wmma_cached(X.to(cuda), make_tensors(kbm, bi, cuda), qt["n_cb"])
+    assert torch.equal(Yw.cpu(), Y.cpu())
+    # caller-supplied Z contract (core GEMM + output-side PCA)
+    ext = _ext()
+    Xp = torch.zeros(M, qt["n_cb"] * 32, dtype=torch.float16)
+    Xp[:, :K] = X
+    Z = ext.compute_z44_batch(Xp.to(cuda), t[2], t[3], qt["n_cb"])
+    Yz = ext.gemm_compact(Xp.to(cuda), t[0], t[1], Z, qt["n_cb"], 6)
+    assert oracle.rel_err(Yz.cpu().numpy(), Y_ref) <= 1e-3
+
+
+def test_prefill_deterministic(hiplib, cuda):
+    import torch
+    from sx8_decode1_v3 import make_tensors_v44
+    from sx8_gemm_compact import gemm_sx8_compact
+    qt, bi = _quantized(1024, 2560, 1001, cuda)
+    t = make_tensors_v44(qt, bi)
+    X = _x(256, 2560, 4).to(cuda)
+    a = gemm_sx8_compact(X, qt, bi, *t)
+    for _ in range(5):
+        assert torch.equal(gemm_sx8_compact(X, qt, bi, *t), a)
+
+
+def test_prefill_small_n_fallback(hiplib, oracle, cuda):
+    from sx8_gemm_compact import gemm_sx8_compact
+    qt, bi = _quantized(32, 2560, 5, cuda)              # N < 64 -> dequant + F.linear
+    X = _x(16, 2560, 6)
+    Y = gemm_sx8_compact(X.to(cuda), qt, bi)
+    Y_ref = oracle.gemm_f64(X.numpy(), oracle.dequant_r64(qt, bi))
+    assert oracle.rel_err(Y.cpu().numpy(), Y_ref) <= 1e-3
+
+
+# ------------------------------------------------------------------------ modules
+
+def test_linear_module_dispatch(hiplib, oracle, cuda, monkeypatch):
+    import torch
+    from integrate_fused_v44 import SX8LinearV44
+    qt, bi = _quantized(512, 2560, 21, cuda)
+    bias = torch.randn(512, dtype=torch.float16, device=cuda)
+    lin = SX8LinearV44(qt, bi, bias=bias)
+    W = oracle.dequant_r64(qt, bi)
+    for shape in [(1, 2560), (1, 1, 2560), (2, 9, 2560)]:
+        x = _x(int(np.prod(shape[:-1])), 2560, 8).reshape(shape)
+        y = lin(x.to(cuda))
+        assert y.shape == (*shape[:-1], 512) and y.dtype == torch.float16
+        ref = oracle.gemm_f64(x.reshape(-1, 2560).numpy(), W) + bias.float().cpu().numpy()
+        assert oracle.rel_err(y.float().cpu().numpy().reshape(-1, 512), ref) <= 2e-3
+    monkeypatch.setenv("SX8_USE_WMMA", "1")
+    x = _x(5, 2560, 9)
+    y = lin(x.to(cuda))
+    ref = oracle.gemm_f64(x.numpy(), W) + bias.float().cpu().numpy()
+    assert oracle.rel_err(y.float().cpu().numpy(), ref) <= 2e-3
+
+
+def test_clone_model_replaces_linears(hiplib, cuda):
+    import torch
+    import torch.nn as nn
+    from integrate_fused_v44 import SX8EmbeddingV44, SX8LinearV44, clone_model_fused_v44
+    from quantize_sx8 import quantize_tensor
+
+    class Tiny(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.embed = nn.Embedding(100, 64)
+            self.layers = nn.ModuleList([nn.Linear(64, 128), nn.Linear(128, 64)])
+
+        def forward(self, ids):
+            h = self.embed(ids)
+            for l in self.layers:
+                h = l(h)
+            return h
+
+    torch.manual_seed(0)
+    m = Tiny().half().to(cuda)
+    wd, bd = {}, {}
+    for name, p in m.named_parameters():
+        if p.dim() == 2:
+            wd[name], bd[name] = quantize_tensor(p.detach().cpu(), device="cpu")
+    ids = torch.tensor([[1, 5, 99]], device=cuda)
+    with torch.no_grad():
+        ref = m(ids).float()
+    m2, n = clone_model_fused_v44(m, wd, bd)
+    assert n == 3
+    assert isinstance(m2.embed, SX8EmbeddingV44) and isinstance(m2.layers[0], SX8LinearV44)
+    with torch.no_grad():
+        out = m2(ids).float()
+    assert (out - ref).abs().max().item() / ref.abs().max().item() < 5e-2

@@ -1,0 +1,368 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it.
+
+The reference ships no golden vectors for this path, so the canonical dequant R64
+(scripts/kernel_sx8_v43.py:14-51 under Numba typing) is pinned by
+  * hand-derived known answers (each test states the derivation), chosen so that a
+    plausible mistake -- 1/63 instead of the 0.015873 literal, a float64 instead of
+    float32 subtraction, a single f64->f16 rounding, a dropped or swapped PCA term,
+    a wrong nibble/quad order -- changes the answer;
+  * brute force against an independent numpy float64 restatement;
+  * exact rational arithmetic for the fused multiply-add.
+"""
+import os
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _block_qt(dmin, dmax, config, levels, coeff):
+    """Single-row tensor of n blocks from per-block fields and (n, 32) levels."""
+    import oracle as O
+    levels = np.asarray(levels, dtype=np.uint8).reshape(-1, 32)
+    n = levels.shape[0]
+    hi, lo = O.pack_levels(levels)
+    return {
+        "shape": (1, n * 32), "orig_shape": (1, n * 32), "n_blocks": n, "n_cb": n,
+        "dmin": np.asarray(dmin, dtype=np.float16).reshape(n),
+        "dmax": np.asarray(dmax, dtype=np.float16).reshape(n),
+        "config": np.asarray(config, dtype=np.uint8).reshape(n),
+        "levels_hi": hi, "levels_lo": lo,
+        "coeff": np.asarray(coeff, dtype=np.uint8).reshape(n, 1),
+    }
+
+
+def _bases(n_cb, b0=0.0, b1=0.0, s0=0.0, s1=0.0):
+    data = np.zeros((n_cb, 64), dtype=np.float32)
+    data[:, :32] = b0
+    data[:, 32:] = b1
+    return {"n_cb": n_cb, "data": data,
+            "scales": np.tile(np.array([s0, s1], dtype=np.float32), (n_cb, 1))}
+
+
+def _r64(oracle, qt, bi, fused=True):
+    return oracle.dequant_r64(qt, bi, fused=fused, blocks_only=True).view(np.uint16)
+
+
+# ------------------------------------------------------------------ fp16 conversions
+
+def test_f16_conversions_match_numpy(oracle):
+    L = oracle.lib()
+    every = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = every.view(np.float16).astype(np.float32)
+    got = np.array([L.sx8o_f16_to_f32(int(h)) for h in every[::97]], dtype=np.float32)
+    exp = f[::97]
+    finite = np.isfinite(exp)
+    assert np.array_equal(got[finite], exp[finite])
+    rng = np.random.default_rng(0)
+    xs = np.concatenate([
+        (rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 5, 20000)).astype(np.float32),
+        # exact ties between fp16 neighbours, including subnormal ties
+        ((np.arange(1, 3000) * 2 + 1) * 2.0 ** -25).astype(np.float32),
+        ((np.arange(1024, 2048) * 2 + 1) * 2.0 ** -11).astype(np.float32),
+        np.array([65519.0, 65520.0, 70000.0, 2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -26], np.float32),
+    ])
+    got16 = np.array([L.sx8o_f32_to_f16(float(x)) for x in xs], dtype=np.uint16)
+    assert np.array_equal(got16, xs.astype(np.float16).view(np.uint16))
+
+
+# --------------------------------------------------------------------- level packing
+
+def test_pack_unpack_all_levels_all_positions(oracle):
+    # every level 0..63 at every position 0..31: 64 blocks with lv[b, t] = (b + t) % 64
+    lv = (np.arange(64)[:, None] + np.arange(32)[None, :]) % 64
+    hi, lo = oracle.pack_levels(lv)
+    assert np.array_equal(oracle.unpack_levels(hi, lo), lv)
+    # closed form of the spec (SPEC.md:20-21) for one block: weight t -> byte/bit
+    hb = hi.reshape(64, 16)[5]
+    lb = lo.reshape(64, 8)[5]
+    for t in range(32):
+        assert (hb[t >> 1] >> ((t & 1) * 4)) & 0xF == lv[5, t] >> 2
+        assert (lb[t >> 2] >> ((3 - (t & 3)) * 2)) & 3 == lv[5, t] & 3
+
+
+def test_product_quantizer_packing_matches_oracle(oracle):
+    from quantize_sx8 import pack_levels_6bit
+    rng = np.random.default_rng(1)
+    lv = rng.integers(0, 64, (300, 32)).astype(np.uint8)
+    a = pack_levels_6bit(lv)
+    b = oracle.pack_levels(lv)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+# ------------------------------------------------------------------- known answers
+
+def test_kat_level_order(oracle):
+    # lo = 0, hi = 63/64 (fp16-exact), s = 0: step = (63/64) * 0.015873 = (1 - 1e-6)/64,
+    # so w = lv/64 * (1 - 1e-6), within 1e-6 relative of lv/64 and far from any fp16
+    # rounding boundary: the decode must return exactly lv/64 for the level stored at
+    # each position.  A wrong nibble or quad order returns another position's level.
+    lv = ((np.arange(32) * 37 + 11) % 64).reshape(1, 32)
+    qt = _block_qt([0.0], [63 / 64], [0], lv, [0])
+    got = _r64(oracle, qt, _bases(1))[0]
+    exp = (lv[0] / 64.0).astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, exp)
+
+
+def test_kat_degenerate_block(oracle):
+    # dmin == dmax = v: q = 0, rlo = rhi = v, step = 0 -> floored to 1e-10, so
+    # w = v + 1e-10 * lv with 1e-10 * 63 below half of the smallest fp16 spacing
+    # (2^-25): the answer is fp16(v) for every level and strategy -- except v = -0,
+    # where -0 + (+0) = +0.
+    vals = [0.0125, -3.5, 2.0 ** -24, -(2.0 ** -20), 0.0, 60000.0]
+    n = len(vals)
+    rng = np.random.default_rng(2)
+    qt = _block_qt(vals, vals, rng.integers(0, 256, n), rng.integers(0, 64, (n, 32)), [0] * n)
+    got = _r64(oracle, qt, _bases(n))
+    exp = np.repeat(np.asarray(vals, np.float16).view(np.uint16)[:, None], 32, axis=1)
+    assert np.array_equal(got, exp)
+    qt = _block_qt([-0.0], [-0.0], [0], np.full((1, 32), 0), [0])
+    assert np.all(_r64(oracle, qt, _bases(1)) == 0x0000)
+    # all-zero block (everything zero, coeff 0) -> +0 everywhere
+    qt = _block_qt([0.0], [0.0], [0], np.zeros((1, 32)), [0])
+    assert np.all(_r64(oracle, qt, _bases(1)) == 0x0000)
+
+
+def test_kat_strategies_endpoints(oracle):
+    # lo = 0, hi = 1: d = 1, q = 0.25.  lv = 0 returns rlo exactly:
+    #   s0 -> 0, s1 -> 0, s2 -> hi - q = 0.75, s3 -> lo + q = 0.25.
+    # lv = 63 returns rlo + range * 63 * 0.015873 = rlo + range * 0.999999, which rounds
+    # to rhi in fp16: s0 -> 1, s1 -> 0.25, s2 -> 1, s3 -> 0.75.
+    lv = np.zeros((1, 32), dtype=np.int64)
+    lv[0, 8 * np.arange(4)[:, None] + np.arange(4)[None, :]] = 0
+    lv[0, 8 * np.arange(4)[:, None] + 4 + np.arange(4)[None, :]] = 63
+    cfg = 0 | (1 << 2) | (2 << 4) | (3 << 6)           # sub-block sb uses strategy sb
+    got = _r64(oracle, _block_qt([0.0], [1.0], [cfg], lv, [0]), _bases(1))[0].view(np.float16)
+    exp_lo = [0.0, 0.0, 0.75, 0.25]
+    exp_hi = [1.0, 0.25, 1.0, 0.75]
+    for sb in range(4):
+        assert np.all(got[8 * sb:8 * sb + 4] == exp_lo[sb])
+        assert np.all(got[8 * sb + 4:8 * sb + 8] == exp_hi[sb])
+
+
+def test_kat_step_literal_is_0_015873(oracle):
+    # lo = -7.43359375, hi = 79.25 (fp16), s = 1, lv = 42.  d = 86.68359375 (exact),
+    # q = 21.6708984375, rlo = lo, range = q.  With 1/63: w = lo + q*2/3 = 7.013671875
+    # = 7 + 3.5 * 2^-8, a tie between fp16 mantissas 771 and 772 -> even -> 0x4704.
+    # With the 0.015873 literal w sits just below the tie -> 0x4703.
+    qt = _block_qt([-7.43359375], [79.25], [1 * 0x55], np.full((1, 32), 42), [0])
+    got = _r64(oracle, qt, _bases(1))[0]
+    assert np.all(got == 0x4703)
+
+
+def test_kat_binary32_subtract_and_double_rounding(oracle):
+    # lo = -0.00014019012451171875, hi = 1089 (fp16), s = 2, lv = 0, so w = rlo = hi - q.
+    # hi - lo = 1089.00014019... rounds in binary32 (spacing 2^-13) to 1089 + 2^-13,
+    # q = 272.250030517578125, w = 816.75 - 2^-15: a binary32 tie between 816.75 - 2^-14
+    # (odd) and 816.75 (even) -> 816.75, itself an fp16 tie between 816.5 (mantissa
+    # 609) and 817 (610) -> 817 = 0x6262.  An exact (float64) subtraction gives
+    # 816.7499649... -> 816.74993896484375 -> 816.5 = 0x6261, and a direct f64->f16
+    # rounding of 816.75 - 2^-15 also gives 0x6261.
+    qt = _block_qt([-0.00014019012451171875], [1089.0], [2 * 0x55], np.zeros((1, 32)), [0])
+    got = _r64(oracle, qt, _bases(1))[0]
+    assert np.all(got == 0x6262)
+
+
+def test_kat_pca_terms(oracle):
+    # lo = hi = 0 (degenerate, core ~ 1e-10 * lv, negligible), coeff = 0x87:
+    # c0 = signed4(7) = 7, c1 = signed4(8) = -8.  s0 = 1/8, b0 = 1/4 -> +7/32;
+    # s1 = 1/16, b1 = 1/4 -> -8/64 = -1/8.  w = 7/32 - 1/8 = 3/32 = 0.09375 -> 0x2E00.
+    # Swapping c0/c1 gives -9/64, dropping either term gives 7/32 or -1/8.
+    qt = _block_qt([0.0], [0.0], [0], np.zeros((1, 32)), [0x87])
+    got = _r64(oracle, qt, _bases(1, b0=0.25, b1=0.25, s0=0.125, s1=0.0625))[0]
+    assert np.all(got == 0x2E00)
+
+
+def test_kat_subnormal_endpoints(oracle):
+    # lo = 3 * 2^-24, hi = 200 * 2^-24 (fp16 subnormals), s = 0, lv = 63:
+    # step * 63 = 197 * 2^-24 * 0.999999 -> w = 199.999803 * 2^-24 -> 200 * 2^-24 = 0x00C8;
+    # lv = 0 -> 3 * 2^-24 = 0x0003; lv = 32 -> 3 + 197*32/63*0.999999 = 103.063 -> 103 = 0x0067.
+    lv = np.zeros((1, 32), dtype=np.int64)
+    lv[0, 1] = 63
+    lv[0, 2] = 32
+    qt = _block_qt([3 * 2.0 ** -24], [200 * 2.0 ** -24], [0], lv, [0])
+    got = _r64(oracle, qt, _bases(1))[0]
+    assert got[0] == 0x0003 and got[1] == 0x00C8 and got[2] == 0x0067
+
+
+def test_kat_reversed_range_floors_step(oracle):
+    # dmin > dmax: every range is negative, so step < 1e-10 -> 1e-10 and w = rlo.
+    # lo = 1, hi = 0.5: q = -0.125; s0 -> 1, s1 -> 1, s2 -> hi - q = 0.625, s3 -> lo + q = 0.875.
+    cfg = 0 | (1 << 2) | (2 << 4) | (3 << 6)
+    got = _r64(oracle, _block_qt([1.0], [0.5], [cfg], np.full((1, 32), 63), [0]), _bases(1))[0]
+    got = got.view(np.float16)
+    for sb, v in enumerate([1.0, 1.0, 0.625, 0.875]):
+        assert np.all(got[8 * sb:8 * sb + 8] == v)
+
+
+# -------------------------------------------------------- brute force and exactness
+
+def _fuzz(rng, n):
+    import sys
+    sys.path.insert(0, os.path.join(HERE, "golden"))
+    from make_golden import fuzz_blocks
+    return fuzz_blocks(rng, n, 8)
+
+
+def test_brute_force_c_vs_independent_numpy(oracle):
+    rng = np.random.default_rng(11)
+    qt, bi = _fuzz(rng, 400)                      # 3200 blocks, 102400 weights
+    c_unfused = oracle.dequant_r64(qt, bi, fused=False, blocks_only=True).view(np.uint16)
+    numpy_unfused = oracle.dequant_r64_numpy(qt, bi).view(np.uint16)
+    assert np.array_equal(c_unfused, numpy_unfused)
+    c_fused = oracle.dequant_r64(qt, bi, fused=True, blocks_only=True).view(np.uint16)
+    # fused and unfused differ only if a 1-ulp binary64 change crosses a binary32 tie
+    assert np.count_nonzero(c_fused != c_unfused) == 0
+
+
+def test_every_strategy_level_pair_grid(oracle):
+    # every (strategy, level) on a grid of fp16 endpoint pairs, C vs numpy
+    rng = np.random.default_rng(12)
+    pairs = []
+    for e in range(-24, 12, 3):
+        for _ in range(6):
+            a = np.float16(rng.standard_normal() * 2.0 ** e)
+            b = np.float16(float(a) + abs(rng.standard_normal()) * 2.0 ** e)
+            pairs.append((a, b))
+    n = len(pairs) * 4 * 2
+    dmin, dmax, cfg, lv = [], [], [], []
+    for a, b in pairs:
+        for s in range(4):
+            for half in range(2):
+                dmin.append(a); dmax.append(b); cfg.append(s * 0x55)
+                lv.append((np.arange(32) + 32 * half) % 64)
+    qt = _block_qt(dmin, dmax, cfg, np.array(lv), rng.integers(0, 256, n))
+    bi = _bases(n, 0.1, -0.2, 1e-3, 2e-3)
+    a = _r64(oracle, qt, bi, fused=False)
+    b = oracle.dequant_r64_numpy(qt, bi).view(np.uint16)
+    assert np.array_equal(a, b)
+
+
+def test_fused_form_exact_rationals(oracle):
+    rng = np.random.default_rng(13)
+    qt, bi = _fuzz(rng, 40)
+    got = oracle.dequant_r64(qt, bi, fused=True, blocks_only=True)
+    lv = oracle.unpack_levels(qt["levels_hi"], qt["levels_lo"])
+    n_cb = qt["n_cb"]
+    bad = 0
+    for bid in range(0, qt["n_blocks"], 3):
+        kb = bid % n_cb
+        for t in range(0, 32, 3):
+            e = oracle.dequant_r64_exact_weight(
+                qt["dmin"][bid], qt["dmax"][bid], int(qt["config"][bid]), int(qt["coeff"][bid, 0]),
+                int(lv[bid, t]), t, bi["scales"][kb, 0], bi["scales"][kb, 1],
+                bi["data"][kb, t], bi["data"][kb, 32 + t])
+            bad += int(e.view(np.uint16) != got[bid, t].view(np.uint16))
+    assert bad == 0
+
+
+def test_r32_variant_differs_in_last_bit_only_rarely(oracle):
+    # The reference's float32 .cu decode is not the canonical recipe; it disagrees
+    # with R64 on a small fraction of weights and by at most a few fp16 ulps.
+    g = np.random.default_rng(5)
+    W = (g.standard_normal((256, 256)) * 0.02).astype(np.float16)
+    qt, bi = oracle.quantize(W)
+    a = oracle.dequant_r64(qt, bi).view(np.uint16).astype(np.int32)
+    b = oracle.dequant_r32(qt, bi).view(np.uint16).astype(np.int32)
+    frac = np.count_nonzero(a != b) / a.size
+    assert frac < 5e-3
+    assert np.max(np.abs(a - b)) <= 2
+
+
+# ----------------------------------------------------------------- golden fixtures
+
+def _golden():
+    return np.load(os.path.join(HERE, "golden", "sx8_golden.npz"))
+
+
+def _qt_from_golden(g, p):
+    out_f, in_f, n_cb = (int(v) for v in g[p + "shape"])
+    qt = {"shape": (out_f, in_f), "orig_shape": (out_f, in_f), "n_blocks": out_f * n_cb,
+          "n_cb": n_cb}
+    for k in ("dmin", "dmax", "config", "levels_hi", "levels_lo", "coeff"):
+        qt[k] = g[p + k]
+    return qt, {"n_cb": n_cb, "data": g[p + "basis"], "scales": g[p + "scales"]}
+
+
+@pytest.mark.parametrize("prefix", ["fuzz_", "q_"])
+def test_oracle_reproduces_golden(oracle, prefix):
+    g = _golden()
+    qt, bi = _qt_from_golden(g, prefix)
+    got = oracle.dequant_r64(qt, bi).view(np.uint16)
+    out_f, in_f = qt["shape"]
+    exp = g[prefix + "w16"].reshape(out_f, in_f)
+    assert np.array_equal(got, exp)
+
+
+def test_golden_quantized_weight_is_close(oracle):
+    g = _golden()
+    qt, bi = _qt_from_golden(g, "q_")
+    W = g["q_weight"].view(np.float16).astype(np.float32)
+    Wq = oracle.dequant_r64(qt, bi).astype(np.float32)
+    assert np.max(np.abs(W - Wq)) < 2e-3
+
+
+# ------------------------------------------------------------------ layout (a3)
+
+def test_v44_layout_invariants(oracle):
+    from prepare_v44 import extract_levels_v43, extract_levels_v44, to_v44, verify
+    g = _golden()
+    qt, bi = _qt_from_golden(g, "q_")
+    for aligned in (False, True):
+        mine = to_v44(qt, bi, hdr_aligned=aligned)
+        ref = oracle.to_v44(qt, bi, hdr_aligned=aligned)
+        assert np.array_equal(mine["hdr"], ref["hdr"])
+        assert np.array_equal(mine["levels"], ref["levels"])
+        hb = 8 if aligned else 6
+        assert mine["hdr"].shape == (qt["n_blocks"], hb)
+        assert mine["levels"].nbytes + qt["n_blocks"] * 6 == qt["n_blocks"] * 30
+    assert verify(qt, bi)
+    out_f, n_cb = qt["shape"][0], qt["n_cb"]
+    lv43 = extract_levels_v43(qt).reshape(out_f, n_cb, 32).transpose(1, 0, 2).reshape(-1, 32)
+    assert np.array_equal(lv43, extract_levels_v44(to_v44(qt, bi)))
+    # header row of block (n=5, kb=2) sits at kb-major row 2*N + 5
+    hdr = to_v44(qt, bi)["hdr"]
+    row = hdr[2 * out_f + 5]
+    bid = 5 * n_cb + 2
+    assert row[0:2].view(np.uint16)[0] == np.asarray(qt["dmin"]).view(np.uint16)[bid]
+    assert row[4] == qt["config"][bid] and row[5] == qt["coeff"].reshape(-1)[bid]
+
+
+def test_v44_device_builder_on_cpu(oracle):
+    torch = pytest.importorskip("torch")
+    from prepare_v44 import to_v44_device
+    g = _golden()
+    qt, bi = _qt_from_golden(g, "fuzz_")
+    for aligned in (False, True):
+        h, lv, bs, sc = to_v44_device(qt, bi, hdr_aligned=aligned, device="cpu")
+        ref = oracle.to_v44(qt, bi, hdr_aligned=aligned)
+        assert np.array_equal(h.numpy(), ref["hdr"])
+        assert np.array_equal(lv.numpy(), ref["levels"])
+        assert torch.equal(bs, torch.from_numpy(ref["bases"]))
+
+
+# --------------------------------------------------------------------- Z and GEMV
+
+def test_z_tree_matches_float64(oracle):
+    rng = np.random.default_rng(3)
+    g = _golden()
+    _, bi = _qt_from_golden(g, "fuzz_")
+    X = rng.standard_normal((3, bi["n_cb"] * 32)).astype(np.float16)
+    Z = oracle.z44(X.astype(np.float64), bi)
+    Z32 = oracle.z44_f32_tree(X, bi)
+    assert np.max(np.abs(Z - Z32)) <= 1e-6 * (1 + np.max(np.abs(Z)))
+
+
+def test_gemv_reference_identity(oracle):
+    # the Z reformulation (SPEC.md:49-61) equals the per-weight PCA product
+    rng = np.random.default_rng(4)
+    g = _golden()
+    qt, bi = _qt_from_golden(g, "q_")
+    from prepare_v44 import decode_v44_numpy, to_v44
+    x = rng.standard_normal(qt["shape"][1]).astype(np.float16)
+    W = oracle.dequant_r64(qt, bi)
+    y = oracle.gemm_f64(x[None, :], W)[0]
+    v44 = to_v44(qt, bi)
+    for n in (0, 17, 95):
+        assert abs(decode_v44_numpy(v44, x.astype(np.float64), n) - y[n]) <= 2e-3 * np.max(np.abs(y))
