@@ -24,7 +24,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # hipcc flags: gfx950 only, no packed-fp32 instruction selection (those forms have
 # given silent wrong results on the target pool), IEEE denormals, no fast-math.
 HIP_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "--offload-arch=gfx950", "-mcode-object-version=5", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fno-fast-math", "-fno-gpu-flush-denormals-to-zero",
     "-Wall", "-Wno-unused-function",
@@ -70,18 +70,37 @@ def lib_path() -> str:
     return os.environ.get("SX8_HIP_LIB", LIB_PATH)
 
 
+def _hip_runtimes_loaded():
+    """Distinct libamdhip64 files mapped into this process."""
+    try:
+        with open("/proc/self/maps") as f:
+            return sorted({ln.split()[-1] for ln in f if "libamdhip64" in ln})
+    except OSError:
+        return []
+
+
 def lib():
-    """Load the HIP library once; raise RuntimeError if it is missing or stale."""
+    """Load the HIP library once; raise RuntimeError if it is missing or stale.
+
+    torch is imported first: it maps its bundled HIP runtime (SONAME libamdhip64.so.7),
+    and the dynamic linker then binds this library's libamdhip64.so.7 dependency to
+    that same copy.  Two HIP runtimes in one process (torch's and /opt/rocm's) do not
+    share devices, streams or allocations, so that case is refused outright."""
     global _lib
     if _lib is not None:
         return _lib
     with _lock:
         if _lib is None:
+            import torch  # noqa: F401  (maps torch's HIP runtime before ours)
             path = lib_path()
             if not os.path.exists(path):
                 raise RuntimeError(f"S-X8 HIP library not found at {path}; run "
                                    "__graft_entry__.build() (or _sx8lib.build()) first")
             L = ctypes.CDLL(path)
+            runtimes = _hip_runtimes_loaded()
+            if len(runtimes) > 1:
+                raise RuntimeError("two HIP runtimes are loaded in this process: "
+                                   + ", ".join(runtimes))
             for name, res, args in SIGNATURES:
                 fn = getattr(L, name)
                 fn.restype = res

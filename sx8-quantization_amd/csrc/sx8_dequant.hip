@@ -62,9 +62,8 @@ __global__ __launch_bounds__(kThreads) void k_dequant_split(
     load_basis(basis, scales, kb, sb, b0, b1, s0, s1);
     const uint32_t H = *reinterpret_cast<const uint32_t*>(hi + bid * 16 + 4 * sb);
     const uint32_t P16 = *reinterpret_cast<const uint16_t*>(lo + bid * 8 + 2 * sb);
-    const uint32_t P = (P16 & 0xFFu) | ((P16 & 0xFF00u) << 8);
     uint32_t w[4];
-    sx8_r64_subblock(sx8_h2f(dmin[bid]), sx8_h2f(dmax[bid]), config[bid], coeff[bid], sb, H, P,
+    sx8_r64_subblock(sx8_h2f(dmin[bid]), sx8_h2f(dmax[bid]), config[bid], coeff[bid], sb, H, P16,
                      b0, b1, s0, s1, w);
     store8(out + n * in_f, kb * 32 + 8 * sb, in_f, vec_ok, w);
 }
@@ -92,11 +91,10 @@ __global__ __launch_bounds__(kThreads) void k_gather_v44(
     const uint32_t H = *reinterpret_cast<const uint32_t*>(lv + 4 * sb);
     const uint32_t Pw = *reinterpret_cast<const uint32_t*>(lv + 16 + 4 * (sb >> 1));
     const uint32_t P16 = (sb & 1) ? (Pw >> 16) : (Pw & 0xFFFFu);
-    const uint32_t P = (P16 & 0xFFu) | ((P16 & 0xFF00u) << 8);
     double b0[8], b1[8], s0, s1;
     load_basis(basis, scales, kb, sb, b0, b1, s0, s1);
     uint32_t w[4];
-    sx8_r64_subblock(sx8_h2f(d0), sx8_h2f(d1), cfg, cf, sb, H, P, b0, b1, s0, s1, w);
+    sx8_r64_subblock(sx8_h2f(d0), sx8_h2f(d1), cfg, cf, sb, H, P16, b0, b1, s0, s1, w);
     store8(out + t * K, kb * 32 + 8 * sb, K, vec_ok, w);
 }
 

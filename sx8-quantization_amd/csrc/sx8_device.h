@@ -20,24 +20,25 @@ typedef _Float16 sx8_half2 __attribute__((ext_vector_type(2)));
 typedef float sx8_float4 __attribute__((ext_vector_type(4)));
 
 // fp16 bit pattern (low 16 bits) -> float, exact.
-__device__ __forceinline__ float sx8_h2f(uint32_t bits) {
+__host__ __device__ __forceinline__ float sx8_h2f(uint32_t bits) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
 }
 
-__device__ __forceinline__ int sx8_sext4(uint32_t v) {
+__host__ __device__ __forceinline__ int sx8_sext4(uint32_t v) {
     return (int)((v & 0xFu) ^ 0x8u) - 8;      // 0..7 -> 0..7, 8..15 -> -8..-1
 }
 
 // 6-bit level of weight i (0..7) of a sub-block, from its 4 hi-nibble bytes H (weight i
 // at bits 4i) and its 2 lo-quad bytes P (weight i at bits 8*(i>>2) + 6 - 2*(i&3)).
 // This is kernel_sx8_v43.py:23-25 restricted to one sub-block.
-__device__ __forceinline__ uint32_t sx8_level(uint32_t H, uint32_t P, int i) {
+__host__ __device__ __forceinline__ uint32_t sx8_level(uint32_t H, uint32_t P, int i) {
     uint32_t nib = (H >> (4 * i)) & 0xFu;
     uint32_t qua = (P >> (8 * (i >> 2) + 6 - 2 * (i & 3))) & 0x3u;
     return (nib << 2) | qua;
 }
 
-// R64 decode of one 8-weight sub-block `sb` of a block.  lo_f/hi_f are the fp16
+// R64 decode of one 8-weight sub-block `sb` of a block (host-callable too, so the CPU
+// tests can run this exact function against the oracle).  lo_f/hi_f are the fp16
 // endpoints widened to float, b0/b1 the sub-block's slice of the two PCA bases and
 // s0/s1 the scales, all widened to double (exact).  Writes the 8 fp16 results as
 // four packed dwords, weight 2j in the low half of out[j].
@@ -52,7 +53,7 @@ __device__ __forceinline__ uint32_t sx8_level(uint32_t H, uint32_t P, int i) {
 // kPca = false drops the two PCA terms (the "core" weights rlo + step*lv), used when
 // the PCA term is applied at the GEMM output from a caller-supplied Z.
 template <bool kPca = true>
-__device__ __forceinline__ void sx8_r64_subblock(float lo_f, float hi_f, uint32_t cfg,
+__host__ __device__ __forceinline__ void sx8_r64_subblock(float lo_f, float hi_f, uint32_t cfg,
                                                  uint32_t coeff, int sb, uint32_t H,
                                                  uint32_t P, const double* b0,
                                                  const double* b1, double s0, double s1,

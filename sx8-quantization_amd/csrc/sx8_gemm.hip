@@ -61,8 +61,7 @@ __device__ __forceinline__ void decode_operand(const uint8_t* __restrict__ hdr,
         H = *reinterpret_cast<const uint32_t*>(lv + 4 * sb);
         P16 = *reinterpret_cast<const uint16_t*>(lv + 16 + 2 * sb);
     }
-    const uint32_t P = (P16 & 0xFFu) | ((P16 & 0xFF00u) << 8);
-    sx8_r64_subblock<MODE != kCore>(sx8_h2f(d0), sx8_h2f(d1), cfg, cf, sb, H, P, b0, b1, s0, s1, w);
+    sx8_r64_subblock<MODE != kCore>(sx8_h2f(d0), sx8_h2f(d1), cfg, cf, sb, H, P16, b0, b1, s0, s1, w);
 }
 
 __device__ __forceinline__ void load_x_tile(const uint16_t* __restrict__ X, int M, int64_t ldx,

@@ -96,10 +96,14 @@ _BUF = {}
 
 
 def _buf(key, shape):
-    b = _BUF.get(key)
-    if b is None or b.shape != tuple(shape) or b.device != DEV:
-        b = torch.empty(*shape, dtype=torch.float32, device=DEV)
-        _BUF[key] = b
+    """Pooled float32 device buffer per key on the current device.  (The reference's
+    check `b.device != DEV` compared cuda:0 with cuda and so reallocated on every call;
+    here the pool is reused as its comment intended.)"""
+    dev = torch.device("cuda", torch.cuda.current_device())
+    b = _BUF.get((key, dev.index))
+    if b is None or b.shape != tuple(shape):
+        b = torch.empty(*shape, dtype=torch.float32, device=dev)
+        _BUF[(key, dev.index)] = b
     return b
 
 
