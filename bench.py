@@ -10,9 +10,10 @@ before timing; the step cycles through --copies distinct copies of the layer (>1
 total by default) so the 256 MB Infinity Cache cannot serve repeats.
 
 Timing: a GPU delay kernel is queued first so the host enqueues the whole timed
-region ahead of the GPU; each GEMV is bracketed by HIP events on the launch stream
-(torch's current stream, which the kernels are launched on), giving the per-launch
-kernel durations of the roofline; start/end events bracket the K steps.
+region ahead of the GPU.  The timed region (K steps back to back) is bracketed by two
+HIP events on the launch stream (torch's current stream, which the kernels use).  A
+second pass of the same K steps brackets every launch with an event pair; its mean is
+the per-launch kernel duration used for the roofline.
 """
 import argparse
 import json
@@ -83,6 +84,43 @@ def build_layer(torch, dev, hdr_bytes):
     return layer
 
 
+class HipEvents:
+    """Timing events straight from the HIP runtime torch already loaded, created with
+    hipEventDisableSystemFence so a record does not flush system-scope caches (torch's
+    default events add several microseconds per record).  Records go to `stream`."""
+
+    def __init__(self, n, stream):
+        import ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so.7")        # binds to the loaded runtime
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.c_void_p, ctypes.c_uint]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.stream = stream
+        self.ev = []
+        flags = 0x20000000                                 # hipEventDisableSystemFence
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            if self.hip.hipEventCreateWithFlags(ctypes.byref(e), flags) != 0:
+                raise RuntimeError("hipEventCreateWithFlags failed")
+            self.ev.append(e)
+        self._f = ctypes.c_float()
+        self._ctypes = ctypes
+
+    def record(self, i):
+        if self.hip.hipEventRecord(self.ev[i], self.stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def ms(self, a, b):
+        if self.hip.hipEventElapsedTime(self._ctypes.byref(self._f), self.ev[a], self.ev[b]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return self._f.value
+
+    def close(self):
+        for e in self.ev:
+            self.hip.hipEventDestroy(e)
+
+
 def bench_gemv(torch, L, layer, args):
     import ctypes
     dev = torch.device("cuda:0")
@@ -93,6 +131,8 @@ def bench_gemv(torch, L, layer, args):
     xs = {K: torch.randn(K, generator=g).half().to(dev) for K in {t["K"] for t in layer}}
     ys = [torch.empty(t["N"], dtype=torch.float32, device=dev) for t in layer]
     zs = [torch.empty(t["n_cb"], 2, dtype=torch.float32, device=dev) for t in layer]
+    wss = [torch.empty(L.lib().sx8_gemv_workspace_bytes(t["n_cb"]) // 4, dtype=torch.float32,
+                       device=dev) for t in layer]
     st = L.stream(dev)
     calls = []
     for r in range(R):
@@ -100,50 +140,59 @@ def bench_gemv(torch, L, layer, args):
         for i, t in enumerate(layer):
             h, lv = copies[r][i]
             step.append((L.ptr(xs[t["K"]]), L.ptr(h), L.ptr(lv), args.hdr_bytes, L.ptr(t["bas"]),
-                         L.ptr(t["sca"]), ctypes.c_void_p(None), L.ptr(zs[i]), t["N"], t["n_cb"],
-                         L.ptr(ys[i]), st))
+                         L.ptr(t["sca"]), ctypes.c_void_p(None), ctypes.c_void_p(None), t["N"], t["n_cb"],
+                         L.ptr(ys[i]), L.ptr(wss[i]), wss[i].numel() * 4, st))
         calls.append(step)
     fn = L.lib().sx8_gemv
     step_bytes = sum(packed_bytes(t["N"], t["K"]) for t in layer)
     log(f"gemv: {R} copies x {step_bytes / 1e6:.1f} MB = {R * step_bytes / 1e9:.2f} GB resident")
+    nL = len(layer)
+    K = args.steps
+    ev = HipEvents(2 + 2 * nL * K, st)
 
-    def run_step(s, evs=None):
+    def run_step(s, pairs=False):
         for i, a in enumerate(calls[s % R]):
-            if evs is not None:
-                evs[2 * i].record()
+            if pairs:
+                ev.record(2 + 2 * (s * nL + i))
             rc = fn(*a)
             if rc != 0:
                 raise RuntimeError(L.lib().sx8_last_error().decode())
-            if evs is not None:
-                evs[2 * i + 1].record()
+            if pairs:
+                ev.record(3 + 2 * (s * nL + i))
 
     for s in range(args.warmup):
         run_step(s)
     torch.cuda.synchronize()
 
-    K = args.steps
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * len(layer))] for _ in range(K)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # timed region: K steps back to back, bracketed by two events (no per-launch events)
     torch.cuda.synchronize()
     gpu_delay(torch, 50)                     # keep the GPU busy while the host enqueues
-    start.record()
+    ev.record(0)
     for s in range(K):
-        run_step(s, evs[s])
-    end.record()
+        run_step(s)
+    ev.record(1)
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    per_shape_ms = [0.0] * len(layer)
+    total_ms = ev.ms(0, 1)
+
+    # kernel-duration pass: the same K steps with an event pair around every launch
+    gpu_delay(torch, 50)
     for s in range(K):
-        for i in range(len(layer)):
-            per_shape_ms[i] += evs[s][2 * i].elapsed_time(evs[s][2 * i + 1])
+        run_step(s, pairs=True)
+    torch.cuda.synchronize()
+    per_shape_ms = [0.0] * nL
+    for s in range(K):
+        for i in range(nL):
+            b = 2 + 2 * (s * nL + i)
+            per_shape_ms[i] += ev.ms(b, b + 1)
+    ev.close()
     kern_ms = sum(per_shape_ms)
     out = {
         "ms_per_step": total_ms / K,
         "value_gbs": step_bytes * K / (total_ms * 1e-3) / 1e9,
         "kernel_ms_total": kern_ms,
-        "launches": K * len(layer),
-        "avg_launch_us": kern_ms * 1e3 / (K * len(layer)),
-        "bytes_per_launch": step_bytes / len(layer),
+        "launches": K * nL,
+        "avg_launch_us": kern_ms * 1e3 / (K * nL),
+        "bytes_per_launch": step_bytes / nL,
         "achieved_gbs": step_bytes * K / (kern_ms * 1e-3) / 1e9,
         "per_shape": {t["name"]: {
             "us": per_shape_ms[i] * 1e3 / K,
@@ -311,7 +360,7 @@ def main():
             "frac_of_hbm_peak": round(gv.get("value_gbs", 0.0) / HBM_PEAK_GBS, 4),
         },
         "roofline": {
-            "kernel": "k_gemv<6,false> (sx8_gemv)" if args.hdr_bytes == 6 else "k_gemv<8,false>",
+            "kernel": f"k_gemv_panel<{args.hdr_bytes},1> (sx8_gemv)",
             "bound": "hbm",
             "achieved": round(gv.get("achieved_gbs", 0.0), 1),
             "peak": HBM_PEAK_GBS,

@@ -77,14 +77,20 @@ int32_t sx8_compute_z(const uint16_t* X, int64_t M, int64_t ldx, const float* ba
 
 /* M = 1 decode GEMV on the v4.4 layout: Y[n] = sum_k X[k] W[n, k], float32 result.
  * If Z_in != NULL it is used as the PCA precompute (n_cb, 2) (the two-launch form,
- * decode1_v44 at cuda/sx8_decode1_v3.cu:197-221); otherwise Z is computed inside the
- * launch from basis/scales and, when Z_out != NULL, also written there (the combined
- * form, decode1_v44_combined at :223-246).  X holds n_cb*32 fp16 values.
+ * decode1_v44 at cuda/sx8_decode1_v3.cu:197-221); otherwise Z is computed from
+ * basis/scales with the reference's summation tree and, when Z_out != NULL, also written
+ * there (the combined form, decode1_v44_combined at :223-246).  X holds n_cb*32 fp16
+ * values (16-byte aligned).  `workspace` (>= sx8_gemv_workspace_bytes(n_cb) bytes, 16-byte aligned)
+ * receives the per-call activation table; NULL uses a library-owned per-device buffer
+ * (allocated on first use; calls overlapping on one device must pass their own).
  * Tolerance against the float64 yardstick: max|dY| / max|Y| <= 1e-3. */
 int32_t sx8_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels,
                  int32_t hdr_bytes, const float* basis, const float* scales,
                  const float* Z_in, float* Z_out, int64_t N, int64_t n_cb, float* Y,
-                 void* stream);
+                 void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes sx8_gemv needs for n_cb K blocks (112 per block). */
+int64_t sx8_gemv_workspace_bytes(int64_t n_cb);
 
 /* Prefill GEMM Y (M, N) float32 = X (M, ldx) fp16 . W^T on the v4.4 layout.
  * Each weight tile is dequantized with R64 (bit-exact fp16) into MFMA operands and

@@ -1,5 +1,5 @@
 // sx8_abi.hip -- library-wide C-ABI plumbing: version, last-error message, and the
-// per-device GEMV workspace.
+// per-device fallback workspace.
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
@@ -12,10 +12,8 @@ namespace {
 thread_local char g_msg[512] = "";
 
 struct Workspace {
-    float* partial = nullptr;
-    uint32_t* counters = nullptr;
-    int64_t partial_cap = 0;
-    int64_t counter_cap = 0;
+    void* ptr = nullptr;
+    int64_t cap = 0;
 };
 std::mutex g_ws_mutex;
 std::vector<Workspace> g_ws;
@@ -40,36 +38,25 @@ int32_t check_launch(const char* what) {
     return ok();
 }
 
-int32_t gemv_workspace(int64_t partial_floats, int64_t n_counters, float** partial,
-                       uint32_t** counters) {
+int32_t device_workspace(int64_t bytes, void** ptr) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return fail(SX8_ERR_HIP, "hipGetDevice failed");
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
     Workspace& w = g_ws[dev];
-    if (w.partial_cap < partial_floats) {
-        if (w.partial) (void)hipFree(w.partial);
-        w.partial = nullptr;
-        w.partial_cap = 0;
-        const int64_t cap = partial_floats + (partial_floats >> 1) + 1024;
-        if (hipMalloc(reinterpret_cast<void**>(&w.partial), cap * sizeof(float)) != hipSuccess)
-            return fail(SX8_ERR_HIP, "hipMalloc of %lld GEMV partials failed", (long long)cap);
-        w.partial_cap = cap;
+    if (w.cap < bytes) {
+        if (w.ptr) {
+            (void)hipDeviceSynchronize();   // earlier launches may still read it
+            (void)hipFree(w.ptr);
+        }
+        w.ptr = nullptr;
+        w.cap = 0;
+        const int64_t cap = ((bytes + (bytes >> 1)) + 4095) & ~int64_t(4095);
+        if (hipMalloc(&w.ptr, cap) != hipSuccess)
+            return fail(SX8_ERR_HIP, "hipMalloc of %lld workspace bytes failed", (long long)cap);
+        w.cap = cap;
     }
-    if (w.counter_cap < n_counters) {
-        if (w.counters) (void)hipFree(w.counters);
-        w.counters = nullptr;
-        w.counter_cap = 0;
-        const int64_t cap = n_counters + (n_counters >> 1) + 256;
-        if (hipMalloc(reinterpret_cast<void**>(&w.counters), cap * sizeof(uint32_t)) != hipSuccess)
-            return fail(SX8_ERR_HIP, "hipMalloc of %lld GEMV counters failed", (long long)cap);
-        // Synchronous clear: the counters start at zero and every launch leaves them there.
-        if (hipMemset(w.counters, 0, cap * sizeof(uint32_t)) != hipSuccess)
-            return fail(SX8_ERR_HIP, "hipMemset of GEMV counters failed");
-        w.counter_cap = cap;
-    }
-    *partial = w.partial;
-    *counters = w.counters;
+    *ptr = w.ptr;
     return SX8_OK;
 }
 

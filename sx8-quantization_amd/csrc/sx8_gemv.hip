@@ -2,46 +2,73 @@
 //
 // Reference roles: compute_z44 / compute_z44_batch (cuda/sx8_decode1_v3.cu:44-65,
 // cuda/sx8_gemm_compact.cu:28-50) and decode1_v44_kernel (cuda/sx8_decode1_v3.cu:75-167)
-// with its combined wrapper (:223-246).
+// with its wrappers decode1_v44 / decode1_v44_combined (:197-246).
 //
 // GEMV design (gfx950, HBM-bound):
-//   * one lane per output column; a 256-thread work-group covers 64 consecutive
-//     columns and a contiguous range of K blocks (kb); its four waves take every
-//     fourth kb of that range.  In the kb-major layout a wave's loads for one kb are
-//     64 consecutive 24-byte level records and 64 consecutive header records.
-//   * the activation side of each kb (x pairs, per-sub-block sums of x, Z0/Z1) is
-//     computed once per work-group into LDS and read back as wave-uniform broadcasts.
-//   * the core dot sum_i x_i (rlo + step lv_i) is rewritten per 8-weight sub-block as
-//     (rlo - 64 step) * Sx + step * sum_i x_i (64 + lv_i): the levels are spliced into
-//     fp16 values 64 + lv (exponent 6, lv in mantissa bits 4..9) with two shifts and
-//     two and-or's per pair of weights, and v_dot2_f32_f16 does two MACs per op.
-//   * PCA is applied per block through Z (docs/SX8_FLASH_V4_3_SPEC.md:49-61).
-//   * small-N shapes split K across work-groups; partial sums go to a workspace and
-//     the last work-group to arrive for a column tile adds them in fixed order, so the
-//     result is deterministic (the reference rejected atomicAdd split-K for that
-//     reason).  The arrival counter is reset by that last work-group.
+//   * k_gemv_panel streams the weights.  A 512-thread work-group owns CT consecutive
+//     columns over the whole K: lane (c, j) = (column c, K slice j), c fastest, so for
+//     each kb the CT lanes of a slice read CT consecutive 24-byte level records and
+//     header records (contiguous runs in the kb-major layout) and slice j walks
+//     kb = j, j + S, ... (S = 512 / CT) four blocks per round.  Slices meet in LDS and
+//     are summed in slice order: nothing leaves a work-group before the final store,
+//     so there are no device-scope fences or atomics and results are deterministic.
+//   * every block's decode needs the activation side of its kb (x pairs, sub-block
+//     sums of x, splice biases, Z0/Z1): a 112-byte table entry per kb, built in LDS by
+//     each work-group while its first weight loads are in flight (one launch).  When
+//     the caller wants Z back (the combined entry point), k_kbinfo builds the table
+//     once with the reference's summation tree -- Z bit-identical to compute_z44 --
+//     and the panel kernel copies it in.
+//   * per 8-weight sub-block the core dot sum_i x_i (rlo + step lv_i) becomes
+//     rlo * Sx + step * (sum x lv) with sum x lv from fp16 "splices" and
+//     v_dot2_f32_f16 (see block_dot); PCA is applied per block through Z
+//     (docs/SX8_FLASH_V4_3_SPEC.md:49-61).
 #include "sx8_device.h"
 #include "sx8_host.h"
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kCols = 64;
-constexpr int kTargetGroups = 512;   // ~2 work-groups per CU on a 256-CU MI355X
-constexpr int kMaxKbPerGroup = 320;  // bounds the LDS staging (96 B per kb)
-
 struct KbInfo {
     uint32_t xp[16];  // (x[8sb+i], x[8sb+i+4]) as fp16 pairs, index 4*sb + i
-    float sx[4];      // sum of the sub-block's 8 x values
+    float sx[4];      // sum of the sub-block's 8 x values (left to right)
+    float nbias[4];   // -sum_i (x[8sb+i] + x[8sb+i+4]) * kSpliceBias[i] (see block_dot)
     float z[2];       // Z0, Z1
     float pad[2];
 };
-static_assert(sizeof(KbInfo) == 96, "KbInfo layout");
+static_assert(sizeof(KbInfo) == 112, "KbInfo layout");
+
+// Constant part of the fp16 splices of block_dot for weight pair i: nibble splice
+// (4096 for pairs 0, 2; 256 for pairs 1, 3) + quad splice (16, 64, 256, 1024).
+__device__ constexpr float kSpliceBias[4] = {4.f * 1024.f + 16.f, 4.f * 64.f + 64.f,
+                                             4.f * 1024.f + 256.f, 4.f * 64.f + 1024.f};
+
+// x pairs, sub-block sums and splice biases of one (kb, sb) from its 8 x values.
+__device__ __forceinline__ void fill_x_side(KbInfo& out, int sb, const uint4 xv) {
+#pragma clang fp contract(off)
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+    float xf[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xf[i] = sx8_h2f(xw[i >> 1] >> (16 * (i & 1)));
+    float s = 0.f, b = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += xf[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t a = (xw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;            // x[i]
+        const uint32_t c = (xw[(i + 4) >> 1] >> (16 * (i & 1))) & 0xFFFFu;      // x[i+4]
+        out.xp[4 * sb + i] = a | (c << 16);
+        b += (xf[i] + xf[i + 4]) * kSpliceBias[i];
+    }
+    out.sx[sb] = s;
+    out.nbias[sb] = -b;
+}
+
+constexpr int kPanelThreads = 512;
+constexpr int kUnroll = 4;
+constexpr int kLdsMaxKb = 640;     // table staged in LDS up to 60 KB, read from L2 beyond
 
 // Z of one (row, kb, j) with the reference's warp tree: products x_t * b_t, then
 // pairwise sums over lane offsets 16, 8, 4, 2, 1 (cuda/sx8_decode1_v3.cu:53-63),
-// then scale * sum.
+// then scale * sum.  One thread does the whole tree (used for M > 1 rows).
 __device__ __forceinline__ float z_tree(const uint16_t* __restrict__ x,
                                         const float* __restrict__ b, float scale) {
 #pragma clang fp contract(off)
@@ -68,16 +95,47 @@ __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ 
     Z[gid] = z_tree(X + m * ldx + kb * 32, basis + kb * 64 + 32 * j, scales[kb * 2 + j]);
 }
 
-// Level pair i (weights i and i+4 of a sub-block) as two fp16 values 64 + lv.
-// H: hi nibbles (weight w at bits 4w); P: lo quads spread so weights 0..3 sit in bits
-// 0..7 and weights 4..7 in bits 16..23 (weight w at bit 6 - 2*(w&3) of its byte).
-__device__ __forceinline__ uint32_t lv_pair(uint32_t H, uint32_t P, int i) {
-    uint32_t hs, ps;
-    if (i == 0)      { hs = H << 6; ps = P >> 2; }
-    else if (i == 1) { hs = H << 2; ps = P; }
-    else if (i == 2) { hs = H >> 2; ps = P << 2; }
-    else             { hs = H >> 6; ps = P << 4; }
-    return (hs & 0x03C003C0u) | (ps & 0x00300030u) | 0x54005400u;
+// Activation-side table, one 32-lane group per kb (8 kb per 256-thread block).
+// Lane t: product x_t * b_jt for j = 0, 1 and the xor tree (bit-identical Z); lanes
+// 0..15 build one x pair each, lanes 16..19 one sub-block sum each.
+template <bool kZGiven>
+__global__ __launch_bounds__(256) void k_kbinfo(const uint16_t* __restrict__ X,
+                                                const float* __restrict__ basis,
+                                                const float* __restrict__ scales,
+                                                const float* __restrict__ Zin,
+                                                float* __restrict__ Zout, int n_cb,
+                                                KbInfo* __restrict__ table) {
+#pragma clang fp contract(off)
+    const int t = threadIdx.x & 31;
+    const int kb = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const bool ok = kb < n_cb;                      // uniform across the 32-lane group
+    const int kbc = ok ? kb : n_cb - 1;
+    const uint16_t* x = X + (int64_t)kbc * 32;
+    KbInfo& out = table[kbc];
+    if constexpr (kZGiven) {
+        if (ok && t < 2) out.z[t] = Zin[(int64_t)kb * 2 + t];
+    } else {
+        float p0 = sx8_h2f(x[t]) * basis[(int64_t)kbc * 64 + t];
+        float p1 = sx8_h2f(x[t]) * basis[(int64_t)kbc * 64 + 32 + t];
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) {
+            p0 = p0 + __shfl_xor(p0, off, 32);
+            p1 = p1 + __shfl_xor(p1, off, 32);
+        }
+        if (ok && t == 0) {
+            const float z0 = scales[(int64_t)kb * 2] * p0;
+            const float z1 = scales[(int64_t)kb * 2 + 1] * p1;
+            out.z[0] = z0;
+            out.z[1] = z1;
+            if (Zout) {
+                Zout[(int64_t)kb * 2] = z0;
+                Zout[(int64_t)kb * 2 + 1] = z1;
+            }
+        }
+    }
+    if (!ok) return;
+    if (t < 4) fill_x_side(out, t, *reinterpret_cast<const uint4*>(x + 8 * t));
+    else if (t < 6) out.pad[t - 4] = 0.f;
 }
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -85,151 +143,300 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
                                   __builtin_bit_cast(sx8_half2, b), c, false);
 }
 
-template <int HB, bool kZGiven>
-__global__ __launch_bounds__(kThreads) void k_gemv(
-    const uint16_t* __restrict__ X, const uint8_t* __restrict__ hdr,
-    const uint8_t* __restrict__ levels, const float* __restrict__ basis,
-    const float* __restrict__ scales, const float* __restrict__ Zin, float* __restrict__ Zout,
-    float* __restrict__ Y, float* __restrict__ partial, uint32_t* __restrict__ counters,
-    int N, int n_cb, int kb_per) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    KbInfo* info = reinterpret_cast<KbInfo*>(smem);
-    float* red = reinterpret_cast<float*>(smem + sizeof(KbInfo) * kb_per);
+// fp32 contribution of one block (one column, one kb) to its output.
+// PCA through Z, then per sub-block rlo * Sx + step * sum_i x_i lv_i, with
+// rlo/rhi/step in the reference's float32 branchless form (cuda/sx8_decode1_v3.cu:
+// 108-117) and sum_i x_i lv_i = 4 * sum x nib + sum x quad computed from fp16 splices:
+// a nibble or quad is or-ed into the mantissa of an fp16 constant whose last mantissa
+// bit is worth the field's weight, e.g. (H & 0x000F000F) | 0x64006400 holds
+// (1024 + nib_0, 1024 + nib_4).  Pair i uses constants 1024/64/1024/64 for the
+// nibbles (bits 0, 4, 8, 12 of H after an 8-bit shift for pairs 2-3) and 16/64/256/1024
+// for the quads (bits 6, 4, 2, 0 of each spread lo byte); v_dot2_f32_f16 multiplies
+// two splices by an x pair, and the constant offsets, weighted by x, are the
+// per-sub-block `bias` of the activation table.  All spliced values are exact fp16.
+// Loop-invariant masks and byte selectors held in VGPRs: on gfx9 a VOP3 instruction
+// takes at most one scalar operand, so with the fp16 constants in SGPRs each splice
+// below is a single v_and_or_b32 and each quad spread a single v_perm_b32.
+struct SpliceK {
+    uint32_t n_lo, n_hi, q0, q1, q2, q3, sel_even, sel_odd;
+};
 
-    const int tile = blockIdx.x;
-    const int split = blockIdx.y;
-    const int S = gridDim.y;
-    const int kb0 = split * kb_per;
-    const int nkb = min(kb_per, n_cb - kb0);
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
+__device__ __forceinline__ SpliceK splice_consts() {
+    SpliceK k{0x000F000Fu, 0x00F000F0u, 0x00C000C0u, 0x00300030u,
+              0x000C000Cu, 0x00030003u, 0x0C010C00u, 0x0C030C02u};
+    asm volatile("" : "+v"(k.n_lo), "+v"(k.n_hi), "+v"(k.q0), "+v"(k.q1));
+    asm volatile("" : "+v"(k.q2), "+v"(k.q3), "+v"(k.sel_even), "+v"(k.sel_odd));
+    return k;
+}
 
-    // ---- stage the activation side of this work-group's kb range in LDS
-    for (int u = tid; u < nkb * 4; u += kThreads) {
-        const int kl = u >> 2, sb = u & 3;
-        const uint4 xv = *reinterpret_cast<const uint4*>(X + (int64_t)(kb0 + kl) * 32 + 8 * sb);
-        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-        float s = 0.f;
+// fp32 contribution of one block (one column, one kb) to its output: PCA through Z,
+// then per 8-weight sub-block rlo * Sx + step * sum_i x_i lv_i.
+//
+// sum_i x_i lv_i (lv = 4 nib + quad) comes from fp16 "splices": a field is or-ed into
+// the mantissa of an fp16 constant whose last mantissa bit is worth the field's
+// weight in lv, e.g. (H & 0x000F000F) | 0x6C006C00 = (4096 + 4 nib_0, 4096 + 4 nib_4)
+// (exponent 12: ulp 4).  Nibble pairs use 4096/256/4096/256 (bits 0/4 of H and of
+// H >> 8), quad pairs 16/64/256/1024 (bits 6/4/2/0 of each spread lo byte).  Eight
+// v_dot2_f32_f16 per sub-block multiply the splices by x pairs into one fp32 sum that
+// starts at -sum x * constants (the table's nbias), leaving sum x lv.  Every spliced
+// value is exact in fp16.
+//
+// Fast path (dmax >= dmin): rlo = lo + q * {0,0,3,1}[s], step = 0.015873 * (hi - lo)
+// * {1, 1/4, 1/4, 1/2}[s] (the strategy range widths), both looked up with bfe on
+// packed byte tables.  It matches the reference's float32 form (cuda/sx8_decode1_v3.cu:
+// 108-117) to rounding, except that the 1e-10 step floor is not applied: the floor
+// only binds when hi - lo < 1.3e-8, where it moves the block's contribution by at most
+// 1e-10 * sum|x| * 63.  Blocks with hi < lo or NaN endpoints, where the floor changes
+// the result, take block_dot_exact (see k_gemv_panel).
+__device__ __forceinline__ float block_dot_fast(float lo, float hi, uint32_t cfg, uint32_t cf,
+                                                const uint32_t H[4], const uint32_t Pw[2],
+                                                const KbInfo& ki, const SpliceK& k) {
+    const float d = hi - lo;
+    const float q = d * 0.25f;
+    const float cd = d * 0.015873f;
+    float acc = (float)sx8_sext4(cf) * ki.z[0] + (float)sx8_sext4(cf >> 4) * ki.z[1];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s += sx8_h2f(xw[i >> 1] >> (16 * (i & 1)));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t a = (xw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;             // x[i]
-            const uint32_t b = (xw[(i + 4) >> 1] >> (16 * (i & 1))) & 0xFFFFu;       // x[i+4]
-            info[kl].xp[4 * sb + i] = a | (b << 16);
-        }
-        info[kl].sx[sb] = s;
+    for (int sb = 0; sb < 4; ++sb) {
+        const uint32_t sh = ((cfg >> (2 * sb)) & 3u) << 3;             // 8 * strategy
+        const float k1 = (float)__builtin_amdgcn_ubfe(0x01030000u, sh, 8);   // 0,0,3,1
+        const int e = __builtin_amdgcn_sbfe((int)0xFFFEFE00u, sh, 8);        // 0,-2,-2,-1
+        const float rlo = lo + q * k1;
+        const float step = __builtin_ldexpf(cd, e);
+        const uint32_t h = H[sb];
+        const uint32_t h8 = h >> 8;
+        const uint32_t P = __builtin_amdgcn_perm(0u, Pw[sb >> 1], (sb & 1) ? k.sel_odd : k.sel_even);
+        const uint32_t* xp = ki.xp + 4 * sb;
+        float t = dot2((h & k.n_lo) | 0x6C006C00u, xp[0], ki.nbias[sb]);
+        t = dot2((h & k.n_hi) | 0x5C005C00u, xp[1], t);
+        t = dot2((h8 & k.n_lo) | 0x6C006C00u, xp[2], t);
+        t = dot2((h8 & k.n_hi) | 0x5C005C00u, xp[3], t);
+        t = dot2((P & k.q0) | 0x4C004C00u, xp[0], t);
+        t = dot2((P & k.q1) | 0x54005400u, xp[1], t);
+        t = dot2((P & k.q2) | 0x5C005C00u, xp[2], t);
+        t = dot2((P & k.q3) | 0x64006400u, xp[3], t);
+        acc = __builtin_fmaf(rlo, ki.sx[sb], acc);
+        acc = __builtin_fmaf(step, t, acc);
     }
-    for (int u = tid; u < nkb * 2; u += kThreads) {
-        const int kl = u >> 1, j = u & 1;
-        const int kb = kb0 + kl;
+    return acc;
+}
+
+// Same contribution with the reference's float32 rlo/rhi/step and its 1e-10 floor
+// (cuda/sx8_decode1_v3.cu:108-117), for waves holding a block with hi < lo or a NaN.
+__device__ __forceinline__ float block_dot_exact(float lo, float hi, uint32_t cfg, uint32_t cf,
+                                              const uint32_t H[4], const uint32_t Pw[2],
+                                              const KbInfo& ki, const SpliceK& k) {
+    const float q = (hi - lo) * 0.25f;
+    float acc = (float)sx8_sext4(cf) * ki.z[0] + (float)sx8_sext4(cf >> 4) * ki.z[1];
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+        const uint32_t s = (cfg >> (2 * sb)) & 3u;
+        const float k1 = (float)((0x1300u >> (4 * s)) & 0xFu);   // 0,0,3,1
+        const float k2 = (float)((0x1030u >> (4 * s)) & 0xFu);   // 0,3,0,1
+        const float rlo = lo + q * k1;
+        const float rhi = hi - q * k2;
+        float step = (rhi - rlo) * 0.015873f;
+        if (step < 1e-10f) step = 1e-10f;
+        const uint32_t h = H[sb];
+        const uint32_t h8 = h >> 8;
+        const uint32_t P = __builtin_amdgcn_perm(0u, Pw[sb >> 1], (sb & 1) ? k.sel_odd : k.sel_even);
+        const uint32_t* xp = ki.xp + 4 * sb;
+        float t = dot2((h & k.n_lo) | 0x6C006C00u, xp[0], ki.nbias[sb]);
+        t = dot2((h & k.n_hi) | 0x5C005C00u, xp[1], t);
+        t = dot2((h8 & k.n_lo) | 0x6C006C00u, xp[2], t);
+        t = dot2((h8 & k.n_hi) | 0x5C005C00u, xp[3], t);
+        t = dot2((P & k.q0) | 0x4C004C00u, xp[0], t);
+        t = dot2((P & k.q1) | 0x54005400u, xp[1], t);
+        t = dot2((P & k.q2) | 0x5C005C00u, xp[2], t);
+        t = dot2((P & k.q3) | 0x64006400u, xp[3], t);
+        acc += rlo * ki.sx[sb] + step * t;
+    }
+    return acc;
+}
+
+// One kb's raw records for one column: hd = {dmin | dmax << 16, config | coeff << 8},
+// lv = the 24 level bytes.
+template <int HB>
+__device__ __forceinline__ void load_block(const uint8_t* __restrict__ hdr,
+                                           const uint8_t* __restrict__ levels, int64_t bid,
+                                           uint32_t hd[2], uint2 lv[3]) {
+    if constexpr (HB == 8) {
+        const uint2 h = *reinterpret_cast<const uint2*>(hdr + bid * 8);
+        hd[0] = h.x;
+        hd[1] = h.y;
+    } else {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(hdr + bid * 6);
+        hd[0] = h[0] | ((uint32_t)h[1] << 16);
+        hd[1] = h[2];
+    }
+    const uint2* lp = reinterpret_cast<const uint2*>(levels + bid * 24);
+    lv[0] = lp[0];
+    lv[1] = lp[1];
+    lv[2] = lp[2];
+}
+
+// Activation table for all n_cb blocks, built by one work-group in its LDS: the x side
+// from one thread per (kb, sb), Z from one thread per (kb, j) (a left-to-right sum of
+// the 32 products, or a copy of Zin).  Used by the panel GEMV when no Z output is
+// requested; the entry point that must return Z runs k_kbinfo (reference tree) instead.
+template <bool kZGiven>
+__device__ __forceinline__ void stage_table(KbInfo* __restrict__ info,
+                                            const uint16_t* __restrict__ X,
+                                            const float* __restrict__ basis,
+                                            const float* __restrict__ scales,
+                                            const float* __restrict__ Zin, int n_cb) {
+    const int tid = threadIdx.x;
+    for (int u = tid; u < n_cb * 4; u += kPanelThreads)
+        fill_x_side(info[u >> 2], u & 3,
+                    *reinterpret_cast<const uint4*>(X + (int64_t)(u >> 2) * 32 + 8 * (u & 3)));
+    for (int u = tid; u < n_cb * 2; u += kPanelThreads) {
+        const int kb = u >> 1, jj = u & 1;
         float z;
         if constexpr (kZGiven) {
-            z = Zin[kb * 2 + j];
+            z = Zin[u];
         } else {
-            z = z_tree(X + (int64_t)kb * 32, basis + kb * 64 + 32 * j, scales[kb * 2 + j]);
-            if (Zout && tile == 0) Zout[kb * 2 + j] = z;
+            const uint4* xv = reinterpret_cast<const uint4*>(X + (int64_t)kb * 32);
+            const float4* bv = reinterpret_cast<const float4*>(basis + (int64_t)kb * 64 + 32 * jj);
+            float a = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 xx = xv[q];
+                const float4 b0 = bv[2 * q], b1 = bv[2 * q + 1];
+                a += sx8_h2f(xx.x) * b0.x + sx8_h2f(xx.x >> 16) * b0.y;
+                a += sx8_h2f(xx.y) * b0.z + sx8_h2f(xx.y >> 16) * b0.w;
+                a += sx8_h2f(xx.z) * b1.x + sx8_h2f(xx.z >> 16) * b1.y;
+                a += sx8_h2f(xx.w) * b1.z + sx8_h2f(xx.w >> 16) * b1.w;
+            }
+            z = scales[u] * a;
         }
-        info[kl].z[j] = z;
+        info[kb].z[jj] = z;
     }
-    __syncthreads();
+}
 
-    // ---- stream this column tile's blocks
-    const int n = tile * kCols + lane;
+// kMode: 0 = read the table k_kbinfo wrote to global memory; 1 = build it in LDS
+// computing Z; 2 = build it in LDS copying Zin.
+template <int HB, int kMode>
+__global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
+    const uint16_t* __restrict__ X, const uint8_t* __restrict__ hdr,
+    const uint8_t* __restrict__ levels, const float* __restrict__ basis,
+    const float* __restrict__ scales, const float* __restrict__ Zin,
+    const KbInfo* __restrict__ table, float* __restrict__ Y, int N, int n_cb, int ct_log2) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* red = reinterpret_cast<float*>(smem);
+    KbInfo* info = reinterpret_cast<KbInfo*>(smem + sizeof(float) * kPanelThreads);
+    const int tid = threadIdx.x;
+    const int CT = 1 << ct_log2;
+    const int S = kPanelThreads >> ct_log2;
+    const int c = tid & (CT - 1);
+    const int j = tid >> ct_log2;
+    const int n = blockIdx.x * CT + c;
     const bool valid = n < N;
     const int64_t nn = valid ? n : N - 1;
-    float acc = 0.f;
-    for (int kl = wave; kl < nkb; kl += kWaves) {
-        const int64_t bid = (int64_t)(kb0 + kl) * N + nn;
-        uint32_t d0, d1, cfg, cf;
-        sx8_load_hdr<HB>(hdr, bid, d0, d1, cfg, cf);
-        const uint2* lp = reinterpret_cast<const uint2*>(levels + bid * 24);
-        const uint2 v0 = lp[0], v1 = lp[1], v2 = lp[2];
-        const uint32_t Hs[4] = {v0.x, v0.y, v1.x, v1.y};
-        const uint32_t Pw[2] = {v2.x, v2.y};
-        const KbInfo& ki = info[kl];
 
-        const float lo = sx8_h2f(d0), hi = sx8_h2f(d1);
-        const float q = (hi - lo) * 0.25f;
-        acc += (float)sx8_sext4(cf) * ki.z[0] + (float)sx8_sext4(cf >> 4) * ki.z[1];
+    // the first round of this lane's weight loads goes out before the table is built
+    uint32_t hd[kUnroll][2];
+    uint2 lv[kUnroll][3];
 #pragma unroll
-        for (int sb = 0; sb < 4; ++sb) {
-            const uint32_t s = (cfg >> (2 * sb)) & 3u;
-            const float k1 = (float)((0x1300u >> (4 * s)) & 0xFu);   // 0,0,3,1
-            const float k2 = (float)((0x1030u >> (4 * s)) & 0xFu);   // 0,3,0,1
-            const float rlo = lo + q * k1;
-            const float rhi = hi - q * k2;
-            float step = (rhi - rlo) * 0.015873f;
-            if (step < 1e-10f) step = 1e-10f;
-            const uint32_t P16 = (sb & 1) ? (Pw[sb >> 1] >> 16) : (Pw[sb >> 1] & 0xFFFFu);
-            const uint32_t P = (P16 & 0xFFu) | ((P16 & 0xFF00u) << 8);
-            float d = 0.f;
+    for (int u = 0; u < kUnroll; ++u) {
+        const int kb = j + u * S;
+        if (kb < n_cb) load_block<HB>(hdr, levels, (int64_t)kb * N + nn, hd[u], lv[u]);
+    }
+    const KbInfo* ti = table;
+    if constexpr (kMode == 0) {
+        if (n_cb <= kLdsMaxKb) {
+            const uint4* src = reinterpret_cast<const uint4*>(table);
+            uint4* dst = reinterpret_cast<uint4*>(info);
+            for (int i = tid; i < n_cb * 7; i += kPanelThreads) dst[i] = src[i];
+            ti = info;
+        }
+    } else {
+        stage_table<kMode == 2>(info, X, basis, scales, Zin, n_cb);
+        ti = info;
+    }
+    __syncthreads();
+
+    const SpliceK sk = splice_consts();
+    float acc = 0.f;
+    for (int kb0 = j;;) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) d = dot2(lv_pair(Hs[sb], P, i), ki.xp[4 * sb + i], d);
-            acc += (rlo - 64.f * step) * ki.sx[sb] + step * d;
+        for (int u = 0; u < kUnroll; ++u) {
+            const int kb = kb0 + u * S;
+            if (kb < n_cb) {
+                const uint32_t H[4] = {lv[u][0].x, lv[u][0].y, lv[u][1].x, lv[u][1].y};
+                const uint32_t Pw[2] = {lv[u][2].x, lv[u][2].y};
+                const float lo = sx8_h2f(hd[u][0]), hi = sx8_h2f(hd[u][0] >> 16);
+                const uint32_t cfg = hd[u][1] & 0xFFu, cf = (hd[u][1] >> 8) & 0xFFu;
+                if (__builtin_amdgcn_ballot_w64(!(hi >= lo)) == 0)   // wave-uniform
+                    acc += block_dot_fast(lo, hi, cfg, cf, H, Pw, ti[kb], sk);
+                else
+                    acc += block_dot_exact(lo, hi, cfg, cf, H, Pw, ti[kb], sk);
+            }
+        }
+        kb0 += kUnroll * S;
+        if (kb0 >= n_cb) break;
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int kb = kb0 + u * S;
+            if (kb < n_cb) load_block<HB>(hdr, levels, (int64_t)kb * N + nn, hd[u], lv[u]);
         }
     }
 
-    // ---- reduce the four waves in a fixed order
-    red[wave * 64 + lane] = acc;
+    // slices -> columns: xor tree over the slices inside each wave (lanes c, c + CT,
+    // ...), then the 8 wave sums in wave order; fixed order, so deterministic
+    for (int off = CT; off < 64; off <<= 1) acc += __shfl_xor(acc, off);
+    const int wave = tid >> 6;
+    if ((tid & 63) < CT) red[wave * CT + c] = acc;
     __syncthreads();
-    if (wave != 0) return;
-    const float total = ((red[lane] + red[64 + lane]) + red[128 + lane]) + red[192 + lane];
-    if (S == 1) {
-        if (valid) Y[n] = total;
-        return;
-    }
-    if (valid) partial[(int64_t)split * N + n] = total;
-    __threadfence();   // release this group's partials device-wide
-    uint32_t prev = 0;
-    if (lane == 0)
-        prev = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_ACQ_REL,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-    prev = __shfl(prev, 0);
-    if (prev != (uint32_t)(S - 1)) return;
-    __threadfence();   // acquire the other groups' partials
-    if (valid) {
+    if (tid < CT && valid) {
         float t = 0.f;
-        for (int s = 0; s < S; ++s)
-            t += __hip_atomic_load(&partial[(int64_t)s * N + n], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int w = 0; w < kPanelThreads / 64; ++w) t += red[w * CT + tid];
         Y[n] = t;
     }
-    if (lane == 0)
-        __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Panel width: the widest power of two <= 64 that still gives >= 256 work-groups (one
+// per CU); wider panels amortise the per-work-group table build over more columns.
+inline int panel_ct_log2(int N) {
+    int lg = 6;
+    while (lg > 2 && (N + (1 << lg) - 1) / (1 << lg) < 256) --lg;
+    return lg;
 }
 
 template <int HB>
 int32_t launch_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels,
                     const float* basis, const float* scales, const float* Zin, float* Zout,
-                    int N, int n_cb, float* Y, hipStream_t st) {
+                    int N, int n_cb, float* Y, KbInfo* table, hipStream_t st) {
     using namespace sx8;
-    const int tiles = (N + kCols - 1) / kCols;
-    int S = 1;
-    if (tiles < kTargetGroups) S = (kTargetGroups + tiles - 1) / tiles;
-    S = std::min(S, std::max(1, n_cb / 8));                                // >= 8 kb per group
-    S = std::max(S, (n_cb + kMaxKbPerGroup - 1) / kMaxKbPerGroup);         // LDS bound
-    const int kb_per = (n_cb + S - 1) / S;
-    S = (n_cb + kb_per - 1) / kb_per;
-    float* partial = nullptr;
-    uint32_t* counters = nullptr;
-    if (S > 1) {
-        const int32_t rc = gemv_workspace((int64_t)S * N, tiles, &partial, &counters);
-        if (rc != SX8_OK) return rc;
+    const int lg = panel_ct_log2(N);
+    const dim3 grid((N + (1 << lg) - 1) >> lg);
+    const bool lds = n_cb <= kLdsMaxKb;
+    const size_t smem = sizeof(float) * kPanelThreads + (lds ? sizeof(KbInfo) * (size_t)n_cb : 0);
+    if (!Zout && lds) {   // single launch: the table is built inside every work-group
+        if (Zin)
+            hipLaunchKernelGGL((k_gemv_panel<HB, 2>), grid, dim3(kPanelThreads), smem, st, X, hdr,
+                               levels, basis, scales, Zin, table, Y, N, n_cb, lg);
+        else
+            hipLaunchKernelGGL((k_gemv_panel<HB, 1>), grid, dim3(kPanelThreads), smem, st, X, hdr,
+                               levels, basis, scales, Zin, table, Y, N, n_cb, lg);
+        return check_launch("sx8_gemv");
     }
-    const size_t smem = sizeof(KbInfo) * (size_t)kb_per + sizeof(float) * kThreads;
-    const dim3 grid(tiles, S);
+    const dim3 tgrid((n_cb + 7) / 8);
     if (Zin)
-        hipLaunchKernelGGL((k_gemv<HB, true>), grid, dim3(kThreads), smem, st, X, hdr, levels,
-                           basis, scales, Zin, Zout, Y, partial, counters, N, n_cb, kb_per);
+        hipLaunchKernelGGL(k_kbinfo<true>, tgrid, dim3(256), 0, st, X, basis, scales, Zin, Zout,
+                           n_cb, table);
     else
-        hipLaunchKernelGGL((k_gemv<HB, false>), grid, dim3(kThreads), smem, st, X, hdr, levels,
-                           basis, scales, Zin, Zout, Y, partial, counters, N, n_cb, kb_per);
+        hipLaunchKernelGGL(k_kbinfo<false>, tgrid, dim3(256), 0, st, X, basis, scales, Zin, Zout,
+                           n_cb, table);
+    hipLaunchKernelGGL((k_gemv_panel<HB, 0>), grid, dim3(kPanelThreads), smem, st, X, hdr, levels,
+                       basis, scales, Zin, table, Y, N, n_cb, lg);
     return check_launch("sx8_gemv");
 }
 
 }  // namespace
+
+extern "C" int64_t sx8_gemv_workspace_bytes(int64_t n_cb) {
+    return n_cb > 0 ? n_cb * (int64_t)sizeof(KbInfo) : 0;
+}
 
 extern "C" int32_t sx8_compute_z(const uint16_t* X, int64_t M, int64_t ldx, const float* basis,
                                  const float* scales, int64_t n_cb, float* Z, void* stream) {
@@ -251,7 +458,7 @@ extern "C" int32_t sx8_compute_z(const uint16_t* X, int64_t M, int64_t ldx, cons
 extern "C" int32_t sx8_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels,
                             int32_t hdr_bytes, const float* basis, const float* scales,
                             const float* Z_in, float* Z_out, int64_t N, int64_t n_cb, float* Y,
-                            void* stream) {
+                            void* workspace, int64_t workspace_bytes, void* stream) {
     using namespace sx8;
     if (!X || !hdr || !levels || !Y) return fail(SX8_ERR_INVALID, "sx8_gemv: null pointer");
     if (!Z_in && (!basis || !scales))
@@ -265,9 +472,21 @@ extern "C" int32_t sx8_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t
         (basis && !aligned(basis, 4)) || (scales && !aligned(scales, 4)) ||
         (Z_in && !aligned(Z_in, 4)) || (Z_out && !aligned(Z_out, 4)) || !aligned(Y, 4))
         return fail(SX8_ERR_INVALID, "sx8_gemv: misaligned pointer (X needs 16-byte alignment)");
+    const int64_t need = sx8_gemv_workspace_bytes(n_cb);
+    KbInfo* table = reinterpret_cast<KbInfo*>(workspace);
+    if (table) {
+        if (workspace_bytes < need || !aligned(table, 16))
+            return fail(SX8_ERR_INVALID, "sx8_gemv: workspace needs %lld bytes, 16-byte aligned",
+                        (long long)need);
+    } else {
+        void* ws = nullptr;
+        const int32_t rc = device_workspace(need, &ws);
+        if (rc != SX8_OK) return rc;
+        table = reinterpret_cast<KbInfo*>(ws);
+    }
     if (hdr_bytes == 8)
         return launch_gemv<8>(X, hdr, levels, basis, scales, Z_in, Z_out, (int)N, (int)n_cb, Y,
-                              as_stream(stream));
-    return launch_gemv<6>(X, hdr, levels, basis, scales, Z_in, Z_out, (int)N, (int)n_cb, Y,
+                              table, as_stream(stream));
+    return launch_gemv<6>(X, hdr, levels, basis, scales, Z_in, Z_out, (int)N, (int)n_cb, Y, table,
                           as_stream(stream));
 }

@@ -23,11 +23,11 @@ inline bool aligned(const void* p, uintptr_t a) {
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-// Device workspace for the split-K GEMV: `partial_floats` float32 partial sums and
-// `n_counters` arrival counters that are zero between launches (each launch's last
-// work-group resets the counters it used).  Grow-only, one per device, allocated
-// with hipMalloc on first need; returns SX8_OK or SX8_ERR_HIP.
-int32_t gemv_workspace(int64_t partial_floats, int64_t n_counters, float** partial,
-                       uint32_t** counters);
+// Library-owned device scratch of at least `bytes` (256-byte aligned) for callers
+// that pass no workspace: grow-only, one buffer per device, allocated with hipMalloc
+// on first need and kept until the process ends.  Calls that overlap on one device
+// (several streams) must pass their own workspaces instead.  Returns SX8_OK or
+// SX8_ERR_HIP.
+int32_t device_workspace(int64_t bytes, void** ptr);
 
 }  // namespace sx8

@@ -62,18 +62,6 @@ def v6_encode_6bit(blocks: torch.Tensor):
     return best_lev.to(torch.uint8).reshape(n, 32), dmin, dmax, config
 
 
-def _bases_gram(err: torch.Tensor, k: int) -> torch.Tensor:
-    """Top-k right singular vectors of err (rows, 32) via eigh of the Gram matrix."""
-    e64 = err.double()
-    g = e64.T @ e64
-    w, v = torch.linalg.eigh(g)                 # ascending eigenvalues
-    basis = v[:, torch.argsort(w, descending=True)[:k]].T.contiguous()
-    idx = basis.abs().argmax(dim=1)
-    sign = torch.sign(basis.gather(1, idx[:, None]))
-    sign[sign == 0] = 1
-    return (basis * sign).float()
-
-
 def pca_correct(levels, dmin, dmax, config, blocks, n_cb, pca_method="svd"):
     """Per-kb PCA post-correction; returns coeff (n_blk,1) u8, data (n_cb,64) f32,
     scales (n_cb,2) f32 (numpy, on the host)."""
@@ -99,20 +87,36 @@ def pca_correct(levels, dmin, dmax, config, blocks, n_cb, pca_method="svd"):
         step_sb = st_j[st, ar]
         rec[:, sb * 8:(sb + 1) * 8] = lo_sb[:, None] + step_sb[:, None] * lv_f[:, sb * 8:(sb + 1) * 8]
     err_all = (blocks - rec).reshape(n_rows, n_cb, 32)
-    for cb in range(n_cb):
-        err = err_all[:, cb, :].contiguous()
-        if pca_method == "gram":
-            basis = _bases_gram(err, N_BASES)
-        else:
+    if pca_method == "gram":
+        # all K blocks at once: batched Gram matrices, batched eigh, batched medians
+        e64 = err_all.double()
+        g = torch.einsum("rci,rcj->cij", e64, e64)
+        w, v = torch.linalg.eigh(g)                                   # ascending
+        order = torch.argsort(w, dim=1, descending=True)[:, :N_BASES]
+        basis = torch.gather(v, 2, order[:, None, :].expand(-1, 32, -1)).transpose(1, 2)
+        idx = basis.abs().argmax(dim=2, keepdim=True)
+        sign = torch.sign(torch.gather(basis, 2, idx))
+        sign[sign == 0] = 1
+        basis = (basis * sign).float()                                # (n_cb, 4, 32)
+        craw = torch.einsum("cki,rci->ckr", basis, err_all)           # (n_cb, 4, n_rows)
+        sc = (torch.median(craw.abs(), dim=2).values / 3.0).clamp(min=1e-10)
+        cq = (craw / sc[:, :, None]).round().clamp(-8, 7).to(torch.int8)
+        byte0 = (cq[:, 0].view(torch.uint8) & 0xF) | ((cq[:, 1].view(torch.uint8) & 0xF) << 4)
+        coeff.view(n_rows, n_cb)[:, :] = byte0.T
+        data[:] = basis[:, :2].reshape(n_cb, 64).cpu().numpy()
+        scales[:] = sc[:, :2].cpu().numpy()
+    else:
+        for cb in range(n_cb):
+            err = err_all[:, cb, :].contiguous()
             _, _, vh = torch.linalg.svd(err, full_matrices=False)
             basis = vh[:N_BASES]
-        craw = basis @ err.T
-        sc = (torch.median(craw.abs(), dim=1).values / 3.0).clamp(min=1e-10)
-        cq = (craw / sc[:, None]).round().clamp(-8, 7).to(torch.int8)
-        byte0 = (cq[0].view(torch.uint8) & 0xF) | ((cq[1].view(torch.uint8) & 0xF) << 4)
-        coeff.view(n_rows, n_cb)[:, cb] = byte0
-        data[cb] = basis[:2].reshape(-1).cpu().numpy()
-        scales[cb] = sc[:2].cpu().numpy()
+            craw = basis @ err.T
+            sc = (torch.median(craw.abs(), dim=1).values / 3.0).clamp(min=1e-10)
+            cq = (craw / sc[:, None]).round().clamp(-8, 7).to(torch.int8)
+            byte0 = (cq[0].view(torch.uint8) & 0xF) | ((cq[1].view(torch.uint8) & 0xF) << 4)
+            coeff.view(n_rows, n_cb)[:, cb] = byte0
+            data[cb] = basis[:2].reshape(-1).cpu().numpy()
+            scales[cb] = sc[:2].cpu().numpy()
     return coeff.cpu().numpy().reshape(n_blk, 1), data, scales
 
 

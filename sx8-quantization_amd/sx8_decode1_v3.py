@@ -3,9 +3,10 @@
 Interface of scripts/sx8_decode1_v3.py (reference): ``_ext()`` (an object with
 ``compute_z44``, ``decode1_v44`` and ``decode1_v44_combined``), ``make_tensors_v44``,
 ``best_split_k``, the ``_BUF``/``_buf`` output pools and ``decode1_v44``.
-The CUDA extension is replaced by libsx8_hip.so (sx8_compute_z / sx8_gemv); the
-combined entry point computes Z inside the GEMV launch (one launch instead of two)
-and still writes it to the caller's Z buffer.
+The CUDA extension is replaced by libsx8_hip.so (sx8_compute_z / sx8_gemv).  Both GEMV
+forms run two launches: a small kernel builds the per-K-block activation table (and,
+for the combined form, Z with the reference's summation tree, written to the caller's
+Z buffer), then the panel GEMV streams the weights.
 """
 from __future__ import annotations
 
@@ -26,6 +27,18 @@ def _x_for_kernel(X, n_cb):
         Xp[:min(Kp, Xc.numel())] = Xc[:Kp]
         Xc = Xp
     return Xc
+
+
+def _workspace(n_cb, device):
+    """Pooled per-device table workspace of sx8_gemv (112 bytes per K block).  Taken
+    from torch's allocator, so it is stream-ordered and capture-safe."""
+    n = (int(_L.lib().sx8_gemv_workspace_bytes(n_cb)) + 3) // 4
+    key = ("WS", torch.device(device).index)
+    b = _BUF.get(key)
+    if b is None or b.numel() < n:
+        b = torch.empty(max(n, 4096), dtype=torch.float32, device=device)
+        _BUF[key] = b
+    return b
 
 
 class _Ext:
@@ -49,8 +62,10 @@ class _Ext:
         Xc = _x_for_kernel(X, n_cb)
         if out is None:
             out = torch.empty(N, dtype=torch.float32, device=Xc.device)
+        ws = _workspace(n_cb, Xc.device)
         _L.call("sx8_gemv", _L.ptr(Xc), _L.ptr(hdr), _L.ptr(levels), int(hdr_bytes), None, None,
-                _L.ptr(Z.contiguous()), None, N, n_cb, _L.ptr(out), _L.stream(Xc.device))
+                _L.ptr(Z.contiguous()), None, N, n_cb, _L.ptr(out), _L.ptr(ws), ws.numel() * 4,
+                _L.stream(Xc.device))
         return out
 
     @staticmethod
@@ -58,9 +73,10 @@ class _Ext:
         n_cb = int(n_cb)
         N = hdr.size(0) // n_cb
         Xc = _x_for_kernel(X, n_cb)
+        ws = _workspace(n_cb, Xc.device)
         _L.call("sx8_gemv", _L.ptr(Xc), _L.ptr(hdr), _L.ptr(levels), int(hdr_bytes),
                 _L.ptr(basis.contiguous()), _L.ptr(scales.contiguous()), None, _L.ptr(Z), N,
-                n_cb, _L.ptr(out), _L.stream(Xc.device))
+                n_cb, _L.ptr(out), _L.ptr(ws), ws.numel() * 4, _L.stream(Xc.device))
         return out
 
 
@@ -116,8 +132,14 @@ def decode1_v44(X, qt, bases_info, hdr_t=None, lvl_t=None, bas_t=None, sca_t=Non
                                                       hdr_aligned=(hdr_bytes == 8))
     n_cb = qt["n_cb"]
     N = qt["shape"][0]
-    ext = _ext()
-    Z = _buf(("Z", n_cb), (n_cb, 2))
+    _ext()
     Y = _buf(("Y", N), (N,))
-    ext.decode1_v44_combined(X, hdr_t, lvl_t, bas_t, sca_t, n_cb, hdr_bytes, Z, Y)
+    # The reference passes a pooled Z scratch to decode1_v44_combined; nothing reads it
+    # afterwards, so the Z output is skipped here, which lets the HIP GEMV build its
+    # activation table inside the single launch.
+    Xc = _x_for_kernel(X, n_cb)
+    ws = _workspace(n_cb, Xc.device)
+    _L.call("sx8_gemv", _L.ptr(Xc), _L.ptr(hdr_t), _L.ptr(lvl_t), int(hdr_bytes), _L.ptr(bas_t),
+            _L.ptr(sca_t), None, None, N, n_cb, _L.ptr(Y), _L.ptr(ws), ws.numel() * 4,
+            _L.stream(Xc.device))
     return Y, (hdr_t, lvl_t, bas_t, sca_t)

@@ -13,7 +13,7 @@ HEADER = os.path.join(REPO, "include", "sx8_hip.h")
 
 def _declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int32_t|const char\*)\s+(sx8_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int32_t|int64_t|const char\*)\s+(sx8_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_the_abi():
@@ -41,14 +41,17 @@ def test_invalid_arguments_rejected_on_host(hiplib):
     L = hiplib
     p = ctypes.c_void_p(4096)   # never dereferenced: validation fails first
     # null pointers
-    assert L.sx8_gemv(NULL, p, p, 6, p, p, NULL, NULL, 64, 2, p, NULL) == 1
+    assert L.sx8_gemv(NULL, p, p, 6, p, p, NULL, NULL, 64, 2, p, NULL, 0, NULL) == 1
     assert "null" in _err(L)
     # hdr_bytes outside {6, 8}
-    assert L.sx8_gemv(p, p, p, 7, p, p, NULL, NULL, 64, 2, p, NULL) == 1
+    assert L.sx8_gemv(p, p, p, 7, p, p, NULL, NULL, 64, 2, p, NULL, 0, NULL) == 1
     assert "hdr_bytes" in _err(L)
-    # misaligned X (needs 16 bytes)
-    assert L.sx8_gemv(ctypes.c_void_p(4098), p, p, 6, p, p, NULL, NULL, 64, 2, p, NULL) == 1
+    # misaligned Y, and a workspace that is too small
+    assert L.sx8_gemv(p, p, p, 6, p, p, NULL, NULL, 64, 2, ctypes.c_void_p(4098), NULL, 0, NULL) == 1
     assert "misaligned" in _err(L)
+    assert L.sx8_gemv(p, p, p, 6, p, p, NULL, NULL, 64, 2, p, p, 100, NULL) == 1
+    assert "workspace" in _err(L)
+    assert L.sx8_gemv_workspace_bytes(80) == 80 * 112
     # inconsistent K / n_cb
     assert L.sx8_dequant_f16(p, p, p, p, p, p, p, p, 4, 100, 2, p, NULL) == 1
     assert "bad shape" in _err(L)
@@ -64,7 +67,7 @@ def test_wrapper_raises_runtime_error(hiplib):
     with pytest.raises(RuntimeError, match="hdr_bytes"):
         _sx8lib.call("sx8_gemv", ctypes.c_void_p(4096), ctypes.c_void_p(4096),
                      ctypes.c_void_p(4096), 9, ctypes.c_void_p(4096), ctypes.c_void_p(4096),
-                     NULL, NULL, 64, 2, ctypes.c_void_p(4096), NULL)
+                     NULL, NULL, 64, 2, ctypes.c_void_p(4096), NULL, 0, NULL)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
