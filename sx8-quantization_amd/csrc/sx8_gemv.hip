@@ -4,24 +4,23 @@
 // cuda/sx8_gemm_compact.cu:28-50) and decode1_v44_kernel (cuda/sx8_decode1_v3.cu:75-167)
 // with its wrappers decode1_v44 / decode1_v44_combined (:197-246).
 //
-// GEMV design (gfx950, HBM-bound):
-//   * k_gemv_panel streams the weights.  A 512-thread work-group owns CT consecutive
-//     columns over the whole K: lane (c, j) = (column c, K slice j), c fastest, so for
-//     each kb the CT lanes of a slice read CT consecutive 24-byte level records and
-//     header records (contiguous runs in the kb-major layout) and slice j walks
-//     kb = j, j + S, ... (S = 512 / CT) four blocks per round.  Slices meet in LDS and
-//     are summed in slice order: nothing leaves a work-group before the final store,
-//     so there are no device-scope fences or atomics and results are deterministic.
-//   * every block's decode needs the activation side of its kb (x pairs, sub-block
-//     sums of x, splice biases, Z0/Z1): a 112-byte table entry per kb, built in LDS by
-//     each work-group while its first weight loads are in flight (one launch).  When
-//     the caller wants Z back (the combined entry point), k_kbinfo builds the table
-//     once with the reference's summation tree -- Z bit-identical to compute_z44 --
-//     and the panel kernel copies it in.
+// GEMV design (gfx950):
+//   * k_gemv_panel streams the weights.  A 512-thread work-group owns a panel of CT
+//     consecutive columns over the whole K; lane (c, j) = (column c, K slice j), so the
+//     CT lanes of a slice read CT consecutive records of one kb row.  Slices are summed
+//     in LDS in a fixed order: no device-scope fences or atomics, deterministic output.
+//   * every block's decode needs the activation side of its kb (x pairs, sub-block sums
+//     of x, splice biases, Z0/Z1): a 112-byte table entry per kb, built in LDS by each
+//     work-group while its first weight loads are in flight (one launch).  When the
+//     caller wants Z back (the combined entry point), k_kbinfo builds the table once
+//     with the reference's summation tree -- Z bit-identical to compute_z44 -- and the
+//     panel kernel copies it in.
 //   * per 8-weight sub-block the core dot sum_i x_i (rlo + step lv_i) becomes
 //     rlo * Sx + step * (sum x lv) with sum x lv from fp16 "splices" and
 //     v_dot2_f32_f16 (see block_dot); PCA is applied per block through Z
 //     (docs/SX8_FLASH_V4_3_SPEC.md:49-61).
+//   * the K loop is software-pipelined (rotating record buffers, unconditional clamped
+//     loads) and panels are renumbered per XCD (see k_gemv_panel).
 #include "sx8_device.h"
 #include "sx8_host.h"
 
@@ -63,8 +62,7 @@ __device__ __forceinline__ void fill_x_side(KbInfo& out, int sb, const uint4 xv)
 }
 
 constexpr int kPanelThreads = 512;
-constexpr int kUnroll = 4;
-constexpr int kLdsMaxKb = 640;     // table staged in LDS up to 60 KB, read from L2 beyond
+constexpr int kLdsMaxKb = 640;     // activation table staged in LDS up to this many K blocks
 
 // Z of one (row, kb, j) with the reference's warp tree: products x_t * b_t, then
 // pairwise sums over lane offsets 16, 8, 4, 2, 1 (cuda/sx8_decode1_v3.cu:53-63),
@@ -97,7 +95,7 @@ __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ 
 
 // Activation-side table, one 32-lane group per kb (8 kb per 256-thread block).
 // Lane t: product x_t * b_jt for j = 0, 1 and the xor tree (bit-identical Z); lanes
-// 0..15 build one x pair each, lanes 16..19 one sub-block sum each.
+// 0..3 build the x side of one sub-block each.  Used when the caller asks for Z back.
 template <bool kZGiven>
 __global__ __launch_bounds__(256) void k_kbinfo(const uint16_t* __restrict__ X,
                                                 const float* __restrict__ basis,
@@ -143,17 +141,6 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
                                   __builtin_bit_cast(sx8_half2, b), c, false);
 }
 
-// fp32 contribution of one block (one column, one kb) to its output.
-// PCA through Z, then per sub-block rlo * Sx + step * sum_i x_i lv_i, with
-// rlo/rhi/step in the reference's float32 branchless form (cuda/sx8_decode1_v3.cu:
-// 108-117) and sum_i x_i lv_i = 4 * sum x nib + sum x quad computed from fp16 splices:
-// a nibble or quad is or-ed into the mantissa of an fp16 constant whose last mantissa
-// bit is worth the field's weight, e.g. (H & 0x000F000F) | 0x64006400 holds
-// (1024 + nib_0, 1024 + nib_4).  Pair i uses constants 1024/64/1024/64 for the
-// nibbles (bits 0, 4, 8, 12 of H after an 8-bit shift for pairs 2-3) and 16/64/256/1024
-// for the quads (bits 6, 4, 2, 0 of each spread lo byte); v_dot2_f32_f16 multiplies
-// two splices by an x pair, and the constant offsets, weighted by x, are the
-// per-sub-block `bias` of the activation table.  All spliced values are exact fp16.
 // Loop-invariant masks and byte selectors held in VGPRs: on gfx9 a VOP3 instruction
 // takes at most one scalar operand, so with the fp16 constants in SGPRs each splice
 // below is a single v_and_or_b32 and each quad spread a single v_perm_b32.
@@ -169,6 +156,32 @@ __device__ __forceinline__ SpliceK splice_consts() {
     return k;
 }
 
+// One block's raw records: lohi = dmin | dmax << 16, cc = config | coeff << 8, then the
+// 16 hi-nibble bytes (a) and the 8 lo-quad bytes (b).
+struct BlockRec {
+    uint32_t lohi, cc;
+    uint4 a;
+    uint2 b;
+};
+
+typedef uint4 sx8_uint4_a8 __attribute__((aligned(8)));
+
+template <int HB>
+__device__ __forceinline__ void load_rec(BlockRec& o, const uint8_t* __restrict__ hdr,
+                                         const uint8_t* __restrict__ levels, int64_t bid) {
+    if constexpr (HB == 8) {
+        const uint2 h = *reinterpret_cast<const uint2*>(hdr + bid * 8);
+        o.lohi = h.x;
+        o.cc = h.y;
+    } else {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(hdr + bid * 6);
+        o.lohi = h[0] | ((uint32_t)h[1] << 16);
+        o.cc = h[2];
+    }
+    o.a = *reinterpret_cast<const sx8_uint4_a8*>(levels + bid * 24);
+    o.b = *reinterpret_cast<const uint2*>(levels + bid * 24 + 16);
+}
+
 // fp32 contribution of one block (one column, one kb) to its output: PCA through Z,
 // then per 8-weight sub-block rlo * Sx + step * sum_i x_i lv_i.
 //
@@ -177,34 +190,39 @@ __device__ __forceinline__ SpliceK splice_consts() {
 // weight in lv, e.g. (H & 0x000F000F) | 0x6C006C00 = (4096 + 4 nib_0, 4096 + 4 nib_4)
 // (exponent 12: ulp 4).  Nibble pairs use 4096/256/4096/256 (bits 0/4 of H and of
 // H >> 8), quad pairs 16/64/256/1024 (bits 6/4/2/0 of each spread lo byte).  Eight
-// v_dot2_f32_f16 per sub-block multiply the splices by x pairs into one fp32 sum that
+// v_dot2_f32_f16 per sub-block multiply the splices by x pairs into one fp32 sum t that
 // starts at -sum x * constants (the table's nbias), leaving sum x lv.  Every spliced
 // value is exact in fp16.
 //
-// Fast path (dmax >= dmin): rlo = lo + q * {0,0,3,1}[s], step = 0.015873 * (hi - lo)
-// * {1, 1/4, 1/4, 1/2}[s] (the strategy range widths), both looked up with bfe on
-// packed byte tables.  It matches the reference's float32 form (cuda/sx8_decode1_v3.cu:
-// 108-117) to rounding, except that the 1e-10 step floor is not applied: the floor
-// only binds when hi - lo < 1.3e-8, where it moves the block's contribution by at most
-// 1e-10 * sum|x| * 63.  Blocks with hi < lo or NaN endpoints, where the floor changes
-// the result, take block_dot_exact (see k_gemv_panel).
-__device__ __forceinline__ float block_dot_fast(float lo, float hi, uint32_t cfg, uint32_t cf,
-                                                const uint32_t H[4], const uint32_t Pw[2],
-                                                const KbInfo& ki, const SpliceK& k) {
+// Range parameters follow the reference's float32 form (cuda/sx8_decode1_v3.cu:108-117):
+// rlo = lo + q k1[s] with q = (hi - lo) / 4, k1 = {0, 0, 3, 1}, and
+// step = max(0.015873 (rhi - rlo), 1e-10) where rhi - rlo = (hi - lo) * {1, 1/4, 1/4, 1/2}.
+// For hi > lo the floor never binds (an fp16 range is at least 2^-24, so step >= 2.4e-10)
+// and step = m 2^e[s] with m = 0.015873 (hi - lo); for hi <= lo every sub-block's
+// range is <= 0, so step = 1e-10 throughout (m = 1e-10, e = 0); NaN endpoints make rlo
+// NaN as in the reference.  The four strategies are moved into the bytes of `sel` so
+// that one v_perm_b32 per table looks k1 and e up for all sub-blocks at once.
+__device__ __forceinline__ float block_dot(const BlockRec& o, const KbInfo& ki, const SpliceK& k) {
+    const float lo = sx8_h2f(o.lohi), hi = sx8_h2f(o.lohi >> 16);
     const float d = hi - lo;
     const float q = d * 0.25f;
-    const float cd = d * 0.015873f;
+    const uint32_t cfg = o.cc & 0xFFu;
+    uint32_t sel = (cfg << 6) | cfg;                  // strategy of sub-block sb -> bits 8sb
+    sel = ((sel << 12) | sel) & 0x03030303u;
+    const uint32_t k1b = __builtin_amdgcn_perm(0u, 0x01030000u, sel);                 // k1[s]
+    const uint32_t eb = d > 0.f ? __builtin_amdgcn_perm(0u, 0xFFFEFE00u, sel) : 0u;  // e[s]
+    const float m = d > 0.f ? d * 0.015873f : 1e-10f;
+    const uint32_t cf = o.cc >> 8;
     float acc = (float)sx8_sext4(cf) * ki.z[0] + (float)sx8_sext4(cf >> 4) * ki.z[1];
+    float T = 0.f;
+    const uint32_t H[4] = {o.a.x, o.a.y, o.a.z, o.a.w};
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
-        const uint32_t sh = ((cfg >> (2 * sb)) & 3u) << 3;             // 8 * strategy
-        const float k1 = (float)__builtin_amdgcn_ubfe(0x01030000u, sh, 8);   // 0,0,3,1
-        const int e = __builtin_amdgcn_sbfe((int)0xFFFEFE00u, sh, 8);        // 0,-2,-2,-1
-        const float rlo = lo + q * k1;
-        const float step = __builtin_ldexpf(cd, e);
+        const float rlo = __builtin_fmaf(q, (float)((k1b >> (8 * sb)) & 0xFFu), lo);
         const uint32_t h = H[sb];
         const uint32_t h8 = h >> 8;
-        const uint32_t P = __builtin_amdgcn_perm(0u, Pw[sb >> 1], (sb & 1) ? k.sel_odd : k.sel_even);
+        const uint32_t P = __builtin_amdgcn_perm(0u, (sb >> 1) ? o.b.y : o.b.x,
+                                                 (sb & 1) ? k.sel_odd : k.sel_even);
         const uint32_t* xp = ki.xp + 4 * sb;
         float t = dot2((h & k.n_lo) | 0x6C006C00u, xp[0], ki.nbias[sb]);
         t = dot2((h & k.n_hi) | 0x5C005C00u, xp[1], t);
@@ -215,106 +233,84 @@ __device__ __forceinline__ float block_dot_fast(float lo, float hi, uint32_t cfg
         t = dot2((P & k.q2) | 0x5C005C00u, xp[2], t);
         t = dot2((P & k.q3) | 0x64006400u, xp[3], t);
         acc = __builtin_fmaf(rlo, ki.sx[sb], acc);
-        acc = __builtin_fmaf(step, t, acc);
+        T += __builtin_ldexpf(t, __builtin_amdgcn_sbfe((int)eb, 8 * sb, 8));
     }
-    return acc;
+    return __builtin_fmaf(m, T, acc);
 }
 
-// Same contribution with the reference's float32 rlo/rhi/step and its 1e-10 floor
-// (cuda/sx8_decode1_v3.cu:108-117), for waves holding a block with hi < lo or a NaN.
-__device__ __forceinline__ float block_dot_exact(float lo, float hi, uint32_t cfg, uint32_t cf,
-                                              const uint32_t H[4], const uint32_t Pw[2],
-                                              const KbInfo& ki, const SpliceK& k) {
-    const float q = (hi - lo) * 0.25f;
-    float acc = (float)sx8_sext4(cf) * ki.z[0] + (float)sx8_sext4(cf >> 4) * ki.z[1];
-#pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-        const uint32_t s = (cfg >> (2 * sb)) & 3u;
-        const float k1 = (float)((0x1300u >> (4 * s)) & 0xFu);   // 0,0,3,1
-        const float k2 = (float)((0x1030u >> (4 * s)) & 0xFu);   // 0,3,0,1
-        const float rlo = lo + q * k1;
-        const float rhi = hi - q * k2;
-        float step = (rhi - rlo) * 0.015873f;
-        if (step < 1e-10f) step = 1e-10f;
-        const uint32_t h = H[sb];
-        const uint32_t h8 = h >> 8;
-        const uint32_t P = __builtin_amdgcn_perm(0u, Pw[sb >> 1], (sb & 1) ? k.sel_odd : k.sel_even);
-        const uint32_t* xp = ki.xp + 4 * sb;
-        float t = dot2((h & k.n_lo) | 0x6C006C00u, xp[0], ki.nbias[sb]);
-        t = dot2((h & k.n_hi) | 0x5C005C00u, xp[1], t);
-        t = dot2((h8 & k.n_lo) | 0x6C006C00u, xp[2], t);
-        t = dot2((h8 & k.n_hi) | 0x5C005C00u, xp[3], t);
-        t = dot2((P & k.q0) | 0x4C004C00u, xp[0], t);
-        t = dot2((P & k.q1) | 0x54005400u, xp[1], t);
-        t = dot2((P & k.q2) | 0x5C005C00u, xp[2], t);
-        t = dot2((P & k.q3) | 0x64006400u, xp[3], t);
-        acc += rlo * ki.sx[sb] + step * t;
-    }
-    return acc;
-}
+// Table entries built inside the GEMV work-group: four threads per kb, thread q doing
+// the x side of sub-block q and a quarter of both Z products (summed over the four
+// threads with two xor shuffles; this Z is only used internally).
+struct TabIn {
+    uint4 x;
+    float4 b0[2], b1[2];
+    float s;
+};
 
-// One kb's raw records for one column: hd = {dmin | dmax << 16, config | coeff << 8},
-// lv = the 24 level bytes.
-template <int HB>
-__device__ __forceinline__ void load_block(const uint8_t* __restrict__ hdr,
-                                           const uint8_t* __restrict__ levels, int64_t bid,
-                                           uint32_t hd[2], uint2 lv[3]) {
-    if constexpr (HB == 8) {
-        const uint2 h = *reinterpret_cast<const uint2*>(hdr + bid * 8);
-        hd[0] = h.x;
-        hd[1] = h.y;
+template <int kMode>
+__device__ __forceinline__ void tab_load(TabIn& t, const uint16_t* __restrict__ X,
+                                         const float* __restrict__ basis,
+                                         const float* __restrict__ scales,
+                                         const float* __restrict__ Zin, int kb, int q) {
+    t.x = *reinterpret_cast<const uint4*>(X + (int64_t)kb * 32 + 8 * q);
+    if constexpr (kMode == 1) {
+        const float4* b = reinterpret_cast<const float4*>(basis + (int64_t)kb * 64 + 8 * q);
+        t.b0[0] = b[0];
+        t.b0[1] = b[1];
+        t.b1[0] = b[8];
+        t.b1[1] = b[9];
+        t.s = scales[2 * kb + (q & 1)];
     } else {
-        const uint16_t* h = reinterpret_cast<const uint16_t*>(hdr + bid * 6);
-        hd[0] = h[0] | ((uint32_t)h[1] << 16);
-        hd[1] = h[2];
+        t.s = Zin[2 * kb + (q & 1)];
     }
-    const uint2* lp = reinterpret_cast<const uint2*>(levels + bid * 24);
-    lv[0] = lp[0];
-    lv[1] = lp[1];
-    lv[2] = lp[2];
 }
 
-// Activation table for all n_cb blocks, built by one work-group in its LDS: the x side
-// from one thread per (kb, sb), Z from one thread per (kb, j) (a left-to-right sum of
-// the 32 products, or a copy of Zin).  Used by the panel GEMV when no Z output is
-// requested; the entry point that must return Z runs k_kbinfo (reference tree) instead.
-template <bool kZGiven>
-__device__ __forceinline__ void stage_table(KbInfo* __restrict__ info,
-                                            const uint16_t* __restrict__ X,
-                                            const float* __restrict__ basis,
-                                            const float* __restrict__ scales,
-                                            const float* __restrict__ Zin, int n_cb) {
-    const int tid = threadIdx.x;
-    for (int u = tid; u < n_cb * 4; u += kPanelThreads)
-        fill_x_side(info[u >> 2], u & 3,
-                    *reinterpret_cast<const uint4*>(X + (int64_t)(u >> 2) * 32 + 8 * (u & 3)));
-    for (int u = tid; u < n_cb * 2; u += kPanelThreads) {
-        const int kb = u >> 1, jj = u & 1;
-        float z;
-        if constexpr (kZGiven) {
-            z = Zin[u];
-        } else {
-            const uint4* xv = reinterpret_cast<const uint4*>(X + (int64_t)kb * 32);
-            const float4* bv = reinterpret_cast<const float4*>(basis + (int64_t)kb * 64 + 32 * jj);
-            float a = 0.f;
+template <int kMode>
+__device__ __forceinline__ void tab_store(KbInfo* info, const TabIn& t, int kb, int q, bool ok) {
+#pragma clang fp contract(off)
+    float z = t.s;
+    if constexpr (kMode == 1) {
+        const uint32_t xw[4] = {t.x.x, t.x.y, t.x.z, t.x.w};
+        const float* b0 = reinterpret_cast<const float*>(t.b0);
+        const float* b1 = reinterpret_cast<const float*>(t.b1);
+        float z0 = 0.f, z1 = 0.f;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint4 xx = xv[q];
-                const float4 b0 = bv[2 * q], b1 = bv[2 * q + 1];
-                a += sx8_h2f(xx.x) * b0.x + sx8_h2f(xx.x >> 16) * b0.y;
-                a += sx8_h2f(xx.y) * b0.z + sx8_h2f(xx.y >> 16) * b0.w;
-                a += sx8_h2f(xx.z) * b1.x + sx8_h2f(xx.z >> 16) * b1.y;
-                a += sx8_h2f(xx.w) * b1.z + sx8_h2f(xx.w >> 16) * b1.w;
-            }
-            z = scales[u] * a;
+        for (int i = 0; i < 8; ++i) {
+            const float xf = sx8_h2f(xw[i >> 1] >> (16 * (i & 1)));
+            z0 += xf * b0[i];
+            z1 += xf * b1[i];
         }
-        info[kb].z[jj] = z;
+        z0 += __shfl_xor(z0, 1);
+        z1 += __shfl_xor(z1, 1);
+        z0 += __shfl_xor(z0, 2);
+        z1 += __shfl_xor(z1, 2);
+        z = t.s * (q == 0 ? z0 : z1);
     }
+    if (!ok) return;
+    fill_x_side(info[kb], q, t.x);
+    if (q < 2) info[kb].z[q] = z;
 }
 
-// kMode: 0 = read the table k_kbinfo wrote to global memory; 1 = build it in LDS
-// computing Z; 2 = build it in LDS copying Zin.
-template <int HB, int kMode>
+// M = 1 GEMV over column panels.  A 512-thread work-group owns CT = 2^ct_log2
+// consecutive columns over the whole K: lane (c, j) = (column c, K slice j), c fastest,
+// so for each kb the CT lanes of a slice read CT consecutive records, and slice j walks
+// kb = j + r S (S = 512 / CT) for r < R = ceil(n_cb / S).  Slices meet in LDS and are
+// summed in a fixed order: nothing leaves a work-group before the final store, so
+// there are no device-scope fences or atomics and results are deterministic.
+//
+// Latency schedule: the table inputs go out first, then the records of rounds 0 .. D
+// (D + 1 rotating buffers), then the table is built while they stream in.  In the main
+// loop the buffer just consumed is refilled with round r + D + 1, so D + 1 rounds are
+// in flight while one is decoded.  Every load is unconditional (indices clamped,
+// contributions past the end masked): the loop body is straight-line code, which keeps
+// the compiler's memory-wait counts exact, and scheduling barriers keep each refill
+// ahead of the decode that follows it.
+//
+// kMode: 0 = copy the table k_kbinfo wrote into LDS; 1 = build it computing Z; 2 = build
+// it with Z from Zin; 3 = read k_kbinfo's table from global memory (n_cb > kLdsMaxKb).  Work-groups go to the 8 XCDs round-robin by block index; panels
+// are renumbered so each XCD gets a contiguous column range and neighbouring panels
+// share their header cache lines in one L2.
+template <int HB, int kMode, int D>
 __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ hdr,
     const uint8_t* __restrict__ levels, const float* __restrict__ basis,
@@ -328,57 +324,59 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     const int S = kPanelThreads >> ct_log2;
     const int c = tid & (CT - 1);
     const int j = tid >> ct_log2;
-    const int n = blockIdx.x * CT + c;
+    const int G = gridDim.x, xcd = blockIdx.x & 7;
+    int panel = blockIdx.x >> 3;
+    for (int y = 0; y < xcd; ++y) panel += (G - y + 7) >> 3;
+    const int n = panel * CT + c;
     const bool valid = n < N;
     const int64_t nn = valid ? n : N - 1;
+    const int R = (n_cb + S - 1) / S;
+    auto kbc = [&](int r) { return min(j + r * S, n_cb - 1); };
+    auto bid = [&](int r) { return (int64_t)kbc(r) * N + nn; };
 
-    // the first round of this lane's weight loads goes out before the table is built
-    uint32_t hd[kUnroll][2];
-    uint2 lv[kUnroll][3];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-        const int kb = j + u * S;
-        if (kb < n_cb) load_block<HB>(hdr, levels, (int64_t)kb * N + nn, hd[u], lv[u]);
+    const int n_units = n_cb * 4;
+    TabIn tin;
+    if constexpr (kMode == 1 || kMode == 2) {
+        const int u = min(tid, n_units - 1);
+        tab_load<kMode>(tin, X, basis, scales, Zin, u >> 2, u & 3);
     }
-    const KbInfo* ti = table;
+    BlockRec buf[D + 1];
+#pragma unroll
+    for (int i = 0; i <= D; ++i) load_rec<HB>(buf[i], hdr, levels, bid(i));
     if constexpr (kMode == 0) {
-        if (n_cb <= kLdsMaxKb) {
-            const uint4* src = reinterpret_cast<const uint4*>(table);
-            uint4* dst = reinterpret_cast<uint4*>(info);
-            for (int i = tid; i < n_cb * 7; i += kPanelThreads) dst[i] = src[i];
-            ti = info;
+        const uint4* src = reinterpret_cast<const uint4*>(table);
+        uint4* dst = reinterpret_cast<uint4*>(info);
+        for (int i = tid; i < n_cb * 7; i += kPanelThreads) dst[i] = src[i];
+    } else if constexpr (kMode == 1 || kMode == 2) {
+        tab_store<kMode>(info, tin, min(tid, n_units - 1) >> 2, tid & 3, tid < n_units);
+        for (int u0 = kPanelThreads; u0 < n_units; u0 += kPanelThreads) {
+            const int u = min(u0 + tid, n_units - 1);
+            tab_load<kMode>(tin, X, basis, scales, Zin, u >> 2, u & 3);
+            tab_store<kMode>(info, tin, u >> 2, u & 3, u0 + tid < n_units);
         }
-    } else {
-        stage_table<kMode == 2>(info, X, basis, scales, Zin, n_cb);
-        ti = info;
     }
     __syncthreads();
 
+    const KbInfo* ti = kMode == 3 ? table : info;
     const SpliceK sk = splice_consts();
     float acc = 0.f;
-    for (int kb0 = j;;) {
+    auto step = [&](const BlockRec& o, int r) {
+        const float v = block_dot(o, ti[kbc(r)], sk);
+        acc += (j + r * S < n_cb) ? v : 0.f;
+    };
+    int r = 0;
+    for (; r + D < R; r += D + 1) {
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const int kb = kb0 + u * S;
-            if (kb < n_cb) {
-                const uint32_t H[4] = {lv[u][0].x, lv[u][0].y, lv[u][1].x, lv[u][1].y};
-                const uint32_t Pw[2] = {lv[u][2].x, lv[u][2].y};
-                const float lo = sx8_h2f(hd[u][0]), hi = sx8_h2f(hd[u][0] >> 16);
-                const uint32_t cfg = hd[u][1] & 0xFFu, cf = (hd[u][1] >> 8) & 0xFFu;
-                if (__builtin_amdgcn_ballot_w64(!(hi >= lo)) == 0)   // wave-uniform
-                    acc += block_dot_fast(lo, hi, cfg, cf, H, Pw, ti[kb], sk);
-                else
-                    acc += block_dot_exact(lo, hi, cfg, cf, H, Pw, ti[kb], sk);
-            }
-        }
-        kb0 += kUnroll * S;
-        if (kb0 >= n_cb) break;
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const int kb = kb0 + u * S;
-            if (kb < n_cb) load_block<HB>(hdr, levels, (int64_t)kb * N + nn, hd[u], lv[u]);
+        for (int i = 0; i <= D; ++i) {
+            step(buf[i], r + i);
+            __builtin_amdgcn_sched_barrier(0);
+            load_rec<HB>(buf[i], hdr, levels, bid(r + i + D + 1));
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
+#pragma unroll
+    for (int i = 0; i < D; ++i)
+        if (r + i < R) step(buf[i], r + i);
 
     // slices -> columns: xor tree over the slices inside each wave (lanes c, c + CT,
     // ...), then the 8 wave sums in wave order; fixed order, so deterministic
@@ -394,12 +392,27 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     }
 }
 
-// Panel width: the widest power of two <= 64 that still gives >= 256 work-groups (one
-// per CU); wider panels amortise the per-work-group table build over more columns.
-inline int panel_ct_log2(int N) {
-    int lg = 6;
-    while (lg > 2 && (N + (1 << lg) - 1) / (1 << lg) < 256) --lg;
-    return lg;
+// Panel width: 16 columns (a slice reads 384 contiguous level bytes, three cache lines),
+// 32 when that still leaves >= 256 work-groups and the K loop is short, 8 when 16 would
+// leave fewer than 128 work-groups.
+inline int panel_ct_log2(int N, int n_cb) {
+    const int g16 = (N + 15) / 16;
+    if (g16 < 128) return N >= 1024 ? 3 : 2;
+    if ((N + 31) / 32 >= 256 && n_cb <= 96) return 5;
+    return 4;
+}
+
+template <int HB, int kMode>
+void launch_panel(int D, dim3 grid, size_t smem, hipStream_t st, const uint16_t* X,
+                  const uint8_t* hdr, const uint8_t* levels, const float* basis,
+                  const float* scales, const float* Zin, const KbInfo* table, float* Y, int N,
+                  int n_cb, int lg) {
+    if (D == 2)
+        hipLaunchKernelGGL((k_gemv_panel<HB, kMode, 2>), grid, dim3(kPanelThreads), smem, st, X,
+                           hdr, levels, basis, scales, Zin, table, Y, N, n_cb, lg);
+    else
+        hipLaunchKernelGGL((k_gemv_panel<HB, kMode, 1>), grid, dim3(kPanelThreads), smem, st, X,
+                           hdr, levels, basis, scales, Zin, table, Y, N, n_cb, lg);
 }
 
 template <int HB>
@@ -407,17 +420,20 @@ int32_t launch_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels
                     const float* basis, const float* scales, const float* Zin, float* Zout,
                     int N, int n_cb, float* Y, KbInfo* table, hipStream_t st) {
     using namespace sx8;
-    const int lg = panel_ct_log2(N);
+    const int lg = panel_ct_log2(N, n_cb);
+    const int S = kPanelThreads >> lg;
+    const int R = (n_cb + S - 1) / S;
+    const int D = R >= 6 ? 2 : 1;
     const dim3 grid((N + (1 << lg) - 1) >> lg);
     const bool lds = n_cb <= kLdsMaxKb;
     const size_t smem = sizeof(float) * kPanelThreads + (lds ? sizeof(KbInfo) * (size_t)n_cb : 0);
     if (!Zout && lds) {   // single launch: the table is built inside every work-group
         if (Zin)
-            hipLaunchKernelGGL((k_gemv_panel<HB, 2>), grid, dim3(kPanelThreads), smem, st, X, hdr,
-                               levels, basis, scales, Zin, table, Y, N, n_cb, lg);
+            launch_panel<HB, 2>(D, grid, smem, st, X, hdr, levels, basis, scales, Zin, table, Y,
+                                N, n_cb, lg);
         else
-            hipLaunchKernelGGL((k_gemv_panel<HB, 1>), grid, dim3(kPanelThreads), smem, st, X, hdr,
-                               levels, basis, scales, Zin, table, Y, N, n_cb, lg);
+            launch_panel<HB, 1>(D, grid, smem, st, X, hdr, levels, basis, scales, Zin, table, Y,
+                                N, n_cb, lg);
         return check_launch("sx8_gemv");
     }
     const dim3 tgrid((n_cb + 7) / 8);
@@ -427,8 +443,12 @@ int32_t launch_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels
     else
         hipLaunchKernelGGL(k_kbinfo<false>, tgrid, dim3(256), 0, st, X, basis, scales, Zin, Zout,
                            n_cb, table);
-    hipLaunchKernelGGL((k_gemv_panel<HB, 0>), grid, dim3(kPanelThreads), smem, st, X, hdr, levels,
-                       basis, scales, Zin, table, Y, N, n_cb, lg);
+    if (lds)
+        launch_panel<HB, 0>(D, grid, smem, st, X, hdr, levels, basis, scales, Zin, table, Y, N,
+                            n_cb, lg);
+    else
+        launch_panel<HB, 3>(D, grid, smem, st, X, hdr, levels, basis, scales, Zin, table, Y, N,
+                            n_cb, lg);
     return check_launch("sx8_gemv");
 }
 
