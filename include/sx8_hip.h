@@ -71,7 +71,8 @@ int32_t sx8_embed_gather(const int64_t* ids, int64_t T, const uint8_t* hdr,
  * for m < M, in float32 with the reference's summation tree.
  * Replaces compute_z44 (cuda/sx8_decode1_v3.cu:185-195, kernel :44-65) for M = 1 and
  * compute_z44_batch (cuda/sx8_gemm_compact.cu:157-169, kernel :28-50) for M > 1.
- * X is (M, ldx) fp16 with ldx >= n_cb*32.  Z is (M, n_cb, 2) float32. */
+ * X is (M, ldx) fp16 with ldx >= n_cb*32.  Z is (M, n_cb, 2) float32 (8-byte aligned);
+ * basis 16-byte aligned. */
 int32_t sx8_compute_z(const uint16_t* X, int64_t M, int64_t ldx, const float* basis,
                       const float* scales, int64_t n_cb, float* Z, void* stream);
 
@@ -93,11 +94,15 @@ int32_t sx8_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels,
 int64_t sx8_gemv_workspace_bytes(int64_t n_cb);
 
 /* Prefill GEMM Y (M, N) float32 = X (M, ldx) fp16 . W^T on the v4.4 layout.
- * Each weight tile is dequantized with R64 (bit-exact fp16) into MFMA operands and
- * accumulated in float32 (v_mfma_f32_16x16x32_f16).  Columns k >= K of X are never
- * read; the kernel zero-fills the padded tail of the last K block.
+ * The PCA-free core weights (rlo + step*lv, float32 then fp16) are decoded straight into
+ * MFMA operands (v_mfma_f32_32x32x16_f16, float32 accumulation); the PCA term
+ * sum_kb c0 Z0 + c1 Z1 is added by extra MFMA k-steps from Z, which this call computes
+ * first (reference summation tree) into the library's per-device workspace (allocated on
+ * first use; calls overlapping on one device must not share it -- use
+ * sx8_gemm_prefill_z with a caller-owned Z instead).  Columns k >= K of X are never
+ * read.  Tolerance against the float64 yardstick: max|dY| / max|Y| <= 1e-3.
  * Replaces gemm_compact (cuda/sx8_gemm_compact.cu:171-194, kernel :55-152) together
- * with its Z precompute: the PCA term is applied per weight instead. */
+ * with its Z precompute compute_z44_batch (:157-169). */
 int32_t sx8_gemm_prefill(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
                          const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
                          const float* basis, const float* scales, int64_t N, int64_t n_cb,
@@ -113,16 +118,23 @@ int32_t sx8_gemm_prefill_split(const uint16_t* X, int64_t M, int64_t ldx, int64_
                                const float* scales, int64_t N, int64_t n_cb, float* Y,
                                void* stream);
 
-/* Output-side PCA GEMM: Y[m, n] += sum_kb c0(kb,n) Z[m,kb,0] + c1(kb,n) Z[m,kb,1],
- * c0/c1 the signed nibbles of the coeff byte in the v4.4 header.  Together with
- * sx8_gemm_prefill_core it forms the reference's gemm_compact(X, hdr, levels, Z, ...)
- * contract (cuda/sx8_gemm_compact.cu:171-194), whose PCA term comes from a
- * caller-supplied Z. */
+/* Same GEMM with the PCA precompute supplied by the caller: Z (M, n_cb, 2) float32 as
+ * written by sx8_compute_z.  One launch; no workspace.
+ * Replaces gemm_compact(X, hdr, levels, Z, n_cb, hdr_bytes) (cuda/sx8_gemm_compact.cu:
+ * 171-194, kernel :55-152). */
+int32_t sx8_gemm_prefill_z(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
+                           const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
+                           const float* Z, int64_t N, int64_t n_cb, float* Y, void* stream);
+
+/* Output-side PCA: Y[m, n] += sum_kb c0(kb,n) Z[m,kb,0] + c1(kb,n) Z[m,kb,1], c0/c1 the
+ * signed nibbles of the coeff byte in the v4.4 header (float32 FMAs, one thread per
+ * column).  The PCA step of gemm_compact's epilogue (cuda/sx8_gemm_compact.cu:130-150)
+ * as a separate pass, for callers that hold a core-only result. */
 int32_t sx8_gemm_pca_z(const float* Z, int64_t M, const uint8_t* hdr, int32_t hdr_bytes,
                        int64_t N, int64_t n_cb, float* Y, void* stream);
 
-/* Prefill GEMM of the PCA-free core weights (rlo + step*lv, R64 without the two PCA
- * terms), used with sx8_gemm_pca_z for the caller-supplied-Z contract. */
+/* Prefill GEMM of the PCA-free core weights only (rlo + step*lv); with sx8_gemm_pca_z it
+ * gives the same product as sx8_gemm_prefill_z in two passes. */
 int32_t sx8_gemm_prefill_core(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
                               const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
                               int64_t N, int64_t n_cb, float* Y, void* stream);

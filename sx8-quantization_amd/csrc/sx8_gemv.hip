@@ -64,33 +64,58 @@ __device__ __forceinline__ void fill_x_side(KbInfo& out, int sb, const uint4 xv)
 constexpr int kPanelThreads = 512;
 constexpr int kLdsMaxKb = 640;     // activation table staged in LDS up to this many K blocks
 
-// Z of one (row, kb, j) with the reference's warp tree: products x_t * b_t, then
-// pairwise sums over lane offsets 16, 8, 4, 2, 1 (cuda/sx8_decode1_v3.cu:53-63),
-// then scale * sum.  One thread does the whole tree (used for M > 1 rows).
-__device__ __forceinline__ float z_tree(const uint16_t* __restrict__ x,
-                                        const float* __restrict__ b, float scale) {
-#pragma clang fp contract(off)
-    float p[32];
-#pragma unroll
-    for (int t = 0; t < 32; ++t) p[t] = sx8_h2f(x[t]) * b[t];
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1)
-#pragma unroll
-        for (int t = 0; t < off; ++t) p[t] = p[t] + p[t + off];
-    return scale * p[0];
-}
-
+// Z of one (row, kb, j) follows the reference's warp tree: products x_t * b_t, then
+// pairwise sums over lane offsets 16, 8, 4, 2, 1 (cuda/sx8_decode1_v3.cu:53-63), then
+// scale * sum.
+// One thread per (row m, kb): both Z values, x read once as four 16-byte vectors (the
+// row's tail past K is zero), products and the reference tree in registers.
 __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ X, int64_t M,
-                                                   int64_t ldx, const float* __restrict__ basis,
+                                                   int64_t ldx, int64_t K,
+                                                   const float* __restrict__ basis,
                                                    const float* __restrict__ scales, int64_t n_cb,
-                                                   float* __restrict__ Z) {
+                                                   bool x_vec, float* __restrict__ Z) {
+#pragma clang fp contract(off)
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (gid >= M * n_cb * 2) return;
-    const int j = (int)(gid & 1);
-    const int64_t mk = gid >> 1;
-    const int64_t m = mk / n_cb;
-    const int64_t kb = mk - m * n_cb;
-    Z[gid] = z_tree(X + m * ldx + kb * 32, basis + kb * 64 + 32 * j, scales[kb * 2 + j]);
+    if (gid >= M * n_cb) return;
+    const int64_t m = gid / n_cb;
+    const int64_t kb = gid - m * n_cb;
+    const uint16_t* x = X + m * ldx + kb * 32;
+    const int kmax = (int)min((int64_t)32, K - kb * 32);
+    uint32_t xw[16];
+    if (x_vec && kmax == 32) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4 v = reinterpret_cast<const uint4*>(x)[q];
+            xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const uint32_t a = 2 * t < kmax ? x[2 * t] : 0u;
+            const uint32_t b = 2 * t + 1 < kmax ? x[2 * t + 1] : 0u;
+            xw[t] = a | (b << 16);
+        }
+    }
+    const float4* bv = reinterpret_cast<const float4*>(basis + kb * 64);
+    float z[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        float p[32];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float4 b = bv[8 * j + q];
+            p[4 * q] = sx8_h2f(xw[2 * q]) * b.x;
+            p[4 * q + 1] = sx8_h2f(xw[2 * q] >> 16) * b.y;
+            p[4 * q + 2] = sx8_h2f(xw[2 * q + 1]) * b.z;
+            p[4 * q + 3] = sx8_h2f(xw[2 * q + 1] >> 16) * b.w;
+        }
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1)
+#pragma unroll
+            for (int t = 0; t < off; ++t) p[t] = p[t] + p[t + off];
+        z[j] = scales[kb * 2 + j] * p[0];
+    }
+    *reinterpret_cast<float2*>(Z + gid * 2) = make_float2(z[0], z[1]);
 }
 
 // Activation-side table, one 32-lane group per kb (8 kb per 256-thread block).
@@ -458,6 +483,17 @@ extern "C" int64_t sx8_gemv_workspace_bytes(int64_t n_cb) {
     return n_cb > 0 ? n_cb * (int64_t)sizeof(KbInfo) : 0;
 }
 
+int32_t sx8::compute_z(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, const float* basis,
+                       const float* scales, int64_t n_cb, float* Z, hipStream_t st) {
+    const int64_t threads = M * n_cb;
+    const int64_t grid = (threads + 255) / 256;
+    if (grid > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "compute_z: too large");
+    const bool x_vec = aligned(X, 16) && ldx % 8 == 0;
+    hipLaunchKernelGGL(k_compute_z, dim3((unsigned)grid), dim3(256), 0, st, X, M, ldx, K, basis,
+                       scales, n_cb, x_vec, Z);
+    return check_launch("compute_z");
+}
+
 extern "C" int32_t sx8_compute_z(const uint16_t* X, int64_t M, int64_t ldx, const float* basis,
                                  const float* scales, int64_t n_cb, float* Z, void* stream) {
     using namespace sx8;
@@ -465,14 +501,9 @@ extern "C" int32_t sx8_compute_z(const uint16_t* X, int64_t M, int64_t ldx, cons
     if (M <= 0 || n_cb <= 0 || ldx < n_cb * 32)
         return fail(SX8_ERR_INVALID, "sx8_compute_z: bad shape M=%lld ldx=%lld n_cb=%lld",
                     (long long)M, (long long)ldx, (long long)n_cb);
-    if (!aligned(X, 2) || !aligned(basis, 4) || !aligned(scales, 4) || !aligned(Z, 4))
-        return fail(SX8_ERR_INVALID, "sx8_compute_z: misaligned pointer");
-    const int64_t threads = M * n_cb * 2;
-    const int64_t grid = (threads + 255) / 256;
-    if (grid > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "sx8_compute_z: too large");
-    hipLaunchKernelGGL(k_compute_z, dim3((unsigned)grid), dim3(256), 0, as_stream(stream), X, M,
-                       ldx, basis, scales, n_cb, Z);
-    return check_launch("sx8_compute_z");
+    if (!aligned(X, 2) || !aligned(basis, 16) || !aligned(scales, 4) || !aligned(Z, 8))
+        return fail(SX8_ERR_INVALID, "sx8_compute_z: misaligned pointer (basis 16 B, Z 8 B)");
+    return compute_z(X, M, ldx, n_cb * 32, basis, scales, n_cb, Z, as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels,

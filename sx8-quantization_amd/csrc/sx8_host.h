@@ -30,4 +30,10 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // SX8_ERR_HIP.
 int32_t device_workspace(int64_t bytes, void** ptr);
 
+// Z[m, kb, j] = scales[kb, j] * sum_t X[m, kb*32+t] * basis[kb, 32j+t] (reference tree
+// order), reading only columns k < K of X (the rest count as zero).  Launch only; the
+// caller validated the arguments.
+int32_t compute_z(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, const float* basis,
+                  const float* scales, int64_t n_cb, float* Z, hipStream_t st);
+
 }  // namespace sx8

@@ -3,11 +3,10 @@
 Interface of scripts/sx8_gemm_compact.py (reference): ``_ext()`` (an object with
 ``compute_z44_batch`` and ``gemm_compact``) and ``gemm_sx8_compact``.
 
-``gemm_sx8_compact`` runs sx8_gemm_prefill: each weight tile is decoded with the
-canonical R64 recipe (bit-exact fp16, PCA per weight) straight into MFMA operands
-and accumulated in float32, so no Z precompute is needed.  ``_ext().gemm_compact``
-keeps the reference's caller-supplied-Z contract: the PCA-free core GEMM plus an
-output-side PCA pass over Z.
+``gemm_sx8_compact`` runs sx8_gemm_prefill: Z is computed inside the call, the core
+weights (rlo + step*lv) are decoded in float32 straight into MFMA operands and the PCA
+term rides along as extra MFMA k-steps over Z.  ``_ext().gemm_compact`` keeps the
+reference's caller-supplied-Z contract with the same kernel (sx8_gemm_prefill_z).
 """
 from __future__ import annotations
 
@@ -51,11 +50,11 @@ class _Ext:
         N = hdr.size(0) // n_cb
         Kc = min(K, n_cb * 32)
         Y = torch.empty((M, N), dtype=torch.float32, device=Xc.device)
-        st = _L.stream(Xc.device)
-        _L.call("sx8_gemm_prefill_core", _L.ptr(Xc), M, K, Kc, _L.ptr(hdr), _L.ptr(levels),
-                int(hdr_bytes), N, n_cb, _L.ptr(Y), st)
-        _L.call("sx8_gemm_pca_z", _L.ptr(Z.contiguous()), M, _L.ptr(hdr), int(hdr_bytes), N,
-                n_cb, _L.ptr(Y), st)
+        Zc = Z.contiguous().float()
+        if Zc.numel() != M * n_cb * 2:
+            raise ValueError(f"Z must hold (M, n_cb, 2) = ({M}, {n_cb}, 2) values")
+        _L.call("sx8_gemm_prefill_z", _L.ptr(Xc), M, K, Kc, _L.ptr(hdr), _L.ptr(levels),
+                int(hdr_bytes), _L.ptr(Zc), N, n_cb, _L.ptr(Y), _L.stream(Xc.device))
         return Y
 
 

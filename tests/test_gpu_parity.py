@@ -214,20 +214,30 @@ def test_prefill_gemm(hiplib, oracle, cuda, name, N, K, M):
     rel = oracle.rel_err(Y.cpu().numpy(), Y_ref)
     _say("   rel", rel)
     assert rel <= 1e-3
-    # bit-exact operands: the GEMM matches fp32 accumulation over the exact fp16 W
+    # against fp32 accumulation over the exact fp16 W (the kernel rounds the PCA-free
+    # core weights to fp16 and adds PCA through Z, so the two differ by fp16 rounding)
     Y32 = X.float() @ torch.from_numpy(W.astype(np.float32)).T
-    assert oracle.rel_err(Y.cpu().numpy(), Y32.numpy()) <= 2e-6
+    _say("   rel vs fp32(W_R64)", oracle.rel_err(Y.cpu().numpy(), Y32.numpy()))
+    assert oracle.rel_err(Y.cpu().numpy(), Y32.numpy()) <= 1e-3
     # the split-array (fused-WMMA) contract runs the same kernel: identical output
     kbm, _ = to_kbmajor(qt, bi)
     Yw = gemm_sx8_wmma_cached(X.to(cuda), make_tensors(kbm, bi, cuda), qt["n_cb"])
     assert torch.equal(Yw.cpu(), Y.cpu())
-    # caller-supplied Z contract (core GEMM + output-side PCA)
+    # caller-supplied Z contract: same kernel, same Z values -> identical output
     ext = _ext()
     Xp = torch.zeros(M, qt["n_cb"] * 32, dtype=torch.float16)
     Xp[:, :K] = X
     Z = ext.compute_z44_batch(Xp.to(cuda), t[2], t[3], qt["n_cb"])
     Yz = ext.gemm_compact(Xp.to(cuda), t[0], t[1], Z, qt["n_cb"], 6)
-    assert oracle.rel_err(Yz.cpu().numpy(), Y_ref) <= 1e-3
+    assert torch.equal(Yz.cpu(), Y.cpu())
+    # two-pass form: core-only GEMM, then the output-side PCA pass over Z
+    import _sx8lib as L
+    Yc = torch.empty_like(Yz)
+    Xd = Xp.to(cuda)
+    L.call("sx8_gemm_prefill_core", L.ptr(Xd), M, Xd.shape[1], Xd.shape[1], L.ptr(t[0]),
+           L.ptr(t[1]), 6, N, qt["n_cb"], L.ptr(Yc), L.stream(cuda))
+    L.call("sx8_gemm_pca_z", L.ptr(Z), M, L.ptr(t[0]), 6, N, qt["n_cb"], L.ptr(Yc), L.stream(cuda))
+    assert oracle.rel_err(Yc.cpu().numpy(), Y_ref) <= 1e-3
 
 
 def test_prefill_deterministic(hiplib, cuda):
