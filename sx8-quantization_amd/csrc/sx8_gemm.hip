@@ -58,32 +58,6 @@ struct LaneRec {
     uint32_t p;
 };
 
-typedef uint32_t sx8_u32_a2 __attribute__((aligned(2)));
-
-template <bool kSplit, int HB>
-__device__ __forceinline__ void load_lane_rec(LaneRec& r, const WeightSrc& w, int64_t bid, int s) {
-    if constexpr (kSplit) {
-        r.lohi = w.dmin[bid];
-        r.hi16 = w.dmax[bid];
-        r.cc = w.config[bid];
-        r.cf = w.coeff[bid];
-        r.h = *reinterpret_cast<const uint2*>(w.hi + bid * 16 + 8 * s);
-        r.p = *reinterpret_cast<const uint32_t*>(w.lo + bid * 8 + 4 * s);
-    } else {
-        if constexpr (HB == 8) {
-            const uint2 v = *reinterpret_cast<const uint2*>(w.hdr + bid * 8);
-            r.lohi = v.x;
-            r.cc = v.y;
-        } else {
-            r.lohi = *reinterpret_cast<const sx8_u32_a2*>(w.hdr + bid * 6);
-            r.cc = *reinterpret_cast<const uint16_t*>(w.hdr + bid * 6 + 4);
-        }
-        r.hi16 = r.cf = 0;
-        r.h = *reinterpret_cast<const uint2*>(w.levels + bid * 24 + 8 * s);
-        r.p = *reinterpret_cast<const uint32_t*>(w.levels + bid * 24 + 16 + 4 * s);
-    }
-}
-
 // endpoints (dmin | dmax << 16) and config of a loaded record
 template <bool kSplit>
 __device__ __forceinline__ void rec_unpack(const LaneRec& r, uint32_t& lohi, uint32_t& cfg) {
@@ -94,12 +68,6 @@ __device__ __forceinline__ void rec_unpack(const LaneRec& r, uint32_t& lohi, uin
         lohi = r.lohi;
         cfg = r.cc & 0xFFu;
     }
-}
-
-template <bool kSplit, int HB>
-__device__ __forceinline__ uint32_t load_coeff(const WeightSrc& w, int64_t bid) {
-    if constexpr (kSplit) return w.coeff[bid];
-    else return w.hdr[bid * HB + 5];
 }
 
 // Core weights (rlo + step * lv, float32, then RNE to fp16) of one 8-weight sub-block in
@@ -214,29 +182,73 @@ __device__ __forceinline__ uint32_t coeff_pair_f16(int c) {
 
 // Everything one K block needs from memory, loaded two iterations before its use: the X
 // chunks of block kb (stored to LDS at the end of iteration kb - 1), this lane's weight
-// record and PCA coefficients of block kb, and the Z-tile value stored at the end of
-// iteration kb - 1.
+// record of block kb, and the Z-tile value stored at the end of iteration kb - 1.
 struct Stage {
     sx8_u32x4 xv[2];
     LaneRec rec;
-    uint32_t ca = 0, cb = 0;
     float zq = 0.f;
 };
 
+// Buffer resources and per-lane byte offsets for the main loop's loads.  Everything that
+// depends on the K block goes into the scalar offset of a buffer load, so the loop does no
+// per-lane address arithmetic; loads past a buffer's end return zero.
+typedef __amdgpu_buffer_rsrc_t sx8_rsrc;
+constexpr int kRsrcFlags = 0x00020000;   // raw 32-bit buffer (gfx9 resource word 3)
+
+__device__ __forceinline__ sx8_rsrc make_rsrc(const void* p, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
+                                             (int)min(bytes, (int64_t)0x7FFFFFFF), kRsrcFlags);
+}
+
+struct LoopSrc {
+    sx8_rsrc x, hdr, lv, z, dmin, dmax, cfg, cf, hi, lo;
+    int x_off[2];      // X chunk i: row * ldx * 2 + 16 * sb
+    int rec_off;       // nn (column) in blocks
+    int z_off;         // Z value of quarter 0 of group 0
+};
+
 template <bool kSplit, int HB, bool kPca, bool kFast>
-__device__ __forceinline__ void load_stage(Stage& st, const uint16_t* __restrict__ X, int M,
-                                           int64_t ldx, int K, const WeightSrc& w,
-                                           const float* __restrict__ Z, int N, int n_cb, int m0,
-                                           int64_t nn, int s, int kb) {
+__device__ __forceinline__ void load_stage(Stage& st, const LoopSrc& ls,
+                                           const uint16_t* __restrict__ X, int M, int64_t ldx,
+                                           int K, int N, int n_cb, int m0, int s, int kb) {
     const int kc = min(kb, n_cb - 1);
-    load_x_chunks<kFast>(X, M, ldx, K, m0, kc, st.xv);
-    load_lane_rec<kSplit, HB>(st.rec, w, (int64_t)kc * N + nn, s);
+    if constexpr (kFast) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            st.xv[i] = __builtin_bit_cast(sx8_u32x4,
+                                          __builtin_amdgcn_raw_buffer_load_b128(ls.x, ls.x_off[i], kc * 64, 0));
+    } else {
+        load_x_chunks<false>(X, M, ldx, K, m0, kc, st.xv);
+    }
+    const int nn = ls.rec_off;
+    const int rowb = kc * N;                       // first block of K row kc
+    if constexpr (kSplit) {
+        st.rec.lohi = __builtin_amdgcn_raw_buffer_load_b16(ls.dmin, nn * 2, rowb * 2, 0);
+        st.rec.hi16 = __builtin_amdgcn_raw_buffer_load_b16(ls.dmax, nn * 2, rowb * 2, 0);
+        st.rec.cc = __builtin_amdgcn_raw_buffer_load_b8(ls.cfg, nn, rowb, 0);
+        st.rec.cf = __builtin_amdgcn_raw_buffer_load_b8(ls.cf, nn, rowb, 0);
+        st.rec.h = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ls.hi, nn * 16 + 8 * s, rowb * 16, 0));
+        st.rec.p = __builtin_amdgcn_raw_buffer_load_b32(ls.lo, nn * 8 + 4 * s, rowb * 8, 0);
+    } else {
+        if constexpr (HB == 8) {
+            const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ls.hdr, nn * 8, rowb * 8, 0));
+            st.rec.lohi = v.x;
+            st.rec.cc = v.y;
+        } else {
+            st.rec.lohi = __builtin_amdgcn_raw_buffer_load_b32(ls.hdr, nn * 6, rowb * 6, 0);
+            st.rec.cc = __builtin_amdgcn_raw_buffer_load_b16(ls.hdr, nn * 6 + 4, rowb * 6, 0);
+        }
+        st.rec.hi16 = st.rec.cf = 0;
+        st.rec.h = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ls.lv, nn * 24 + 8 * s, rowb * 24, 0));
+        st.rec.p = __builtin_amdgcn_raw_buffer_load_b32(ls.lv, nn * 24 + 16 + 4 * s, rowb * 24, 0);
+    }
     if constexpr (kPca) {
-        const int ka = (kc & ~3) + 2 * s;
-        st.ca = load_coeff<kSplit, HB>(w, (int64_t)min(ka, n_cb - 1) * N + nn);
-        st.cb = load_coeff<kSplit, HB>(w, (int64_t)min(ka + 1, n_cb - 1) * N + nn);
         const int i = max(kb - 1, 0);   // iteration whose end stores this value
-        st.zq = load_z_quarter(Z, M, n_cb, m0, (i >> 2) + 1, i & 3);
+        const int g = (i >> 2) + 1, q = i & 3;
+        // value e of row 32 q + t / 8: Z[(m n_cb + 4 g + e / 2) * 2 + e % 2]; the whole offset
+        // is in the vector part, so the buffer range check zeroes reads past the end
+        st.zq = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                              ls.z, ls.z_off + (q * 32 * n_cb * 2 + g * 8) * 4, 0, 0));
     }
 }
 
@@ -263,10 +275,36 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ 
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[r][i] = 0.f;
 
+    LoopSrc ls;
+    ls.x = make_rsrc(X, (int64_t)M * ldx * 2);
+    const int64_t n_blk = (int64_t)N * n_cb;
+    if constexpr (kSplit) {
+        ls.dmin = make_rsrc(w.dmin, n_blk * 2);
+        ls.dmax = make_rsrc(w.dmax, n_blk * 2);
+        ls.cfg = make_rsrc(w.config, n_blk);
+        ls.cf = make_rsrc(w.coeff, n_blk);
+        ls.hi = make_rsrc(w.hi, n_blk * 16);
+        ls.lo = make_rsrc(w.lo, n_blk * 8);
+    } else {
+        ls.hdr = make_rsrc(w.hdr, n_blk * HB);
+        ls.lv = make_rsrc(w.levels, n_blk * 24);
+    }
+    if constexpr (kPca) ls.z = make_rsrc(Z, (int64_t)M * n_cb * 8);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = tid + i * kThreads;
+        ls.x_off[i] = (int)((int64_t)(m0 + (c >> 2)) * ldx * 2) + 16 * (c & 3);
+    }
+    ls.rec_off = (int)nn;
+    {
+        const int e = tid & 7;
+        ls.z_off = (int)(((int64_t)(m0 + (tid >> 3)) * n_cb * 2 + (e >> 1) * 2 + (e & 1)) * 4);
+    }
+
     // prologue: stages of blocks 0 and 1 in flight, X tile 0 and the Z tile of group 0
     Stage S0, S1;
-    load_stage<kSplit, HB, kPca, kFast>(S0, X, M, ldx, K, w, Z, N, n_cb, m0, nn, s, 0);
-    load_stage<kSplit, HB, kPca, kFast>(S1, X, M, ldx, K, w, Z, N, n_cb, m0, nn, s, 1);
+    load_stage<kSplit, HB, kPca, kFast>(S0, ls, X, M, ldx, K, N, n_cb, m0, s, 0);
+    load_stage<kSplit, HB, kPca, kFast>(S1, ls, X, M, ldx, K, N, n_cb, m0, s, 1);
     if constexpr (kPca) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -275,6 +313,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ 
     store_x_chunks(xs[0], S0.xv);
     __syncthreads();
 
+    uint32_t cfa = 0, cfb = 0;
     // One K block: decode from `cur` (then refill it with block kb + 2), MFMAs on X tile
     // kb, PCA k-step at the end of a group, publish `nxt`'s X tile and Z value.
     auto body = [&](int kb, Stage& cur, const Stage& nxt) __attribute__((always_inline)) {
@@ -296,14 +335,19 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ 
         }
         sx8_half8 cop;
         if constexpr (kPca) {
-            const int ka = (min(kb, n_cb - 1) & ~3) + 2 * s;
-            const uint32_t ca = ka < n_cb ? cur.ca : 0u;
-            const uint32_t cb = ka + 1 < n_cb ? cur.cb : 0u;
-            const sx8_u32x4 cv = {coeff_pair_f16(sx8_sext4(ca)), coeff_pair_f16(sx8_sext4(ca >> 4)),
-                                  coeff_pair_f16(sx8_sext4(cb)), coeff_pair_f16(sx8_sext4(cb >> 4))};
+            // this lane's PCA k-step needs the coefficients of blocks 4g + 2s and 4g + 2s + 1
+            // of its column: keep them as the group's blocks pass by (0 for absent blocks)
+            const int j = kb & 3;
+            const uint32_t cf = kSplit ? cur.rec.cf : (cur.rec.cc >> 8);
+            if (live) {
+                cfa = j == 2 * s ? cf : (j == 0 ? 0u : cfa);
+                cfb = j == 2 * s + 1 ? cf : (j == 0 ? 0u : cfb);
+            }
+            const sx8_u32x4 cv = {coeff_pair_f16(sx8_sext4(cfa)), coeff_pair_f16(sx8_sext4(cfa >> 4)),
+                                  coeff_pair_f16(sx8_sext4(cfb)), coeff_pair_f16(sx8_sext4(cfb >> 4))};
             cop = __builtin_bit_cast(sx8_half8, cv);
         }
-        load_stage<kSplit, HB, kPca, kFast>(cur, X, M, ldx, K, w, Z, N, n_cb, m0, nn, s, kb + 2);
+        load_stage<kSplit, HB, kPca, kFast>(cur, ls, X, M, ldx, K, N, n_cb, m0, s, kb + 2);
 
         const uint16_t* xt = xs[kb & 1];
 #pragma unroll
@@ -382,6 +426,9 @@ int32_t check_shape(const char* what, int64_t M, int64_t ldx, int64_t K, int64_t
         return fail(SX8_ERR_INVALID, "%s: bad shape M=%lld K=%lld ldx=%lld N=%lld n_cb=%lld", what,
                     (long long)M, (long long)K, (long long)ldx, (long long)N, (long long)n_cb);
     if ((M + kBM - 1) / kBM > 65535) return fail(SX8_ERR_UNSUPPORTED, "%s: M too large", what);
+    // the main loop addresses every operand with 32-bit buffer offsets
+    if (M * ldx * 2 > 0x7FFFFFFF || N * n_cb * 24 > 0x7FFFFFFF || M * n_cb * 8 > 0x7FFFFFFF)
+        return fail(SX8_ERR_UNSUPPORTED, "%s: operands beyond 2 GiB", what);
     return SX8_OK;
 }
 
