@@ -49,7 +49,8 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|embed")
+    ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|embed|copy (copy: the "
+                    "512 MiB device copy that calibrates the HBM byte counters)")
     return ap.parse_args()
 
 
@@ -269,6 +270,27 @@ def bench_embed(torch, L, layer, args):
     return {"table": f"{t['N']}x{t['K']}", "ids": 512, "us": us, "gbs": (rd + wr) / (us * 1e-6) / 1e9}
 
 
+def bench_copy(torch, args):
+    """Plain device copy of 512 MiB (torch's elementwise copy kernel), 10 launches: the
+    known-size kernel that calibrates the FETCH_SIZE / WRITE_SIZE counters (each launch
+    reads and writes exactly 512 MiB), and the achievable streaming rate of this GPU."""
+    nbytes = 512 << 20
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gpu_delay(torch, 10)
+    a.record()
+    for _ in range(10):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / 10
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "us": us,
+            "gbs": 2 * nbytes / (us * 1e-6) / 1e9}
+
+
 def cpu_baseline(layer, seconds):
     """The oracle's C restatement (R64 dequant to fp16 + fp32 GEMV, OpenMP) on the host,
     over as many layer shapes as fit in about `seconds`."""
@@ -323,6 +345,9 @@ def main():
     L.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.only == "copy":
+        log("copy", json.dumps(bench_copy(torch, args)))
+        return
     t0 = time.time()
     layer = build_layer(torch, dev, args.hdr_bytes)
     log(f"setup {time.time() - t0:.1f}s")

@@ -24,6 +24,15 @@ __host__ __device__ __forceinline__ float sx8_h2f(uint32_t bits) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
 }
 
+// z as two fp16 values hi = fp16(z), lo = fp16(z - hi) packed hi | lo << 16 (hi + lo
+// keeps ~22 significant bits of z).
+__device__ __forceinline__ uint32_t sx8_split_hl(float z) {
+    const _Float16 hi = (_Float16)z;
+    const _Float16 lo = (_Float16)(z - (float)hi);
+    return (uint32_t)__builtin_bit_cast(uint16_t, hi) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+}
+
 __host__ __device__ __forceinline__ int sx8_sext4(uint32_t v) {
     return (int)((v & 0xFu) ^ 0x8u) - 8;      // 0..7 -> 0..7, 8..15 -> -8..-1
 }

@@ -3,35 +3,32 @@
 // Reference roles: gemm_compact (cuda/sx8_gemm_compact.cu:55-194, CUDA-core FMAs with
 // PCA applied through Z) and sx8_wmma_kernel / fused_forward (cuda/sx8_fused_wmma.cu:
 // 11-154, WMMA 16x16x16 with per-weight PCA).  One kernel serves every contract: the
-// PCA-free core weights rlo + step*lv are decoded in float32 straight into MFMA B
-// operands, and the PCA term sum_kb c0 Z0 + c1 Z1 rides along as extra MFMA k-steps
-// (Z split into fp16 hi + lo parts, coefficients as exact fp16 integers).
+// PCA-free core weights rlo + step*lv are decoded in float32 into fp16 MFMA B operands,
+// and the PCA term sum_kb c0 Z0 + c1 Z1 rides along as extra MFMA k-steps (Z split into
+// fp16 hi + lo parts, coefficients as exact fp16 integers).
 //
-// Work decomposition (gfx950, wave64, v_mfma_f32_32x32x16_f16):
-//   * a 256-thread work-group owns a 128 x 128 output tile; wave w owns the 32 columns
-//     [32w, 32w + 32) for all 128 rows (four 32 x 32 accumulators, 64 registers).
-//   * K advances one S-X8 block (32 weights = two MFMA k-steps) per iteration.  For a
-//     32x32x16 MFMA lane l holds the B values of column l % 32 for 8 consecutive k;
-//     lane half s = l / 32 decodes sub-blocks 2s (k-step 0) and 2s + 1 (k-step 1) of
-//     its column, so every weight of the tile is decoded exactly once per work-group.
-//     The X tile keeps sub-blocks in the order 0, 2, 1, 3 to match.
-//   * X tiles (128 x 32 fp16) and Z tiles (128 rows x 4 blocks x {Z0h, Z0l, Z1h, Z1l})
-//     are double-buffered in LDS.  Global loads run two blocks ahead in two register
-//     stages, so no iteration waits for a load it issued itself (each iteration ends
-//     with a work-group barrier, and a one-block lead left every iteration waiting for a
-//     full memory latency).
+// Work decomposition (gfx950, wave64, v_mfma_f32_32x32x16_f16, 256 CUs in 8 XCDs):
+//   * a 256-thread work-group owns a (128 MF) x 128 output tile (MF = 2 once M > 128);
+//     wave w owns 32 MF rows for all 128 columns (MF x 4 accumulators of 32 x 32), so one
+//     decoded weight feeds 4 MF MFMA rows of work and each wave's X rows are its own.
+//   * K advances one S-X8 block (32 weights = two MFMA k-steps) per iteration.  Every
+//     weight of the tile is decoded once per work-group (thread t: column t % 128,
+//     sub-blocks 2 (t / 128), 2 (t / 128) + 1) into a double-buffered LDS B tile laid out
+//     in MFMA lane order; X goes from global memory straight into A registers.
+//   * global loads run two blocks ahead, and the per-iteration barrier waits for LDS only.
 //   * every 4 K blocks (and after the last one) one PCA k-step per accumulator adds
 //     Zhl (rows x 16) . C (16 x columns), C = the blocks' signed coefficient nibbles.
+//   * tiles are dealt XCD by XCD in m-major order; shapes with fewer tiles than CUs
+//     split K into ranges of whole 4-block groups and add the partials in a fixed order.
+#include <algorithm>
+
 #include "sx8_device.h"
 #include "sx8_host.h"
 
 namespace {
 
-constexpr int kBM = 128;
 constexpr int kBN = 128;
-constexpr int kThreads = 256;
-constexpr int kXPitch = 40;   // fp16 per LDS row of an X tile: 32 + 8 pad (conflict-free b128 reads)
-constexpr int kZPitch = 24;   // fp16 per LDS row of a Z tile: 16 + 8 pad
+constexpr int kThreads = 512;   // waves 0-3 run the MFMAs, waves 4-7 decode weights
 
 typedef float sx8_float16v __attribute__((ext_vector_type(16)));
 typedef uint32_t sx8_u32x4 __attribute__((ext_vector_type(4)));
@@ -48,14 +45,15 @@ struct WeightSrc {
     const uint8_t* lo;
 };
 
-// The part of one block a lane needs, as loaded (no arithmetic on freshly loaded values,
-// so prefetches stay in flight until use): v4.4 -> lohi = dmin | dmax << 16, cc = config |
-// coeff << 8; split arrays -> lohi = dmin, hi16 = dmax, cc = config, cf = coeff.  Then the
-// hi-nibble bytes of sub-blocks 2s, 2s + 1 and their four lo-quad bytes.
+// The part of one block a decoding thread needs, as loaded (no arithmetic on freshly
+// loaded values, so prefetches stay in flight until use): v4.4 -> lohi = dmin | dmax << 16,
+// cc = config | coeff << 8, q = this lane's 12-byte half of the 24 level bytes (the two
+// lanes of a column load its record contiguously and trade one word, see rec_levels);
+// split arrays -> lohi = dmin, hi16 = dmax, cc = config, cf = coeff, q = the hi-nibble
+// bytes of sub-blocks 2h, 2h + 1 and their four lo-quad bytes.
 struct LaneRec {
     uint32_t lohi, hi16, cc, cf;
-    uint2 h;
-    uint32_t p;
+    uint32_t q0, q1, q2;
 };
 
 // endpoints (dmin | dmax << 16) and config of a loaded record
@@ -70,28 +68,6 @@ __device__ __forceinline__ void rec_unpack(const LaneRec& r, uint32_t& lohi, uin
     }
 }
 
-// Core weights (rlo + step * lv, float32, then RNE to fp16) of one 8-weight sub-block in
-// natural k order: out[j] = (w[2j], w[2j+1]).  H holds the sub-block's 8 nibbles (weight
-// t at bits 4t), P its two quad bytes (weight t at bits 8(t >> 2) + 6 - 2(t & 3)).  The
-// levels of the even and the odd weights are assembled as bytes and widened with
-// v_cvt_f32_ubyte.
-__device__ __forceinline__ sx8_half8 decode_sub(uint32_t H, uint32_t P, float rlo, float step) {
-    const uint32_t x = __builtin_amdgcn_perm(0u, P, 0x01010000u);        // P0, P0, P1, P1
-    const uint32_t qe = ((x >> 6) & 0x00030003u) | ((x >> 2) & 0x03000300u);   // q0 q2 q4 q6
-    const uint32_t qo = ((x >> 4) & 0x00030003u) | (x & 0x03000300u);          // q1 q3 q5 q7
-    const uint32_t le = ((H & 0x0F0F0F0Fu) << 2) | qe;                         // lv0 lv2 lv4 lv6
-    const uint32_t lo = (((H >> 4) & 0x0F0F0F0Fu) << 2) | qo;                  // lv1 lv3 lv5 lv7
-    sx8_half8 out;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float we = __builtin_fmaf(step, (float)((le >> (8 * j)) & 0xFFu), rlo);
-        const float wo = __builtin_fmaf(step, (float)((lo >> (8 * j)) & 0xFFu), rlo);
-        out[2 * j] = (_Float16)we;
-        out[2 * j + 1] = (_Float16)wo;
-    }
-    return out;
-}
-
 // Range of sub-block sb: rlo = lo + q k1[s], step = max(0.015873 (rhi - rlo), 1e-10) in the
 // reference's float32 form (cuda/sx8_fused_wmma.cu:70-94); the floor binds only for
 // hi <= lo, where every sub-block's step is 1e-10.
@@ -104,73 +80,151 @@ __device__ __forceinline__ void sub_range(float lo, float d, float q, float m, u
     step = d > 0.f ? __builtin_ldexpf(m, -e) : 1e-10f;
 }
 
-// X tile of block kb into LDS: 128 rows x 4 sub-block chunks of 16 B, chunk of sub-block
-// sb at position (sb & 1) * 2 + (sb >> 1).  kFast (X 16-byte aligned rows, K a multiple
-// of 32): unconditional vector loads, rows >= M clamped to M - 1 (those output rows are
-// never stored).  Otherwise rows >= M and columns >= K read as zero, element by element.
-template <bool kFast>
-__device__ __forceinline__ void load_x_chunks(const uint16_t* __restrict__ X, int M, int64_t ldx,
-                                              int K, int m0, int kb, sx8_u32x4 v[2]) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = threadIdx.x + i * kThreads;
-        const int row = c >> 2, sb = c & 3;
-        const int m = m0 + row;
-        const int k = kb * 32 + 8 * sb;
-        if constexpr (kFast) {
-            v[i] = *reinterpret_cast<const sx8_u32x4*>(X + (int64_t)min(m, M - 1) * ldx + k);
+// LDS of one work-group: B operands in lane order, so every MFMA operand read is one
+// conflict-free ds_read_b128 at lane * 16.
+//   wt[b][j][st][l]: decoded weights of K block kb (b = kb % 3), n-fragment j (columns
+//                    32j .. 32j + 31 of the tile), MFMA k-step st, MFMA lane l
+//   pt[b][j][l]:     PCA k-step operand of group g (b = g & 1): for lane l = 32 hf + c,
+//                    (c0, c0, c1, c1) of blocks 4g + 2hf and 4g + 2hf + 1 of column c
+// Three weight buffers: while the MFMA waves multiply block kb (held in registers) and
+// read block kb + 1, the decode waves write block kb + 2.
+constexpr int kWtBufBytes = 4 * 2 * 64 * 16;
+struct GemmSmem {
+    sx8_u32x4 wt[3][4][2][64];
+    sx8_u32x4 pt[2][4][64];
+};
+
+// Buffer resources and per-lane byte offsets for the main loop's loads.  The K block goes
+// into the scalar offset, so the loop does no per-lane address arithmetic; a lane whose
+// vector offset lies past the end of a buffer (X rows >= M) reads zero.
+typedef __amdgpu_buffer_rsrc_t sx8_rsrc;
+constexpr int kRsrcFlags = 0x00020000;   // raw 32-bit buffer (gfx9 resource word 3)
+
+__device__ __forceinline__ sx8_rsrc make_rsrc(const void* p, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
+                                             (int)min(bytes, (int64_t)0x7FFFFFFF), kRsrcFlags);
+}
+
+template <int MF>
+struct LoopSrc {
+    sx8_rsrc x, hdr, lv, z, dmin, dmax, cfg, cf, hi, lo;
+    int a_off[MF];     // packed X of m-fragment f: row group * n_cb * 2048 + lane * 16
+    int z_off[MF];     // Zhl row of m-fragment f: (row * n_cb + 2 hf) * 8
+    int nn;            // weight column (clamped to N - 1)
+    int h;             // sub-block pair {2h, 2h + 1} this thread decodes
+};
+
+// Header part (endpoints, config, coefficients) and level part (hi nibbles, lo quads) of
+// this thread's record of K block kb; the main loop refills each part once its previous
+// contents are consumed.
+template <bool kSplit, int HB, int MF>
+__device__ __forceinline__ void load_rec_hdr(LaneRec& r, const LoopSrc<MF>& ls, int N, int kb) {
+    const int nn = ls.nn;
+    const int rowb = kb * N;                       // first block of K row kb
+    if constexpr (kSplit) {
+        r.lohi = __builtin_amdgcn_raw_buffer_load_b16(ls.dmin, nn * 2, rowb * 2, 0);
+        r.hi16 = __builtin_amdgcn_raw_buffer_load_b16(ls.dmax, nn * 2, rowb * 2, 0);
+        r.cc = __builtin_amdgcn_raw_buffer_load_b8(ls.cfg, nn, rowb, 0);
+        r.cf = __builtin_amdgcn_raw_buffer_load_b8(ls.cf, nn, rowb, 0);
+    } else {
+        if constexpr (HB == 8) {
+            const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ls.hdr, nn * 8, rowb * 8, 0));
+            r.lohi = v.x;
+            r.cc = v.y;
         } else {
-            uint32_t e[4] = {0, 0, 0, 0};
-            if (m < M) {
-                const uint16_t* src = X + (int64_t)m * ldx + k;
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (k + j < K) e[j >> 1] |= (uint32_t)src[j] << (16 * (j & 1));
-            }
-            v[i] = sx8_u32x4{e[0], e[1], e[2], e[3]};
+            r.lohi = __builtin_amdgcn_raw_buffer_load_b32(ls.hdr, nn * 6, rowb * 6, 0);
+            r.cc = __builtin_amdgcn_raw_buffer_load_b16(ls.hdr, nn * 6 + 4, rowb * 6, 0);
         }
+        r.hi16 = r.cf = 0;
     }
 }
 
-__device__ __forceinline__ void store_x_chunks(uint16_t* __restrict__ xs, const sx8_u32x4 v[2]) {
+template <bool kSplit, int HB, int MF>
+__device__ __forceinline__ void load_rec_lv(LaneRec& r, const LoopSrc<MF>& ls, int N, int kb) {
+    const int nn = ls.nn, s = ls.h;
+    const int rowb = kb * N;
+    if constexpr (kSplit) {
+        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ls.hi, nn * 16 + 8 * s, rowb * 16, 0));
+        r.q0 = v.x;
+        r.q1 = v.y;
+        r.q2 = __builtin_amdgcn_raw_buffer_load_b32(ls.lo, nn * 8 + 4 * s, rowb * 8, 0);
+    } else {
+        typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+        const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(ls.lv, nn * 24 + 12 * s, rowb * 24, 0);
+        r.q0 = v.x;
+        r.q1 = v.y;
+        r.q2 = v.z;
+    }
+}
+
+// Hi-nibble words of sub-blocks 2h (Hx) and 2h + 1 (Hy) and their lo-quad bytes (P, low
+// half for 2h).  v4.4: the level record of a column is qh[16] | ql[8]; lane h = 0 holds
+// bytes 0-11 (qh 0-11), lane h = 1 bytes 12-23 (qh 12-15, ql 0-7).  h = 0 needs ql 0-3
+// from its partner, h = 1 needs qh 8-11: one quad_perm swap between the lane pair.
+template <bool kSplit>
+__device__ __forceinline__ void rec_levels(const LaneRec& r, int h, uint32_t& Hx, uint32_t& Hy,
+                                           uint32_t& P) {
+    if constexpr (kSplit) {
+        Hx = r.q0;
+        Hy = r.q1;
+        P = r.q2;
+    } else {
+        const uint32_t send = h ? r.q1 : r.q2;
+        const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xB1, 0xF, 0xF, true);
+        Hx = h ? recv : r.q0;
+        Hy = h ? r.q0 : r.q1;
+        P = h ? r.q2 : recv;
+    }
+}
+
+template <bool kSplit, int HB, int MF>
+__device__ __forceinline__ void load_rec(LaneRec& r, const LoopSrc<MF>& ls, int N, int kb) {
+    load_rec_hdr<kSplit, HB, MF>(r, ls, N, kb);
+    load_rec_lv<kSplit, HB, MF>(r, ls, N, kb);
+}
+
+// A operands of K block kb from the packed X (see k_compute_z): for m-fragment f and k-step
+// st, lane l = 32 hf + r holds X[row r][32 kb + 16 hf + 8 st .. + 8], one contiguous 1 KB
+// wave load.  (The MFMA pairs A lane l's k with B lane l's k, so this K order -- each
+// lane's 16 consecutive values split over the two k-steps -- only has to match the order
+// in which the weights are placed, see decode_block.)  Row groups past the packed rows
+// read zero.
+template <int MF>
+__device__ __forceinline__ void load_a_step(sx8_u32x4 (&a)[MF][2], const LoopSrc<MF>& ls, int kb, int st) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = threadIdx.x + i * kThreads;
-        const int row = c >> 2, sb = c & 3;
-        const int pos = ((sb & 1) << 1) | (sb >> 1);
-        *reinterpret_cast<sx8_u32x4*>(xs + row * kXPitch + 8 * pos) = v[i];
-    }
+    for (int f = 0; f < MF; ++f)
+        a[f][st] = __builtin_bit_cast(sx8_u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     ls.x, ls.a_off[f] + 1024 * st, kb * 2048, 0));
 }
 
-// One quarter (32 rows) of the Z tile of group g (blocks 4g .. 4g+3): thread t handles
-// row 32 q + t / 8 and value e = t % 8 (block 4g + e / 2, basis e % 2).  Loaded from a
-// clamped index; store_z_quarter zeroes rows >= M and blocks >= n_cb.  Z is split into
-// fp16 hi + lo so the PCA k-step keeps ~22 bits.
-__device__ __forceinline__ float load_z_quarter(const float* __restrict__ Z, int M, int n_cb, int m0,
-                                                int g, int q) {
-    const int m = min(m0 + 32 * q + (int)(threadIdx.x >> 3), M - 1);
-    const int e = threadIdx.x & 7;
-    const int kb = min(4 * g + (e >> 1), n_cb - 1);
-    return Z[((int64_t)m * n_cb + kb) * 2 + (e & 1)];
+template <int MF>
+__device__ __forceinline__ void load_a(sx8_u32x4 (&a)[MF][2], const LoopSrc<MF>& ls, int kb) {
+    load_a_step<MF>(a, ls, kb, 0);
+    load_a_step<MF>(a, ls, kb, 1);
 }
 
-__device__ __forceinline__ void store_z_quarter(uint16_t* __restrict__ zs, int M, int n_cb, int m0,
-                                                int g, int q, float z) {
-    const int row = 32 * q + (threadIdx.x >> 3);
-    const int e = threadIdx.x & 7;
-    if (m0 + row >= M || 4 * g + (e >> 1) >= n_cb) z = 0.f;
-    const _Float16 h = (_Float16)z;
-    const _Float16 l = (_Float16)(z - (float)h);
-    const uint32_t v = (uint32_t)__builtin_bit_cast(uint16_t, h) |
-                       ((uint32_t)__builtin_bit_cast(uint16_t, l) << 16);
-    // value e -> k = 4 (e / 2) + 2 (e % 2): block-major, (Z0h, Z0l, Z1h, Z1l) per block
-    *reinterpret_cast<uint32_t*>(zs + row * kZPitch + 4 * (e >> 1) + 2 * (e & 1)) = v;
+// Zhl operand of group g (blocks 4g .. 4g + 3): lane l = 32 hf + r gets the 8 fp16 values
+// (Z0 hi, Z0 lo, Z1 hi, Z1 lo) of blocks 4g + 2hf and 4g + 2hf + 1 of its row; values of
+// blocks >= n_cb are zeroed here (their coefficient slots may hold stale values).
+template <int MF>
+__device__ __forceinline__ void load_za(sx8_u32x4 (&za)[MF], const LoopSrc<MF>& ls, int g) {
+#pragma unroll
+    for (int f = 0; f < MF; ++f)
+        za[f] = __builtin_bit_cast(sx8_u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  ls.z, ls.z_off[f] + g * 32, 0, 0));
 }
 
-// Work-group barrier for LDS hand-offs only: wait for this wave's LDS writes, then
+__device__ __forceinline__ sx8_half8 mask_za(sx8_u32x4 v, int n_cb, int g, int hf) {
+    const int kb0 = 4 * g + 2 * hf;
+    if (kb0 >= n_cb) v.x = v.y = 0u;
+    if (kb0 + 1 >= n_cb) v.z = v.w = 0u;
+    return __builtin_bit_cast(sx8_half8, v);
+}
+
+// Work-group barrier for LDS hand-offs only: wait for this wave's LDS accesses, then
 // s_barrier.  __syncthreads() would also wait for every global load in flight (its
-// release fence), which would undo the two-block load lead of the main loop.  The memory
-// clobber keeps the compiler from moving LDS accesses across it.
+// release fence), which would undo the load lead of the main loop.  The memory clobber
+// keeps the compiler from moving LDS accesses across it.
 __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
@@ -180,214 +234,291 @@ __device__ __forceinline__ uint32_t coeff_pair_f16(int c) {
     return h | (h << 16);
 }
 
-// Everything one K block needs from memory, loaded two iterations before its use: the X
-// chunks of block kb (stored to LDS at the end of iteration kb - 1), this lane's weight
-// record of block kb, and the Z-tile value stored at the end of iteration kb - 1.
-struct Stage {
-    sx8_u32x4 xv[2];
-    LaneRec rec;
-    float zq = 0.f;
-};
-
-// Buffer resources and per-lane byte offsets for the main loop's loads.  Everything that
-// depends on the K block goes into the scalar offset of a buffer load, so the loop does no
-// per-lane address arithmetic; loads past a buffer's end return zero.
-typedef __amdgpu_buffer_rsrc_t sx8_rsrc;
-constexpr int kRsrcFlags = 0x00020000;   // raw 32-bit buffer (gfx9 resource word 3)
-
-__device__ __forceinline__ sx8_rsrc make_rsrc(const void* p, int64_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
-                                             (int)min(bytes, (int64_t)0x7FFFFFFF), kRsrcFlags);
+// levels of the even (le) and odd (lo) weights of a sub-block, one byte each
+__device__ __forceinline__ void dec_unpack(uint32_t H, uint32_t P, uint32_t& le, uint32_t& lo) {
+    const uint32_t x = __builtin_amdgcn_perm(0u, P, 0x01010000u);        // P0, P0, P1, P1
+    const uint32_t qe = ((x >> 6) & 0x00030003u) | ((x >> 2) & 0x03000300u);   // q0 q2 q4 q6
+    const uint32_t qo = ((x >> 4) & 0x00030003u) | (x & 0x03000300u);          // q1 q3 q5 q7
+    le = ((H & 0x0F0F0F0Fu) << 2) | qe;
+    lo = (((H >> 4) & 0x0F0F0F0Fu) << 2) | qo;
 }
 
-struct LoopSrc {
-    sx8_rsrc x, hdr, lv, z, dmin, dmax, cfg, cf, hi, lo;
-    int x_off[2];      // X chunk i: row * ldx * 2 + 16 * sb
-    int rec_off;       // nn (column) in blocks
-    int z_off;         // Z value of quarter 0 of group 0
-};
+// weights 2j, 2j + 1 of a sub-block as a packed fp16 pair
+__device__ __forceinline__ uint32_t dec_pair(uint32_t le, uint32_t lo, int j, float rlo, float step) {
+    const float we = __builtin_fmaf(step, (float)((le >> (8 * j)) & 0xFFu), rlo);
+    const float wo = __builtin_fmaf(step, (float)((lo >> (8 * j)) & 0xFFu), rlo);
+    const sx8_half2 v = {(_Float16)we, (_Float16)wo};
+    return __builtin_bit_cast(uint32_t, v);
+}
 
-template <bool kSplit, int HB, bool kPca, bool kFast>
-__device__ __forceinline__ void load_stage(Stage& st, const LoopSrc& ls,
-                                           const uint16_t* __restrict__ X, int M, int64_t ldx,
-                                           int K, int N, int n_cb, int m0, int s, int kb) {
-    const int kc = min(kb, n_cb - 1);
-    if constexpr (kFast) {
+// Decode this thread's two sub-blocks of K block kb into weight buffer b, and its half of
+// the block's PCA coefficients into the group's coefficient tile.
+template <bool kSplit, bool kPca>
+__device__ __forceinline__ void decode_block(GemmSmem& sm, const LaneRec& rec, int kb, int b, int wj,
+                                             int wl, int h) {
+    uint32_t lohi, cfg;
+    rec_unpack<kSplit>(rec, lohi, cfg);
+    const float lo = sx8_h2f(lohi), hi = sx8_h2f(lohi >> 16);
+    const float d = hi - lo;
+    const float q = d * 0.25f;
+    const float mstep = d * 0.015873f;
+    uint32_t Hx, Hy, P;
+    rec_levels<kSplit>(rec, h, Hx, Hy, P);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            st.xv[i] = __builtin_bit_cast(sx8_u32x4,
-                                          __builtin_amdgcn_raw_buffer_load_b128(ls.x, ls.x_off[i], kc * 64, 0));
-    } else {
-        load_x_chunks<false>(X, M, ldx, K, m0, kc, st.xv);
-    }
-    const int nn = ls.rec_off;
-    const int rowb = kc * N;                       // first block of K row kc
-    if constexpr (kSplit) {
-        st.rec.lohi = __builtin_amdgcn_raw_buffer_load_b16(ls.dmin, nn * 2, rowb * 2, 0);
-        st.rec.hi16 = __builtin_amdgcn_raw_buffer_load_b16(ls.dmax, nn * 2, rowb * 2, 0);
-        st.rec.cc = __builtin_amdgcn_raw_buffer_load_b8(ls.cfg, nn, rowb, 0);
-        st.rec.cf = __builtin_amdgcn_raw_buffer_load_b8(ls.cf, nn, rowb, 0);
-        st.rec.h = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ls.hi, nn * 16 + 8 * s, rowb * 16, 0));
-        st.rec.p = __builtin_amdgcn_raw_buffer_load_b32(ls.lo, nn * 8 + 4 * s, rowb * 8, 0);
-    } else {
-        if constexpr (HB == 8) {
-            const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ls.hdr, nn * 8, rowb * 8, 0));
-            st.rec.lohi = v.x;
-            st.rec.cc = v.y;
-        } else {
-            st.rec.lohi = __builtin_amdgcn_raw_buffer_load_b32(ls.hdr, nn * 6, rowb * 6, 0);
-            st.rec.cc = __builtin_amdgcn_raw_buffer_load_b16(ls.hdr, nn * 6 + 4, rowb * 6, 0);
-        }
-        st.rec.hi16 = st.rec.cf = 0;
-        st.rec.h = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ls.lv, nn * 24 + 8 * s, rowb * 24, 0));
-        st.rec.p = __builtin_amdgcn_raw_buffer_load_b32(ls.lv, nn * 24 + 16 + 4 * s, rowb * 24, 0);
+    for (int st = 0; st < 2; ++st) {
+        float rlo, step;
+        sub_range(lo, d, q, mstep, cfg, 2 * h + st, rlo, step);
+        uint32_t le, lv;
+        dec_unpack(st ? Hy : Hx, st ? (P >> 16) : P, le, lv);
+        sm.wt[b][wj][st][wl] = sx8_u32x4{dec_pair(le, lv, 0, rlo, step), dec_pair(le, lv, 1, rlo, step),
+                                         dec_pair(le, lv, 2, rlo, step), dec_pair(le, lv, 3, rlo, step)};
     }
     if constexpr (kPca) {
-        const int i = max(kb - 1, 0);   // iteration whose end stores this value
-        const int g = (i >> 2) + 1, q = i & 3;
-        // value e of row 32 q + t / 8: Z[(m n_cb + 4 g + e / 2) * 2 + e % 2]; the whole offset
-        // is in the vector part, so the buffer range check zeroes reads past the end
-        st.zq = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                              ls.z, ls.z_off + (q * 32 * n_cb * 2 + g * 8) * 4, 0, 0));
+        // both threads of a column read its coefficient byte: h = 0 stores the (c0, c0)
+        // pair of the slot, h = 1 the (c1, c1) pair
+        const uint32_t cf = kSplit ? rec.cf : (rec.cc >> 8);
+        const int t4 = kb & 3;
+        uint32_t* dst = reinterpret_cast<uint32_t*>(&sm.pt[(kb >> 2) & 1][wj][(t4 >> 1) * 32 + (wl & 31)]);
+        dst[2 * (t4 & 1) + h] = coeff_pair_f16(sx8_sext4(cf >> (4 * h)));
     }
 }
 
-template <bool kSplit, int HB, bool kPca, bool kFast>
-__global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ X, int M,
-                                                   int64_t ldx, int K, WeightSrc w,
-                                                   const float* __restrict__ Z, int N, int n_cb,
-                                                   float* __restrict__ Y) {
-    __shared__ __align__(16) uint16_t xs[2][kBM * kXPitch];
-    __shared__ __align__(16) uint16_t zs[kPca ? 2 : 1][kPca ? kBM * kZPitch : 8];
+#define SX8_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+// XCD-aware work order: the dispatcher deals work-groups round-robin over the 8 XCDs, so
+// work-group b runs on XCD b % 8.  Give each XCD a contiguous run of the m-major tile order
+// (consecutive tiles share their X rows, which then stay in that XCD's L2).
+__device__ __forceinline__ int xcd_order(int b, int G) {
+    const int x = b & 7;
+    int start = 0;
+    for (int y = 0; y < x; ++y) start += (G - y + 7) >> 3;
+    return start + (b >> 3);
+}
+
+// Y (M, N) f32 = X . W^T (+ PCA term via Zhl).  Work-group: 8 waves, tile of 128 MF rows
+// x 128 columns.  Waves 0-3 (one per SIMD) own 32 MF rows each for all 128 columns (MF x 4
+// accumulators of 32 x 32) and issue only MFMAs, LDS reads and X loads; waves 4-7 decode
+// every weight of the tile once (thread t: column t % 128, sub-blocks 2 (t / 128),
+// 2 (t / 128) + 1) into the LDS ring two blocks ahead.  Each SIMD so runs one MFMA wave and
+// one decode wave, and the decode VALU work proceeds while the matrix pipe is busy.
+// One work-group barrier per K block.  S > 1 splits K into S ranges of whole 4-block
+// groups; range ks > 0 writes its partial tile to part + (ks - 1) M N and k_reduce adds the
+// partials to Y in a fixed order.
+template <bool kSplit, int HB, bool kPca, int MF, int kRD = 2>
+__global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ Xp, int M,
+                                                   WeightSrc w,
+                                                   const uint32_t* __restrict__ Zhl, int N,
+                                                   int n_cb, int S, int kb_per_split,
+                                                   float* __restrict__ Y, float* __restrict__ part) {
+    __shared__ GemmSmem sm;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int c32 = lane & 31;
-    const int s = lane >> 5;
-    const int m0 = blockIdx.y * kBM;
-    const int n = blockIdx.x * kBN + wave * 32 + c32;
-    const bool n_ok = n < N;
-    const int64_t nn = n_ok ? n : N - 1;
+    const int NB = (N + kBN - 1) / kBN;
+    const int MB = (M + 128 * MF - 1) / (128 * MF);
+    const int G = MB * NB * S;
+    const int o = xcd_order(blockIdx.x, G);
+    const int nb = o % NB;
+    const int ks = (o / NB) % S;
+    const int mb = o / (NB * S);
+    const int m0 = mb * 128 * MF;
+    const int n0 = nb * kBN;
+    const int kb0 = ks * kb_per_split;
+    const int kb1 = min(n_cb, kb0 + kb_per_split);
 
-    sx8_float16v acc[kBM / 32];
-#pragma unroll
-    for (int r = 0; r < kBM / 32; ++r)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[r][i] = 0.f;
-
-    LoopSrc ls;
-    ls.x = make_rsrc(X, (int64_t)M * ldx * 2);
-    const int64_t n_blk = (int64_t)N * n_cb;
-    if constexpr (kSplit) {
-        ls.dmin = make_rsrc(w.dmin, n_blk * 2);
-        ls.dmax = make_rsrc(w.dmax, n_blk * 2);
-        ls.cfg = make_rsrc(w.config, n_blk);
-        ls.cf = make_rsrc(w.coeff, n_blk);
-        ls.hi = make_rsrc(w.hi, n_blk * 16);
-        ls.lo = make_rsrc(w.lo, n_blk * 8);
-    } else {
-        ls.hdr = make_rsrc(w.hdr, n_blk * HB);
-        ls.lv = make_rsrc(w.levels, n_blk * 24);
-    }
-    if constexpr (kPca) ls.z = make_rsrc(Z, (int64_t)M * n_cb * 8);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = tid + i * kThreads;
-        ls.x_off[i] = (int)((int64_t)(m0 + (c >> 2)) * ldx * 2) + 16 * (c & 3);
-    }
-    ls.rec_off = (int)nn;
-    {
-        const int e = tid & 7;
-        ls.z_off = (int)(((int64_t)(m0 + (tid >> 3)) * n_cb * 2 + (e >> 1) * 2 + (e & 1)) * 4);
-    }
-
-    // prologue: stages of blocks 0 and 1 in flight, X tile 0 and the Z tile of group 0
-    Stage S0, S1;
-    load_stage<kSplit, HB, kPca, kFast>(S0, ls, X, M, ldx, K, N, n_cb, m0, s, 0);
-    load_stage<kSplit, HB, kPca, kFast>(S1, ls, X, M, ldx, K, N, n_cb, m0, s, 1);
     if constexpr (kPca) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            store_z_quarter(zs[0], M, n_cb, m0, 0, q, load_z_quarter(Z, M, n_cb, m0, 0, q));
+        // coefficient slots of blocks past n_cb are never written: start them at zero
+        reinterpret_cast<sx8_u32x4*>(&sm.pt[0][0][0])[tid] = sx8_u32x4{0u, 0u, 0u, 0u};
+        lds_barrier();
     }
-    store_x_chunks(xs[0], S0.xv);
-    __syncthreads();
 
-    uint32_t cfa = 0, cfb = 0;
-    // One K block: decode from `cur` (then refill it with block kb + 2), MFMAs on X tile
-    // kb, PCA k-step at the end of a group, publish `nxt`'s X tile and Z value.
-    auto body = [&](int kb, Stage& cur, const Stage& nxt) __attribute__((always_inline)) {
-        uint32_t lohi, cfg;
-        rec_unpack<kSplit>(cur.rec, lohi, cfg);
-        const float lo = sx8_h2f(lohi), hi = sx8_h2f(lohi >> 16);
-        const float d = hi - lo;
-        const float q = d * 0.25f;
-        const float mstep = d * 0.015873f;
-        const bool live = kb < n_cb;
-        sx8_half8 bop[2];
+    if (wave >= 4) {
+        // ---------------- decode waves ----------------
+        // lane pair (2c, 2c + 1) of the decode waves owns column c, halves h = 0, 1
+        const int t = tid - 256;
+        const int nl = t >> 1, h = t & 1;
+        const int wj = nl >> 5, wl = h * 32 + (nl & 31);
+        LoopSrc<MF> ls;
+        const int64_t n_blk = (int64_t)N * n_cb;
+        if constexpr (kSplit) {
+            ls.dmin = make_rsrc(w.dmin, n_blk * 2);
+            ls.dmax = make_rsrc(w.dmax, n_blk * 2);
+            ls.cfg = make_rsrc(w.config, n_blk);
+            ls.cf = make_rsrc(w.coeff, n_blk);
+            ls.hi = make_rsrc(w.hi, n_blk * 16);
+            ls.lo = make_rsrc(w.lo, n_blk * 8);
+        } else {
+            ls.hdr = make_rsrc(w.hdr, n_blk * HB);
+            ls.lv = make_rsrc(w.levels, n_blk * 24);
+        }
+        ls.nn = min(n0 + nl, N - 1);
+        ls.h = h;
+        // prologue: blocks kb0, kb0 + 1 decoded; records of kb0 + 2 .. kb0 + 1 + kRD in flight
+        // (records of block k in R[(k - kb0 - 2) % kRD]).  Weight records miss in L2 (each
+        // work-group of an XCD streams its own columns), so they are requested kRD blocks
+        // ahead of their decode.
+        LaneRec R[kRD];
+        {
+            LaneRec r0, r1;
+            load_rec<kSplit, HB, MF>(r0, ls, N, kb0);
+            load_rec<kSplit, HB, MF>(r1, ls, N, min(kb0 + 1, kb1 - 1));
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            float rlo, step;
-            sub_range(lo, d, q, mstep, cfg, 2 * s + h, rlo, step);
-            if (!live) rlo = step = 0.f;           // padding iteration: contributes zeros
-            bop[h] = decode_sub(h ? cur.rec.h.y : cur.rec.h.x, h ? (cur.rec.p >> 16) : cur.rec.p,
-                                rlo, step);
+            for (int i = 0; i < kRD; ++i) load_rec<kSplit, HB, MF>(R[i], ls, N, min(kb0 + 2 + i, kb1 - 1));
+            decode_block<kSplit, kPca>(sm, r0, kb0, kb0 % 3, wj, wl, h);
+            decode_block<kSplit, kPca>(sm, r1, kb0 + 1, (kb0 + 1) % 3, wj, wl, h);
+            lds_barrier();
         }
-        sx8_half8 cop;
-        if constexpr (kPca) {
-            // this lane's PCA k-step needs the coefficients of blocks 4g + 2s and 4g + 2s + 1
-            // of its column: keep them as the group's blocks pass by (0 for absent blocks)
-            const int j = kb & 3;
-            const uint32_t cf = kSplit ? cur.rec.cf : (cur.rec.cc >> 8);
-            if (live) {
-                cfa = j == 2 * s ? cf : (j == 0 ? 0u : cfa);
-                cfb = j == 2 * s + 1 ? cf : (j == 0 ? 0u : cfb);
-            }
-            const sx8_u32x4 cv = {coeff_pair_f16(sx8_sext4(cfa)), coeff_pair_f16(sx8_sext4(cfa >> 4)),
-                                  coeff_pair_f16(sx8_sext4(cfb)), coeff_pair_f16(sx8_sext4(cfb >> 4))};
-            cop = __builtin_bit_cast(sx8_half8, cv);
+        // iteration kb: decode block kb + 2 (a block past the range decodes a clamped
+        // record into a buffer nobody reads; its coefficient slot meets a zeroed Z value)
+        auto step = [&](int kb, LaneRec& r) __attribute__((always_inline)) {
+            decode_block<kSplit, kPca>(sm, r, kb + 2, (kb + 2) % 3, wj, wl, h);
+            load_rec<kSplit, HB, MF>(r, ls, N, min(kb + 2 + kRD, kb1 - 1));
+            lds_barrier();
+        };
+        int kb = kb0;
+        for (; kb + kRD <= kb1; kb += kRD) {
+#pragma unroll
+            for (int u = 0; u < kRD; ++u) step(kb + u, R[u]);
         }
-        load_stage<kSplit, HB, kPca, kFast>(cur, ls, X, M, ldx, K, N, n_cb, m0, s, kb + 2);
+#pragma unroll
+        for (int u = 0; u < kRD - 1; ++u)
+            if (kb + u < kb1) step(kb + u, R[u]);
+        return;
+    }
 
-        const uint16_t* xt = xs[kb & 1];
+    // ---------------- MFMA waves ----------------
+    const int hf = lane >> 5, r = lane & 31;
+    LoopSrc<MF> ls;
+    ls.x = make_rsrc(Xp, (int64_t)((M + 31) / 32) * n_cb * 2048);
+    if constexpr (kPca) ls.z = make_rsrc(Zhl, (int64_t)M * n_cb * 8);
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+    for (int f = 0; f < MF; ++f) {
+        const int g32 = (m0 >> 5) + wave * MF + f;
+        ls.a_off[f] = (int)((int64_t)g32 * n_cb * 2048) + lane * 16;
+        const int row = m0 + wave * 32 * MF + 32 * f + r;
+        ls.z_off[f] = (int)(((int64_t)row * n_cb + 2 * hf) * 8);
+    }
+
+    sx8_float16v acc[MF][4];
 #pragma unroll
-            for (int r = 0; r < kBM / 32; ++r) {
-                const sx8_half8 a = *reinterpret_cast<const sx8_half8*>(
-                    xt + (32 * r + c32) * kXPitch + 8 * (2 * h + s));
-                acc[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bop[h], acc[r], 0, 0, 0);
-            }
+    for (int f = 0; f < MF; ++f)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[f][j][i] = 0.f;
+
+    // prologue: A of kb0, kb0 + 1 and the group's Z operand in flight; B of kb0 read once
+    // the decode waves' prologue barrier has passed
+    sx8_u32x4 A[2][MF][2];
+    sx8_u32x4 za[MF];
+    load_a<MF>(A[0], ls, kb0);
+    load_a<MF>(A[1], ls, min(kb0 + 1, kb1 - 1));
+    if constexpr (kPca) load_za<MF>(za, ls, kb0 >> 2);
+    lds_barrier();
+    const uint8_t* wbase = reinterpret_cast<const uint8_t*>(&sm.wt[0][0][0][lane]);
+    sx8_u32x4 bw[2][4][2];
+    {
+        const uint8_t* src = wbase + (kb0 % 3) * kWtBufBytes;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+                bw[0][j][st] = *reinterpret_cast<const sx8_u32x4*>(src + (j * 2 + st) * 1024);
+    }
+
+    // iteration kb: request B of kb + 1, 16 MFMAs of block kb (A of kb + 2 requested as its
+    // registers free up), PCA k-step at the end of a group, barrier
+    auto body = [&](int kb, sx8_u32x4 (&acur)[MF][2], sx8_u32x4 (&bcur)[4][2], sx8_u32x4 (&bnext)[4][2])
+        __attribute__((always_inline)) {
+        {
+            const uint8_t* src = wbase + ((kb + 1) % 3) * kWtBufBytes;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int st = 0; st < 2; ++st)
+                    bnext[j][st] = *reinterpret_cast<const sx8_u32x4*>(src + (j * 2 + st) * 1024);
+        }
+        const int ka = min(kb + 2, kb1 - 1);
+        SX8_SCHED_FENCE();
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int f = 0; f < MF; ++f)
+                    acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        __builtin_bit_cast(sx8_half8, acur[f][st]),
+                        __builtin_bit_cast(sx8_half8, bcur[j][st]), acc[f][j], 0, 0, 0);
+            SX8_SCHED_FENCE();
+            load_a_step<MF>(acur, ls, ka, st);
+            SX8_SCHED_FENCE();
+        }
         if constexpr (kPca) {
-            if (live && ((kb & 3) == 3 || kb == n_cb - 1)) {
-                const uint16_t* zt = zs[(kb >> 2) & 1];
+            if ((kb & 3) == 3 || kb == kb1 - 1) {
+                const int g = kb >> 2;
+                sx8_half8 zh[MF];
 #pragma unroll
-                for (int r = 0; r < kBM / 32; ++r) {
-                    const sx8_half8 a = *reinterpret_cast<const sx8_half8*>(
-                        zt + (32 * r + c32) * kZPitch + 8 * s);
-                    acc[r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, cop, acc[r], 0, 0, 0);
+                for (int f = 0; f < MF; ++f) zh[f] = mask_za(za[f], n_cb, g, hf);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const sx8_half8 c = __builtin_bit_cast(sx8_half8, sm.pt[g & 1][j][lane]);
+#pragma unroll
+                    for (int f = 0; f < MF; ++f)
+                        acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(zh[f], c, acc[f][j], 0, 0, 0);
                 }
+                load_za<MF>(za, ls, min(g + 1, (kb1 - 1) >> 2));
             }
         }
-        store_x_chunks(xs[(kb + 1) & 1], nxt.xv);
-        if constexpr (kPca)
-            store_z_quarter(zs[((kb >> 2) + 1) & 1], M, n_cb, m0, (kb >> 2) + 1, kb & 3, nxt.zq);
         lds_barrier();
     };
-    for (int kb = 0; kb < n_cb; kb += 2) {
-        body(kb, S0, S1);
-        body(kb + 1, S1, S0);
+    int kb = kb0;
+    for (; kb + 2 <= kb1; kb += 2) {
+        body(kb, A[0], bw[0], bw[1]);
+        body(kb + 1, A[1], bw[1], bw[0]);
     }
+    if (kb < kb1) body(kb, A[0], bw[0], bw[1]);
 
-    // ---- epilogue: lane holds column n, rows 32r + (i % 4) + 4 s + 8 (i / 4)
-    if (!n_ok) return;
+    // epilogue: accumulator (f, j) element i of lane l = 32 hf + c is row
+    // 32 MF wave + 32 f + (i % 4) + 4 hf + 8 (i / 4), column 32 j + c
+    float* dst = ks == 0 ? Y : part + (int64_t)(ks - 1) * M * N;
 #pragma unroll
-    for (int r = 0; r < kBM / 32; ++r)
+    for (int j = 0; j < 4; ++j) {
+        const int n = n0 + 32 * j + r;
+        if (n >= N) continue;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int m = m0 + 32 * r + (i & 3) + 4 * s + 8 * (i >> 2);
-            if (m < M) Y[(int64_t)m * N + n] = acc[r][i];
-        }
+        for (int f = 0; f < MF; ++f)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int m = m0 + wave * 32 * MF + 32 * f + (i & 3) + 4 * hf + 8 * (i >> 2);
+                if (m < M) dst[(int64_t)m * N + n] = acc[f][j][i];
+            }
+    }
+}
+
+// Y += partial slices 0 .. S - 2, in slice order (deterministic).  kVec (Y 16-byte aligned,
+// M N a multiple of 4): 4 floats per thread; otherwise one.
+template <bool kVec>
+__global__ __launch_bounds__(256) void k_reduce(float* __restrict__ Y, const float* __restrict__ part,
+                                                int64_t MN, int nparts) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if constexpr (kVec) {
+        const int64_t i = t * 4;
+        if (i >= MN) return;
+        sx8_float4 y = *reinterpret_cast<const sx8_float4*>(Y + i);
+        for (int p = 0; p < nparts; ++p) y += *reinterpret_cast<const sx8_float4*>(part + p * MN + i);
+        *reinterpret_cast<sx8_float4*>(Y + i) = y;
+    } else {
+        if (t >= MN) return;
+        float y = Y[t];
+        for (int p = 0; p < nparts; ++p) y += part[p * MN + t];
+        Y[t] = y;
+    }
+}
+
+// fp32 Z (M, n_cb, 2) -> Zhl (M, n_cb, 4 x fp16): each value as the pair sx8_split_hl(z).
+__global__ __launch_bounds__(256) void k_z_hl(const float* __restrict__ Z, int64_t n, uint32_t* __restrict__ Zhl) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) Zhl[i] = sx8_split_hl(Z[i]);
 }
 
 // Output-side PCA: Y[m, n] += sum_kb c0(kb,n) Z[m,kb,0] + c1(kb,n) Z[m,kb,1].
@@ -425,52 +556,108 @@ int32_t check_shape(const char* what, int64_t M, int64_t ldx, int64_t K, int64_t
         ldx < K || M > 0x7FFFFFFF || N > 0x7FFFFFFF || n_cb > 0x7FFFFFFF / 64)
         return fail(SX8_ERR_INVALID, "%s: bad shape M=%lld K=%lld ldx=%lld N=%lld n_cb=%lld", what,
                     (long long)M, (long long)K, (long long)ldx, (long long)N, (long long)n_cb);
-    if ((M + kBM - 1) / kBM > 65535) return fail(SX8_ERR_UNSUPPORTED, "%s: M too large", what);
     // the main loop addresses every operand with 32-bit buffer offsets
-    if (M * ldx * 2 > 0x7FFFFFFF || N * n_cb * 24 > 0x7FFFFFFF || M * n_cb * 8 > 0x7FFFFFFF)
+    if (M * ldx * 2 > 0x7FFFFFFF || N * n_cb * 24 > 0x7FFFFFFF || M * n_cb * 8 > 0x7FFFFFFF ||
+        (M + 31) / 32 * n_cb * 2048 > 0x7FFFFFFF)
         return fail(SX8_ERR_UNSUPPORTED, "%s: operands beyond 2 GiB", what);
     return SX8_OK;
 }
 
+// Work split of one call: m-fragments per wave MF (tile rows 128 MF), and S K ranges of
+// kb_per_split blocks (a multiple of 4).  Grids with fewer tiles than the 256 CUs split K
+// (at most 8 ways) and pay (S - 1) M N f32 partials written and read back once.
+struct Plan {
+    int MF, S, kb_per_split;
+    int64_t G;
+};
+
+Plan plan_gemm(int64_t M, int64_t N, int64_t n_cb) {
+    Plan p;
+    p.MF = M > 128 ? 2 : 1;
+    const int64_t T = ((M + 128 * p.MF - 1) / (128 * p.MF)) * ((N + kBN - 1) / kBN);
+    const int64_t groups = (n_cb + 3) / 4;
+    int64_t S = T >= 256 ? 1 : (256 + T - 1) / T;
+    S = std::min<int64_t>(std::min<int64_t>(S, 8), groups);
+    p.kb_per_split = (int)(4 * ((groups + S - 1) / S));
+    p.S = (int)((n_cb + p.kb_per_split - 1) / p.kb_per_split);
+    p.G = T * p.S;
+    return p;
+}
+
+// How the PCA operand reaches the kernel: none (core weights only), computed here from
+// basis/scales, or converted from a caller's f32 Z.
+enum class ZMode { kNone, kBasis, kGiven };
+
+template <bool kSplit, bool kPca, int HB, int MF>
+void launch_mf(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, const WeightSrc& w,
+               const uint32_t* Zhl, int64_t N, int64_t n_cb, float* Y, float* part) {
+    hipLaunchKernelGGL((k_gemm<kSplit, HB, kPca, MF>), dim3((unsigned)p.G), dim3(kThreads), 0, st, Xp,
+                       (int)M, w, Zhl, (int)N, (int)n_cb, p.S, p.kb_per_split, Y, part);
+}
+
 template <bool kSplit, bool kPca, int HB>
-void launch_gemm_hb(dim3 grid, hipStream_t st, bool fast, const uint16_t* X, int64_t M,
-                    int64_t ldx, int64_t K, const WeightSrc& w, const float* Z, int64_t N,
-                    int64_t n_cb, float* Y) {
-    if (fast)
-        hipLaunchKernelGGL((k_gemm<kSplit, HB, kPca, true>), grid, dim3(kThreads), 0, st, X,
-                           (int)M, ldx, (int)K, w, Z, (int)N, (int)n_cb, Y);
+void launch_hb(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, const WeightSrc& w,
+               const uint32_t* Zhl, int64_t N, int64_t n_cb, float* Y, float* part) {
+    if (p.MF == 2)
+        launch_mf<kSplit, kPca, HB, 2>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
     else
-        hipLaunchKernelGGL((k_gemm<kSplit, HB, kPca, false>), grid, dim3(kThreads), 0, st, X,
-                           (int)M, ldx, (int)K, w, Z, (int)N, (int)n_cb, Y);
+        launch_mf<kSplit, kPca, HB, 1>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
 }
 
-template <bool kSplit, bool kPca>
-int32_t launch_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
-                    const WeightSrc& w, int32_t hdr_bytes, const float* Z, int64_t N, int64_t n_cb,
-                    float* Y, hipStream_t st) {
+// Plan; in the library's per-device workspace, stage the packed X and (PCA contracts) the
+// Zhl operand with one pass over X, followed by the split-K partials; run the GEMM and,
+// for S > 1, the fixed-order partial sum.
+template <bool kSplit>
+int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
+                 const WeightSrc& w, int32_t hdr_bytes, ZMode zm, const float* basis,
+                 const float* scales, const float* Z, int64_t N, int64_t n_cb, float* Y,
+                 hipStream_t st) {
     using namespace sx8;
-    const bool fast = aligned(X, 16) && (ldx % 8 == 0) && (K % 32 == 0);
-    const dim3 grid((unsigned)((N + kBN - 1) / kBN), (unsigned)((M + kBM - 1) / kBM));
-    if (hdr_bytes == 8)
-        launch_gemm_hb<kSplit, kPca, 8>(grid, st, fast, X, M, ldx, K, w, Z, N, n_cb, Y);
-    else
-        launch_gemm_hb<kSplit, kPca, 6>(grid, st, fast, X, M, ldx, K, w, Z, N, n_cb, Y);
-    return check_launch(what);
-}
-
-// Z (M, n_cb, 2) f32 for the contracts that pass basis/scales, in the library's
-// per-device workspace (columns k >= K of a ragged last block count as zero).
-int32_t z_from_basis(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, const float* basis,
-                     const float* scales, int64_t n_cb, hipStream_t st, const float** Zp) {
-    using namespace sx8;
-    void* ws = nullptr;
-    const int32_t rc = device_workspace(M * n_cb * 2 * (int64_t)sizeof(float), &ws);
+    const Plan p = plan_gemm(M, N, n_cb);
+    if (p.G > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "%s: grid too large", what);
+    const int64_t z_bytes = zm == ZMode::kNone ? 0 : ((M * n_cb * 8 + 255) & ~int64_t(255));
+    const int64_t xp_bytes = (M + 31) / 32 * n_cb * 2048;
+    const int64_t part_bytes = (int64_t)(p.S - 1) * M * N * 4;
+    void* v = nullptr;
+    int32_t rc = device_workspace(z_bytes + xp_bytes + part_bytes, &v);
     if (rc != SX8_OK) return rc;
-    float* Zw = reinterpret_cast<float*>(ws);
-    const int32_t zr = compute_z(X, M, ldx, K, basis, scales, n_cb, Zw, st);
-    if (zr != SX8_OK) return zr;
-    *Zp = Zw;
-    return SX8_OK;
+    uint8_t* ws = reinterpret_cast<uint8_t*>(v);
+    uint32_t* Zhl = reinterpret_cast<uint32_t*>(ws);
+    uint16_t* Xp = reinterpret_cast<uint16_t*>(ws + z_bytes);
+    float* part = reinterpret_cast<float*>(ws + z_bytes + xp_bytes);
+    if (zm == ZMode::kBasis) {
+        rc = compute_z(X, M, ldx, K, basis, scales, n_cb, Zhl, true, Xp, st);
+    } else {
+        if (zm == ZMode::kGiven) {
+            const int64_t n = M * n_cb * 2;
+            hipLaunchKernelGGL(k_z_hl, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, Z, n, Zhl);
+        }
+        rc = compute_z(X, M, ldx, K, nullptr, nullptr, n_cb, nullptr, false, Xp, st);
+    }
+    if (rc != SX8_OK) return rc;
+    if constexpr (kSplit) {
+        launch_hb<true, true, 6>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
+    } else if (zm == ZMode::kNone) {
+        if (hdr_bytes == 8)
+            launch_hb<false, false, 8>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
+        else
+            launch_hb<false, false, 6>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
+    } else {
+        if (hdr_bytes == 8)
+            launch_hb<false, true, 8>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
+        else
+            launch_hb<false, true, 6>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
+    }
+    if (p.S > 1) {
+        const int64_t MN = M * N;
+        if (aligned(Y, 16) && MN % 4 == 0)
+            hipLaunchKernelGGL(k_reduce<true>, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0,
+                               st, Y, part, MN, p.S - 1);
+        else
+            hipLaunchKernelGGL(k_reduce<false>, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, st,
+                               Y, part, MN, p.S - 1);
+    }
+    return check_launch(what);
 }
 
 }  // namespace
@@ -487,17 +674,13 @@ extern "C" int32_t sx8_gemm_prefill(const uint16_t* X, int64_t M, int64_t ldx, i
     if (!aligned(hdr, hdr_bytes == 8 ? 8 : 2) || !aligned(levels, 8) || !aligned(X, 2) ||
         !aligned(Y, 4) || !aligned(basis, 16) || !aligned(scales, 8))
         return fail(SX8_ERR_INVALID, "sx8_gemm_prefill: misaligned pointer");
-    int32_t rc = check_shape("sx8_gemm_prefill", M, ldx, K, N, n_cb);
-    if (rc != SX8_OK) return rc;
-    const hipStream_t st = as_stream(stream);
-    const float* Z = nullptr;
-    rc = z_from_basis(X, M, ldx, K, basis, scales, n_cb, st, &Z);
+    const int32_t rc = check_shape("sx8_gemm_prefill", M, ldx, K, N, n_cb);
     if (rc != SX8_OK) return rc;
     WeightSrc w{};
     w.hdr = hdr;
     w.levels = levels;
-    return launch_gemm<false, true>("sx8_gemm_prefill", X, M, ldx, K, w, hdr_bytes, Z, N, n_cb, Y,
-                                    st);
+    return run_gemm<false>("sx8_gemm_prefill", X, M, ldx, K, w, hdr_bytes, ZMode::kBasis, basis,
+                           scales, nullptr, N, n_cb, Y, as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemm_prefill_split(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
@@ -512,11 +695,7 @@ extern "C" int32_t sx8_gemm_prefill_split(const uint16_t* X, int64_t M, int64_t 
     if (!aligned(dmin, 2) || !aligned(dmax, 2) || !aligned(hi, 8) || !aligned(lo, 4) ||
         !aligned(X, 2) || !aligned(Y, 4) || !aligned(basis, 16) || !aligned(scales, 8))
         return fail(SX8_ERR_INVALID, "sx8_gemm_prefill_split: misaligned pointer");
-    int32_t rc = check_shape("sx8_gemm_prefill_split", M, ldx, K, N, n_cb);
-    if (rc != SX8_OK) return rc;
-    const hipStream_t st = as_stream(stream);
-    const float* Z = nullptr;
-    rc = z_from_basis(X, M, ldx, K, basis, scales, n_cb, st, &Z);
+    const int32_t rc = check_shape("sx8_gemm_prefill_split", M, ldx, K, N, n_cb);
     if (rc != SX8_OK) return rc;
     WeightSrc w{};
     w.dmin = dmin;
@@ -525,7 +704,8 @@ extern "C" int32_t sx8_gemm_prefill_split(const uint16_t* X, int64_t M, int64_t 
     w.coeff = coeff;
     w.hi = hi;
     w.lo = lo;
-    return launch_gemm<true, true>("sx8_gemm_prefill_split", X, M, ldx, K, w, 6, Z, N, n_cb, Y, st);
+    return run_gemm<true>("sx8_gemm_prefill_split", X, M, ldx, K, w, 6, ZMode::kBasis, basis,
+                          scales, nullptr, N, n_cb, Y, as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemm_prefill_z(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
@@ -545,8 +725,8 @@ extern "C" int32_t sx8_gemm_prefill_z(const uint16_t* X, int64_t M, int64_t ldx,
     WeightSrc w{};
     w.hdr = hdr;
     w.levels = levels;
-    return launch_gemm<false, true>("sx8_gemm_prefill_z", X, M, ldx, K, w, hdr_bytes, Z, N, n_cb,
-                                    Y, as_stream(stream));
+    return run_gemm<false>("sx8_gemm_prefill_z", X, M, ldx, K, w, hdr_bytes, ZMode::kGiven, nullptr,
+                           nullptr, Z, N, n_cb, Y, as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemm_prefill_core(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
@@ -565,8 +745,8 @@ extern "C" int32_t sx8_gemm_prefill_core(const uint16_t* X, int64_t M, int64_t l
     WeightSrc w{};
     w.hdr = hdr;
     w.levels = levels;
-    return launch_gemm<false, false>("sx8_gemm_prefill_core", X, M, ldx, K, w, hdr_bytes, nullptr,
-                                     N, n_cb, Y, as_stream(stream));
+    return run_gemm<false>("sx8_gemm_prefill_core", X, M, ldx, K, w, hdr_bytes, ZMode::kNone,
+                           nullptr, nullptr, nullptr, N, n_cb, Y, as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemm_pca_z(const float* Z, int64_t M, const uint8_t* hdr, int32_t hdr_bytes,

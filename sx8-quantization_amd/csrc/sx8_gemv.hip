@@ -69,18 +69,27 @@ constexpr int kLdsMaxKb = 640;     // activation table staged in LDS up to this 
 // scale * sum.
 // One thread per (row m, kb): both Z values, x read once as four 16-byte vectors (the
 // row's tail past K is zero), products and the reference tree in registers.
+// Optional outputs: Z as f32 pairs or as split fp16 hi/lo pairs (hl), and the prefill
+// GEMM's packed copy of X (Xp != nullptr): for each 32-row group G and block kb a 2 KB
+// chunk [k-step st][MFMA lane l = 32 hf + r][8 values] holding X[32 G + r][32 kb + 16 hf +
+// 8 st .. + 8], so the GEMM reads every A operand as one contiguous 1 KB wave load.  When
+// packing, the grid covers the rows up to the next multiple of 32 (rows >= M pack zeros).
+template <bool kZ, bool kPack>
 __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ X, int64_t M,
                                                    int64_t ldx, int64_t K,
                                                    const float* __restrict__ basis,
                                                    const float* __restrict__ scales, int64_t n_cb,
-                                                   bool x_vec, float* __restrict__ Z) {
+                                                   bool x_vec, bool hl, float* __restrict__ Z,
+                                                   uint16_t* __restrict__ Xp) {
 #pragma clang fp contract(off)
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (gid >= M * n_cb) return;
+    const int64_t rows = kPack ? (M + 31) / 32 * 32 : M;
+    if (gid >= rows * n_cb) return;
     const int64_t m = gid / n_cb;
     const int64_t kb = gid - m * n_cb;
-    const uint16_t* x = X + m * ldx + kb * 32;
-    const int kmax = (int)min((int64_t)32, K - kb * 32);
+    const bool row_ok = m < M;
+    const uint16_t* x = X + min(m, M - 1) * ldx + kb * 32;
+    const int kmax = row_ok ? (int)min((int64_t)32, K - kb * 32) : 0;
     uint32_t xw[16];
     if (x_vec && kmax == 32) {
 #pragma unroll
@@ -96,26 +105,44 @@ __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ 
             xw[t] = a | (b << 16);
         }
     }
-    const float4* bv = reinterpret_cast<const float4*>(basis + kb * 64);
-    float z[2];
+    if constexpr (kPack) {
+        const int64_t G = m >> 5;
+        const int r = (int)(m & 31);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        float p[32];
+        for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const float4 b = bv[8 * j + q];
-            p[4 * q] = sx8_h2f(xw[2 * q]) * b.x;
-            p[4 * q + 1] = sx8_h2f(xw[2 * q] >> 16) * b.y;
-            p[4 * q + 2] = sx8_h2f(xw[2 * q + 1]) * b.z;
-            p[4 * q + 3] = sx8_h2f(xw[2 * q + 1] >> 16) * b.w;
-        }
-#pragma unroll
-        for (int off = 16; off > 0; off >>= 1)
-#pragma unroll
-            for (int t = 0; t < off; ++t) p[t] = p[t] + p[t + off];
-        z[j] = scales[kb * 2 + j] * p[0];
+            for (int st = 0; st < 2; ++st) {
+                uint4* dst = reinterpret_cast<uint4*>(Xp + ((G * n_cb + kb) * 2 + st) * 512 + (hf * 32 + r) * 8);
+                const int q = 8 * hf + 4 * st;
+                *dst = make_uint4(xw[q], xw[q + 1], xw[q + 2], xw[q + 3]);
+            }
     }
-    *reinterpret_cast<float2*>(Z + gid * 2) = make_float2(z[0], z[1]);
+    if constexpr (kZ) {
+        if (!row_ok) return;
+        const float4* bv = reinterpret_cast<const float4*>(basis + kb * 64);
+        float z[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float p[32];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 b = bv[8 * j + q];
+                p[4 * q] = sx8_h2f(xw[2 * q]) * b.x;
+                p[4 * q + 1] = sx8_h2f(xw[2 * q] >> 16) * b.y;
+                p[4 * q + 2] = sx8_h2f(xw[2 * q + 1]) * b.z;
+                p[4 * q + 3] = sx8_h2f(xw[2 * q + 1] >> 16) * b.w;
+            }
+#pragma unroll
+            for (int off = 16; off > 0; off >>= 1)
+#pragma unroll
+                for (int t = 0; t < off; ++t) p[t] = p[t] + p[t + off];
+            z[j] = scales[kb * 2 + j] * p[0];
+        }
+        if (hl)
+            *reinterpret_cast<uint2*>(Z + gid * 2) = make_uint2(sx8_split_hl(z[0]), sx8_split_hl(z[1]));
+        else
+            *reinterpret_cast<float2*>(Z + gid * 2) = make_float2(z[0], z[1]);
+    }
 }
 
 // Activation-side table, one 32-lane group per kb (8 kb per 256-thread block).
@@ -484,13 +511,22 @@ extern "C" int64_t sx8_gemv_workspace_bytes(int64_t n_cb) {
 }
 
 int32_t sx8::compute_z(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, const float* basis,
-                       const float* scales, int64_t n_cb, float* Z, hipStream_t st) {
-    const int64_t threads = M * n_cb;
-    const int64_t grid = (threads + 255) / 256;
+                       const float* scales, int64_t n_cb, void* Z, bool hl, uint16_t* xpack,
+                       hipStream_t st) {
+    const int64_t rows = xpack ? (M + 31) / 32 * 32 : M;
+    const int64_t grid = (rows * n_cb + 255) / 256;
     if (grid > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "compute_z: too large");
     const bool x_vec = aligned(X, 16) && ldx % 8 == 0;
-    hipLaunchKernelGGL(k_compute_z, dim3((unsigned)grid), dim3(256), 0, st, X, M, ldx, K, basis,
-                       scales, n_cb, x_vec, Z);
+    float* Zf = reinterpret_cast<float*>(Z);
+    if (Z && xpack)
+        hipLaunchKernelGGL((k_compute_z<true, true>), dim3((unsigned)grid), dim3(256), 0, st, X, M, ldx,
+                           K, basis, scales, n_cb, x_vec, hl, Zf, xpack);
+    else if (Z)
+        hipLaunchKernelGGL((k_compute_z<true, false>), dim3((unsigned)grid), dim3(256), 0, st, X, M,
+                           ldx, K, basis, scales, n_cb, x_vec, hl, Zf, xpack);
+    else if (xpack)
+        hipLaunchKernelGGL((k_compute_z<false, true>), dim3((unsigned)grid), dim3(256), 0, st, X, M,
+                           ldx, K, basis, scales, n_cb, x_vec, hl, Zf, xpack);
     return check_launch("compute_z");
 }
 
@@ -503,7 +539,7 @@ extern "C" int32_t sx8_compute_z(const uint16_t* X, int64_t M, int64_t ldx, cons
                     (long long)M, (long long)ldx, (long long)n_cb);
     if (!aligned(X, 2) || !aligned(basis, 16) || !aligned(scales, 4) || !aligned(Z, 8))
         return fail(SX8_ERR_INVALID, "sx8_compute_z: misaligned pointer (basis 16 B, Z 8 B)");
-    return compute_z(X, M, ldx, n_cb * 32, basis, scales, n_cb, Z, as_stream(stream));
+    return compute_z(X, M, ldx, n_cb * 32, basis, scales, n_cb, Z, false, nullptr, as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels,

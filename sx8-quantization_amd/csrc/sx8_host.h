@@ -31,9 +31,14 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 int32_t device_workspace(int64_t bytes, void** ptr);
 
 // Z[m, kb, j] = scales[kb, j] * sum_t X[m, kb*32+t] * basis[kb, 32j+t] (reference tree
-// order), reading only columns k < K of X (the rest count as zero).  Launch only; the
-// caller validated the arguments.
+// order), reading only columns k < K of X (the rest count as zero).  hl = false: Z as f32
+// (M, n_cb, 2); hl = true: each value stored as the fp16 pair sx8_split_hl(z), i.e.
+// (Z0 hi, Z0 lo, Z1 hi, Z1 lo) per (m, kb), the prefill GEMM's PCA operand.  Same size.
+// Z may be null (no Z).  xpack != null also writes the prefill GEMM's packed X:
+// ceil(M / 32) * n_cb chunks of 2 KB (see k_compute_z).  Launch only; the caller
+// validated the arguments.
 int32_t compute_z(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, const float* basis,
-                  const float* scales, int64_t n_cb, float* Z, hipStream_t st);
+                  const float* scales, int64_t n_cb, void* Z, bool hl, uint16_t* xpack,
+                  hipStream_t st);
 
 }  // namespace sx8
