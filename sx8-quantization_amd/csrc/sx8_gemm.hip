@@ -158,9 +158,9 @@ __device__ __forceinline__ void load_rec_lv(LaneRec& r, const LoopSrc<MF>& ls, i
 }
 
 // Hi-nibble words of sub-blocks 2h (Hx) and 2h + 1 (Hy) and their lo-quad bytes (P, low
-// half for 2h).  v4.4: the level record of a column is qh[16] | ql[8]; lane h = 0 holds
-// bytes 0-11 (qh 0-11), lane h = 1 bytes 12-23 (qh 12-15, ql 0-7).  h = 0 needs ql 0-3
-// from its partner, h = 1 needs qh 8-11: one quad_perm swap between the lane pair.
+// half for 2h).  v4.4: the level record of a column is qh[16] | ql[8]; lane c (h = 0) holds
+// bytes 0-11 (qh 0-11), lane c + 32 (h = 1) bytes 12-23 (qh 12-15, ql 0-7).  h = 0 needs
+// ql 0-3 from its partner, h = 1 needs qh 8-11: one swap of the wave's lane halves.
 template <bool kSplit>
 __device__ __forceinline__ void rec_levels(const LaneRec& r, int h, uint32_t& Hx, uint32_t& Hy,
                                            uint32_t& P) {
@@ -170,7 +170,10 @@ __device__ __forceinline__ void rec_levels(const LaneRec& r, int h, uint32_t& Hx
         P = r.q2;
     } else {
         const uint32_t send = h ? r.q1 : r.q2;
-        const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xB1, 0xF, 0xF, true);
+        // v_permlane32_swap: result[0] = send with lanes 32-63 taken from lanes 0-31,
+        // result[1] = send with lanes 0-31 taken from lanes 32-63
+        const auto sw = __builtin_amdgcn_permlane32_swap(send, send, false, false);
+        const uint32_t recv = h ? sw[0] : sw[1];
         Hx = h ? recv : r.q0;
         Hy = h ? r.q0 : r.q1;
         P = h ? r.q2 : recv;
@@ -226,7 +229,11 @@ __device__ __forceinline__ sx8_half8 mask_za(sx8_u32x4 v, int n_cb, int g, int h
 // release fence), which would undo the load lead of the main loop.  The memory clobber
 // keeps the compiler from moving LDS accesses across it.
 __device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // the wait is a builtin so the compiler's wait-count tracking sees that this wave's LDS
+    // reads have landed (an opaque asm wait would make it wait again for the next
+    // iteration's reads before their first use)
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt, expcnt untouched
+    asm volatile("s_barrier" ::: "memory");
 }
 
 __device__ __forceinline__ uint32_t coeff_pair_f16(int c) {
@@ -251,11 +258,19 @@ __device__ __forceinline__ uint32_t dec_pair(uint32_t le, uint32_t lo, int j, fl
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// Decode this thread's two sub-blocks of K block kb into weight buffer b, and its half of
-// the block's PCA coefficients into the group's coefficient tile.
-template <bool kSplit, bool kPca>
-__device__ __forceinline__ void decode_block(GemmSmem& sm, const LaneRec& rec, int kb, int b, int wj,
-                                             int wl, int h) {
+// Decode of this thread's two sub-blocks of a block, in two halves so the decode waves can
+// overlap the second half of block kb with the first half of block kb + 1 (one decode wave
+// per SIMD has no other wave to hide its dependency chains behind).
+// dec_prep: sub-block ranges, level bytes and the PCA coefficient (h = 0: c0, h = 1: c1)
+// as an fp16 pair.
+struct DecPrep {
+    float rlo[2], step[2];
+    uint32_t le[2], lv[2];
+    uint32_t cpair;
+};
+
+template <bool kSplit>
+__device__ __forceinline__ DecPrep dec_prep(const LaneRec& rec, int h) {
     uint32_t lohi, cfg;
     rec_unpack<kSplit>(rec, lohi, cfg);
     const float lo = sx8_h2f(lohi), hi = sx8_h2f(lohi >> 16);
@@ -264,23 +279,39 @@ __device__ __forceinline__ void decode_block(GemmSmem& sm, const LaneRec& rec, i
     const float mstep = d * 0.015873f;
     uint32_t Hx, Hy, P;
     rec_levels<kSplit>(rec, h, Hx, Hy, P);
+    DecPrep p;
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-        float rlo, step;
-        sub_range(lo, d, q, mstep, cfg, 2 * h + st, rlo, step);
-        uint32_t le, lv;
-        dec_unpack(st ? Hy : Hx, st ? (P >> 16) : P, le, lv);
-        sm.wt[b][wj][st][wl] = sx8_u32x4{dec_pair(le, lv, 0, rlo, step), dec_pair(le, lv, 1, rlo, step),
-                                         dec_pair(le, lv, 2, rlo, step), dec_pair(le, lv, 3, rlo, step)};
+        sub_range(lo, d, q, mstep, cfg, 2 * h + st, p.rlo[st], p.step[st]);
+        dec_unpack(st ? Hy : Hx, st ? (P >> 16) : P, p.le[st], p.lv[st]);
     }
+    const uint32_t cf = kSplit ? rec.cf : (rec.cc >> 8);
+    p.cpair = coeff_pair_f16(sx8_sext4(cf >> (4 * h)));
+    return p;
+}
+
+// dec_finish: the 16 weights into weight buffer b, the coefficient pair into the group's
+// coefficient tile (h = 0 stores the slot's (c0, c0) pair, h = 1 its (c1, c1) pair).
+template <bool kPca>
+__device__ __forceinline__ void dec_finish(GemmSmem& sm, const DecPrep& p, int kb, int b, int wj, int wl,
+                                           int h) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+        sm.wt[b][wj][st][wl] = sx8_u32x4{dec_pair(p.le[st], p.lv[st], 0, p.rlo[st], p.step[st]),
+                                         dec_pair(p.le[st], p.lv[st], 1, p.rlo[st], p.step[st]),
+                                         dec_pair(p.le[st], p.lv[st], 2, p.rlo[st], p.step[st]),
+                                         dec_pair(p.le[st], p.lv[st], 3, p.rlo[st], p.step[st])};
     if constexpr (kPca) {
-        // both threads of a column read its coefficient byte: h = 0 stores the (c0, c0)
-        // pair of the slot, h = 1 the (c1, c1) pair
-        const uint32_t cf = kSplit ? rec.cf : (rec.cc >> 8);
         const int t4 = kb & 3;
         uint32_t* dst = reinterpret_cast<uint32_t*>(&sm.pt[(kb >> 2) & 1][wj][(t4 >> 1) * 32 + (wl & 31)]);
-        dst[2 * (t4 & 1) + h] = coeff_pair_f16(sx8_sext4(cf >> (4 * h)));
+        dst[2 * (t4 & 1) + h] = p.cpair;
     }
+}
+
+template <bool kSplit, bool kPca>
+__device__ __forceinline__ void decode_block(GemmSmem& sm, const LaneRec& rec, int kb, int b, int wj,
+                                             int wl, int h) {
+    dec_finish<kPca>(sm, dec_prep<kSplit>(rec, h), kb, b, wj, wl, h);
 }
 
 #define SX8_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
@@ -304,7 +335,7 @@ __device__ __forceinline__ int xcd_order(int b, int G) {
 // One work-group barrier per K block.  S > 1 splits K into S ranges of whole 4-block
 // groups; range ks > 0 writes its partial tile to part + (ks - 1) M N and k_reduce adds the
 // partials to Y in a fixed order.
-template <bool kSplit, int HB, bool kPca, int MF, int kRD = 2>
+template <bool kSplit, int HB, bool kPca, int MF>
 __global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ Xp, int M,
                                                    WeightSrc w,
                                                    const uint32_t* __restrict__ Zhl, int N,
@@ -334,10 +365,11 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ 
 
     if (wave >= 4) {
         // ---------------- decode waves ----------------
-        // lane pair (2c, 2c + 1) of the decode waves owns column c, halves h = 0, 1
-        const int t = tid - 256;
-        const int nl = t >> 1, h = t & 1;
-        const int wj = nl >> 5, wl = h * 32 + (nl & 31);
+        // decode wave d (0..3) owns columns 32d .. 32d + 31 (n-fragment d); lane l handles
+        // column 32d + l % 32, sub-block pair h = l / 32, and writes B-tile slot l
+        const int dw = wave - 4, l = lane;
+        const int nl = 32 * dw + (l & 31), h = l >> 5;
+        const int wj = dw, wl = l;
         LoopSrc<MF> ls;
         const int64_t n_blk = (int64_t)N * n_cb;
         if constexpr (kSplit) {
@@ -353,36 +385,39 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ 
         }
         ls.nn = min(n0 + nl, N - 1);
         ls.h = h;
-        // prologue: blocks kb0, kb0 + 1 decoded; records of kb0 + 2 .. kb0 + 1 + kRD in flight
-        // (records of block k in R[(k - kb0 - 2) % kRD]).  Weight records miss in L2 (each
-        // work-group of an XCD streams its own columns), so they are requested kRD blocks
-        // ahead of their decode.
-        LaneRec R[kRD];
+        // prologue: blocks kb0, kb0 + 1 decoded, block kb0 + 2 prepared, records of kb0 + 3,
+        // kb0 + 4 in flight.  Weight records miss in L2 (each work-group of an XCD streams its
+        // own columns), so they are requested two iterations before their first use.
+        LaneRec R[2];
+        DecPrep P[2];
         {
             LaneRec r0, r1;
             load_rec<kSplit, HB, MF>(r0, ls, N, kb0);
             load_rec<kSplit, HB, MF>(r1, ls, N, min(kb0 + 1, kb1 - 1));
-#pragma unroll
-            for (int i = 0; i < kRD; ++i) load_rec<kSplit, HB, MF>(R[i], ls, N, min(kb0 + 2 + i, kb1 - 1));
+            load_rec<kSplit, HB, MF>(R[0], ls, N, min(kb0 + 2, kb1 - 1));
+            load_rec<kSplit, HB, MF>(R[1], ls, N, min(kb0 + 3, kb1 - 1));
             decode_block<kSplit, kPca>(sm, r0, kb0, kb0 % 3, wj, wl, h);
             decode_block<kSplit, kPca>(sm, r1, kb0 + 1, (kb0 + 1) % 3, wj, wl, h);
+            P[0] = dec_prep<kSplit>(R[0], h);
+            load_rec<kSplit, HB, MF>(R[0], ls, N, min(kb0 + 4, kb1 - 1));
             lds_barrier();
         }
-        // iteration kb: decode block kb + 2 (a block past the range decodes a clamped
-        // record into a buffer nobody reads; its coefficient slot meets a zeroed Z value)
-        auto step = [&](int kb, LaneRec& r) __attribute__((always_inline)) {
-            decode_block<kSplit, kPca>(sm, r, kb + 2, (kb + 2) % 3, wj, wl, h);
-            load_rec<kSplit, HB, MF>(r, ls, N, min(kb + 2 + kRD, kb1 - 1));
+        // iteration kb: finish block kb + 2 (prepared last iteration), prepare block kb + 3
+        // (records in R[(kb - kb0 + 1) & 1], refilled with block kb + 5).  A block past the
+        // range decodes a clamped record into a buffer nobody reads; its coefficient slot
+        // meets a zeroed Z value.
+        auto step = [&](int kb, LaneRec& r, const DecPrep& pcur, DecPrep& pnext) __attribute__((always_inline)) {
+            pnext = dec_prep<kSplit>(r, h);
+            dec_finish<kPca>(sm, pcur, kb + 2, (kb + 2) % 3, wj, wl, h);
+            load_rec<kSplit, HB, MF>(r, ls, N, min(kb + 5, kb1 - 1));
             lds_barrier();
         };
         int kb = kb0;
-        for (; kb + kRD <= kb1; kb += kRD) {
-#pragma unroll
-            for (int u = 0; u < kRD; ++u) step(kb + u, R[u]);
+        for (; kb + 2 <= kb1; kb += 2) {
+            step(kb, R[1], P[0], P[1]);
+            step(kb + 1, R[0], P[1], P[0]);
         }
-#pragma unroll
-        for (int u = 0; u < kRD - 1; ++u)
-            if (kb + u < kb1) step(kb + u, R[u]);
+        if (kb < kb1) step(kb, R[1], P[0], P[1]);
         return;
     }
 
@@ -424,12 +459,15 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ 
 #pragma unroll
             for (int st = 0; st < 2; ++st)
                 bw[0][j][st] = *reinterpret_cast<const sx8_u32x4*>(src + (j * 2 + st) * 1024);
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the loop starts with no LDS read in flight
     }
 
     // iteration kb: request B of kb + 1, 16 MFMAs of block kb (A of kb + 2 requested as its
-    // registers free up), PCA k-step at the end of a group, barrier
-    auto body = [&](int kb, sx8_u32x4 (&acur)[MF][2], sx8_u32x4 (&bcur)[4][2], sx8_u32x4 (&bnext)[4][2])
-        __attribute__((always_inline)) {
+    // registers free up), PCA k-step when `pca` (end of a group), barrier.  The main loop
+    // runs whole groups with `pca` a constant, so its body has no branch (a branch around
+    // the PCA step makes the compiler wait for every LDS read before the next MFMA).
+    auto body = [&](int kb, sx8_u32x4 (&acur)[MF][2], sx8_u32x4 (&bcur)[4][2], sx8_u32x4 (&bnext)[4][2],
+                    const bool pca) __attribute__((always_inline)) {
         {
             const uint8_t* src = wbase + ((kb + 1) % 3) * kWtBufBytes;
 #pragma unroll
@@ -447,14 +485,14 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ 
 #pragma unroll
                 for (int f = 0; f < MF; ++f)
                     acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                        __builtin_bit_cast(sx8_half8, acur[f][st]),
-                        __builtin_bit_cast(sx8_half8, bcur[j][st]), acc[f][j], 0, 0, 0);
+                        __builtin_bit_cast(sx8_half8, bcur[j][st]),
+                        __builtin_bit_cast(sx8_half8, acur[f][st]), acc[f][j], 0, 0, 0);
             SX8_SCHED_FENCE();
             load_a_step<MF>(acur, ls, ka, st);
             SX8_SCHED_FENCE();
         }
         if constexpr (kPca) {
-            if ((kb & 3) == 3 || kb == kb1 - 1) {
+            if (pca) {
                 const int g = kb >> 2;
                 sx8_half8 zh[MF];
 #pragma unroll
@@ -464,33 +502,50 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ 
                     const sx8_half8 c = __builtin_bit_cast(sx8_half8, sm.pt[g & 1][j][lane]);
 #pragma unroll
                     for (int f = 0; f < MF; ++f)
-                        acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(zh[f], c, acc[f][j], 0, 0, 0);
+                        acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(c, zh[f], acc[f][j], 0, 0, 0);
                 }
                 load_za<MF>(za, ls, min(g + 1, (kb1 - 1) >> 2));
             }
         }
         lds_barrier();
     };
-    int kb = kb0;
-    for (; kb + 2 <= kb1; kb += 2) {
-        body(kb, A[0], bw[0], bw[1]);
-        body(kb + 1, A[1], bw[1], bw[0]);
+    int kb = kb0;   // a multiple of 4
+    for (; kb + 4 <= kb1; kb += 4) {
+        body(kb, A[0], bw[0], bw[1], false);
+        body(kb + 1, A[1], bw[1], bw[0], false);
+        body(kb + 2, A[0], bw[0], bw[1], false);
+        body(kb + 3, A[1], bw[1], bw[0], true);
     }
-    if (kb < kb1) body(kb, A[0], bw[0], bw[1]);
+    // last partial group (n_cb % 4 blocks): its PCA step after its last block
+    if (kb < kb1) body(kb, A[0], bw[0], bw[1], kb + 1 == kb1);
+    if (kb + 1 < kb1) body(kb + 1, A[1], bw[1], bw[0], kb + 2 == kb1);
+    if (kb + 2 < kb1) body(kb + 2, A[0], bw[0], bw[1], true);
 
-    // epilogue: accumulator (f, j) element i of lane l = 32 hf + c is row
-    // 32 MF wave + 32 f + (i % 4) + 4 hf + 8 (i / 4), column 32 j + c
+    // epilogue: the MFMAs take the weights as the A operand, so accumulator (f, j) holds the
+    // transposed tile: element i of lane l = 32 hf + c is column 32 j + 4 hf + 8 (i / 4) +
+    // i % 4 of row 32 MF wave + 32 f + c, and elements 4q .. 4q + 3 are 4 consecutive
+    // columns (one 16-byte store when N % 4 == 0 and Y is 16-byte aligned)
     float* dst = ks == 0 ? Y : part + (int64_t)(ks - 1) * M * N;
+    const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int n = n0 + 32 * j + r;
-        if (n >= N) continue;
+    for (int f = 0; f < MF; ++f) {
+        const int m = m0 + wave * 32 * MF + 32 * f + r;
+        if (m >= M) continue;
+        float* row = dst + (int64_t)m * N;
 #pragma unroll
-        for (int f = 0; f < MF; ++f)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int m = m0 + wave * 32 * MF + 32 * f + (i & 3) + 4 * hf + 8 * (i >> 2);
-                if (m < M) dst[(int64_t)m * N + n] = acc[f][j][i];
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + 32 * j + 8 * q + 4 * hf;
+                const sx8_float4 v = {acc[f][j][4 * q], acc[f][j][4 * q + 1], acc[f][j][4 * q + 2],
+                                      acc[f][j][4 * q + 3]};
+                if (vec && n + 3 < N) {
+                    *reinterpret_cast<sx8_float4*>(row + n) = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < N) row[n + e] = v[e];
+                }
             }
     }
 }
