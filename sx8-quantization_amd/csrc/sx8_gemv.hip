@@ -85,8 +85,17 @@ __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ 
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t rows = kPack ? (M + 31) / 32 * 32 : M;
     if (gid >= rows * n_cb) return;
-    const int64_t m = gid / n_cb;
-    const int64_t kb = gid - m * n_cb;
+    // packing: the row within its 32-row group runs fastest, so a wave's packed stores
+    // fill whole 512-byte runs; otherwise kb runs fastest (contiguous X reads, Z writes)
+    int64_t m, kb;
+    if constexpr (kPack) {
+        const int64_t rest = gid >> 5;
+        kb = rest % n_cb;
+        m = (rest / n_cb) * 32 + (gid & 31);
+    } else {
+        m = gid / n_cb;
+        kb = gid - m * n_cb;
+    }
     const bool row_ok = m < M;
     const uint16_t* x = X + min(m, M - 1) * ldx + kb * 32;
     const int kmax = row_ok ? (int)min((int64_t)32, K - kb * 32) : 0;
@@ -138,10 +147,11 @@ __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ 
                 for (int t = 0; t < off; ++t) p[t] = p[t] + p[t + off];
             z[j] = scales[kb * 2 + j] * p[0];
         }
+        const int64_t zi = m * n_cb + kb;
         if (hl)
-            *reinterpret_cast<uint2*>(Z + gid * 2) = make_uint2(sx8_split_hl(z[0]), sx8_split_hl(z[1]));
+            *reinterpret_cast<uint2*>(Z + zi * 2) = make_uint2(sx8_split_hl(z[0]), sx8_split_hl(z[1]));
         else
-            *reinterpret_cast<float2*>(Z + gid * 2) = make_float2(z[0], z[1]);
+            *reinterpret_cast<float2*>(Z + zi * 2) = make_float2(z[0], z[1]);
     }
 }
 
