@@ -31,6 +31,10 @@ LAYER = [  # (name, N, K)
     ("down_proj", 2560, 9728),
 ]
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
+# HBM bytes per k_gemv_panel launch on this workload (hdr_bytes=6), measured with two
+# rocprofv3 passes (FETCH_SIZE, WRITE_SIZE) scaled by what the counters read for a 512 MiB
+# copy (fetch x2.000, write x1.000); passes and calibration: profiles/gemv_decode_layer.md
+GEMV_TRAFFIC_PER_LAUNCH = 13.94e6
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, vendor figure
 
 
@@ -393,7 +397,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gv.get("achieved_gbs", 0.0) / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": GEMV_TRAFFIC_PER_LAUNCH if args.hdr_bytes == 6 else None,
+            "traffic_unit": "bytes per launch (HBM, rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
             "avg_launch_us": round(gv.get("avg_launch_us", 0.0), 3),
             "bytes_per_launch": gv.get("bytes_per_launch"),
         },
