@@ -53,8 +53,11 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|embed|copy (copy: the "
-                    "512 MiB device copy that calibrates the HBM byte counters)")
+    ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|embed|e2e|copy "
+                    "(copy: the 512 MiB device copy that calibrates the HBM byte counters)")
+    ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--e2e-prompt", type=int, default=512)
+    ap.add_argument("--e2e-new", type=int, default=256)
     return ap.parse_args()
 
 
@@ -274,6 +277,33 @@ def bench_embed(torch, L, layer, args):
     return {"table": f"{t['N']}x{t['K']}", "ids": 512, "us": us, "gbs": (rd + wr) / (us * 1e-6) / 1e9}
 
 
+def bench_e2e(torch, args):
+    """Config 5: 36-layer random-init Qwen3-4B-style decoder on S-X8 weights (every layer
+    quantized separately), batch 1: a 512-token prefill of uniform-random ids, then 256
+    greedy tokens, one decode step replayed from a HIP graph.  The whole generate() runs
+    twice; the second (warm) run is reported."""
+    from e2e_decoder import QWEN3_4B, SX8Decoder
+    t0 = time.time()
+    dec = SX8Decoder(QWEN3_4B, device="cuda", seed=7, max_len=1024)
+    log(f"e2e: built in {time.time() - t0:.1f}s")
+    g = torch.Generator(device="cpu").manual_seed(11)
+    ids = torch.randint(0, QWEN3_4B["vocab"], (args.e2e_prompt,), generator=g).cuda()
+    res = None
+    for _ in range(2):
+        out, tp, td = dec.generate(ids, args.e2e_new, use_graph=True)
+        res = {"prompt": args.e2e_prompt, "new_tokens": args.e2e_new,
+               "prefill_ms": tp * 1e3, "prefill_tok_s": args.e2e_prompt / tp,
+               "decode_ms_per_token": td * 1e3 / (args.e2e_new - 1),
+               "decode_tok_s": (args.e2e_new - 1) / td,
+               "weights_gb": sum(t.numel() for ly in dec.layers for lin in
+                                 (ly.q, ly.k, ly.v, ly.o, ly.gate, ly.up, ly.down)
+                                 for t in lin._t44[:2]) / 1e9 + sum(t.numel() for t in dec.head._t44[:2]) / 1e9}
+        log("e2e", json.dumps(res))
+    del dec
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_copy(torch, args):
     """Plain device copy of 512 MiB (torch's elementwise copy kernel), 10 launches: the
     known-size kernel that calibrates the FETCH_SIZE / WRITE_SIZE counters (each launch
@@ -364,6 +394,8 @@ def main():
     if args.only in ("", "embed"):
         res["embed"] = bench_embed(torch, L, layer, args)
         log("embed", json.dumps(res["embed"]))
+    if args.only in ("", "e2e") and not args.no_e2e:
+        res["e2e"] = bench_e2e(torch, args)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(layer, args.cpu_seconds)
@@ -405,6 +437,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill": res.get("prefill"),
         "embed": res.get("embed"),
+        "e2e": res.get("e2e"),
     }
     print(json.dumps(line), flush=True)
 

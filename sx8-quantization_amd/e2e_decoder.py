@@ -1,0 +1,234 @@
+"""End-to-end decoder stack on S-X8 weights: prefill, then greedy decode replayed from a
+HIP graph (the caller role of scripts/infer_sx8.py:109-173 and the CUDA-graph decode
+of results/fase4_v44_velocidad.json:70-80).
+
+A Qwen3-style dense decoder (RMSNorm, q/k RMSNorm per head, RoPE, GQA attention with
+a KV cache, SwiGLU MLP, tied S-X8 embedding / lm_head).  Every linear weight is an
+SX8LinearV44 (M = 1 -> the HIP decode GEMV, M > 1 -> the HIP prefill GEMM), the token
+embedding is an SX8EmbeddingV44 (HIP row gather); norms stay fp16.  The ops between
+the S-X8 kernels (norms, RoPE, attention over the cache, SiLU) are plain torch ops.
+
+Decode is graph-friendly: the step reads the current token and position from device
+tensors, writes the KV cache at that position with index_copy_, masks the unused cache
+tail, and writes the next token (argmax) and position back, so one captured step can be
+replayed for every generated token.
+"""
+from __future__ import annotations
+
+import math
+import time
+
+import torch
+import torch.nn as nn
+
+from integrate_fused_v44 import SX8LinearV44
+from prepare_v44 import to_v44_device
+from quantize_sx8 import quantize_tensor
+from sx8_embed_v44 import SX8EmbeddingV44
+
+QWEN3_4B = dict(hidden=2560, n_layers=36, n_heads=32, n_kv=8, head_dim=128,
+                inter=9728, vocab=151936, rope_theta=1.0e6, eps=1e-6)
+
+
+def _rms(x, w, eps):
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).half()
+
+
+def sx8_linear(out_f, in_f, gen, device, std=0.02, degenerate_frac=0.0):
+    """A random N(0, std) weight quantized to S-X8 on `device`, as an SX8LinearV44 with
+    its v4.4 device tensors already built."""
+    W = (torch.randn(out_f, in_f, generator=gen, device=device) * std).half()
+    qt, bi = quantize_tensor(W, device=device, degenerate_frac=degenerate_frac,
+                             seed=int(torch.randint(0, 1 << 30, (1,), generator=gen, device=device)))
+    lin = SX8LinearV44(qt, bi, None, out_f, in_f, hdr_bytes=6)
+    lin._t44 = to_v44_device(qt, bi, hdr_aligned=False, device=device)
+    return lin
+
+
+def clone_linear(lin):
+    """Same values in new device memory (so every layer streams its own bytes)."""
+    new = SX8LinearV44(lin.qt, lin.bases_info, None, lin.out_f, lin.in_f, hdr_bytes=6)
+    new._t44 = tuple(t.clone() for t in lin._t44)
+    return new
+
+
+class Layer(nn.Module):
+    def __init__(self, cfg, lins, device):
+        super().__init__()
+        H, hd = cfg["hidden"], cfg["head_dim"]
+        self.q, self.k, self.v, self.o, self.gate, self.up, self.down = lins
+        self.in_norm = torch.ones(H, dtype=torch.float16, device=device)
+        self.post_norm = torch.ones(H, dtype=torch.float16, device=device)
+        self.q_norm = torch.ones(hd, dtype=torch.float16, device=device)
+        self.k_norm = torch.ones(hd, dtype=torch.float16, device=device)
+
+
+class SX8Decoder(nn.Module):
+    """Random-init decoder.  `n_distinct` layers get their own random weights; layer i
+    reuses the values of layer i % n_distinct in its own device memory."""
+
+    def __init__(self, cfg=QWEN3_4B, device=None, seed=0, n_distinct=None, max_len=1024,
+                 log=None):
+        super().__init__()
+        self.cfg = cfg = dict(cfg)
+        device = torch.device(device or "cuda")
+        self.device = device
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed)
+        H, nh, nk, hd, I = cfg["hidden"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["inter"]
+        L = cfg["n_layers"]
+        n_distinct = L if n_distinct is None else max(1, min(n_distinct, L))
+        t0 = time.time()
+        base = []
+        for i in range(n_distinct):
+            base.append([sx8_linear(nh * hd, H, gen, device), sx8_linear(nk * hd, H, gen, device),
+                         sx8_linear(nk * hd, H, gen, device), sx8_linear(H, nh * hd, gen, device),
+                         sx8_linear(I, H, gen, device), sx8_linear(I, H, gen, device),
+                         sx8_linear(H, I, gen, device)])
+            if log:
+                log(f"e2e: quantized layer {i} ({time.time() - t0:.1f}s)")
+        layers = []
+        for i in range(L):
+            src = base[i % n_distinct]
+            lins = src if i < n_distinct else [clone_linear(l) for l in src]
+            layers.append(Layer(cfg, lins, device))
+        self.layers = layers
+        self.head = sx8_linear(cfg["vocab"], H, gen, device)      # tied lm_head / embedding
+        self.embed = SX8EmbeddingV44(self.head.qt, self.head.bases_info, hdr_bytes=6)
+        self.embed._t = self.head._t44                              # share the device tensors
+        self.embed._hdr, self.embed._lvl, self.embed._bas, self.embed._sca = self.head._t44
+        self.final_norm = torch.ones(H, dtype=torch.float16, device=device)
+        if log:
+            log(f"e2e: quantized lm_head {cfg['vocab']}x{H} ({time.time() - t0:.1f}s)")
+        # RoPE tables (neox halves) and the KV cache
+        inv = 1.0 / (cfg["rope_theta"] ** (torch.arange(0, hd, 2, device=device).float() / hd))
+        pos = torch.arange(max_len, device=device).float()
+        ang = torch.outer(pos, inv)
+        self.cos, self.sin = ang.cos(), ang.sin()                   # (max_len, hd / 2)
+        self.max_len = max_len
+        self.k_cache = [torch.zeros(nk, hd, max_len, dtype=torch.float16, device=device) for _ in range(L)]
+        self.v_cache = [torch.zeros(nk, max_len, hd, dtype=torch.float16, device=device) for _ in range(L)]
+        self.arange = torch.arange(max_len, device=device)
+
+    # ---------------------------------------------------------------- helpers
+    def _rope(self, x, cos, sin):
+        """x (T, heads, hd) fp16; cos/sin (T, hd / 2) fp32."""
+        h = x.shape[-1] // 2
+        xf = x.float()
+        x1, x2 = xf[..., :h], xf[..., h:]
+        c, s = cos[:, None, :], sin[:, None, :]
+        return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1).half()
+
+    def _mlp(self, ly, x):
+        h = _rms(x, ly.post_norm, self.cfg["eps"])
+        g = ly.gate(h)
+        u = ly.up(h)
+        return ly.down((torch.nn.functional.silu(g.float()) * u.float()).half())
+
+    # ---------------------------------------------------------------- prefill
+    @torch.no_grad()
+    def prefill(self, ids):
+        """ids (T,) int64 on the device -> next token (1,) int64; fills the KV cache."""
+        cfg = self.cfg
+        nh, nk, hd, eps = cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["eps"]
+        T = ids.shape[0]
+        x = self.embed(ids)                                        # (T, H) fp16
+        cos, sin = self.cos[:T], self.sin[:T]
+        for li, ly in enumerate(self.layers):
+            h = _rms(x, ly.in_norm, eps)
+            q = _rms(ly.q(h).view(T, nh, hd), ly.q_norm, eps)
+            k = _rms(ly.k(h).view(T, nk, hd), ly.k_norm, eps)
+            v = ly.v(h).view(T, nk, hd)
+            q, k = self._rope(q, cos, sin), self._rope(k, cos, sin)
+            self.k_cache[li][:, :, :T] = k.permute(1, 2, 0)
+            self.v_cache[li][:, :T, :] = v.permute(1, 0, 2)
+            rep = nh // nk
+            qf = q.permute(1, 0, 2).float().contiguous()                       # (nh, T, hd)
+            kf = k.permute(1, 0, 2).float().repeat_interleave(rep, 0).contiguous()
+            vf = v.permute(1, 0, 2).float().repeat_interleave(rep, 0).contiguous()
+            a = torch.nn.functional.scaled_dot_product_attention(qf[None], kf[None], vf[None],
+                                                                 is_causal=True)[0]
+            x = x + ly.o(a.permute(1, 0, 2).reshape(T, nh * hd).half())
+            x = x + self._mlp(ly, x)
+        logits = self.head(_rms(x[-1:], self.final_norm, eps))
+        return logits.float().argmax(-1)
+
+    # ---------------------------------------------------------------- decode
+    @torch.no_grad()
+    def decode_step(self, tok, pos):
+        """One greedy step: tok (1,) int64, pos (1,) int64 device tensors (the position
+        the token is written at).  Updates tok and pos in place; no host sync."""
+        cfg = self.cfg
+        nh, nk, hd, eps = cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["eps"]
+        rep = nh // nk
+        x = self.embed(tok)                                        # (1, H)
+        cos, sin = self.cos.index_select(0, pos), self.sin.index_select(0, pos)
+        mask = torch.where(self.arange <= pos, 0.0, float("-inf"))            # (max_len,)
+        scale = 1.0 / math.sqrt(hd)
+        for li, ly in enumerate(self.layers):
+            h = _rms(x, ly.in_norm, eps)
+            q = _rms(ly.q(h).view(1, nh, hd), ly.q_norm, eps)
+            k = _rms(ly.k(h).view(1, nk, hd), ly.k_norm, eps)
+            v = ly.v(h).view(1, nk, hd)
+            q, k = self._rope(q, cos, sin), self._rope(k, cos, sin)
+            self.k_cache[li].index_copy_(2, pos, k.view(nk, hd, 1))
+            self.v_cache[li].index_copy_(1, pos, v.view(nk, 1, hd))
+            s = torch.matmul(q.view(nk, rep, hd), self.k_cache[li]).float() * scale + mask
+            p = torch.softmax(s, dim=-1).half()                                 # (nk, rep, L)
+            a = torch.matmul(p, self.v_cache[li])                                # (nk, rep, hd)
+            x = x + ly.o(a.reshape(1, nh * hd))
+            x = x + self._mlp(ly, x)
+        logits = self.head(_rms(x, self.final_norm, eps))
+        tok.copy_(logits.float().argmax(-1))
+        pos.add_(1)
+        return tok
+
+    # ---------------------------------------------------------------- generation
+    @torch.no_grad()
+    def generate(self, ids, n_new, use_graph=True):
+        """Prefill `ids`, then greedily decode `n_new` tokens.  Returns (tokens (n_new,)
+        on the device, prefill seconds, decode seconds)."""
+        dev = self.device
+        T = ids.shape[0]
+        assert T + n_new <= self.max_len
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        first = self.prefill(ids)
+        torch.cuda.synchronize()
+        t_prefill = time.perf_counter() - t0
+        tok = first.clone()
+        pos = torch.full((1,), T, dtype=torch.int64, device=dev)
+        out = torch.empty(n_new, dtype=torch.int64, device=dev)
+        out[0] = first[0]
+        if use_graph:
+            # warm-up (pools, workspaces) on a side stream, then capture one step
+            saved = (tok.clone(), pos.clone())
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                self.decode_step(tok, pos)
+            torch.cuda.current_stream().wait_stream(s)
+            tok.copy_(saved[0])
+            pos.copy_(saved[1])
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.decode_step(tok, pos)
+            tok.copy_(saved[0])
+            pos.copy_(saved[1])
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            for i in range(1, n_new):
+                g.replay()
+                out[i:i + 1].copy_(tok)
+            torch.cuda.synchronize()
+            t_decode = time.perf_counter() - t1
+        else:
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            for i in range(1, n_new):
+                self.decode_step(tok, pos)
+                out[i:i + 1].copy_(tok)
+            torch.cuda.synchronize()
+            t_decode = time.perf_counter() - t1
+        return out, t_prefill, t_decode
