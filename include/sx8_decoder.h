@@ -1,0 +1,55 @@
+/* sx8_decoder.h -- per-token ops of the end-to-end S-X8 decoder (libsx8_hip.so).
+ *
+ * These sit between the S-X8 GEMVs of sx8_hip.h in one decode step.  They replace the
+ * Hugging Face Qwen module ops (RMSNorm, rotary embedding, SDPA over the KV cache, SiLU,
+ * greedy argmax) that the reference's runtime runs around its S-X8 linears
+ * (scripts/infer_sx8.py:109-173).  Every entry point reads the decode position from
+ * device memory, so one step can be captured in a HIP graph and replayed.  Conventions as
+ * in sx8_hip.h: device pointers, fp16 as uint16_t bits, int32_t status, stream as void*.
+ */
+#ifndef SX8_DECODER_H
+#define SX8_DECODER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* For each of M rows of H: resid = (init ? fp16 init : resid) + (delta ? delta : 0) in
+ * float32 (the updated residual stream is written back), then out = fp16(resid *
+ * rsqrt(mean(resid^2) + eps) * w).  delta and init may be NULL. */
+int32_t sx8_dec_add_rmsnorm(float* resid, const float* delta, const uint16_t* init,
+                            const uint16_t* w, uint16_t* out, int64_t M, int64_t H, float eps,
+                            void* stream);
+
+/* One token at position *pos: per query/key head RMSNorm (q_norm/k_norm weights, over hd),
+ * fp16 rounding, rotate-half RoPE with cos_t/sin_t rows (L, hd/2) float32; q into q_out
+ * (nh*hd fp16), k and v into row *pos of k_cache / v_cache ((nk, L, hd) fp16 each).  A
+ * position outside [0, L) writes nothing.  hd even and <= 256. */
+int32_t sx8_dec_qk_rope_cache(const float* q_raw, const float* k_raw, const float* v_raw,
+                              const uint16_t* q_norm, const uint16_t* k_norm, const float* cos_t,
+                              const float* sin_t, const int64_t* pos, uint16_t* q_out,
+                              uint16_t* k_cache, uint16_t* v_cache, int32_t nh, int32_t nk,
+                              int32_t hd, int64_t L, float eps, void* stream);
+
+/* Decode attention of one token: for each of nh query heads (kv head = h / (nh/nk)),
+ * softmax(scale * q . K[0..*pos]) . V[0..*pos] over the caches written by
+ * sx8_dec_qk_rope_cache; out (nh*hd) fp16.  hd 64 or 128, L <= 4096, q and caches
+ * 16-byte aligned. */
+int32_t sx8_dec_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                     const int64_t* pos, uint16_t* out, int32_t nh, int32_t nk, int32_t hd,
+                     int64_t L, float scale, void* stream);
+
+/* out = fp16(silu(g) * u) over n float32 elements. */
+int32_t sx8_dec_silu_mul(const float* g, const float* u, uint16_t* out, int64_t n, void* stream);
+
+/* *tok = argmax(logits[0..n)) (first index among equal maxima), then *pos += 1. */
+int32_t sx8_dec_argmax_advance(const float* logits, int64_t n, int64_t* tok, int64_t* pos,
+                               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SX8_DECODER_H */

@@ -18,7 +18,7 @@ CSRC_DIR = os.path.join(PKG_DIR, "csrc")
 INCLUDE_DIR = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libsx8_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["sx8_abi.hip", "sx8_dequant.hip", "sx8_gemv.hip", "sx8_gemm.hip"]
+SOURCES = ["sx8_abi.hip", "sx8_dequant.hip", "sx8_gemv.hip", "sx8_gemm.hip", "sx8_decoder.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # hipcc flags: gfx950 only, no packed-fp32 instruction selection (those forms have
@@ -47,6 +47,13 @@ SIGNATURES = [
     ("sx8_gemm_prefill_z", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _I64, _I64, _P, _P]),
     ("sx8_gemm_pca_z", _I32, [_P, _I64, _P, _I32, _I64, _I64, _P, _P]),
     ("sx8_gemm_prefill_core", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _I64, _I64, _P, _P]),
+    # include/sx8_decoder.h
+    ("sx8_dec_add_rmsnorm", _I32, [_P, _P, _P, _P, _P, _I64, _I64, ctypes.c_float, _P]),
+    ("sx8_dec_qk_rope_cache", _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                                     _I64, ctypes.c_float, _P]),
+    ("sx8_dec_attn", _I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I64, ctypes.c_float, _P]),
+    ("sx8_dec_silu_mul", _I32, [_P, _P, _P, _I64, _P]),
+    ("sx8_dec_argmax_advance", _I32, [_P, _I64, _P, _P, _P]),
 ]
 ABI_VERSION = 1
 

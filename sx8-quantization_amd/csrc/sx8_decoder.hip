@@ -1,0 +1,347 @@
+// sx8_decoder.hip -- the small per-token ops of the end-to-end decoder that sit between
+// the S-X8 GEMVs: residual add + RMSNorm, q/k RMSNorm + RoPE + KV-cache write, decode
+// attention over the cache, SiLU * up, greedy argmax.  (In the reference these are the
+// Hugging Face Qwen modules driven by scripts/infer_sx8.py:109-173.)  Each is one launch
+// that reads its position from device memory, so a whole decode step can be captured in
+// a HIP graph and replayed.
+#include "sx8_device.h"
+#include "sx8_host.h"
+
+namespace {
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+typedef uint32_t sx8_u32x4 __attribute__((ext_vector_type(4)));
+
+// Sum over a 256-thread block (wave64 shuffles, then 4 partials through LDS).
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+}
+
+__device__ __forceinline__ float block_max256(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Row r: resid = (init ? fp16 init : resid) + (delta ? delta : 0) in f32; out = fp16(resid *
+// rsqrt(mean(resid^2) + eps) * w).  Rows of up to 256 * kRmsPer values stay in registers
+// (every load of the row is issued before the reduction); longer rows loop.
+constexpr int kRmsPer = 16;
+
+__global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ resid, const float* __restrict__ delta,
+                                                     const uint16_t* __restrict__ init,
+                                                     const uint16_t* __restrict__ w,
+                                                     uint16_t* __restrict__ out, int H, float eps) {
+    __shared__ float red[4];
+    const int64_t base = (int64_t)blockIdx.x * H;
+    if (H <= 256 * kRmsPer) {
+        float v[kRmsPer], wv[kRmsPer];
+#pragma unroll
+        for (int u = 0; u < kRmsPer; ++u) {
+            const int i = threadIdx.x + 256 * u;
+            const int ic = min(i, H - 1);
+            float x = init ? h2f(init[base + ic]) : resid[base + ic];
+            if (delta) x += delta[base + ic];
+            v[u] = i < H ? x : 0.f;
+            wv[u] = h2f(w[ic]);
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < kRmsPer; ++u) ss += v[u] * v[u];
+        const float inv = 1.0f / sqrtf(block_sum256(ss, red) / (float)H + eps);
+#pragma unroll
+        for (int u = 0; u < kRmsPer; ++u) {
+            const int i = threadIdx.x + 256 * u;
+            if (i < H) {
+                resid[base + i] = v[u];
+                out[base + i] = f2h(v[u] * inv * wv[u]);
+            }
+        }
+        return;
+    }
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < H; i += 256) {
+        float x = init ? h2f(init[base + i]) : resid[base + i];
+        if (delta) x += delta[base + i];
+        resid[base + i] = x;
+        ss += x * x;
+    }
+    const float inv = 1.0f / sqrtf(block_sum256(ss, red) / (float)H + eps);
+    for (int i = threadIdx.x; i < H; i += 256) out[base + i] = f2h(resid[base + i] * inv * h2f(w[i]));
+}
+
+// One block per head (nh query heads, then nk key heads, then nk value heads) of
+// 64 * ceil(hd / 128) threads, thread d < hd / 2 owning the pair (d, d + hd / 2): q/k RMSNorm
+// over the head, RoPE (rotate-half) at position *pos, q to q_out, k into k_cache and v into
+// v_cache (both (nk, L, hd)).
+__global__ __launch_bounds__(128) void k_qk_rope_cache(const float* __restrict__ q_raw,
+                                                       const float* __restrict__ k_raw,
+                                                       const float* __restrict__ v_raw,
+                                                       const uint16_t* __restrict__ qn,
+                                                       const uint16_t* __restrict__ kn,
+                                                       const float* __restrict__ cos_t,
+                                                       const float* __restrict__ sin_t,
+                                                       const int64_t* __restrict__ pos_p,
+                                                       uint16_t* __restrict__ q_out,
+                                                       uint16_t* __restrict__ k_cache,
+                                                       uint16_t* __restrict__ v_cache, int nh,
+                                                       int nk, int hd, int L, float eps) {
+    __shared__ float red[2];
+    const int64_t pos = *pos_p;
+    if (pos < 0 || pos >= L) return;         // position outside the cache: nothing to write
+    const int half = hd >> 1;
+    const int d = threadIdx.x;
+    const int b = blockIdx.x;
+    if (b >= nh + nk) {                      // value head: copy into the cache
+        const int h = b - nh - nk;
+        for (int e = d; e < hd; e += blockDim.x) v_cache[((int64_t)h * L + pos) * hd + e] = f2h(v_raw[h * hd + e]);
+        return;
+    }
+    const bool is_q = b < nh;
+    const int h = is_q ? b : b - nh;
+    const float* src = is_q ? q_raw + h * hd : k_raw + h * hd;
+    const uint16_t* nw = is_q ? qn : kn;
+    const bool act = d < half;
+    const float x1 = act ? src[d] : 0.f, x2 = act ? src[d + half] : 0.f;
+    float ss = x1 * x1 + x2 * x2;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (blockDim.x > 64) {
+        if ((d & 63) == 0) red[d >> 6] = ss;
+        __syncthreads();
+        ss = red[0] + red[1];
+    }
+    if (!act) return;
+    const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+    // round to fp16 after the norm, as the fp16 activations of the model do
+    const float n1 = h2f(f2h(x1 * inv * h2f(nw[d]))), n2 = h2f(f2h(x2 * inv * h2f(nw[d + half])));
+    const float c = cos_t[pos * half + d], s = sin_t[pos * half + d];
+    const float o1 = n1 * c - n2 * s, o2 = n2 * c + n1 * s;
+    if (is_q) {
+        q_out[h * hd + d] = f2h(o1);
+        q_out[h * hd + d + half] = f2h(o2);
+    } else {
+        k_cache[((int64_t)h * L + pos) * hd + d] = f2h(o1);
+        k_cache[((int64_t)h * L + pos) * hd + d + half] = f2h(o2);
+    }
+}
+
+// Decode attention: one 256-thread block per query head over cache positions 0..*pos,
+// caches (nk, L, hd).  Work-group b runs query head (b % 8) * (nh / 8) + b / 8, so the
+// query heads sharing a KV head run on one XCD and share its L2 copy of the cache (for
+// nh % 8 == 0).  Scores: a lane holds 8 consecutive dims of one position (one 16-byte
+// load), the CH = hd / 8 lanes of a position reduce with shuffles.  Output: thread
+// (position group, 8-dim chunk) accumulates its positions, the groups meet in LDS.
+constexpr int kAttnMaxL = 4096;
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_decode(const uint16_t* __restrict__ q,
+                                                     const uint16_t* __restrict__ k_cache,
+                                                     const uint16_t* __restrict__ v_cache,
+                                                     const int64_t* __restrict__ pos_p,
+                                                     uint16_t* __restrict__ out, int nh, int nk,
+                                                     int L, float scale) {
+    constexpr int CH = HD / 8;             // 16-byte chunks per cache row
+    constexpr int PG = 256 / CH;           // position groups of the output pass
+    __shared__ float p[kAttnMaxL];
+    __shared__ float red[4];
+    __shared__ float acc[PG][HD + 4];
+    const int b = blockIdx.x;
+    const int h = (nh % 8 == 0) ? (b % 8) * (nh / 8) + b / 8 : b;
+    const int kv = h / (nh / nk);
+    const int64_t pos = *pos_p;
+    const int n = (int)min(max(pos, (int64_t)0) + 1, (int64_t)L);   // positions 0..pos, inside the cache
+    const int tid = threadIdx.x;
+    const int c = tid % CH;
+    float qv[8];
+    {
+        const sx8_u32x4 w = *reinterpret_cast<const sx8_u32x4*>(q + h * HD + 8 * c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            qv[2 * e] = h2f(w[e] & 0xFFFFu);
+            qv[2 * e + 1] = h2f(w[e] >> 16);
+        }
+    }
+    const uint16_t* kc = k_cache + (int64_t)kv * L * HD;
+    float m = -INFINITY;
+    // kU positions per lane in flight: all loads of a round are issued before any is used
+    constexpr int kU = 8;
+    for (int j0 = tid / CH; j0 < n; j0 += kU * PG) {
+        sx8_u32x4 w[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int j = min(j0 + u * PG, n - 1);      // past the end: a valid row, result unused
+            w[u] = *reinterpret_cast<const sx8_u32x4*>(kc + (int64_t)j * HD + 8 * c);
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            float s = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                s += qv[2 * e] * h2f(w[u][e] & 0xFFFFu) + qv[2 * e + 1] * h2f(w[u][e] >> 16);
+#pragma unroll
+            for (int o = CH / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+            s *= scale;
+            const int j = j0 + u * PG;
+            if (j < n) {
+                if (c == 0) p[j] = s;
+                m = fmaxf(m, s);
+            }
+        }
+    }
+    m = block_max256(m, red);            // its barriers also publish p[]
+    float sum = 0.f;
+    for (int j = tid; j < n; j += 256) {
+        const float e = __expf(p[j] - m);
+        p[j] = e;
+        sum += e;
+    }
+    sum = block_sum256(sum, red);
+    const uint16_t* vc = v_cache + (int64_t)kv * L * HD;
+    const int pg = tid / CH;
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j0 = pg; j0 < n; j0 += kU * PG) {
+        sx8_u32x4 w[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int j = min(j0 + u * PG, n - 1);
+            w[u] = *reinterpret_cast<const sx8_u32x4*>(vc + (int64_t)j * HD + 8 * c);
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int j = j0 + u * PG;
+            const float pj = j < n ? p[j] : 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                a[2 * e] += pj * h2f(w[u][e] & 0xFFFFu);
+                a[2 * e + 1] += pj * h2f(w[u][e] >> 16);
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[pg][8 * c + e] = a[e];
+    __syncthreads();
+    if (tid < HD) {
+        float t = 0.f;
+        for (int g = 0; g < PG; ++g) t += acc[g][tid];
+        out[h * HD + tid] = f2h(t / sum);
+    }
+}
+
+// out = fp16(silu(g) * u), g and u f32
+__global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ g, const float* __restrict__ u,
+                                                  uint16_t* __restrict__ out, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float x = g[i];
+    out[i] = f2h(x / (1.0f + __expf(-x)) * u[i]);
+}
+
+// tok = argmax(logits) (first index among equal maxima), *pos += 1.  One 1024-thread block.
+__global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict__ logits, int64_t n,
+                                                         int64_t* __restrict__ tok,
+                                                         int64_t* __restrict__ pos) {
+    __shared__ float bv[16];
+    __shared__ int64_t bi[16];
+    float v = -INFINITY;
+    int64_t idx = INT64_MAX;
+    for (int64_t i = threadIdx.x; i < n; i += 1024) {
+        const float x = logits[i];
+        if (x > v || (x == v && i < idx)) { v = x; idx = i; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o, 64);
+        const int64_t oi = __shfl_xor(idx, o, 64);
+        if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+    }
+    if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = v; bi[threadIdx.x >> 6] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 16; ++w)
+            if (bv[w] > v || (bv[w] == v && bi[w] < idx)) { v = bv[w]; idx = bi[w]; }
+        tok[0] = idx;
+        pos[0] += 1;
+    }
+}
+
+}  // namespace
+
+extern "C" int32_t sx8_dec_add_rmsnorm(float* resid, const float* delta, const uint16_t* init,
+                                       const uint16_t* w, uint16_t* out, int64_t M, int64_t H,
+                                       float eps, void* stream) {
+    using namespace sx8;
+    if (!resid || !w || !out) return fail(SX8_ERR_INVALID, "sx8_dec_add_rmsnorm: null pointer");
+    if (M <= 0 || H <= 0 || M > 0x7FFFFFFF || H > 0x7FFFFFFF)
+        return fail(SX8_ERR_INVALID, "sx8_dec_add_rmsnorm: bad shape");
+    hipLaunchKernelGGL(k_add_rmsnorm, dim3((unsigned)M), dim3(256), 0, as_stream(stream), resid, delta,
+                       init, w, out, (int)H, eps);
+    return check_launch("sx8_dec_add_rmsnorm");
+}
+
+extern "C" int32_t sx8_dec_qk_rope_cache(const float* q_raw, const float* k_raw, const float* v_raw,
+                                         const uint16_t* q_norm, const uint16_t* k_norm,
+                                         const float* cos_t, const float* sin_t, const int64_t* pos,
+                                         uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+                                         int32_t nh, int32_t nk, int32_t hd, int64_t L, float eps,
+                                         void* stream) {
+    using namespace sx8;
+    if (!q_raw || !k_raw || !v_raw || !q_norm || !k_norm || !cos_t || !sin_t || !pos || !q_out ||
+        !k_cache || !v_cache)
+        return fail(SX8_ERR_INVALID, "sx8_dec_qk_rope_cache: null pointer");
+    if (nh <= 0 || nk <= 0 || nh % nk || hd <= 0 || (hd & 1) || hd > 256 || L <= 0 || L > 0x7FFFFFFF)
+        return fail(SX8_ERR_INVALID, "sx8_dec_qk_rope_cache: bad shape (hd even, <= 256)");
+    hipLaunchKernelGGL(k_qk_rope_cache, dim3((unsigned)(nh + 2 * nk)), dim3(hd > 128 ? 128 : 64), 0,
+                       as_stream(stream), q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, pos,
+                       q_out, k_cache, v_cache, nh, nk, hd, (int)L, eps);
+    return check_launch("sx8_dec_qk_rope_cache");
+}
+
+extern "C" int32_t sx8_dec_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                const int64_t* pos, uint16_t* out, int32_t nh, int32_t nk, int32_t hd,
+                                int64_t L, float scale, void* stream) {
+    using namespace sx8;
+    if (!q || !k_cache || !v_cache || !pos || !out) return fail(SX8_ERR_INVALID, "sx8_dec_attn: null pointer");
+    if (nh <= 0 || nk <= 0 || nh % nk || (hd != 64 && hd != 128) || L <= 0 || L > kAttnMaxL)
+        return fail(SX8_ERR_INVALID, "sx8_dec_attn: bad shape (hd 64 or 128, cache length <= %d)",
+                    kAttnMaxL);
+    if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
+        return fail(SX8_ERR_INVALID, "sx8_dec_attn: q and caches must be 16-byte aligned");
+    if (hd == 128)
+        hipLaunchKernelGGL(k_attn_decode<128>, dim3((unsigned)nh), dim3(256), 0, as_stream(stream), q,
+                           k_cache, v_cache, pos, out, nh, nk, (int)L, scale);
+    else
+        hipLaunchKernelGGL(k_attn_decode<64>, dim3((unsigned)nh), dim3(256), 0, as_stream(stream), q,
+                           k_cache, v_cache, pos, out, nh, nk, (int)L, scale);
+    return check_launch("sx8_dec_attn");
+}
+
+extern "C" int32_t sx8_dec_silu_mul(const float* g, const float* u, uint16_t* out, int64_t n, void* stream) {
+    using namespace sx8;
+    if (!g || !u || !out) return fail(SX8_ERR_INVALID, "sx8_dec_silu_mul: null pointer");
+    if (n <= 0 || (n + 255) / 256 > 0x7FFFFFFF) return fail(SX8_ERR_INVALID, "sx8_dec_silu_mul: bad size");
+    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream), g,
+                       u, out, n);
+    return check_launch("sx8_dec_silu_mul");
+}
+
+extern "C" int32_t sx8_dec_argmax_advance(const float* logits, int64_t n, int64_t* tok, int64_t* pos,
+                                          void* stream) {
+    using namespace sx8;
+    if (!logits || !tok || !pos) return fail(SX8_ERR_INVALID, "sx8_dec_argmax_advance: null pointer");
+    if (n <= 0) return fail(SX8_ERR_INVALID, "sx8_dec_argmax_advance: bad size");
+    hipLaunchKernelGGL(k_argmax_advance, dim3(1), dim3(1024), 0, as_stream(stream), logits, n, tok, pos);
+    return check_launch("sx8_dec_argmax_advance");
+}

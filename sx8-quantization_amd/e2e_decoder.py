@@ -21,6 +21,7 @@ import time
 import torch
 import torch.nn as nn
 
+import _sx8lib as _L
 from integrate_fused_v44 import SX8LinearV44
 from prepare_v44 import to_v44_device
 from quantize_sx8 import quantize_tensor
@@ -107,7 +108,7 @@ class SX8Decoder(nn.Module):
         ang = torch.outer(pos, inv)
         self.cos, self.sin = ang.cos(), ang.sin()                   # (max_len, hd / 2)
         self.max_len = max_len
-        self.k_cache = [torch.zeros(nk, hd, max_len, dtype=torch.float16, device=device) for _ in range(L)]
+        self.k_cache = [torch.zeros(nk, max_len, hd, dtype=torch.float16, device=device) for _ in range(L)]
         self.v_cache = [torch.zeros(nk, max_len, hd, dtype=torch.float16, device=device) for _ in range(L)]
         self.arange = torch.arange(max_len, device=device)
 
@@ -141,7 +142,7 @@ class SX8Decoder(nn.Module):
             k = _rms(ly.k(h).view(T, nk, hd), ly.k_norm, eps)
             v = ly.v(h).view(T, nk, hd)
             q, k = self._rope(q, cos, sin), self._rope(k, cos, sin)
-            self.k_cache[li][:, :, :T] = k.permute(1, 2, 0)
+            self.k_cache[li][:, :T, :] = k.permute(1, 0, 2)
             self.v_cache[li][:, :T, :] = v.permute(1, 0, 2)
             rep = nh // nk
             qf = q.permute(1, 0, 2).float().contiguous()                       # (nh, T, hd)
@@ -172,9 +173,10 @@ class SX8Decoder(nn.Module):
             k = _rms(ly.k(h).view(1, nk, hd), ly.k_norm, eps)
             v = ly.v(h).view(1, nk, hd)
             q, k = self._rope(q, cos, sin), self._rope(k, cos, sin)
-            self.k_cache[li].index_copy_(2, pos, k.view(nk, hd, 1))
+            self.k_cache[li].index_copy_(1, pos, k.view(nk, 1, hd))
             self.v_cache[li].index_copy_(1, pos, v.view(nk, 1, hd))
-            s = torch.matmul(q.view(nk, rep, hd), self.k_cache[li]).float() * scale + mask
+            qt = q.view(nk, rep, hd).transpose(1, 2).contiguous()               # (nk, hd, rep)
+            s = torch.matmul(self.k_cache[li], qt).transpose(1, 2).float() * scale + mask
             p = torch.softmax(s, dim=-1).half()                                 # (nk, rep, L)
             a = torch.matmul(p, self.v_cache[li])                                # (nk, rep, hd)
             x = x + ly.o(a.reshape(1, nh * hd))
@@ -184,9 +186,76 @@ class SX8Decoder(nn.Module):
         pos.add_(1)
         return tok
 
+    # ---------------------------------------------------------------- fused decode
+    def _fused_setup(self):
+        """Buffers and ctypes argument lists of the fused decode step (built once)."""
+        if getattr(self, "_fz", None) is not None:
+            return self._fz
+        cfg, dev = self.cfg, self.device
+        H, nh, nk, hd, I, V = (cfg["hidden"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"],
+                               cfg["inter"], cfg["vocab"])
+        f32 = dict(dtype=torch.float32, device=dev)
+        f16 = dict(dtype=torch.float16, device=dev)
+        z = {"resid": torch.zeros(1, H, **f32), "h": torch.zeros(H, **f16),
+             "q": torch.zeros(nh * hd, **f32), "k": torch.zeros(nk * hd, **f32),
+             "v": torch.zeros(nk * hd, **f32), "qh": torch.zeros(nh * hd, **f16),
+             "a": torch.zeros(nh * hd, **f16), "o": torch.zeros(H, **f32),
+             "g": torch.zeros(I, **f32), "u": torch.zeros(I, **f32), "m": torch.zeros(I, **f16),
+             "d": torch.zeros(H, **f32), "logits": torch.zeros(V, **f32)}
+        n_cb_max = max(lin.qt["n_cb"] for ly in self.layers for lin in (ly.q, ly.o, ly.down))
+        ws_bytes = int(_L.lib().sx8_gemv_workspace_bytes(max(n_cb_max, self.head.qt["n_cb"])))
+        z["ws"] = torch.zeros((ws_bytes + 3) // 4 + 64, **f32)
+        self._fz = z
+        return z
+
+    def _gemv(self, lin, x, y, st):
+        z = self._fz
+        hdr, lvl, bas, sca = lin._t44
+        _L.call("sx8_gemv", _L.ptr(x), _L.ptr(hdr), _L.ptr(lvl), 6, _L.ptr(bas), _L.ptr(sca), None,
+                None, lin.out_f, lin.qt["n_cb"], _L.ptr(y), _L.ptr(z["ws"]), z["ws"].numel() * 4, st)
+
+    @torch.no_grad()
+    def decode_step_fused(self, tok, pos):
+        """decode_step with the per-token ops as single HIP launches (sx8_decoder.h) and the
+        GEMVs called through the C ABI; the residual stream is float32."""
+        cfg = self.cfg
+        nh, nk, hd, eps = cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["eps"]
+        z = self._fused_setup()
+        st = _L.stream(self.device)
+        P = _L.ptr
+        emb = self.embed(tok)                                       # (1, H) fp16
+        L = self.max_len
+        for li, ly in enumerate(self.layers):
+            if li == 0:
+                _L.call("sx8_dec_add_rmsnorm", P(z["resid"]), None, P(emb), P(ly.in_norm), P(z["h"]), 1,
+                        cfg["hidden"], eps, st)
+            else:
+                _L.call("sx8_dec_add_rmsnorm", P(z["resid"]), P(z["d"]), None, P(ly.in_norm), P(z["h"]),
+                        1, cfg["hidden"], eps, st)
+            self._gemv(ly.q, z["h"], z["q"], st)
+            self._gemv(ly.k, z["h"], z["k"], st)
+            self._gemv(ly.v, z["h"], z["v"], st)
+            _L.call("sx8_dec_qk_rope_cache", P(z["q"]), P(z["k"]), P(z["v"]), P(ly.q_norm), P(ly.k_norm),
+                    P(self.cos), P(self.sin), P(pos), P(z["qh"]), P(self.k_cache[li]),
+                    P(self.v_cache[li]), nh, nk, hd, L, eps, st)
+            _L.call("sx8_dec_attn", P(z["qh"]), P(self.k_cache[li]), P(self.v_cache[li]), P(pos),
+                    P(z["a"]), nh, nk, hd, L, 1.0 / math.sqrt(hd), st)
+            self._gemv(ly.o, z["a"], z["o"], st)
+            _L.call("sx8_dec_add_rmsnorm", P(z["resid"]), P(z["o"]), None, P(ly.post_norm), P(z["h"]), 1,
+                    cfg["hidden"], eps, st)
+            self._gemv(ly.gate, z["h"], z["g"], st)
+            self._gemv(ly.up, z["h"], z["u"], st)
+            _L.call("sx8_dec_silu_mul", P(z["g"]), P(z["u"]), P(z["m"]), cfg["inter"], st)
+            self._gemv(ly.down, z["m"], z["d"], st)
+        _L.call("sx8_dec_add_rmsnorm", P(z["resid"]), P(z["d"]), None, P(self.final_norm), P(z["h"]), 1,
+                cfg["hidden"], eps, st)
+        self._gemv(self.head, z["h"], z["logits"], st)
+        _L.call("sx8_dec_argmax_advance", P(z["logits"]), cfg["vocab"], P(tok), P(pos), st)
+        return tok
+
     # ---------------------------------------------------------------- generation
     @torch.no_grad()
-    def generate(self, ids, n_new, use_graph=True):
+    def generate(self, ids, n_new, use_graph=True, fused=True):
         """Prefill `ids`, then greedily decode `n_new` tokens.  Returns (tokens (n_new,)
         on the device, prefill seconds, decode seconds)."""
         dev = self.device
@@ -201,19 +270,20 @@ class SX8Decoder(nn.Module):
         pos = torch.full((1,), T, dtype=torch.int64, device=dev)
         out = torch.empty(n_new, dtype=torch.int64, device=dev)
         out[0] = first[0]
+        step = self.decode_step_fused if fused else self.decode_step
         if use_graph:
             # warm-up (pools, workspaces) on a side stream, then capture one step
             saved = (tok.clone(), pos.clone())
             s = torch.cuda.Stream()
             s.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(s):
-                self.decode_step(tok, pos)
+                step(tok, pos)
             torch.cuda.current_stream().wait_stream(s)
             tok.copy_(saved[0])
             pos.copy_(saved[1])
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                self.decode_step(tok, pos)
+                step(tok, pos)
             tok.copy_(saved[0])
             pos.copy_(saved[1])
             torch.cuda.synchronize()
@@ -227,7 +297,7 @@ class SX8Decoder(nn.Module):
             torch.cuda.synchronize()
             t1 = time.perf_counter()
             for i in range(1, n_new):
-                self.decode_step(tok, pos)
+                step(tok, pos)
                 out[i:i + 1].copy_(tok)
             torch.cuda.synchronize()
             t_decode = time.perf_counter() - t1

@@ -1,18 +1,19 @@
 """CPU-side checks of the C ABI: the library loads, exports every symbol that
-include/sx8_hip.h declares, and rejects bad arguments on the host (before any HIP
+include/*.h declare, and rejects bad arguments on the host (before any HIP
 call) with an error code and a message.  No kernel is launched here."""
 import ctypes
+import glob
 import os
 import re
 
 import pytest
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(REPO, "include", "sx8_hip.h")
+HEADERS = sorted(glob.glob(os.path.join(REPO, "include", "*.h")))
 
 
 def _declared():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     return sorted(set(re.findall(r"^\s*(?:int32_t|int64_t|const char\*)\s+(sx8_\w+)\s*\(", text, re.M)))
 
 

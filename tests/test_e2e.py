@@ -62,13 +62,15 @@ def test_e2e_prefill_decode_graph(hiplib, cuda):
     first = dec.prefill(ids)
     ref_last = ref[-1]
     assert ref_last[first[0]] >= ref_last.max() - 2e-2 * ref_last.abs().max()
-    # decode: graph replay and eager steps give the same tokens
-    out_g, _, _ = dec.generate(ids, 6, use_graph=True)
-    out_e, _, _ = dec.generate(ids, 6, use_graph=False)
-    assert torch.equal(out_g.cpu(), out_e.cpu())
-    # each decoded token is (near-)argmax of the reference over the extended sequence
-    seq = torch.cat([ids, out_e[:-1]])
-    ref_all = _ref_forward(dec, seq, W)
-    for i in range(6):
-        row = ref_all[len(ids) - 1 + i]
-        assert row[out_e[i]] >= row.max() - 2e-2 * row.abs().max(), i
+    # decode: graph replay and eager steps give the same tokens, for the torch-op step
+    # and for the fused step (HIP decoder ops); each token is (near-)argmax of the fp32
+    # reference over the sequence it extends
+    for fused in (False, True):
+        out_g, _, _ = dec.generate(ids, 6, use_graph=True, fused=fused)
+        out_e, _, _ = dec.generate(ids, 6, use_graph=False, fused=fused)
+        assert torch.equal(out_g.cpu(), out_e.cpu()), fused
+        seq = torch.cat([ids, out_e[:-1]])
+        ref_all = _ref_forward(dec, seq, W)
+        for i in range(6):
+            row = ref_all[len(ids) - 1 + i]
+            assert row[out_e[i]] >= row.max() - 2e-2 * row.abs().max(), (fused, i)
