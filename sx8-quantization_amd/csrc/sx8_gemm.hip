@@ -22,6 +22,7 @@
 //     split K into ranges of whole 4-block groups and add the partials in a fixed order.
 #include <algorithm>
 
+#include "sx8_buffer.h"
 #include "sx8_device.h"
 #include "sx8_host.h"
 
@@ -97,13 +98,6 @@ struct GemmSmem {
 // Buffer resources and per-lane byte offsets for the main loop's loads.  The K block goes
 // into the scalar offset, so the loop does no per-lane address arithmetic; a lane whose
 // vector offset lies past the end of a buffer (X rows >= M) reads zero.
-typedef __amdgpu_buffer_rsrc_t sx8_rsrc;
-constexpr int kRsrcFlags = 0x00020000;   // raw 32-bit buffer (gfx9 resource word 3)
-
-__device__ __forceinline__ sx8_rsrc make_rsrc(const void* p, int64_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
-                                             (int)min(bytes, (int64_t)0x7FFFFFFF), kRsrcFlags);
-}
 
 template <int MF>
 struct LoopSrc {

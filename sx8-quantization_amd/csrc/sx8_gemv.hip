@@ -19,8 +19,12 @@
 //     rlo * Sx + step * (sum x lv) with sum x lv from fp16 "splices" and
 //     v_dot2_f32_f16 (see block_dot); PCA is applied per block through Z
 //     (docs/SX8_FLASH_V4_3_SPEC.md:49-61).
-//   * the K loop is software-pipelined (rotating record buffers, unconditional clamped
-//     loads) and panels are renumbered per XCD (see k_gemv_panel).
+//   * the K loop is software-pipelined (rotating record buffers, unconditional buffer
+//     loads that read zeros past the end) and panels are renumbered per XCD (see
+//     k_gemv_panel).
+#include <algorithm>
+
+#include "sx8_buffer.h"
 #include "sx8_device.h"
 #include "sx8_host.h"
 
@@ -35,30 +39,31 @@ struct KbInfo {
 };
 static_assert(sizeof(KbInfo) == 112, "KbInfo layout");
 
-// Constant part of the fp16 splices of block_dot for weight pair i: nibble splice
-// (4096 for pairs 0, 2; 256 for pairs 1, 3) + quad splice (16, 64, 256, 1024).
-__device__ constexpr float kSpliceBias[4] = {4.f * 1024.f + 16.f, 4.f * 64.f + 64.f,
-                                             4.f * 1024.f + 256.f, 4.f * 64.f + 1024.f};
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(sx8_half2, a),
+                                  __builtin_bit_cast(sx8_half2, b), c, false);
+}
 
-// x pairs, sub-block sums and splice biases of one (kb, sb) from its 8 x values.
+// Negated constant parts of block_dot's fp16 splices for weight pair i, as fp16 pairs:
+// nibble splice (4096 for pairs 0, 2; 256 for pairs 1, 3) + quad splice (16, 64, 256,
+// 1024), i.e. -4112, -320, -4352, -1280 (all exact in fp16).
+constexpr uint32_t kNegSplice[4] = {0xEC04EC04u, 0xDD00DD00u, 0xEC40EC40u, 0xE500E500u};
+constexpr uint32_t kOnePair = 0x3C003C00u;   // (1.0, 1.0)
+
+// x pairs, sub-block sum and splice bias of one (kb, sb) from its 8 x values (fp16 pairs
+// (x0,x1) (x2,x3) (x4,x5) (x6,x7) in xv): pair i = (x_i, x_{i+4}) by byte permutes, the
+// sum and the bias -sum_i (x_i + x_{i+4}) * splice_i as v_dot2_f32_f16 chains (each
+// product is exact in fp32).
 __device__ __forceinline__ void fill_x_side(KbInfo& out, int sb, const uint4 xv) {
-#pragma clang fp contract(off)
-    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-    float xf[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xf[i] = sx8_h2f(xw[i >> 1] >> (16 * (i & 1)));
-    float s = 0.f, b = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s += xf[i];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t a = (xw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;            // x[i]
-        const uint32_t c = (xw[(i + 4) >> 1] >> (16 * (i & 1))) & 0xFFFFu;      // x[i+4]
-        out.xp[4 * sb + i] = a | (c << 16);
-        b += (xf[i] + xf[i + 4]) * kSpliceBias[i];
-    }
-    out.sx[sb] = s;
-    out.nbias[sb] = -b;
+    const uint32_t p0 = __builtin_amdgcn_perm(xv.z, xv.x, 0x05040100u);
+    const uint32_t p1 = __builtin_amdgcn_perm(xv.z, xv.x, 0x07060302u);
+    const uint32_t p2 = __builtin_amdgcn_perm(xv.w, xv.y, 0x05040100u);
+    const uint32_t p3 = __builtin_amdgcn_perm(xv.w, xv.y, 0x07060302u);
+    *reinterpret_cast<uint4*>(out.xp + 4 * sb) = make_uint4(p0, p1, p2, p3);
+    out.sx[sb] = dot2(xv.w, kOnePair, dot2(xv.z, kOnePair, dot2(xv.y, kOnePair,
+                                                                 dot2(xv.x, kOnePair, 0.f))));
+    out.nbias[sb] = dot2(p3, kNegSplice[3], dot2(p2, kNegSplice[2], dot2(p1, kNegSplice[1],
+                                                                       dot2(p0, kNegSplice[0], 0.f))));
 }
 
 constexpr int kPanelThreads = 512;
@@ -198,11 +203,6 @@ __global__ __launch_bounds__(256) void k_kbinfo(const uint16_t* __restrict__ X,
     else if (t < 6) out.pad[t - 4] = 0.f;
 }
 
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(sx8_half2, a),
-                                  __builtin_bit_cast(sx8_half2, b), c, false);
-}
-
 // Loop-invariant masks and byte selectors held in VGPRs: on gfx9 a VOP3 instruction
 // takes at most one scalar operand, so with the fp16 constants in SGPRs each splice
 // below is a single v_and_or_b32 and each quad spread a single v_perm_b32.
@@ -222,26 +222,26 @@ __device__ __forceinline__ SpliceK splice_consts() {
 // 16 hi-nibble bytes (a) and the 8 lo-quad bytes (b).
 struct BlockRec {
     uint32_t lohi, cc;
+    unsigned short cc16;   // 6-byte headers: cc as loaded, widened at its first use
     uint4 a;
     uint2 b;
 };
 
-typedef uint4 sx8_uint4_a8 __attribute__((aligned(8)));
-
+// Records of block `bid` through buffer loads (header at bid * HB, levels at bid * 24);
+// an offset past the end of a buffer reads zeros and moves no data.  The 6-byte header
+// is read as a dword (possibly 2-byte aligned; buffer loads allow it) and a short.
 template <int HB>
-__device__ __forceinline__ void load_rec(BlockRec& o, const uint8_t* __restrict__ hdr,
-                                         const uint8_t* __restrict__ levels, int64_t bid) {
+__device__ __forceinline__ void load_rec(BlockRec& o, sx8_rsrc hdr, sx8_rsrc lv, uint32_t bid) {
     if constexpr (HB == 8) {
-        const uint2 h = *reinterpret_cast<const uint2*>(hdr + bid * 8);
+        const uint2 h = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(hdr, bid * 8, 0, 0));
         o.lohi = h.x;
         o.cc = h.y;
     } else {
-        const uint16_t* h = reinterpret_cast<const uint16_t*>(hdr + bid * 6);
-        o.lohi = h[0] | ((uint32_t)h[1] << 16);
-        o.cc = h[2];
+        o.lohi = __builtin_amdgcn_raw_buffer_load_b32(hdr, bid * 6, 0, 0);
+        o.cc16 = __builtin_amdgcn_raw_buffer_load_b16(hdr, bid * 6 + 4, 0, 0);
     }
-    o.a = *reinterpret_cast<const sx8_uint4_a8*>(levels + bid * 24);
-    o.b = *reinterpret_cast<const uint2*>(levels + bid * 24 + 16);
+    o.a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(lv, bid * 24, 0, 0));
+    o.b = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(lv, bid * 24 + 16, 0, 0));
 }
 
 // fp32 contribution of one block (one column, one kb) to its output: PCA through Z,
@@ -300,9 +300,10 @@ __device__ __forceinline__ float block_dot(const BlockRec& o, const KbInfo& ki, 
     return __builtin_fmaf(m, T, acc);
 }
 
-// Table entries built inside the GEMV work-group: four threads per kb, thread q doing
-// the x side of sub-block q and a quarter of both Z products (summed over the four
-// threads with two xor shuffles; this Z is only used internally).
+// Table entries built inside the GEMV work-group: four threads per kb, thread q holding
+// sub-block q's 8 x values and the matching 8 + 8 basis values.  Z is a quarter dot per
+// thread summed over the four threads with two xor shuffles (this Z is only used
+// internally; the combined entry point's Z comes from k_kbinfo).
 struct TabIn {
     uint4 x;
     float4 b0[2], b1[2];
@@ -327,9 +328,11 @@ __device__ __forceinline__ void tab_load(TabIn& t, const uint16_t* __restrict__ 
     }
 }
 
+// Writes entry kb, or the spare entry past the table when !ok: no branch, so the compiler
+// has no conditional block to sink the table loads into (below the weight records).
 template <int kMode>
-__device__ __forceinline__ void tab_store(KbInfo* info, const TabIn& t, int kb, int q, bool ok) {
-#pragma clang fp contract(off)
+__device__ __forceinline__ void tab_store(KbInfo* info, const TabIn& t, int kb, int q, bool ok,
+                                          int n_cb) {
     float z = t.s;
     if constexpr (kMode == 1) {
         const uint32_t xw[4] = {t.x.x, t.x.y, t.x.z, t.x.w};
@@ -339,82 +342,111 @@ __device__ __forceinline__ void tab_store(KbInfo* info, const TabIn& t, int kb, 
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float xf = sx8_h2f(xw[i >> 1] >> (16 * (i & 1)));
-            z0 += xf * b0[i];
-            z1 += xf * b1[i];
+            z0 = __builtin_fmaf(xf, b0[i], z0);
+            z1 = __builtin_fmaf(xf, b1[i], z1);
         }
         z0 += __shfl_xor(z0, 1);
         z1 += __shfl_xor(z1, 1);
         z0 += __shfl_xor(z0, 2);
         z1 += __shfl_xor(z1, 2);
-        z = t.s * (q == 0 ? z0 : z1);
+        z = t.s * ((q & 1) == 0 ? z0 : z1);     // t.s is scale (q & 1)
     }
-    if (!ok) return;
-    fill_x_side(info[kb], q, t.x);
-    if (q < 2) info[kb].z[q] = z;
+    KbInfo& e = info[ok ? kb : n_cb];
+    fill_x_side(e, q, t.x);
+    e.z[q & 1] = z;      // q = 2, 3 write the same values as q = 0, 1
 }
 
-// M = 1 GEMV over column panels.  A 512-thread work-group owns CT = 2^ct_log2
-// consecutive columns over the whole K: lane (c, j) = (column c, K slice j), c fastest,
-// so for each kb the CT lanes of a slice read CT consecutive records, and slice j walks
-// kb = j + r S (S = 512 / CT) for r < R = ceil(n_cb / S).  Slices meet in LDS and are
-// summed in a fixed order: nothing leaves a work-group before the final store, so
-// there are no device-scope fences or atomics and results are deterministic.
+// Table passes whose inputs are loaded before the weight records (the rest, for
+// n_cb > kTabPasses * 128, load after them).
+constexpr int kTabPassesShort = 1;   // n_cb <= 128
+constexpr int kTabPassesLong = 3;    // n_cb <= 384
+
+// M = 1 GEMV over column panels.  A 512-thread work-group owns CT consecutive columns
+// over the whole K: lane tid = (slice j = tid / CT, column c = tid % CT), so for each kb
+// the CT lanes of a slice read CT consecutive records, and slice j walks kb = j + r S
+// (S = 512 / CT slices, rounds r < R = ceil(n_cb / S)); the 512 - S CT leftover lanes
+// only take part in the table build and the reduction.  The host picks CT so that the
+// grid is about one work-group per CU.  Slices meet in LDS and are summed in a fixed
+// order: nothing leaves a work-group before the final store, so there are no
+// device-scope fences or atomics and results are deterministic.
 //
-// Latency schedule: the table inputs go out first, then the records of rounds 0 .. D
-// (D + 1 rotating buffers), then the table is built while they stream in.  In the main
-// loop the buffer just consumed is refilled with round r + D + 1, so D + 1 rounds are
-// in flight while one is decoded.  Every load is unconditional (indices clamped,
-// contributions past the end masked): the loop body is straight-line code, which keeps
-// the compiler's memory-wait counts exact, and scheduling barriers keep each refill
-// ahead of the decode that follows it.
+// Latency schedule: the table inputs go out first, then the records of the first NR
+// rounds, then the table is built while they stream in.  The buffers form a ring: the
+// one just decoded is refilled with the round NR ahead.  Loads are unconditional buffer
+// loads; rounds and slices past
+// the end of K have offsets past the end of the buffers and read zeros without memory
+// traffic, and their contributions are masked, so the decode loop is straight-line code
+// (exact memory-wait counts) with scheduling barriers keeping each refill ahead of the
+// decode after it.
 //
 // kMode: 0 = copy the table k_kbinfo wrote into LDS; 1 = build it computing Z; 2 = build
-// it with Z from Zin; 3 = read k_kbinfo's table from global memory (n_cb > kLdsMaxKb).  Work-groups go to the 8 XCDs round-robin by block index; panels
-// are renumbered so each XCD gets a contiguous column range and neighbouring panels
-// share their header cache lines in one L2.
-template <int HB, int kMode, int D>
+// it with Z from Zin; 3 = read k_kbinfo's table from global memory (n_cb > kLdsMaxKb).
+// Work-groups go to the 8 XCDs round-robin by block index; panels are renumbered so each
+// XCD gets a contiguous column range and neighbouring panels share cache lines in one L2.
+template <int HB, int kMode, int NR, int TP>
 __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ hdr,
     const uint8_t* __restrict__ levels, const float* __restrict__ basis,
     const float* __restrict__ scales, const float* __restrict__ Zin,
-    const KbInfo* __restrict__ table, float* __restrict__ Y, int N, int n_cb, int ct_log2) {
+    const KbInfo* __restrict__ table, float* __restrict__ Y, int N, int n_cb, int CT, int S,
+    int R) {
     extern __shared__ __align__(16) unsigned char smem[];
-    float* red = reinterpret_cast<float*>(smem);
-    KbInfo* info = reinterpret_cast<KbInfo*>(smem + sizeof(float) * kPanelThreads);
+    float* red = reinterpret_cast<float*>(smem);                 // 2 x 512 floats
+    KbInfo* info = reinterpret_cast<KbInfo*>(smem + sizeof(float) * 2 * kPanelThreads);
     const int tid = threadIdx.x;
-    const int CT = 1 << ct_log2;
-    const int S = kPanelThreads >> ct_log2;
-    const int c = tid & (CT - 1);
-    const int j = tid >> ct_log2;
+    const int j0 = tid / CT;
+    const int c = tid - j0 * CT;
     const int G = gridDim.x, xcd = blockIdx.x & 7;
     int panel = blockIdx.x >> 3;
     for (int y = 0; y < xcd; ++y) panel += (G - y + 7) >> 3;
     const int n = panel * CT + c;
-    const bool valid = n < N;
-    const int64_t nn = valid ? n : N - 1;
-    const int R = (n_cb + S - 1) / S;
-    auto kbc = [&](int r) { return min(j + r * S, n_cb - 1); };
-    auto bid = [&](int r) { return (int64_t)kbc(r) * N + nn; };
+    const bool col_ok = n < N;
+    const uint32_t nn = (uint32_t)min(n, N - 1);
+    const bool lane_ok = j0 < S;
+    const int j = lane_ok ? j0 : n_cb;           // leftover lanes: past the end of K
+    const uint32_t n_blk = (uint32_t)n_cb * (uint32_t)N;
+    const sx8_rsrc rh = make_rsrc(hdr, (int64_t)n_blk * HB);
+    const sx8_rsrc rl = make_rsrc(levels, (int64_t)n_blk * 24);
+    // block index of round r: (j + r S) N + nn < (n_cb + (NR + 1) S) N < 2^31 / 24
+    // (checked by the host); leftover lanes stay at n_blk, the first block past the end
+    const uint32_t bid0 = lane_ok ? (uint32_t)j * (uint32_t)N + nn : n_blk;
+    const uint32_t dbid = lane_ok ? (uint32_t)S * (uint32_t)N : 0u;
+    auto load = [&](BlockRec& o, int r) { load_rec<HB>(o, rh, rl, bid0 + (uint32_t)r * dbid); };
 
     const int n_units = n_cb * 4;
-    TabIn tin;
+    TabIn tin[TP];
     if constexpr (kMode == 1 || kMode == 2) {
-        const int u = min(tid, n_units - 1);
-        tab_load<kMode>(tin, X, basis, scales, Zin, u >> 2, u & 3);
-    }
-    BlockRec buf[D + 1];
 #pragma unroll
-    for (int i = 0; i <= D; ++i) load_rec<HB>(buf[i], hdr, levels, bid(i));
+        for (int p = 0; p < TP; ++p) {
+            const int u = min(p * kPanelThreads + tid, n_units - 1);
+            tab_load<kMode>(tin[p], X, basis, scales, Zin, u >> 2, u & 3);
+        }
+    }
+    // issue order = wait order (the memory counter retires loads in order): table
+    // inputs, then round 0, 1, ...  (the clobber keeps the compiler from sinking a
+    // table load below the record loads, which would make the table wait for them)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    BlockRec buf[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        load(buf[i], i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     if constexpr (kMode == 0) {
         const uint4* src = reinterpret_cast<const uint4*>(table);
         uint4* dst = reinterpret_cast<uint4*>(info);
         for (int i = tid; i < n_cb * 7; i += kPanelThreads) dst[i] = src[i];
     } else if constexpr (kMode == 1 || kMode == 2) {
-        tab_store<kMode>(info, tin, min(tid, n_units - 1) >> 2, tid & 3, tid < n_units);
-        for (int u0 = kPanelThreads; u0 < n_units; u0 += kPanelThreads) {
+#pragma unroll
+        for (int p = 0; p < TP; ++p) {
+            const int u = p * kPanelThreads + tid;
+            tab_store<kMode>(info, tin[p], min(u, n_units - 1) >> 2, u & 3, u < n_units, n_cb);
+        }
+        for (int u0 = TP * kPanelThreads; u0 < n_units; u0 += kPanelThreads) {
             const int u = min(u0 + tid, n_units - 1);
-            tab_load<kMode>(tin, X, basis, scales, Zin, u >> 2, u & 3);
-            tab_store<kMode>(info, tin, u >> 2, u & 3, u0 + tid < n_units);
+            tab_load<kMode>(tin[0], X, basis, scales, Zin, u >> 2, u & 3);
+            tab_store<kMode>(info, tin[0], u >> 2, u & 3, u0 + tid < n_units, n_cb);
         }
     }
     __syncthreads();
@@ -422,59 +454,97 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     const KbInfo* ti = kMode == 3 ? table : info;
     const SpliceK sk = splice_consts();
     float acc = 0.f;
-    auto step = [&](const BlockRec& o, int r) {
-        const float v = block_dot(o, ti[kbc(r)], sk);
-        acc += (j + r * S < n_cb) ? v : 0.f;
+    auto step = [&](const BlockRec& rec, int r) {
+        // pin the record's first use here: nothing derived from it may be hoisted
+        // above this point (that would wait for the loads of later rounds)
+        BlockRec o = rec;
+        if constexpr (HB == 8) {
+            asm volatile("" : "+v"(o.lohi), "+v"(o.cc));
+        } else {
+            asm volatile("" : "+v"(o.lohi), "+v"(o.cc16));
+            o.cc = o.cc16;
+        }
+        asm volatile("" : "+v"(o.a.x), "+v"(o.a.y), "+v"(o.a.z), "+v"(o.a.w), "+v"(o.b.x), "+v"(o.b.y));
+        const int kb = j + r * S;
+        const float v = block_dot(o, ti[min(kb, n_cb - 1)], sk);
+        acc += (col_ok && kb < n_cb) ? v : 0.f;
     };
     int r = 0;
-    for (; r + D < R; r += D + 1) {
+    for (; r + NR < R; r += NR) {
 #pragma unroll
-        for (int i = 0; i <= D; ++i) {
+        for (int i = 0; i < NR; ++i) {
             step(buf[i], r + i);
             __builtin_amdgcn_sched_barrier(0);
-            load_rec<HB>(buf[i], hdr, levels, bid(r + i + D + 1));
+            load(buf[i], r + NR + i);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
 #pragma unroll
-    for (int i = 0; i < D; ++i)
+    for (int i = 0; i < NR; ++i)
         if (r + i < R) step(buf[i], r + i);
 
-    // slices -> columns: xor tree over the slices inside each wave (lanes c, c + CT,
-    // ...), then the 8 wave sums in wave order; fixed order, so deterministic
-    for (int off = CT; off < 64; off <<= 1) acc += __shfl_xor(acc, off);
-    const int wave = tid >> 6;
-    if ((tid & 63) < CT) red[wave * CT + c] = acc;
+    // slices -> columns in a fixed order: thread t < 8 CT sums slices g, g + 8, ... of
+    // column t % CT (g = t / CT), then thread c < CT sums the 8 partials of column c
+    red[tid] = acc;
     __syncthreads();
-    if (tid < CT && valid) {
+    if (tid < 8 * CT) {
+        float t = 0.f;
+        for (int s = j0; s < S; s += 8) t += red[s * CT + c];
+        red[kPanelThreads + tid] = t;
+    }
+    __syncthreads();
+    if (tid < CT && col_ok) {
         float t = 0.f;
 #pragma unroll
-        for (int w = 0; w < kPanelThreads / 64; ++w) t += red[w * CT + tid];
+        for (int g = 0; g < 8; ++g) t += red[kPanelThreads + g * CT + tid];
         Y[n] = t;
     }
 }
 
-// Panel width: 16 columns (a slice reads 384 contiguous level bytes, three cache lines),
-// 32 when that still leaves >= 256 work-groups and the K loop is short, 8 when 16 would
-// leave fewer than 128 work-groups.
-inline int panel_ct_log2(int N, int n_cb) {
-    const int g16 = (N + 15) / 16;
-    if (g16 < 128) return N >= 1024 ? 3 : 2;
-    if ((N + 31) / 32 >= 256 && n_cb <= 96) return 5;
-    return 4;
+// Panel geometry: CT = ceil(N / 256) columns (at most 64) gives about one work-group per
+// CU for every layer shape.  Two record buffers: deeper prefetch measured slower on
+// MI355X (the loop already streams near the HBM rate; extra rounds only lengthen the
+// prologue, which is where a launch loses most of its time).
+struct PanelPlan {
+    int CT, S, R, NR, TP;
+    unsigned grid;
+};
+
+inline PanelPlan plan_panels(int N, int n_cb) {
+    PanelPlan p;
+    p.CT = std::max(1, std::min(64, (N + 255) / 256));
+    p.S = kPanelThreads / p.CT;
+    p.R = (n_cb + p.S - 1) / p.S;
+    p.NR = 2;
+    p.TP = n_cb <= 128 * kTabPassesShort ? kTabPassesShort : kTabPassesLong;
+    p.grid = (unsigned)((N + p.CT - 1) / p.CT);
+    return p;
+}
+
+template <int HB, int kMode, int TP>
+void launch_panel_tp(const PanelPlan& p, size_t smem, hipStream_t st, const uint16_t* X,
+                     const uint8_t* hdr, const uint8_t* levels, const float* basis,
+                     const float* scales, const float* Zin, const KbInfo* table, float* Y, int N,
+                     int n_cb) {
+    const dim3 grid(p.grid), block(kPanelThreads);
+    hipLaunchKernelGGL((k_gemv_panel<HB, kMode, 2, TP>), grid, block, smem, st, X, hdr, levels,
+                       basis, scales, Zin, table, Y, N, n_cb, p.CT, p.S, p.R);
 }
 
 template <int HB, int kMode>
-void launch_panel(int D, dim3 grid, size_t smem, hipStream_t st, const uint16_t* X,
+void launch_panel(const PanelPlan& p, size_t smem, hipStream_t st, const uint16_t* X,
                   const uint8_t* hdr, const uint8_t* levels, const float* basis,
                   const float* scales, const float* Zin, const KbInfo* table, float* Y, int N,
-                  int n_cb, int lg) {
-    if (D == 2)
-        hipLaunchKernelGGL((k_gemv_panel<HB, kMode, 2>), grid, dim3(kPanelThreads), smem, st, X,
-                           hdr, levels, basis, scales, Zin, table, Y, N, n_cb, lg);
-    else
-        hipLaunchKernelGGL((k_gemv_panel<HB, kMode, 1>), grid, dim3(kPanelThreads), smem, st, X,
-                           hdr, levels, basis, scales, Zin, table, Y, N, n_cb, lg);
+                  int n_cb) {
+    if constexpr (kMode == 1 || kMode == 2) {
+        if (p.TP == kTabPassesLong) {
+            launch_panel_tp<HB, kMode, kTabPassesLong>(p, smem, st, X, hdr, levels, basis,
+                                                       scales, Zin, table, Y, N, n_cb);
+            return;
+        }
+    }
+    launch_panel_tp<HB, kMode, kTabPassesShort>(p, smem, st, X, hdr, levels, basis, scales, Zin,
+                                                table, Y, N, n_cb);
 }
 
 template <int HB>
@@ -482,20 +552,19 @@ int32_t launch_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels
                     const float* basis, const float* scales, const float* Zin, float* Zout,
                     int N, int n_cb, float* Y, KbInfo* table, hipStream_t st) {
     using namespace sx8;
-    const int lg = panel_ct_log2(N, n_cb);
-    const int S = kPanelThreads >> lg;
-    const int R = (n_cb + S - 1) / S;
-    const int D = R >= 6 ? 2 : 1;
-    const dim3 grid((N + (1 << lg) - 1) >> lg);
+    const PanelPlan p = plan_panels(N, n_cb);
+    // 32-bit buffer offsets: every block index a lane forms stays below 2^31 / 24
+    if (((int64_t)n_cb + (int64_t)(p.NR + 1) * p.S) * N * 24 >= ((int64_t)1 << 31))
+        return fail(SX8_ERR_UNSUPPORTED, "sx8_gemv: %lld x %lld blocks exceed 32-bit offsets",
+                    (long long)N, (long long)n_cb);
     const bool lds = n_cb <= kLdsMaxKb;
-    const size_t smem = sizeof(float) * kPanelThreads + (lds ? sizeof(KbInfo) * (size_t)n_cb : 0);
+    // table: n_cb entries + one spare entry for the build's idle threads
+    const size_t smem = sizeof(float) * 2 * kPanelThreads + (lds ? sizeof(KbInfo) * (size_t)(n_cb + 1) : 0);
     if (!Zout && lds) {   // single launch: the table is built inside every work-group
         if (Zin)
-            launch_panel<HB, 2>(D, grid, smem, st, X, hdr, levels, basis, scales, Zin, table, Y,
-                                N, n_cb, lg);
+            launch_panel<HB, 2>(p, smem, st, X, hdr, levels, basis, scales, Zin, table, Y, N, n_cb);
         else
-            launch_panel<HB, 1>(D, grid, smem, st, X, hdr, levels, basis, scales, Zin, table, Y,
-                                N, n_cb, lg);
+            launch_panel<HB, 1>(p, smem, st, X, hdr, levels, basis, scales, Zin, table, Y, N, n_cb);
         return check_launch("sx8_gemv");
     }
     const dim3 tgrid((n_cb + 7) / 8);
@@ -506,11 +575,9 @@ int32_t launch_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels
         hipLaunchKernelGGL(k_kbinfo<false>, tgrid, dim3(256), 0, st, X, basis, scales, Zin, Zout,
                            n_cb, table);
     if (lds)
-        launch_panel<HB, 0>(D, grid, smem, st, X, hdr, levels, basis, scales, Zin, table, Y, N,
-                            n_cb, lg);
+        launch_panel<HB, 0>(p, smem, st, X, hdr, levels, basis, scales, Zin, table, Y, N, n_cb);
     else
-        launch_panel<HB, 3>(D, grid, smem, st, X, hdr, levels, basis, scales, Zin, table, Y, N,
-                            n_cb, lg);
+        launch_panel<HB, 3>(p, smem, st, X, hdr, levels, basis, scales, Zin, table, Y, N, n_cb);
     return check_launch("sx8_gemv");
 }
 

@@ -139,7 +139,10 @@ def test_embed_ragged_k(hiplib, oracle, cuda):
 
 GEMV_CASES = [("cpu_config", 2560, 2560, 0)] + [
     (k, n, kk, 1000 + i) for i, (k, (n, kk)) in enumerate(SHAPES_4B.items())] + [
-    ("odd_N", 1000, 2560, 7), ("tiny", 65, 96, 8), ("ragged_K", 200, 80, 9)]
+    ("odd_N", 1000, 2560, 7), ("tiny", 65, 96, 8), ("ragged_K", 200, 80, 9),
+    # n_cb = 512: table inputs beyond the three up-front passes; 64-column panels
+    # with 10 rounds: the record-buffer ring
+    ("long_K", 300, 16384, 10), ("wide_N", 20000, 2560, 11)]
 
 
 @pytest.mark.parametrize("hdr_bytes", [6, 8])
@@ -178,7 +181,7 @@ def test_gemv_within_1e3(hiplib, oracle, cuda, name, N, K, seed, hdr_bytes):
 def test_gemv_deterministic_and_pool(hiplib, cuda):
     import torch
     from sx8_decode1_v3 import decode1_v44, make_tensors_v44
-    qt, bi = _quantized(1024, 2560, 1001, cuda)      # split-K path (few column tiles)
+    qt, bi = _quantized(1024, 2560, 1001, cuda)      # 4-column panels, one round
     t = make_tensors_v44(qt, bi)
     x = _x(1, 2560, 3)[0].to(cuda)
     first = decode1_v44(x, qt, bi, *t)[0].clone()
