@@ -192,8 +192,50 @@ def bench_gemv(torch, L, layer, args):
         for i in range(nL):
             b = 2 + 2 * (s * nL + i)
             per_shape_ms[i] += ev.ms(b, b + 1)
-    ev.close()
     kern_ms = sum(per_shape_ms)
+
+    # the same layer as a decoder step runs it: q/k/v and gate/up share their input and
+    # go out as one launch each (sx8_gemv_group), o and down alone -> 4 launches per step
+    idx = {t["name"]: i for i, t in enumerate(layer)}
+    groups = [["q_proj", "k_proj", "v_proj"], ["o_proj"], ["gate_proj", "up_proj"], ["down_proj"]]
+    gfn = L.lib().sx8_gemv_group
+    gcalls = []
+    for r in range(R):
+        step = []
+        for grp in groups:
+            ii = [idx[n] for n in grp if n in idx]
+            if not ii:
+                continue
+            n = len(ii)
+            P = ctypes.c_void_p * n
+            t0 = layer[ii[0]]
+            step.append((L.ptr(xs[t0["K"]]), n, P(*[copies[r][i][0].data_ptr() for i in ii]),
+                         P(*[copies[r][i][1].data_ptr() for i in ii]), args.hdr_bytes,
+                         P(*[layer[i]["bas"].data_ptr() for i in ii]),
+                         P(*[layer[i]["sca"].data_ptr() for i in ii]), None,
+                         (ctypes.c_int64 * n)(*[layer[i]["N"] for i in ii]), t0["n_cb"],
+                         P(*[ys[i].data_ptr() for i in ii]), st))
+        gcalls.append(step)
+
+    def run_group_step(s):
+        for a in gcalls[s % R]:
+            if gfn(*a) != 0:
+                raise RuntimeError(L.lib().sx8_last_error().decode())
+
+    for s in range(args.warmup):
+        run_group_step(s)
+    torch.cuda.synchronize()
+    gpu_delay(torch, 50)
+    ev.record(0)
+    for s in range(K):
+        run_group_step(s)
+    ev.record(1)
+    torch.cuda.synchronize()
+    g_ms = ev.ms(0, 1)
+    ev.close()
+    grouped = {"launches_per_step": len(gcalls[0]), "ms_per_step": g_ms / K,
+               "gbs": step_bytes * K / (g_ms * 1e-3) / 1e9,
+               "groups": [g for g in groups]}
     out = {
         "ms_per_step": total_ms / K,
         "value_gbs": step_bytes * K / (total_ms * 1e-3) / 1e9,
@@ -207,6 +249,7 @@ def bench_gemv(torch, L, layer, args):
             "gbs": packed_bytes(t["N"], t["K"]) / (per_shape_ms[i] * 1e-3 / K) / 1e9}
             for i, t in enumerate(layer)},
         "step_bytes": step_bytes,
+        "grouped": grouped,
     }
     return out
 
@@ -423,7 +466,7 @@ def main():
             "frac_of_hbm_peak": round(gv.get("value_gbs", 0.0) / HBM_PEAK_GBS, 4),
         },
         "roofline": {
-            "kernel": f"k_gemv_panel<{args.hdr_bytes},1,D> (sx8_gemv)",
+            "kernel": f"k_gemv_panel<{args.hdr_bytes},1,2,TP> (sx8_gemv)",
             "bound": "hbm",
             "achieved": round(gv.get("achieved_gbs", 0.0), 1),
             "peak": HBM_PEAK_GBS,
@@ -435,6 +478,7 @@ def main():
             "bytes_per_launch": gv.get("bytes_per_launch"),
         },
         "cpu_baseline": cpu,
+        "gemv_grouped": gv.get("grouped"),
         "prefill": res.get("prefill"),
         "embed": res.get("embed"),
         "e2e": res.get("e2e"),

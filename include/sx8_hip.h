@@ -90,6 +90,19 @@ int32_t sx8_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels,
                  const float* Z_in, float* Z_out, int64_t N, int64_t n_cb, float* Y,
                  void* workspace, int64_t workspace_bytes, void* stream);
 
+/* GEMVs of n_mats (1..4) v4.4 weights that share X (same K, same hdr_bytes), e.g. the
+ * q/k/v or gate/up projections of a decoder layer, as one launch: Ys[i] (Ns[i],) float32 =
+ * W_i . X.  Per matrix either Z_in[i] (Z_in non-NULL) or bases[i] + scales[i]; arrays are
+ * host arrays of n_mats device pointers.  Each output is what sx8_gemv gives for that
+ * matrix (same decode, same tolerance); one dispatch instead of n_mats, which is most of
+ * an M = 1 GEMV's fixed cost.  No counterpart in the reference, whose decode path runs
+ * one decode1_v44 per projection (cuda/sx8_decode1_v3.cu:197-246). */
+int32_t sx8_gemv_group(const uint16_t* X, int32_t n_mats, const uint8_t* const* hdrs,
+                       const uint8_t* const* levels, int32_t hdr_bytes,
+                       const float* const* bases, const float* const* scales,
+                       const float* const* Z_in, const int64_t* Ns, int64_t n_cb,
+                       float* const* Ys, void* stream);
+
 /* Workspace bytes sx8_gemv needs for n_cb K blocks (112 per block). */
 int64_t sx8_gemv_workspace_bytes(int64_t n_cb);
 

@@ -40,6 +40,7 @@ SIGNATURES = [
     ("sx8_embed_gather", _I32, [_P, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _P, _P]),
     ("sx8_compute_z", _I32, [_P, _I64, _I64, _P, _P, _I64, _P, _P]),
     ("sx8_gemv", _I32, [_P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P]),
+    ("sx8_gemv_group", _I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _I64, _P, _P]),
     ("sx8_gemv_workspace_bytes", _I64, [_I64]),
     ("sx8_gemm_prefill", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P]),
     ("sx8_gemm_prefill_split", _I32,

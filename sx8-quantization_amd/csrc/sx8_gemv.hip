@@ -383,13 +383,27 @@ constexpr int kTabPassesLong = 3;    // n_cb <= 384
 // it with Z from Zin; 3 = read k_kbinfo's table from global memory (n_cb > kLdsMaxKb).
 // Work-groups go to the 8 XCDs round-robin by block index; panels are renumbered so each
 // XCD gets a contiguous column range and neighbouring panels share cache lines in one L2.
+// Weight matrices of one launch: every matrix multiplies the same x (same K); matrix m
+// owns `panels` consecutive panels of the grid.
+constexpr int kMaxGroup = 4;
+struct GemvMat {
+    const uint8_t* hdr;
+    const uint8_t* levels;
+    const float* basis;
+    const float* scales;
+    const float* Zin;
+    float* Y;
+    int N, panels;
+};
+struct GemvGroup {
+    GemvMat m[kMaxGroup];
+    int n_mats;
+};
+
 template <int HB, int kMode, int NR, int TP>
 __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
-    const uint16_t* __restrict__ X, const uint8_t* __restrict__ hdr,
-    const uint8_t* __restrict__ levels, const float* __restrict__ basis,
-    const float* __restrict__ scales, const float* __restrict__ Zin,
-    const KbInfo* __restrict__ table, float* __restrict__ Y, int N, int n_cb, int CT, int S,
-    int R) {
+    const uint16_t* __restrict__ X, const GemvGroup grp, const KbInfo* __restrict__ table,
+    int n_cb, int CT, int S, int R) {
     extern __shared__ __align__(16) unsigned char smem[];
     float* red = reinterpret_cast<float*>(smem);                 // 2 x 512 floats
     KbInfo* info = reinterpret_cast<KbInfo*>(smem + sizeof(float) * 2 * kPanelThreads);
@@ -399,6 +413,15 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     const int G = gridDim.x, xcd = blockIdx.x & 7;
     int panel = blockIdx.x >> 3;
     for (int y = 0; y < xcd; ++y) panel += (G - y + 7) >> 3;
+    int mi = 0;                                  // the matrix this panel belongs to
+    while (mi + 1 < grp.n_mats && panel >= grp.m[mi].panels) panel -= grp.m[mi++].panels;
+    const uint8_t* __restrict__ hdr = grp.m[mi].hdr;
+    const uint8_t* __restrict__ levels = grp.m[mi].levels;
+    const float* __restrict__ basis = grp.m[mi].basis;
+    const float* __restrict__ scales = grp.m[mi].scales;
+    const float* __restrict__ Zin = grp.m[mi].Zin;
+    float* __restrict__ Y = grp.m[mi].Y;
+    const int N = grp.m[mi].N;
     const int n = panel * CT + c;
     const bool col_ok = n < N;
     const uint32_t nn = (uint32_t)min(n, N - 1);
@@ -501,50 +524,57 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     }
 }
 
-// Panel geometry: CT = ceil(N / 256) columns (at most 64) gives about one work-group per
-// CU for every layer shape.  Two record buffers: deeper prefetch measured slower on
-// MI355X (the loop already streams near the HBM rate; extra rounds only lengthen the
-// prologue, which is where a launch loses most of its time).
+// Panel geometry: CT columns per panel (at most 64), from the group's total width:
+// ceil(sum N / 256) gives about one work-group per CU; wider groups take two per CU
+// (co-resident).  Two record buffers: deeper prefetch measured slower on MI355X (the loop
+// already streams near the HBM rate; extra rounds only lengthen the prologue, which is
+// where a launch loses most of its time).
 struct PanelPlan {
-    int CT, S, R, NR, TP;
+    int CT, S, R, TP;
     unsigned grid;
 };
 
-inline PanelPlan plan_panels(int N, int n_cb) {
+inline PanelPlan plan_panels(const int64_t* Ns, int n_mats, int n_cb) {
+    int64_t total = 0;
+    for (int i = 0; i < n_mats; ++i) total += Ns[i];
+    int64_t ct = (total + 255) / 256;
+    if (ct > 64) ct = (total + 511) / 512;
     PanelPlan p;
-    p.CT = std::max(1, std::min(64, (N + 255) / 256));
+    p.CT = (int)std::max<int64_t>(1, std::min<int64_t>(64, ct));
     p.S = kPanelThreads / p.CT;
     p.R = (n_cb + p.S - 1) / p.S;
-    p.NR = 2;
     p.TP = n_cb <= 128 * kTabPassesShort ? kTabPassesShort : kTabPassesLong;
-    p.grid = (unsigned)((N + p.CT - 1) / p.CT);
+    int64_t grid = 0;
+    for (int i = 0; i < n_mats; ++i) grid += (Ns[i] + p.CT - 1) / p.CT;
+    p.grid = (unsigned)grid;
     return p;
 }
 
-template <int HB, int kMode, int TP>
-void launch_panel_tp(const PanelPlan& p, size_t smem, hipStream_t st, const uint16_t* X,
-                     const uint8_t* hdr, const uint8_t* levels, const float* basis,
-                     const float* scales, const float* Zin, const KbInfo* table, float* Y, int N,
-                     int n_cb) {
-    const dim3 grid(p.grid), block(kPanelThreads);
-    hipLaunchKernelGGL((k_gemv_panel<HB, kMode, 2, TP>), grid, block, smem, st, X, hdr, levels,
-                       basis, scales, Zin, table, Y, N, n_cb, p.CT, p.S, p.R);
-}
+constexpr int kRing = 2;   // record buffers per lane
 
 template <int HB, int kMode>
 void launch_panel(const PanelPlan& p, size_t smem, hipStream_t st, const uint16_t* X,
-                  const uint8_t* hdr, const uint8_t* levels, const float* basis,
-                  const float* scales, const float* Zin, const KbInfo* table, float* Y, int N,
-                  int n_cb) {
+                  const GemvGroup& g, const KbInfo* table, int n_cb) {
+    const dim3 grid(p.grid), block(kPanelThreads);
     if constexpr (kMode == 1 || kMode == 2) {
         if (p.TP == kTabPassesLong) {
-            launch_panel_tp<HB, kMode, kTabPassesLong>(p, smem, st, X, hdr, levels, basis,
-                                                       scales, Zin, table, Y, N, n_cb);
+            hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesLong>), grid, block,
+                               smem, st, X, g, table, n_cb, p.CT, p.S, p.R);
             return;
         }
     }
-    launch_panel_tp<HB, kMode, kTabPassesShort>(p, smem, st, X, hdr, levels, basis, scales, Zin,
-                                                table, Y, N, n_cb);
+    hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesShort>), grid, block, smem, st,
+                       X, g, table, n_cb, p.CT, p.S, p.R);
+}
+
+// 32-bit buffer offsets: every block index a lane forms stays below 2^31 / 24.
+inline bool offsets_fit(const PanelPlan& p, int64_t N, int64_t n_cb) {
+    return (n_cb + (int64_t)(kRing + 1) * p.S) * N * 24 < ((int64_t)1 << 31);
+}
+
+inline size_t panel_smem(int n_cb, bool lds) {
+    // table: n_cb entries + one spare entry for the build's idle threads
+    return sizeof(float) * 2 * kPanelThreads + (lds ? sizeof(KbInfo) * (size_t)(n_cb + 1) : 0);
 }
 
 template <int HB>
@@ -552,19 +582,21 @@ int32_t launch_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels
                     const float* basis, const float* scales, const float* Zin, float* Zout,
                     int N, int n_cb, float* Y, KbInfo* table, hipStream_t st) {
     using namespace sx8;
-    const PanelPlan p = plan_panels(N, n_cb);
-    // 32-bit buffer offsets: every block index a lane forms stays below 2^31 / 24
-    if (((int64_t)n_cb + (int64_t)(p.NR + 1) * p.S) * N * 24 >= ((int64_t)1 << 31))
+    const int64_t N64 = N;
+    const PanelPlan p = plan_panels(&N64, 1, n_cb);
+    if (!offsets_fit(p, N, n_cb))
         return fail(SX8_ERR_UNSUPPORTED, "sx8_gemv: %lld x %lld blocks exceed 32-bit offsets",
                     (long long)N, (long long)n_cb);
+    GemvGroup g{};
+    g.n_mats = 1;
+    g.m[0] = GemvMat{hdr, levels, basis, scales, Zin, Y, N, (int)p.grid};
     const bool lds = n_cb <= kLdsMaxKb;
-    // table: n_cb entries + one spare entry for the build's idle threads
-    const size_t smem = sizeof(float) * 2 * kPanelThreads + (lds ? sizeof(KbInfo) * (size_t)(n_cb + 1) : 0);
+    const size_t smem = panel_smem(n_cb, lds);
     if (!Zout && lds) {   // single launch: the table is built inside every work-group
         if (Zin)
-            launch_panel<HB, 2>(p, smem, st, X, hdr, levels, basis, scales, Zin, table, Y, N, n_cb);
+            launch_panel<HB, 2>(p, smem, st, X, g, table, n_cb);
         else
-            launch_panel<HB, 1>(p, smem, st, X, hdr, levels, basis, scales, Zin, table, Y, N, n_cb);
+            launch_panel<HB, 1>(p, smem, st, X, g, table, n_cb);
         return check_launch("sx8_gemv");
     }
     const dim3 tgrid((n_cb + 7) / 8);
@@ -575,10 +607,37 @@ int32_t launch_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels
         hipLaunchKernelGGL(k_kbinfo<false>, tgrid, dim3(256), 0, st, X, basis, scales, Zin, Zout,
                            n_cb, table);
     if (lds)
-        launch_panel<HB, 0>(p, smem, st, X, hdr, levels, basis, scales, Zin, table, Y, N, n_cb);
+        launch_panel<HB, 0>(p, smem, st, X, g, table, n_cb);
     else
-        launch_panel<HB, 3>(p, smem, st, X, hdr, levels, basis, scales, Zin, table, Y, N, n_cb);
+        launch_panel<HB, 3>(p, smem, st, X, g, table, n_cb);
     return check_launch("sx8_gemv");
+}
+
+// One launch over up to kMaxGroup matrices that share x; each work-group builds the table
+// of its own matrix.  Z given (Zin) or computed must be the same for every matrix.
+template <int HB>
+int32_t launch_gemv_group(const uint16_t* X, int n_mats, const uint8_t* const* hdrs,
+                          const uint8_t* const* levels, const float* const* bases,
+                          const float* const* scales, const float* const* Zins,
+                          const int64_t* Ns, int n_cb, float* const* Ys, hipStream_t st) {
+    using namespace sx8;
+    const PanelPlan p = plan_panels(Ns, n_mats, n_cb);
+    GemvGroup g{};
+    g.n_mats = n_mats;
+    for (int i = 0; i < n_mats; ++i) {
+        if (!offsets_fit(p, Ns[i], n_cb))
+            return fail(SX8_ERR_UNSUPPORTED, "sx8_gemv_group: %lld x %lld blocks exceed 32-bit offsets",
+                        (long long)Ns[i], (long long)n_cb);
+        g.m[i] = GemvMat{hdrs[i], levels[i], bases ? bases[i] : nullptr,
+                         scales ? scales[i] : nullptr, Zins ? Zins[i] : nullptr, Ys[i],
+                         (int)Ns[i], (int)((Ns[i] + p.CT - 1) / p.CT)};
+    }
+    const size_t smem = panel_smem(n_cb, true);
+    if (Zins)
+        launch_panel<HB, 2>(p, smem, st, X, g, nullptr, n_cb);
+    else
+        launch_panel<HB, 1>(p, smem, st, X, g, nullptr, n_cb);
+    return check_launch("sx8_gemv_group");
 }
 
 }  // namespace
@@ -653,4 +712,54 @@ extern "C" int32_t sx8_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t
                               table, as_stream(stream));
     return launch_gemv<6>(X, hdr, levels, basis, scales, Z_in, Z_out, (int)N, (int)n_cb, Y, table,
                           as_stream(stream));
+}
+
+extern "C" int32_t sx8_gemv_group(const uint16_t* X, int32_t n_mats, const uint8_t* const* hdrs,
+                                  const uint8_t* const* levels, int32_t hdr_bytes,
+                                  const float* const* bases, const float* const* scales,
+                                  const float* const* Z_in, const int64_t* Ns, int64_t n_cb,
+                                  float* const* Ys, void* stream) {
+    using namespace sx8;
+    if (!X || !hdrs || !levels || !Ns || !Ys) return fail(SX8_ERR_INVALID, "sx8_gemv_group: null pointer");
+    if (n_mats < 1 || n_mats > kMaxGroup)
+        return fail(SX8_ERR_INVALID, "sx8_gemv_group: n_mats must be 1..%d, got %d", kMaxGroup, n_mats);
+    if (!Z_in && (!bases || !scales))
+        return fail(SX8_ERR_INVALID, "sx8_gemv_group: bases/scales required when Z_in is NULL");
+    if (hdr_bytes != 6 && hdr_bytes != 8)
+        return fail(SX8_ERR_INVALID, "sx8_gemv_group: hdr_bytes must be 6 or 8, got %d", hdr_bytes);
+    if (n_cb <= 0 || n_cb > 0x7FFFFFFF / 64 || !aligned(X, 16))
+        return fail(SX8_ERR_INVALID, "sx8_gemv_group: bad n_cb %lld or X not 16-byte aligned",
+                    (long long)n_cb);
+    for (int i = 0; i < n_mats; ++i) {
+        const bool have_z = Z_in ? Z_in[i] != nullptr : (bases[i] && scales[i]);
+        if (!hdrs[i] || !levels[i] || !Ys[i] || !have_z)
+            return fail(SX8_ERR_INVALID, "sx8_gemv_group: null pointer in matrix %d", i);
+        if (Ns[i] <= 0 || Ns[i] > 0x7FFFFFFF / 2)
+            return fail(SX8_ERR_INVALID, "sx8_gemv_group: bad N %lld (matrix %d)", (long long)Ns[i], i);
+        if (!aligned(hdrs[i], hdr_bytes == 8 ? 8 : 2) || !aligned(levels[i], 8) || !aligned(Ys[i], 4) ||
+            (Z_in && !aligned(Z_in[i], 4)) ||
+            (!Z_in && (!aligned(bases[i], 16) || !aligned(scales[i], 4))))
+            return fail(SX8_ERR_INVALID, "sx8_gemv_group: misaligned pointer in matrix %d", i);
+    }
+    const hipStream_t st = as_stream(stream);
+    if (n_cb > kLdsMaxKb) {   // table past LDS: one two-launch GEMV per matrix
+        void* ws = nullptr;
+        const int32_t rc = device_workspace(sx8_gemv_workspace_bytes(n_cb), &ws);
+        if (rc != SX8_OK) return rc;
+        for (int i = 0; i < n_mats; ++i) {
+            const float* b = Z_in ? nullptr : bases[i];
+            const float* sc = Z_in ? nullptr : scales[i];
+            const float* z = Z_in ? Z_in[i] : nullptr;
+            const int32_t r = hdr_bytes == 8
+                ? launch_gemv<8>(X, hdrs[i], levels[i], b, sc, z, nullptr, (int)Ns[i], (int)n_cb, Ys[i],
+                                 reinterpret_cast<KbInfo*>(ws), st)
+                : launch_gemv<6>(X, hdrs[i], levels[i], b, sc, z, nullptr, (int)Ns[i], (int)n_cb, Ys[i],
+                                 reinterpret_cast<KbInfo*>(ws), st);
+            if (r != SX8_OK) return r;
+        }
+        return SX8_OK;
+    }
+    if (hdr_bytes == 8)
+        return launch_gemv_group<8>(X, n_mats, hdrs, levels, bases, scales, Z_in, Ns, (int)n_cb, Ys, st);
+    return launch_gemv_group<6>(X, n_mats, hdrs, levels, bases, scales, Z_in, Ns, (int)n_cb, Ys, st);
 }

@@ -15,6 +15,7 @@ replayed for every generated token.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 import time
 
@@ -205,8 +206,28 @@ class SX8Decoder(nn.Module):
         n_cb_max = max(lin.qt["n_cb"] for ly in self.layers for lin in (ly.q, ly.o, ly.down))
         ws_bytes = int(_L.lib().sx8_gemv_workspace_bytes(max(n_cb_max, self.head.qt["n_cb"])))
         z["ws"] = torch.zeros((ws_bytes + 3) // 4 + 64, **f32)
+        # grouped GEMV arguments (q/k/v and gate/up share their input): ctypes arrays
+        # of device pointers, built once per layer
+        z["groups"] = []
+        for ly in self.layers:
+            z["groups"].append((self._group_args((ly.q, ly.k, ly.v), (z["q"], z["k"], z["v"])),
+                                self._group_args((ly.gate, ly.up), (z["g"], z["u"]))))
         self._fz = z
         return z
+
+    @staticmethod
+    def _group_args(lins, ys):
+        n = len(lins)
+        P = ctypes.c_void_p * n
+        return (n, P(*[l._t44[0].data_ptr() for l in lins]), P(*[l._t44[1].data_ptr() for l in lins]),
+                P(*[l._t44[2].data_ptr() for l in lins]), P(*[l._t44[3].data_ptr() for l in lins]),
+                (ctypes.c_int64 * n)(*[l.out_f for l in lins]), lins[0].qt["n_cb"],
+                P(*[y.data_ptr() for y in ys]))
+
+    @staticmethod
+    def _gemv_group(args, x, st):
+        n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
+        _L.call("sx8_gemv_group", _L.ptr(x), n, hdrs, lvls, 6, bas, sca, None, ns, n_cb, ys, st)
 
     def _gemv(self, lin, x, y, st):
         z = self._fz
@@ -232,9 +253,8 @@ class SX8Decoder(nn.Module):
             else:
                 _L.call("sx8_dec_add_rmsnorm", P(z["resid"]), P(z["d"]), None, P(ly.in_norm), P(z["h"]),
                         1, cfg["hidden"], eps, st)
-            self._gemv(ly.q, z["h"], z["q"], st)
-            self._gemv(ly.k, z["h"], z["k"], st)
-            self._gemv(ly.v, z["h"], z["v"], st)
+            g_qkv, g_gu = z["groups"][li]
+            self._gemv_group(g_qkv, z["h"], st)                     # q, k, v: one launch
             _L.call("sx8_dec_qk_rope_cache", P(z["q"]), P(z["k"]), P(z["v"]), P(ly.q_norm), P(ly.k_norm),
                     P(self.cos), P(self.sin), P(pos), P(z["qh"]), P(self.k_cache[li]),
                     P(self.v_cache[li]), nh, nk, hd, L, eps, st)
@@ -243,8 +263,7 @@ class SX8Decoder(nn.Module):
             self._gemv(ly.o, z["a"], z["o"], st)
             _L.call("sx8_dec_add_rmsnorm", P(z["resid"]), P(z["o"]), None, P(ly.post_norm), P(z["h"]), 1,
                     cfg["hidden"], eps, st)
-            self._gemv(ly.gate, z["h"], z["g"], st)
-            self._gemv(ly.up, z["h"], z["u"], st)
+            self._gemv_group(g_gu, z["h"], st)                      # gate, up: one launch
             _L.call("sx8_dec_silu_mul", P(z["g"]), P(z["u"]), P(z["m"]), cfg["inter"], st)
             self._gemv(ly.down, z["m"], z["d"], st)
         _L.call("sx8_dec_add_rmsnorm", P(z["resid"]), P(z["d"]), None, P(self.final_norm), P(z["h"]), 1,

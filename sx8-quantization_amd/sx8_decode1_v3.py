@@ -3,12 +3,16 @@
 Interface of scripts/sx8_decode1_v3.py (reference): ``_ext()`` (an object with
 ``compute_z44``, ``decode1_v44`` and ``decode1_v44_combined``), ``make_tensors_v44``,
 ``best_split_k``, the ``_BUF``/``_buf`` output pools and ``decode1_v44``.
-The CUDA extension is replaced by libsx8_hip.so (sx8_compute_z / sx8_gemv).  Both GEMV
-forms run two launches: a small kernel builds the per-K-block activation table (and,
-for the combined form, Z with the reference's summation tree, written to the caller's
-Z buffer), then the panel GEMV streams the weights.
+The CUDA extension is replaced by libsx8_hip.so (sx8_compute_z / sx8_gemv).  The GEMV is
+one launch: every work-group builds the per-K-block activation table (x pairs, sums, Z)
+in LDS while its first weight records stream in.  The combined form, which hands Z back
+with the reference's summation tree, puts a small table kernel in front.
+``decode1_v44_group`` (no counterpart upstream) runs the GEMVs of up to four weights that
+share x -- q/k/v, gate/up -- as one launch.
 """
 from __future__ import annotations
+
+import ctypes
 
 import torch
 
@@ -143,3 +147,25 @@ def decode1_v44(X, qt, bases_info, hdr_t=None, lvl_t=None, bas_t=None, sca_t=Non
             _L.ptr(sca_t), None, None, N, n_cb, _L.ptr(Y), _L.ptr(ws), ws.numel() * 4,
             _L.stream(Xc.device))
     return Y, (hdr_t, lvl_t, bas_t, sca_t)
+
+
+def decode1_v44_group(X, tensors, Ns, n_cb, hdr_bytes=6, outs=None):
+    """Y_i = W_i . X for up to four v4.4 weights with the same K, in one launch.
+    tensors: [(hdr_t, lvl_t, bas_t, sca_t), ...]; Ns: output widths; outs: optional
+    float32 (N_i,) outputs.  Returns the list of outputs.  Each Y_i equals what
+    decode1_v44 gives for W_i (same panel decode; only the work split differs)."""
+    n = len(tensors)
+    Xc = _x_for_kernel(X, int(n_cb))
+    if outs is None:
+        outs = [torch.empty(int(N), dtype=torch.float32, device=Xc.device) for N in Ns]
+    P = ctypes.c_void_p * n
+    keep = [(t[2].contiguous(), t[3].contiguous()) for t in tensors]   # alive for the call
+    hdrs = P(*[t[0].data_ptr() for t in tensors])
+    lvls = P(*[t[1].data_ptr() for t in tensors])
+    bas = P(*[k[0].data_ptr() for k in keep])
+    sca = P(*[k[1].data_ptr() for k in keep])
+    ys = P(*[y.data_ptr() for y in outs])
+    ns = (ctypes.c_int64 * n)(*[int(N) for N in Ns])
+    _L.call("sx8_gemv_group", _L.ptr(Xc), n, hdrs, lvls, int(hdr_bytes), bas, sca, None, ns,
+            int(n_cb), ys, _L.stream(Xc.device))
+    return outs

@@ -65,6 +65,36 @@ def test_invalid_arguments_rejected_on_host(hiplib):
     assert L.sx8_gemm_prefill_z(p, 4, 64, 64, p, p, 6, p, 64, 3, p, NULL) == 1      # n_cb != K/32
 
 
+def test_gemv_group_rejects_bad_arguments(hiplib):
+    L = hiplib
+    p = ctypes.c_void_p(4096)
+    P2 = ctypes.c_void_p * 2
+    ptrs = P2(4096, 8192)
+    ns = (ctypes.c_int64 * 2)(64, 32)
+    # n_mats out of range, hdr_bytes, null bases without Z, misaligned X
+    assert L.sx8_gemv_group(p, 0, ptrs, ptrs, 6, ptrs, ptrs, NULL, ns, 2, ptrs, NULL) == 1
+    assert "n_mats" in _err(L)
+    assert L.sx8_gemv_group(p, 5, ptrs, ptrs, 6, ptrs, ptrs, NULL, ns, 2, ptrs, NULL) == 1
+    assert L.sx8_gemv_group(p, 2, ptrs, ptrs, 7, ptrs, ptrs, NULL, ns, 2, ptrs, NULL) == 1
+    assert "hdr_bytes" in _err(L)
+    assert L.sx8_gemv_group(p, 2, ptrs, ptrs, 6, NULL, NULL, NULL, ns, 2, ptrs, NULL) == 1
+    assert "bases" in _err(L)
+    assert L.sx8_gemv_group(ctypes.c_void_p(4098), 2, ptrs, ptrs, 6, ptrs, ptrs, NULL, ns, 2,
+                            ptrs, NULL) == 1
+    bad_n = (ctypes.c_int64 * 2)(64, 0)
+    assert L.sx8_gemv_group(p, 2, ptrs, ptrs, 6, ptrs, ptrs, NULL, bad_n, 2, ptrs, NULL) == 1
+    assert "bad N" in _err(L)
+
+
+def test_product_modules_import():
+    """Every Python module of the package imports without a GPU (no work at import)."""
+    import importlib
+    for m in ("_sx8lib", "kernel_sx8_v43", "prepare_v44", "quantize_sx8", "sx8_decode1_v3",
+              "sx8_embed_v44", "sx8_fused_wmma", "sx8_gemm_compact", "integrate_fused_v44",
+              "e2e_decoder"):
+        importlib.import_module(m)
+
+
 def test_wrapper_raises_runtime_error(hiplib):
     import _sx8lib
     with pytest.raises(RuntimeError, match="hdr_bytes"):

@@ -193,6 +193,35 @@ def test_gemv_deterministic_and_pool(hiplib, cuda):
     assert y2.data_ptr() == y.data_ptr()
 
 
+GROUP_CASES = [  # name, [N_i], K
+    ("qkv", [4096, 1024, 1024], 2560), ("gate_up", [9728, 9728], 2560),
+    ("ragged", [1000, 65, 300, 7], 96), ("long_K", [64, 100], 20512)]
+
+
+@pytest.mark.parametrize("name,Ns,K", GROUP_CASES)
+def test_gemv_group_matches_single(hiplib, oracle, cuda, name, Ns, K):
+    """One launch over weights that share x: each output within 1e-3 of the float64
+    yardstick and within 1e-5 of the single-matrix GEMV (only the panel split, hence the
+    fp32 summation order, differs).  long_K (n_cb = 641) takes the per-matrix path."""
+    import torch
+    from sx8_decode1_v3 import decode1_v44, decode1_v44_group, make_tensors_v44
+    _say("gemv_group", name, Ns, K)
+    x = _x(1, K, 77)[0]
+    qts = [_quantized(N, K, 500 + i, cuda) for i, N in enumerate(Ns)]
+    tens = [make_tensors_v44(qt, bi) for qt, bi in qts]
+    n_cb = qts[0][0]["n_cb"]
+    ys = decode1_v44_group(x.to(cuda), tens, Ns, n_cb)
+    torch.cuda.synchronize()
+    for i, ((qt, bi), t) in enumerate(zip(qts, tens)):
+        y_ref = oracle.gemm_f64(x.numpy()[None], oracle.dequant_r64(qt, bi))[0]
+        y = ys[i].cpu().numpy().astype(np.float64)
+        rel = oracle.rel_err(y, y_ref)
+        single = decode1_v44(x.to(cuda), qt, bi, *t)[0].cpu().numpy()
+        _say("   ", i, "rel", rel, "vs single", oracle.rel_err(y, single))
+        assert rel <= 1e-3
+        assert oracle.rel_err(y, single) <= 1e-5
+
+
 # -------------------------------------------------------------------------- GEMM
 
 PREFILL_CASES = [
