@@ -1,5 +1,7 @@
-"""S-X8 hot-path benchmark on one MI355X: decode GEMV sweep (headline), fused prefill
-GEMM at M = 2048, embedding gather, plus the CPU dequant+GEMV baseline.
+"""S-X8 hot-path benchmark on one MI355X: decode GEMV sweep (headline, plus the same layer
+as a decoder runs it with grouped launches), fused prefill GEMM at M = 128, 512, 2048, the
+vocab-sized matrix (lm_head GEMV at M = 1, GEMM at M = 512, embedding gather of 512 ids),
+the end-to-end 36-layer decoder, plus the CPU dequant+GEMV baseline.
 
 Headline (BASELINE.json metric, configs[1]): one step = the M = 1 decode GEMV of every
 linear of one synthetic Qwen3-4B-class layer (q 4096x2560, k/v 1024x2560,
@@ -34,7 +36,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
 # HBM bytes per k_gemv_panel launch on this workload (hdr_bytes=6), measured with two
 # rocprofv3 passes (FETCH_SIZE, WRITE_SIZE) scaled by what the counters read for a 512 MiB
 # copy (fetch x2.000, write x1.000); passes and calibration: profiles/gemv_decode_layer.md
-GEMV_TRAFFIC_PER_LAUNCH = 13.94e6
+GEMV_TRAFFIC_PER_LAUNCH = 13.96e6
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, vendor figure
 
 
@@ -49,11 +51,12 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--copies", type=int, default=12, help="distinct layer copies (cold cache)")
     ap.add_argument("--hdr-bytes", type=int, default=6, choices=[6, 8])
-    ap.add_argument("--prefill-m", type=int, default=2048)
+    ap.add_argument("--prefill-m", default="128,512,2048",
+                    help="comma-separated M values of the prefill sweep (the last is the headline)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|embed|e2e|copy "
+    ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|vocab|e2e|copy "
                     "(copy: the 512 MiB device copy that calibrates the HBM byte counters)")
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--e2e-prompt", type=int, default=512)
@@ -254,9 +257,8 @@ def bench_gemv(torch, L, layer, args):
     return out
 
 
-def bench_prefill(torch, L, layer, args):
+def bench_prefill_m(torch, L, layer, args, M):
     dev = torch.device("cuda:0")
-    M = args.prefill_m
     g = torch.Generator(device="cpu").manual_seed(12)
     xs = {K: torch.randn(M, K, generator=g).half().to(dev) for K in {t["K"] for t in layer}}
     ys = [torch.empty(M, t["N"], dtype=torch.float32, device=dev) for t in layer]
@@ -290,34 +292,86 @@ def bench_prefill(torch, L, layer, args):
         tot_flop += flop
         tot_ms += ms
         log(f"prefill {t['name']} M={M}: {ms * 1e3:.1f} us {res[t['name']]['tflops']:.1f} TFLOP/s")
-    return {"M": M, "tflops": tot_flop / (tot_ms * 1e-3) / 1e12, "per_shape": res,
-            "frac_of_mfma_peak": tot_flop / (tot_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS}
+    tf = tot_flop / (tot_ms * 1e-3) / 1e12
+    return {"M": M, "tflops": tf, "per_shape": res, "frac_of_mfma_peak": tf / MFMA_F16_PEAK_TFLOPS}
 
 
-def bench_embed(torch, L, layer, args):
-    """Row gather of 512 ids from the largest layer matrix (gate_proj, 9728 rows)."""
+def bench_prefill(torch, L, layer, args):
+    """Fused dequant + GEMM over the layer at every M of --prefill-m (config 2); the last M
+    (2048 by default) is the headline."""
+    ms = [int(v) for v in str(args.prefill_m).split(",") if v.strip()]
+    sweep = {M: bench_prefill_m(torch, L, layer, args, M) for M in ms}
+    out = dict(sweep[ms[-1]])
+    out["sweep"] = {str(M): {"tflops": r["tflops"], "frac_of_mfma_peak": r["frac_of_mfma_peak"],
+                             "per_shape_tflops": {k: v["tflops"] for k, v in r["per_shape"].items()}}
+                    for M, r in sweep.items()}
+    return out
+
+
+VOCAB = 151936
+
+
+def bench_vocab(torch, L, args):
+    """Config 3 on one vocab-sized S-X8 matrix (151936 x 2560, seeded N(0, 0.02), 1%
+    degenerate blocks): the lm_head GEMV at M = 1 and the prefill GEMM at M = 512 through
+    it, and the embedding row gather of 512 ids drawn uniformly from [0, 151936)."""
+    from prepare_v44 import to_v44_device
+    from quantize_sx8 import quantize_tensor
     dev = torch.device("cuda:0")
-    t = max(layer, key=lambda t: t["N"])
-    g = torch.Generator(device="cpu").manual_seed(3)
-    ids = torch.randint(0, t["N"], (512,), generator=g).to(dev)
-    out = torch.empty(512, t["K"], dtype=torch.float16, device=dev)
+    N, K = VOCAB, 2560
+    g = torch.Generator(device="cpu").manual_seed(4242)
+    W = (torch.randn(N, K, generator=g) * 0.02).half()
+    qt, bi = quantize_tensor(W, device=dev, degenerate_frac=0.01, seed=4243)
+    del W
+    hdr, lvl, bas, sca = to_v44_device(qt, bi, hdr_aligned=(args.hdr_bytes == 8), device=dev)
+    n_cb = qt["n_cb"]
     st = L.stream(dev)
-    args_ = (L.ptr(ids), 512, L.ptr(t["hdr"]), L.ptr(t["lvl"]), args.hdr_bytes, L.ptr(t["bas"]),
-             L.ptr(t["sca"]), t["K"], t["N"], t["n_cb"], L.ptr(out), st)
-    fn = L.lib().sx8_embed_gather
-    fn(*args_)
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    gpu_delay(torch, 10)
-    a.record()
-    for _ in range(20):
-        fn(*args_)
-    b.record()
-    torch.cuda.synchronize()
-    us = a.elapsed_time(b) * 1e3 / 20
-    rd = 512 * t["n_cb"] * 30
-    wr = 512 * t["K"] * 2
-    return {"table": f"{t['N']}x{t['K']}", "ids": 512, "us": us, "gbs": (rd + wr) / (us * 1e-6) / 1e9}
+    lib = L.lib()
+    out = {"shape": f"{N}x{K}", "packed_bytes": packed_bytes(N, K)}
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        gpu_delay(torch, 10)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    def ok(rc):
+        if rc != 0:
+            raise RuntimeError(lib.sx8_last_error().decode())
+
+    # lm_head GEMV, M = 1
+    x1 = torch.randn(K, generator=g).half().to(dev)
+    y1 = torch.empty(N, dtype=torch.float32, device=dev)
+    ws = torch.empty(int(lib.sx8_gemv_workspace_bytes(n_cb)) // 4 + 64, dtype=torch.float32, device=dev)
+    ms = timed(lambda: ok(lib.sx8_gemv(L.ptr(x1), L.ptr(hdr), L.ptr(lvl), args.hdr_bytes, L.ptr(bas),
+                                       L.ptr(sca), None, None, N, n_cb, L.ptr(y1), L.ptr(ws),
+                                       ws.numel() * 4, st)), 20)
+    out["gemv_m1"] = {"us": ms * 1e3, "gbs": packed_bytes(N, K) / (ms * 1e-3) / 1e9}
+    log(f"vocab gemv M=1: {ms * 1e3:.1f} us {out['gemv_m1']['gbs']:.0f} GB/s")
+    # lm_head prefill GEMM, M = 512
+    M = 512
+    xm = torch.randn(M, K, generator=g).half().to(dev)
+    ym = torch.empty(M, N, dtype=torch.float32, device=dev)
+    ms = timed(lambda: ok(lib.sx8_gemm_prefill(L.ptr(xm), M, K, K, L.ptr(hdr), L.ptr(lvl), args.hdr_bytes,
+                                               L.ptr(bas), L.ptr(sca), N, n_cb, L.ptr(ym), st)), 5)
+    out["gemm_m512"] = {"us": ms * 1e3, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
+    log(f"vocab gemm M=512: {ms * 1e3:.1f} us {out['gemm_m512']['tflops']:.0f} TFLOP/s")
+    del ym
+    # embedding gather of 512 ids
+    ids = torch.randint(0, N, (512,), generator=g).to(dev)
+    rows = torch.empty(512, K, dtype=torch.float16, device=dev)
+    ms = timed(lambda: ok(lib.sx8_embed_gather(L.ptr(ids), 512, L.ptr(hdr), L.ptr(lvl), args.hdr_bytes,
+                                               L.ptr(bas), L.ptr(sca), K, N, n_cb, L.ptr(rows), st)), 20)
+    rd, wr = 512 * n_cb * 30, 512 * K * 2
+    out["embed"] = {"ids": 512, "us": ms * 1e3, "gbs": (rd + wr) / (ms * 1e-3) / 1e9}
+    log(f"vocab embed 512 ids: {ms * 1e3:.1f} us")
+    return out
 
 
 def bench_e2e(torch, args):
@@ -434,9 +488,9 @@ def main():
         log("gemv", json.dumps(res["gemv"]))
     if args.only in ("", "prefill") and not args.no_prefill:
         res["prefill"] = bench_prefill(torch, L, layer, args)
-    if args.only in ("", "embed"):
-        res["embed"] = bench_embed(torch, L, layer, args)
-        log("embed", json.dumps(res["embed"]))
+    if args.only in ("", "vocab", "embed"):
+        res["vocab"] = bench_vocab(torch, L, args)
+        log("vocab", json.dumps(res["vocab"]))
     if args.only in ("", "e2e") and not args.no_e2e:
         res["e2e"] = bench_e2e(torch, args)
     cpu = None
@@ -480,7 +534,7 @@ def main():
         "cpu_baseline": cpu,
         "gemv_grouped": gv.get("grouped"),
         "prefill": res.get("prefill"),
-        "embed": res.get("embed"),
+        "vocab": res.get("vocab"),
         "e2e": res.get("e2e"),
     }
     print(json.dumps(line), flush=True)
