@@ -23,6 +23,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 REPO = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(REPO, "sx8-quantization_amd")
 sys.path.insert(0, PKG)
@@ -56,7 +58,7 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|vocab|e2e|copy "
+    ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|vocab|container|e2e|copy "
                     "(copy: the 512 MiB device copy that calibrates the HBM byte counters)")
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--e2e-prompt", type=int, default=512)
@@ -308,6 +310,77 @@ def bench_prefill(torch, L, layer, args):
     return out
 
 
+def bench_container(torch, L, layer, args):
+    """§8f row 2: the layer written as an .sx8v43 container (v1.1, with a small-tensor
+    section) and loaded straight into the v4.4 device layout (load_v44: file map, one
+    host-to-device copy of each tensor's block payload, sx8_v43_to_v44 on the GPU), plus
+    the layout kernel alone on device-resident payloads (30 B read + 30 B written per
+    block)."""
+    import tempfile
+    import sx8_container_v43 as C
+    dev = torch.device("cuda:0")
+    wd = {t["name"] + ".weight": t["qt"] for t in layer}
+    bd = {t["name"] + ".weight": t["bi"] for t in layer}
+    small = {"norm.weight": {"shape": (2560,), "dtype": "fp16",
+                             "data": np.ones(2560, dtype=np.float16)}}
+    out = {}
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "layer.sx8v43")
+        t0 = time.time()
+        C.write_sx43((wd, bd, {"bench": 1}), path, verbose=False, config={"hidden_size": 2560},
+                     small=small)
+        out["write_s"] = time.time() - t0
+        out["file_bytes"] = os.path.getsize(path)
+        C.load_v44(path, device=dev, hdr_bytes=args.hdr_bytes)     # warm the page cache
+        torch.cuda.synchronize()
+        t0 = time.time()
+        t44 = C.load_v44(path, device=dev, hdr_bytes=args.hdr_bytes)
+        torch.cuda.synchronize()
+        out["load_s"] = time.time() - t0
+        out["load_gbs"] = out["file_bytes"] / out["load_s"] / 1e9
+    # the layout kernel alone
+    lib = L.lib()
+    st = L.stream(dev)
+    jobs = []
+    for t in layer:
+        qt = t["qt"]
+        nb = qt["n_blocks"]
+        raw = torch.from_numpy(np.concatenate([np.asarray(qt[k]).reshape(-1).view(np.uint8) for k in
+                                               ("dmin", "dmax", "config", "levels_hi", "levels_lo",
+                                                "coeff")])).to(dev)
+        hdr = torch.empty(nb, args.hdr_bytes, dtype=torch.uint8, device=dev)
+        lvl = torch.empty(nb, 24, dtype=torch.uint8, device=dev)
+        jobs.append((raw, hdr, lvl, qt["shape"][0], qt["n_cb"], nb))
+
+    def run():
+        for raw, hdr, lvl, out_f, n_cb, nb in jobs:
+            b = raw.data_ptr()
+            P = L.ctypes.c_void_p
+            rc = lib.sx8_v43_to_v44(P(b), P(b + 2 * nb), P(b + 4 * nb), P(b + 29 * nb), P(b + 5 * nb),
+                                    P(b + 21 * nb), out_f, n_cb, args.hdr_bytes, L.ptr(hdr), L.ptr(lvl), st)
+            if rc != 0:
+                raise RuntimeError(lib.sx8_last_error().decode())
+    run()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gpu_delay(torch, 10)
+    a.record()
+    for _ in range(10):
+        run()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / 10
+    blocks = sum(j[5] for j in jobs)
+    out["layout_us"] = ms * 1e3
+    out["layout_gbs"] = blocks * 60 / (ms * 1e-3) / 1e9
+    ok = all(torch.equal(t44[t["name"] + ".weight"][0], t["hdr"]) and
+             torch.equal(t44[t["name"] + ".weight"][1], t["lvl"]) for t in layer)
+    out["matches_in_memory_layout"] = bool(ok)
+    log(f"container: load {out['load_s'] * 1e3:.1f} ms ({out['load_gbs']:.2f} GB/s), "
+        f"layout kernel {out['layout_us']:.1f} us ({out['layout_gbs']:.0f} GB/s)")
+    return out
+
+
 VOCAB = 151936
 
 
@@ -488,6 +561,9 @@ def main():
         log("gemv", json.dumps(res["gemv"]))
     if args.only in ("", "prefill") and not args.no_prefill:
         res["prefill"] = bench_prefill(torch, L, layer, args)
+    if args.only in ("", "container"):
+        res["container"] = bench_container(torch, L, layer, args)
+        log("container", json.dumps(res["container"]))
     if args.only in ("", "vocab", "embed"):
         res["vocab"] = bench_vocab(torch, L, args)
         log("vocab", json.dumps(res["vocab"]))
@@ -535,6 +611,7 @@ def main():
         "gemv_grouped": gv.get("grouped"),
         "prefill": res.get("prefill"),
         "vocab": res.get("vocab"),
+        "container": res.get("container"),
         "e2e": res.get("e2e"),
     }
     print(json.dumps(line), flush=True)

@@ -67,6 +67,18 @@ int32_t sx8_embed_gather(const int64_t* ids, int64_t T, const uint8_t* hdr,
                          const float* scales, int64_t K, int64_t N, int64_t n_cb,
                          uint16_t* out, void* stream);
 
+/* Load-time layout transform: S-X8 v4.3 split arrays in pkl / .sx8v43 container order
+ * (n-major, bid' = n*n_cb + kb: dmin/dmax fp16 as bytes, config, coeff, levels_hi
+ * (16 B per block), levels_lo (8 B per block); no alignment required) -> the v4.4
+ * kb-major device records (bid = kb*N + n): hdr (n_blk, hdr_bytes) = dmin | dmax | config
+ * | coeff (| 2 zero bytes) and levels (n_blk, 24) = levels_hi | levels_lo.  Byte-identical
+ * to the reference's to_v44 (scripts/prepare_v44.py:35-79), which it replaces on the
+ * device side of a container load. */
+int32_t sx8_v43_to_v44(const uint8_t* dmin, const uint8_t* dmax, const uint8_t* config,
+                       const uint8_t* coeff, const uint8_t* levels_hi, const uint8_t* levels_lo,
+                       int64_t out_f, int64_t n_cb, int32_t hdr_bytes, uint8_t* hdr,
+                       uint8_t* levels, void* stream);
+
 /* PCA precompute Z[m, kb, j] = scales[kb, j] * sum_t X[m, kb*32+t] * basis[kb, 32j+t]
  * for m < M, in float32 with the reference's summation tree.
  * Replaces compute_z44 (cuda/sx8_decode1_v3.cu:185-195, kernel :44-65) for M = 1 and

@@ -18,7 +18,8 @@ CSRC_DIR = os.path.join(PKG_DIR, "csrc")
 INCLUDE_DIR = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libsx8_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["sx8_abi.hip", "sx8_dequant.hip", "sx8_gemv.hip", "sx8_gemm.hip", "sx8_decoder.hip"]
+SOURCES = ["sx8_abi.hip", "sx8_dequant.hip", "sx8_layout.hip", "sx8_gemv.hip", "sx8_gemm.hip",
+           "sx8_decoder.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # hipcc flags: gfx950 only, no packed-fp32 instruction selection (those forms have
@@ -37,6 +38,7 @@ SIGNATURES = [
     ("sx8_abi_version", _I32, []),
     ("sx8_last_error", ctypes.c_char_p, []),
     ("sx8_dequant_f16", _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P]),
+    ("sx8_v43_to_v44", _I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P]),
     ("sx8_embed_gather", _I32, [_P, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _P, _P]),
     ("sx8_compute_z", _I32, [_P, _I64, _I64, _P, _P, _I64, _P, _P]),
     ("sx8_gemv", _I32, [_P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P]),

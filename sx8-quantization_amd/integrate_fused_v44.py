@@ -72,9 +72,12 @@ class SX8LinearV44(nn.Module):
         return y.reshape(*orig_shape[:-1], self.out_f)
 
 
-def clone_model_fused_v44(model, wd, bd, hdr_bytes=6):
+def clone_model_fused_v44(model, wd, bd, hdr_bytes=6, t44=None):
     """Replace, in place, every nn.Linear / nn.Embedding whose parameter name is in
-    ``wd`` by SX8LinearV44 / SX8EmbeddingV44.  Returns (model, n_replaced)."""
+    ``wd`` by SX8LinearV44 / SX8EmbeddingV44.  Returns (model, n_replaced).
+    ``t44`` (optional, not in the reference): {name: (hdr, levels, bases, scales)} device
+    tensors already in the v4.4 layout, e.g. from sx8_container_v43.load_v44; the
+    replaced modules use them instead of building their own."""
     n_replaced = 0
     for name, p in list(model.named_parameters()):
         if name not in wd or p.dim() < 2:
@@ -86,14 +89,22 @@ def clone_model_fused_v44(model, wd, bd, hdr_bytes=6):
             parent = parent[int(part)] if part.isdigit() else getattr(parent, part)
         attr = parts[-2]
         mod = getattr(parent, attr)
+        pre = t44.get(name) if t44 is not None else None
         if isinstance(mod, nn.Embedding):
-            setattr(parent, attr, SX8EmbeddingV44(qt, bi, hdr_bytes=6))
+            emb = SX8EmbeddingV44(qt, bi, hdr_bytes=6)
+            if pre is not None and pre[0].shape[1] == 6:
+                emb._t = pre
+                emb._hdr, emb._lvl, emb._bas, emb._sca = pre
+                emb.qt = emb.bases_info = None
+            setattr(parent, attr, emb)
             n_replaced += 1
             continue
         if not isinstance(mod, nn.Linear):
             continue
         new = SX8LinearV44(qt, bi, mod.bias, mod.out_features, mod.in_features,
                            hdr_bytes=hdr_bytes)
+        if pre is not None and pre[0].shape[1] == hdr_bytes:
+            new._t44 = pre
         setattr(parent, attr, new)
         del mod.weight
         n_replaced += 1

@@ -222,6 +222,38 @@ def test_gemv_group_matches_single(hiplib, oracle, cuda, name, Ns, K):
         assert oracle.rel_err(y, single) <= 1e-5
 
 
+@pytest.mark.parametrize("hdr_bytes", [6, 8])
+def test_container_load_v44_matches_to_v44(hiplib, oracle, cuda, tmp_path, hdr_bytes):
+    """.sx8v43 -> device v4.4 layout through sx8_v43_to_v44: byte-identical to the numpy
+    to_v44 (prepare_v44.py:35-79) for every tensor, and the loaded tensors drive the GEMV
+    to the same output as tensors built in memory."""
+    import torch
+    import sx8_container_v43 as C
+    from prepare_v44 import to_v44
+    from sx8_decode1_v3 import decode1_v44, make_tensors_v44
+    wd, bd = {}, {}
+    for i, (N, K) in enumerate([(300, 2560), (64, 96), (1000, 80), (4096, 2560)]):
+        wd[f"t{i}.weight"], bd[f"t{i}.weight"] = _quantized(N, K, 600 + i, cuda)
+    path = tmp_path / "m.sx8v43"
+    C.write_sx43((wd, bd, {"test": 1}), path, verbose=False)
+    _say("container", hdr_bytes, path.stat().st_size)
+    t44 = C.load_v44(path, device=cuda, hdr_bytes=hdr_bytes)
+    torch.cuda.synchronize()
+    for name, (qt, bi) in ((n, (wd[n], bd[n])) for n in sorted(wd)):
+        ref = to_v44(qt, bi, hdr_aligned=(hdr_bytes == 8))
+        hdr, lvl, bas, sca = t44[name]
+        assert np.array_equal(hdr.cpu().numpy(), ref["hdr"]), name
+        assert np.array_equal(lvl.cpu().numpy(), ref["levels"]), name
+        assert np.array_equal(bas.cpu().numpy(), ref["bases"]), name
+        assert np.array_equal(sca.cpu().numpy(), ref["scales"]), name
+    qt, bi = wd["t3.weight"], bd["t3.weight"]
+    x = _x(1, 2560, 41)[0].to(cuda)
+    y_file = decode1_v44(x, qt, bi, *t44["t3.weight"], hdr_bytes=hdr_bytes)[0].clone()
+    y_mem = decode1_v44(x, qt, bi, *make_tensors_v44(qt, bi, hdr_aligned=(hdr_bytes == 8)),
+                        hdr_bytes=hdr_bytes)[0]
+    assert torch.equal(y_file, y_mem)
+
+
 # -------------------------------------------------------------------------- GEMM
 
 PREFILL_CASES = [
