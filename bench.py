@@ -378,6 +378,46 @@ def bench_container(torch, L, layer, args):
     out["matches_in_memory_layout"] = bool(ok)
     log(f"container: load {out['load_s'] * 1e3:.1f} ms ({out['load_gbs']:.2f} GB/s), "
         f"layout kernel {out['layout_us']:.1f} us ({out['layout_gbs']:.0f} GB/s)")
+
+    # §8f row 4: the same layer as a GGUF (block_sx8 records), loaded into the v4.4 layout,
+    # and the llama.cpp fork's no-PCA float32 dequant (R32-ggml) of all its blocks
+    import sx8_gguf as G
+    gg = {}
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "layer.gguf")
+        G.convert(wd, path)
+        gg["file_bytes"] = os.path.getsize(path)
+        G.load_v44(path, device=dev, hdr_bytes=args.hdr_bytes)
+        torch.cuda.synchronize()
+        t0 = time.time()
+        g44 = G.load_v44(path, device=dev, hdr_bytes=args.hdr_bytes)
+        torch.cuda.synchronize()
+        gg["load_s"] = time.time() - t0
+        gg["matches_container_layout"] = bool(all(
+            torch.equal(g44[n][0], t44[n][0]) and torch.equal(g44[n][1], t44[n][1]) for n in wd))
+    dq = []
+    for t in layer:
+        qt = t["qt"]
+        blk = torch.from_numpy(G.blockify(qt).reshape(-1)).to(dev)
+        dq.append((blk, qt["shape"][0], qt["n_cb"], torch.empty(qt["shape"][0], t["K"], dtype=torch.float32,
+                                                                device=dev)))
+
+    def run_dq():
+        for blk, out_f, n_cb, y in dq:
+            G.dequant_ggml(blk, out_f, n_cb, contract=True, out=y)
+    run_dq()
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(5):
+        run_dq()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / 5
+    gg["r32_ggml_dequant_us"] = ms * 1e3
+    gg["r32_ggml_gbs"] = blocks * (30 + 128) / (ms * 1e-3) / 1e9
+    out["gguf"] = gg
+    log(f"gguf: load {gg['load_s'] * 1e3:.1f} ms, R32-ggml dequant {gg['r32_ggml_dequant_us']:.0f} us "
+        f"({gg['r32_ggml_gbs']:.0f} GB/s)")
     return out
 
 

@@ -79,6 +79,21 @@ int32_t sx8_v43_to_v44(const uint8_t* dmin, const uint8_t* dmax, const uint8_t* 
                        int64_t out_f, int64_t n_cb, int32_t hdr_bytes, uint8_t* hdr,
                        uint8_t* levels, void* stream);
 
+/* Same transform from GGUF block_sx8 records: `blocks` is (out_f * n_cb) interleaved 30-byte
+ * records dmin | dmax | config | qh[16] | ql[8] | coeff in n-major order, the tensor data of
+ * a GGUF SX8 tensor (llama-cpp-sx8.patch:131-144; converter blockify_vec,
+ * scripts/convert_pkl_to_gguf_sx8.py:21-38).  No alignment required. */
+int32_t sx8_blocks_to_v44(const uint8_t* blocks, int64_t out_f, int64_t n_cb, int32_t hdr_bytes,
+                          uint8_t* hdr, uint8_t* levels, void* stream);
+
+/* llama.cpp's no-PCA float32 dequant of block_sx8 records ("R32-ggml", dequantize_row_sx8,
+ * llama-cpp-sx8.patch:746-767): out (out_f, in_f) float32 row-major, the coeff byte
+ * ignored.  contract != 0 evaluates rlo, rhi and rlo + step*lv as fused multiply-adds (a
+ * C build that contracts them); contract == 0 rounds every operation separately.  For
+ * comparing this engine with the reference's llama.cpp fork on the same GGUF file. */
+int32_t sx8_dequant_ggml_f32(const uint8_t* blocks, int64_t out_f, int64_t in_f, int64_t n_cb,
+                             int32_t contract, float* out, void* stream);
+
 /* PCA precompute Z[m, kb, j] = scales[kb, j] * sum_t X[m, kb*32+t] * basis[kb, 32j+t]
  * for m < M, in float32 with the reference's summation tree.
  * Replaces compute_z44 (cuda/sx8_decode1_v3.cu:185-195, kernel :44-65) for M = 1 and

@@ -21,6 +21,8 @@ Contents (each restates a reference function; paths are relative to
   for spot checks of the fused form.
 * ``z44`` -- cuda/sx8_decode1_v3.cu:44-65 in float64.
 * ``gemm_f64`` -- the float64 yardstick Y = X . W16^T.
+* ``dequant_ggml`` -- C R32-ggml, llama.cpp's no-PCA float32 dequant of block_sx8
+  records (llama-cpp-sx8.patch:746-767), with or without fused multiply-adds.
 
 Parity status of each function is recorded next to it.
 """
@@ -61,6 +63,8 @@ def lib():
         L.sx8o_dequant_r64.argtypes = [i64, i32, p, p, p, p, p, p, p, p, i32, p, p]
         L.sx8o_dequant_r64.restype = None
         L.sx8o_dequant_r32.argtypes = [i64, i32, p, p, p, p, p, p, p, p, p]
+        L.sx8o_dequant_ggml.restype = None
+        L.sx8o_dequant_ggml.argtypes = [i64, p, i32, p]
         L.sx8o_dequant_r32.restype = None
         L.sx8o_gemm_f64.argtypes = [i32, i32, i32, p, i32, p, i32, p]
         L.sx8o_gemm_f64.restype = None
@@ -308,6 +312,15 @@ def dequant_r32(qt, bases_info):
                            _ptr(hi), _ptr(lo), _ptr(data), _ptr(sc), _ptr(out))
     out_f, in_f = qt["shape"]
     return out.view(np.float16).reshape(out_f, qt["n_cb"] * 32)[:, :in_f]
+
+
+def dequant_ggml(blocks: np.ndarray, contract: bool = True) -> np.ndarray:
+    """R32-ggml (llama-cpp-sx8.patch:746-767) of (n_blk, 30) u8 block_sx8 records ->
+    (n_blk, 32) float32, no PCA."""
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1, 30)
+    out = np.empty((b.shape[0], 32), dtype=np.float32)
+    lib().sx8o_dequant_ggml(b.shape[0], _ptr(b), int(bool(contract)), _ptr(out))
+    return out
 
 
 def dequant_r64_numpy(qt, bases_info):

@@ -19,6 +19,8 @@
  *     decode_tensor_gpu_fast (:141) then rounds to fp16 with torch .half() (RNE);
  *   - R32, the float32 variant used by the reference's .cu kernels
  *     (cuda/sx8_embed_v44.cu:46-75), kept only to count last-bit disagreements;
+ *   - R32-ggml, llama.cpp's no-PCA float32 dequant of GGUF block_sx8 records
+ *     (llama-cpp-sx8.patch:746-767), with and without fused multiply-adds;
  *   - float64-accumulated GEMV/GEMM references used as the 1e-3 yardstick
  *     (scripts/sx8_decode1_v3.py:131-133, scripts/sx8_fused_wmma.py:128-132);
  *   - the CPU dequant + fp32-accumulated GEMV that bench.py reports as its CPU
@@ -193,6 +195,32 @@ void sx8o_dequant_r32(int64_t n_blocks, int32_t n_cb,
                     + (float)c0 * scales[cb * 2] * basis[cb * 64 + t]
                     + (float)c1 * scales[cb * 2 + 1] * basis[cb * 64 + 32 + t];
             out16[bid * 32 + t] = sx8o_f32_to_f16(w);
+        }
+    }
+}
+
+/* R32-ggml: llama.cpp's dequantize_row_sx8 (llama-cpp-sx8.patch:746-767) on interleaved
+ * 30-byte block_sx8 records (patch:131-144): float32 arithmetic, no PCA (coeff ignored),
+ * branch-free strategy offsets, 0.015873f and 1e-10f.  contract = 1 writes the three
+ * a*b+c forms as fmaf (what a contracting C build computes), contract = 0 rounds every
+ * operation.  out: n_blocks * 32 floats in block order. */
+void sx8o_dequant_ggml(int64_t n_blocks, const uint8_t* blocks, int32_t contract, float* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t b = 0; b < n_blocks; b++) {
+        const uint8_t* r = blocks + b * 30;
+        const float lo_f = sx8o_f16_to_f32((uint16_t)(r[0] | (r[1] << 8)));
+        const float hi_f = sx8o_f16_to_f32((uint16_t)(r[2] | (r[3] << 8)));
+        const float q = (hi_f - lo_f) * 0.25f;
+        for (int t = 0; t < 32; t++) {
+            const int s = (r[4] >> ((t >> 3) * 2)) & 3;
+            const float k1 = (float)(3 * (s == 2) + (s == 3));
+            const float k2 = (float)(3 * (s == 1) + (s == 3));
+            const float rlo = contract ? fmaf(q, k1, lo_f) : lo_f + q * k1;
+            const float rhi = contract ? fmaf(-q, k2, hi_f) : hi_f - q * k2;
+            float step = (rhi - rlo) * 0.015873f;
+            if (step < 1e-10f) step = 1e-10f;
+            const float lv = (float)sx8o_level(r + 5, r + 21, t);
+            out[b * 32 + t] = contract ? fmaf(step, lv, rlo) : rlo + step * lv;
         }
     }
 }

@@ -39,6 +39,8 @@ SIGNATURES = [
     ("sx8_last_error", ctypes.c_char_p, []),
     ("sx8_dequant_f16", _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P]),
     ("sx8_v43_to_v44", _I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P]),
+    ("sx8_blocks_to_v44", _I32, [_P, _I64, _I64, _I32, _P, _P, _P]),
+    ("sx8_dequant_ggml_f32", _I32, [_P, _I64, _I64, _I64, _I32, _P, _P]),
     ("sx8_embed_gather", _I32, [_P, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _P, _P]),
     ("sx8_compute_z", _I32, [_P, _I64, _I64, _P, _P, _I64, _P, _P]),
     ("sx8_gemv", _I32, [_P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P]),

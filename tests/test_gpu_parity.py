@@ -254,6 +254,53 @@ def test_container_load_v44_matches_to_v44(hiplib, oracle, cuda, tmp_path, hdr_b
     assert torch.equal(y_file, y_mem)
 
 
+@pytest.mark.parametrize("hdr_bytes", [6, 8])
+def test_gguf_load_and_r32_ggml(hiplib, oracle, cuda, tmp_path, hdr_bytes):
+    """GGUF SX8 tensors (convert_pkl_to_gguf_sx8.py's layout): sx8_blocks_to_v44 gives
+    to_v44's bytes; the fork's no-PCA float32 dequant (R32-ggml) is bit-exact to the
+    oracle with and without contraction, NaN blocks included; the GEMV on the GGUF tensors
+    (zero PCA bases) is within 1e-3 of the float64 product with those weights."""
+    import torch
+    import sx8_gguf as G
+    from prepare_v44 import to_v44
+    from sx8_decode1_v3 import decode1_v44
+    wd = {f"t{i}": _quantized(N, K, 700 + i, cuda)[0] for i, (N, K) in enumerate([(300, 2560), (1000, 96)])}
+    path = tmp_path / "m.gguf"
+    G.convert(wd, path)
+    t44 = G.load_v44(path, device=cuda, hdr_bytes=hdr_bytes)
+    torch.cuda.synchronize()
+    for name, qt in wd.items():
+        zero = {"n_cb": qt["n_cb"], "data": np.zeros((qt["n_cb"], 64), np.float32),
+                "scales": np.zeros((qt["n_cb"], 2), np.float32)}
+        ref = to_v44(qt, zero, hdr_aligned=(hdr_bytes == 8))
+        assert np.array_equal(t44[name][0].cpu().numpy(), ref["hdr"]), name
+        assert np.array_equal(t44[name][1].cpu().numpy(), ref["levels"]), name
+        assert not t44[name][2].any() and not t44[name][3].any()
+    # R32-ggml, bit for bit (golden fuzz blocks: degenerate, reversed, NaN/inf endpoints)
+    g = np.load(os.path.join(HERE, "golden", "sx8_golden.npz"))
+    fq = {"n_blocks": 384}
+    for k in ("dmin", "dmax", "config", "levels_hi", "levels_lo", "coeff"):
+        fq[k] = g["fuzz_" + k]
+    cases = [(G.blockify(fq), 64, 6, 192)] + [
+        (G.blockify(qt), qt["shape"][0], qt["n_cb"], qt["shape"][1]) for qt in wd.values()]
+    for blocks, out_f, n_cb, in_f in cases:
+        dev_blocks = torch.from_numpy(blocks.reshape(-1).copy()).to(cuda)
+        for contract in (True, False):
+            got = G.dequant_ggml(dev_blocks, out_f, n_cb, in_f, contract=contract).cpu().numpy()
+            exp = oracle.dequant_ggml(blocks, contract).reshape(out_f, n_cb * 32)[:, :in_f]
+            _say("r32-ggml", out_f, n_cb, in_f, contract)
+            assert np.array_equal(got, exp, equal_nan=True)
+            fin = np.isfinite(exp)
+            assert np.array_equal(got[fin].view(np.uint32), exp[fin].view(np.uint32))
+    # GEMV through the GGUF-loaded tensors
+    qt = wd["t0"]
+    x = _x(1, 2560, 51)[0]
+    W = oracle.dequant_ggml(G.blockify(qt), True).reshape(300, 2560).astype(np.float64)
+    y_ref = W @ x.numpy().astype(np.float64)
+    y = decode1_v44(x.to(cuda), qt, None, *t44["t0"], hdr_bytes=hdr_bytes)[0].cpu().numpy()
+    assert oracle.rel_err(y, y_ref) <= 1e-3
+
+
 # -------------------------------------------------------------------------- GEMM
 
 PREFILL_CASES = [
