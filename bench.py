@@ -58,7 +58,7 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|vocab|container|e2e|copy "
+    ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|vocab|container|quantizer|e2e|copy "
                     "(copy: the 512 MiB device copy that calibrates the HBM byte counters)")
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--e2e-prompt", type=int, default=512)
@@ -421,6 +421,43 @@ def bench_container(torch, L, layer, args):
     return out
 
 
+def bench_quantizer(torch, L, args):
+    """§8f row 3: the S-X8 quantizer on the GPU over one layer's shapes (weights already
+    on the device): V6 encode + packing as one HIP kernel (timed alone with HIP events) and
+    the whole quantize_tensor (V6 kernel + batched Gram/eigh PCA in torch + copies to host
+    arrays), wall time.  weights/s and the time that rate gives for 4.0e9 weights."""
+    from quantize_sx8 import quantize_tensor, v6_encode_hip
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(9)
+    Ws = [(torch.randn(N, K, generator=g, device=dev) * 0.02).half() for _, N, K in LAYER]
+    n_w = sum(w.numel() for w in Ws)
+    blocks = [w.reshape(-1, 32) for w in Ws]
+    for b in blocks:
+        v6_encode_hip(b)
+    torch.cuda.synchronize()
+    a, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for b in blocks:
+        v6_encode_hip(b)
+    b_.record()
+    torch.cuda.synchronize()
+    v6_ms = a.elapsed_time(b_)
+    quantize_tensor(Ws[1], device=dev)
+    torch.cuda.synchronize()
+    t0 = time.time()
+    for w in Ws:
+        quantize_tensor(w, device=dev)
+    torch.cuda.synchronize()
+    q_s = time.time() - t0
+    out = {"weights": n_w, "v6_encode_ms": v6_ms, "v6_weights_per_s": n_w / (v6_ms * 1e-3),
+           "quantize_s": q_s, "quantize_weights_per_s": n_w / q_s,
+           "model_4b_s": 4.0e9 / (n_w / q_s)}
+    log(f"quantizer: V6 kernel {v6_ms:.2f} ms for {n_w / 1e6:.0f} M weights; quantize_tensor "
+        f"{q_s:.2f} s ({out['quantize_weights_per_s'] / 1e6:.0f} M weights/s, 4e9 weights in "
+        f"{out['model_4b_s']:.0f} s)")
+    return out
+
+
 VOCAB = 151936
 
 
@@ -604,6 +641,9 @@ def main():
     if args.only in ("", "container"):
         res["container"] = bench_container(torch, L, layer, args)
         log("container", json.dumps(res["container"]))
+    if args.only in ("", "quantizer"):
+        res["quantizer"] = bench_quantizer(torch, L, args)
+        log("quantizer", json.dumps(res["quantizer"]))
     if args.only in ("", "vocab", "embed"):
         res["vocab"] = bench_vocab(torch, L, args)
         log("vocab", json.dumps(res["vocab"]))
@@ -652,6 +692,7 @@ def main():
         "prefill": res.get("prefill"),
         "vocab": res.get("vocab"),
         "container": res.get("container"),
+        "quantizer": res.get("quantizer"),
         "e2e": res.get("e2e"),
     }
     print(json.dumps(line), flush=True)

@@ -94,6 +94,17 @@ int32_t sx8_blocks_to_v44(const uint8_t* blocks, int64_t out_f, int64_t n_cb, in
 int32_t sx8_dequant_ggml_f32(const uint8_t* blocks, int64_t out_f, int64_t in_f, int64_t n_cb,
                              int32_t contract, float* out, void* stream);
 
+/* V6 encode + level packing of a (out_f, in_f) fp16 weight (row pitch ld elements), the
+ * deterministic half of the quantizer (scripts/quantize_qwen35_4b_sx8_v43_gpu.py:22-47
+ * v6_encode_6bit_gpu, :148-167 pack_levels_6bit): per 32-weight block (columns past in_f
+ * count as zero) dmin/dmax (fp16), config, levels_hi (16 B), levels_lo (8 B), in the
+ * pkl / container n-major order; `levels` (optional, 32 B per block) receives the unpacked
+ * 6-bit levels for the PCA step.  Binary32 arithmetic with every operation rounded, MSE
+ * summed left to right, first strictly-lowest candidate wins. */
+int32_t sx8_v6_encode(const uint16_t* W, int64_t out_f, int64_t in_f, int64_t ld, uint8_t* levels,
+                      uint16_t* dmin, uint16_t* dmax, uint8_t* config, uint8_t* levels_hi,
+                      uint8_t* levels_lo, void* stream);
+
 /* PCA precompute Z[m, kb, j] = scales[kb, j] * sum_t X[m, kb*32+t] * basis[kb, 32j+t]
  * for m < M, in float32 with the reference's summation tree.
  * Replaces compute_z44 (cuda/sx8_decode1_v3.cu:185-195, kernel :44-65) for M = 1 and

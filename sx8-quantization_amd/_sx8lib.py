@@ -18,8 +18,8 @@ CSRC_DIR = os.path.join(PKG_DIR, "csrc")
 INCLUDE_DIR = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libsx8_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["sx8_abi.hip", "sx8_dequant.hip", "sx8_layout.hip", "sx8_gemv.hip", "sx8_gemm.hip",
-           "sx8_decoder.hip"]
+SOURCES = ["sx8_abi.hip", "sx8_dequant.hip", "sx8_layout.hip", "sx8_quant.hip", "sx8_gemv.hip",
+           "sx8_gemm.hip", "sx8_decoder.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # hipcc flags: gfx950 only, no packed-fp32 instruction selection (those forms have
@@ -41,6 +41,7 @@ SIGNATURES = [
     ("sx8_v43_to_v44", _I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P]),
     ("sx8_blocks_to_v44", _I32, [_P, _I64, _I64, _I32, _P, _P, _P]),
     ("sx8_dequant_ggml_f32", _I32, [_P, _I64, _I64, _I64, _I32, _P, _P]),
+    ("sx8_v6_encode", _I32, [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P]),
     ("sx8_embed_gather", _I32, [_P, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _P, _P]),
     ("sx8_compute_z", _I32, [_P, _I64, _I64, _P, _P, _I64, _P, _P]),
     ("sx8_gemv", _I32, [_P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P]),

@@ -8,6 +8,8 @@ reference, which runs at module import time and cannot be imported:
     of the V6 residual, coefficients quantized to signed 4 bits with scale
     median(|c|)/3; the first two are kept (1 coeff byte, 2 bases, 2 scales).
   * ``pack_levels_6bit`` -- :148-167.
+  * on a GPU the V6 encode and the packing run as one HIP kernel (``v6_encode_hip``,
+    sx8_v6_encode), bit-identical to ``v6_encode_6bit``; the PCA stays in torch.
   * ``quantize_tensor``  -- the tensor loop of :235-282 and the dict layout of
     :383-395.
 
@@ -158,16 +160,42 @@ def quantize_tensor(W, device=None, pca_method=None, degenerate_frac=0.0, seed=N
         n_deg = int(round(degenerate_frac * blocks.shape[0]))
         idx = torch.randperm(blocks.shape[0], generator=g)[:n_deg].to(device)
         blocks[idx] = blocks[idx, :1].expand(-1, B)
-    lv, dmin, dmax, cfg = v6_encode_6bit(blocks)
+    if blocks.is_cuda:
+        lv, dmin16, dmax16, cfg, hi_t, lo_t = v6_encode_hip(blocks)
+        dmin, dmax = dmin16.float(), dmax16.float()
+        hi, lo = hi_t.cpu().numpy(), lo_t.cpu().numpy()
+        dmin_np, dmax_np = dmin16.cpu().numpy(), dmax16.cpu().numpy()
+    else:
+        lv, dmin, dmax, cfg = v6_encode_6bit(blocks)
+        hi, lo = pack_levels_6bit(lv.cpu().numpy())
+        dmin_np = dmin.cpu().numpy().astype(np.float16)
+        dmax_np = dmax.cpu().numpy().astype(np.float16)
     coeff, data, scales = pca_correct(lv, dmin, dmax, cfg, blocks, n_cb, pca_method)
-    lv_np = lv.cpu().numpy()
-    hi, lo = pack_levels_6bit(lv_np)
     qt = {
         "shape": (out_f, in_f), "orig_shape": (out_f, in_f),
         "n_blocks": out_f * n_cb, "n_cb": n_cb,
-        "dmin": dmin.cpu().numpy().astype(np.float16),
-        "dmax": dmax.cpu().numpy().astype(np.float16),
+        "dmin": dmin_np, "dmax": dmax_np,
         "config": cfg.cpu().numpy().astype(np.uint8),
         "levels_hi": hi, "levels_lo": lo, "coeff": coeff,
     }
     return qt, {"n_cb": n_cb, "data": data, "scales": scales}
+
+
+def v6_encode_hip(blocks: torch.Tensor):
+    """V6 encode + packing of (n, 32) fp16-valued blocks on the GPU (sx8_v6_encode) ->
+    levels (n, 32) u8, dmin (n,) f16, dmax (n,) f16, config (n,) int32, levels_hi (16 n,)
+    u8, levels_lo (8 n,) u8, all on the blocks' device.  Same bits as v6_encode_6bit."""
+    import _sx8lib as _L
+    b16 = blocks.to(torch.float16).contiguous()
+    n = b16.shape[0]
+    dev = b16.device
+    u8 = dict(dtype=torch.uint8, device=dev)
+    lv = torch.empty(n, 32, **u8)
+    dmin = torch.empty(n, dtype=torch.float16, device=dev)
+    dmax = torch.empty(n, dtype=torch.float16, device=dev)
+    cfg = torch.empty(n, **u8)
+    hi = torch.empty(n * 16, **u8)
+    lo = torch.empty(n * 8, **u8)
+    _L.call("sx8_v6_encode", _L.ptr(b16), n, 32, 32, _L.ptr(lv), _L.ptr(dmin), _L.ptr(dmax), _L.ptr(cfg),
+            _L.ptr(hi), _L.ptr(lo), _L.stream(dev))
+    return lv, dmin, dmax, cfg.int(), hi, lo
