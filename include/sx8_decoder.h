@@ -41,6 +41,21 @@ int32_t sx8_dec_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
                      const int64_t* pos, uint16_t* out, int32_t nh, int32_t nk, int32_t hd,
                      int64_t L, float scale, void* stream);
 
+/* The same attention split over cache positions: two launches, n_kv x 32 work-groups each
+ * taking one KV head's share of positions for all nh/nk query heads that share it (nh/nk
+ * in {1, 2, 4, 8}), then a combine of the per-chunk partial softmax sums in fixed order.
+ * `workspace` (16-byte aligned, >= sx8_dec_attn_workspace_bytes(nh, hd)) holds the
+ * partials; it needs no clearing.  Each work-group streams its positions once with an
+ * online softmax, so the cache length is limited only to 2^20.  Same result as
+ * sx8_dec_attn up to float32 summation order. */
+int32_t sx8_dec_attn_split(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                           const int64_t* pos, uint16_t* out, int32_t nh, int32_t nk, int32_t hd,
+                           int64_t L, float scale, void* workspace, int64_t workspace_bytes,
+                           void* stream);
+
+/* Workspace bytes of sx8_dec_attn_split. */
+int64_t sx8_dec_attn_workspace_bytes(int32_t nh, int32_t hd);
+
 /* out = fp16(silu(g) * u) over n float32 elements. */
 int32_t sx8_dec_silu_mul(const float* g, const float* u, uint16_t* out, int64_t n, void* stream);
 

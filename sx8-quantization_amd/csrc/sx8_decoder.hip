@@ -240,6 +240,165 @@ __global__ __launch_bounds__(256) void k_attn_decode(const uint16_t* __restrict_
     }
 }
 
+// Split decode attention, two launches.  k_attn_split: work-group (kv head, chunk) takes
+// positions [chunk T, chunk T + T) of 0..*pos (T = ceil(n / kAttnChunks)) for all G query
+// heads that share the KV head, so every cache row is read once.  Lane group pg (CH lanes,
+// 8 dims each) streams positions pg, pg + PG, ... of the chunk with an online softmax: the
+// K and V rows of kU positions are loaded together, then per head the running max m, sum
+// l of exp(s - m) and acc = sum exp(s - m) v are rescaled and updated, so one pass over
+// the cache suffices and no score array is kept.  The lane groups meet in LDS and the
+// chunk's (m, l, acc[hd]) per head goes to the workspace.  k_attn_combine: per head and
+// dim, out = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c over the chunks in order
+// (deterministic; an empty chunk has m = -inf, l = 0 and weighs nothing).
+// kAttnChunks x n_kv work-groups fill the GPU where one work-group per query head
+// (k_attn_decode) leaves most CUs idle and waits on the cache latency round after round.
+constexpr int kAttnChunks = 32;
+constexpr int64_t kAttnSplitMaxL = (int64_t)1 << 20;
+
+template <int HD, int G>
+__global__ __launch_bounds__(256) void k_attn_split(const uint16_t* __restrict__ q,
+                                                    const uint16_t* __restrict__ k_cache,
+                                                    const uint16_t* __restrict__ v_cache,
+                                                    const int64_t* __restrict__ pos_p,
+                                                    float* __restrict__ part, int L, float scale) {
+    constexpr int CH = HD / 8;
+    constexpr int PG = 256 / CH;
+    constexpr int kU = 4;
+    __shared__ float sm[PG][G], sl[PG][G];
+    __shared__ float sacc[PG][G][HD + 4];
+    const int kv = blockIdx.x / kAttnChunks, chunk = blockIdx.x % kAttnChunks;
+    const int64_t pos = *pos_p;
+    const int n = (int)min(max(pos, (int64_t)0) + 1, (int64_t)L);
+    const int T = (n + kAttnChunks - 1) / kAttnChunks;
+    const int jb = chunk * T, je = min(jb + T, n);
+    const int tid = threadIdx.x, c = tid % CH, pg = tid / CH;
+    float qv[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const sx8_u32x4 x = *reinterpret_cast<const sx8_u32x4*>(q + (kv * G + g) * HD + 8 * c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            qv[g][2 * e] = h2f(x[e] & 0xFFFFu);
+            qv[g][2 * e + 1] = h2f(x[e] >> 16);
+        }
+    }
+    const uint16_t* kc = k_cache + (int64_t)kv * L * HD;
+    const uint16_t* vc = v_cache + (int64_t)kv * L * HD;
+    float m[G], l[G], a[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[g][e] = 0.f;
+    }
+    for (int j0 = jb + pg; j0 < je; j0 += kU * PG) {
+        sx8_u32x4 kr[kU], vr[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u)      // past the chunk: a valid row, its score is -inf
+            kr[u] = *reinterpret_cast<const sx8_u32x4*>(kc + (int64_t)min(j0 + u * PG, je - 1) * HD + 8 * c);
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+            vr[u] = *reinterpret_cast<const sx8_u32x4*>(vc + (int64_t)min(j0 + u * PG, je - 1) * HD + 8 * c);
+        float s[kU][G];
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float sc = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    sc += qv[g][2 * e] * h2f(kr[u][e] & 0xFFFFu) + qv[g][2 * e + 1] * h2f(kr[u][e] >> 16);
+#pragma unroll
+                for (int o = CH / 2; o > 0; o >>= 1) sc += __shfl_xor(sc, o, 64);
+                s[u][g] = j0 + u * PG < je ? sc * scale : -INFINITY;
+            }
+        float vf[kU][8];
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vf[u][2 * e] = h2f(vr[u][e] & 0xFFFFu);
+                vf[u][2 * e + 1] = h2f(vr[u][e] >> 16);
+            }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float mx = m[g];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) mx = fmaxf(mx, s[u][g]);       // finite: u = 0 is in the chunk
+            const float alpha = __expf(m[g] - mx);                       // 0 on the first pass
+            l[g] *= alpha;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[g][e] *= alpha;
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const float pu = __expf(s[u][g] - mx);
+                l[g] += pu;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) a[g][e] += pu * vf[u][e];
+            }
+            m[g] = mx;
+        }
+    }
+    if (c == 0)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            sm[pg][g] = m[g];
+            sl[pg][g] = l[g];
+        }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sacc[pg][g][8 * c + e] = a[g][e];
+    __syncthreads();
+    for (int t = tid; t < G * HD; t += 256) {
+        const int g = t / HD, d = t - g * HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < PG; ++i) M = fmaxf(M, sm[i][g]);
+        float num = 0.f, den = 0.f;
+        if (M != -INFINITY) {                  // a lane group without positions weighs e^-inf = 0
+#pragma unroll
+            for (int i = 0; i < PG; ++i) {
+                const float wi = __expf(sm[i][g] - M);
+                num += wi * sacc[i][g][d];
+                den += wi * sl[i][g];
+            }
+        }
+        float* ph = part + ((int64_t)(kv * G + g) * kAttnChunks + chunk) * (HD + 2);
+        ph[2 + d] = num;
+        if (d == 0) {
+            ph[0] = M;
+            ph[1] = den;
+        }
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ part,
+                                                     uint16_t* __restrict__ out) {
+    const int h = blockIdx.x, d = threadIdx.x;
+    const float* ph = part + (int64_t)h * kAttnChunks * (HD + 2);
+    float mc[kAttnChunks], lc[kAttnChunks], ac[kAttnChunks];
+#pragma unroll
+    for (int c = 0; c < kAttnChunks; ++c) {      // every load of the head issued at once
+        mc[c] = ph[c * (HD + 2)];
+        lc[c] = ph[c * (HD + 2) + 1];
+        ac[c] = ph[c * (HD + 2) + 2 + d];
+    }
+    float M = mc[0];                             // chunk 0 always holds position 0
+#pragma unroll
+    for (int c = 1; c < kAttnChunks; ++c) M = fmaxf(M, mc[c]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int c = 0; c < kAttnChunks; ++c) {
+        const float wc = __expf(mc[c] - M);      // empty chunk: e^-inf = 0, l = acc = 0
+        num += wc * ac[c];
+        den += wc * lc[c];
+    }
+    out[h * HD + d] = f2h(num / den);
+}
+
 // out = fp16(silu(g) * u), g and u f32
 __global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ g, const float* __restrict__ u,
                                                   uint16_t* __restrict__ out, int64_t n) {
@@ -326,6 +485,44 @@ extern "C" int32_t sx8_dec_attn(const uint16_t* q, const uint16_t* k_cache, cons
         hipLaunchKernelGGL(k_attn_decode<64>, dim3((unsigned)nh), dim3(256), 0, as_stream(stream), q,
                            k_cache, v_cache, pos, out, nh, nk, (int)L, scale);
     return check_launch("sx8_dec_attn");
+}
+
+extern "C" int64_t sx8_dec_attn_workspace_bytes(int32_t nh, int32_t hd) {
+    return nh > 0 && hd > 0 ? (int64_t)nh * kAttnChunks * (hd + 2) * (int64_t)sizeof(float) : 0;
+}
+
+extern "C" int32_t sx8_dec_attn_split(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                      const int64_t* pos, uint16_t* out, int32_t nh, int32_t nk,
+                                      int32_t hd, int64_t L, float scale, void* workspace,
+                                      int64_t workspace_bytes, void* stream) {
+    using namespace sx8;
+    if (!q || !k_cache || !v_cache || !pos || !out || !workspace)
+        return fail(SX8_ERR_INVALID, "sx8_dec_attn_split: null pointer");
+    const int G = nk > 0 ? nh / nk : 0;
+    if (nh <= 0 || nk <= 0 || nh % nk || (G != 1 && G != 2 && G != 4 && G != 8) ||
+        (hd != 64 && hd != 128) || L <= 0 || L > kAttnSplitMaxL)
+        return fail(SX8_ERR_INVALID, "sx8_dec_attn_split: bad shape (nh / nk in {1, 2, 4, 8}, hd 64 or "
+                                     "128, cache length <= %lld)", (long long)kAttnSplitMaxL);
+    if (workspace_bytes < sx8_dec_attn_workspace_bytes(nh, hd) || !aligned(workspace, 16))
+        return fail(SX8_ERR_INVALID, "sx8_dec_attn_split: workspace needs %lld bytes, 16-byte aligned",
+                    (long long)sx8_dec_attn_workspace_bytes(nh, hd));
+    if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
+        return fail(SX8_ERR_INVALID, "sx8_dec_attn_split: q and caches must be 16-byte aligned");
+    float* part = reinterpret_cast<float*>(workspace);
+    const hipStream_t st = as_stream(stream);
+    const dim3 grid((unsigned)(nk * kAttnChunks));
+#define SX8_ATTN(HDV, GV)                                                                           \
+    hipLaunchKernelGGL((k_attn_split<HDV, GV>), grid, dim3(256), 0, st, q, k_cache, v_cache, pos,  \
+                       part, (int)L, scale)
+    if (hd == 128) {
+        if (G == 1) SX8_ATTN(128, 1); else if (G == 2) SX8_ATTN(128, 2); else if (G == 4) SX8_ATTN(128, 4); else SX8_ATTN(128, 8);
+        hipLaunchKernelGGL(k_attn_combine<128>, dim3((unsigned)nh), dim3(128), 0, st, part, out);
+    } else {
+        if (G == 1) SX8_ATTN(64, 1); else if (G == 2) SX8_ATTN(64, 2); else if (G == 4) SX8_ATTN(64, 4); else SX8_ATTN(64, 8);
+        hipLaunchKernelGGL(k_attn_combine<64>, dim3((unsigned)nh), dim3(64), 0, st, part, out);
+    }
+#undef SX8_ATTN
+    return check_launch("sx8_dec_attn_split");
 }
 
 extern "C" int32_t sx8_dec_silu_mul(const float* g, const float* u, uint16_t* out, int64_t n, void* stream) {

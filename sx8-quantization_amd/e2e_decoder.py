@@ -206,6 +206,7 @@ class SX8Decoder(nn.Module):
         n_cb_max = max(lin.qt["n_cb"] for ly in self.layers for lin in (ly.q, ly.o, ly.down))
         ws_bytes = int(_L.lib().sx8_gemv_workspace_bytes(max(n_cb_max, self.head.qt["n_cb"])))
         z["ws"] = torch.zeros((ws_bytes + 3) // 4 + 64, **f32)
+        z["attn_ws"] = torch.zeros(int(_L.lib().sx8_dec_attn_workspace_bytes(nh, hd)) // 4 + 64, **f32)
         # grouped GEMV arguments (q/k/v and gate/up share their input): ctypes arrays
         # of device pointers, built once per layer
         z["groups"] = []
@@ -258,8 +259,9 @@ class SX8Decoder(nn.Module):
             _L.call("sx8_dec_qk_rope_cache", P(z["q"]), P(z["k"]), P(z["v"]), P(ly.q_norm), P(ly.k_norm),
                     P(self.cos), P(self.sin), P(pos), P(z["qh"]), P(self.k_cache[li]),
                     P(self.v_cache[li]), nh, nk, hd, L, eps, st)
-            _L.call("sx8_dec_attn", P(z["qh"]), P(self.k_cache[li]), P(self.v_cache[li]), P(pos),
-                    P(z["a"]), nh, nk, hd, L, 1.0 / math.sqrt(hd), st)
+            _L.call("sx8_dec_attn_split", P(z["qh"]), P(self.k_cache[li]), P(self.v_cache[li]), P(pos),
+                    P(z["a"]), nh, nk, hd, L, 1.0 / math.sqrt(hd), P(z["attn_ws"]),
+                    z["attn_ws"].numel() * 4, st)
             self._gemv(ly.o, z["a"], z["o"], st)
             _L.call("sx8_dec_add_rmsnorm", P(z["resid"]), P(z["o"]), None, P(ly.post_norm), P(z["h"]), 1,
                     cfg["hidden"], eps, st)
