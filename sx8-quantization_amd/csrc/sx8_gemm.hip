@@ -95,6 +95,11 @@ struct GemmSmem {
     sx8_u32x4 pt[2][4][64];
 };
 
+// A wave-uniform value kept in a scalar register (buffer loads take their K-block offset
+// as the scalar offset; if the compiler loses track of its uniformity it wraps every load
+// in a loop over distinct lane values).
+__device__ __forceinline__ int sx8_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
 // Buffer resources and per-lane byte offsets for the main loop's loads.  The K block goes
 // into the scalar offset, so the loop does no per-lane address arithmetic; a lane whose
 // vector offset lies past the end of a buffer (X rows >= M) reads zero.
@@ -114,7 +119,7 @@ struct LoopSrc {
 template <bool kSplit, int HB, int MF>
 __device__ __forceinline__ void load_rec_hdr(LaneRec& r, const LoopSrc<MF>& ls, int N, int kb) {
     const int nn = ls.nn;
-    const int rowb = kb * N;                       // first block of K row kb
+    const int rowb = sx8_uniform(kb * N);          // first block of K row kb
     if constexpr (kSplit) {
         r.lohi = __builtin_amdgcn_raw_buffer_load_b16(ls.dmin, nn * 2, rowb * 2, 0);
         r.hi16 = __builtin_amdgcn_raw_buffer_load_b16(ls.dmax, nn * 2, rowb * 2, 0);
@@ -136,7 +141,7 @@ __device__ __forceinline__ void load_rec_hdr(LaneRec& r, const LoopSrc<MF>& ls, 
 template <bool kSplit, int HB, int MF>
 __device__ __forceinline__ void load_rec_lv(LaneRec& r, const LoopSrc<MF>& ls, int N, int kb) {
     const int nn = ls.nn, s = ls.h;
-    const int rowb = kb * N;
+    const int rowb = sx8_uniform(kb * N);
     if constexpr (kSplit) {
         const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ls.hi, nn * 16 + 8 * s, rowb * 16, 0));
         r.q0 = v.x;
@@ -191,7 +196,7 @@ __device__ __forceinline__ void load_a_step(sx8_u32x4 (&a)[MF][2], const LoopSrc
 #pragma unroll
     for (int f = 0; f < MF; ++f)
         a[f][st] = __builtin_bit_cast(sx8_u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                     ls.x, ls.a_off[f] + 1024 * st, kb * 2048, 0));
+                                                     ls.x, ls.a_off[f] + 1024 * st, sx8_uniform(kb * 2048), 0));
 }
 
 template <int MF>
@@ -227,6 +232,14 @@ __device__ __forceinline__ void lds_barrier() {
     // reads have landed (an opaque asm wait would make it wait again for the next
     // iteration's reads before their first use)
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt, expcnt untouched
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// The same barrier with up to four of this wave's LDS operations still in flight: LDS
+// operations complete in issue order, so lgkmcnt(4) covers every LDS access but the last
+// four (the caller issues no scalar memory loads, which share the counter, in its loop).
+__device__ __forceinline__ void lds_barrier_keep4() {
+    __builtin_amdgcn_s_waitcnt(0xC47F);   // lgkmcnt(4); vmcnt, expcnt untouched
     asm volatile("s_barrier" ::: "memory");
 }
 
@@ -544,6 +557,278 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ 
     }
 }
 
+// One wave per SIMD, tile 512 x 128 (k_gemm_w1).  The decode VALU work per MFMA falls with
+// the tile height: a 512-row tile does 32 MFMAs per wave per K block against the 16
+// weights each lane decodes, half the ratio of the 256-row tile.  Each wave needs 256
+// accumulator registers (4 m-fragments x 4 n-fragments of 32 x 32), so it runs alone on
+// its SIMD (waves_per_eu = 1, up to 512 registers) and interleaves its own decode with its
+// MFMAs: wave w owns rows 128 w .. 128 w + 127 for all 128 columns and decodes n-fragment
+// w (columns 32 w .. 32 w + 31, lane l: column 32 w + l % 32, sub-blocks 2 (l / 32),
+// 2 (l / 32) + 1) of every K block into the same three-deep LDS ring as k_gemm.
+constexpr int kW1Threads = 256;
+constexpr int kW1MF = 4;
+constexpr int kW1BM = 128 * kW1MF;
+
+// Work of one launch: T tiles in m-major order (tile t = row block t / NB, column block
+// t % NB).  Work-groups 0 .. Tf - 1 (whole rounds of the 256 CUs, or none) each own one of
+// the first Tf tiles over the whole K; the remaining T - Tf tiles are split into St K
+// ranges of kbs blocks, one work-group each, which start as the full tiles finish.  K range
+// 0 of a split tile writes Y, range s > 0 its partial tile part[(t - Tf) (St - 1) + s - 1]
+// (512 x 128 f32, row-major), added to Y by k_reduce_tiles in range order.
+template <bool kSplit, int HB, bool kPca>
+__global__ __launch_bounds__(kW1Threads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_w1(
+    const uint16_t* __restrict__ Xp, int M, WeightSrc w, const uint32_t* __restrict__ Zhl, int N,
+    int n_cb, int Tf, int St, int kbs, float* __restrict__ Y, float* __restrict__ part) {
+    constexpr int MF = kW1MF;
+    __shared__ GemmSmem sm;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int NB = (N + kBN - 1) / kBN;
+    const int b = blockIdx.x;
+    int t, ks = 0, kb0 = 0, kb1 = n_cb;
+    if (b < Tf) {
+        t = xcd_order(b, Tf);
+    } else {
+        // Tf is a multiple of 8, so work-group b still runs on XCD b % 8
+        const int o = xcd_order(b - Tf, gridDim.x - Tf);
+        t = Tf + o / St;
+        ks = o % St;
+        kb0 = ks * kbs;
+        kb1 = min(n_cb, kb0 + kbs);
+    }
+    const int nb = t % NB;
+    const int mb = t / NB;
+    const int m0 = mb * kW1BM;
+    const int n0 = nb * kBN;
+    const int hf = lane >> 5, r = lane & 31;
+    const int h = hf;                     // decode: sub-block pair {2h, 2h + 1}
+    const int wj = wave, wl = lane;       // decode: n-fragment and B-tile slot
+
+    if constexpr (kPca) {
+        // coefficient slots of blocks past n_cb are never written: start them at zero.
+        // Thread t clears slots [b][wave][lane] of both groups, the slots only this wave
+        // writes, so program order makes the clear precede its own coefficient stores.
+        sx8_u32x4* p = reinterpret_cast<sx8_u32x4*>(&sm.pt[0][0][0]);
+        p[tid] = sx8_u32x4{0u, 0u, 0u, 0u};
+        p[tid + kW1Threads] = sx8_u32x4{0u, 0u, 0u, 0u};
+    }
+
+    LoopSrc<MF> ls;
+    const int64_t n_blk = (int64_t)N * n_cb;
+    if constexpr (kSplit) {
+        ls.dmin = make_rsrc(w.dmin, n_blk * 2);
+        ls.dmax = make_rsrc(w.dmax, n_blk * 2);
+        ls.cfg = make_rsrc(w.config, n_blk);
+        ls.cf = make_rsrc(w.coeff, n_blk);
+        ls.hi = make_rsrc(w.hi, n_blk * 16);
+        ls.lo = make_rsrc(w.lo, n_blk * 8);
+    } else {
+        ls.hdr = make_rsrc(w.hdr, n_blk * HB);
+        ls.lv = make_rsrc(w.levels, n_blk * 24);
+    }
+    ls.nn = min(n0 + 32 * wave + r, N - 1);
+    ls.h = h;
+    ls.x = make_rsrc(Xp, (int64_t)((M + 31) / 32) * n_cb * 2048);
+    if constexpr (kPca) ls.z = make_rsrc(Zhl, (int64_t)M * n_cb * 8);
+#pragma unroll
+    for (int f = 0; f < MF; ++f) {
+        // rows past M lie past the end of both buffers (read as zero); the host checks that
+        // these offsets fit 31 bits for the padded row count
+        const int g32 = (m0 >> 5) + wave * MF + f;
+        ls.a_off[f] = (int)((int64_t)g32 * n_cb * 2048) + lane * 16;
+        const int row = m0 + wave * 32 * MF + 32 * f + r;
+        ls.z_off[f] = (int)(((int64_t)row * n_cb + 2 * hf) * 8);
+    }
+
+    sx8_float16v acc[MF][4];
+#pragma unroll
+    for (int f = 0; f < MF; ++f)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[f][j][i] = 0.f;
+
+    // prologue: blocks kb0, kb0 + 1 decoded, block kb0 + 2 prepared, records of kb0 + 3 ..
+    // kb0 + 6 and A of kb0, kb0 + 1 in flight; B of kb0 read after the barrier.  Records
+    // form a ring of four (block b in R[(b - kb0) % 4]) so that each is requested four
+    // iterations before its first use: this wave issues the MFMAs too, and a record that
+    // has not arrived would stall them.
+    LaneRec R[4];
+    DecPrep P[2];
+    sx8_u32x4 A[2][MF][2];
+    sx8_u32x4 za[MF];
+    {
+        LaneRec r0, r1, r2;
+        load_rec<kSplit, HB, MF>(r0, ls, N, kb0);
+        load_rec<kSplit, HB, MF>(r1, ls, N, min(kb0 + 1, kb1 - 1));
+        load_rec<kSplit, HB, MF>(r2, ls, N, min(kb0 + 2, kb1 - 1));
+        load_a<MF>(A[0], ls, kb0);
+        load_a<MF>(A[1], ls, min(kb0 + 1, kb1 - 1));
+        if constexpr (kPca) load_za<MF>(za, ls, kb0 >> 2);
+        load_rec<kSplit, HB, MF>(R[3], ls, N, min(kb0 + 3, kb1 - 1));
+        load_rec<kSplit, HB, MF>(R[0], ls, N, min(kb0 + 4, kb1 - 1));
+        load_rec<kSplit, HB, MF>(R[1], ls, N, min(kb0 + 5, kb1 - 1));
+        load_rec<kSplit, HB, MF>(R[2], ls, N, min(kb0 + 6, kb1 - 1));
+        decode_block<kSplit, kPca>(sm, r0, kb0, kb0 % 3, wj, wl, h);
+        decode_block<kSplit, kPca>(sm, r1, kb0 + 1, (kb0 + 1) % 3, wj, wl, h);
+        P[0] = dec_prep<kSplit>(r2, h);
+        lds_barrier();
+    }
+    const uint8_t* wbase = reinterpret_cast<const uint8_t*>(&sm.wt[0][0][0][lane]);
+    // B operands of one block, refilled per k-step right after that k-step's MFMAs
+    sx8_u32x4 bw[4][2];
+    auto read_b = [&](int kb, int st) __attribute__((always_inline)) {
+        const uint8_t* src = wbase + (kb % 3) * kWtBufBytes;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            bw[j][st] = *reinterpret_cast<const sx8_u32x4*>(src + (j * 2 + st) * 1024);
+    };
+    read_b(kb0, 0);
+    read_b(kb0, 1);
+
+    // iteration kb: finish block kb + 2 into the ring and prepare block kb + 3 (its
+    // records refilled with block kb + 7); 32 MFMAs of block kb, each k-step followed by
+    // the refill of its A registers (block kb + 2) and B registers (block kb + 1, in LDS
+    // since the previous barrier); PCA k-step at the end of a 4-block group; one barrier.
+    // The decode VALU work is spread between the MFMAs (one MFMA, then up to three or four
+    // VALU instructions), so it issues while the matrix core is busy.
+    auto body = [&](int kb, sx8_u32x4 (&acur)[MF][2], LaneRec& rx, const DecPrep& pcur,
+                    DecPrep& pnext, const bool pca) __attribute__((always_inline)) {
+        const int ka = min(kb + 2, kb1 - 1);
+        // k-step 0: prepare block kb + 3 between the MFMAs, then refill A, B and the records
+        pnext = dec_prep<kSplit>(rx, h);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int f = 0; f < MF; ++f)
+                acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                    __builtin_bit_cast(sx8_half8, bw[j][0]),
+                    __builtin_bit_cast(sx8_half8, acur[f][0]), acc[f][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // up to three VALU
+        }
+        SX8_SCHED_FENCE();
+        load_a_step<MF>(acur, ls, ka, 0);
+        load_rec<kSplit, HB, MF>(rx, ls, N, min(kb + 7, kb1 - 1));
+        read_b(kb + 1, 0);
+        SX8_SCHED_FENCE();
+        // k-step 1: finish block kb + 2 into the ring between the MFMAs, then refill A, B
+        dec_finish<kPca>(sm, pcur, kb + 2, (kb + 2) % 3, wj, wl, h);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int f = 0; f < MF; ++f)
+                acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                    __builtin_bit_cast(sx8_half8, bw[j][1]),
+                    __builtin_bit_cast(sx8_half8, acur[f][1]), acc[f][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // up to four VALU
+        }
+        SX8_SCHED_FENCE();
+        load_a_step<MF>(acur, ls, ka, 1);
+        read_b(kb + 1, 1);
+        SX8_SCHED_FENCE();
+        if constexpr (kPca) {
+            if (pca) {
+                const int g = kb >> 2;
+                sx8_half8 zh[MF];
+#pragma unroll
+                for (int f = 0; f < MF; ++f) zh[f] = mask_za(za[f], n_cb, g, hf);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const sx8_half8 c = __builtin_bit_cast(sx8_half8, sm.pt[g & 1][j][lane]);
+#pragma unroll
+                    for (int f = 0; f < MF; ++f)
+                        acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(c, zh[f], acc[f][j], 0, 0, 0);
+                }
+                load_za<MF>(za, ls, min(g + 1, (kb1 - 1) >> 2));
+            }
+        }
+        // the barrier waits for this wave's LDS accesses except the four B reads just
+        // issued (slot (kb + 1) % 3 is next written two barriers later)
+        lds_barrier_keep4();
+    };
+    int kb = kb0;   // a multiple of 4
+    for (; kb + 4 <= kb1; kb += 4) {
+        body(kb, A[0], R[3], P[0], P[1], false);
+        body(kb + 1, A[1], R[0], P[1], P[0], false);
+        body(kb + 2, A[0], R[1], P[0], P[1], false);
+        body(kb + 3, A[1], R[2], P[1], P[0], true);
+    }
+    // last partial group (n_cb % 4 blocks): its PCA step after its last block
+    if (kb < kb1) body(kb, A[0], R[3], P[0], P[1], kb + 1 == kb1);
+    if (kb + 1 < kb1) body(kb + 1, A[1], R[0], P[1], P[0], kb + 2 == kb1);
+    if (kb + 2 < kb1) body(kb + 2, A[0], R[1], P[0], P[1], true);
+
+    // epilogue: accumulator (f, j) holds the transposed 32 x 32 tile (see k_gemm): a 16-byte
+    // store of 4 consecutive columns per (f, j, q).  Partial tiles are dense 512 x 128.
+    if (ks > 0) {
+        float* pt = part + ((int64_t)(t - Tf) * (St - 1) + ks - 1) * (kW1BM * kBN);
+#pragma unroll
+        for (int f = 0; f < MF; ++f) {
+            float* row = pt + (wave * 32 * MF + 32 * f + r) * kBN;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<sx8_float4*>(row + 32 * j + 8 * q + 4 * hf) =
+                        sx8_float4{acc[f][j][4 * q], acc[f][j][4 * q + 1], acc[f][j][4 * q + 2],
+                                   acc[f][j][4 * q + 3]};
+        }
+        return;
+    }
+    const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+#pragma unroll
+    for (int f = 0; f < MF; ++f) {
+        const int m = m0 + wave * 32 * MF + 32 * f + r;
+        if (m >= M) continue;
+        float* row = Y + (int64_t)m * N;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + 32 * j + 8 * q + 4 * hf;
+                const sx8_float4 v = {acc[f][j][4 * q], acc[f][j][4 * q + 1], acc[f][j][4 * q + 2],
+                                      acc[f][j][4 * q + 3]};
+                if (vec && n + 3 < N) {
+                    *reinterpret_cast<sx8_float4*>(row + n) = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < N) row[n + e] = v[e];
+                }
+            }
+    }
+}
+
+// Y += the St - 1 partial tiles of each split tile Tf .. T - 1 of k_gemm_w1, in range order
+// (deterministic).  One thread per 4 consecutive columns of a tile row.
+__global__ __launch_bounds__(256) void k_reduce_tiles(float* __restrict__ Y, const float* __restrict__ part,
+                                                      int M, int N, int Tf, int n_split, int St) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;     // float4 index
+    constexpr int kQ = kW1BM * kBN / 4;                            // float4s per tile
+    if (i >= (int64_t)n_split * kQ) return;
+    const int ts = (int)(i / kQ);
+    const int e = (int)(i - (int64_t)ts * kQ) * 4;
+    const int t = Tf + ts;
+    const int NB = (N + kBN - 1) / kBN;
+    const int m = (t / NB) * kW1BM + e / kBN;
+    const int n = (t % NB) * kBN + e % kBN;
+    if (m >= M || n >= N) return;
+    const float* p = part + (int64_t)ts * (St - 1) * (kW1BM * kBN) + e;
+    float* y = Y + (int64_t)m * N + n;
+    const int ne = min(4, N - n);
+    sx8_float4 v = sx8_float4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < ne; ++c) v[c] = y[c];
+    for (int s = 0; s < St - 1; ++s) v += *reinterpret_cast<const sx8_float4*>(p + (int64_t)s * (kW1BM * kBN));
+    for (int c = 0; c < ne; ++c) y[c] = v[c];
+}
+
 // Y += partial slices 0 .. S - 2, in slice order (deterministic).  kVec (Y 16-byte aligned,
 // M N a multiple of 4): 4 floats per thread; otherwise one.
 template <bool kVec>
@@ -612,25 +897,97 @@ int32_t check_shape(const char* what, int64_t M, int64_t ldx, int64_t K, int64_t
     return SX8_OK;
 }
 
-// Work split of one call: m-fragments per wave MF (tile rows 128 MF), and S K ranges of
-// kb_per_split blocks (a multiple of 4).  Grids with fewer tiles than the 256 CUs split K
-// (at most 8 ways) and pay (S - 1) M N f32 partials written and read back once.
+// Work split of one call.  k_gemm (w1 = false): tiles of 128 MF rows, S K ranges of
+// kb_per_split blocks (a multiple of 4); grids with fewer tiles than the 256 CUs split K and
+// pay (S - 1) M N f32 partials written and read back once (k_reduce).  k_gemm_w1 (w1 =
+// true): 512-row tiles, the first Tf whole (full rounds of the CUs), the other n_split
+// tiles in St K ranges of kbs blocks (partials added by k_reduce_tiles).
 struct Plan {
-    int MF, S, kb_per_split;
-    int64_t G;
+    bool w1;
+    int MF, S, kb_per_split;   // k_gemm
+    int Tf, St, kbs;           // k_gemm_w1
+    int64_t n_split;           // k_gemm_w1: tiles split St ways
+    int64_t G;                 // work-groups
+    double cost;
 };
 
-Plan plan_gemm(int64_t M, int64_t N, int64_t n_cb) {
-    Plan p;
-    p.MF = M > 128 ? 2 : 1;
-    const int64_t T = ((M + 128 * p.MF - 1) / (128 * p.MF)) * ((N + kBN - 1) / kBN);
+// Costs are in units of one 256-row tile iteration (~0.5 us): rounds of work-groups over the
+// 256 CUs times the K blocks per work-group (a 512-row iteration costs kW1Cost of them, a
+// 128-row one kMF1Cost), plus partial sums written and read once at about 10 KB per CU per
+// unit.
+constexpr double kW1Cost = 1.60, kMF1Cost = 0.62;
+constexpr double kBytesPerUnit = 256.0 * 10240.0;
+
+Plan plan_split(int64_t M, int64_t N, int64_t T, int64_t n_cb, int64_t S, int MF) {
+    Plan p{};
+    p.w1 = false;
+    p.MF = MF;
     const int64_t groups = (n_cb + 3) / 4;
-    int64_t S = T >= 256 ? 1 : (256 + T - 1) / T;
-    S = std::min<int64_t>(std::min<int64_t>(S, 8), groups);
     p.kb_per_split = (int)(4 * ((groups + S - 1) / S));
     p.S = (int)((n_cb + p.kb_per_split - 1) / p.kb_per_split);
     p.G = T * p.S;
+    const double rounds = (double)((p.G + 255) / 256);
+    p.cost = rounds * p.kb_per_split * (MF == 2 ? 1.0 : kMF1Cost) +
+             (double)(p.S - 1) * M * N * 8.0 / kBytesPerUnit;
     return p;
+}
+
+// Tiles of 128 MF rows; the number of K ranges (1..8, at most one per 4-block group) that
+// the cost model prefers.
+Plan plan_k_gemm(int64_t M, int64_t N, int64_t n_cb, int MF) {
+    const int64_t T = ((M + 128 * MF - 1) / (128 * MF)) * ((N + kBN - 1) / kBN);
+    const int64_t groups = (n_cb + 3) / 4;
+    Plan best = plan_split(M, N, T, n_cb, 1, MF);
+    for (int64_t S = 2; S <= std::min<int64_t>(8, groups); ++S) {
+        const Plan p = plan_split(M, N, T, n_cb, S, MF);
+        if (p.cost < best.cost) best = p;
+    }
+    return best;
+}
+
+// 512-row tiles: Tf = 0 (every tile split St ways) or the whole rounds of 256 tiles with
+// the remainder split; St from 1 to 8.
+Plan plan_w1(int64_t M, int64_t N, int64_t n_cb) {
+    const int64_t T = ((M + kW1BM - 1) / kW1BM) * ((N + kBN - 1) / kBN);
+    const int64_t groups = (n_cb + 3) / 4;
+    Plan best{};
+    best.cost = 1e300;
+    for (int64_t Tf : {int64_t(0), T / 256 * 256}) {
+        const int64_t rem = T - Tf;
+        for (int64_t St = 1; St <= std::min<int64_t>(8, groups); ++St) {
+            Plan p{};
+            p.w1 = true;
+            p.MF = kW1MF;
+            p.Tf = (int)Tf;
+            p.kbs = (int)(4 * ((groups + St - 1) / St));
+            p.St = (int)((n_cb + p.kbs - 1) / p.kbs);
+            p.n_split = p.St > 1 ? rem : 0;
+            p.G = Tf + rem * p.St;
+            const double tile_bytes = (double)kW1BM * kBN * 4.0;
+            p.cost = (double)(Tf / 256) * n_cb * kW1Cost +
+                     (double)((rem * p.St + 255) / 256) * p.kbs * kW1Cost +
+                     (p.St > 1 ? (double)rem * (p.St + 1) * tile_bytes * 2.0 / kBytesPerUnit : 0.0);
+            if (p.cost < best.cost) best = p;
+            if (rem == 0) break;
+        }
+    }
+    return best;
+}
+
+// SX8_GEMM_TILE=256 or 512 forces a tile height (tuning); otherwise the cheaper plan.
+Plan plan_gemm(int64_t M, int64_t N, int64_t n_cb) {
+    const int MF = M > 128 ? 2 : 1;
+    const Plan p256 = plan_k_gemm(M, N, n_cb, MF);
+    // k_gemm_w1 addresses rows up to the next multiple of 512 with 31-bit offsets
+    const int64_t Mp = (M + kW1BM - 1) / kW1BM * kW1BM;
+    const bool w1_ok = M > 256 && Mp / 32 * n_cb * 2048 <= 0x7FFFFFFF && Mp * n_cb * 8 <= 0x7FFFFFFF;
+    if (!w1_ok) return p256;
+    const Plan p512 = plan_w1(M, N, n_cb);
+    const char* e = getenv("SX8_GEMM_TILE");
+    const int forced = e ? atoi(e) : 0;
+    if (forced == 256) return p256;
+    if (forced == 512) return p512;
+    return p512.cost < p256.cost ? p512 : p256;
 }
 
 // How the PCA operand reaches the kernel: none (core weights only), computed here from
@@ -647,7 +1004,10 @@ void launch_mf(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, con
 template <bool kSplit, bool kPca, int HB>
 void launch_hb(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, const WeightSrc& w,
                const uint32_t* Zhl, int64_t N, int64_t n_cb, float* Y, float* part) {
-    if (p.MF == 2)
+    if (p.w1)
+        hipLaunchKernelGGL((k_gemm_w1<kSplit, HB, kPca>), dim3((unsigned)p.G), dim3(kW1Threads), 0, st,
+                           Xp, (int)M, w, Zhl, (int)N, (int)n_cb, p.Tf, p.St, p.kbs, Y, part);
+    else if (p.MF == 2)
         launch_mf<kSplit, kPca, HB, 2>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
     else
         launch_mf<kSplit, kPca, HB, 1>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
@@ -666,7 +1026,8 @@ int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, in
     if (p.G > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "%s: grid too large", what);
     const int64_t z_bytes = zm == ZMode::kNone ? 0 : ((M * n_cb * 8 + 255) & ~int64_t(255));
     const int64_t xp_bytes = (M + 31) / 32 * n_cb * 2048;
-    const int64_t part_bytes = (int64_t)(p.S - 1) * M * N * 4;
+    const int64_t part_bytes = p.w1 ? p.n_split * (p.St - 1) * kW1BM * kBN * 4
+                                    : (int64_t)(p.S - 1) * M * N * 4;
     void* v = nullptr;
     int32_t rc = device_workspace(z_bytes + xp_bytes + part_bytes, &v);
     if (rc != SX8_OK) return rc;
@@ -697,7 +1058,11 @@ int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, in
         else
             launch_hb<false, true, 6>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
     }
-    if (p.S > 1) {
+    if (p.w1 && p.n_split > 0) {
+        const int64_t n4 = p.n_split * (kW1BM * kBN / 4);
+        hipLaunchKernelGGL(k_reduce_tiles, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, Y, part,
+                           (int)M, (int)N, p.Tf, (int)p.n_split, p.St);
+    } else if (!p.w1 && p.S > 1) {
         const int64_t MN = M * N;
         if (aligned(Y, 16) && MN % 4 == 0)
             hipLaunchKernelGGL(k_reduce<true>, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0,

@@ -304,14 +304,25 @@ def test_gguf_load_and_r32_ggml(hiplib, oracle, cuda, tmp_path, hdr_bytes):
 # -------------------------------------------------------------------------- GEMM
 
 PREFILL_CASES = [
-    ("q_proj", 4096, 2560, 128), ("k_proj", 1024, 2560, 512), ("down", 2560, 9728, 130),
-    ("odd", 1000, 2560, 7), ("tiny", 64, 96, 1), ("ragged_K", 300, 80, 33),
+    ("q_proj", 4096, 2560, 128, "auto"), ("k_proj", 1024, 2560, 512, "auto"),
+    ("down", 2560, 9728, 130, "auto"), ("odd", 1000, 2560, 7, "auto"), ("tiny", 64, 96, 1, "auto"),
+    ("ragged_K", 300, 80, 33, "auto"),
+    # the 512-row tile kernel (k_gemm_w1), forced: ragged M and N, split K, long K, the
+    # 256-row kernel on the same shape for comparison
+    ("w1_ragged", 1000, 2560, 700, "512"), ("w1_ragged_256", 1000, 2560, 700, "256"),
+    ("w1_q", 4096, 2560, 1024, "512"), ("w1_long_k", 640, 9728, 600, "512"),
+    ("w1_ragged_k", 384, 2080, 513, "512"),
+    # 272 tiles of 512 x 128: one full round of 256, the other 16 split over K (partial tiles
+    # added by the tile reducer)
+    ("w1_tail", 17408, 640, 600, "512"),
 ]
 
 
-@pytest.mark.parametrize("name,N,K,M", PREFILL_CASES)
-def test_prefill_gemm(hiplib, oracle, cuda, name, N, K, M):
+@pytest.mark.parametrize("name,N,K,M,tile", PREFILL_CASES)
+def test_prefill_gemm(hiplib, oracle, cuda, monkeypatch, name, N, K, M, tile):
     import torch
+    if tile != "auto":
+        monkeypatch.setenv("SX8_GEMM_TILE", tile)
     from sx8_decode1_v3 import make_tensors_v44
     from sx8_gemm_compact import _ext, gemm_sx8_compact
     from sx8_fused_wmma import gemm_sx8_wmma_cached, make_tensors, to_kbmajor
