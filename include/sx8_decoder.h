@@ -59,6 +59,29 @@ int64_t sx8_dec_attn_workspace_bytes(int32_t nh, int32_t hd);
 /* out = fp16(silu(g) * u) over n float32 elements. */
 int32_t sx8_dec_silu_mul(const float* g, const float* u, uint16_t* out, int64_t n, void* stream);
 
+/* Decoder GEMVs with their input produced inside the GEMV (no separate launch for it).
+ * No reference counterpart: in scripts/infer_sx8.py:109-173 the Hugging Face modules run
+ * the RMSNorm / SiLU ops and SX8LinearV44.forward (scripts/integrate_fused_v44.py:43-77)
+ * then runs the M = 1 GEMV (sx8_gemv_group above) on their output.
+ *
+ * sx8_dec_gemv_rmsnorm: x = fp16(h * rsqrt(mean(h^2) + eps) * norm_w) with h = (init ? fp16
+ * init : resid) + (delta ? delta : 0) in float32 (K = n_cb * 32 values, as
+ * sx8_dec_add_rmsnorm with M = 1, up to the summation order of mean(h^2)); then Ys[i] =
+ * W_i . x for the n_mats matrices, as sx8_gemv_group.  When resid_out is not NULL it
+ * receives h; it must not alias resid or delta.  State vectors 16-byte aligned.
+ * sx8_dec_gemv_silu: the same with x = fp16(silu(g) * u) (as sx8_dec_silu_mul).
+ * Both need n_cb <= 384 and take bases/scales (no caller Z). */
+int32_t sx8_dec_gemv_rmsnorm(const float* resid, const uint16_t* init, const float* delta,
+                             const uint16_t* norm_w, float eps, float* resid_out, int32_t n_mats,
+                             const uint8_t* const* hdrs, const uint8_t* const* levels,
+                             int32_t hdr_bytes, const float* const* bases,
+                             const float* const* scales, const int64_t* Ns, int64_t n_cb,
+                             float* const* Ys, void* stream);
+int32_t sx8_dec_gemv_silu(const float* g, const float* u, int32_t n_mats,
+                          const uint8_t* const* hdrs, const uint8_t* const* levels,
+                          int32_t hdr_bytes, const float* const* bases, const float* const* scales,
+                          const int64_t* Ns, int64_t n_cb, float* const* Ys, void* stream);
+
 /* *tok = argmax(logits[0..n)) (first index among equal maxima), then *pos += 1. */
 int32_t sx8_dec_argmax_advance(const float* logits, int64_t n, int64_t* tok, int64_t* pos,
                                void* stream);

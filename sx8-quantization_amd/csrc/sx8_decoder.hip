@@ -408,7 +408,16 @@ __global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ g, c
     out[i] = f2h(x / (1.0f + __expf(-x)) * u[i]);
 }
 
-// tok = argmax(logits) (first index among equal maxima), *pos += 1.  One 1024-thread block.
+// tok = argmax(logits) (first index among equal maxima; NaN entries are skipped), *pos += 1.
+// One 1024-thread block; 16-byte loads, eight per thread in flight (the scan is bound by
+// the latency of one CU's loads, 4 B x n).
+__device__ __forceinline__ void arg_better(float x, int64_t i, float& v, int64_t& idx) {
+    if (x > v || (x == v && i < idx)) {
+        v = x;
+        idx = i;
+    }
+}
+
 __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict__ logits, int64_t n,
                                                          int64_t* __restrict__ tok,
                                                          int64_t* __restrict__ pos) {
@@ -416,21 +425,38 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict
     __shared__ int64_t bi[16];
     float v = -INFINITY;
     int64_t idx = INT64_MAX;
-    for (int64_t i = threadIdx.x; i < n; i += 1024) {
-        const float x = logits[i];
-        if (x > v || (x == v && i < idx)) { v = x; idx = i; }
+    constexpr int kU = 8;
+    const int64_t n4 = (reinterpret_cast<uintptr_t>(logits) & 15) == 0 ? n / 4 : 0;
+    const float4* l4 = reinterpret_cast<const float4*>(logits);
+    for (int64_t b = threadIdx.x; b < n4; b += 1024 * kU) {
+        float4 x[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t i4 = b + 1024 * u;
+            x[u] = l4[i4 < n4 ? i4 : n4 - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int64_t i4 = b + 1024 * u;
+            if (i4 < n4) {
+                arg_better(x[u].x, 4 * i4, v, idx);
+                arg_better(x[u].y, 4 * i4 + 1, v, idx);
+                arg_better(x[u].z, 4 * i4 + 2, v, idx);
+                arg_better(x[u].w, 4 * i4 + 3, v, idx);
+            }
+        }
     }
+    for (int64_t i = 4 * n4 + threadIdx.x; i < n; i += 1024) arg_better(logits[i], i, v, idx);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(v, o, 64);
         const int64_t oi = __shfl_xor(idx, o, 64);
-        if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+        arg_better(ov, oi, v, idx);
     }
     if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = v; bi[threadIdx.x >> 6] = idx; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 16; ++w)
-            if (bv[w] > v || (bv[w] == v && bi[w] < idx)) { v = bv[w]; idx = bi[w]; }
+        for (int w = 1; w < 16; ++w) arg_better(bv[w], bi[w], v, idx);
         tok[0] = idx;
         pos[0] += 1;
     }

@@ -310,12 +310,12 @@ struct TabIn {
     float s;
 };
 
-template <int kMode>
+template <int kMode, bool kLoadX = true>
 __device__ __forceinline__ void tab_load(TabIn& t, const uint16_t* __restrict__ X,
                                          const float* __restrict__ basis,
                                          const float* __restrict__ scales,
                                          const float* __restrict__ Zin, int kb, int q) {
-    t.x = *reinterpret_cast<const uint4*>(X + (int64_t)kb * 32 + 8 * q);
+    if constexpr (kLoadX) t.x = *reinterpret_cast<const uint4*>(X + (int64_t)kb * 32 + 8 * q);
     if constexpr (kMode == 1) {
         const float4* b = reinterpret_cast<const float4*>(basis + (int64_t)kb * 64 + 8 * q);
         t.b0[0] = b[0];
@@ -354,6 +354,106 @@ __device__ __forceinline__ void tab_store(KbInfo* info, const TabIn& t, int kb, 
     KbInfo& e = info[ok ? kb : n_cb];
     fill_x_side(e, q, t.x);
     e.z[q & 1] = z;      // q = 2, 3 write the same values as q = 0, 1
+}
+
+// Input producers of the decoder's fused GEMVs: instead of reading x as fp16, every
+// work-group computes it in its table build from the decoder state (K = n_cb * 32).
+//   kXRms:  h = (init ? fp16 init : resid) + (delta ? delta : 0) in f32,
+//           x = fp16(h * (1 / sqrt(sum(h^2) / K + eps)) * w); work-group 0 also stores h to
+//           resid_out (the next residual; it must not alias resid or delta, which the other
+//           work-groups are still reading).
+//   kXSilu: x = fp16(silu(g) * u) = fp16(g / (1 + exp(-g)) * u).
+constexpr int kXPlain = 0, kXRms = 1, kXSilu = 2;
+struct XProd {
+    const float* resid;
+    const uint16_t* init;
+    const float* delta;
+    const uint16_t* w;
+    float* resid_out;
+    const float* g;
+    const float* u;
+    float eps;
+};
+
+// Raw producer inputs of one table unit (kb, q): 8 consecutive elements 32 kb + 8 q.
+// Loaded with buffer loads over resources whose size is zero for an absent input (init,
+// resid or delta), so the loads are unconditional, read zeros for absent inputs and keep
+// their issue order (the table inputs must all be requested before the weight records).
+struct XRaw {
+    float4 a0, a1;   // kXRms: resid, kXSilu: g
+    float4 b0, b1;   // kXRms: delta, kXSilu: u
+    uint4 h16;       // kXRms: init fp16
+    uint4 w;         // kXRms: norm weight fp16
+};
+
+struct XRsrc {
+    sx8_rsrc a, b, h16, w;
+};
+
+template <int kX>
+__device__ __forceinline__ XRsrc xraw_rsrc(const XProd& xp, int K) {
+    XRsrc r;
+    if constexpr (kX == kXRms) {
+        r.a = make_rsrc(xp.resid, xp.resid ? (int64_t)K * 4 : 0);
+        r.b = make_rsrc(xp.delta, xp.delta ? (int64_t)K * 4 : 0);
+        r.h16 = make_rsrc(xp.init, xp.init ? (int64_t)K * 2 : 0);
+        r.w = make_rsrc(xp.w, (int64_t)K * 2);
+    } else {
+        r.a = make_rsrc(xp.g, (int64_t)K * 4);
+        r.b = make_rsrc(xp.u, (int64_t)K * 4);
+    }
+    return r;
+}
+
+__device__ __forceinline__ float4 ld_f4(sx8_rsrc r, uint32_t off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+template <int kX>
+__device__ __forceinline__ void xraw_load(XRaw& r, const XRsrc& rs, int kb, int q) {
+    const uint32_t e = (uint32_t)(kb * 32 + 8 * q);
+    r.a0 = ld_f4(rs.a, e * 4);
+    r.a1 = ld_f4(rs.a, e * 4 + 16);
+    r.b0 = ld_f4(rs.b, e * 4);
+    r.b1 = ld_f4(rs.b, e * 4 + 16);
+    if constexpr (kX == kXRms) {
+        r.h16 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.h16, e * 2, 0, 0));
+        r.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, e * 2, 0, 0));
+    }
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+}
+
+// Sum over a wave64 in a fixed order: DPP butterflies within each row of 16 lanes, then the
+// four row sums (lanes 0, 16, 32, 48) in order.  Uniform result.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl,
+                                                                      0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v = dpp_add<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+    v = dpp_add<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+    v = dpp_add<0x141>(v);   // row_half_mirror
+    v = dpp_add<0x140>(v);   // row_mirror
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return ((r0 + r1) + r2) + r3;
+}
+
+// The 8 residual values h of a unit (kXRms): (init + resid) + delta, one of init and resid
+// absent (zero), delta possibly absent (zero).
+__device__ __forceinline__ void xraw_h(const XRaw& r, float h[8]) {
+    const float a[8] = {r.a0.x, r.a0.y, r.a0.z, r.a0.w, r.a1.x, r.a1.y, r.a1.z, r.a1.w};
+    const float d[8] = {r.b0.x, r.b0.y, r.b0.z, r.b0.w, r.b1.x, r.b1.y, r.b1.z, r.b1.w};
+    const uint32_t hw[4] = {r.h16.x, r.h16.y, r.h16.z, r.h16.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = (sx8_h2f(hw[i >> 1] >> (16 * (i & 1))) + a[i]) + d[i];
 }
 
 // Table passes whose inputs are loaded before the weight records (the rest, for
@@ -400,10 +500,10 @@ struct GemvGroup {
     int n_mats;
 };
 
-template <int HB, int kMode, int NR, int TP>
+template <int HB, int kMode, int NR, int TP, int kX = kXPlain>
 __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     const uint16_t* __restrict__ X, const GemvGroup grp, const KbInfo* __restrict__ table,
-    int n_cb, int CT, int S, int R) {
+    int n_cb, int CT, int S, int R, const XProd xp) {
     extern __shared__ __align__(16) unsigned char smem[];
     float* red = reinterpret_cast<float*>(smem);                 // 2 x 512 floats
     KbInfo* info = reinterpret_cast<KbInfo*>(smem + sizeof(float) * 2 * kPanelThreads);
@@ -438,11 +538,15 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
 
     const int n_units = n_cb * 4;
     TabIn tin[TP];
+    XRaw xr[kX == kXPlain ? 1 : TP];
     if constexpr (kMode == 1 || kMode == 2) {
+        XRsrc xs;
+        if constexpr (kX != kXPlain) xs = xraw_rsrc<kX>(xp, n_cb * 32);
 #pragma unroll
         for (int p = 0; p < TP; ++p) {
             const int u = min(p * kPanelThreads + tid, n_units - 1);
-            tab_load<kMode>(tin[p], X, basis, scales, Zin, u >> 2, u & 3);
+            tab_load<kMode, kX == kXPlain>(tin[p], X, basis, scales, Zin, u >> 2, u & 3);
+            if constexpr (kX != kXPlain) xraw_load<kX>(xr[p], xs, u >> 2, u & 3);
         }
     }
     // issue order = wait order (the memory counter retires loads in order): table
@@ -461,15 +565,71 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
         uint4* dst = reinterpret_cast<uint4*>(info);
         for (int i = tid; i < n_cb * 7; i += kPanelThreads) dst[i] = src[i];
     } else if constexpr (kMode == 1 || kMode == 2) {
+        if constexpr (kX == kXRms) {
+            // every unit fits the TP passes (checked by the host): sum h^2 over the
+            // work-group, then normalize; the sum's order is fixed, so every work-group
+            // produces the same x
+            float h[TP][8];
+            float ss = 0.f;
+#pragma unroll
+            for (int p = 0; p < TP; ++p) {
+                xraw_h(xr[p], h[p]);
+                if (p * kPanelThreads + tid < n_units) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(h[p][i], h[p][i], ss);
+                }
+            }
+            ss = wave_sum(ss);
+            if ((tid & 63) == 0) red[tid >> 6] = ss;
+            __builtin_amdgcn_s_waitcnt(0xC07F);       // lgkmcnt(0): LDS only, records stay in flight
+            asm volatile("s_barrier" ::: "memory");
+            float tot = 0.f;
+#pragma unroll
+            for (int wv = 0; wv < kPanelThreads / 64; ++wv) tot += red[wv];
+            const float inv = 1.0f / sqrtf(tot / (float)(n_cb * 32) + xp.eps);
+            const bool writer = blockIdx.x == 0 && xp.resid_out != nullptr;
+#pragma unroll
+            for (int p = 0; p < TP; ++p) {
+                const uint32_t ww[4] = {xr[p].w.x, xr[p].w.y, xr[p].w.z, xr[p].w.w};
+                uint32_t xw[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    xw[i] = pack_h2(h[p][2 * i] * inv * sx8_h2f(ww[i]),
+                                    h[p][2 * i + 1] * inv * sx8_h2f(ww[i] >> 16));
+                tin[p].x = make_uint4(xw[0], xw[1], xw[2], xw[3]);
+                const int u = p * kPanelThreads + tid;
+                if (writer && u < n_units) {
+                    float4* ro = reinterpret_cast<float4*>(xp.resid_out + (int64_t)u * 8);
+                    ro[0] = make_float4(h[p][0], h[p][1], h[p][2], h[p][3]);
+                    ro[1] = make_float4(h[p][4], h[p][5], h[p][6], h[p][7]);
+                }
+            }
+        } else if constexpr (kX == kXSilu) {
+#pragma unroll
+            for (int p = 0; p < TP; ++p) {
+                const float g8[8] = {xr[p].a0.x, xr[p].a0.y, xr[p].a0.z, xr[p].a0.w,
+                                     xr[p].a1.x, xr[p].a1.y, xr[p].a1.z, xr[p].a1.w};
+                const float u8[8] = {xr[p].b0.x, xr[p].b0.y, xr[p].b0.z, xr[p].b0.w,
+                                     xr[p].b1.x, xr[p].b1.y, xr[p].b1.z, xr[p].b1.w};
+                uint32_t xw[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    xw[i] = pack_h2(g8[2 * i] / (1.0f + __expf(-g8[2 * i])) * u8[2 * i],
+                                    g8[2 * i + 1] / (1.0f + __expf(-g8[2 * i + 1])) * u8[2 * i + 1]);
+                tin[p].x = make_uint4(xw[0], xw[1], xw[2], xw[3]);
+            }
+        }
 #pragma unroll
         for (int p = 0; p < TP; ++p) {
             const int u = p * kPanelThreads + tid;
             tab_store<kMode>(info, tin[p], min(u, n_units - 1) >> 2, u & 3, u < n_units, n_cb);
         }
-        for (int u0 = TP * kPanelThreads; u0 < n_units; u0 += kPanelThreads) {
-            const int u = min(u0 + tid, n_units - 1);
-            tab_load<kMode>(tin[0], X, basis, scales, Zin, u >> 2, u & 3);
-            tab_store<kMode>(info, tin[0], u >> 2, u & 3, u0 + tid < n_units, n_cb);
+        if constexpr (kX == kXPlain) {
+            for (int u0 = TP * kPanelThreads; u0 < n_units; u0 += kPanelThreads) {
+                const int u = min(u0 + tid, n_units - 1);
+                tab_load<kMode>(tin[0], X, basis, scales, Zin, u >> 2, u & 3);
+                tab_store<kMode>(info, tin[0], u >> 2, u & 3, u0 + tid < n_units, n_cb);
+            }
         }
     }
     __syncthreads();
@@ -552,19 +712,19 @@ inline PanelPlan plan_panels(const int64_t* Ns, int n_mats, int n_cb) {
 
 constexpr int kRing = 2;   // record buffers per lane
 
-template <int HB, int kMode>
+template <int HB, int kMode, int kX = kXPlain>
 void launch_panel(const PanelPlan& p, size_t smem, hipStream_t st, const uint16_t* X,
-                  const GemvGroup& g, const KbInfo* table, int n_cb) {
+                  const GemvGroup& g, const KbInfo* table, int n_cb, const XProd& xp = XProd{}) {
     const dim3 grid(p.grid), block(kPanelThreads);
     if constexpr (kMode == 1 || kMode == 2) {
         if (p.TP == kTabPassesLong) {
-            hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesLong>), grid, block,
-                               smem, st, X, g, table, n_cb, p.CT, p.S, p.R);
+            hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesLong, kX>), grid, block,
+                               smem, st, X, g, table, n_cb, p.CT, p.S, p.R, xp);
             return;
         }
     }
-    hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesShort>), grid, block, smem, st,
-                       X, g, table, n_cb, p.CT, p.S, p.R);
+    hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesShort, kX>), grid, block, smem, st,
+                       X, g, table, n_cb, p.CT, p.S, p.R, xp);
 }
 
 // 32-bit buffer offsets: every block index a lane forms stays below 2^31 / 24.
@@ -762,4 +922,107 @@ extern "C" int32_t sx8_gemv_group(const uint16_t* X, int32_t n_mats, const uint8
     if (hdr_bytes == 8)
         return launch_gemv_group<8>(X, n_mats, hdrs, levels, bases, scales, Z_in, Ns, (int)n_cb, Ys, st);
     return launch_gemv_group<6>(X, n_mats, hdrs, levels, bases, scales, Z_in, Ns, (int)n_cb, Ys, st);
+}
+
+// ------------------------------------------------------------------ fused decoder GEMVs
+
+namespace {
+
+// Argument checks shared by the fused entry points; fills the group (bases/scales form).
+int32_t check_fused_group(const char* what, int32_t n_mats, const uint8_t* const* hdrs,
+                          const uint8_t* const* levels, int32_t hdr_bytes, const float* const* bases,
+                          const float* const* scales, const int64_t* Ns, int64_t n_cb,
+                          float* const* Ys) {
+    using namespace sx8;
+    if (!hdrs || !levels || !bases || !scales || !Ns || !Ys) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (n_mats < 1 || n_mats > kMaxGroup)
+        return fail(SX8_ERR_INVALID, "%s: n_mats must be 1..%d, got %d", what, kMaxGroup, n_mats);
+    if (hdr_bytes != 6 && hdr_bytes != 8)
+        return fail(SX8_ERR_INVALID, "%s: hdr_bytes must be 6 or 8, got %d", what, hdr_bytes);
+    // every table unit is produced within the kTabPassesLong up-front passes
+    if (n_cb <= 0 || n_cb * 4 > (int64_t)kTabPassesLong * kPanelThreads)
+        return fail(SX8_ERR_UNSUPPORTED, "%s: n_cb %lld outside 1..%d", what, (long long)n_cb,
+                    kTabPassesLong * kPanelThreads / 4);
+    for (int i = 0; i < n_mats; ++i) {
+        if (!hdrs[i] || !levels[i] || !Ys[i] || !bases[i] || !scales[i])
+            return fail(SX8_ERR_INVALID, "%s: null pointer in matrix %d", what, i);
+        if (Ns[i] <= 0 || Ns[i] > 0x7FFFFFFF / 2)
+            return fail(SX8_ERR_INVALID, "%s: bad N %lld (matrix %d)", what, (long long)Ns[i], i);
+        if (!aligned(hdrs[i], hdr_bytes == 8 ? 8 : 2) || !aligned(levels[i], 8) || !aligned(Ys[i], 4) ||
+            !aligned(bases[i], 16) || !aligned(scales[i], 4))
+            return fail(SX8_ERR_INVALID, "%s: misaligned pointer in matrix %d", what, i);
+    }
+    return SX8_OK;
+}
+
+template <int kX>
+int32_t launch_fused(const char* what, const XProd& xp, int32_t n_mats, const uint8_t* const* hdrs,
+                     const uint8_t* const* levels, int32_t hdr_bytes, const float* const* bases,
+                     const float* const* scales, const int64_t* Ns, int64_t n_cb, float* const* Ys,
+                     hipStream_t st) {
+    using namespace sx8;
+    PanelPlan p = plan_panels(Ns, n_mats, (int)n_cb);
+    GemvGroup g{};
+    g.n_mats = n_mats;
+    for (int i = 0; i < n_mats; ++i) {
+        if (!offsets_fit(p, Ns[i], n_cb))
+            return fail(SX8_ERR_UNSUPPORTED, "%s: %lld x %lld blocks exceed 32-bit offsets", what,
+                        (long long)Ns[i], (long long)n_cb);
+        g.m[i] = GemvMat{hdrs[i], levels[i], bases[i], scales[i], nullptr, Ys[i], (int)Ns[i],
+                         (int)((Ns[i] + p.CT - 1) / p.CT)};
+    }
+    const size_t smem = panel_smem((int)n_cb, true);
+    if (hdr_bytes == 8)
+        launch_panel<8, 1, kX>(p, smem, st, nullptr, g, nullptr, (int)n_cb, xp);
+    else
+        launch_panel<6, 1, kX>(p, smem, st, nullptr, g, nullptr, (int)n_cb, xp);
+    return check_launch(what);
+}
+
+}  // namespace
+
+extern "C" int32_t sx8_dec_gemv_rmsnorm(const float* resid, const uint16_t* init, const float* delta,
+                                        const uint16_t* norm_w, float eps, float* resid_out,
+                                        int32_t n_mats, const uint8_t* const* hdrs,
+                                        const uint8_t* const* levels, int32_t hdr_bytes,
+                                        const float* const* bases, const float* const* scales,
+                                        const int64_t* Ns, int64_t n_cb, float* const* Ys,
+                                        void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_dec_gemv_rmsnorm";
+    if ((!resid && !init) || !norm_w) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if ((resid && !aligned(resid, 16)) || (init && !aligned(init, 16)) || (delta && !aligned(delta, 16)) ||
+        !aligned(norm_w, 16) || (resid_out && !aligned(resid_out, 16)))
+        return fail(SX8_ERR_INVALID, "%s: state vectors must be 16-byte aligned", what);
+    if (resid_out && (resid_out == resid || resid_out == delta))
+        return fail(SX8_ERR_INVALID, "%s: resid_out must not alias resid or delta", what);
+    const int32_t rc = check_fused_group(what, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys);
+    if (rc != SX8_OK) return rc;
+    XProd xp{};
+    xp.resid = init ? nullptr : resid;
+    xp.init = init;
+    xp.delta = delta;
+    xp.w = norm_w;
+    xp.resid_out = resid_out;
+    xp.eps = eps;
+    return launch_fused<kXRms>(what, xp, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys,
+                               as_stream(stream));
+}
+
+extern "C" int32_t sx8_dec_gemv_silu(const float* g, const float* u, int32_t n_mats,
+                                     const uint8_t* const* hdrs, const uint8_t* const* levels,
+                                     int32_t hdr_bytes, const float* const* bases,
+                                     const float* const* scales, const int64_t* Ns, int64_t n_cb,
+                                     float* const* Ys, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_dec_gemv_silu";
+    if (!g || !u) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (!aligned(g, 16) || !aligned(u, 16)) return fail(SX8_ERR_INVALID, "%s: g and u must be 16-byte aligned", what);
+    const int32_t rc = check_fused_group(what, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys);
+    if (rc != SX8_OK) return rc;
+    XProd xp{};
+    xp.g = g;
+    xp.u = u;
+    return launch_fused<kXSilu>(what, xp, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys,
+                                as_stream(stream));
 }

@@ -198,6 +198,7 @@ class SX8Decoder(nn.Module):
         f32 = dict(dtype=torch.float32, device=dev)
         f16 = dict(dtype=torch.float16, device=dev)
         z = {"resid": torch.zeros(1, H, **f32), "h": torch.zeros(H, **f16),
+             "ra": torch.zeros(H, **f32), "rb": torch.zeros(H, **f32),
              "q": torch.zeros(nh * hd, **f32), "k": torch.zeros(nk * hd, **f32),
              "v": torch.zeros(nk * hd, **f32), "qh": torch.zeros(nh * hd, **f16),
              "a": torch.zeros(nh * hd, **f16), "o": torch.zeros(H, **f32),
@@ -212,7 +213,9 @@ class SX8Decoder(nn.Module):
         z["groups"] = []
         for ly in self.layers:
             z["groups"].append((self._group_args((ly.q, ly.k, ly.v), (z["q"], z["k"], z["v"])),
-                                self._group_args((ly.gate, ly.up), (z["g"], z["u"]))))
+                                self._group_args((ly.gate, ly.up), (z["g"], z["u"])),
+                                self._group_args((ly.down,), (z["d"],))))
+        z["head_group"] = self._group_args((self.head,), (z["logits"],))
         self._fz = z
         return z
 
@@ -230,6 +233,21 @@ class SX8Decoder(nn.Module):
         n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
         _L.call("sx8_gemv_group", _L.ptr(x), n, hdrs, lvls, 6, bas, sca, None, ns, n_cb, ys, st)
 
+    @staticmethod
+    def _gemv_rms(args, resid, init, delta, w, resid_out, eps, st):
+        """GEMVs of `args` on RMSNorm((init or resid) + delta) * w, the sum to resid_out."""
+        n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
+        P = _L.ptr
+        _L.call("sx8_dec_gemv_rmsnorm", P(resid) if resid is not None else None,
+                P(init) if init is not None else None, P(delta) if delta is not None else None,
+                P(w), eps, P(resid_out) if resid_out is not None else None, n, hdrs, lvls, 6, bas,
+                sca, ns, n_cb, ys, st)
+
+    @staticmethod
+    def _gemv_silu(args, g, u, st):
+        n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
+        _L.call("sx8_dec_gemv_silu", _L.ptr(g), _L.ptr(u), n, hdrs, lvls, 6, bas, sca, ns, n_cb, ys, st)
+
     def _gemv(self, lin, x, y, st):
         z = self._fz
         hdr, lvl, bas, sca = lin._t44
@@ -239,7 +257,11 @@ class SX8Decoder(nn.Module):
     @torch.no_grad()
     def decode_step_fused(self, tok, pos):
         """decode_step with the per-token ops as single HIP launches (sx8_decoder.h) and the
-        GEMVs called through the C ABI; the residual stream is float32."""
+        GEMVs called through the C ABI; the residual stream is float32.  Each RMSNorm runs
+        inside the GEMV that consumes it (sx8_dec_gemv_rmsnorm: q/k/v, gate/up, lm_head)
+        and SiLU * up inside the down GEMV (sx8_dec_gemv_silu): per layer one launch each
+        for q/k/v, q/k norm + RoPE, attention (two), o, gate/up and down.  The residual
+        ping-pongs between ra and rb (a fused GEMV reads one and writes the other)."""
         cfg = self.cfg
         nh, nk, hd, eps = cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["eps"]
         z = self._fused_setup()
@@ -247,15 +269,13 @@ class SX8Decoder(nn.Module):
         P = _L.ptr
         emb = self.embed(tok)                                       # (1, H) fp16
         L = self.max_len
+        ra, rb = z["ra"], z["rb"]
         for li, ly in enumerate(self.layers):
-            if li == 0:
-                _L.call("sx8_dec_add_rmsnorm", P(z["resid"]), None, P(emb), P(ly.in_norm), P(z["h"]), 1,
-                        cfg["hidden"], eps, st)
-            else:
-                _L.call("sx8_dec_add_rmsnorm", P(z["resid"]), P(z["d"]), None, P(ly.in_norm), P(z["h"]),
-                        1, cfg["hidden"], eps, st)
-            g_qkv, g_gu = z["groups"][li]
-            self._gemv_group(g_qkv, z["h"], st)                     # q, k, v: one launch
+            g_qkv, g_gu, g_dn = z["groups"][li]
+            if li == 0:                                             # h = embedding row
+                self._gemv_rms(g_qkv, None, emb, None, ly.in_norm, rb, eps, st)
+            else:                                                   # h = ra + down output
+                self._gemv_rms(g_qkv, ra, None, z["d"], ly.in_norm, rb, eps, st)
             _L.call("sx8_dec_qk_rope_cache", P(z["q"]), P(z["k"]), P(z["v"]), P(ly.q_norm), P(ly.k_norm),
                     P(self.cos), P(self.sin), P(pos), P(z["qh"]), P(self.k_cache[li]),
                     P(self.v_cache[li]), nh, nk, hd, L, eps, st)
@@ -263,14 +283,9 @@ class SX8Decoder(nn.Module):
                     P(z["a"]), nh, nk, hd, L, 1.0 / math.sqrt(hd), P(z["attn_ws"]),
                     z["attn_ws"].numel() * 4, st)
             self._gemv(ly.o, z["a"], z["o"], st)
-            _L.call("sx8_dec_add_rmsnorm", P(z["resid"]), P(z["o"]), None, P(ly.post_norm), P(z["h"]), 1,
-                    cfg["hidden"], eps, st)
-            self._gemv_group(g_gu, z["h"], st)                      # gate, up: one launch
-            _L.call("sx8_dec_silu_mul", P(z["g"]), P(z["u"]), P(z["m"]), cfg["inter"], st)
-            self._gemv(ly.down, z["m"], z["d"], st)
-        _L.call("sx8_dec_add_rmsnorm", P(z["resid"]), P(z["d"]), None, P(self.final_norm), P(z["h"]), 1,
-                cfg["hidden"], eps, st)
-        self._gemv(self.head, z["h"], z["logits"], st)
+            self._gemv_rms(g_gu, rb, None, z["o"], ly.post_norm, ra, eps, st)   # h = rb + o
+            self._gemv_silu(g_dn, z["g"], z["u"], st)
+        self._gemv_rms(z["head_group"], ra, None, z["d"], self.final_norm, None, eps, st)
         _L.call("sx8_dec_argmax_advance", P(z["logits"]), cfg["vocab"], P(tok), P(pos), st)
         return tok
 

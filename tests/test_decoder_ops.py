@@ -89,3 +89,111 @@ def test_add_rmsnorm_and_silu_mul(hiplib, cuda):
     _L.call("sx8_dec_silu_mul", P(ad), P(bd), P(o), 9728, _L.stream(cuda))
     refm = torch.nn.functional.silu(a) * b
     assert (o.cpu().float() - refm).abs().max().item() <= 2e-3 * refm.abs().max().item()
+
+
+def _group(lins_t, Ns, n_cb, ys):
+    import ctypes
+    n = len(lins_t)
+    P = ctypes.c_void_p * n
+    return (n, P(*[t[0].data_ptr() for t in lins_t]), P(*[t[1].data_ptr() for t in lins_t]),
+            P(*[t[2].data_ptr() for t in lins_t]), P(*[t[3].data_ptr() for t in lins_t]),
+            (ctypes.c_int64 * n)(*Ns), n_cb, P(*[y.data_ptr() for y in ys]))
+
+
+def _mats(cuda, Ns, K, seed):
+    import torch
+    from quantize_sx8 import quantize_tensor
+    from sx8_decode1_v3 import make_tensors_v44
+    out = []
+    for i, N in enumerate(Ns):
+        g = torch.Generator().manual_seed(seed + i)
+        W = (torch.randn(N, K, generator=g) * 0.02).half()
+        qt, bi = quantize_tensor(W, device=cuda, degenerate_frac=0.01, seed=seed + 100 + i)
+        out.append(make_tensors_v44(qt, bi))
+    return out
+
+
+def test_fused_gemv_rmsnorm(hiplib, cuda):
+    """sx8_dec_gemv_rmsnorm against sx8_dec_add_rmsnorm + sx8_gemv_group (q/k/v-like group)."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    K, Ns, eps = 2560, [1024, 512, 300], 1e-6
+    ts = _mats(cuda, Ns, K, 40)
+    g = torch.Generator().manual_seed(7)
+    resid = torch.randn(K, generator=g).to(cuda)
+    delta = torch.randn(K, generator=g).to(cuda)
+    w = (torch.rand(K, generator=g) + 0.5).half().to(cuda)
+    init = torch.randn(K, generator=g).half().to(cuda)
+    for use_init in (False, True):
+        # reference: the two-launch path
+        r_ref = (torch.zeros(1, K) if use_init else resid.cpu().clone().view(1, K)).to(cuda)
+        h16 = torch.empty(1, K, dtype=torch.float16, device=cuda)
+        _L.call("sx8_dec_add_rmsnorm", P(r_ref), None if use_init else P(delta),
+                P(init) if use_init else None, P(w), P(h16), 1, K, eps, st)
+        y_ref = [torch.empty(N, device=cuda) for N in Ns]
+        n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y_ref)
+        _L.call("sx8_gemv_group", P(h16), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, st)
+        # fused
+        r_out = torch.full((K,), float("nan"), device=cuda)
+        y = [torch.empty(N, device=cuda) for N in Ns]
+        n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y)
+        _L.call("sx8_dec_gemv_rmsnorm", None if use_init else P(resid), P(init) if use_init else None,
+                None if use_init else P(delta), P(w), eps, P(r_out), n, hd, lv, 6, bs, sc, ns, n_cb, ys, st)
+        torch.cuda.synchronize()
+        assert torch.equal(r_out.cpu(), r_ref.cpu().view(K))        # h = resid + delta, exact
+        for a, b in zip(y, y_ref):
+            rel = (a - b).abs().max().item() / b.abs().max().item()
+            assert rel <= 1e-5, rel
+    # resid_out may not alias an input still being read by other work-groups
+    with pytest.raises(RuntimeError, match="alias"):
+        _L.call("sx8_dec_gemv_rmsnorm", P(resid), None, P(delta), P(w), eps, P(resid), n, hd, lv, 6, bs,
+                sc, ns, n_cb, ys, st)
+
+
+def test_fused_gemv_silu(hiplib, cuda):
+    """sx8_dec_gemv_silu equals sx8_dec_silu_mul + sx8_gemv_group bit for bit (down-like,
+    K = 9728: three table passes)."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    K, Ns = 9728, [2560]
+    ts = _mats(cuda, Ns, K, 60)
+    g = torch.Generator().manual_seed(8)
+    a = torch.randn(K, generator=g).to(cuda)
+    b = torch.randn(K, generator=g).to(cuda)
+    m = torch.empty(K, dtype=torch.float16, device=cuda)
+    _L.call("sx8_dec_silu_mul", P(a), P(b), P(m), K, st)
+    y_ref = [torch.empty(N, device=cuda) for N in Ns]
+    n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y_ref)
+    _L.call("sx8_gemv_group", P(m), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, st)
+    y = [torch.empty(N, device=cuda) for N in Ns]
+    n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y)
+    _L.call("sx8_dec_gemv_silu", P(a), P(b), n, hd, lv, 6, bs, sc, ns, n_cb, ys, st)
+    torch.cuda.synchronize()
+    assert torch.equal(y[0].cpu(), y_ref[0].cpu())
+    # more K blocks than the up-front table passes hold: refused
+    with pytest.raises(RuntimeError, match="n_cb"):
+        _L.call("sx8_dec_gemv_silu", P(a), P(b), n, hd, lv, 6, bs, sc, ns, 385, ys, st)
+
+
+@pytest.mark.parametrize("n,offset", [(151936, 0), (151937, 1), (5, 0), (4099, 3)])
+def test_argmax_advance(hiplib, cuda, n, offset):
+    import torch
+    import _sx8lib as _L
+    g = torch.Generator().manual_seed(n)
+    buf = torch.randn(n + offset, generator=g)
+    x = buf[offset:]
+    if n > 10:
+        x[n // 3] = 7.5                  # tie: the first index wins
+        x[n - 2] = 7.5
+        x[n // 2] = float("nan")         # skipped
+    xd = buf.to(cuda)[offset:]           # offset 1/3: not 16-byte aligned -> scalar path
+    tok = torch.zeros(1, dtype=torch.int64, device=cuda)
+    pos = torch.full((1,), 41, dtype=torch.int64, device=cuda)
+    _L.call("sx8_dec_argmax_advance", _L.ptr(xd), n, _L.ptr(tok), _L.ptr(pos), _L.stream(cuda))
+    torch.cuda.synchronize()
+    assert tok.item() == int(np.nanargmax(x.numpy()))
+    assert pos.item() == 42
