@@ -53,6 +53,20 @@ int32_t sx8_dec_attn_split(const uint16_t* q, const uint16_t* k_cache, const uin
                            int64_t L, float scale, void* workspace, int64_t workspace_bytes,
                            void* stream);
 
+/* sx8_dec_qk_rope_cache followed by sx8_dec_attn_split in one pass over the cache: the
+ * q/k RMSNorm + RoPE of the raw f32 projections are computed inside the attention
+ * work-groups, and the work-group whose chunk holds *pos writes that position's k and v
+ * into the caches and uses them from registers.  Same arguments as the two calls (cos_t,
+ * sin_t: (L, hd / 2) tables), out (nh*hd) fp16; equal to the two-call form up to the
+ * summation order of the RMSNorm sums.  Positions outside [0, L) write nothing.  No
+ * reference counterpart (the Hugging Face attention module of scripts/infer_sx8.py). */
+int32_t sx8_dec_attn_rope(const float* q_raw, const float* k_raw, const float* v_raw,
+                          const uint16_t* q_norm, const uint16_t* k_norm, const float* cos_t,
+                          const float* sin_t, const int64_t* pos, uint16_t* k_cache,
+                          uint16_t* v_cache, uint16_t* out, int32_t nh, int32_t nk, int32_t hd,
+                          int64_t L, float scale, float eps, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
 /* Workspace bytes of sx8_dec_attn_split. */
 int64_t sx8_dec_attn_workspace_bytes(int32_t nh, int32_t hd);
 

@@ -61,6 +61,8 @@ SIGNATURES = [
     ("sx8_dec_attn_split", _I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I64, ctypes.c_float, _P, _I64,
                                   _P]),
     ("sx8_dec_attn_workspace_bytes", _I64, [_I32, _I32]),
+    ("sx8_dec_attn_rope", _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I64,
+                                 ctypes.c_float, ctypes.c_float, _P, _I64, _P]),
     ("sx8_dec_silu_mul", _I32, [_P, _P, _P, _I64, _P]),
     ("sx8_dec_argmax_advance", _I32, [_P, _I64, _P, _P, _P]),
     ("sx8_dec_gemv_rmsnorm", _I32, [_P, _P, _P, _P, ctypes.c_float, _P, _I32, _P, _P, _I32, _P, _P, _P,

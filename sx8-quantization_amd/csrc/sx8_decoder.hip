@@ -255,12 +255,63 @@ __global__ __launch_bounds__(256) void k_attn_decode(const uint16_t* __restrict_
 constexpr int kAttnChunks = 32;
 constexpr int64_t kAttnSplitMaxL = (int64_t)1 << 20;
 
-template <int HD, int G>
+// Inputs of the RoPE-fused form (kRope): the raw f32 projections and what
+// k_qk_rope_cache takes; the work-group whose chunk holds *pos also writes that
+// position's k and v into the caches.
+struct RopeIn {
+    const float* q_raw;      // (nh, HD)
+    const float* k_raw;      // (nk, HD)
+    const float* v_raw;      // (nk, HD)
+    const uint16_t* qn;      // q RMSNorm weight (HD)
+    const uint16_t* kn;      // k RMSNorm weight (HD)
+    const float* cos_t;      // (L, HD / 2)
+    const float* sin_t;
+    uint16_t* k_out;         // k_cache, written at *pos
+    uint16_t* v_out;         // v_cache
+    float eps;
+};
+
+// RMSNorm over one head row of HD values held 8 per lane by the CH = HD / 8 lanes of a
+// lane group (lane c: dims 8c .. 8c + 7), fp16 rounding, then rotate-half RoPE at row
+// `pos` of the tables: dim d < HD / 2 pairs with d + HD / 2, i.e. lane c with c ^ (CH / 2).
+// Returns the fp16-rounded results (as k_qk_rope_cache stores them) in o.
+template <int HD>
+__device__ __forceinline__ void norm_rope8(const float* __restrict__ src, const uint16_t* __restrict__ w,
+                                           const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                           int64_t pos, int c, float eps, float o[8]) {
+    constexpr int CH = HD / 8, half = HD / 2;
+    const float4 a = *reinterpret_cast<const float4*>(src + 8 * c);
+    const float4 b = *reinterpret_cast<const float4*>(src + 8 * c + 4);
+    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+#pragma unroll
+    for (int m = CH / 2; m > 0; m >>= 1) ss += __shfl_xor(ss, m, CH);
+    const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
+    const sx8_u32x4 wv = *reinterpret_cast<const sx8_u32x4*>(w + 8 * c);
+    float nv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        nv[e] = h2f(f2h(x[e] * inv * h2f((uint16_t)(wv[e >> 1] >> (16 * (e & 1))))));
+    const bool lo = c < CH / 2;
+    const int d0 = (lo ? 8 * c : 8 * c - half);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float other = __shfl_xor(nv[e], CH / 2, CH);
+        const float cs = cos_t[pos * half + d0 + e], sn = sin_t[pos * half + d0 + e];
+        // first half: n1 c - n2 s; second half: n2 c + n1 s (own value is n2, partner n1)
+        o[e] = h2f(f2h(lo ? nv[e] * cs - other * sn : nv[e] * cs + other * sn));
+    }
+}
+
+template <int HD, int G, bool kRope = false>
 __global__ __launch_bounds__(256) void k_attn_split(const uint16_t* __restrict__ q,
                                                     const uint16_t* __restrict__ k_cache,
                                                     const uint16_t* __restrict__ v_cache,
                                                     const int64_t* __restrict__ pos_p,
-                                                    float* __restrict__ part, int L, float scale) {
+                                                    float* __restrict__ part, int L, float scale,
+                                                    const RopeIn ri = RopeIn{}) {
     constexpr int CH = HD / 8;
     constexpr int PG = 256 / CH;
     constexpr int kU = 4;
@@ -273,13 +324,40 @@ __global__ __launch_bounds__(256) void k_attn_split(const uint16_t* __restrict__
     const int jb = chunk * T, je = min(jb + T, n);
     const int tid = threadIdx.x, c = tid % CH, pg = tid / CH;
     float qv[G][8];
+    // kRope: the new position's row (pos inside the cache and inside this chunk) comes from
+    // registers, not from the cache this launch is writing
+    const bool own_new = kRope && pos >= 0 && pos < L && pos >= jb && pos < je;
+    sx8_u32x4 knew = sx8_u32x4{0u, 0u, 0u, 0u}, vnew = knew;
+    if constexpr (kRope) {
+        const int64_t pr = min(max(pos, (int64_t)0), (int64_t)L - 1);   // table row
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const sx8_u32x4 x = *reinterpret_cast<const sx8_u32x4*>(q + (kv * G + g) * HD + 8 * c);
+        for (int g = 0; g < G; ++g)
+            norm_rope8<HD>(ri.q_raw + (kv * G + g) * HD, ri.qn, ri.cos_t, ri.sin_t, pr, c, ri.eps, qv[g]);
+        if (own_new) {
+            float kf[8];
+            norm_rope8<HD>(ri.k_raw + kv * HD, ri.kn, ri.cos_t, ri.sin_t, pr, c, ri.eps, kf);
+            const float4 va = *reinterpret_cast<const float4*>(ri.v_raw + kv * HD + 8 * c);
+            const float4 vb = *reinterpret_cast<const float4*>(ri.v_raw + kv * HD + 8 * c + 4);
+            const float vf8[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            qv[g][2 * e] = h2f(x[e] & 0xFFFFu);
-            qv[g][2 * e + 1] = h2f(x[e] >> 16);
+            for (int e = 0; e < 4; ++e) {
+                knew[e] = (uint32_t)f2h(kf[2 * e]) | ((uint32_t)f2h(kf[2 * e + 1]) << 16);
+                vnew[e] = (uint32_t)f2h(vf8[2 * e]) | ((uint32_t)f2h(vf8[2 * e + 1]) << 16);
+            }
+            if (pg == 0) {
+                *reinterpret_cast<sx8_u32x4*>(ri.k_out + ((int64_t)kv * L + pos) * HD + 8 * c) = knew;
+                *reinterpret_cast<sx8_u32x4*>(ri.v_out + ((int64_t)kv * L + pos) * HD + 8 * c) = vnew;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const sx8_u32x4 x = *reinterpret_cast<const sx8_u32x4*>(q + (kv * G + g) * HD + 8 * c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                qv[g][2 * e] = h2f(x[e] & 0xFFFFu);
+                qv[g][2 * e + 1] = h2f(x[e] >> 16);
+            }
         }
     }
     const uint16_t* kc = k_cache + (int64_t)kv * L * HD;
@@ -300,6 +378,16 @@ __global__ __launch_bounds__(256) void k_attn_split(const uint16_t* __restrict__
 #pragma unroll
         for (int u = 0; u < kU; ++u)
             vr[u] = *reinterpret_cast<const sx8_u32x4*>(vc + (int64_t)min(j0 + u * PG, je - 1) * HD + 8 * c);
+        if constexpr (kRope) {
+            if (own_new) {
+#pragma unroll
+                for (int u = 0; u < kU; ++u)
+                    if (min(j0 + u * PG, je - 1) == pos) {
+                        kr[u] = knew;
+                        vr[u] = vnew;
+                    }
+            }
+        }
         float s[kU][G];
 #pragma unroll
         for (int u = 0; u < kU; ++u)
@@ -549,6 +637,46 @@ extern "C" int32_t sx8_dec_attn_split(const uint16_t* q, const uint16_t* k_cache
     }
 #undef SX8_ATTN
     return check_launch("sx8_dec_attn_split");
+}
+
+extern "C" int32_t sx8_dec_attn_rope(const float* q_raw, const float* k_raw, const float* v_raw,
+                                     const uint16_t* q_norm, const uint16_t* k_norm, const float* cos_t,
+                                     const float* sin_t, const int64_t* pos, uint16_t* k_cache,
+                                     uint16_t* v_cache, uint16_t* out, int32_t nh, int32_t nk, int32_t hd,
+                                     int64_t L, float scale, float eps, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_dec_attn_rope";
+    if (!q_raw || !k_raw || !v_raw || !q_norm || !k_norm || !cos_t || !sin_t || !pos || !k_cache ||
+        !v_cache || !out || !workspace)
+        return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    const int G = nk > 0 ? nh / nk : 0;
+    if (nh <= 0 || nk <= 0 || nh % nk || (G != 1 && G != 2 && G != 4 && G != 8) ||
+        (hd != 64 && hd != 128) || L <= 0 || L > kAttnSplitMaxL)
+        return fail(SX8_ERR_INVALID, "%s: bad shape (nh / nk in {1, 2, 4, 8}, hd 64 or 128, cache length "
+                                     "<= %lld)", what, (long long)kAttnSplitMaxL);
+    if (workspace_bytes < sx8_dec_attn_workspace_bytes(nh, hd) || !aligned(workspace, 16))
+        return fail(SX8_ERR_INVALID, "%s: workspace needs %lld bytes, 16-byte aligned", what,
+                    (long long)sx8_dec_attn_workspace_bytes(nh, hd));
+    if (!aligned(q_raw, 16) || !aligned(k_raw, 16) || !aligned(v_raw, 16) || !aligned(q_norm, 16) ||
+        !aligned(k_norm, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
+        return fail(SX8_ERR_INVALID, "%s: projections, norm weights and caches must be 16-byte aligned", what);
+    RopeIn ri{q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, k_cache, v_cache, eps};
+    float* part = reinterpret_cast<float*>(workspace);
+    const hipStream_t st = as_stream(stream);
+    const dim3 grid((unsigned)(nk * kAttnChunks));
+#define SX8_ATTN(HDV, GV)                                                                               \
+    hipLaunchKernelGGL((k_attn_split<HDV, GV, true>), grid, dim3(256), 0, st, nullptr, k_cache, v_cache, \
+                       pos, part, (int)L, scale, ri)
+    if (hd == 128) {
+        if (G == 1) SX8_ATTN(128, 1); else if (G == 2) SX8_ATTN(128, 2); else if (G == 4) SX8_ATTN(128, 4); else SX8_ATTN(128, 8);
+        hipLaunchKernelGGL(k_attn_combine<128>, dim3((unsigned)nh), dim3(128), 0, st, part, out);
+    } else {
+        if (G == 1) SX8_ATTN(64, 1); else if (G == 2) SX8_ATTN(64, 2); else if (G == 4) SX8_ATTN(64, 4); else SX8_ATTN(64, 8);
+        hipLaunchKernelGGL(k_attn_combine<64>, dim3((unsigned)nh), dim3(64), 0, st, part, out);
+    }
+#undef SX8_ATTN
+    return check_launch(what);
 }
 
 extern "C" int32_t sx8_dec_silu_mul(const float* g, const float* u, uint16_t* out, int64_t n, void* stream) {

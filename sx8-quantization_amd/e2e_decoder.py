@@ -259,8 +259,9 @@ class SX8Decoder(nn.Module):
         """decode_step with the per-token ops as single HIP launches (sx8_decoder.h) and the
         GEMVs called through the C ABI; the residual stream is float32.  Each RMSNorm runs
         inside the GEMV that consumes it (sx8_dec_gemv_rmsnorm: q/k/v, gate/up, lm_head)
-        and SiLU * up inside the down GEMV (sx8_dec_gemv_silu): per layer one launch each
-        for q/k/v, q/k norm + RoPE, attention (two), o, gate/up and down.  The residual
+        and SiLU * up inside the down GEMV (sx8_dec_gemv_silu); q/k norm + RoPE + KV-cache
+        write inside attention (sx8_dec_attn_rope): per layer one launch each for q/k/v,
+        attention (two: chunks, combine), o, gate/up and down.  The residual
         ping-pongs between ra and rb (a fused GEMV reads one and writes the other)."""
         cfg = self.cfg
         nh, nk, hd, eps = cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["eps"]
@@ -276,11 +277,10 @@ class SX8Decoder(nn.Module):
                 self._gemv_rms(g_qkv, None, emb, None, ly.in_norm, rb, eps, st)
             else:                                                   # h = ra + down output
                 self._gemv_rms(g_qkv, ra, None, z["d"], ly.in_norm, rb, eps, st)
-            _L.call("sx8_dec_qk_rope_cache", P(z["q"]), P(z["k"]), P(z["v"]), P(ly.q_norm), P(ly.k_norm),
-                    P(self.cos), P(self.sin), P(pos), P(z["qh"]), P(self.k_cache[li]),
-                    P(self.v_cache[li]), nh, nk, hd, L, eps, st)
-            _L.call("sx8_dec_attn_split", P(z["qh"]), P(self.k_cache[li]), P(self.v_cache[li]), P(pos),
-                    P(z["a"]), nh, nk, hd, L, 1.0 / math.sqrt(hd), P(z["attn_ws"]),
+            # q/k norm + RoPE + KV-cache write inside the attention pass
+            _L.call("sx8_dec_attn_rope", P(z["q"]), P(z["k"]), P(z["v"]), P(ly.q_norm), P(ly.k_norm),
+                    P(self.cos), P(self.sin), P(pos), P(self.k_cache[li]), P(self.v_cache[li]),
+                    P(z["a"]), nh, nk, hd, L, 1.0 / math.sqrt(hd), eps, P(z["attn_ws"]),
                     z["attn_ws"].numel() * 4, st)
             self._gemv(ly.o, z["a"], z["o"], st)
             self._gemv_rms(g_gu, rb, None, z["o"], ly.post_norm, ra, eps, st)   # h = rb + o

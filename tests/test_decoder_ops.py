@@ -197,3 +197,57 @@ def test_argmax_advance(hiplib, cuda, n, offset):
     torch.cuda.synchronize()
     assert tok.item() == int(np.nanargmax(x.numpy()))
     assert pos.item() == 42
+
+
+@pytest.mark.parametrize("nh,nk,hd,L,positions", [
+    (32, 8, 128, 1024, [0, 31, 32, 700, 1023]),
+    (16, 16, 64, 300, [0, 5, 299]),
+])
+def test_attn_rope_matches_two_calls(hiplib, cuda, nh, nk, hd, L, positions):
+    """sx8_dec_attn_rope against sx8_dec_qk_rope_cache + sx8_dec_attn_split: the new k/v rows
+    written into the caches, every other row untouched, and the attention output (the two
+    forms differ only in the summation order of the q/k RMSNorm sums)."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    g = torch.Generator().manual_seed(nh * 7 + L)
+    half = hd // 2
+    inv = 1.0 / (1e6 ** (torch.arange(half, dtype=torch.float32) / half))
+    ang = torch.arange(L, dtype=torch.float32)[:, None] * inv[None]
+    cos, sin = ang.cos().to(cuda), ang.sin().to(cuda)
+    qn = (torch.rand(hd, generator=g) + 0.5).half().to(cuda)
+    kn = (torch.rand(hd, generator=g) + 0.5).half().to(cuda)
+    ws_n = int(_L.lib().sx8_dec_attn_workspace_bytes(nh, hd)) // 4 + 64
+    base_k = (torch.randn(nk, L, hd, generator=g) * 0.5).half()
+    base_v = torch.randn(nk, L, hd, generator=g).half()
+    for p in positions:
+        q = torch.randn(nh * hd, generator=g).to(cuda)
+        k = torch.randn(nk * hd, generator=g).to(cuda)
+        v = torch.randn(nk * hd, generator=g).to(cuda)
+        pos = torch.full((1,), p, dtype=torch.int64, device=cuda)
+        # two calls
+        kc1, vc1 = base_k.clone().to(cuda), base_v.clone().to(cuda)
+        qh = torch.empty(nh * hd, dtype=torch.float16, device=cuda)
+        out1 = torch.empty(nh * hd, dtype=torch.float16, device=cuda)
+        ws1 = torch.zeros(ws_n, device=cuda)
+        _L.call("sx8_dec_qk_rope_cache", P(q), P(k), P(v), P(qn), P(kn), P(cos), P(sin), P(pos), P(qh),
+                P(kc1), P(vc1), nh, nk, hd, L, 1e-6, st)
+        _L.call("sx8_dec_attn_split", P(qh), P(kc1), P(vc1), P(pos), P(out1), nh, nk, hd, L,
+                1.0 / math.sqrt(hd), P(ws1), ws_n * 4, st)
+        # fused
+        kc2, vc2 = base_k.clone().to(cuda), base_v.clone().to(cuda)
+        out2 = torch.empty(nh * hd, dtype=torch.float16, device=cuda)
+        ws2 = torch.zeros(ws_n, device=cuda)
+        _L.call("sx8_dec_attn_rope", P(q), P(k), P(v), P(qn), P(kn), P(cos), P(sin), P(pos), P(kc2), P(vc2),
+                P(out2), nh, nk, hd, L, 1.0 / math.sqrt(hd), 1e-6, P(ws2), ws_n * 4, st)
+        torch.cuda.synchronize()
+        kc1, vc1, kc2, vc2 = kc1.cpu(), vc1.cpu(), kc2.cpu(), vc2.cpu()
+        keep = torch.ones(L, dtype=torch.bool)
+        keep[p] = False
+        assert torch.equal(kc2[:, keep], base_k[:, keep]) and torch.equal(vc2[:, keep], base_v[:, keep])
+        assert torch.equal(vc2[:, p], vc1[:, p])
+        dk = (kc2[:, p].float() - kc1[:, p].float()).abs().max().item()
+        assert dk <= 2e-3 * kc1[:, p].float().abs().max().item(), dk
+        o1, o2 = out1.cpu().float(), out2.cpu().float()
+        assert (o1 - o2).abs().max().item() <= 5e-3 * o1.abs().max().item()
