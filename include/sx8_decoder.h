@@ -33,6 +33,17 @@ int32_t sx8_dec_qk_rope_cache(const float* q_raw, const float* k_raw, const floa
                               uint16_t* k_cache, uint16_t* v_cache, int32_t nh, int32_t nk,
                               int32_t hd, int64_t L, float eps, void* stream);
 
+/* The same for `rows` consecutive tokens at positions *pos .. *pos + rows - 1 (a prompt):
+ * q_raw (rows, nh*hd), k_raw / v_raw (rows, nk*hd) float32, q_out (rows, nh*hd) fp16;
+ * token y is what sx8_dec_qk_rope_cache computes at position *pos + y.  No reference
+ * counterpart (the Hugging Face attention module's prompt pass, scripts/infer_sx8.py). */
+int32_t sx8_dec_qk_rope_cache_rows(const float* q_raw, const float* k_raw, const float* v_raw,
+                                   const uint16_t* q_norm, const uint16_t* k_norm,
+                                   const float* cos_t, const float* sin_t, const int64_t* pos,
+                                   int64_t rows, uint16_t* q_out, uint16_t* k_cache,
+                                   uint16_t* v_cache, int32_t nh, int32_t nk, int32_t hd,
+                                   int64_t L, float eps, void* stream);
+
 /* Decode attention of one token: for each of nh query heads (kv head = h / (nh/nk)),
  * softmax(scale * q . K[0..*pos]) . V[0..*pos] over the caches written by
  * sx8_dec_qk_rope_cache; out (nh*hd) fp16.  hd 64 or 128, L <= 4096, q and caches

@@ -99,8 +99,14 @@ __global__ __launch_bounds__(128) void k_qk_rope_cache(const float* __restrict__
                                                        uint16_t* __restrict__ v_cache, int nh,
                                                        int nk, int hd, int L, float eps) {
     __shared__ float red[2];
-    const int64_t pos = *pos_p;
+    // row y of a multi-row call: token y at position *pos + y, inputs and q_out offset by y rows
+    const int y = blockIdx.y;
+    const int64_t pos = *pos_p + y;
     if (pos < 0 || pos >= L) return;         // position outside the cache: nothing to write
+    q_raw += (int64_t)y * nh * hd;
+    k_raw += (int64_t)y * nk * hd;
+    v_raw += (int64_t)y * nk * hd;
+    q_out += (int64_t)y * nh * hd;
     const int half = hd >> 1;
     const int d = threadIdx.x;
     const int b = blockIdx.x;
@@ -580,6 +586,25 @@ extern "C" int32_t sx8_dec_qk_rope_cache(const float* q_raw, const float* k_raw,
                        as_stream(stream), q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, pos,
                        q_out, k_cache, v_cache, nh, nk, hd, (int)L, eps);
     return check_launch("sx8_dec_qk_rope_cache");
+}
+
+extern "C" int32_t sx8_dec_qk_rope_cache_rows(const float* q_raw, const float* k_raw, const float* v_raw,
+                                              const uint16_t* q_norm, const uint16_t* k_norm,
+                                              const float* cos_t, const float* sin_t, const int64_t* pos,
+                                              int64_t rows, uint16_t* q_out, uint16_t* k_cache,
+                                              uint16_t* v_cache, int32_t nh, int32_t nk, int32_t hd,
+                                              int64_t L, float eps, void* stream) {
+    using namespace sx8;
+    if (!q_raw || !k_raw || !v_raw || !q_norm || !k_norm || !cos_t || !sin_t || !pos || !q_out ||
+        !k_cache || !v_cache)
+        return fail(SX8_ERR_INVALID, "sx8_dec_qk_rope_cache_rows: null pointer");
+    if (nh <= 0 || nk <= 0 || nh % nk || hd <= 0 || (hd & 1) || hd > 256 || L <= 0 || L > 0x7FFFFFFF ||
+        rows <= 0 || rows > 65535)
+        return fail(SX8_ERR_INVALID, "sx8_dec_qk_rope_cache_rows: bad shape (hd even, <= 256, rows 1..65535)");
+    hipLaunchKernelGGL(k_qk_rope_cache, dim3((unsigned)(nh + 2 * nk), (unsigned)rows), dim3(hd > 128 ? 128 : 64),
+                       0, as_stream(stream), q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, pos,
+                       q_out, k_cache, v_cache, nh, nk, hd, (int)L, eps);
+    return check_launch("sx8_dec_qk_rope_cache_rows");
 }
 
 extern "C" int32_t sx8_dec_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,

@@ -156,6 +156,81 @@ class SX8Decoder(nn.Module):
         logits = self.head(_rms(x[-1:], self.final_norm, eps))
         return logits.float().argmax(-1)
 
+    def _prefill_bufs(self, T):
+        """Activation buffers of prefill_fused for T tokens (built once per T)."""
+        pb = getattr(self, "_pb", None)
+        if pb is not None and pb["T"] == T:
+            return pb
+        cfg, dev = self.cfg, self.device
+        H, nh, nk, hd, I = cfg["hidden"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["inter"]
+        f32 = dict(dtype=torch.float32, device=dev)
+        f16 = dict(dtype=torch.float16, device=dev)
+        pb = {"T": T, "resid": torch.empty(T, H, **f32), "h": torch.empty(T, H, **f16),
+              "q": torch.empty(T, nh * hd, **f32), "k": torch.empty(T, nk * hd, **f32),
+              "v": torch.empty(T, nk * hd, **f32), "qh": torch.empty(T, nh, hd, **f16),
+              "o": torch.empty(T, H, **f32), "g": torch.empty(T, I, **f32), "u": torch.empty(T, I, **f32),
+              "m": torch.empty(T, I, **f16), "d": torch.empty(T, H, **f32),
+              "pos0": torch.zeros(1, dtype=torch.int64, device=dev),
+              "logits": torch.empty(cfg["vocab"], **f32), "tok": torch.zeros(1, dtype=torch.int64, device=dev),
+              "scratch_pos": torch.zeros(1, dtype=torch.int64, device=dev)}
+        pb["head_group"] = self._group_args((self.head,), (pb["logits"],))
+        self._pb = pb
+        return pb
+
+    @staticmethod
+    def _gemm(lin, X, Y, st):
+        """Y (M, N) f32 = X (M, K) fp16 . W^T through sx8_gemm_prefill."""
+        hdr, lvl, bas, sca = lin._t44
+        M, K = X.shape
+        _L.call("sx8_gemm_prefill", _L.ptr(X), M, K, K, _L.ptr(hdr), _L.ptr(lvl), 6, _L.ptr(bas),
+                _L.ptr(sca), lin.out_f, lin.qt["n_cb"], _L.ptr(Y), st)
+
+    @torch.no_grad()
+    def prefill_fused(self, ids):
+        """prefill() with the library ops over the T prompt rows: add + RMSNorm
+        (sx8_dec_add_rmsnorm, M = T), the prefill GEMMs into preallocated buffers, q/k
+        norm + RoPE + KV-cache write (sx8_dec_qk_rope_cache_rows), SiLU * up
+        (sx8_dec_silu_mul) and the final norm inside the lm_head GEMV; attention stays the
+        float32 SDPA of prefill().  The residual stream is float32."""
+        cfg = self.cfg
+        H, nh, nk, hd, eps = cfg["hidden"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["eps"]
+        T = ids.shape[0]
+        pb = self._prefill_bufs(T)
+        st = _L.stream(self.device)
+        P = _L.ptr
+        emb = self.embed(ids)                                      # (T, H) fp16
+        rep = nh // nk
+        for li, ly in enumerate(self.layers):
+            if li == 0:
+                _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), None, P(emb), P(ly.in_norm), P(pb["h"]), T, H,
+                        eps, st)
+            else:
+                _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["d"]), None, P(ly.in_norm), P(pb["h"]), T,
+                        H, eps, st)
+            self._gemm(ly.q, pb["h"], pb["q"], st)
+            self._gemm(ly.k, pb["h"], pb["k"], st)
+            self._gemm(ly.v, pb["h"], pb["v"], st)
+            _L.call("sx8_dec_qk_rope_cache_rows", P(pb["q"]), P(pb["k"]), P(pb["v"]), P(ly.q_norm),
+                    P(ly.k_norm), P(self.cos), P(self.sin), P(pb["pos0"]), T, P(pb["qh"]),
+                    P(self.k_cache[li]), P(self.v_cache[li]), nh, nk, hd, self.max_len, eps, st)
+            qf = pb["qh"].permute(1, 0, 2).float().contiguous()                 # (nh, T, hd)
+            kf = self.k_cache[li][:, :T].float().repeat_interleave(rep, 0).contiguous()
+            vf = self.v_cache[li][:, :T].float().repeat_interleave(rep, 0).contiguous()
+            a = torch.nn.functional.scaled_dot_product_attention(qf[None], kf[None], vf[None],
+                                                                 is_causal=True)[0]
+            self._gemm(ly.o, a.permute(1, 0, 2).reshape(T, nh * hd).half(), pb["o"], st)
+            _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["o"]), None, P(ly.post_norm), P(pb["h"]), T,
+                    H, eps, st)
+            self._gemm(ly.gate, pb["h"], pb["g"], st)
+            self._gemm(ly.up, pb["h"], pb["u"], st)
+            _L.call("sx8_dec_silu_mul", P(pb["g"]), P(pb["u"]), P(pb["m"]), T * cfg["inter"], st)
+            self._gemm(ly.down, pb["m"], pb["d"], st)
+        # last row: residual + down output, final norm and lm_head in one launch
+        self._gemv_rms(pb["head_group"], pb["resid"][T - 1], None, pb["d"][T - 1], self.final_norm, None,
+                       eps, st)
+        _L.call("sx8_dec_argmax_advance", P(pb["logits"]), cfg["vocab"], P(pb["tok"]), P(pb["scratch_pos"]), st)
+        return pb["tok"].clone()
+
     # ---------------------------------------------------------------- decode
     @torch.no_grad()
     def decode_step(self, tok, pos):
@@ -299,7 +374,7 @@ class SX8Decoder(nn.Module):
         assert T + n_new <= self.max_len
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        first = self.prefill(ids)
+        first = self.prefill_fused(ids) if fused else self.prefill(ids)
         torch.cuda.synchronize()
         t_prefill = time.perf_counter() - t0
         tok = first.clone()

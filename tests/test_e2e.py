@@ -62,6 +62,15 @@ def test_e2e_prefill_decode_graph(hiplib, cuda):
     first = dec.prefill(ids)
     ref_last = ref[-1]
     assert ref_last[first[0]] >= ref_last.max() - 2e-2 * ref_last.abs().max()
+    kc = [c[:, :len(ids)].float().clone() for c in dec.k_cache]
+    vc = [c[:, :len(ids)].float().clone() for c in dec.v_cache]
+    # the library-op prefill: same token rule, and the KV rows it writes agree with the
+    # torch prefill's (both round the normalized, rotated k and v to fp16)
+    first_f = dec.prefill_fused(ids)
+    assert ref_last[first_f[0]] >= ref_last.max() - 2e-2 * ref_last.abs().max()
+    for li in range(len(dec.layers)):
+        for a, b in ((dec.k_cache[li][:, :len(ids)].float(), kc[li]), (dec.v_cache[li][:, :len(ids)].float(), vc[li])):
+            assert (a - b).abs().max().item() <= 1e-2 * b.abs().max().item(), li
     # decode: graph replay and eager steps give the same tokens, for the torch-op step
     # and for the fused step (HIP decoder ops); each token is (near-)argmax of the fp32
     # reference over the sequence it extends
