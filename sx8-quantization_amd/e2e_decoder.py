@@ -20,6 +20,7 @@ import math
 import time
 
 import torch
+import torch.nn.attention
 import torch.nn as nn
 
 import _sx8lib as _L
@@ -178,6 +179,20 @@ class SX8Decoder(nn.Module):
         return pb
 
     @staticmethod
+    def _prefill_attn(qh, kc, vc, rep):
+        """Causal attention of the T prompt rows: qh (T, nh, hd) fp16, kc / vc (nk, T, hd)
+        fp16 views of the caches; returns (T, nh * hd) fp16.  fp16 flash attention (fp32
+        accumulation inside) with the flash backend forced, so a configuration it does not
+        cover raises instead of running the math path."""
+        T, nh, hd = qh.shape
+        q = qh.permute(1, 0, 2)[None]                                          # (1, nh, T, hd)
+        k = kc.repeat_interleave(rep, 0)[None]
+        v = vc.repeat_interleave(rep, 0)[None]
+        with torch.nn.attention.sdpa_kernel(torch.nn.attention.SDPBackend.FLASH_ATTENTION):
+            a = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True)[0]
+        return a.permute(1, 0, 2).reshape(T, nh * hd)
+
+    @staticmethod
     def _gemm(lin, X, Y, st):
         """Y (M, N) f32 = X (M, K) fp16 . W^T through sx8_gemm_prefill."""
         hdr, lvl, bas, sca = lin._t44
@@ -190,8 +205,8 @@ class SX8Decoder(nn.Module):
         """prefill() with the library ops over the T prompt rows: add + RMSNorm
         (sx8_dec_add_rmsnorm, M = T), the prefill GEMMs into preallocated buffers, q/k
         norm + RoPE + KV-cache write (sx8_dec_qk_rope_cache_rows), SiLU * up
-        (sx8_dec_silu_mul) and the final norm inside the lm_head GEMV; attention stays the
-        float32 SDPA of prefill().  The residual stream is float32."""
+        (sx8_dec_silu_mul) and the final norm inside the lm_head GEMV; attention is fp16
+        flash attention over the cache rows (_prefill_attn).  The residual stream is float32."""
         cfg = self.cfg
         H, nh, nk, hd, eps = cfg["hidden"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["eps"]
         T = ids.shape[0]
@@ -213,12 +228,8 @@ class SX8Decoder(nn.Module):
             _L.call("sx8_dec_qk_rope_cache_rows", P(pb["q"]), P(pb["k"]), P(pb["v"]), P(ly.q_norm),
                     P(ly.k_norm), P(self.cos), P(self.sin), P(pb["pos0"]), T, P(pb["qh"]),
                     P(self.k_cache[li]), P(self.v_cache[li]), nh, nk, hd, self.max_len, eps, st)
-            qf = pb["qh"].permute(1, 0, 2).float().contiguous()                 # (nh, T, hd)
-            kf = self.k_cache[li][:, :T].float().repeat_interleave(rep, 0).contiguous()
-            vf = self.v_cache[li][:, :T].float().repeat_interleave(rep, 0).contiguous()
-            a = torch.nn.functional.scaled_dot_product_attention(qf[None], kf[None], vf[None],
-                                                                 is_causal=True)[0]
-            self._gemm(ly.o, a.permute(1, 0, 2).reshape(T, nh * hd).half(), pb["o"], st)
+            a = self._prefill_attn(pb["qh"], self.k_cache[li][:, :T], self.v_cache[li][:, :T], rep)
+            self._gemm(ly.o, a, pb["o"], st)
             _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["o"]), None, P(ly.post_norm), P(pb["h"]), T,
                     H, eps, st)
             self._gemm(ly.gate, pb["h"], pb["g"], st)
