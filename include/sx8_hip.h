@@ -177,6 +177,18 @@ int32_t sx8_gemm_prefill_z(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
                            const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
                            const float* Z, int64_t N, int64_t n_cb, float* Y, void* stream);
 
+/* Prefill GEMMs of n_mats (1..4) v4.4 weights that share X (same K, same hdr_bytes), e.g.
+ * the q/k/v or gate/up projections of a prompt: Ys[i] (M, Ns[i]) float32 = X . W_i^T + PCA,
+ * each what sx8_gemm_prefill gives for that matrix up to the split-K summation order.
+ * Host arrays of n_mats device pointers.  One pass over X packs it for all matrices and one
+ * launch covers the column tiles of the whole group.  No counterpart in the reference, whose
+ * runtime calls gemm_sx8_compact once per projection (scripts/sx8_gemm_compact.py:42-74). */
+int32_t sx8_gemm_prefill_group(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, int32_t n_mats,
+                               const uint8_t* const* hdrs, const uint8_t* const* levels,
+                               int32_t hdr_bytes, const float* const* bases,
+                               const float* const* scales, const int64_t* Ns, int64_t n_cb,
+                               float* const* Ys, void* stream);
+
 /* Output-side PCA: Y[m, n] += sum_kb c0(kb,n) Z[m,kb,0] + c1(kb,n) Z[m,kb,1], c0/c1 the
  * signed nibbles of the coeff byte in the v4.4 header (float32 FMAs, one thread per
  * column).  The PCA step of gemm_compact's epilogue (cuda/sx8_gemm_compact.cu:130-150)

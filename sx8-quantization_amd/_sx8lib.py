@@ -51,6 +51,7 @@ SIGNATURES = [
     ("sx8_gemm_prefill_split", _I32,
      [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P]),
     ("sx8_gemm_prefill_z", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _I64, _I64, _P, _P]),
+    ("sx8_gemm_prefill_group", _I32, [_P, _I64, _I64, _I64, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P]),
     ("sx8_gemm_pca_z", _I32, [_P, _I64, _P, _I32, _I64, _I64, _P, _P]),
     ("sx8_gemm_prefill_core", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _I64, _I64, _P, _P]),
     # include/sx8_decoder.h

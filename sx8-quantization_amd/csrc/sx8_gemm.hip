@@ -46,6 +46,33 @@ struct WeightSrc {
     const uint8_t* lo;
 };
 
+// Matrices of one launch that multiply the same X (q/k/v, gate/up): column tiles are
+// numbered across the group, matrix after matrix; each matrix has its own weights, Zhl
+// operand and output.  poff: offset (floats) of this matrix's (M, N) block inside a
+// k_gemm split-K partial slice (slices hold the whole group, M * Ntot floats).
+constexpr int kMaxGemmGroup = 4;
+struct GemmMat {
+    WeightSrc w;
+    const uint32_t* Zhl;
+    float* Y;
+    int N;
+    int nb;          // column tiles, ceil(N / kBN)
+    int64_t poff;
+};
+struct GemmGroup {
+    GemmMat m[kMaxGemmGroup];
+    int n_mats;
+    int NB;          // column tiles of the group
+    int64_t Ntot;    // columns of the group
+};
+
+// The matrix that owns global column tile nb; nb becomes the tile within it.
+__device__ __forceinline__ int group_mat(const GemmGroup& g, int& nb) {
+    int mi = 0;
+    while (mi + 1 < g.n_mats && nb >= g.m[mi].nb) nb -= g.m[mi++].nb;
+    return mi;
+}
+
 // The part of one block a decoding thread needs, as loaded (no arithmetic on freshly
 // loaded values, so prefetches stay in flight until use): v4.4 -> lohi = dmin | dmax << 16,
 // cc = config | coeff << 8, q = this lane's 12-byte half of the 24 level bytes (the two
@@ -344,21 +371,24 @@ __device__ __forceinline__ int xcd_order(int b, int G) {
 // partials to Y in a fixed order.
 template <bool kSplit, int HB, bool kPca, int MF>
 __global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ Xp, int M,
-                                                   WeightSrc w,
-                                                   const uint32_t* __restrict__ Zhl, int N,
-                                                   int n_cb, int S, int kb_per_split,
-                                                   float* __restrict__ Y, float* __restrict__ part) {
+                                                   const GemmGroup g, int n_cb, int S, int kb_per_split,
+                                                   float* __restrict__ part) {
     __shared__ GemmSmem sm;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int NB = (N + kBN - 1) / kBN;
+    const int NB = g.NB;
     const int MB = (M + 128 * MF - 1) / (128 * MF);
     const int G = MB * NB * S;
     const int o = xcd_order(blockIdx.x, G);
-    const int nb = o % NB;
+    int nb = o % NB;
     const int ks = (o / NB) % S;
     const int mb = o / (NB * S);
+    const int mi = group_mat(g, nb);
+    const WeightSrc w = g.m[mi].w;
+    const uint32_t* __restrict__ Zhl = g.m[mi].Zhl;
+    float* __restrict__ Y = g.m[mi].Y;
+    const int N = g.m[mi].N;
     const int m0 = mb * 128 * MF;
     const int n0 = nb * kBN;
     const int kb0 = ks * kb_per_split;
@@ -532,7 +562,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const uint16_t* __restrict__ 
     // transposed tile: element i of lane l = 32 hf + c is column 32 j + 4 hf + 8 (i / 4) +
     // i % 4 of row 32 MF wave + 32 f + c, and elements 4q .. 4q + 3 are 4 consecutive
     // columns (one 16-byte store when N % 4 == 0 and Y is 16-byte aligned)
-    float* dst = ks == 0 ? Y : part + (int64_t)(ks - 1) * M * N;
+    float* dst = ks == 0 ? Y : part + (int64_t)(ks - 1) * M * g.Ntot + g.m[mi].poff;
     const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
 #pragma unroll
     for (int f = 0; f < MF; ++f) {
@@ -577,14 +607,14 @@ constexpr int kW1BM = 128 * kW1MF;
 // (512 x 128 f32, row-major), added to Y by k_reduce_tiles in range order.
 template <bool kSplit, int HB, bool kPca>
 __global__ __launch_bounds__(kW1Threads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_w1(
-    const uint16_t* __restrict__ Xp, int M, WeightSrc w, const uint32_t* __restrict__ Zhl, int N,
-    int n_cb, int Tf, int St, int kbs, float* __restrict__ Y, float* __restrict__ part) {
+    const uint16_t* __restrict__ Xp, int M, const GemmGroup g, int n_cb, int Tf, int St, int kbs,
+    float* __restrict__ part) {
     constexpr int MF = kW1MF;
     __shared__ GemmSmem sm;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int NB = (N + kBN - 1) / kBN;
+    const int NB = g.NB;
     const int b = blockIdx.x;
     int t, ks = 0, kb0 = 0, kb1 = n_cb;
     if (b < Tf) {
@@ -597,8 +627,13 @@ __global__ __launch_bounds__(kW1Threads) __attribute__((amdgpu_waves_per_eu(1, 1
         kb0 = ks * kbs;
         kb1 = min(n_cb, kb0 + kbs);
     }
-    const int nb = t % NB;
+    int nb = t % NB;
     const int mb = t / NB;
+    const int mi = group_mat(g, nb);
+    const WeightSrc w = g.m[mi].w;
+    const uint32_t* __restrict__ Zhl = g.m[mi].Zhl;
+    float* __restrict__ Y = g.m[mi].Y;
+    const int N = g.m[mi].N;
     const int m0 = mb * kW1BM;
     const int n0 = nb * kBN;
     const int hf = lane >> 5, r = lane & 31;
@@ -808,20 +843,22 @@ __global__ __launch_bounds__(kW1Threads) __attribute__((amdgpu_waves_per_eu(1, 1
 
 // Y += the St - 1 partial tiles of each split tile Tf .. T - 1 of k_gemm_w1, in range order
 // (deterministic).  One thread per 4 consecutive columns of a tile row.
-__global__ __launch_bounds__(256) void k_reduce_tiles(float* __restrict__ Y, const float* __restrict__ part,
-                                                      int M, int N, int Tf, int n_split, int St) {
+__global__ __launch_bounds__(256) void k_reduce_tiles(const GemmGroup g, const float* __restrict__ part,
+                                                      int M, int Tf, int n_split, int St) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;     // float4 index
     constexpr int kQ = kW1BM * kBN / 4;                            // float4s per tile
     if (i >= (int64_t)n_split * kQ) return;
     const int ts = (int)(i / kQ);
     const int e = (int)(i - (int64_t)ts * kQ) * 4;
     const int t = Tf + ts;
-    const int NB = (N + kBN - 1) / kBN;
-    const int m = (t / NB) * kW1BM + e / kBN;
-    const int n = (t % NB) * kBN + e % kBN;
+    int nb = t % g.NB;
+    const int mi = group_mat(g, nb);
+    const int N = g.m[mi].N;
+    const int m = (t / g.NB) * kW1BM + e / kBN;
+    const int n = nb * kBN + e % kBN;
     if (m >= M || n >= N) return;
     const float* p = part + (int64_t)ts * (St - 1) * (kW1BM * kBN) + e;
-    float* y = Y + (int64_t)m * N + n;
+    float* y = g.m[mi].Y + (int64_t)m * N + n;
     const int ne = min(4, N - n);
     sx8_float4 v = sx8_float4{0.f, 0.f, 0.f, 0.f};
     for (int c = 0; c < ne; ++c) v[c] = y[c];
@@ -829,22 +866,22 @@ __global__ __launch_bounds__(256) void k_reduce_tiles(float* __restrict__ Y, con
     for (int c = 0; c < ne; ++c) y[c] = v[c];
 }
 
-// Y += partial slices 0 .. S - 2, in slice order (deterministic).  kVec (Y 16-byte aligned,
+// Y += partial slices 0 .. S - 2 (stride floats apart), in slice order (deterministic).  kVec (Y 16-byte aligned,
 // M N a multiple of 4): 4 floats per thread; otherwise one.
 template <bool kVec>
 __global__ __launch_bounds__(256) void k_reduce(float* __restrict__ Y, const float* __restrict__ part,
-                                                int64_t MN, int nparts) {
+                                                int64_t MN, int nparts, int64_t stride) {
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if constexpr (kVec) {
         const int64_t i = t * 4;
         if (i >= MN) return;
         sx8_float4 y = *reinterpret_cast<const sx8_float4*>(Y + i);
-        for (int p = 0; p < nparts; ++p) y += *reinterpret_cast<const sx8_float4*>(part + p * MN + i);
+        for (int p = 0; p < nparts; ++p) y += *reinterpret_cast<const sx8_float4*>(part + p * stride + i);
         *reinterpret_cast<sx8_float4*>(Y + i) = y;
     } else {
         if (t >= MN) return;
         float y = Y[t];
-        for (int p = 0; p < nparts; ++p) y += part[p * MN + t];
+        for (int p = 0; p < nparts; ++p) y += part[p * stride + t];
         Y[t] = y;
     }
 }
@@ -932,10 +969,10 @@ Plan plan_split(int64_t M, int64_t N, int64_t T, int64_t n_cb, int64_t S, int MF
     return p;
 }
 
-// Tiles of 128 MF rows; the number of K ranges (1..8, at most one per 4-block group) that
-// the cost model prefers.
-Plan plan_k_gemm(int64_t M, int64_t N, int64_t n_cb, int MF) {
-    const int64_t T = ((M + 128 * MF - 1) / (128 * MF)) * ((N + kBN - 1) / kBN);
+// Tiles of 128 MF rows over NB column tiles (N columns in all); the number of K ranges
+// (1..8, at most one per 4-block group) that the cost model prefers.
+Plan plan_k_gemm(int64_t M, int64_t N, int64_t NB, int64_t n_cb, int MF) {
+    const int64_t T = ((M + 128 * MF - 1) / (128 * MF)) * NB;
     const int64_t groups = (n_cb + 3) / 4;
     Plan best = plan_split(M, N, T, n_cb, 1, MF);
     for (int64_t S = 2; S <= std::min<int64_t>(8, groups); ++S) {
@@ -947,8 +984,8 @@ Plan plan_k_gemm(int64_t M, int64_t N, int64_t n_cb, int MF) {
 
 // 512-row tiles: Tf = 0 (every tile split St ways) or the whole rounds of 256 tiles with
 // the remainder split; St from 1 to 8.
-Plan plan_w1(int64_t M, int64_t N, int64_t n_cb) {
-    const int64_t T = ((M + kW1BM - 1) / kW1BM) * ((N + kBN - 1) / kBN);
+Plan plan_w1(int64_t M, int64_t NB, int64_t n_cb) {
+    const int64_t T = ((M + kW1BM - 1) / kW1BM) * NB;
     const int64_t groups = (n_cb + 3) / 4;
     Plan best{};
     best.cost = 1e300;
@@ -974,15 +1011,16 @@ Plan plan_w1(int64_t M, int64_t N, int64_t n_cb) {
     return best;
 }
 
+// N columns in NB column tiles (a group pads every matrix to whole tiles).
 // SX8_GEMM_TILE=256 or 512 forces a tile height (tuning); otherwise the cheaper plan.
-Plan plan_gemm(int64_t M, int64_t N, int64_t n_cb) {
+Plan plan_gemm(int64_t M, int64_t N, int64_t NB, int64_t n_cb) {
     const int MF = M > 128 ? 2 : 1;
-    const Plan p256 = plan_k_gemm(M, N, n_cb, MF);
+    const Plan p256 = plan_k_gemm(M, N, NB, n_cb, MF);
     // k_gemm_w1 addresses rows up to the next multiple of 512 with 31-bit offsets
     const int64_t Mp = (M + kW1BM - 1) / kW1BM * kW1BM;
     const bool w1_ok = M > 256 && Mp / 32 * n_cb * 2048 <= 0x7FFFFFFF && Mp * n_cb * 8 <= 0x7FFFFFFF;
     if (!w1_ok) return p256;
-    const Plan p512 = plan_w1(M, N, n_cb);
+    const Plan p512 = plan_w1(M, NB, n_cb);
     const char* e = getenv("SX8_GEMM_TILE");
     const int forced = e ? atoi(e) : 0;
     if (forced == 256) return p256;
@@ -995,81 +1033,109 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t n_cb) {
 enum class ZMode { kNone, kBasis, kGiven };
 
 template <bool kSplit, bool kPca, int HB, int MF>
-void launch_mf(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, const WeightSrc& w,
-               const uint32_t* Zhl, int64_t N, int64_t n_cb, float* Y, float* part) {
+void launch_mf(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, const GemmGroup& g,
+               int64_t n_cb, float* part) {
     hipLaunchKernelGGL((k_gemm<kSplit, HB, kPca, MF>), dim3((unsigned)p.G), dim3(kThreads), 0, st, Xp,
-                       (int)M, w, Zhl, (int)N, (int)n_cb, p.S, p.kb_per_split, Y, part);
+                       (int)M, g, (int)n_cb, p.S, p.kb_per_split, part);
 }
 
 template <bool kSplit, bool kPca, int HB>
-void launch_hb(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, const WeightSrc& w,
-               const uint32_t* Zhl, int64_t N, int64_t n_cb, float* Y, float* part) {
+void launch_hb(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, const GemmGroup& g,
+               int64_t n_cb, float* part) {
     if (p.w1)
         hipLaunchKernelGGL((k_gemm_w1<kSplit, HB, kPca>), dim3((unsigned)p.G), dim3(kW1Threads), 0, st,
-                           Xp, (int)M, w, Zhl, (int)N, (int)n_cb, p.Tf, p.St, p.kbs, Y, part);
+                           Xp, (int)M, g, (int)n_cb, p.Tf, p.St, p.kbs, part);
     else if (p.MF == 2)
-        launch_mf<kSplit, kPca, HB, 2>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
+        launch_mf<kSplit, kPca, HB, 2>(p, st, Xp, M, g, n_cb, part);
     else
-        launch_mf<kSplit, kPca, HB, 1>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
+        launch_mf<kSplit, kPca, HB, 1>(p, st, Xp, M, g, n_cb, part);
 }
 
-// Plan; in the library's per-device workspace, stage the packed X and (PCA contracts) the
-// Zhl operand with one pass over X, followed by the split-K partials; run the GEMM and,
-// for S > 1, the fixed-order partial sum.
+// One call over n_mats matrices that share X (all of one contract).  Plan over the group's
+// total width; in the library's per-device workspace, stage the packed X (one pass over
+// X, with the first matrix's Zhl operand) and every other matrix's Zhl, followed by the
+// split-K partials; run the GEMM and, for a split plan, the fixed-order partial sums.
 template <bool kSplit>
-int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
-                 const WeightSrc& w, int32_t hdr_bytes, ZMode zm, const float* basis,
-                 const float* scales, const float* Z, int64_t N, int64_t n_cb, float* Y,
-                 hipStream_t st) {
+int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, int64_t K, int n_mats,
+                 const WeightSrc* ws_in, int32_t hdr_bytes, ZMode zm, const float* const* bases,
+                 const float* const* scales, const float* Z, const int64_t* Ns, int64_t n_cb,
+                 float* const* Ys, hipStream_t st) {
     using namespace sx8;
-    const Plan p = plan_gemm(M, N, n_cb);
+    int64_t Ntot = 0, NB = 0;
+    for (int i = 0; i < n_mats; ++i) {
+        Ntot += Ns[i];
+        NB += (Ns[i] + kBN - 1) / kBN;
+    }
+    if (Ntot > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "%s: group too wide", what);
+    const Plan p = plan_gemm(M, Ntot, NB, n_cb);
     if (p.G > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "%s: grid too large", what);
     const int64_t z_bytes = zm == ZMode::kNone ? 0 : ((M * n_cb * 8 + 255) & ~int64_t(255));
     const int64_t xp_bytes = (M + 31) / 32 * n_cb * 2048;
     const int64_t part_bytes = p.w1 ? p.n_split * (p.St - 1) * kW1BM * kBN * 4
-                                    : (int64_t)(p.S - 1) * M * N * 4;
+                                    : (int64_t)(p.S - 1) * M * Ntot * 4;
     void* v = nullptr;
-    int32_t rc = device_workspace(z_bytes + xp_bytes + part_bytes, &v);
+    int32_t rc = device_workspace(z_bytes * n_mats + xp_bytes + part_bytes, &v);
     if (rc != SX8_OK) return rc;
     uint8_t* ws = reinterpret_cast<uint8_t*>(v);
-    uint32_t* Zhl = reinterpret_cast<uint32_t*>(ws);
-    uint16_t* Xp = reinterpret_cast<uint16_t*>(ws + z_bytes);
-    float* part = reinterpret_cast<float*>(ws + z_bytes + xp_bytes);
-    if (zm == ZMode::kBasis) {
-        rc = compute_z(X, M, ldx, K, basis, scales, n_cb, Zhl, true, Xp, st);
-    } else {
-        if (zm == ZMode::kGiven) {
-            const int64_t n = M * n_cb * 2;
-            hipLaunchKernelGGL(k_z_hl, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, Z, n, Zhl);
+    uint16_t* Xp = reinterpret_cast<uint16_t*>(ws + z_bytes * n_mats);
+    float* part = reinterpret_cast<float*>(ws + z_bytes * n_mats + xp_bytes);
+    GemmGroup g{};
+    g.n_mats = n_mats;
+    g.Ntot = Ntot;
+    int64_t off = 0;
+    for (int i = 0; i < n_mats; ++i) {
+        GemmMat& m = g.m[i];
+        m.w = ws_in[i];
+        m.Zhl = reinterpret_cast<const uint32_t*>(ws + z_bytes * i);
+        m.Y = Ys[i];
+        m.N = (int)Ns[i];
+        m.nb = (int)((Ns[i] + kBN - 1) / kBN);
+        m.poff = M * off;
+        off += Ns[i];
+        g.NB += m.nb;
+    }
+    for (int i = 0; i < n_mats && rc == SX8_OK; ++i) {
+        uint32_t* Zhl = reinterpret_cast<uint32_t*>(ws + z_bytes * i);
+        uint16_t* pack = i == 0 ? Xp : nullptr;
+        if (zm == ZMode::kBasis) {
+            rc = compute_z(X, M, ldx, K, bases[i], scales[i], n_cb, Zhl, true, pack, st);
+        } else {
+            if (zm == ZMode::kGiven) {
+                const int64_t n = M * n_cb * 2;
+                hipLaunchKernelGGL(k_z_hl, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, Z, n, Zhl);
+            }
+            if (pack) rc = compute_z(X, M, ldx, K, nullptr, nullptr, n_cb, nullptr, false, pack, st);
         }
-        rc = compute_z(X, M, ldx, K, nullptr, nullptr, n_cb, nullptr, false, Xp, st);
     }
     if (rc != SX8_OK) return rc;
     if constexpr (kSplit) {
-        launch_hb<true, true, 6>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
+        launch_hb<true, true, 6>(p, st, Xp, M, g, n_cb, part);
     } else if (zm == ZMode::kNone) {
         if (hdr_bytes == 8)
-            launch_hb<false, false, 8>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
+            launch_hb<false, false, 8>(p, st, Xp, M, g, n_cb, part);
         else
-            launch_hb<false, false, 6>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
+            launch_hb<false, false, 6>(p, st, Xp, M, g, n_cb, part);
     } else {
         if (hdr_bytes == 8)
-            launch_hb<false, true, 8>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
+            launch_hb<false, true, 8>(p, st, Xp, M, g, n_cb, part);
         else
-            launch_hb<false, true, 6>(p, st, Xp, M, w, Zhl, N, n_cb, Y, part);
+            launch_hb<false, true, 6>(p, st, Xp, M, g, n_cb, part);
     }
     if (p.w1 && p.n_split > 0) {
         const int64_t n4 = p.n_split * (kW1BM * kBN / 4);
-        hipLaunchKernelGGL(k_reduce_tiles, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, Y, part,
-                           (int)M, (int)N, p.Tf, (int)p.n_split, p.St);
+        hipLaunchKernelGGL(k_reduce_tiles, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, g, part,
+                           (int)M, p.Tf, (int)p.n_split, p.St);
     } else if (!p.w1 && p.S > 1) {
-        const int64_t MN = M * N;
-        if (aligned(Y, 16) && MN % 4 == 0)
-            hipLaunchKernelGGL(k_reduce<true>, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0,
-                               st, Y, part, MN, p.S - 1);
-        else
-            hipLaunchKernelGGL(k_reduce<false>, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, st,
-                               Y, part, MN, p.S - 1);
+        for (int i = 0; i < n_mats; ++i) {
+            const int64_t MN = M * Ns[i];
+            const float* pm = part + g.m[i].poff;
+            if (aligned(Ys[i], 16) && MN % 4 == 0 && g.m[i].poff % 4 == 0 && (M * Ntot) % 4 == 0)
+                hipLaunchKernelGGL(k_reduce<true>, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0,
+                                   st, Ys[i], pm, MN, p.S - 1, M * Ntot);
+            else
+                hipLaunchKernelGGL(k_reduce<false>, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, st,
+                                   Ys[i], pm, MN, p.S - 1, M * Ntot);
+        }
     }
     return check_launch(what);
 }
@@ -1093,8 +1159,8 @@ extern "C" int32_t sx8_gemm_prefill(const uint16_t* X, int64_t M, int64_t ldx, i
     WeightSrc w{};
     w.hdr = hdr;
     w.levels = levels;
-    return run_gemm<false>("sx8_gemm_prefill", X, M, ldx, K, w, hdr_bytes, ZMode::kBasis, basis,
-                           scales, nullptr, N, n_cb, Y, as_stream(stream));
+    return run_gemm<false>("sx8_gemm_prefill", X, M, ldx, K, 1, &w, hdr_bytes, ZMode::kBasis, &basis,
+                           &scales, nullptr, &N, n_cb, &Y, as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemm_prefill_split(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
@@ -1118,8 +1184,8 @@ extern "C" int32_t sx8_gemm_prefill_split(const uint16_t* X, int64_t M, int64_t 
     w.coeff = coeff;
     w.hi = hi;
     w.lo = lo;
-    return run_gemm<true>("sx8_gemm_prefill_split", X, M, ldx, K, w, 6, ZMode::kBasis, basis,
-                          scales, nullptr, N, n_cb, Y, as_stream(stream));
+    return run_gemm<true>("sx8_gemm_prefill_split", X, M, ldx, K, 1, &w, 6, ZMode::kBasis, &basis,
+                          &scales, nullptr, &N, n_cb, &Y, as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemm_prefill_z(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
@@ -1139,8 +1205,8 @@ extern "C" int32_t sx8_gemm_prefill_z(const uint16_t* X, int64_t M, int64_t ldx,
     WeightSrc w{};
     w.hdr = hdr;
     w.levels = levels;
-    return run_gemm<false>("sx8_gemm_prefill_z", X, M, ldx, K, w, hdr_bytes, ZMode::kGiven, nullptr,
-                           nullptr, Z, N, n_cb, Y, as_stream(stream));
+    return run_gemm<false>("sx8_gemm_prefill_z", X, M, ldx, K, 1, &w, hdr_bytes, ZMode::kGiven, nullptr,
+                           nullptr, Z, &N, n_cb, &Y, as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemm_prefill_core(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
@@ -1159,8 +1225,38 @@ extern "C" int32_t sx8_gemm_prefill_core(const uint16_t* X, int64_t M, int64_t l
     WeightSrc w{};
     w.hdr = hdr;
     w.levels = levels;
-    return run_gemm<false>("sx8_gemm_prefill_core", X, M, ldx, K, w, hdr_bytes, ZMode::kNone,
-                           nullptr, nullptr, nullptr, N, n_cb, Y, as_stream(stream));
+    return run_gemm<false>("sx8_gemm_prefill_core", X, M, ldx, K, 1, &w, hdr_bytes, ZMode::kNone,
+                           nullptr, nullptr, nullptr, &N, n_cb, &Y, as_stream(stream));
+}
+
+extern "C" int32_t sx8_gemm_prefill_group(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
+                                          int32_t n_mats, const uint8_t* const* hdrs,
+                                          const uint8_t* const* levels, int32_t hdr_bytes,
+                                          const float* const* bases, const float* const* scales,
+                                          const int64_t* Ns, int64_t n_cb, float* const* Ys,
+                                          void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_gemm_prefill_group";
+    if (!X || !hdrs || !levels || !bases || !scales || !Ns || !Ys) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (n_mats < 1 || n_mats > kMaxGemmGroup)
+        return fail(SX8_ERR_INVALID, "%s: n_mats must be 1..%d, got %d", what, kMaxGemmGroup, n_mats);
+    if (hdr_bytes != 6 && hdr_bytes != 8)
+        return fail(SX8_ERR_INVALID, "%s: hdr_bytes must be 6 or 8, got %d", what, hdr_bytes);
+    if (!aligned(X, 2)) return fail(SX8_ERR_INVALID, "%s: misaligned X", what);
+    WeightSrc w[kMaxGemmGroup]{};
+    for (int i = 0; i < n_mats; ++i) {
+        if (!hdrs[i] || !levels[i] || !bases[i] || !scales[i] || !Ys[i])
+            return fail(SX8_ERR_INVALID, "%s: null pointer in matrix %d", what, i);
+        if (!aligned(hdrs[i], hdr_bytes == 8 ? 8 : 2) || !aligned(levels[i], 8) || !aligned(Ys[i], 4) ||
+            !aligned(bases[i], 16) || !aligned(scales[i], 8))
+            return fail(SX8_ERR_INVALID, "%s: misaligned pointer in matrix %d", what, i);
+        const int32_t rc = check_shape(what, M, ldx, K, Ns[i], n_cb);
+        if (rc != SX8_OK) return rc;
+        w[i].hdr = hdrs[i];
+        w[i].levels = levels[i];
+    }
+    return run_gemm<false>(what, X, M, ldx, K, n_mats, w, hdr_bytes, ZMode::kBasis, bases, scales, nullptr,
+                           Ns, n_cb, Ys, as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemm_pca_z(const float* Z, int64_t M, const uint8_t* hdr, int32_t hdr_bytes,

@@ -175,6 +175,8 @@ class SX8Decoder(nn.Module):
               "logits": torch.empty(cfg["vocab"], **f32), "tok": torch.zeros(1, dtype=torch.int64, device=dev),
               "scratch_pos": torch.zeros(1, dtype=torch.int64, device=dev)}
         pb["head_group"] = self._group_args((self.head,), (pb["logits"],))
+        pb["groups"] = [(self._group_args((ly.q, ly.k, ly.v), (pb["q"], pb["k"], pb["v"])),
+                         self._group_args((ly.gate, ly.up), (pb["g"], pb["u"]))) for ly in self.layers]
         self._pb = pb
         return pb
 
@@ -191,6 +193,13 @@ class SX8Decoder(nn.Module):
         with torch.nn.attention.sdpa_kernel(torch.nn.attention.SDPBackend.FLASH_ATTENTION):
             a = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True)[0]
         return a.permute(1, 0, 2).reshape(T, nh * hd)
+
+    @staticmethod
+    def _gemm_group(args, X, st):
+        """The prefill GEMMs of matrices sharing X (sx8_gemm_prefill_group), outputs (M, N_i)."""
+        n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
+        M, K = X.shape
+        _L.call("sx8_gemm_prefill_group", _L.ptr(X), M, K, K, n, hdrs, lvls, 6, bas, sca, ns, n_cb, ys, st)
 
     @staticmethod
     def _gemm(lin, X, Y, st):
@@ -222,9 +231,7 @@ class SX8Decoder(nn.Module):
             else:
                 _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["d"]), None, P(ly.in_norm), P(pb["h"]), T,
                         H, eps, st)
-            self._gemm(ly.q, pb["h"], pb["q"], st)
-            self._gemm(ly.k, pb["h"], pb["k"], st)
-            self._gemm(ly.v, pb["h"], pb["v"], st)
+            self._gemm_group(pb["groups"][li][0], pb["h"], st)      # q, k, v: one call
             _L.call("sx8_dec_qk_rope_cache_rows", P(pb["q"]), P(pb["k"]), P(pb["v"]), P(ly.q_norm),
                     P(ly.k_norm), P(self.cos), P(self.sin), P(pb["pos0"]), T, P(pb["qh"]),
                     P(self.k_cache[li]), P(self.v_cache[li]), nh, nk, hd, self.max_len, eps, st)
@@ -232,8 +239,7 @@ class SX8Decoder(nn.Module):
             self._gemm(ly.o, a, pb["o"], st)
             _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["o"]), None, P(ly.post_norm), P(pb["h"]), T,
                     H, eps, st)
-            self._gemm(ly.gate, pb["h"], pb["g"], st)
-            self._gemm(ly.up, pb["h"], pb["u"], st)
+            self._gemm_group(pb["groups"][li][1], pb["h"], st)      # gate, up: one call
             _L.call("sx8_dec_silu_mul", P(pb["g"]), P(pb["u"]), P(pb["m"]), T * cfg["inter"], st)
             self._gemm(ly.down, pb["m"], pb["d"], st)
         # last row: residual + down output, final norm and lm_head in one launch

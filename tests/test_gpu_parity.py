@@ -438,3 +438,41 @@ def test_clone_model_replaces_linears(hiplib, cuda):
     with torch.no_grad():
         out = m2(ids).float()
     assert (out - ref).abs().max().item() / ref.abs().max().item() < 5e-2
+
+
+@pytest.mark.parametrize("name,Ns,K,M,tile", [
+    ("qkv_m512", [4096, 1024, 1024], 2560, 512, "auto"),
+    ("gate_up_m700_w1", [1000, 1300], 2560, 700, "512"),
+    ("ragged_four", [300, 64, 129, 700], 80, 33, "auto"),
+])
+def test_prefill_gemm_group(hiplib, oracle, cuda, monkeypatch, name, Ns, K, M, tile):
+    """sx8_gemm_prefill_group against the oracle (1e-3) and against one sx8_gemm_prefill per
+    matrix (the same kernel arithmetic; only the split-K summation order can differ)."""
+    import ctypes
+    import torch
+    import _sx8lib as L
+    from sx8_decode1_v3 import make_tensors_v44
+    if tile != "auto":
+        monkeypatch.setenv("SX8_GEMM_TILE", tile)
+    _say("prefill group", name, Ns, K, M)
+    mats = [_quantized(N, K, 500 + i, cuda) for i, N in enumerate(Ns)]
+    ts = [make_tensors_v44(qt, bi) for qt, bi in mats]
+    n_cb = mats[0][0]["n_cb"]
+    X = _x(M, K, 13)
+    Xd = X.to(cuda)
+    n = len(Ns)
+    Pa = ctypes.c_void_p * n
+    ys = [torch.empty(M, N, device=cuda) for N in Ns]
+    L.call("sx8_gemm_prefill_group", L.ptr(Xd), M, K, K, n, Pa(*[t[0].data_ptr() for t in ts]),
+           Pa(*[t[1].data_ptr() for t in ts]), 6, Pa(*[t[2].data_ptr() for t in ts]),
+           Pa(*[t[3].data_ptr() for t in ts]), (ctypes.c_int64 * n)(*Ns), n_cb,
+           Pa(*[y.data_ptr() for y in ys]), L.stream(cuda))
+    for i, (qt, bi) in enumerate(mats):
+        y1 = torch.empty(M, Ns[i], device=cuda)
+        t = ts[i]
+        L.call("sx8_gemm_prefill", L.ptr(Xd), M, K, K, L.ptr(t[0]), L.ptr(t[1]), 6, L.ptr(t[2]), L.ptr(t[3]),
+               Ns[i], n_cb, L.ptr(y1), L.stream(cuda))
+        ref = oracle.gemm_f64(X.numpy(), oracle.dequant_r64(qt, bi))
+        got = ys[i].cpu().numpy()
+        assert oracle.rel_err(got, ref) <= 1e-3, i
+        assert oracle.rel_err(got, y1.cpu().numpy()) <= 1e-5, i
