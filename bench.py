@@ -298,12 +298,61 @@ def bench_prefill_m(torch, L, layer, args, M):
     return {"M": M, "tflops": tf, "per_shape": res, "frac_of_mfma_peak": tf / MFMA_F16_PEAK_TFLOPS}
 
 
+def bench_prefill_grouped(torch, L, layer, args, M):
+    """The layer at M rows as a prompt pass runs it: q/k/v and gate/up each one
+    sx8_gemm_prefill_group call, o and down alone (4 calls); TFLOP/s over the layer."""
+    import ctypes
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(12)
+    xs = {K: torch.randn(M, K, generator=g).half().to(dev) for K in {t["K"] for t in layer}}
+    ys = [torch.empty(M, t["N"], dtype=torch.float32, device=dev) for t in layer]
+    st = L.stream(dev)
+    fn = L.lib().sx8_gemm_prefill_group
+    by = {t["name"]: i for i, t in enumerate(layer)}
+    groups = [["q_proj", "k_proj", "v_proj"], ["o_proj"], ["gate_proj", "up_proj"], ["down_proj"]]
+    calls = []
+    for grp in groups:
+        ii = [by[n] for n in grp]
+        n = len(ii)
+        P = ctypes.c_void_p * n
+        t0 = layer[ii[0]]
+        calls.append((L.ptr(xs[t0["K"]]), M, t0["K"], t0["K"], n, P(*[layer[i]["hdr"].data_ptr() for i in ii]),
+                      P(*[layer[i]["lvl"].data_ptr() for i in ii]), args.hdr_bytes,
+                      P(*[layer[i]["bas"].data_ptr() for i in ii]), P(*[layer[i]["sca"].data_ptr() for i in ii]),
+                      (ctypes.c_int64 * n)(*[layer[i]["N"] for i in ii]), t0["n_cb"],
+                      P(*[ys[i].data_ptr() for i in ii]), st))
+
+    def step():
+        for a in calls:
+            if fn(*a) != 0:
+                raise RuntimeError(L.lib().sx8_last_error().decode())
+
+    step()
+    torch.cuda.synchronize()
+    reps = 5
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gpu_delay(torch, 10)
+    a.record()
+    for _ in range(reps):
+        step()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    flop = sum(2.0 * M * t["N"] * t["K"] for t in layer)
+    tf = flop / (ms * 1e-3) / 1e12
+    log(f"prefill grouped M={M}: {ms * 1e3:.1f} us {tf:.1f} TFLOP/s")
+    return {"M": M, "calls_per_layer": len(calls), "us": ms * 1e3, "tflops": tf,
+            "frac_of_mfma_peak": tf / MFMA_F16_PEAK_TFLOPS, "groups": groups}
+
+
 def bench_prefill(torch, L, layer, args):
     """Fused dequant + GEMM over the layer at every M of --prefill-m (config 2); the last M
-    (2048 by default) is the headline."""
+    (2048 by default) is the headline.  Also the layer as a prompt pass runs it (grouped
+    calls) at every M."""
     ms = [int(v) for v in str(args.prefill_m).split(",") if v.strip()]
     sweep = {M: bench_prefill_m(torch, L, layer, args, M) for M in ms}
     out = dict(sweep[ms[-1]])
+    out["grouped"] = {str(M): bench_prefill_grouped(torch, L, layer, args, M) for M in ms}
     out["sweep"] = {str(M): {"tflops": r["tflops"], "frac_of_mfma_peak": r["frac_of_mfma_peak"],
                              "per_shape_tflops": {k: v["tflops"] for k, v in r["per_shape"].items()}}
                     for M, r in sweep.items()}
