@@ -699,7 +699,7 @@ __global__ __launch_bounds__(kW1Threads) __attribute__((amdgpu_waves_per_eu(1, 1
         load_rec<kSplit, HB, MF>(r1, ls, N, min(kb0 + 1, kb1 - 1));
         load_rec<kSplit, HB, MF>(r2, ls, N, min(kb0 + 2, kb1 - 1));
         load_a<MF>(A[0], ls, kb0);
-        load_a<MF>(A[1], ls, min(kb0 + 1, kb1 - 1));
+        load_a_step<MF>(A[1], ls, min(kb0 + 1, kb1 - 1), 0);   // k-step 1: in iteration kb0
         if constexpr (kPca) load_za<MF>(za, ls, kb0 >> 2);
         load_rec<kSplit, HB, MF>(R[3], ls, N, min(kb0 + 3, kb1 - 1));
         load_rec<kSplit, HB, MF>(R[0], ls, N, min(kb0 + 4, kb1 - 1));
@@ -719,19 +719,20 @@ __global__ __launch_bounds__(kW1Threads) __attribute__((amdgpu_waves_per_eu(1, 1
         for (int j = 0; j < 4; ++j)
             bw[j][st] = *reinterpret_cast<const sx8_u32x4*>(src + (j * 2 + st) * 1024);
     };
-    read_b(kb0, 0);
-    read_b(kb0, 1);
+    read_b(kb0, 0);   // k-step 1: in iteration kb0
 
     // iteration kb: finish block kb + 2 into the ring and prepare block kb + 3 (its
-    // records refilled with block kb + 7); 32 MFMAs of block kb, each k-step followed by
-    // the refill of its A registers (block kb + 2) and B registers (block kb + 1, in LDS
-    // since the previous barrier); PCA k-step at the end of a 4-block group; one barrier.
-    // The decode VALU work is spread between the MFMAs (one MFMA, then up to three or four
-    // VALU instructions), so it issues while the matrix core is busy.
-    auto body = [&](int kb, sx8_u32x4 (&acur)[MF][2], LaneRec& rx, const DecPrep& pcur,
-                    DecPrep& pnext, const bool pca) __attribute__((always_inline)) {
+    // records refilled with block kb + 7); 32 MFMAs of block kb; PCA k-step at the end of a
+    // 4-block group; one barrier.  Each k-step's registers are refilled during the other
+    // k-step's MFMAs (A: block kb + 2, B: the next block, in LDS since a barrier), and the
+    // decode VALU work, the loads and the LDS accesses are spread between the MFMAs
+    // (sched_group_barrier patterns), so they issue while the matrix core is busy.
+    auto body = [&](int kb, sx8_u32x4 (&acur)[MF][2], sx8_u32x4 (&aprev)[MF][2], LaneRec& rx,
+                    const DecPrep& pcur, DecPrep& pnext, const bool pca) __attribute__((always_inline)) {
         const int ka = min(kb + 2, kb1 - 1);
-        // k-step 0: prepare block kb + 3 between the MFMAs, then refill A, B and the records
+        const int kp = min(kb + 1, kb1 - 1);
+        // k-step 0: prepare block kb + 3; between the MFMAs, the second-k-step refills the
+        // previous iteration left (A of kb + 1 into its buffer, B of kb from LDS)
         pnext = dec_prep<kSplit>(rx, h);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -740,17 +741,18 @@ __global__ __launch_bounds__(kW1Threads) __attribute__((amdgpu_waves_per_eu(1, 1
                 acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
                     __builtin_bit_cast(sx8_half8, bw[j][0]),
                     __builtin_bit_cast(sx8_half8, acur[f][0]), acc[f][j], 0, 0, 0);
+        load_a_step<MF>(aprev, ls, kp, 1);
+        read_b(kb, 1);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
             __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // up to three VALU
+            if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);           // a B read
+            else if (i < 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);      // an A load
         }
         SX8_SCHED_FENCE();
-        load_a_step<MF>(acur, ls, ka, 0);
-        load_rec<kSplit, HB, MF>(rx, ls, N, min(kb + 7, kb1 - 1));
-        read_b(kb + 1, 0);
-        SX8_SCHED_FENCE();
-        // k-step 1: finish block kb + 2 into the ring between the MFMAs, then refill A, B
+        // k-step 1: finish block kb + 2 into the ring; between the MFMAs, refill A (block
+        // kb + 2) and B (block kb + 1) for k-step 0 and the record ring
         dec_finish<kPca>(sm, pcur, kb + 2, (kb + 2) % 3, wj, wl, h);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -759,14 +761,17 @@ __global__ __launch_bounds__(kW1Threads) __attribute__((amdgpu_waves_per_eu(1, 1
                 acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
                     __builtin_bit_cast(sx8_half8, bw[j][1]),
                     __builtin_bit_cast(sx8_half8, acur[f][1]), acc[f][j], 0, 0, 0);
+        load_a_step<MF>(acur, ls, ka, 0);
+        load_rec<kSplit, HB, MF>(rx, ls, N, min(kb + 7, kb1 - 1));
+        read_b(kb + 1, 0);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
             __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // up to four VALU
+            if (i < 3) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);           // ring writes
+            else if (i < 10) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);     // A / record loads
+            else if (i < 14) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // B reads
         }
-        SX8_SCHED_FENCE();
-        load_a_step<MF>(acur, ls, ka, 1);
-        read_b(kb + 1, 1);
         SX8_SCHED_FENCE();
         if constexpr (kPca) {
             if (pca) {
@@ -784,21 +789,19 @@ __global__ __launch_bounds__(kW1Threads) __attribute__((amdgpu_waves_per_eu(1, 1
                 load_za<MF>(za, ls, min(g + 1, (kb1 - 1) >> 2));
             }
         }
-        // the barrier waits for this wave's LDS accesses except the four B reads just
-        // issued (slot (kb + 1) % 3 is next written two barriers later)
-        lds_barrier_keep4();
+        lds_barrier();
     };
     int kb = kb0;   // a multiple of 4
     for (; kb + 4 <= kb1; kb += 4) {
-        body(kb, A[0], R[3], P[0], P[1], false);
-        body(kb + 1, A[1], R[0], P[1], P[0], false);
-        body(kb + 2, A[0], R[1], P[0], P[1], false);
-        body(kb + 3, A[1], R[2], P[1], P[0], true);
+        body(kb, A[0], A[1], R[3], P[0], P[1], false);
+        body(kb + 1, A[1], A[0], R[0], P[1], P[0], false);
+        body(kb + 2, A[0], A[1], R[1], P[0], P[1], false);
+        body(kb + 3, A[1], A[0], R[2], P[1], P[0], true);
     }
     // last partial group (n_cb % 4 blocks): its PCA step after its last block
-    if (kb < kb1) body(kb, A[0], R[3], P[0], P[1], kb + 1 == kb1);
-    if (kb + 1 < kb1) body(kb + 1, A[1], R[0], P[1], P[0], kb + 2 == kb1);
-    if (kb + 2 < kb1) body(kb + 2, A[0], R[1], P[0], P[1], true);
+    if (kb < kb1) body(kb, A[0], A[1], R[3], P[0], P[1], kb + 1 == kb1);
+    if (kb + 1 < kb1) body(kb + 1, A[1], A[0], R[0], P[1], P[0], kb + 2 == kb1);
+    if (kb + 2 < kb1) body(kb + 2, A[0], A[1], R[1], P[0], P[1], true);
 
     // epilogue: accumulator (f, j) holds the transposed 32 x 32 tile (see k_gemm): a 16-byte
     // store of 4 consecutive columns per (f, j, q).  Partial tiles are dense 512 x 128.
