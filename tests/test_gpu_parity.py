@@ -476,3 +476,40 @@ def test_prefill_gemm_group(hiplib, oracle, cuda, monkeypatch, name, Ns, K, M, t
         got = ys[i].cpu().numpy()
         assert oracle.rel_err(got, ref) <= 1e-3, i
         assert oracle.rel_err(got, y1.cpu().numpy()) <= 1e-5, i
+
+
+def test_vocab_sized_tensor_full(hiplib, oracle, cuda):
+    """BASELINE config 4 at its full size: one 151936 x 2560 S-X8 matrix (seeded N(0, 0.02),
+    1% degenerate blocks).  lm_head GEMV (M = 1) within 1e-3 of the float64 oracle; prefill
+    GEMM at M = 512 within 1e-3 of a float32 matmul of the bit-exact R64 weights; 512
+    uniform ids gathered bit-exact against the oracle's rows."""
+    import torch
+    from kernel_sx8_v43 import decode_tensor_gpu_fast
+    from sx8_decode1_v3 import decode1_v44, make_tensors_v44
+    from sx8_embed_v44 import ext
+    from sx8_gemm_compact import gemm_sx8_compact
+    N, K = 151936, 2560
+    qt, bi = _quantized(N, K, 4, cuda)
+    _say("vocab", N, K)
+    W = oracle.dequant_r64(qt, bi)                               # (N, K) fp16, the oracle's bits
+    t = make_tensors_v44(qt, bi)
+    x = _x(1, K, 21)
+    y, _ = decode1_v44(x[0].to(cuda), qt, bi, *t)
+    rel = oracle.rel_err(y.cpu().numpy(), oracle.gemm_f64(x.numpy(), W)[0])
+    _say("   gemv rel", rel)
+    assert rel <= 1e-3
+    # the device dequant is the oracle's bits, so the GEMM reference can be an fp32 matmul
+    Wd = decode_tensor_gpu_fast(qt, bi).to(cuda)
+    assert np.array_equal(Wd.cpu().numpy().view(np.uint16), W.view(np.uint16))
+    X = _x(512, K, 22).to(cuda)
+    Y = gemm_sx8_compact(X, qt, bi, *t)
+    Y32 = X.float() @ Wd.float().T
+    rel = (Y - Y32).abs().max().item() / Y32.abs().max().item()
+    _say("   gemm rel", rel)
+    assert rel <= 1e-3
+    del Y, Y32, Wd
+    g = torch.Generator(device="cpu").manual_seed(23)
+    ids = torch.randint(0, N, (512,), generator=g)
+    out = torch.empty(512, K, dtype=torch.float16, device=cuda)
+    ext().sx8_embed_v44(ids.to(cuda), t[0], t[1], t[2], t[3], K, N, qt["n_cb"], out)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), W.view(np.uint16)[ids.numpy()])
