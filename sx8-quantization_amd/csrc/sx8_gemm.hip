@@ -1097,19 +1097,21 @@ int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, in
         off += Ns[i];
         g.NB += m.nb;
     }
-    for (int i = 0; i < n_mats && rc == SX8_OK; ++i) {
-        uint32_t* Zhl = reinterpret_cast<uint32_t*>(ws + z_bytes * i);
-        uint16_t* pack = i == 0 ? Xp : nullptr;
-        if (zm == ZMode::kBasis) {
-            rc = compute_z(X, M, ldx, K, bases[i], scales[i], n_cb, Zhl, true, pack, st);
-        } else {
-            if (zm == ZMode::kGiven) {
-                const int64_t n = M * n_cb * 2;
-                hipLaunchKernelGGL(k_z_hl, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, Z, n, Zhl);
-            }
-            if (pack) rc = compute_z(X, M, ldx, K, nullptr, nullptr, n_cb, nullptr, false, pack, st);
+    // one pass over X: the packed copy and every matrix's Zhl
+    ZSets zs{};
+    if (zm == ZMode::kBasis) {
+        zs.n = n_mats;
+        for (int i = 0; i < n_mats; ++i) {
+            zs.basis[i] = bases[i];
+            zs.scales[i] = scales[i];
+            zs.Z[i] = reinterpret_cast<float*>(ws + z_bytes * i);
         }
+    } else if (zm == ZMode::kGiven) {
+        const int64_t n = M * n_cb * 2;
+        hipLaunchKernelGGL(k_z_hl, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, Z, n,
+                           reinterpret_cast<uint32_t*>(ws));
     }
+    rc = compute_z_sets(X, M, ldx, K, zs, n_cb, true, Xp, st);
     if (rc != SX8_OK) return rc;
     if constexpr (kSplit) {
         launch_hb<true, true, 6>(p, st, Xp, M, g, n_cb, part);

@@ -72,8 +72,9 @@ constexpr int kLdsMaxKb = 640;     // activation table staged in LDS up to this 
 // Z of one (row, kb, j) follows the reference's warp tree: products x_t * b_t, then
 // pairwise sums over lane offsets 16, 8, 4, 2, 1 (cuda/sx8_decode1_v3.cu:53-63), then
 // scale * sum.
-// One thread per (row m, kb): both Z values, x read once as four 16-byte vectors (the
-// row's tail past K is zero), products and the reference tree in registers.
+// One thread per (row m, kb): x read once as four 16-byte vectors (the row's tail past K
+// is zero), then for every basis set s of `zs` both Z values (products and the reference
+// tree in registers) -- one pass over X serves all matrices of a prefill group.
 // Optional outputs: Z as f32 pairs or as split fp16 hi/lo pairs (hl), and the prefill
 // GEMM's packed copy of X (Xp != nullptr): for each 32-row group G and block kb a 2 KB
 // chunk [k-step st][MFMA lane l = 32 hf + r][8 values] holding X[32 G + r][32 kb + 16 hf +
@@ -81,17 +82,16 @@ constexpr int kLdsMaxKb = 640;     // activation table staged in LDS up to this 
 // packing, the grid covers the rows up to the next multiple of 32 (rows >= M pack zeros).
 template <bool kZ, bool kPack>
 __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ X, int64_t M,
-                                                   int64_t ldx, int64_t K,
-                                                   const float* __restrict__ basis,
-                                                   const float* __restrict__ scales, int64_t n_cb,
-                                                   bool x_vec, bool hl, float* __restrict__ Z,
+                                                   int64_t ldx, int64_t K, const sx8::ZSets zs,
+                                                   int64_t n_cb, bool x_vec, bool hl,
                                                    uint16_t* __restrict__ Xp) {
 #pragma clang fp contract(off)
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t rows = kPack ? (M + 31) / 32 * 32 : M;
     if (gid >= rows * n_cb) return;
-    // packing: the row within its 32-row group runs fastest, so a wave's packed stores
-    // fill whole 512-byte runs; otherwise kb runs fastest (contiguous X reads, Z writes)
+    // packing: the row within its 32-row group runs fastest (broadcast basis loads, whole
+    // 512-byte runs of packed stores); otherwise kb runs fastest, which keeps every lane
+    // busy for the M = 1 callers
     int64_t m, kb;
     if constexpr (kPack) {
         const int64_t rest = gid >> 5;
@@ -133,30 +133,33 @@ __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ 
     }
     if constexpr (kZ) {
         if (!row_ok) return;
-        const float4* bv = reinterpret_cast<const float4*>(basis + kb * 64);
-        float z[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            float p[32];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const float4 b = bv[8 * j + q];
-                p[4 * q] = sx8_h2f(xw[2 * q]) * b.x;
-                p[4 * q + 1] = sx8_h2f(xw[2 * q] >> 16) * b.y;
-                p[4 * q + 2] = sx8_h2f(xw[2 * q + 1]) * b.z;
-                p[4 * q + 3] = sx8_h2f(xw[2 * q + 1] >> 16) * b.w;
-            }
-#pragma unroll
-            for (int off = 16; off > 0; off >>= 1)
-#pragma unroll
-                for (int t = 0; t < off; ++t) p[t] = p[t] + p[t + off];
-            z[j] = scales[kb * 2 + j] * p[0];
-        }
         const int64_t zi = m * n_cb + kb;
-        if (hl)
-            *reinterpret_cast<uint2*>(Z + zi * 2) = make_uint2(sx8_split_hl(z[0]), sx8_split_hl(z[1]));
-        else
-            *reinterpret_cast<float2*>(Z + zi * 2) = make_float2(z[0], z[1]);
+        for (int s = 0; s < zs.n; ++s) {
+            const float4* bv = reinterpret_cast<const float4*>(zs.basis[s] + kb * 64);
+            float z[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float p[32];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const float4 b = bv[8 * j + q];
+                    p[4 * q] = sx8_h2f(xw[2 * q]) * b.x;
+                    p[4 * q + 1] = sx8_h2f(xw[2 * q] >> 16) * b.y;
+                    p[4 * q + 2] = sx8_h2f(xw[2 * q + 1]) * b.z;
+                    p[4 * q + 3] = sx8_h2f(xw[2 * q + 1] >> 16) * b.w;
+                }
+#pragma unroll
+                for (int off = 16; off > 0; off >>= 1)
+#pragma unroll
+                    for (int t = 0; t < off; ++t) p[t] = p[t] + p[t + off];
+                z[j] = zs.scales[s][kb * 2 + j] * p[0];
+            }
+            float* Z = zs.Z[s];
+            if (hl)
+                *reinterpret_cast<uint2*>(Z + zi * 2) = make_uint2(sx8_split_hl(z[0]), sx8_split_hl(z[1]));
+            else
+                *reinterpret_cast<float2*>(Z + zi * 2) = make_float2(z[0], z[1]);
+        }
     }
 }
 
@@ -806,24 +809,35 @@ extern "C" int64_t sx8_gemv_workspace_bytes(int64_t n_cb) {
     return n_cb > 0 ? n_cb * (int64_t)sizeof(KbInfo) : 0;
 }
 
-int32_t sx8::compute_z(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, const float* basis,
-                       const float* scales, int64_t n_cb, void* Z, bool hl, uint16_t* xpack,
-                       hipStream_t st) {
+int32_t sx8::compute_z_sets(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, const ZSets& zs,
+                           int64_t n_cb, bool hl, uint16_t* xpack, hipStream_t st) {
     const int64_t rows = xpack ? (M + 31) / 32 * 32 : M;
     const int64_t grid = (rows * n_cb + 255) / 256;
     if (grid > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "compute_z: too large");
     const bool x_vec = aligned(X, 16) && ldx % 8 == 0;
-    float* Zf = reinterpret_cast<float*>(Z);
-    if (Z && xpack)
+    if (zs.n > 0 && xpack)
         hipLaunchKernelGGL((k_compute_z<true, true>), dim3((unsigned)grid), dim3(256), 0, st, X, M, ldx,
-                           K, basis, scales, n_cb, x_vec, hl, Zf, xpack);
-    else if (Z)
+                           K, zs, n_cb, x_vec, hl, xpack);
+    else if (zs.n > 0)
         hipLaunchKernelGGL((k_compute_z<true, false>), dim3((unsigned)grid), dim3(256), 0, st, X, M,
-                           ldx, K, basis, scales, n_cb, x_vec, hl, Zf, xpack);
+                           ldx, K, zs, n_cb, x_vec, hl, xpack);
     else if (xpack)
         hipLaunchKernelGGL((k_compute_z<false, true>), dim3((unsigned)grid), dim3(256), 0, st, X, M,
-                           ldx, K, basis, scales, n_cb, x_vec, hl, Zf, xpack);
+                           ldx, K, zs, n_cb, x_vec, hl, xpack);
     return check_launch("compute_z");
+}
+
+int32_t sx8::compute_z(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, const float* basis,
+                       const float* scales, int64_t n_cb, void* Z, bool hl, uint16_t* xpack,
+                       hipStream_t st) {
+    ZSets zs{};
+    if (Z) {
+        zs.basis[0] = basis;
+        zs.scales[0] = scales;
+        zs.Z[0] = reinterpret_cast<float*>(Z);
+        zs.n = 1;
+    }
+    return compute_z_sets(X, M, ldx, K, zs, n_cb, hl, xpack, st);
 }
 
 extern "C" int32_t sx8_compute_z(const uint16_t* X, int64_t M, int64_t ldx, const float* basis,

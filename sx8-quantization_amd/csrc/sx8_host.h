@@ -41,4 +41,16 @@ int32_t compute_z(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, const fl
                   const float* scales, int64_t n_cb, void* Z, bool hl, uint16_t* xpack,
                   hipStream_t st);
 
+// The same for n (0..kMaxZSets) basis sets in one pass over X (the matrices of a prefill
+// group): Z[s] from basis[s] / scales[s].
+constexpr int kMaxZSets = 4;
+struct ZSets {
+    const float* basis[kMaxZSets];
+    const float* scales[kMaxZSets];
+    float* Z[kMaxZSets];
+    int n;
+};
+int32_t compute_z_sets(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, const ZSets& zs,
+                       int64_t n_cb, bool hl, uint16_t* xpack, hipStream_t st);
+
 }  // namespace sx8
