@@ -78,6 +78,17 @@ int32_t sx8_dec_attn_rope(const float* q_raw, const float* k_raw, const float* v
                           int64_t L, float scale, float eps, void* workspace,
                           int64_t workspace_bytes, void* stream);
 
+/* Causal attention of T prompt rows (prefill): q (T, nh, hd) fp16 (normalized and
+ * rotated, as sx8_dec_qk_rope_cache_rows writes it), caches (nk, L, hd) fp16 holding
+ * keys/values 0 .. start + T - 1; row i (position start + i) attends keys 0 .. start + i.
+ * out (T, nh * hd) fp16; scale = 1 / sqrt(hd).  nh / nk in {1, 2, 4, 8} with 16 nh / nk
+ * <= hd, hd 64 or 128.  fp16 products on MFMA with fp32 accumulation and an fp32 online
+ * softmax (probabilities rounded to fp16 for the second product).  No reference
+ * counterpart: the Hugging Face attention of the prompt pass in scripts/infer_sx8.py. */
+int32_t sx8_dec_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                             uint16_t* out, int64_t T, int64_t start, int32_t nh, int32_t nk, int32_t hd,
+                             int64_t L, float scale, void* stream);
+
 /* Workspace bytes of sx8_dec_attn_split. */
 int64_t sx8_dec_attn_workspace_bytes(int32_t nh, int32_t hd);
 

@@ -558,6 +558,158 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict
 
 }  // namespace
 
+// Causal attention of T prompt rows over the cache (prefill), on MFMA
+// (v_mfma_f32_32x32x16_f16, fp32 accumulation).  Work-group = (32-row query tile, KV
+// head); wave w takes query head kvh * G + w, so the G heads that share a KV head share its
+// staged V.  Per 32-key block a wave computes S^T = K Q^T: keys are the MFMA rows and the
+// tile's 32 queries the columns, so lane l = 32 h + c owns query c (keys 8 g + 4 h + r of
+// the block in accumulator 4 g + r) and the online softmax is lane-local (one exchange
+// with lane l ^ 32 for the other 16 keys).  Then O^T += V^T P^T: the P^T operand of k-step
+// st is the lane's own accumulators 8 st .. 8 st + 7 converted to fp16 (the k index order
+// is free as long as both operands use it: slot t of half h is key 16 st + 8 (t / 4) +
+// 4 h + t % 4), and V^T comes from LDS, where the staging writes each block transposed
+// with that key order (key bits 2 and 3 swapped), so a lane's 8 values are one 16-byte
+// read.  Row i (position start + i) attends keys 0 .. start + i; keys >= start + T are
+// never read.  Output (T, nh * HD) fp16.
+constexpr int kApVRow = 40;      // halves per LDS row of V^T: 32 keys + 8 pad (conflict-free reads)
+
+__device__ __forceinline__ float lane_swap32(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 32) ? sw[0] : sw[1]);
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(64 * G) void k_attn_prefill(const uint16_t* __restrict__ q,
+                                                         const uint16_t* __restrict__ k_cache,
+                                                         const uint16_t* __restrict__ v_cache,
+                                                         uint16_t* __restrict__ out, int T, int start,
+                                                         int nh, int L, float scale_log2) {
+    typedef float f32x16 __attribute__((ext_vector_type(16)));
+    typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+    constexpr int KS = HD / 16;                 // k-steps of S^T over the head dimension
+    constexpr int NT = HD / 32;                 // 32-row tiles of O^T
+    constexpr int CPR = HD / 8;                 // 16-byte chunks per key row
+    constexpr int VCH = 32 * CPR / (64 * G);    // V chunks staged per thread and block
+    static_assert(VCH >= 1 && VCH * 64 * G == 32 * CPR, "V staging split");
+    __shared__ __align__(16) uint16_t vt[2][HD * kApVRow];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int c = lane & 31, h = lane >> 5;
+    const int kvh = blockIdx.y, head = kvh * G + w;
+    const int q0 = blockIdx.x * 32, qi = q0 + c;
+    const int ktot = start + T;                                 // keys in the cache
+    const int nblk = (start + min(q0 + 32, T) + 31) / 32;       // key blocks this tile needs
+    const sx8_u32x4 zero4 = {0u, 0u, 0u, 0u};
+    sx8_u32x4 qb[KS];
+    {
+        const uint16_t* qr = q + ((int64_t)min(qi, T - 1) * nh + head) * HD + 8 * h;
+#pragma unroll
+        for (int st = 0; st < KS; ++st)
+            qb[st] = qi < T ? *reinterpret_cast<const sx8_u32x4*>(qr + 16 * st) : zero4;
+    }
+    const uint16_t* kbase = k_cache + (int64_t)kvh * L * HD;
+    const uint16_t* vbase = v_cache + (int64_t)kvh * L * HD;
+    sx8_u32x4 kreg[KS], vreg[VCH];
+    auto load_blk = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < VCH; ++i) {
+            const int ch = tid + i * 64 * G;
+            const int key = kb * 32 + ch / CPR;
+            vreg[i] = key < ktot ? *reinterpret_cast<const sx8_u32x4*>(vbase + (int64_t)key * HD + 8 * (ch % CPR))
+                                 : zero4;
+        }
+        const int key = kb * 32 + c;
+        const uint16_t* kr = kbase + (int64_t)min(key, ktot - 1) * HD + 8 * h;
+#pragma unroll
+        for (int st = 0; st < KS; ++st)
+            kreg[st] = key < ktot ? *reinterpret_cast<const sx8_u32x4*>(kr + 16 * st) : zero4;
+    };
+    auto store_v = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < VCH; ++i) {
+            const int ch = tid + i * 64 * G;
+            const int kl = ch / CPR, d0 = 8 * (ch % CPR);
+            const int col = (kl & ~12) | ((kl & 4) << 1) | ((kl & 8) >> 1);
+            const uint32_t wv[4] = {vreg[i].x, vreg[i].y, vreg[i].z, vreg[i].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                vt[b][(d0 + e) * kApVRow + col] = (uint16_t)(wv[e >> 1] >> (16 * (e & 1)));
+        }
+    };
+    f32x16 o[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[n][r] = 0.f;
+    float m = -__builtin_inff(), lsum = 0.f;
+    const int qpos = start + qi;
+    load_blk(0);
+    for (int kb = 0; kb < nblk; ++kb) {
+        const int b = kb & 1;
+        store_v(b);
+        sx8_u32x4 kc[KS];
+#pragma unroll
+        for (int st = 0; st < KS; ++st) kc[st] = kreg[st];
+        if (kb + 1 < nblk) load_blk(kb + 1);
+        f32x16 sacc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+#pragma unroll
+        for (int st = 0; st < KS; ++st)
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kc[st]),
+                                                          __builtin_bit_cast(f16x8, qb[st]), sacc, 0, 0, 0);
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = kb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const float v = key <= qpos && key < ktot ? sacc[r] * scale_log2 : -__builtin_inff();
+            sacc[r] = v;
+            mx = fmaxf(mx, v);
+        }
+        mx = fmaxf(mx, lane_swap32(mx));
+        const float mn = fmaxf(m, mx);          // finite: key 0 is always visible
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float pv = __builtin_amdgcn_exp2f(sacc[r] - mn);
+            sacc[r] = pv;
+            ps += pv;
+        }
+        ps += lane_swap32(ps);
+        lsum = lsum * alpha + ps;
+        m = mn;
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[n][r] *= alpha;
+        __syncthreads();      // V^T of block kb staged by every wave
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            f16x8 pb;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) pb[t] = (_Float16)sacc[8 * st + t];
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                const sx8_u32x4 a = *reinterpret_cast<const sx8_u32x4*>(&vt[b][(32 * n + c) * kApVRow + 16 * st + 8 * h]);
+                o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), pb, o[n], 0, 0, 0);
+            }
+        }
+    }
+    if (qi >= T) return;
+    const float inv = 1.0f / lsum;
+    uint16_t* orow = out + ((int64_t)qi * nh + head) * HD;
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * n + 8 * g + 4 * h;
+            const uint32_t lo = (uint32_t)f2h(o[n][4 * g] * inv) | ((uint32_t)f2h(o[n][4 * g + 1] * inv) << 16);
+            const uint32_t hi = (uint32_t)f2h(o[n][4 * g + 2] * inv) | ((uint32_t)f2h(o[n][4 * g + 3] * inv) << 16);
+            *reinterpret_cast<uint2*>(orow + d) = make_uint2(lo, hi);
+        }
+}
+
 extern "C" int32_t sx8_dec_add_rmsnorm(float* resid, const float* delta, const uint16_t* init,
                                        const uint16_t* w, uint16_t* out, int64_t M, int64_t H,
                                        float eps, void* stream) {
@@ -624,6 +776,33 @@ extern "C" int32_t sx8_dec_attn(const uint16_t* q, const uint16_t* k_cache, cons
         hipLaunchKernelGGL(k_attn_decode<64>, dim3((unsigned)nh), dim3(256), 0, as_stream(stream), q,
                            k_cache, v_cache, pos, out, nh, nk, (int)L, scale);
     return check_launch("sx8_dec_attn");
+}
+
+extern "C" int32_t sx8_dec_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                        uint16_t* out, int64_t T, int64_t start, int32_t nh, int32_t nk,
+                                        int32_t hd, int64_t L, float scale, void* stream) {
+    using namespace sx8;
+    if (!q || !k_cache || !v_cache || !out) return fail(SX8_ERR_INVALID, "sx8_dec_attn_prefill: null pointer");
+    const int G = nk > 0 ? nh / nk : 0;
+    if (nh <= 0 || nk <= 0 || nh % nk || (G != 1 && G != 2 && G != 4 && G != 8) || (hd != 64 && hd != 128) ||
+        16 * G > hd || T <= 0 || start < 0 || L <= 0 || start + T > L || L * (int64_t)hd > 0x7FFFFFFF ||
+        (T + 31) / 32 > 0x7FFFFFFF)
+        return fail(SX8_ERR_INVALID, "sx8_dec_attn_prefill: bad shape (nh / nk in {1, 2, 4, 8} with 16 nh / nk "
+                    "<= hd, hd 64 or 128, 0 <= start, start + T <= L)");
+    if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(out, 8))
+        return fail(SX8_ERR_INVALID, "sx8_dec_attn_prefill: q and caches must be 16-byte aligned, out 8-byte");
+    const float sl2 = scale * 1.4426950408889634f;
+    const dim3 grid((unsigned)((T + 31) / 32), (unsigned)nk);
+#define SX8_AP(HD_, G_)                                                                                      \
+    hipLaunchKernelGGL((k_attn_prefill<HD_, G_>), grid, dim3(64 * G_), 0, as_stream(stream), q, k_cache,     \
+                       v_cache, out, (int)T, (int)start, nh, (int)L, sl2)
+    if (hd == 128) {
+        if (G == 1) SX8_AP(128, 1); else if (G == 2) SX8_AP(128, 2); else if (G == 4) SX8_AP(128, 4); else SX8_AP(128, 8);
+    } else {
+        if (G == 1) SX8_AP(64, 1); else if (G == 2) SX8_AP(64, 2); else SX8_AP(64, 4);
+    }
+#undef SX8_AP
+    return check_launch("sx8_dec_attn_prefill");
 }
 
 extern "C" int64_t sx8_dec_attn_workspace_bytes(int32_t nh, int32_t hd) {

@@ -869,23 +869,27 @@ __global__ __launch_bounds__(256) void k_reduce_tiles(const GemmGroup g, const f
     for (int c = 0; c < ne; ++c) y[c] = v[c];
 }
 
-// Y += partial slices 0 .. S - 2 (stride floats apart), in slice order (deterministic).  kVec (Y 16-byte aligned,
-// M N a multiple of 4): 4 floats per thread; otherwise one.
+// Y_i += partial slices 0 .. S - 2 of every matrix of the group, in slice order
+// (deterministic).  Slice s holds the group's M x Ntot partials, matrix i's M x N_i block at
+// poff_i; one launch covers all matrices.  kVec (every Y_i 16-byte aligned, every M N_i a
+// multiple of 4): 4 floats per thread, never straddling two matrices; otherwise one.
 template <bool kVec>
-__global__ __launch_bounds__(256) void k_reduce(float* __restrict__ Y, const float* __restrict__ part,
-                                                int64_t MN, int nparts, int64_t stride) {
+__global__ __launch_bounds__(256) void k_reduce(const GemmGroup g, const float* __restrict__ part,
+                                                int64_t MNtot, int nparts) {
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t e = kVec ? t * 4 : t;
+    if (e >= MNtot) return;
+    int mi = 0;
+    while (mi + 1 < g.n_mats && e >= g.m[mi + 1].poff) ++mi;
+    float* Y = g.m[mi].Y + (e - g.m[mi].poff);
     if constexpr (kVec) {
-        const int64_t i = t * 4;
-        if (i >= MN) return;
-        sx8_float4 y = *reinterpret_cast<const sx8_float4*>(Y + i);
-        for (int p = 0; p < nparts; ++p) y += *reinterpret_cast<const sx8_float4*>(part + p * stride + i);
-        *reinterpret_cast<sx8_float4*>(Y + i) = y;
+        sx8_float4 y = *reinterpret_cast<const sx8_float4*>(Y);
+        for (int p = 0; p < nparts; ++p) y += *reinterpret_cast<const sx8_float4*>(part + p * MNtot + e);
+        *reinterpret_cast<sx8_float4*>(Y) = y;
     } else {
-        if (t >= MN) return;
-        float y = Y[t];
-        for (int p = 0; p < nparts; ++p) y += part[p * stride + t];
-        Y[t] = y;
+        float y = *Y;
+        for (int p = 0; p < nparts; ++p) y += part[p * MNtot + e];
+        *Y = y;
     }
 }
 
@@ -1131,16 +1135,15 @@ int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, in
         hipLaunchKernelGGL(k_reduce_tiles, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, g, part,
                            (int)M, p.Tf, (int)p.n_split, p.St);
     } else if (!p.w1 && p.S > 1) {
-        for (int i = 0; i < n_mats; ++i) {
-            const int64_t MN = M * Ns[i];
-            const float* pm = part + g.m[i].poff;
-            if (aligned(Ys[i], 16) && MN % 4 == 0 && g.m[i].poff % 4 == 0 && (M * Ntot) % 4 == 0)
-                hipLaunchKernelGGL(k_reduce<true>, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0,
-                                   st, Ys[i], pm, MN, p.S - 1, M * Ntot);
-            else
-                hipLaunchKernelGGL(k_reduce<false>, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, st,
-                                   Ys[i], pm, MN, p.S - 1, M * Ntot);
-        }
+        bool vec = true;
+        for (int i = 0; i < n_mats; ++i) vec = vec && aligned(Ys[i], 16) && (M * Ns[i]) % 4 == 0;
+        const int64_t MN = M * Ntot;
+        if (vec)
+            hipLaunchKernelGGL(k_reduce<true>, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0, st, g,
+                               part, MN, p.S - 1);
+        else
+            hipLaunchKernelGGL(k_reduce<false>, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, st, g,
+                               part, MN, p.S - 1);
     }
     return check_launch(what);
 }

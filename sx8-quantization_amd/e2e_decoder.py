@@ -20,7 +20,6 @@ import math
 import time
 
 import torch
-import torch.nn.attention
 import torch.nn as nn
 
 import _sx8lib as _L
@@ -169,6 +168,7 @@ class SX8Decoder(nn.Module):
         pb = {"T": T, "resid": torch.empty(T, H, **f32), "h": torch.empty(T, H, **f16),
               "q": torch.empty(T, nh * hd, **f32), "k": torch.empty(T, nk * hd, **f32),
               "v": torch.empty(T, nk * hd, **f32), "qh": torch.empty(T, nh, hd, **f16),
+              "a": torch.empty(T, nh * hd, **f16),
               "o": torch.empty(T, H, **f32), "g": torch.empty(T, I, **f32), "u": torch.empty(T, I, **f32),
               "m": torch.empty(T, I, **f16), "d": torch.empty(T, H, **f32),
               "pos0": torch.zeros(1, dtype=torch.int64, device=dev),
@@ -179,20 +179,6 @@ class SX8Decoder(nn.Module):
                          self._group_args((ly.gate, ly.up), (pb["g"], pb["u"]))) for ly in self.layers]
         self._pb = pb
         return pb
-
-    @staticmethod
-    def _prefill_attn(qh, kc, vc, rep):
-        """Causal attention of the T prompt rows: qh (T, nh, hd) fp16, kc / vc (nk, T, hd)
-        fp16 views of the caches; returns (T, nh * hd) fp16.  fp16 flash attention (fp32
-        accumulation inside) with the flash backend forced, so a configuration it does not
-        cover raises instead of running the math path."""
-        T, nh, hd = qh.shape
-        q = qh.permute(1, 0, 2)[None]                                          # (1, nh, T, hd)
-        k = kc.repeat_interleave(rep, 0)[None]
-        v = vc.repeat_interleave(rep, 0)[None]
-        with torch.nn.attention.sdpa_kernel(torch.nn.attention.SDPBackend.FLASH_ATTENTION):
-            a = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True)[0]
-        return a.permute(1, 0, 2).reshape(T, nh * hd)
 
     @staticmethod
     def _gemm_group(args, X, st):
@@ -214,8 +200,8 @@ class SX8Decoder(nn.Module):
         """prefill() with the library ops over the T prompt rows: add + RMSNorm
         (sx8_dec_add_rmsnorm, M = T), the prefill GEMMs into preallocated buffers, q/k
         norm + RoPE + KV-cache write (sx8_dec_qk_rope_cache_rows), SiLU * up
-        (sx8_dec_silu_mul) and the final norm inside the lm_head GEMV; attention is fp16
-        flash attention over the cache rows (_prefill_attn).  The residual stream is float32."""
+        (sx8_dec_silu_mul), causal attention over the cache rows (sx8_dec_attn_prefill) and
+        the final norm inside the lm_head GEMV.  The residual stream is float32."""
         cfg = self.cfg
         H, nh, nk, hd, eps = cfg["hidden"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["eps"]
         T = ids.shape[0]
@@ -223,7 +209,6 @@ class SX8Decoder(nn.Module):
         st = _L.stream(self.device)
         P = _L.ptr
         emb = self.embed(ids)                                      # (T, H) fp16
-        rep = nh // nk
         for li, ly in enumerate(self.layers):
             if li == 0:
                 _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), None, P(emb), P(ly.in_norm), P(pb["h"]), T, H,
@@ -235,8 +220,9 @@ class SX8Decoder(nn.Module):
             _L.call("sx8_dec_qk_rope_cache_rows", P(pb["q"]), P(pb["k"]), P(pb["v"]), P(ly.q_norm),
                     P(ly.k_norm), P(self.cos), P(self.sin), P(pb["pos0"]), T, P(pb["qh"]),
                     P(self.k_cache[li]), P(self.v_cache[li]), nh, nk, hd, self.max_len, eps, st)
-            a = self._prefill_attn(pb["qh"], self.k_cache[li][:, :T], self.v_cache[li][:, :T], rep)
-            self._gemm(ly.o, a, pb["o"], st)
+            _L.call("sx8_dec_attn_prefill", P(pb["qh"]), P(self.k_cache[li]), P(self.v_cache[li]), P(pb["a"]),
+                    T, 0, nh, nk, hd, self.max_len, 1.0 / math.sqrt(hd), st)
+            self._gemm(ly.o, pb["a"], pb["o"], st)
             _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["o"]), None, P(ly.post_norm), P(pb["h"]), T,
                     H, eps, st)
             self._gemm_group(pb["groups"][li][1], pb["h"], st)      # gate, up: one call

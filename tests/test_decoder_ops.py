@@ -53,6 +53,56 @@ def test_decode_attention_split_and_single(hiplib, cuda, nh, nk, hd, L, position
             assert err <= 2e-3 * max(1.0, ref.abs().max().item()), (pos, err)
 
 
+@pytest.mark.parametrize("nh,nk,hd,L,T,start", [
+    (32, 8, 128, 1024, 512, 0),     # the decoder's prompt pass (G = 4)
+    (32, 8, 128, 1024, 77, 100),    # ragged tile, keys already in the cache before the prompt
+    (4, 2, 64, 64, 12, 0),          # the tiny e2e decoder (G = 2)
+    (16, 16, 64, 300, 33, 0),       # G = 1
+    (8, 1, 128, 200, 70, 3),        # G = 8
+    (8, 2, 64, 96, 64, 31),         # G = 4 at hd 64, start one short of a block
+])
+def test_prefill_attention(hiplib, cuda, nh, nk, hd, L, T, start):
+    """sx8_dec_attn_prefill against float32 causal attention; cache rows past start + T
+    hold NaN, which must never reach the output."""
+    import torch
+    import _sx8lib as _L
+    g = torch.Generator().manual_seed(nh * 13 + T + start)
+    q = torch.randn(T, nh, hd, generator=g).half()
+    kc = torch.full((nk, L, hd), float("nan")).half()
+    vc = torch.full((nk, L, hd), float("nan")).half()
+    kc[:, :start + T] = torch.randn(nk, start + T, hd, generator=g).half()
+    vc[:, :start + T] = torch.randn(nk, start + T, hd, generator=g).half()
+    scale = 1.0 / math.sqrt(hd)
+    out = torch.empty(T, nh * hd, dtype=torch.float16, device=cuda)
+    qd, kd, vd = q.to(cuda), kc.to(cuda), vc.to(cuda)
+    print("attn_prefill", nh, nk, hd, L, T, start, flush=True)
+    _L.call("sx8_dec_attn_prefill", _L.ptr(qd), _L.ptr(kd), _L.ptr(vd), _L.ptr(out), T, start, nh, nk, hd, L,
+            scale, _L.stream(cuda))
+    G = nh // nk
+    n = start + T
+    mask = torch.arange(n)[None, :] > (start + torch.arange(T))[:, None]
+    ref = torch.empty(T, nh, hd)
+    for h in range(nh):
+        s = (q[:, h].float() @ kc[h // G, :n].float().T) * scale
+        s = s.masked_fill(mask, float("-inf"))
+        ref[:, h] = torch.softmax(s, -1) @ vc[h // G, :n].float()
+    got = out.cpu().float().view(T, nh, hd)
+    assert torch.isfinite(got).all()
+    err = (got - ref).abs().max().item()
+    assert err <= 3e-3 * max(1.0, ref.abs().max().item()), err
+
+
+def test_prefill_attention_rejects_bad_arguments(hiplib, cuda):
+    import torch
+    import _sx8lib as _L
+    t = torch.zeros(4096, dtype=torch.float16, device=cuda)
+    P = _L.ptr
+    with pytest.raises(RuntimeError, match="bad shape"):      # start + T > L
+        _L.call("sx8_dec_attn_prefill", P(t), P(t), P(t), P(t), 8, 1, 4, 2, 64, 8, 0.125, _L.stream(cuda))
+    with pytest.raises(RuntimeError, match="bad shape"):      # 16 * G > hd
+        _L.call("sx8_dec_attn_prefill", P(t), P(t), P(t), P(t), 8, 0, 8, 1, 64, 8, 0.125, _L.stream(cuda))
+
+
 def test_attention_split_rejects_bad_arguments(hiplib, cuda):
     import torch
     import _sx8lib as _L
