@@ -560,18 +560,23 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict
 
 // Causal attention of T prompt rows over the cache (prefill), on MFMA
 // (v_mfma_f32_32x32x16_f16, fp32 accumulation).  Work-group = (32-row query tile, KV
-// head); wave w takes query head kvh * G + w, so the G heads that share a KV head share its
-// staged V.  Per 32-key block a wave computes S^T = K Q^T: keys are the MFMA rows and the
-// tile's 32 queries the columns, so lane l = 32 h + c owns query c (keys 8 g + 4 h + r of
-// the block in accumulator 4 g + r) and the online softmax is lane-local (one exchange
-// with lane l ^ 32 for the other 16 keys).  Then O^T += V^T P^T: the P^T operand of k-step
-// st is the lane's own accumulators 8 st .. 8 st + 7 converted to fp16 (the k index order
-// is free as long as both operands use it: slot t of half h is key 16 st + 8 (t / 4) +
-// 4 h + t % 4), and V^T comes from LDS, where the staging writes each block transposed
-// with that key order (key bits 2 and 3 swapped), so a lane's 8 values are one 16-byte
-// read.  Row i (position start + i) attends keys 0 .. start + i; keys >= start + T are
-// never read.  Output (T, nh * HD) fp16.
+// head), two sets of G waves (one for G = 8): wave g of set s takes query head kvh * G + g
+// and the key blocks s, s + 2, s + 4, ... (two waves per SIMD, each with half of the
+// tile's serial chain; the sets merge their softmax states at the end).  The G heads of a set share
+// the staged K and V of its block.  Per 32-key block a wave computes S^T = K Q^T: keys
+// are the MFMA rows and the tile's 32 queries the columns, so lane l = 32 h + c owns query
+// c (keys 8 g + 4 h + r of the block in accumulator 4 g + r) and the online softmax is
+// lane-local (one exchange with lane l ^ 32 for the other 16 keys).  Then O^T += V^T P^T:
+// the P^T operand of k-step st is the lane's own accumulators 8 st .. 8 st + 7 converted
+// to fp16 (the k index order is free as long as both operands use it: slot t of half h is
+// key 16 st + 8 (t / 4) + 4 h + t % 4), and V^T comes from LDS, where the staging writes
+// each block transposed with that key order (key bits 2 and 3 swapped; two keys per
+// 4-byte write), so a lane's 8 values are one 16-byte read.  K goes through LDS as well
+// (one coalesced global read per set instead of one per wave).  Row i (position start +
+// i) attends keys 0 .. start + i; keys >= start + T are never read.  Output (T, nh * HD)
+// fp16.
 constexpr int kApVRow = 40;      // halves per LDS row of V^T: 32 keys + 8 pad (conflict-free reads)
+constexpr int kApKRow = 136;     // halves per LDS row of K: up to 128 + 8 pad (conflict-free reads)
 
 __device__ __forceinline__ float lane_swap32(float v) {
     const uint32_t u = __builtin_bit_cast(uint32_t, v);
@@ -579,26 +584,50 @@ __device__ __forceinline__ float lane_swap32(float v) {
     return __builtin_bit_cast(float, (threadIdx.x & 32) ? sw[0] : sw[1]);
 }
 
+// Wave sets per work-group: two while 2 G waves (two per SIMD) keep their registers.
+template <int G>
+constexpr int ap_sets() { return G <= 4 ? 2 : 1; }
+
 template <int HD, int G>
-__global__ __launch_bounds__(64 * G) void k_attn_prefill(const uint16_t* __restrict__ q,
-                                                         const uint16_t* __restrict__ k_cache,
-                                                         const uint16_t* __restrict__ v_cache,
-                                                         uint16_t* __restrict__ out, int T, int start,
-                                                         int nh, int L, float scale_log2) {
+struct ApLds {
+    static constexpr int NS = ap_sets<G>();
+    static constexpr int kK = 32 * kApKRow * 2;                 // bytes of one staged K block
+    static constexpr int kV = HD * kApVRow * 2;                 // bytes of one staged V^T block
+    static constexpr int kStage = 2 * NS * (kK + kV);           // [buffer][set]
+    static constexpr int kMerge = NS > 1 ? G * 64 * (2 + 16 * (HD / 32)) * 4 : 0;
+    static constexpr int kBytes = kStage > kMerge ? kStage : kMerge;
+};
+
+template <int HD, int G>
+__global__ __launch_bounds__(64 * G * ap_sets<G>()) void k_attn_prefill(const uint16_t* __restrict__ q,
+                                                          const uint16_t* __restrict__ k_cache,
+                                                          const uint16_t* __restrict__ v_cache,
+                                                          uint16_t* __restrict__ out, int T, int start,
+                                                          int nh, int L, float scale_log2) {
     typedef float f32x16 __attribute__((ext_vector_type(16)));
     typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+    using Lds = ApLds<HD, G>;
+    constexpr int NS = Lds::NS;
     constexpr int KS = HD / 16;                 // k-steps of S^T over the head dimension
     constexpr int NT = HD / 32;                 // 32-row tiles of O^T
     constexpr int CPR = HD / 8;                 // 16-byte chunks per key row
-    constexpr int VCH = 32 * CPR / (64 * G);    // V chunks staged per thread and block
-    static_assert(VCH >= 1 && VCH * 64 * G == 32 * CPR, "V staging split");
-    __shared__ __align__(16) uint16_t vt[2][HD * kApVRow];
+    constexpr int ST = 64 * G;                  // threads per set
+    constexpr int KCH = 32 * CPR / ST;          // K chunks staged per thread and block
+    static_assert(KCH >= 1 && KCH * ST == 32 * CPR, "K staging split");
+    constexpr int VPT = (16 * CPR + ST - 1) / ST;   // V key-pair tasks per thread
+    __shared__ __align__(16) unsigned char lds[Lds::kBytes];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int set = w / G, g = w % G, ts = tid % ST;
     const int c = lane & 31, h = lane >> 5;
-    const int kvh = blockIdx.y, head = kvh * G + w;
+    const int kvh = blockIdx.y, head = kvh * G + g;
     const int q0 = blockIdx.x * 32, qi = q0 + c;
     const int ktot = start + T;                                 // keys in the cache
     const int nblk = (start + min(q0 + 32, T) + 31) / 32;       // key blocks this tile needs
+    const int nstep = (nblk + NS - 1) / NS;
+    auto kt = [&](int buf) { return reinterpret_cast<uint16_t*>(lds + (buf * NS + set) * Lds::kK); };
+    auto vt = [&](int buf) {
+        return reinterpret_cast<uint16_t*>(lds + 2 * NS * Lds::kK + (buf * NS + set) * Lds::kV);
+    };
     const sx8_u32x4 zero4 = {0u, 0u, 0u, 0u};
     sx8_u32x4 qb[KS];
     {
@@ -609,31 +638,55 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const uint16_t* __restr
     }
     const uint16_t* kbase = k_cache + (int64_t)kvh * L * HD;
     const uint16_t* vbase = v_cache + (int64_t)kvh * L * HD;
-    sx8_u32x4 kreg[KS], vreg[VCH];
-    auto load_blk = [&](int kb) {
+    // Step j: set s computes block NS j + s from LDS buffer j & 1 and stages its block of
+    // step j + 1 into the other buffer; its global loads run kPf steps ahead of the
+    // staging (a ring of kPf register sets, the loop unrolled by kPf).  One barrier per
+    // step.
+    constexpr int kPf = 2;
+    sx8_u32x4 kreg[kPf][KCH], vreg[kPf][2 * VPT];
+    auto load_blk = [&](sx8_u32x4 (&kr)[KCH], sx8_u32x4 (&vr)[2 * VPT], int kb) {
 #pragma unroll
-        for (int i = 0; i < VCH; ++i) {
-            const int ch = tid + i * 64 * G;
+        for (int i = 0; i < KCH; ++i) {          // K: coalesced 16-byte chunks of whole rows
+            const int ch = ts + i * ST;
             const int key = kb * 32 + ch / CPR;
-            vreg[i] = key < ktot ? *reinterpret_cast<const sx8_u32x4*>(vbase + (int64_t)key * HD + 8 * (ch % CPR))
-                                 : zero4;
+            kr[i] = key < ktot ? *reinterpret_cast<const sx8_u32x4*>(kbase + (int64_t)key * HD + 8 * (ch % CPR))
+                               : zero4;
         }
-        const int key = kb * 32 + c;
-        const uint16_t* kr = kbase + (int64_t)min(key, ktot - 1) * HD + 8 * h;
 #pragma unroll
-        for (int st = 0; st < KS; ++st)
-            kreg[st] = key < ktot ? *reinterpret_cast<const sx8_u32x4*>(kr + 16 * st) : zero4;
+        for (int i = 0; i < VPT; ++i) {          // V: keys 2 kp, 2 kp + 1 at columns d0 .. d0 + 7
+            const int t = ts + i * ST;
+            const int kp = t & 15, d0 = 8 * (t >> 4);
+            const int key = kb * 32 + 2 * kp;
+            const bool ok = t < 16 * CPR;
+            vr[2 * i] = ok && key < ktot ? *reinterpret_cast<const sx8_u32x4*>(vbase + (int64_t)key * HD + d0) : zero4;
+            vr[2 * i + 1] = ok && key + 1 < ktot
+                                ? *reinterpret_cast<const sx8_u32x4*>(vbase + (int64_t)(key + 1) * HD + d0) : zero4;
+        }
     };
-    auto store_v = [&](int b) {
+    auto stage = [&](int buf, const sx8_u32x4 (&kr)[KCH], const sx8_u32x4 (&vr)[2 * VPT]) {
+        uint16_t* kd = kt(buf);
+        uint16_t* vd = vt(buf);
 #pragma unroll
-        for (int i = 0; i < VCH; ++i) {
-            const int ch = tid + i * 64 * G;
-            const int kl = ch / CPR, d0 = 8 * (ch % CPR);
-            const int col = (kl & ~12) | ((kl & 4) << 1) | ((kl & 8) >> 1);
-            const uint32_t wv[4] = {vreg[i].x, vreg[i].y, vreg[i].z, vreg[i].w};
+        for (int i = 0; i < KCH; ++i) {
+            const int ch = ts + i * ST;
+            *reinterpret_cast<sx8_u32x4*>(kd + (ch / CPR) * kApKRow + 8 * (ch % CPR)) = kr[i];
+        }
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                vt[b][(d0 + e) * kApVRow + col] = (uint16_t)(wv[e >> 1] >> (16 * (e & 1)));
+        for (int i = 0; i < VPT; ++i) {
+            const int t = ts + i * ST;
+            if (t < 16 * CPR) {
+                const int kp = t & 15, d0 = 8 * (t >> 4);
+                const int kl = 2 * kp;
+                const int col = (kl & ~12) | ((kl & 4) << 1) | ((kl & 8) >> 1);   // even; col + 1 is key kl + 1
+                const uint32_t a[4] = {vr[2 * i].x, vr[2 * i].y, vr[2 * i].z, vr[2 * i].w};
+                const uint32_t bb[4] = {vr[2 * i + 1].x, vr[2 * i + 1].y, vr[2 * i + 1].z, vr[2 * i + 1].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t lo = (a[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+                    const uint32_t hi = (bb[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+                    *reinterpret_cast<uint32_t*>(vd + (d0 + e) * kApVRow + col) = lo | (hi << 16);
+                }
+            }
         }
     };
     f32x16 o[NT];
@@ -641,71 +694,136 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const uint16_t* __restr
     for (int n = 0; n < NT; ++n)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[n][r] = 0.f;
+    // running max m (log2 units) and sum; m is raised only when a block's max exceeds it by
+    // more than kLazy (the wave then rescales together), so probabilities stay <= 2^kLazy
+    constexpr float kLazy = 8.f;
     float m = -__builtin_inff(), lsum = 0.f;
     const int qpos = start + qi;
-    load_blk(0);
-    for (int kb = 0; kb < nblk; ++kb) {
-        const int b = kb & 1;
-        store_v(b);
-        sx8_u32x4 kc[KS];
-#pragma unroll
-        for (int st = 0; st < KS; ++st) kc[st] = kreg[st];
-        if (kb + 1 < nblk) load_blk(kb + 1);
-        f32x16 sacc;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
-#pragma unroll
-        for (int st = 0; st < KS; ++st)
-            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kc[st]),
-                                                          __builtin_bit_cast(f16x8, qb[st]), sacc, 0, 0, 0);
-        float mx = -__builtin_inff();
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = kb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            const float v = key <= qpos && key < ktot ? sacc[r] * scale_log2 : -__builtin_inff();
-            sacc[r] = v;
-            mx = fmaxf(mx, v);
+    auto body = [&](int j, sx8_u32x4 (&kr)[KCH], sx8_u32x4 (&vr)[2 * VPT]) {
+        const int b = j & 1, kb = NS * j + set;
+        if (kb + NS < nblk) {
+            stage(b ^ 1, kr, vr);
+            if (kb + NS * (1 + kPf) < nblk) load_blk(kr, vr, kb + NS * (1 + kPf));
         }
-        mx = fmaxf(mx, lane_swap32(mx));
-        const float mn = fmaxf(m, mx);          // finite: key 0 is always visible
-        const float alpha = __builtin_amdgcn_exp2f(m - mn);
-        float ps = 0.f;
+        if (kb < nblk) {
+            const uint16_t* kd = kt(b);
+            const uint16_t* vd = vt(b);
+            f32x16 sacc;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float pv = __builtin_amdgcn_exp2f(sacc[r] - mn);
-            sacc[r] = pv;
-            ps += pv;
+            for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+#pragma unroll
+            for (int st = 0; st < KS; ++st) {
+                const sx8_u32x4 a = *reinterpret_cast<const sx8_u32x4*>(kd + c * kApKRow + 16 * st + 8 * h);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                              __builtin_bit_cast(f16x8, qb[st]), sacc, 0, 0, 0);
+            }
+            // raw scores; the scale (> 0) is applied after the max, inside the exponent's fma.
+            // Masking only where the block reaches past the tile's first query or the keys.
+            if (kb * 32 + 31 > start + q0 || kb * 32 + 31 >= ktot) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    sacc[r] = key <= qpos && key < ktot ? sacc[r] : -__builtin_inff();
+                }
+            }
+            float mx = sacc[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[r]);
+            mx = fmaxf(mx, lane_swap32(mx)) * scale_log2;
+            // set 1 may meet a fully masked block first: it then keeps m = -inf (mx is -inf)
+            if (__builtin_amdgcn_ballot_w64(mx > m + kLazy) != 0) {
+                const float mn = fmaxf(m, mx);
+                const float alpha = mn == -__builtin_inff() ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+                lsum *= alpha;
+#pragma unroll
+                for (int n = 0; n < NT; ++n)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[n][r] *= alpha;
+                m = mn;
+            }
+            float ps = 0.f;
+            const float nm = m == -__builtin_inff() ? 0.f : -m;   // m = -inf: every score is -inf
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], scale_log2, nm));
+                sacc[r] = pv;
+                ps += pv;
+            }
+            lsum += ps + lane_swap32(ps);
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                f16x8 pb;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) pb[t] = (_Float16)sacc[8 * st + t];
+#pragma unroll
+                for (int n = 0; n < NT; ++n) {
+                    const sx8_u32x4 a = *reinterpret_cast<const sx8_u32x4*>(vd + (32 * n + c) * kApVRow + 16 * st + 8 * h);
+                    o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), pb, o[n], 0, 0, 0);
+                }
+            }
         }
-        ps += lane_swap32(ps);
-        lsum = lsum * alpha + ps;
-        m = mn;
+        __syncthreads();      // step j + 1 staged; step j's buffers free for step j + 2
+    };
+    // ring slot i holds the set's blocks of steps i + 1, i + 1 + kPf, ...; step 0 is staged first
+    {
+        sx8_u32x4 k0[KCH], v0[2 * VPT];
+        if (set < nblk) load_blk(k0, v0, set);
+#pragma unroll
+        for (int i = 0; i < kPf; ++i)
+            if (NS * (i + 1) + set < nblk) load_blk(kreg[i], vreg[i], NS * (i + 1) + set);
+        if (set < nblk) stage(0, k0, v0);
+        __syncthreads();
+    }
+    for (int j = 0; j < nstep; j += kPf) {
+#pragma unroll
+        for (int i = 0; i < kPf; ++i)
+            if (j + i < nstep) body(j + i, kreg[i], vreg[i]);
+    }
+    // merge: set 1 hands (m, lsum, O^T) to its partner wave of set 0 through LDS (the
+    // staging buffers are free after the last barrier); lane-contiguous rows
+    float* mg = reinterpret_cast<float*>(lds) + g * 64 * (2 + 16 * NT);
+    if (NS == 1) {
+        if (qi >= T) return;
+        const float inv = 1.0f / lsum;
+        uint16_t* orow = out + ((int64_t)qi * nh + head) * HD;
 #pragma unroll
         for (int n = 0; n < NT; ++n)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[n][r] *= alpha;
-        __syncthreads();      // V^T of block kb staged by every wave
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            f16x8 pb;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) pb[t] = (_Float16)sacc[8 * st + t];
-#pragma unroll
-            for (int n = 0; n < NT; ++n) {
-                const sx8_u32x4 a = *reinterpret_cast<const sx8_u32x4*>(&vt[b][(32 * n + c) * kApVRow + 16 * st + 8 * h]);
-                o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), pb, o[n], 0, 0, 0);
+            for (int gq = 0; gq < 4; ++gq) {
+                const int d = 32 * n + 8 * gq + 4 * h;
+                const uint32_t lo = (uint32_t)f2h(o[n][4 * gq] * inv) | ((uint32_t)f2h(o[n][4 * gq + 1] * inv) << 16);
+                const uint32_t hi = (uint32_t)f2h(o[n][4 * gq + 2] * inv) | ((uint32_t)f2h(o[n][4 * gq + 3] * inv) << 16);
+                *reinterpret_cast<uint2*>(orow + d) = make_uint2(lo, hi);
             }
-        }
+        return;
     }
-    if (qi >= T) return;
-    const float inv = 1.0f / lsum;
+    if (set == 1) {
+        mg[lane] = m;
+        mg[64 + lane] = lsum;
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mg[(2 + 16 * n + r) * 64 + lane] = o[n][r];
+    }
+    __syncthreads();
+    if (set == 1 || qi >= T) return;
+    const float m1 = mg[lane], l1 = mg[64 + lane];
+    const float mm = fmaxf(m, m1);                    // m is finite: set 0 owns block 0
+    const float f0 = __builtin_amdgcn_exp2f(m - mm);
+    const float f1 = m1 == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
+    const float inv = 1.0f / (lsum * f0 + l1 * f1);
+    const float a0 = f0 * inv, a1 = f1 * inv;
     uint16_t* orow = out + ((int64_t)qi * nh + head) * HD;
 #pragma unroll
     for (int n = 0; n < NT; ++n)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d = 32 * n + 8 * g + 4 * h;
-            const uint32_t lo = (uint32_t)f2h(o[n][4 * g] * inv) | ((uint32_t)f2h(o[n][4 * g + 1] * inv) << 16);
-            const uint32_t hi = (uint32_t)f2h(o[n][4 * g + 2] * inv) | ((uint32_t)f2h(o[n][4 * g + 3] * inv) << 16);
+        for (int gq = 0; gq < 4; ++gq) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = o[n][4 * gq + e] * a0 + mg[(2 + 16 * n + 4 * gq + e) * 64 + lane] * a1;
+            const int d = 32 * n + 8 * gq + 4 * h;
+            const uint32_t lo = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
+            const uint32_t hi = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
             *reinterpret_cast<uint2*>(orow + d) = make_uint2(lo, hi);
         }
 }
@@ -794,8 +912,8 @@ extern "C" int32_t sx8_dec_attn_prefill(const uint16_t* q, const uint16_t* k_cac
     const float sl2 = scale * 1.4426950408889634f;
     const dim3 grid((unsigned)((T + 31) / 32), (unsigned)nk);
 #define SX8_AP(HD_, G_)                                                                                      \
-    hipLaunchKernelGGL((k_attn_prefill<HD_, G_>), grid, dim3(64 * G_), 0, as_stream(stream), q, k_cache,     \
-                       v_cache, out, (int)T, (int)start, nh, (int)L, sl2)
+    hipLaunchKernelGGL((k_attn_prefill<HD_, G_>), grid, dim3(64 * G_ * ap_sets<G_>()), 0, as_stream(stream), q, \
+                       k_cache, v_cache, out, (int)T, (int)start, nh, (int)L, sl2)
     if (hd == 128) {
         if (G == 1) SX8_AP(128, 1); else if (G == 2) SX8_AP(128, 2); else if (G == 4) SX8_AP(128, 4); else SX8_AP(128, 8);
     } else {
