@@ -61,6 +61,7 @@ SIGNATURES = [
     ("sx8_dec_qk_rope_cache_rows", _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _I32, _I32,
                                           _I32, _I64, ctypes.c_float, _P]),
     ("sx8_dec_attn", _I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I64, ctypes.c_float, _P]),
+    ("sx8_dec_gemm_silu", _I32, [_P, _P, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P]),
     ("sx8_dec_attn_prefill", _I32, [_P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _I64, ctypes.c_float, _P]),
     ("sx8_dec_attn_split", _I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I64, ctypes.c_float, _P, _I64,
                                   _P]),

@@ -1066,7 +1066,8 @@ template <bool kSplit>
 int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, int64_t K, int n_mats,
                  const WeightSrc* ws_in, int32_t hdr_bytes, ZMode zm, const float* const* bases,
                  const float* const* scales, const float* Z, const int64_t* Ns, int64_t n_cb,
-                 float* const* Ys, hipStream_t st) {
+                 float* const* Ys, hipStream_t st, const float* silu_g = nullptr,
+                 const float* silu_u = nullptr) {
     using namespace sx8;
     int64_t Ntot = 0, NB = 0;
     for (int i = 0; i < n_mats; ++i) {
@@ -1115,7 +1116,8 @@ int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, in
         hipLaunchKernelGGL(k_z_hl, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, Z, n,
                            reinterpret_cast<uint32_t*>(ws));
     }
-    rc = compute_z_sets(X, M, ldx, K, zs, n_cb, true, Xp, st);
+    rc = silu_g ? compute_z_silu(silu_g, silu_u, M, ldx, K, zs, n_cb, Xp, st)
+                : compute_z_sets(X, M, ldx, K, zs, n_cb, true, Xp, st);
     if (rc != SX8_OK) return rc;
     if constexpr (kSplit) {
         launch_hb<true, true, 6>(p, st, Xp, M, g, n_cb, part);
@@ -1169,6 +1171,27 @@ extern "C" int32_t sx8_gemm_prefill(const uint16_t* X, int64_t M, int64_t ldx, i
     w.levels = levels;
     return run_gemm<false>("sx8_gemm_prefill", X, M, ldx, K, 1, &w, hdr_bytes, ZMode::kBasis, &basis,
                            &scales, nullptr, &N, n_cb, &Y, as_stream(stream));
+}
+
+extern "C" int32_t sx8_dec_gemm_silu(const float* g, const float* u, int64_t M, int64_t K,
+                                     const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
+                                     const float* basis, const float* scales, int64_t N, int64_t n_cb,
+                                     float* Y, void* stream) {
+    using namespace sx8;
+    if (!g || !u || !hdr || !levels || !basis || !scales || !Y)
+        return fail(SX8_ERR_INVALID, "sx8_dec_gemm_silu: null pointer");
+    if (hdr_bytes != 6 && hdr_bytes != 8)
+        return fail(SX8_ERR_INVALID, "sx8_dec_gemm_silu: hdr_bytes must be 6 or 8, got %d", hdr_bytes);
+    if (!aligned(hdr, hdr_bytes == 8 ? 8 : 2) || !aligned(levels, 8) || !aligned(g, 4) || !aligned(u, 4) ||
+        !aligned(Y, 4) || !aligned(basis, 16) || !aligned(scales, 8))
+        return fail(SX8_ERR_INVALID, "sx8_dec_gemm_silu: misaligned pointer");
+    const int32_t rc = check_shape("sx8_dec_gemm_silu", M, K, K, N, n_cb);
+    if (rc != SX8_OK) return rc;
+    WeightSrc w{};
+    w.hdr = hdr;
+    w.levels = levels;
+    return run_gemm<false>("sx8_dec_gemm_silu", nullptr, M, K, K, 1, &w, hdr_bytes, ZMode::kBasis, &basis,
+                           &scales, nullptr, &N, n_cb, &Y, as_stream(stream), g, u);
 }
 
 extern "C" int32_t sx8_gemm_prefill_split(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,

@@ -80,11 +80,17 @@ constexpr int kLdsMaxKb = 640;     // activation table staged in LDS up to this 
 // chunk [k-step st][MFMA lane l = 32 hf + r][8 values] holding X[32 G + r][32 kb + 16 hf +
 // 8 st .. + 8], so the GEMM reads every A operand as one contiguous 1 KB wave load.  When
 // packing, the grid covers the rows up to the next multiple of 32 (rows >= M pack zeros).
-template <bool kZ, bool kPack>
+// kSilu: x is not read from X but produced from two float32 matrices (g, u with row
+// stride ldx) as fp16(silu(g) * u) = fp16(g / (1 + exp(-g)) * u), the arithmetic of
+// sx8_dec_silu_mul, so the prefill GEMM of the MLP's down projection takes the gate / up
+// outputs directly.
+template <bool kZ, bool kPack, bool kSilu = false>
 __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ X, int64_t M,
                                                    int64_t ldx, int64_t K, const sx8::ZSets zs,
                                                    int64_t n_cb, bool x_vec, bool hl,
-                                                   uint16_t* __restrict__ Xp) {
+                                                   uint16_t* __restrict__ Xp,
+                                                   const float* __restrict__ sg,
+                                                   const float* __restrict__ su) {
 #pragma clang fp contract(off)
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t rows = kPack ? (M + 31) / 32 * 32 : M;
@@ -102,9 +108,35 @@ __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ 
         kb = gid - m * n_cb;
     }
     const bool row_ok = m < M;
-    const uint16_t* x = X + min(m, M - 1) * ldx + kb * 32;
     const int kmax = row_ok ? (int)min((int64_t)32, K - kb * 32) : 0;
     uint32_t xw[16];
+    if constexpr (kSilu) {
+        const int64_t off = min(m, M - 1) * ldx + kb * 32;
+        float gv[32], uv[32];
+        if (x_vec && kmax == 32) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 a = reinterpret_cast<const float4*>(sg + off)[q];
+                const float4 b = reinterpret_cast<const float4*>(su + off)[q];
+                gv[4 * q] = a.x; gv[4 * q + 1] = a.y; gv[4 * q + 2] = a.z; gv[4 * q + 3] = a.w;
+                uv[4 * q] = b.x; uv[4 * q + 1] = b.y; uv[4 * q + 2] = b.z; uv[4 * q + 3] = b.w;
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 32; ++t) {
+                gv[t] = t < kmax ? sg[off + t] : 0.f;
+                uv[t] = t < kmax ? su[off + t] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const float x0 = gv[2 * t] / (1.0f + __expf(-gv[2 * t])) * uv[2 * t];
+            const float x1 = gv[2 * t + 1] / (1.0f + __expf(-gv[2 * t + 1])) * uv[2 * t + 1];
+            xw[t] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x0) |
+                    ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x1) << 16);
+        }
+    } else {
+    const uint16_t* x = X + min(m, M - 1) * ldx + kb * 32;
     if (x_vec && kmax == 32) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -118,6 +150,7 @@ __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ 
             const uint32_t b = 2 * t + 1 < kmax ? x[2 * t + 1] : 0u;
             xw[t] = a | (b << 16);
         }
+    }
     }
     if constexpr (kPack) {
         const int64_t G = m >> 5;
@@ -817,13 +850,28 @@ int32_t sx8::compute_z_sets(const uint16_t* X, int64_t M, int64_t ldx, int64_t K
     const bool x_vec = aligned(X, 16) && ldx % 8 == 0;
     if (zs.n > 0 && xpack)
         hipLaunchKernelGGL((k_compute_z<true, true>), dim3((unsigned)grid), dim3(256), 0, st, X, M, ldx,
-                           K, zs, n_cb, x_vec, hl, xpack);
+                           K, zs, n_cb, x_vec, hl, xpack, nullptr, nullptr);
     else if (zs.n > 0)
         hipLaunchKernelGGL((k_compute_z<true, false>), dim3((unsigned)grid), dim3(256), 0, st, X, M,
-                           ldx, K, zs, n_cb, x_vec, hl, xpack);
+                           ldx, K, zs, n_cb, x_vec, hl, xpack, nullptr, nullptr);
     else if (xpack)
         hipLaunchKernelGGL((k_compute_z<false, true>), dim3((unsigned)grid), dim3(256), 0, st, X, M,
-                           ldx, K, zs, n_cb, x_vec, hl, xpack);
+                           ldx, K, zs, n_cb, x_vec, hl, xpack, nullptr, nullptr);
+    return check_launch("compute_z");
+}
+
+int32_t sx8::compute_z_silu(const float* g, const float* u, int64_t M, int64_t ld, int64_t K,
+                           const ZSets& zs, int64_t n_cb, uint16_t* xpack, hipStream_t st) {
+    const int64_t rows = (M + 31) / 32 * 32;
+    const int64_t grid = (rows * n_cb + 255) / 256;
+    if (grid > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "compute_z: too large");
+    const bool vec = aligned(g, 16) && aligned(u, 16) && ld % 4 == 0;
+    if (zs.n > 0)
+        hipLaunchKernelGGL((k_compute_z<true, true, true>), dim3((unsigned)grid), dim3(256), 0, st, nullptr, M,
+                           ld, K, zs, n_cb, vec, true, xpack, g, u);
+    else
+        hipLaunchKernelGGL((k_compute_z<false, true, true>), dim3((unsigned)grid), dim3(256), 0, st, nullptr, M,
+                           ld, K, zs, n_cb, vec, true, xpack, g, u);
     return check_launch("compute_z");
 }
 

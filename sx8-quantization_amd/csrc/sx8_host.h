@@ -53,4 +53,9 @@ struct ZSets {
 int32_t compute_z_sets(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, const ZSets& zs,
                        int64_t n_cb, bool hl, uint16_t* xpack, hipStream_t st);
 
+// compute_z_sets (split Z, packed X) with x = fp16(silu(g) * u) produced from two float32
+// matrices with row stride ld (the arithmetic of sx8_dec_silu_mul).
+int32_t compute_z_silu(const float* g, const float* u, int64_t M, int64_t ld, int64_t K,
+                       const ZSets& zs, int64_t n_cb, uint16_t* xpack, hipStream_t st);
+
 }  // namespace sx8

@@ -170,7 +170,7 @@ class SX8Decoder(nn.Module):
               "v": torch.empty(T, nk * hd, **f32), "qh": torch.empty(T, nh, hd, **f16),
               "a": torch.empty(T, nh * hd, **f16),
               "o": torch.empty(T, H, **f32), "g": torch.empty(T, I, **f32), "u": torch.empty(T, I, **f32),
-              "m": torch.empty(T, I, **f16), "d": torch.empty(T, H, **f32),
+              "d": torch.empty(T, H, **f32),
               "pos0": torch.zeros(1, dtype=torch.int64, device=dev),
               "logits": torch.empty(cfg["vocab"], **f32), "tok": torch.zeros(1, dtype=torch.int64, device=dev),
               "scratch_pos": torch.zeros(1, dtype=torch.int64, device=dev)}
@@ -199,9 +199,10 @@ class SX8Decoder(nn.Module):
     def prefill_fused(self, ids):
         """prefill() with the library ops over the T prompt rows: add + RMSNorm
         (sx8_dec_add_rmsnorm, M = T), the prefill GEMMs into preallocated buffers, q/k
-        norm + RoPE + KV-cache write (sx8_dec_qk_rope_cache_rows), SiLU * up
-        (sx8_dec_silu_mul), causal attention over the cache rows (sx8_dec_attn_prefill) and
-        the final norm inside the lm_head GEMV.  The residual stream is float32."""
+        norm + RoPE + KV-cache write (sx8_dec_qk_rope_cache_rows), causal attention over
+        the cache rows (sx8_dec_attn_prefill), SiLU * up inside the down GEMM
+        (sx8_dec_gemm_silu) and the final norm inside the lm_head GEMV.  The residual
+        stream is float32."""
         cfg = self.cfg
         H, nh, nk, hd, eps = cfg["hidden"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["eps"]
         T = ids.shape[0]
@@ -226,8 +227,9 @@ class SX8Decoder(nn.Module):
             _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["o"]), None, P(ly.post_norm), P(pb["h"]), T,
                     H, eps, st)
             self._gemm_group(pb["groups"][li][1], pb["h"], st)      # gate, up: one call
-            _L.call("sx8_dec_silu_mul", P(pb["g"]), P(pb["u"]), P(pb["m"]), T * cfg["inter"], st)
-            self._gemm(ly.down, pb["m"], pb["d"], st)
+            hdr, lvl, bas, sca = ly.down._t44                       # SiLU * up inside the down GEMM
+            _L.call("sx8_dec_gemm_silu", P(pb["g"]), P(pb["u"]), T, cfg["inter"], P(hdr), P(lvl), 6, P(bas),
+                    P(sca), ly.down.out_f, ly.down.qt["n_cb"], P(pb["d"]), st)
         # last row: residual + down output, final norm and lm_head in one launch
         self._gemv_rms(pb["head_group"], pb["resid"][T - 1], None, pb["d"][T - 1], self.final_norm, None,
                        eps, st)

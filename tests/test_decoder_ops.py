@@ -60,6 +60,10 @@ def test_decode_attention_split_and_single(hiplib, cuda, nh, nk, hd, L, position
     (16, 16, 64, 300, 33, 0),       # G = 1
     (8, 1, 128, 200, 70, 3),        # G = 8
     (8, 2, 64, 96, 64, 31),         # G = 4 at hd 64, start one short of a block
+    (32, 8, 128, 64, 1, 0),         # one row
+    (32, 8, 128, 128, 1, 77),       # one row after 77 cached positions
+    (2, 1, 128, 160, 40, 5),        # G = 2 at hd 128
+    (8, 8, 128, 256, 100, 0),       # G = 1 at hd 128
 ])
 def test_prefill_attention(hiplib, cuda, nh, nk, hd, L, T, start):
     """sx8_dec_attn_prefill against float32 causal attention; cache rows past start + T
@@ -227,6 +231,30 @@ def test_fused_gemv_silu(hiplib, cuda):
     # more K blocks than the up-front table passes hold: refused
     with pytest.raises(RuntimeError, match="n_cb"):
         _L.call("sx8_dec_gemv_silu", P(a), P(b), n, hd, lv, 6, bs, sc, ns, 385, ys, st)
+
+
+@pytest.mark.parametrize("M,K,N", [(512, 9728, 2560), (77, 9728, 300), (40, 1000, 130)])
+def test_gemm_silu_matches_two_calls(hiplib, cuda, M, K, N):
+    """sx8_dec_gemm_silu equals sx8_dec_silu_mul + sx8_gemm_prefill bit for bit (the pack
+    pass forms the same fp16 x); K = 1000 takes the unaligned, ragged-tail loads."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    (hdr, lvl, bas, sca), = _mats(cuda, [N], K, 70 + M)
+    n_cb = (K + 31) // 32
+    g = torch.Generator().manual_seed(M + K)
+    a = (torch.randn(M, K, generator=g) * 3).to(cuda)
+    b = torch.randn(M, K, generator=g).to(cuda)
+    m = torch.empty(M, K, dtype=torch.float16, device=cuda)
+    _L.call("sx8_dec_silu_mul", P(a), P(b), P(m), M * K, st)
+    y_ref = torch.empty(M, N, device=cuda)
+    _L.call("sx8_gemm_prefill", P(m), M, K, K, P(hdr), P(lvl), 6, P(bas), P(sca), N, n_cb, P(y_ref), st)
+    y = torch.empty(M, N, device=cuda)
+    print("gemm_silu", M, K, N, flush=True)
+    _L.call("sx8_dec_gemm_silu", P(a), P(b), M, K, P(hdr), P(lvl), 6, P(bas), P(sca), N, n_cb, P(y), st)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), y_ref.cpu())
 
 
 @pytest.mark.parametrize("n,offset", [(151936, 0), (151937, 1), (5, 0), (4099, 3)])
