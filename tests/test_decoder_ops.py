@@ -280,6 +280,9 @@ def test_argmax_advance(hiplib, cuda, n, offset):
 @pytest.mark.parametrize("nh,nk,hd,L,positions", [
     (32, 8, 128, 1024, [0, 31, 32, 700, 1023]),
     (16, 16, 64, 300, [0, 5, 299]),
+    (8, 4, 64, 64, [0, 63]),
+    (32, 8, 128, 1500, [0, 700, 1499]),
+    (16, 2, 128, 400, [0, 399]),                   # G = 8
 ])
 def test_attn_rope_matches_two_calls(hiplib, cuda, nh, nk, hd, L, positions):
     """sx8_dec_attn_rope against sx8_dec_qk_rope_cache + sx8_dec_attn_split: the new k/v rows
