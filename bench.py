@@ -241,6 +241,35 @@ def bench_gemv(torch, L, layer, args):
     grouped = {"launches_per_step": len(gcalls[0]), "ms_per_step": g_ms / K,
                "gbs": step_bytes * K / (g_ms * 1e-3) / 1e9,
                "groups": [g for g in groups]}
+
+    # the same seven launches per step, replayed from a HIP graph (how a decode loop that
+    # captures its step launches them): one graph holds the R rotated steps; the kernels are
+    # the eager ones, only the host dispatch between them goes away
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            cst = L.stream(dev)
+            for r in range(R):
+                for a in calls[r]:
+                    if fn(*(a[:-1] + (cst,))) != 0:
+                        raise RuntimeError(L.lib().sx8_last_error().decode())
+    torch.cuda.current_stream().wait_stream(side)
+    n_rep = max(1, K // R)
+    graph.replay()
+    torch.cuda.synchronize()
+    ge0, ge1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gpu_delay(torch, 50)
+    ge0.record()
+    for _ in range(n_rep):
+        graph.replay()
+    ge1.record()
+    torch.cuda.synchronize()
+    gr_ms = ge0.elapsed_time(ge1)
+    del graph
+    graph_res = {"steps": n_rep * R, "ms_per_step": gr_ms / (n_rep * R),
+                 "gbs": step_bytes * n_rep * R / (gr_ms * 1e-3) / 1e9}
     out = {
         "ms_per_step": total_ms / K,
         "value_gbs": step_bytes * K / (total_ms * 1e-3) / 1e9,
@@ -255,6 +284,7 @@ def bench_gemv(torch, L, layer, args):
             for i, t in enumerate(layer)},
         "step_bytes": step_bytes,
         "grouped": grouped,
+        "graph": graph_res,
     }
     return out
 
@@ -738,6 +768,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "gemv_grouped": gv.get("grouped"),
+        "gemv_graph": gv.get("graph"),
         "prefill": res.get("prefill"),
         "vocab": res.get("vocab"),
         "container": res.get("container"),
