@@ -94,10 +94,21 @@ __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ 
 #pragma clang fp contract(off)
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t rows = kPack ? (M + 31) / 32 * 32 : M;
+    // packing: the row within its 32-row group runs fastest (whole 512-byte runs of packed
+    // stores), so a work-group covers 8 (row group, kb) pairs and its basis rows are staged
+    // once in LDS; otherwise kb runs fastest, which keeps every lane busy for the M = 1
+    // callers
+    __shared__ float4 bsh[kPack && kZ ? sx8::kMaxZSets : 1][8][16];
+    if constexpr (kPack && kZ) {
+        const int64_t rest0 = (int64_t)blockIdx.x * 8, nrest = rows / 32 * n_cb;
+        for (int t = threadIdx.x; t < zs.n * 128; t += 256) {
+            const int si = t >> 7, i = (t >> 4) & 7, q = t & 15;
+            const int64_t r = min(rest0 + i, nrest - 1);
+            bsh[si][i][q] = reinterpret_cast<const float4*>(zs.basis[si] + (r % n_cb) * 64)[q];
+        }
+        __syncthreads();
+    }
     if (gid >= rows * n_cb) return;
-    // packing: the row within its 32-row group runs fastest (broadcast basis loads, whole
-    // 512-byte runs of packed stores); otherwise kb runs fastest, which keeps every lane
-    // busy for the M = 1 callers
     int64_t m, kb;
     if constexpr (kPack) {
         const int64_t rest = gid >> 5;
@@ -168,7 +179,8 @@ __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ 
         if (!row_ok) return;
         const int64_t zi = m * n_cb + kb;
         for (int s = 0; s < zs.n; ++s) {
-            const float4* bv = reinterpret_cast<const float4*>(zs.basis[s] + kb * 64);
+            const float4* bv = kPack ? &bsh[s][threadIdx.x >> 5][0]
+                                     : reinterpret_cast<const float4*>(zs.basis[s] + kb * 64);
             float z[2];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
