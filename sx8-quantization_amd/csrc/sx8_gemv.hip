@@ -348,9 +348,16 @@ __device__ __forceinline__ float block_dot(const BlockRec& o, const KbInfo& ki, 
     return __builtin_fmaf(m, T, acc);
 }
 
+// v + (v of another lane), the lane picked by a DPP control (quad_perm, row mirrors).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl,
+                                                                      0xF, 0xF, false));
+}
+
 // Table entries built inside the GEMV work-group: four threads per kb, thread q holding
 // sub-block q's 8 x values and the matching 8 + 8 basis values.  Z is a quarter dot per
-// thread summed over the four threads with two xor shuffles (this Z is only used
+// thread summed over the four threads with two DPP exchanges (this Z is only used
 // internally; the combined entry point's Z comes from k_kbinfo).
 struct TabIn {
     uint4 x;
@@ -393,10 +400,10 @@ __device__ __forceinline__ void tab_store(KbInfo* info, const TabIn& t, int kb, 
             z0 = __builtin_fmaf(xf, b0[i], z0);
             z1 = __builtin_fmaf(xf, b1[i], z1);
         }
-        z0 += __shfl_xor(z0, 1);
-        z1 += __shfl_xor(z1, 1);
-        z0 += __shfl_xor(z0, 2);
-        z1 += __shfl_xor(z1, 2);
+        z0 = dpp_add<0xB1>(z0);      // + lane ^ 1
+        z1 = dpp_add<0xB1>(z1);
+        z0 = dpp_add<0x4E>(z0);      // + lane ^ 2
+        z1 = dpp_add<0x4E>(z1);
         z = t.s * ((q & 1) == 0 ? z0 : z1);     // t.s is scale (q & 1)
     }
     KbInfo& e = info[ok ? kb : n_cb];
@@ -477,11 +484,6 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
 
 // Sum over a wave64 in a fixed order: DPP butterflies within each row of 16 lanes, then the
 // four row sums (lanes 0, 16, 32, 48) in order.  Uniform result.
-template <int kCtrl>
-__device__ __forceinline__ float dpp_add(float v) {
-    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl,
-                                                                      0xF, 0xF, false));
-}
 __device__ __forceinline__ float wave_sum(float v) {
     v = dpp_add<0xB1>(v);    // quad_perm [1, 0, 3, 2]
     v = dpp_add<0x4E>(v);    // quad_perm [2, 3, 0, 1]
