@@ -560,18 +560,35 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     const int tid = threadIdx.x;
     const int j0 = tid / CT;
     const int c = tid - j0 * CT;
+    // panel number: XCD x (= blockIdx % 8) gets the contiguous range after the
+    // sum_{y < x} ceil((G - y) / 8) panels of the XCDs before it (G = 8 q + r)
     const int G = gridDim.x, xcd = blockIdx.x & 7;
-    int panel = blockIdx.x >> 3;
-    for (int y = 0; y < xcd; ++y) panel += (G - y + 7) >> 3;
-    int mi = 0;                                  // the matrix this panel belongs to
-    while (mi + 1 < grp.n_mats && panel >= grp.m[mi].panels) panel -= grp.m[mi++].panels;
-    const uint8_t* __restrict__ hdr = grp.m[mi].hdr;
-    const uint8_t* __restrict__ levels = grp.m[mi].levels;
-    const float* __restrict__ basis = grp.m[mi].basis;
-    const float* __restrict__ scales = grp.m[mi].scales;
-    const float* __restrict__ Zin = grp.m[mi].Zin;
-    float* __restrict__ Y = grp.m[mi].Y;
-    const int N = grp.m[mi].N;
+    int panel = (blockIdx.x >> 3) + xcd * (G >> 3) + min(xcd, G & 7);
+    // the matrix this panel belongs to; every field is read at a fixed kernel-argument
+    // offset and picked with uniform selects (no chain of dependent argument loads)
+    int mi = 0;
+    if (grp.n_mats > 1 && panel >= grp.m[0].panels) {
+        panel -= grp.m[0].panels;
+        mi = 1;
+        if (grp.n_mats > 2 && panel >= grp.m[1].panels) {
+            panel -= grp.m[1].panels;
+            mi = 2;
+            if (grp.n_mats > 3 && panel >= grp.m[2].panels) {
+                panel -= grp.m[2].panels;
+                mi = 3;
+            }
+        }
+    }
+    auto pick = [&](auto field) {
+        return mi == 0 ? field(grp.m[0]) : mi == 1 ? field(grp.m[1]) : mi == 2 ? field(grp.m[2]) : field(grp.m[3]);
+    };
+    const uint8_t* __restrict__ hdr = pick([](const GemvMat& g) { return g.hdr; });
+    const uint8_t* __restrict__ levels = pick([](const GemvMat& g) { return g.levels; });
+    const float* __restrict__ basis = pick([](const GemvMat& g) { return g.basis; });
+    const float* __restrict__ scales = pick([](const GemvMat& g) { return g.scales; });
+    const float* __restrict__ Zin = pick([](const GemvMat& g) { return g.Zin; });
+    float* __restrict__ Y = pick([](const GemvMat& g) { return g.Y; });
+    const int N = pick([](const GemvMat& g) { return g.N; });
     const int n = panel * CT + c;
     const bool col_ok = n < N;
     const uint32_t nn = (uint32_t)min(n, N - 1);
