@@ -550,7 +550,9 @@ struct GemvGroup {
     int n_mats;
 };
 
-template <int HB, int kMode, int NR, int TP, int kX = kXPlain>
+// kOne: a single matrix (n_mats = 1), so its fields sit at fixed argument offsets and load
+// in the first batch of argument loads.
+template <int HB, int kMode, int NR, int TP, int kX = kXPlain, bool kOne = false>
 __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     const uint16_t* __restrict__ X, const GemvGroup grp, const KbInfo* __restrict__ table,
     int n_cb, int CT, int S, int R, const XProd xp) {
@@ -567,7 +569,7 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     // the matrix this panel belongs to; every field is read at a fixed kernel-argument
     // offset and picked with uniform selects (no chain of dependent argument loads)
     int mi = 0;
-    if (grp.n_mats > 1 && panel >= grp.m[0].panels) {
+    if (!kOne && grp.n_mats > 1 && panel >= grp.m[0].panels) {
         panel -= grp.m[0].panels;
         mi = 1;
         if (grp.n_mats > 2 && panel >= grp.m[1].panels) {
@@ -783,15 +785,24 @@ template <int HB, int kMode, int kX = kXPlain>
 void launch_panel(const PanelPlan& p, size_t smem, hipStream_t st, const uint16_t* X,
                   const GemvGroup& g, const KbInfo* table, int n_cb, const XProd& xp = XProd{}) {
     const dim3 grid(p.grid), block(kPanelThreads);
+    const bool one = g.n_mats == 1;
     if constexpr (kMode == 1 || kMode == 2) {
         if (p.TP == kTabPassesLong) {
-            hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesLong, kX>), grid, block,
-                               smem, st, X, g, table, n_cb, p.CT, p.S, p.R, xp);
+            if (one)
+                hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesLong, kX, true>), grid, block,
+                                   smem, st, X, g, table, n_cb, p.CT, p.S, p.R, xp);
+            else
+                hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesLong, kX>), grid, block,
+                                   smem, st, X, g, table, n_cb, p.CT, p.S, p.R, xp);
             return;
         }
     }
-    hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesShort, kX>), grid, block, smem, st,
-                       X, g, table, n_cb, p.CT, p.S, p.R, xp);
+    if (one)
+        hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesShort, kX, true>), grid, block, smem,
+                           st, X, g, table, n_cb, p.CT, p.S, p.R, xp);
+    else
+        hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesShort, kX>), grid, block, smem, st,
+                           X, g, table, n_cb, p.CT, p.S, p.R, xp);
 }
 
 // 32-bit buffer offsets: every block index a lane forms stays below 2^31 / 24.
