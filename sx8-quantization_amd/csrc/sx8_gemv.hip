@@ -23,6 +23,7 @@
 //     loads that read zeros past the end) and panels are renumbered per XCD (see
 //     k_gemv_panel).
 #include <algorithm>
+#include <type_traits>
 
 #include "sx8_buffer.h"
 #include "sx8_device.h"
@@ -623,9 +624,11 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     // table load below the record loads, which would make the table wait for them)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
+    // the first kNR0 rounds go out before the table build, the rest of the ring after it
+    constexpr int kNR0 = NR < 2 ? NR : 2;
     BlockRec buf[NR];
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
+    for (int i = 0; i < kNR0; ++i) {
         load(buf[i], i);
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -702,6 +705,8 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
         }
     }
     __syncthreads();
+#pragma unroll
+    for (int i = kNR0; i < NR; ++i) load(buf[i], i);
 
     const KbInfo* ti = kMode == 3 ? table : info;
     const SpliceK sk = splice_consts();
@@ -755,9 +760,9 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
 
 // Panel geometry: CT columns per panel (at most 64), from the group's total width:
 // ceil(sum N / 256) gives about one work-group per CU; wider groups take two per CU
-// (co-resident).  Two record buffers: deeper prefetch measured slower on MI355X (the loop
-// already streams near the HBM rate; extra rounds only lengthen the prologue, which is
-// where a launch loses most of its time).
+// (co-resident).  Three record buffers, two of them requested before the table build and
+// the third right after it: more rounds ahead of the table lengthen the prologue, which is
+// where a launch loses most of its time (measured slower on MI355X).
 struct PanelPlan {
     int CT, S, R, TP;
     unsigned grid;
@@ -779,30 +784,38 @@ inline PanelPlan plan_panels(const int64_t* Ns, int n_mats, int n_cb) {
     return p;
 }
 
-constexpr int kRing = 2;   // record buffers per lane
+constexpr int kRing = 3;   // record buffers per lane (at most)
+// Grids above this many work-groups (the vocab-sized matrices: many rounds of panels, each
+// work-group's prologue amortized) run with two record buffers, which measured faster there.
+constexpr unsigned kRing3MaxGrid = 1024;
 
 template <int HB, int kMode, int kX = kXPlain>
 void launch_panel(const PanelPlan& p, size_t smem, hipStream_t st, const uint16_t* X,
                   const GemvGroup& g, const KbInfo* table, int n_cb, const XProd& xp = XProd{}) {
     const dim3 grid(p.grid), block(kPanelThreads);
     const bool one = g.n_mats == 1;
+    auto go = [&](auto nr, auto tp) {
+        constexpr int NR = decltype(nr)::value, TP = decltype(tp)::value;
+        if (one)
+            hipLaunchKernelGGL((k_gemv_panel<HB, kMode, NR, TP, kX, true>), grid, block, smem, st, X, g, table,
+                               n_cb, p.CT, p.S, p.R, xp);
+        else
+            hipLaunchKernelGGL((k_gemv_panel<HB, kMode, NR, TP, kX>), grid, block, smem, st, X, g, table, n_cb,
+                               p.CT, p.S, p.R, xp);
+    };
+    auto by_ring = [&](auto tp) {
+        if (p.grid <= kRing3MaxGrid)
+            go(std::integral_constant<int, kRing>{}, tp);
+        else
+            go(std::integral_constant<int, 2>{}, tp);
+    };
     if constexpr (kMode == 1 || kMode == 2) {
         if (p.TP == kTabPassesLong) {
-            if (one)
-                hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesLong, kX, true>), grid, block,
-                                   smem, st, X, g, table, n_cb, p.CT, p.S, p.R, xp);
-            else
-                hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesLong, kX>), grid, block,
-                                   smem, st, X, g, table, n_cb, p.CT, p.S, p.R, xp);
+            by_ring(std::integral_constant<int, kTabPassesLong>{});
             return;
         }
     }
-    if (one)
-        hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesShort, kX, true>), grid, block, smem,
-                           st, X, g, table, n_cb, p.CT, p.S, p.R, xp);
-    else
-        hipLaunchKernelGGL((k_gemv_panel<HB, kMode, kRing, kTabPassesShort, kX>), grid, block, smem, st,
-                           X, g, table, n_cb, p.CT, p.S, p.R, xp);
+    by_ring(std::integral_constant<int, kTabPassesShort>{});
 }
 
 // 32-bit buffer offsets: every block index a lane forms stays below 2^31 / 24.
