@@ -755,7 +755,7 @@ def main():
             "frac_of_hbm_peak": round(gv.get("value_gbs", 0.0) / HBM_PEAK_GBS, 4),
         },
         "roofline": {
-            "kernel": f"k_gemv_panel<{args.hdr_bytes},1,2,TP> (sx8_gemv)",
+            "kernel": f"k_gemv_panel<{args.hdr_bytes},1,3,TP> (sx8_gemv)",
             "bound": "hbm",
             "achieved": round(gv.get("achieved_gbs", 0.0), 1),
             "peak": HBM_PEAK_GBS,
