@@ -219,7 +219,7 @@ def bench_gemv(torch, L, layer, args):
                          P(*[layer[i]["bas"].data_ptr() for i in ii]),
                          P(*[layer[i]["sca"].data_ptr() for i in ii]), None,
                          (ctypes.c_int64 * n)(*[layer[i]["N"] for i in ii]), t0["n_cb"],
-                         P(*[ys[i].data_ptr() for i in ii]), st))
+                         P(*[ys[i].data_ptr() for i in ii]), None, 0, st))
         gcalls.append(step)
 
     def run_group_step(s):
@@ -294,13 +294,14 @@ def bench_prefill_m(torch, L, layer, args, M):
     g = torch.Generator(device="cpu").manual_seed(12)
     xs = {K: torch.randn(M, K, generator=g).half().to(dev) for K in {t["K"] for t in layer}}
     ys = [torch.empty(M, t["N"], dtype=torch.float32, device=dev) for t in layer]
+    wss = [L.gemm_workspace(M, (t["N"],), t["n_cb"], dev) for t in layer]
     st = L.stream(dev)
     fn = L.lib().sx8_gemm_prefill
 
     def one(i, t):
         rc = fn(L.ptr(xs[t["K"]]), M, t["K"], t["K"], L.ptr(t["hdr"]), L.ptr(t["lvl"]),
                 args.hdr_bytes, L.ptr(t["bas"]), L.ptr(t["sca"]), t["N"], t["n_cb"],
-                L.ptr(ys[i]), st)
+                L.ptr(ys[i]), L.ptr(wss[i][0]), wss[i][1], st)
         if rc != 0:
             raise RuntimeError(L.lib().sx8_last_error().decode())
 
@@ -340,17 +341,19 @@ def bench_prefill_grouped(torch, L, layer, args, M):
     fn = L.lib().sx8_gemm_prefill_group
     by = {t["name"]: i for i, t in enumerate(layer)}
     groups = [["q_proj", "k_proj", "v_proj"], ["o_proj"], ["gate_proj", "up_proj"], ["down_proj"]]
-    calls = []
+    calls, keep = [], []
     for grp in groups:
         ii = [by[n] for n in grp]
         n = len(ii)
         P = ctypes.c_void_p * n
         t0 = layer[ii[0]]
+        ws, nb = L.gemm_workspace(M, [layer[i]["N"] for i in ii], t0["n_cb"], dev)
+        keep.append(ws)
         calls.append((L.ptr(xs[t0["K"]]), M, t0["K"], t0["K"], n, P(*[layer[i]["hdr"].data_ptr() for i in ii]),
                       P(*[layer[i]["lvl"].data_ptr() for i in ii]), args.hdr_bytes,
                       P(*[layer[i]["bas"].data_ptr() for i in ii]), P(*[layer[i]["sca"].data_ptr() for i in ii]),
                       (ctypes.c_int64 * n)(*[layer[i]["N"] for i in ii]), t0["n_cb"],
-                      P(*[ys[i].data_ptr() for i in ii]), st))
+                      P(*[ys[i].data_ptr() for i in ii]), L.ptr(ws), nb, st))
 
     def step():
         for a in calls:
@@ -587,8 +590,10 @@ def bench_vocab(torch, L, args):
     M = 512
     xm = torch.randn(M, K, generator=g).half().to(dev)
     ym = torch.empty(M, N, dtype=torch.float32, device=dev)
+    wsm, nbm = L.gemm_workspace(M, (N,), n_cb, dev)
     ms = timed(lambda: ok(lib.sx8_gemm_prefill(L.ptr(xm), M, K, K, L.ptr(hdr), L.ptr(lvl), args.hdr_bytes,
-                                               L.ptr(bas), L.ptr(sca), N, n_cb, L.ptr(ym), st)), 5)
+                                               L.ptr(bas), L.ptr(sca), N, n_cb, L.ptr(ym), L.ptr(wsm), nbm,
+                                               st)), 5)
     out["gemm_m512"] = {"us": ms * 1e3, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
     log(f"vocab gemm M=512: {ms * 1e3:.1f} us {out['gemm_m512']['tflops']:.0f} TFLOP/s")
     del ym

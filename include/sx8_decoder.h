@@ -81,11 +81,13 @@ int32_t sx8_dec_attn_rope(const float* q_raw, const float* k_raw, const float* v
 /* sx8_dec_silu_mul followed by sx8_gemm_prefill, without the intermediate: the prefill
  * GEMM's pass that packs X and computes Z reads g and u (M x K float32, row stride K)
  * and forms x = fp16(silu(g) * u) itself.  Y (M, N) float32 as sx8_gemm_prefill gives it
- * for that x.  No reference counterpart: the MLP of scripts/infer_sx8.py's prompt pass
- * (Hugging Face SiLU * up, then SX8LinearV44.forward on the down projection). */
+ * for that x; workspace as sx8_gemm_prefill_workspace_bytes(M, 1, &N, n_cb) with
+ * n_cb = ceil(K / 32).  No reference counterpart: the MLP of scripts/infer_sx8.py's prompt
+ * pass (Hugging Face SiLU * up, then SX8LinearV44.forward on the down projection). */
 int32_t sx8_dec_gemm_silu(const float* g, const float* u, int64_t M, int64_t K, const uint8_t* hdr,
                           const uint8_t* levels, int32_t hdr_bytes, const float* basis,
-                          const float* scales, int64_t N, int64_t n_cb, float* Y, void* stream);
+                          const float* scales, int64_t N, int64_t n_cb, float* Y, void* workspace,
+                          int64_t workspace_bytes, void* stream);
 
 /* Causal attention of T prompt rows (prefill): q (T, nh, hd) fp16 (normalized and
  * rotated, as sx8_dec_qk_rope_cache_rows writes it), caches (nk, L, hd) fp16 holding

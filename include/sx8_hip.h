@@ -7,8 +7,11 @@
  *   - fp16 tensors are passed as uint16_t bit patterns; no HIP or torch types appear
  *     in the signatures except the stream, passed as an opaque void* (a hipStream_t;
  *     NULL means the legacy default stream).
- *   - Every entry point enqueues work on `stream`, never synchronises the device and
- *     returns SX8_OK or an error code; sx8_last_error() then holds a message.
+ *   - Every entry point enqueues work on `stream`, never synchronises the device, never
+ *     allocates device memory, and returns SX8_OK or an error code; sx8_last_error() then
+ *     holds a message.  Scratch memory comes from the caller (`workspace`, sized by the
+ *     matching *_workspace_bytes query), so every call can be captured into a HIP graph
+ *     and calls on different streams never share scratch.
  *   - Argument checks (null pointers, sizes, hdr_bytes, alignment) happen on the
  *     host before any launch, so an invalid call never reaches the GPU.
  *
@@ -33,7 +36,7 @@
 extern "C" {
 #endif
 
-#define SX8_ABI_VERSION 1
+#define SX8_ABI_VERSION 2
 
 #define SX8_OK 0
 #define SX8_ERR_INVALID 1      /* bad argument (null pointer, size, hdr_bytes, alignment) */
@@ -119,9 +122,10 @@ int32_t sx8_compute_z(const uint16_t* X, int64_t M, int64_t ldx, const float* ba
  * decode1_v44 at cuda/sx8_decode1_v3.cu:197-221); otherwise Z is computed from
  * basis/scales with the reference's summation tree and, when Z_out != NULL, also written
  * there (the combined form, decode1_v44_combined at :223-246).  X holds n_cb*32 fp16
- * values (16-byte aligned).  `workspace` (>= sx8_gemv_workspace_bytes(n_cb) bytes, 16-byte aligned)
- * receives the per-call activation table; NULL uses a library-owned per-device buffer
- * (allocated on first use; calls overlapping on one device must pass their own).
+ * values (16-byte aligned).  `workspace` (>= sx8_gemv_workspace_bytes(n_cb) bytes, 16-byte
+ * aligned) receives the activation table of the two-launch forms (Z_out != NULL, or
+ * n_cb > 640); the single-launch form builds it in LDS and takes workspace = NULL.  A call
+ * that needs the workspace and gets NULL returns SX8_ERR_INVALID.
  * Tolerance against the float64 yardstick: max|dY| / max|Y| <= 1e-3. */
 int32_t sx8_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels,
                  int32_t hdr_bytes, const float* basis, const float* scales,
@@ -133,61 +137,89 @@ int32_t sx8_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels,
  * W_i . X.  Per matrix either Z_in[i] (Z_in non-NULL) or bases[i] + scales[i]; arrays are
  * host arrays of n_mats device pointers.  Each output is what sx8_gemv gives for that
  * matrix (same decode, same tolerance); one dispatch instead of n_mats, which is most of
- * an M = 1 GEMV's fixed cost.  No counterpart in the reference, whose decode path runs
- * one decode1_v44 per projection (cuda/sx8_decode1_v3.cu:197-246). */
+ * an M = 1 GEMV's fixed cost.  n_cb > 640 runs one two-launch GEMV per matrix and then
+ * needs `workspace` (sx8_gemv_workspace_bytes(n_cb) bytes); otherwise NULL.  No
+ * counterpart in the reference, whose decode path runs one decode1_v44 per projection
+ * (cuda/sx8_decode1_v3.cu:197-246). */
 int32_t sx8_gemv_group(const uint16_t* X, int32_t n_mats, const uint8_t* const* hdrs,
                        const uint8_t* const* levels, int32_t hdr_bytes,
                        const float* const* bases, const float* const* scales,
                        const float* const* Z_in, const int64_t* Ns, int64_t n_cb,
-                       float* const* Ys, void* stream);
+                       float* const* Ys, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Workspace bytes sx8_gemv needs for n_cb K blocks (112 per block). */
 int64_t sx8_gemv_workspace_bytes(int64_t n_cb);
 
+/* Workspace bytes of a prefill call over n_mats (1..4) matrices of Ns[i] output columns
+ * that share an (M, K) X with n_cb = ceil(K / 32): the PCA operand of every matrix, the
+ * packed copy of X and the split-K partials of the plan the call will run.  The same value
+ * serves sx8_gemm_prefill, _split, _z, _core (n_mats = 1) and _group; sx8_dec_gemm_silu
+ * (K = its inner size).  -1 for an invalid shape.  The plan depends only on (M, sum Ns,
+ * the group's column tiles, n_cb) and on the SX8_GEMM_TILE environment variable at the
+ * time of the call.  No counterpart in the reference, whose wrappers allocate outputs and
+ * Z with torch inside each call (cuda/sx8_gemm_compact.cu:157-194). */
+int64_t sx8_gemm_prefill_workspace_bytes(int64_t M, int32_t n_mats, const int64_t* Ns, int64_t n_cb);
+
+/* The plan a prefill call with these sizes runs (for logs and tests): desc[0] tile rows
+ * (128, 256 or 512), desc[1] work-groups, desc[2] K ranges, desc[3] K blocks per range,
+ * desc[4] whole 512-row tiles before the split tail, desc[5] tiles of the split tail,
+ * desc[6] workspace bytes, desc[7] 0.  No counterpart in the reference. */
+int32_t sx8_gemm_prefill_plan(int64_t M, int32_t n_mats, const int64_t* Ns, int64_t n_cb,
+                              int64_t* desc);
+
 /* Prefill GEMM Y (M, N) float32 = X (M, ldx) fp16 . W^T on the v4.4 layout.
- * The PCA-free core weights (rlo + step*lv, float32 then fp16) are decoded straight into
- * MFMA operands (v_mfma_f32_32x32x16_f16, float32 accumulation); the PCA term
- * sum_kb c0 Z0 + c1 Z1 is added by extra MFMA k-steps from Z, which this call computes
- * first (reference summation tree) into the library's per-device workspace (allocated on
- * first use; calls overlapping on one device must not share it -- use
- * sx8_gemm_prefill_z with a caller-owned Z instead).  Columns k >= K of X are never
+ * The PCA-free core weights rlo + step*lv are decoded in float32 (the reference's
+ * R32 form, cuda/sx8_fused_wmma.cu:70-94), rounded to fp16 and fed to
+ * v_mfma_f32_32x32x16_f16 with float32 accumulation; the PCA term sum_kb c0 Z0 + c1 Z1 is
+ * added by extra MFMA k-steps over Z (split into fp16 hi + lo parts), which the call
+ * computes first with the reference's summation tree.  The MFMA operands are therefore
+ * not the canonical R64 fp16 weights (those come from sx8_dequant_f16); the product is
+ * within the tolerance below.  `workspace` (256-byte aligned, >= sx8_gemm_prefill_
+ * workspace_bytes(M, 1, &N, n_cb) bytes) holds Z, the packed X and any split-K partials;
+ * calls that overlap in time need distinct workspaces.  Columns k >= K of X are never
  * read.  Tolerance against the float64 yardstick: max|dY| / max|Y| <= 1e-3.
  * Replaces gemm_compact (cuda/sx8_gemm_compact.cu:171-194, kernel :55-152) together
  * with its Z precompute compute_z44_batch (:157-169). */
 int32_t sx8_gemm_prefill(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
                          const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
                          const float* basis, const float* scales, int64_t N, int64_t n_cb,
-                         float* Y, void* stream);
+                         float* Y, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Same GEMM from kb-major split arrays (dmin/dmax fp16, config, coeff, hi (n_blk*16),
- * lo (n_blk*8), all in bid = kb*N + n order).
+ * lo (n_blk*8), all in bid = kb*N + n order).  Same workspace as sx8_gemm_prefill.
  * Replaces fused_forward (cuda/sx8_fused_wmma.cu:134-154, kernel :11-132). */
 int32_t sx8_gemm_prefill_split(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
                                const uint16_t* dmin, const uint16_t* dmax,
                                const uint8_t* config, const uint8_t* coeff,
                                const uint8_t* hi, const uint8_t* lo, const float* basis,
                                const float* scales, int64_t N, int64_t n_cb, float* Y,
-                               void* stream);
+                               void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Same GEMM with the PCA precompute supplied by the caller: Z (M, n_cb, 2) float32 as
- * written by sx8_compute_z.  One launch; no workspace.
+ * written by sx8_compute_z.  Three launches: Z converted to the fp16 hi/lo operand and X
+ * packed (both into `workspace`, sized as for sx8_gemm_prefill), the GEMM, and for a
+ * split-K plan the fixed-order sum of the partials.
  * Replaces gemm_compact(X, hdr, levels, Z, n_cb, hdr_bytes) (cuda/sx8_gemm_compact.cu:
  * 171-194, kernel :55-152). */
 int32_t sx8_gemm_prefill_z(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
                            const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
-                           const float* Z, int64_t N, int64_t n_cb, float* Y, void* stream);
+                           const float* Z, int64_t N, int64_t n_cb, float* Y,
+                           void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Prefill GEMMs of n_mats (1..4) v4.4 weights that share X (same K, same hdr_bytes), e.g.
  * the q/k/v or gate/up projections of a prompt: Ys[i] (M, Ns[i]) float32 = X . W_i^T + PCA,
  * each what sx8_gemm_prefill gives for that matrix up to the split-K summation order.
- * Host arrays of n_mats device pointers.  One pass over X packs it for all matrices and one
- * launch covers the column tiles of the whole group.  No counterpart in the reference, whose
- * runtime calls gemm_sx8_compact once per projection (scripts/sx8_gemm_compact.py:42-74). */
+ * Host arrays of n_mats device pointers; workspace sized by
+ * sx8_gemm_prefill_workspace_bytes(M, n_mats, Ns, n_cb).  One pass over X packs it for all
+ * matrices and one launch covers the column tiles of the whole group.  No counterpart in
+ * the reference, whose runtime calls gemm_sx8_compact once per projection
+ * (scripts/sx8_gemm_compact.py:42-74). */
 int32_t sx8_gemm_prefill_group(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, int32_t n_mats,
                                const uint8_t* const* hdrs, const uint8_t* const* levels,
                                int32_t hdr_bytes, const float* const* bases,
                                const float* const* scales, const int64_t* Ns, int64_t n_cb,
-                               float* const* Ys, void* stream);
+                               float* const* Ys, void* workspace, int64_t workspace_bytes,
+                               void* stream);
 
 /* Output-side PCA: Y[m, n] += sum_kb c0(kb,n) Z[m,kb,0] + c1(kb,n) Z[m,kb,1], c0/c1 the
  * signed nibbles of the coeff byte in the v4.4 header (float32 FMAs, one thread per
@@ -197,10 +229,13 @@ int32_t sx8_gemm_pca_z(const float* Z, int64_t M, const uint8_t* hdr, int32_t hd
                        int64_t N, int64_t n_cb, float* Y, void* stream);
 
 /* Prefill GEMM of the PCA-free core weights only (rlo + step*lv); with sx8_gemm_pca_z it
- * gives the same product as sx8_gemm_prefill_z in two passes. */
+ * gives the same product as sx8_gemm_prefill_z in two passes.  With X = the identity
+ * (M = K = n_cb*32 rows of unit vectors) Y[k, n] is exactly the fp16 MFMA operand of weight
+ * (n, k), which pins the operand decode bit for bit.  Workspace as for sx8_gemm_prefill. */
 int32_t sx8_gemm_prefill_core(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
                               const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
-                              int64_t N, int64_t n_cb, float* Y, void* stream);
+                              int64_t N, int64_t n_cb, float* Y, void* workspace,
+                              int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

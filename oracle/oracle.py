@@ -23,6 +23,10 @@ Contents (each restates a reference function; paths are relative to
 * ``gemm_f64`` -- the float64 yardstick Y = X . W16^T.
 * ``dequant_ggml`` -- C R32-ggml, llama.cpp's no-PCA float32 dequant of block_sx8
   records (llama-cpp-sx8.patch:746-767), with or without fused multiply-adds.
+* ``core_f16`` -- C: the prefill GEMM's fp16 MFMA operand, the PCA-free core of the
+  reference's float32 decode (cuda/sx8_fused_wmma.cu:70-94) in the kernel's evaluation
+  order; ``core_exact_weight`` -- the same recipe in exact rational arithmetic with every
+  binary32 operation correctly rounded (independent check).
 
 Parity status of each function is recorded next to it.
 """
@@ -66,6 +70,8 @@ def lib():
         L.sx8o_dequant_ggml.restype = None
         L.sx8o_dequant_ggml.argtypes = [i64, p, i32, p]
         L.sx8o_dequant_r32.restype = None
+        L.sx8o_core_f16.argtypes = [i64, p, p, p, p, p, p]
+        L.sx8o_core_f16.restype = None
         L.sx8o_gemm_f64.argtypes = [i32, i32, i32, p, i32, p, i32, p]
         L.sx8o_gemm_f64.restype = None
         L.sx8o_gemv_f32.argtypes = [i32, i32, i32, p, p, p]
@@ -158,13 +164,16 @@ def v6_encode(blocks: np.ndarray):
     return best_lev.astype(np.uint8).reshape(n, 32), dmin, dmax, config.astype(np.uint8), best_str
 
 
-def pca_correct(levels, dmin, dmax, config, blocks, n_cb, n_bases=4):
+def pca_correct(levels, dmin, dmax, config, blocks, n_cb, n_bases=4, _plant=None):
     """PCA post-correction per column slice kb (quantize…:75-142), numpy float32.
 
-    Parity unpinned against the reference bit for bit: the SVD's singular-vector
-    signs depend on the LAPACK build and the [-8, 7] clamp makes a sign flip
-    visible.  Tests pin it by invariants (orthonormal bases, |c| <= 8, residual
-    MSE not worse than without PCA on the kept coefficients).
+    Pinned by known answers (tests/test_quantizer.py, test_pca_known_answers): residual
+    slices built from orthonormal directions and mutually orthogonal coefficient rows of
+    distinct energy, so the kept directions (Vh[:2], up to the sign the SVD returns), the
+    lower-median / 3 scales and every coefficient byte (given that sign) are known in
+    closed form.  The sign itself is not pinnable: it depends on the LAPACK build, and
+    the [-8, 7] clamp makes a flip visible in the bytes.  ``_plant`` (tests only) swaps in
+    a known mistake -- "median/4", "upper_median" or "vh1:3" -- to show the pin fails.
     Returns coeff (n_blk,1) u8, data (n_cb,64) f32, scales (n_cb,2) f32.
     """
     n_blk = blocks.shape[0]
@@ -191,12 +200,14 @@ def pca_correct(levels, dmin, dmax, config, blocks, n_cb, n_bases=4):
             rec[:, sb * 8:(sb + 1) * 8] = lo_sb[:, None] + step_sb[:, None] * lv_f[si][:, sb * 8:(sb + 1) * 8]
         err = (blocks[si] - rec).astype(np.float32)
         _, _, vh = np.linalg.svd(err, full_matrices=False)
-        basis = vh[:n_bases].astype(np.float32)
+        first = 1 if _plant == "vh1:3" else 0
+        basis = vh[first:first + n_bases].astype(np.float32)
         craw = basis @ err.T
         # torch.median returns the lower median for even counts
         srt = np.sort(np.abs(craw), axis=1)
-        med = srt[:, (srt.shape[1] - 1) // 2]
-        sc = np.maximum(med / np.float32(3.0), np.float32(1e-10)).astype(np.float32)
+        med = srt[:, srt.shape[1] // 2 if _plant == "upper_median" else (srt.shape[1] - 1) // 2]
+        div = np.float32(4.0 if _plant == "median/4" else 3.0)
+        sc = np.maximum(med / div, np.float32(1e-10)).astype(np.float32)
         cq = np.clip(np.rint(craw / sc[:, None]), -8, 7).astype(np.int8)
         byte0 = (cq[0].view(np.uint8) & 0xF) | ((cq[1].view(np.uint8) & 0xF) << 4)
         coeff[si, 0] = byte0
@@ -321,6 +332,53 @@ def dequant_ggml(blocks: np.ndarray, contract: bool = True) -> np.ndarray:
     out = np.empty((b.shape[0], 32), dtype=np.float32)
     lib().sx8o_dequant_ggml(b.shape[0], _ptr(b), int(bool(contract)), _ptr(out))
     return out
+
+
+def core_f16(qt):
+    """fp16 (out_f, in_f) operand tile values of the prefill GEMM (no PCA), C oracle.
+
+    Pinned by closed forms (degenerate block -> dmin, level 0 -> rlo per strategy, signed
+    zero), by ``core_exact_weight`` on fuzzed and quantized blocks, and by its distance
+    to R64 without PCA (at most one fp16 ulp, rarely nonzero): tests/test_oracle.py."""
+    n_blk, dmin, dmax, cfg, _, hi, lo = _fields(qt)
+    out = np.empty(n_blk * 32, dtype=np.uint16)
+    lib().sx8o_core_f16(n_blk, _ptr(dmin), _ptr(dmax), _ptr(cfg), _ptr(hi), _ptr(lo), _ptr(out))
+    out_f, in_f = qt["shape"]
+    return out.view(np.float16).reshape(out_f, qt["n_cb"] * 32)[:, :in_f]
+
+
+def _rn32(fr: Fraction) -> Fraction:
+    """Correctly rounded binary32 (round to nearest, ties to even) of an exact rational,
+    subnormals included (the three float32 neighbours of the float64 approximation
+    bracket the exact value)."""
+    if fr == 0:
+        return Fraction(0)
+    x = np.float32(float(fr))
+    cands = [np.nextafter(x, np.float32(-np.inf)), x, np.nextafter(x, np.float32(np.inf))]
+
+    def key(c):
+        return abs(Fraction(float(c)) - fr), int(np.array(c, dtype=np.float32).view(np.uint32)) & 1
+    return Fraction(float(min(cands, key=key)))
+
+
+def core_exact_weight(dmin16, dmax16, cfg, lv, t, c_step=None):
+    """One operand value of ``core_f16`` from exact rationals: every binary32 operation
+    rounded once (a fused multiply-add rounds the exact a*b + c once), then fp16 RNE.
+    ``c_step`` overrides the 0.015873 constant (tests plant 1/63 here to show that the
+    checks discriminate).  Finite endpoints only."""
+    lo = Fraction(float(np.float16(dmin16)))
+    hi = Fraction(float(np.float16(dmax16)))
+    c = Fraction(float(np.float32(C_STEP))) if c_step is None else Fraction(c_step)
+    d = _rn32(hi - lo)
+    q = _rn32(d / 4)
+    m = _rn32(d * c)
+    s = (cfg >> ((t >> 3) * 2)) & 3
+    k1 = (0, 0, 3, 1)[s]
+    e = (0, 2, 2, 1)[s]
+    rlo = _rn32(q * k1 + lo)
+    step = m / (2 ** e) if d > 0 else Fraction(float(np.float32(STEP_FLOOR)))
+    w = _rn32(step * lv + rlo)
+    return np.float16(np.float32(float(w)))
 
 
 def dequant_r64_numpy(qt, bases_info):

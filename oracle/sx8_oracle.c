@@ -21,6 +21,8 @@
  *     (cuda/sx8_embed_v44.cu:46-75), kept only to count last-bit disagreements;
  *   - R32-ggml, llama.cpp's no-PCA float32 dequant of GGUF block_sx8 records
  *     (llama-cpp-sx8.patch:746-767), with and without fused multiply-adds;
+ *   - the prefill GEMM's fp16 MFMA operand (the PCA-free core of the reference's float32
+ *     decode, cuda/sx8_fused_wmma.cu:70-94, in the HIP kernel's evaluation order);
  *   - float64-accumulated GEMV/GEMM references used as the 1e-3 yardstick
  *     (scripts/sx8_decode1_v3.py:131-133, scripts/sx8_fused_wmma.py:128-132);
  *   - the CPU dequant + fp32-accumulated GEMV that bench.py reports as its CPU
@@ -195,6 +197,43 @@ void sx8o_dequant_r32(int64_t n_blocks, int32_t n_cb,
                     + (float)c0 * scales[cb * 2] * basis[cb * 64 + t]
                     + (float)c1 * scales[cb * 2 + 1] * basis[cb * 64 + 32 + t];
             out16[bid * 32 + t] = sx8o_f32_to_f16(w);
+        }
+    }
+}
+
+/* ------------------------------------------------- prefill GEMM operand (core) */
+
+/* The fp16 operand the prefill GEMM feeds to its MFMAs for weight t of a block: the
+ * PCA-free core rlo + step*lv of the reference's float32 decode (cuda/sx8_fused_wmma.cu:
+ * 70-94, whose WMMA tiles also hold float32 weights rounded with __float2half), evaluated
+ * the way the HIP kernel does it (csrc/sx8_gemm.hip, sub_range / dec_pair):
+ *   d = hi - lo, q = d * 0.25f, m = d * 0.015873f           (binary32, each rounded)
+ *   s = strategy of sub-block t/8; k1 = {0, 0, 3, 1}[s], e = {0, 2, 2, 1}[s]
+ *   rlo  = fmaf(q, k1, lo)                                  (= lo + q*(3*(s==2)+(s==3)))
+ *   step = d > 0 ? m * 2^-e : 1e-10f    (the range rhi - rlo is d * {1, 1/4, 1/4, 1/2})
+ *   w    = fmaf(step, lv, rlo), then binary32 -> fp16 (RNE).
+ * The PCA term is not part of the operand (the kernel adds it through Z).  The reference
+ * floors step at 1e-10 after scaling; for hi > lo the unfloored step is at least
+ * 2.4e-10 (the smallest fp16 range times 0.015873 / 4), so the floor binds exactly when
+ * d <= 0 (NaN endpoints: d is NaN, step = 1e-10 and rlo NaN propagates).
+ * out16: n_blocks * 32 fp16 bit patterns, pkl block order. */
+void sx8o_core_f16(int64_t n_blocks, const uint16_t* dmin, const uint16_t* dmax,
+                   const uint8_t* config, const uint8_t* hi, const uint8_t* lo, uint16_t* out16) {
+#pragma omp parallel for schedule(static)
+    for (int64_t bid = 0; bid < n_blocks; bid++) {
+        const float lo_f = sx8o_f16_to_f32(dmin[bid]);
+        const float hi_f = sx8o_f16_to_f32(dmax[bid]);
+        const float d = hi_f - lo_f;
+        const float q = d * 0.25f;
+        const float m = d * 0.015873f;
+        for (int t = 0; t < 32; t++) {
+            const int s = (config[bid] >> ((t >> 3) * 2)) & 3;
+            static const float k1t[4] = {0.f, 0.f, 3.f, 1.f};
+            static const int et[4] = {0, 2, 2, 1};
+            const float rlo = fmaf(q, k1t[s], lo_f);
+            const float step = d > 0.f ? ldexpf(m, -et[s]) : 1e-10f;
+            const float lv = (float)sx8o_level(hi + bid * 16, lo + bid * 8, t);
+            out16[bid * 32 + t] = sx8o_f32_to_f16(fmaf(step, lv, rlo));
         }
     }
 }

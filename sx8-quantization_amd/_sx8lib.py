@@ -45,15 +45,18 @@ SIGNATURES = [
     ("sx8_embed_gather", _I32, [_P, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _P, _P]),
     ("sx8_compute_z", _I32, [_P, _I64, _I64, _P, _P, _I64, _P, _P]),
     ("sx8_gemv", _I32, [_P, _P, _P, _I32, _P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P]),
-    ("sx8_gemv_group", _I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _I64, _P, _P]),
+    ("sx8_gemv_group", _I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _P, _I64, _P, _P, _I64, _P]),
     ("sx8_gemv_workspace_bytes", _I64, [_I64]),
-    ("sx8_gemm_prefill", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P]),
+    ("sx8_gemm_prefill_workspace_bytes", _I64, [_I64, _I32, _P, _I64]),
+    ("sx8_gemm_prefill_plan", _I32, [_I64, _I32, _P, _I64, _P]),
+    ("sx8_gemm_prefill", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _I64, _P]),
     ("sx8_gemm_prefill_split", _I32,
-     [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P]),
-    ("sx8_gemm_prefill_z", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _I64, _I64, _P, _P]),
-    ("sx8_gemm_prefill_group", _I32, [_P, _I64, _I64, _I64, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P]),
+     [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P]),
+    ("sx8_gemm_prefill_z", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _I64, _I64, _P, _P, _I64, _P]),
+    ("sx8_gemm_prefill_group", _I32,
+     [_P, _I64, _I64, _I64, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P, _I64, _P]),
     ("sx8_gemm_pca_z", _I32, [_P, _I64, _P, _I32, _I64, _I64, _P, _P]),
-    ("sx8_gemm_prefill_core", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _I64, _I64, _P, _P]),
+    ("sx8_gemm_prefill_core", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _I64, _I64, _P, _P, _I64, _P]),
     # include/sx8_decoder.h
     ("sx8_dec_add_rmsnorm", _I32, [_P, _P, _P, _P, _P, _I64, _I64, ctypes.c_float, _P]),
     ("sx8_dec_qk_rope_cache", _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
@@ -61,7 +64,7 @@ SIGNATURES = [
     ("sx8_dec_qk_rope_cache_rows", _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _I32, _I32,
                                           _I32, _I64, ctypes.c_float, _P]),
     ("sx8_dec_attn", _I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I64, ctypes.c_float, _P]),
-    ("sx8_dec_gemm_silu", _I32, [_P, _P, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P]),
+    ("sx8_dec_gemm_silu", _I32, [_P, _P, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _I64, _P]),
     ("sx8_dec_attn_prefill", _I32, [_P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _I64, ctypes.c_float, _P]),
     ("sx8_dec_attn_split", _I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I64, ctypes.c_float, _P, _I64,
                                   _P]),
@@ -74,22 +77,38 @@ SIGNATURES = [
                                     _I64, _P, _P]),
     ("sx8_dec_gemv_silu", _I32, [_P, _P, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P]),
 ]
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 _lock = threading.Lock()
 
 
 def build(verbose: bool = False) -> str:
-    """Compile every HIP source into LIB_PATH with hipcc for gfx950 (always rebuilds)."""
-    srcs = [os.path.join(CSRC_DIR, s) for s in SOURCES]
-    tmp = LIB_PATH + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, "-I", CSRC_DIR, "-I", INCLUDE_DIR, "-o", tmp, *srcs]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + res.stdout + res.stderr)
-    if verbose:
-        print(res.stderr)
+    """Compile every HIP source for gfx950 with hipcc (one object per source, in parallel)
+    and link LIB_PATH (always rebuilds)."""
+    from concurrent.futures import ThreadPoolExecutor
+    import tempfile
+    with tempfile.TemporaryDirectory(prefix="sx8_build_") as d:
+        def compile_one(name):
+            obj = os.path.join(d, name + ".o")
+            flags = [f for f in HIP_FLAGS if f != "-shared"]
+            cmd = [HIPCC, *flags, "-I", CSRC_DIR, "-I", INCLUDE_DIR, "-c", "-o", obj,
+                   os.path.join(CSRC_DIR, name)]
+            return obj, subprocess.run(cmd, capture_output=True, text=True)
+        jobs = min(len(SOURCES), max(1, (os.cpu_count() or 1)), 8)
+        with ThreadPoolExecutor(jobs) as ex:
+            results = list(ex.map(compile_one, SOURCES))
+        errs = [r.stdout + r.stderr for _, r in results if r.returncode != 0]
+        if errs:
+            raise RuntimeError("hipcc failed:\n" + "\n".join(errs))
+        if verbose:
+            for _, r in results:
+                print(r.stderr)
+        tmp = LIB_PATH + ".tmp"
+        cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *[o for o, _ in results]]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError("hipcc link failed:\n" + res.stdout + res.stderr)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 
@@ -159,6 +178,30 @@ def stream(device=None) -> ctypes.c_void_p:
     """The current torch stream on `device` as a hipStream_t."""
     import torch
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def gemm_workspace(M, Ns, n_cb, device):
+    """A fresh workspace for a prefill call over matrices of Ns output columns sharing an
+    (M, K) X (sx8_gemm_prefill_workspace_bytes), from torch's caching allocator on the
+    current stream: stream-ordered, so calls on different streams never share it, and
+    capture-safe (a graph keeps its own copy).  Returns (tensor, bytes)."""
+    import torch
+    n = len(Ns)
+    nb = int(lib().sx8_gemm_prefill_workspace_bytes(int(M), n, (ctypes.c_int64 * n)(*[int(v) for v in Ns]),
+                                                    int(n_cb)))
+    if nb < 0:
+        raise RuntimeError(f"sx8_gemm_prefill_workspace_bytes: bad shape M={M} Ns={list(Ns)} n_cb={n_cb}")
+    return torch.empty(max(nb, 256), dtype=torch.uint8, device=device), nb
+
+
+def gemm_plan(M, Ns, n_cb):
+    """The plan a prefill call with these sizes runs: dict(tile, groups, k_ranges,
+    kb_per_range, whole_tiles, split_tiles, workspace)."""
+    n = len(Ns)
+    desc = (ctypes.c_int64 * 8)()
+    call("sx8_gemm_prefill_plan", int(M), n, (ctypes.c_int64 * n)(*[int(v) for v in Ns]), int(n_cb), desc)
+    keys = ("tile", "groups", "k_ranges", "kb_per_range", "whole_tiles", "split_tiles", "workspace")
+    return dict(zip(keys, (int(v) for v in desc[:7])))
 
 
 def as_device(a, np_dtype, device):

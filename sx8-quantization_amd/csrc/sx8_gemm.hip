@@ -1058,35 +1058,61 @@ void launch_hb(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, con
         launch_mf<kSplit, kPca, HB, 1>(p, st, Xp, M, g, n_cb, part);
 }
 
-// One call over n_mats matrices that share X (all of one contract).  Plan over the group's
-// total width; in the library's per-device workspace, stage the packed X (one pass over
-// X, with the first matrix's Zhl operand) and every other matrix's Zhl, followed by the
-// split-K partials; run the GEMM and, for a split plan, the fixed-order partial sums.
-template <bool kSplit>
-int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, int64_t K, int n_mats,
-                 const WeightSrc* ws_in, int32_t hdr_bytes, ZMode zm, const float* const* bases,
-                 const float* const* scales, const float* Z, const int64_t* Ns, int64_t n_cb,
-                 float* const* Ys, hipStream_t st, const float* silu_g = nullptr,
-                 const float* silu_u = nullptr) {
-    using namespace sx8;
-    int64_t Ntot = 0, NB = 0;
+// Workspace of one call, carved from the caller's buffer (256-byte aligned): every matrix's
+// Zhl operand (M * n_cb * 8 bytes each, 256-byte padded; absent for the core-only form),
+// the packed X (ceil(M / 32) * n_cb * 2 KB) and the split-K partials of the plan.
+struct WsLayout {
+    int64_t z_bytes;      // per matrix
+    int64_t xp_bytes;
+    int64_t part_bytes;
+    int64_t total;
+};
+
+WsLayout ws_layout(const Plan& p, int64_t M, int64_t Ntot, int64_t n_cb, int n_mats, bool with_z) {
+    WsLayout l;
+    l.z_bytes = with_z ? ((M * n_cb * 8 + 255) & ~int64_t(255)) : 0;
+    l.xp_bytes = ((M + 31) / 32 * n_cb * 2048 + 255) & ~int64_t(255);
+    l.part_bytes = p.w1 ? p.n_split * (p.St - 1) * kW1BM * kBN * 4 : (int64_t)(p.S - 1) * M * Ntot * 4;
+    l.total = l.z_bytes * n_mats + l.xp_bytes + l.part_bytes;
+    return l;
+}
+
+// Group width and column tiles; false if the group is too wide for 32-bit column indices.
+bool group_width(int n_mats, const int64_t* Ns, int64_t& Ntot, int64_t& NB) {
+    Ntot = NB = 0;
     for (int i = 0; i < n_mats; ++i) {
         Ntot += Ns[i];
         NB += (Ns[i] + kBN - 1) / kBN;
     }
-    if (Ntot > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "%s: group too wide", what);
+    return Ntot <= 0x7FFFFFFF;
+}
+
+// One call over n_mats matrices that share X (all of one contract).  Plan over the group's
+// total width; in the caller's workspace, stage the packed X (one pass over X, with every
+// matrix's Zhl operand) followed by the split-K partials; run the GEMM and, for a split
+// plan, the fixed-order partial sums.  Nothing is allocated and nothing synchronizes: the
+// call only enqueues kernels on `st`.
+template <bool kSplit>
+int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, int64_t K, int n_mats,
+                 const WeightSrc* ws_in, int32_t hdr_bytes, ZMode zm, const float* const* bases,
+                 const float* const* scales, const float* Z, const int64_t* Ns, int64_t n_cb,
+                 float* const* Ys, void* workspace, int64_t workspace_bytes, hipStream_t st,
+                 const float* silu_g = nullptr, const float* silu_u = nullptr) {
+    using namespace sx8;
+    int64_t Ntot = 0, NB = 0;
+    if (!group_width(n_mats, Ns, Ntot, NB)) return fail(SX8_ERR_UNSUPPORTED, "%s: group too wide", what);
     const Plan p = plan_gemm(M, Ntot, NB, n_cb);
     if (p.G > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "%s: grid too large", what);
-    const int64_t z_bytes = zm == ZMode::kNone ? 0 : ((M * n_cb * 8 + 255) & ~int64_t(255));
-    const int64_t xp_bytes = (M + 31) / 32 * n_cb * 2048;
-    const int64_t part_bytes = p.w1 ? p.n_split * (p.St - 1) * kW1BM * kBN * 4
-                                    : (int64_t)(p.S - 1) * M * Ntot * 4;
-    void* v = nullptr;
-    int32_t rc = device_workspace(z_bytes * n_mats + xp_bytes + part_bytes, &v);
-    if (rc != SX8_OK) return rc;
-    uint8_t* ws = reinterpret_cast<uint8_t*>(v);
+    const WsLayout lay = ws_layout(p, M, Ntot, n_cb, n_mats, zm != ZMode::kNone);
+    if (!workspace || workspace_bytes < lay.total || !aligned(workspace, 256))
+        return fail(SX8_ERR_INVALID,
+                    "%s: needs a 256-byte aligned workspace of %lld bytes "
+                    "(sx8_gemm_prefill_workspace_bytes), got %lld bytes at %p",
+                    what, (long long)lay.total, (long long)workspace_bytes, workspace);
+    uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+    const int64_t z_bytes = lay.z_bytes;
     uint16_t* Xp = reinterpret_cast<uint16_t*>(ws + z_bytes * n_mats);
-    float* part = reinterpret_cast<float*>(ws + z_bytes * n_mats + xp_bytes);
+    float* part = reinterpret_cast<float*>(ws + z_bytes * n_mats + lay.xp_bytes);
     GemmGroup g{};
     g.n_mats = n_mats;
     g.Ntot = Ntot;
@@ -1116,8 +1142,8 @@ int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, in
         hipLaunchKernelGGL(k_z_hl, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, Z, n,
                            reinterpret_cast<uint32_t*>(ws));
     }
-    rc = silu_g ? compute_z_silu(silu_g, silu_u, M, ldx, K, zs, n_cb, Xp, st)
-                : compute_z_sets(X, M, ldx, K, zs, n_cb, true, Xp, st);
+    int32_t rc = silu_g ? compute_z_silu(silu_g, silu_u, M, ldx, K, zs, n_cb, Xp, st)
+                        : compute_z_sets(X, M, ldx, K, zs, n_cb, true, Xp, st);
     if (rc != SX8_OK) return rc;
     if constexpr (kSplit) {
         launch_hb<true, true, 6>(p, st, Xp, M, g, n_cb, part);
@@ -1152,10 +1178,41 @@ int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, in
 
 }  // namespace
 
+extern "C" int64_t sx8_gemm_prefill_workspace_bytes(int64_t M, int32_t n_mats, const int64_t* Ns,
+                                                    int64_t n_cb) {
+    if (M <= 0 || n_cb <= 0 || !Ns || n_mats < 1 || n_mats > kMaxGemmGroup || M > 0x7FFFFFFF) return -1;
+    for (int i = 0; i < n_mats; ++i)
+        if (Ns[i] <= 0) return -1;
+    int64_t Ntot = 0, NB = 0;
+    if (!group_width(n_mats, Ns, Ntot, NB)) return -1;
+    const Plan p = plan_gemm(M, Ntot, NB, n_cb);
+    return ws_layout(p, M, Ntot, n_cb, n_mats, true).total;
+}
+
+extern "C" int32_t sx8_gemm_prefill_plan(int64_t M, int32_t n_mats, const int64_t* Ns, int64_t n_cb,
+                                         int64_t* desc) {
+    using namespace sx8;
+    if (!desc || sx8_gemm_prefill_workspace_bytes(M, n_mats, Ns, n_cb) < 0)
+        return fail(SX8_ERR_INVALID, "sx8_gemm_prefill_plan: bad shape");
+    int64_t Ntot = 0, NB = 0;
+    group_width(n_mats, Ns, Ntot, NB);
+    const Plan p = plan_gemm(M, Ntot, NB, n_cb);
+    desc[0] = p.w1 ? kW1BM : 128 * p.MF;
+    desc[1] = p.G;
+    desc[2] = p.w1 ? p.St : p.S;
+    desc[3] = p.w1 ? p.kbs : p.kb_per_split;
+    desc[4] = p.w1 ? p.Tf : 0;
+    desc[5] = p.w1 ? p.n_split : 0;
+    desc[6] = ws_layout(p, M, Ntot, n_cb, n_mats, true).total;
+    desc[7] = 0;
+    return ok();
+}
+
 extern "C" int32_t sx8_gemm_prefill(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
                                     const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
                                     const float* basis, const float* scales, int64_t N,
-                                    int64_t n_cb, float* Y, void* stream) {
+                                    int64_t n_cb, float* Y, void* workspace, int64_t workspace_bytes,
+                                    void* stream) {
     using namespace sx8;
     if (!X || !hdr || !levels || !basis || !scales || !Y)
         return fail(SX8_ERR_INVALID, "sx8_gemm_prefill: null pointer");
@@ -1170,13 +1227,13 @@ extern "C" int32_t sx8_gemm_prefill(const uint16_t* X, int64_t M, int64_t ldx, i
     w.hdr = hdr;
     w.levels = levels;
     return run_gemm<false>("sx8_gemm_prefill", X, M, ldx, K, 1, &w, hdr_bytes, ZMode::kBasis, &basis,
-                           &scales, nullptr, &N, n_cb, &Y, as_stream(stream));
+                           &scales, nullptr, &N, n_cb, &Y, workspace, workspace_bytes, as_stream(stream));
 }
 
 extern "C" int32_t sx8_dec_gemm_silu(const float* g, const float* u, int64_t M, int64_t K,
                                      const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
                                      const float* basis, const float* scales, int64_t N, int64_t n_cb,
-                                     float* Y, void* stream) {
+                                     float* Y, void* workspace, int64_t workspace_bytes, void* stream) {
     using namespace sx8;
     if (!g || !u || !hdr || !levels || !basis || !scales || !Y)
         return fail(SX8_ERR_INVALID, "sx8_dec_gemm_silu: null pointer");
@@ -1191,7 +1248,7 @@ extern "C" int32_t sx8_dec_gemm_silu(const float* g, const float* u, int64_t M, 
     w.hdr = hdr;
     w.levels = levels;
     return run_gemm<false>("sx8_dec_gemm_silu", nullptr, M, K, K, 1, &w, hdr_bytes, ZMode::kBasis, &basis,
-                           &scales, nullptr, &N, n_cb, &Y, as_stream(stream), g, u);
+                           &scales, nullptr, &N, n_cb, &Y, workspace, workspace_bytes, as_stream(stream), g, u);
 }
 
 extern "C" int32_t sx8_gemm_prefill_split(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
@@ -1199,7 +1256,7 @@ extern "C" int32_t sx8_gemm_prefill_split(const uint16_t* X, int64_t M, int64_t 
                                           const uint8_t* config, const uint8_t* coeff,
                                           const uint8_t* hi, const uint8_t* lo, const float* basis,
                                           const float* scales, int64_t N, int64_t n_cb, float* Y,
-                                          void* stream) {
+                                          void* workspace, int64_t workspace_bytes, void* stream) {
     using namespace sx8;
     if (!X || !dmin || !dmax || !config || !coeff || !hi || !lo || !basis || !scales || !Y)
         return fail(SX8_ERR_INVALID, "sx8_gemm_prefill_split: null pointer");
@@ -1216,13 +1273,13 @@ extern "C" int32_t sx8_gemm_prefill_split(const uint16_t* X, int64_t M, int64_t 
     w.hi = hi;
     w.lo = lo;
     return run_gemm<true>("sx8_gemm_prefill_split", X, M, ldx, K, 1, &w, 6, ZMode::kBasis, &basis,
-                          &scales, nullptr, &N, n_cb, &Y, as_stream(stream));
+                          &scales, nullptr, &N, n_cb, &Y, workspace, workspace_bytes, as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemm_prefill_z(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
                                       const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
                                       const float* Z, int64_t N, int64_t n_cb, float* Y,
-                                      void* stream) {
+                                      void* workspace, int64_t workspace_bytes, void* stream) {
     using namespace sx8;
     if (!X || !hdr || !levels || !Z || !Y)
         return fail(SX8_ERR_INVALID, "sx8_gemm_prefill_z: null pointer");
@@ -1237,13 +1294,13 @@ extern "C" int32_t sx8_gemm_prefill_z(const uint16_t* X, int64_t M, int64_t ldx,
     w.hdr = hdr;
     w.levels = levels;
     return run_gemm<false>("sx8_gemm_prefill_z", X, M, ldx, K, 1, &w, hdr_bytes, ZMode::kGiven, nullptr,
-                           nullptr, Z, &N, n_cb, &Y, as_stream(stream));
+                           nullptr, Z, &N, n_cb, &Y, workspace, workspace_bytes, as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemm_prefill_core(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
                                          const uint8_t* hdr, const uint8_t* levels,
                                          int32_t hdr_bytes, int64_t N, int64_t n_cb, float* Y,
-                                         void* stream) {
+                                         void* workspace, int64_t workspace_bytes, void* stream) {
     using namespace sx8;
     if (!X || !hdr || !levels || !Y) return fail(SX8_ERR_INVALID, "sx8_gemm_prefill_core: null pointer");
     if (hdr_bytes != 6 && hdr_bytes != 8)
@@ -1257,7 +1314,8 @@ extern "C" int32_t sx8_gemm_prefill_core(const uint16_t* X, int64_t M, int64_t l
     w.hdr = hdr;
     w.levels = levels;
     return run_gemm<false>("sx8_gemm_prefill_core", X, M, ldx, K, 1, &w, hdr_bytes, ZMode::kNone,
-                           nullptr, nullptr, nullptr, &N, n_cb, &Y, as_stream(stream));
+                           nullptr, nullptr, nullptr, &N, n_cb, &Y, workspace, workspace_bytes,
+                           as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemm_prefill_group(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
@@ -1265,7 +1323,7 @@ extern "C" int32_t sx8_gemm_prefill_group(const uint16_t* X, int64_t M, int64_t 
                                           const uint8_t* const* levels, int32_t hdr_bytes,
                                           const float* const* bases, const float* const* scales,
                                           const int64_t* Ns, int64_t n_cb, float* const* Ys,
-                                          void* stream) {
+                                          void* workspace, int64_t workspace_bytes, void* stream) {
     using namespace sx8;
     const char* what = "sx8_gemm_prefill_group";
     if (!X || !hdrs || !levels || !bases || !scales || !Ns || !Ys) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
@@ -1287,7 +1345,7 @@ extern "C" int32_t sx8_gemm_prefill_group(const uint16_t* X, int64_t M, int64_t 
         w[i].levels = levels[i];
     }
     return run_gemm<false>(what, X, M, ldx, K, n_mats, w, hdr_bytes, ZMode::kBasis, bases, scales, nullptr,
-                           Ns, n_cb, Ys, as_stream(stream));
+                           Ns, n_cb, Ys, workspace, workspace_bytes, as_stream(stream));
 }
 
 extern "C" int32_t sx8_gemm_pca_z(const float* Z, int64_t M, const uint8_t* hdr, int32_t hdr_bytes,

@@ -972,18 +972,18 @@ extern "C" int32_t sx8_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t
         (basis && !aligned(basis, 4)) || (scales && !aligned(scales, 4)) ||
         (Z_in && !aligned(Z_in, 4)) || (Z_out && !aligned(Z_out, 4)) || !aligned(Y, 4))
         return fail(SX8_ERR_INVALID, "sx8_gemv: misaligned pointer (X needs 16-byte alignment)");
+    // the single-launch form builds its table in LDS; the Z-returning form and K beyond the
+    // LDS table run k_kbinfo first and need the caller's workspace for its table
     const int64_t need = sx8_gemv_workspace_bytes(n_cb);
+    const bool needs_ws = Z_out != nullptr || n_cb > kLdsMaxKb;
     KbInfo* table = reinterpret_cast<KbInfo*>(workspace);
-    if (table) {
-        if (workspace_bytes < need || !aligned(table, 16))
-            return fail(SX8_ERR_INVALID, "sx8_gemv: workspace needs %lld bytes, 16-byte aligned",
-                        (long long)need);
-    } else {
-        void* ws = nullptr;
-        const int32_t rc = device_workspace(need, &ws);
-        if (rc != SX8_OK) return rc;
-        table = reinterpret_cast<KbInfo*>(ws);
-    }
+    if (table && (workspace_bytes < need || !aligned(table, 16)))
+        return fail(SX8_ERR_INVALID, "sx8_gemv: workspace needs %lld bytes, 16-byte aligned",
+                    (long long)need);
+    if (!table && needs_ws)
+        return fail(SX8_ERR_INVALID,
+                    "sx8_gemv: this call (Z_out given or n_cb > %d) needs a workspace of %lld bytes",
+                    kLdsMaxKb, (long long)need);
     if (hdr_bytes == 8)
         return launch_gemv<8>(X, hdr, levels, basis, scales, Z_in, Z_out, (int)N, (int)n_cb, Y,
                               table, as_stream(stream));
@@ -995,7 +995,8 @@ extern "C" int32_t sx8_gemv_group(const uint16_t* X, int32_t n_mats, const uint8
                                   const uint8_t* const* levels, int32_t hdr_bytes,
                                   const float* const* bases, const float* const* scales,
                                   const float* const* Z_in, const int64_t* Ns, int64_t n_cb,
-                                  float* const* Ys, void* stream) {
+                                  float* const* Ys, void* workspace, int64_t workspace_bytes,
+                                  void* stream) {
     using namespace sx8;
     if (!X || !hdrs || !levels || !Ns || !Ys) return fail(SX8_ERR_INVALID, "sx8_gemv_group: null pointer");
     if (n_mats < 1 || n_mats > kMaxGroup)
@@ -1020,9 +1021,11 @@ extern "C" int32_t sx8_gemv_group(const uint16_t* X, int32_t n_mats, const uint8
     }
     const hipStream_t st = as_stream(stream);
     if (n_cb > kLdsMaxKb) {   // table past LDS: one two-launch GEMV per matrix
-        void* ws = nullptr;
-        const int32_t rc = device_workspace(sx8_gemv_workspace_bytes(n_cb), &ws);
-        if (rc != SX8_OK) return rc;
+        void* ws = workspace;
+        if (!ws || workspace_bytes < sx8_gemv_workspace_bytes(n_cb) || !aligned(ws, 16))
+            return fail(SX8_ERR_INVALID,
+                        "sx8_gemv_group: n_cb > %d needs a 16-byte aligned workspace of %lld bytes",
+                        kLdsMaxKb, (long long)sx8_gemv_workspace_bytes(n_cb));
         for (int i = 0; i < n_mats; ++i) {
             const float* b = Z_in ? nullptr : bases[i];
             const float* sc = Z_in ? nullptr : scales[i];

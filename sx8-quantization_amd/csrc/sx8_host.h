@@ -1,5 +1,5 @@
 // sx8_host.h -- host-side helpers shared by the C-ABI entry points: error reporting,
-// argument checks and the per-device workspace used by the split-K GEMV.
+// argument checks and the Z / packed-X pass shared by the GEMV and the prefill GEMM.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -22,13 +22,6 @@ inline bool aligned(const void* p, uintptr_t a) {
 }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
-
-// Library-owned device scratch of at least `bytes` (256-byte aligned) for callers
-// that pass no workspace: grow-only, one buffer per device, allocated with hipMalloc
-// on first need and kept until the process ends.  Calls that overlap on one device
-// (several streams) must pass their own workspaces instead.  Returns SX8_OK or
-// SX8_ERR_HIP.
-int32_t device_workspace(int64_t bytes, void** ptr);
 
 // Z[m, kb, j] = scales[kb, j] * sum_t X[m, kb*32+t] * basis[kb, 32j+t] (reference tree
 // order), reading only columns k < K of X (the rest count as zero).  hl = false: Z as f32

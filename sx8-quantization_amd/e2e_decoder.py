@@ -175,34 +175,49 @@ class SX8Decoder(nn.Module):
               "logits": torch.empty(cfg["vocab"], **f32), "tok": torch.zeros(1, dtype=torch.int64, device=dev),
               "scratch_pos": torch.zeros(1, dtype=torch.int64, device=dev)}
         pb["head_group"] = self._group_args((self.head,), (pb["logits"],))
+        # one prefill workspace for every GEMM of the pass (the calls run in stream order),
+        # sized for the largest of them
+        ly0 = self.layers[0]
+        need = max(int(_L.lib().sx8_gemm_prefill_workspace_bytes(T, len(Ns), (ctypes.c_int64 * len(Ns))(*Ns),
+                                                                 n_cb))
+                   for Ns, n_cb in (((ly0.q.out_f, ly0.k.out_f, ly0.v.out_f), ly0.q.qt["n_cb"]),
+                                    ((ly0.o.out_f,), ly0.o.qt["n_cb"]),
+                                    ((ly0.gate.out_f, ly0.up.out_f), ly0.gate.qt["n_cb"]),
+                                    ((ly0.down.out_f,), ly0.down.qt["n_cb"])))
+        pb["ws"] = torch.empty(need, dtype=torch.uint8, device=dev)
         pb["groups"] = [(self._group_args((ly.q, ly.k, ly.v), (pb["q"], pb["k"], pb["v"])),
                          self._group_args((ly.gate, ly.up), (pb["g"], pb["u"]))) for ly in self.layers]
         self._pb = pb
         return pb
 
     @staticmethod
-    def _gemm_group(args, X, st):
+    def _gemm_group(args, X, ws, st):
         """The prefill GEMMs of matrices sharing X (sx8_gemm_prefill_group), outputs (M, N_i)."""
         n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
         M, K = X.shape
-        _L.call("sx8_gemm_prefill_group", _L.ptr(X), M, K, K, n, hdrs, lvls, 6, bas, sca, ns, n_cb, ys, st)
+        _L.call("sx8_gemm_prefill_group", _L.ptr(X), M, K, K, n, hdrs, lvls, 6, bas, sca, ns, n_cb, ys,
+                _L.ptr(ws), ws.numel(), st)
 
     @staticmethod
-    def _gemm(lin, X, Y, st):
+    def _gemm(lin, X, Y, ws, st):
         """Y (M, N) f32 = X (M, K) fp16 . W^T through sx8_gemm_prefill."""
         hdr, lvl, bas, sca = lin._t44
         M, K = X.shape
         _L.call("sx8_gemm_prefill", _L.ptr(X), M, K, K, _L.ptr(hdr), _L.ptr(lvl), 6, _L.ptr(bas),
-                _L.ptr(sca), lin.out_f, lin.qt["n_cb"], _L.ptr(Y), st)
+                _L.ptr(sca), lin.out_f, lin.qt["n_cb"], _L.ptr(Y), _L.ptr(ws), ws.numel(), st)
 
     @torch.no_grad()
-    def prefill_fused(self, ids):
+    def prefill_fused(self, ids, all_logits=False):
         """prefill() with the library ops over the T prompt rows: add + RMSNorm
         (sx8_dec_add_rmsnorm, M = T), the prefill GEMMs into preallocated buffers, q/k
         norm + RoPE + KV-cache write (sx8_dec_qk_rope_cache_rows), causal attention over
         the cache rows (sx8_dec_attn_prefill), SiLU * up inside the down GEMM
         (sx8_dec_gemm_silu) and the final norm inside the lm_head GEMV.  The residual
-        stream is float32."""
+        stream is float32.  Returns the next token (1,); generation only needs the last
+        row's logits, so that is all the lm_head computes.  all_logits=True instead runs
+        the final norm over every row and the lm_head as a prefill GEMM (M = T), as a
+        Hugging Face forward does (scripts/integrate_fused_v44.py:119-167 compares those
+        logits), and returns the (T, vocab) float32 logits."""
         cfg = self.cfg
         H, nh, nk, hd, eps = cfg["hidden"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["eps"]
         T = ids.shape[0]
@@ -217,19 +232,27 @@ class SX8Decoder(nn.Module):
             else:
                 _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["d"]), None, P(ly.in_norm), P(pb["h"]), T,
                         H, eps, st)
-            self._gemm_group(pb["groups"][li][0], pb["h"], st)      # q, k, v: one call
+            self._gemm_group(pb["groups"][li][0], pb["h"], pb["ws"], st)      # q, k, v: one call
             _L.call("sx8_dec_qk_rope_cache_rows", P(pb["q"]), P(pb["k"]), P(pb["v"]), P(ly.q_norm),
                     P(ly.k_norm), P(self.cos), P(self.sin), P(pb["pos0"]), T, P(pb["qh"]),
                     P(self.k_cache[li]), P(self.v_cache[li]), nh, nk, hd, self.max_len, eps, st)
             _L.call("sx8_dec_attn_prefill", P(pb["qh"]), P(self.k_cache[li]), P(self.v_cache[li]), P(pb["a"]),
                     T, 0, nh, nk, hd, self.max_len, 1.0 / math.sqrt(hd), st)
-            self._gemm(ly.o, pb["a"], pb["o"], st)
+            self._gemm(ly.o, pb["a"], pb["o"], pb["ws"], st)
             _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["o"]), None, P(ly.post_norm), P(pb["h"]), T,
                     H, eps, st)
-            self._gemm_group(pb["groups"][li][1], pb["h"], st)      # gate, up: one call
+            self._gemm_group(pb["groups"][li][1], pb["h"], pb["ws"], st)      # gate, up: one call
             hdr, lvl, bas, sca = ly.down._t44                       # SiLU * up inside the down GEMM
             _L.call("sx8_dec_gemm_silu", P(pb["g"]), P(pb["u"]), T, cfg["inter"], P(hdr), P(lvl), 6, P(bas),
-                    P(sca), ly.down.out_f, ly.down.qt["n_cb"], P(pb["d"]), st)
+                    P(sca), ly.down.out_f, ly.down.qt["n_cb"], P(pb["d"]), P(pb["ws"]), pb["ws"].numel(), st)
+        if all_logits:
+            # every row: residual + down output, final norm, lm_head GEMM over T rows
+            _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["d"]), None, P(self.final_norm), P(pb["h"]),
+                    T, H, eps, st)
+            logits = torch.empty(T, cfg["vocab"], dtype=torch.float32, device=self.device)
+            ws, nb = _L.gemm_workspace(T, (cfg["vocab"],), self.head.qt["n_cb"], self.device)
+            self._gemm(self.head, pb["h"], logits, ws, st)
+            return logits
         # last row: residual + down output, final norm and lm_head in one launch
         self._gemv_rms(pb["head_group"], pb["resid"][T - 1], None, pb["d"][T - 1], self.final_norm, None,
                        eps, st)
@@ -311,7 +334,7 @@ class SX8Decoder(nn.Module):
     @staticmethod
     def _gemv_group(args, x, st):
         n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
-        _L.call("sx8_gemv_group", _L.ptr(x), n, hdrs, lvls, 6, bas, sca, None, ns, n_cb, ys, st)
+        _L.call("sx8_gemv_group", _L.ptr(x), n, hdrs, lvls, 6, bas, sca, None, ns, n_cb, ys, None, 0, st)
 
     @staticmethod
     def _gemv_rms(args, resid, init, delta, w, resid_out, eps, st):

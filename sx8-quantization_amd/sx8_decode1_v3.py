@@ -19,6 +19,9 @@ import torch
 import _sx8lib as _L
 
 DEV = torch.device("cuda")
+# K blocks up to which sx8_gemv builds its activation table in LDS (single launch, no
+# workspace); beyond it the table goes through the caller's workspace
+_LDS_MAX_KB = 640
 
 
 def _x_for_kernel(X, n_cb):
@@ -34,15 +37,10 @@ def _x_for_kernel(X, n_cb):
 
 
 def _workspace(n_cb, device):
-    """Pooled per-device table workspace of sx8_gemv (112 bytes per K block).  Taken
-    from torch's allocator, so it is stream-ordered and capture-safe."""
+    """Table workspace of sx8_gemv's two-launch forms (112 bytes per K block), fresh from
+    torch's caching allocator on the current stream: stream-ordered and capture-safe."""
     n = (int(_L.lib().sx8_gemv_workspace_bytes(n_cb)) + 3) // 4
-    key = ("WS", torch.device(device).index)
-    b = _BUF.get(key)
-    if b is None or b.numel() < n:
-        b = torch.empty(max(n, 4096), dtype=torch.float32, device=device)
-        _BUF[key] = b
-    return b
+    return torch.empty(max(n, 4), dtype=torch.float32, device=device)
 
 
 class _Ext:
@@ -142,9 +140,9 @@ def decode1_v44(X, qt, bases_info, hdr_t=None, lvl_t=None, bas_t=None, sca_t=Non
     # afterwards, so the Z output is skipped here, which lets the HIP GEMV build its
     # activation table inside the single launch.
     Xc = _x_for_kernel(X, n_cb)
-    ws = _workspace(n_cb, Xc.device)
+    ws = _workspace(n_cb, Xc.device) if n_cb > _LDS_MAX_KB else None
     _L.call("sx8_gemv", _L.ptr(Xc), _L.ptr(hdr_t), _L.ptr(lvl_t), int(hdr_bytes), _L.ptr(bas_t),
-            _L.ptr(sca_t), None, None, N, n_cb, _L.ptr(Y), _L.ptr(ws), ws.numel() * 4,
+            _L.ptr(sca_t), None, None, N, n_cb, _L.ptr(Y), _L.ptr(ws), 0 if ws is None else ws.numel() * 4,
             _L.stream(Xc.device))
     return Y, (hdr_t, lvl_t, bas_t, sca_t)
 
@@ -166,6 +164,7 @@ def decode1_v44_group(X, tensors, Ns, n_cb, hdr_bytes=6, outs=None):
     sca = P(*[k[1].data_ptr() for k in keep])
     ys = P(*[y.data_ptr() for y in outs])
     ns = (ctypes.c_int64 * n)(*[int(N) for N in Ns])
+    ws = _workspace(int(n_cb), Xc.device) if int(n_cb) > _LDS_MAX_KB else None
     _L.call("sx8_gemv_group", _L.ptr(Xc), n, hdrs, lvls, int(hdr_bytes), bas, sca, None, ns,
-            int(n_cb), ys, _L.stream(Xc.device))
+            int(n_cb), ys, _L.ptr(ws), 0 if ws is None else ws.numel() * 4, _L.stream(Xc.device))
     return outs

@@ -6,9 +6,12 @@ Interface of scripts/sx8_fused_wmma.py (reference): ``_get_module()`` (an object
 which builds the kb-major dict these functions consume.
 
 The kernel behind it is the same MFMA prefill as gemm_sx8_compact (sx8_gemm_prefill_
-split): R64 per-weight decode into v_mfma_f32_16x16x32_f16 operands.  ``make_tensors``
-no longer builds the rlo/step fp16 tables of precompute_rlo_step.py: no kernel here
-reads them.
+split): the PCA-free core weights rlo + step*lv decoded in float32 (the reference's R32
+form), rounded to fp16 into v_mfma_f32_32x32x16_f16 operands, PCA added through Z as
+extra k-steps.  Like the reference's WMMA tiles (cuda/sx8_fused_wmma.cu:70-97) these
+operands are not the canonical R64 weights; the product meets the 1e-3 bar.
+``make_tensors`` no longer builds the rlo/step fp16 tables of precompute_rlo_step.py: no
+kernel here reads them.
 """
 from __future__ import annotations
 
@@ -49,9 +52,10 @@ class _Module:
         M, K = Xc.shape
         N = dmin.numel() // n_cb
         Y = torch.empty((M, N), dtype=torch.float32, device=Xc.device)
+        ws, nb = _L.gemm_workspace(M, (N,), n_cb, Xc.device)
         _L.call("sx8_gemm_prefill_split", _L.ptr(Xc), M, K, min(K, n_cb * 32),
                 _L.ptr(dmin), _L.ptr(dmax), _L.ptr(config), _L.ptr(coeff), _L.ptr(hi),
-                _L.ptr(lo), _L.ptr(basis), _L.ptr(scales), N, n_cb, _L.ptr(Y),
+                _L.ptr(lo), _L.ptr(basis), _L.ptr(scales), N, n_cb, _L.ptr(Y), _L.ptr(ws), nb,
                 _L.stream(Xc.device))
         return Y
 

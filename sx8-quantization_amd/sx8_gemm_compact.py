@@ -4,9 +4,12 @@ Interface of scripts/sx8_gemm_compact.py (reference): ``_ext()`` (an object with
 ``compute_z44_batch`` and ``gemm_compact``) and ``gemm_sx8_compact``.
 
 ``gemm_sx8_compact`` runs sx8_gemm_prefill: Z is computed inside the call, the core
-weights (rlo + step*lv) are decoded in float32 straight into MFMA operands and the PCA
-term rides along as extra MFMA k-steps over Z.  ``_ext().gemm_compact`` keeps the
-reference's caller-supplied-Z contract with the same kernel (sx8_gemm_prefill_z).
+weights (rlo + step*lv) are decoded in float32, rounded to fp16 and fed to
+v_mfma_f32_32x32x16_f16, and the PCA term rides along as extra MFMA k-steps over Z.
+``_ext().gemm_compact`` keeps the reference's caller-supplied-Z contract with the same
+kernel (sx8_gemm_prefill_z).  The library allocates nothing: each call takes its
+workspace (Z, packed X, split-K partials) from torch's caching allocator on the current
+stream, the way the reference's wrappers allocate their outputs.
 """
 from __future__ import annotations
 
@@ -53,8 +56,9 @@ class _Ext:
         Zc = Z.contiguous().float()
         if Zc.numel() != M * n_cb * 2:
             raise ValueError(f"Z must hold (M, n_cb, 2) = ({M}, {n_cb}, 2) values")
+        ws, nb = _L.gemm_workspace(M, (N,), n_cb, Xc.device)
         _L.call("sx8_gemm_prefill_z", _L.ptr(Xc), M, K, Kc, _L.ptr(hdr), _L.ptr(levels),
-                int(hdr_bytes), _L.ptr(Zc), N, n_cb, _L.ptr(Y), _L.stream(Xc.device))
+                int(hdr_bytes), _L.ptr(Zc), N, n_cb, _L.ptr(Y), _L.ptr(ws), nb, _L.stream(Xc.device))
         return Y
 
 
@@ -94,7 +98,8 @@ def gemm_sx8_compact(X, qt, bases_info, hdr_t=None, lvl_t=None, bas_t=None, sca_
     if K < in_f:
         raise ValueError(f"X has {K} columns, weight needs {in_f}")
     Y = torch.empty((M, out_f), dtype=torch.float32, device=Xc.device)
+    ws, nb = _L.gemm_workspace(M, (out_f,), int(n_cb), Xc.device)
     _L.call("sx8_gemm_prefill", _L.ptr(Xc), M, K, int(in_f), _L.ptr(hdr_t), _L.ptr(lvl_t),
-            int(hdr_bytes), _L.ptr(bas_t), _L.ptr(sca_t), out_f, int(n_cb), _L.ptr(Y),
+            int(hdr_bytes), _L.ptr(bas_t), _L.ptr(sca_t), out_f, int(n_cb), _L.ptr(Y), _L.ptr(ws), nb,
             _L.stream(Xc.device))
     return Y

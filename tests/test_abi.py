@@ -56,13 +56,13 @@ def test_invalid_arguments_rejected_on_host(hiplib):
     # inconsistent K / n_cb
     assert L.sx8_dequant_f16(p, p, p, p, p, p, p, p, 4, 100, 2, p, NULL) == 1
     assert "bad shape" in _err(L)
-    assert L.sx8_gemm_prefill(p, 4, 64, 64, p, p, 6, p, p, 0, 2, p, NULL) == 1
-    assert L.sx8_gemm_prefill(p, 4, 32, 64, p, p, 6, p, p, 64, 2, p, NULL) == 1   # ldx < K
+    assert L.sx8_gemm_prefill(p, 4, 64, 64, p, p, 6, p, p, 0, 2, p, p, 1 << 20, NULL) == 1
+    assert L.sx8_gemm_prefill(p, 4, 32, 64, p, p, 6, p, p, 64, 2, p, p, 1 << 20, NULL) == 1   # ldx < K
     assert L.sx8_embed_gather(p, 4, p, p, 5, p, p, 64, 10, 2, p, NULL) == 1
     assert L.sx8_compute_z(p, 1, 16, p, p, 1, p, NULL) == 1                      # ldx < 32
     assert L.sx8_gemm_pca_z(NULL, 1, p, 6, 64, 2, p, NULL) == 1
-    assert L.sx8_gemm_prefill_z(p, 4, 64, 64, p, p, 6, NULL, 64, 2, p, NULL) == 1   # Z missing
-    assert L.sx8_gemm_prefill_z(p, 4, 64, 64, p, p, 6, p, 64, 3, p, NULL) == 1      # n_cb != K/32
+    assert L.sx8_gemm_prefill_z(p, 4, 64, 64, p, p, 6, NULL, 64, 2, p, p, 1 << 20, NULL) == 1   # Z missing
+    assert L.sx8_gemm_prefill_z(p, 4, 64, 64, p, p, 6, p, 64, 3, p, p, 1 << 20, NULL) == 1      # n_cb != K/32
 
 
 def test_gemv_group_rejects_bad_arguments(hiplib):
@@ -72,18 +72,49 @@ def test_gemv_group_rejects_bad_arguments(hiplib):
     ptrs = P2(4096, 8192)
     ns = (ctypes.c_int64 * 2)(64, 32)
     # n_mats out of range, hdr_bytes, null bases without Z, misaligned X
-    assert L.sx8_gemv_group(p, 0, ptrs, ptrs, 6, ptrs, ptrs, NULL, ns, 2, ptrs, NULL) == 1
+    assert L.sx8_gemv_group(p, 0, ptrs, ptrs, 6, ptrs, ptrs, NULL, ns, 2, ptrs, NULL, 0, NULL) == 1
     assert "n_mats" in _err(L)
-    assert L.sx8_gemv_group(p, 5, ptrs, ptrs, 6, ptrs, ptrs, NULL, ns, 2, ptrs, NULL) == 1
-    assert L.sx8_gemv_group(p, 2, ptrs, ptrs, 7, ptrs, ptrs, NULL, ns, 2, ptrs, NULL) == 1
+    assert L.sx8_gemv_group(p, 5, ptrs, ptrs, 6, ptrs, ptrs, NULL, ns, 2, ptrs, NULL, 0, NULL) == 1
+    assert L.sx8_gemv_group(p, 2, ptrs, ptrs, 7, ptrs, ptrs, NULL, ns, 2, ptrs, NULL, 0, NULL) == 1
     assert "hdr_bytes" in _err(L)
-    assert L.sx8_gemv_group(p, 2, ptrs, ptrs, 6, NULL, NULL, NULL, ns, 2, ptrs, NULL) == 1
+    assert L.sx8_gemv_group(p, 2, ptrs, ptrs, 6, NULL, NULL, NULL, ns, 2, ptrs, NULL, 0, NULL) == 1
     assert "bases" in _err(L)
     assert L.sx8_gemv_group(ctypes.c_void_p(4098), 2, ptrs, ptrs, 6, ptrs, ptrs, NULL, ns, 2,
-                            ptrs, NULL) == 1
+                            ptrs, NULL, 0, NULL) == 1
     bad_n = (ctypes.c_int64 * 2)(64, 0)
-    assert L.sx8_gemv_group(p, 2, ptrs, ptrs, 6, ptrs, ptrs, NULL, bad_n, 2, ptrs, NULL) == 1
+    assert L.sx8_gemv_group(p, 2, ptrs, ptrs, 6, ptrs, ptrs, NULL, bad_n, 2, ptrs, NULL, 0, NULL) == 1
     assert "bad N" in _err(L)
+    # K beyond the LDS table (n_cb > 640) without the workspace it then needs
+    assert L.sx8_gemv_group(p, 2, ptrs, ptrs, 6, ptrs, ptrs, NULL, ns, 641, ptrs, NULL, 0, NULL) == 1
+    assert "workspace" in _err(L)
+
+
+def test_workspace_contract(hiplib):
+    """The library allocates nothing: prefill calls need a caller workspace of the size the
+    query gives (256-byte aligned), and the GEMV's two-launch forms need theirs; a missing
+    or short workspace is refused on the host."""
+    L = hiplib
+    p = ctypes.c_void_p(4096)
+    N = (ctypes.c_int64 * 1)(4096)
+    nb = L.sx8_gemm_prefill_workspace_bytes(2048, 1, N, 80)
+    # Zhl (M * n_cb * 8) + packed X (M * n_cb * 64) at least
+    assert nb >= 2048 * 80 * 72
+    assert L.sx8_gemm_prefill_workspace_bytes(0, 1, N, 80) == -1
+    assert L.sx8_gemm_prefill_workspace_bytes(16, 5, N, 80) == -1
+    desc = (ctypes.c_int64 * 8)()
+    assert L.sx8_gemm_prefill_plan(2048, 1, N, 80, desc) == 0
+    assert desc[0] in (128, 256, 512) and desc[1] > 0 and desc[6] == nb
+    # K = 2560 -> n_cb = 80; no workspace, a short one, a misaligned one
+    assert L.sx8_gemm_prefill(p, 2048, 2560, 2560, p, p, 6, p, p, 4096, 80, p, NULL, 0, NULL) == 1
+    assert "workspace" in _err(L)
+    assert L.sx8_gemm_prefill(p, 2048, 2560, 2560, p, p, 6, p, p, 4096, 80, p, p, nb - 1, NULL) == 1
+    assert "workspace" in _err(L)
+    assert L.sx8_gemm_prefill(p, 2048, 2560, 2560, p, p, 6, p, p, 4096, 80, p, ctypes.c_void_p(4096 + 16),
+                              nb, NULL) == 1
+    assert "workspace" in _err(L)
+    # GEMV: the Z-returning form needs the table workspace
+    assert L.sx8_gemv(p, p, p, 6, p, p, NULL, p, 64, 2, p, NULL, 0, NULL) == 1
+    assert "workspace" in _err(L)
 
 
 def test_product_modules_import():

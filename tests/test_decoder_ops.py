@@ -188,7 +188,7 @@ def test_fused_gemv_rmsnorm(hiplib, cuda):
                 P(init) if use_init else None, P(w), P(h16), 1, K, eps, st)
         y_ref = [torch.empty(N, device=cuda) for N in Ns]
         n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y_ref)
-        _L.call("sx8_gemv_group", P(h16), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, st)
+        _L.call("sx8_gemv_group", P(h16), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, None, 0, st)
         # fused
         r_out = torch.full((K,), float("nan"), device=cuda)
         y = [torch.empty(N, device=cuda) for N in Ns]
@@ -222,7 +222,7 @@ def test_fused_gemv_silu(hiplib, cuda):
     _L.call("sx8_dec_silu_mul", P(a), P(b), P(m), K, st)
     y_ref = [torch.empty(N, device=cuda) for N in Ns]
     n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y_ref)
-    _L.call("sx8_gemv_group", P(m), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, st)
+    _L.call("sx8_gemv_group", P(m), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, None, 0, st)
     y = [torch.empty(N, device=cuda) for N in Ns]
     n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y)
     _L.call("sx8_dec_gemv_silu", P(a), P(b), n, hd, lv, 6, bs, sc, ns, n_cb, ys, st)
@@ -249,10 +249,13 @@ def test_gemm_silu_matches_two_calls(hiplib, cuda, M, K, N):
     m = torch.empty(M, K, dtype=torch.float16, device=cuda)
     _L.call("sx8_dec_silu_mul", P(a), P(b), P(m), M * K, st)
     y_ref = torch.empty(M, N, device=cuda)
-    _L.call("sx8_gemm_prefill", P(m), M, K, K, P(hdr), P(lvl), 6, P(bas), P(sca), N, n_cb, P(y_ref), st)
+    ws, nb = _L.gemm_workspace(M, (N,), n_cb, cuda)
+    _L.call("sx8_gemm_prefill", P(m), M, K, K, P(hdr), P(lvl), 6, P(bas), P(sca), N, n_cb, P(y_ref), P(ws), nb,
+            st)
     y = torch.empty(M, N, device=cuda)
     print("gemm_silu", M, K, N, flush=True)
-    _L.call("sx8_dec_gemm_silu", P(a), P(b), M, K, P(hdr), P(lvl), 6, P(bas), P(sca), N, n_cb, P(y), st)
+    _L.call("sx8_dec_gemm_silu", P(a), P(b), M, K, P(hdr), P(lvl), 6, P(bas), P(sca), N, n_cb, P(y), P(ws), nb,
+            st)
     torch.cuda.synchronize()
     assert torch.equal(y.cpu(), y_ref.cpu())
 

@@ -9,9 +9,24 @@ TINY = dict(hidden=256, n_layers=2, n_heads=4, n_kv=2, head_dim=64, inter=512, v
             rope_theta=1.0e6, eps=1e-6)
 
 
+def _dequant_all(dec, cuda):
+    """Every S-X8 weight of the decoder as float32 (canonical R64 dequant), by layer."""
+    from kernel_sx8_v43 import decode_tensor_gpu_fast
+
+    class _Lazy(dict):
+        def __missing__(self, li):
+            ly = dec.layers[li]
+            return {n: decode_tensor_gpu_fast(getattr(ly, n).qt, getattr(ly, n).bases_info).to(cuda).float()
+                    for n in ("q", "k", "v", "o", "gate", "up", "down")}
+    W = _Lazy()
+    W["head"] = decode_tensor_gpu_fast(dec.head.qt, dec.head.bases_info).to(cuda).float()
+    return W
+
+
 def _ref_forward(dec, ids, W):
     """fp32 re-statement of SX8Decoder's math over dequantized weights; returns logits
-    for every position of `ids`."""
+    for every position of `ids`.  Attention products are float32 matmuls on contiguous
+    operands."""
     import torch
     cfg = dec.cfg
     nh, nk, hd, eps = cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["eps"]
@@ -33,11 +48,12 @@ def _ref_forward(dec, ids, W):
         k = rope(rms((h @ w["k"].T).view(T, nk, hd), ly.k_norm))
         v = (h @ w["v"].T).view(T, nk, hd)
         rep = nh // nk
-        k = k.repeat_interleave(rep, 1)
-        v = v.repeat_interleave(rep, 1)
-        s = torch.einsum("thd,shd->hts", q, k) / math.sqrt(hd)
+        qh = q.permute(1, 0, 2).contiguous()                                  # (nh, T, hd)
+        kt = k.repeat_interleave(rep, 1).permute(1, 2, 0).contiguous()        # (nh, hd, T)
+        vh = v.repeat_interleave(rep, 1).permute(1, 0, 2).contiguous()        # (nh, T, hd)
+        s = torch.matmul(qh, kt) / math.sqrt(hd)
         s = s + torch.triu(torch.full((T, T), float("-inf"), device=s.device), 1)
-        a = torch.einsum("hts,shd->thd", torch.softmax(s, -1), v).reshape(T, nh * hd)
+        a = torch.matmul(torch.softmax(s, -1), vh).permute(1, 0, 2).reshape(T, nh * hd)
         x = x + a @ w["o"].T
         h2 = rms(x, ly.post_norm)
         x = x + (torch.nn.functional.silu(h2 @ w["gate"].T) * (h2 @ w["up"].T)) @ w["down"].T
@@ -83,3 +99,34 @@ def test_e2e_prefill_decode_graph(hiplib, cuda):
         for i in range(6):
             row = ref_all[len(ids) - 1 + i]
             assert row[out_e[i]] >= row.max() - 2e-2 * row.abs().max(), (fused, i)
+
+
+@pytest.mark.gpu
+def test_e2e_full_depth_qwen3_4b(hiplib, cuda):
+    """BASELINE config 5 at full depth: the 36-layer Qwen3-4B-style decoder (hidden 2560,
+    32/8 heads of 128, SwiGLU 9728, vocab 151936, every linear S-X8 with its own weights).
+    The library-op prefill's logits at every prompt position against an fp32 decoder over
+    the canonical R64 weights, max|dlogits| / max|logits| <= 5e-2 -- the reference's own
+    end-to-end bar (scripts/integrate_fused_v44.py:119-167, 16 tokens there, 96 here) --
+    and 16 greedy tokens replayed from a HIP graph equal to the eager steps."""
+    import torch
+    from e2e_decoder import QWEN3_4B, SX8Decoder
+    print("e2e full depth: building 36 layers", flush=True)
+    dec = SX8Decoder(QWEN3_4B, device=cuda, seed=7, max_len=256)
+    g = torch.Generator(device="cpu").manual_seed(17)
+    ids = torch.randint(0, QWEN3_4B["vocab"], (96,), generator=g).to(cuda)
+    logits = dec.prefill_fused(ids, all_logits=True)
+    torch.cuda.synchronize()
+    print("e2e full depth: reference forward", flush=True)
+    ref = _ref_forward(dec, ids, _dequant_all(dec, cuda))
+    rel = ((logits - ref).abs().max() / ref.abs().max()).item()
+    agree = (logits.argmax(-1) == ref.argmax(-1)).float().mean().item()
+    print(f"e2e full depth: logits rel {rel:.3e}, argmax agreement {agree:.3f}", flush=True)
+    assert rel <= 5e-2
+    # the last row's token through the generation path (final norm inside the lm_head GEMV)
+    first = dec.prefill_fused(ids)
+    assert first.item() == logits[-1].argmax().item() or \
+        ref[-1, first.item()] >= ref[-1].max() - 5e-2 * ref[-1].abs().max()
+    out_g, _, _ = dec.generate(ids, 16, use_graph=True)
+    out_e, _, _ = dec.generate(ids, 16, use_graph=False)
+    assert torch.equal(out_g.cpu(), out_e.cpu())

@@ -356,8 +356,9 @@ def test_prefill_gemm(hiplib, oracle, cuda, monkeypatch, name, N, K, M, tile):
     import _sx8lib as L
     Yc = torch.empty_like(Yz)
     Xd = Xp.to(cuda)
+    ws, nb = L.gemm_workspace(M, (N,), qt["n_cb"], cuda)
     L.call("sx8_gemm_prefill_core", L.ptr(Xd), M, Xd.shape[1], Xd.shape[1], L.ptr(t[0]),
-           L.ptr(t[1]), 6, N, qt["n_cb"], L.ptr(Yc), L.stream(cuda))
+           L.ptr(t[1]), 6, N, qt["n_cb"], L.ptr(Yc), L.ptr(ws), nb, L.stream(cuda))
     L.call("sx8_gemm_pca_z", L.ptr(Z), M, L.ptr(t[0]), 6, N, qt["n_cb"], L.ptr(Yc), L.stream(cuda))
     assert oracle.rel_err(Yc.cpu().numpy(), Y_ref) <= 1e-3
 
@@ -463,15 +464,17 @@ def test_prefill_gemm_group(hiplib, oracle, cuda, monkeypatch, name, Ns, K, M, t
     n = len(Ns)
     Pa = ctypes.c_void_p * n
     ys = [torch.empty(M, N, device=cuda) for N in Ns]
+    ws, nb = L.gemm_workspace(M, Ns, n_cb, cuda)
     L.call("sx8_gemm_prefill_group", L.ptr(Xd), M, K, K, n, Pa(*[t[0].data_ptr() for t in ts]),
            Pa(*[t[1].data_ptr() for t in ts]), 6, Pa(*[t[2].data_ptr() for t in ts]),
            Pa(*[t[3].data_ptr() for t in ts]), (ctypes.c_int64 * n)(*Ns), n_cb,
-           Pa(*[y.data_ptr() for y in ys]), L.stream(cuda))
+           Pa(*[y.data_ptr() for y in ys]), L.ptr(ws), nb, L.stream(cuda))
     for i, (qt, bi) in enumerate(mats):
         y1 = torch.empty(M, Ns[i], device=cuda)
         t = ts[i]
+        ws1, nb1 = L.gemm_workspace(M, (Ns[i],), n_cb, cuda)
         L.call("sx8_gemm_prefill", L.ptr(Xd), M, K, K, L.ptr(t[0]), L.ptr(t[1]), 6, L.ptr(t[2]), L.ptr(t[3]),
-               Ns[i], n_cb, L.ptr(y1), L.stream(cuda))
+               Ns[i], n_cb, L.ptr(y1), L.ptr(ws1), nb1, L.stream(cuda))
         ref = oracle.gemm_f64(X.numpy(), oracle.dequant_r64(qt, bi))
         got = ys[i].cpu().numpy()
         assert oracle.rel_err(got, ref) <= 1e-3, i

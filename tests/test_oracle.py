@@ -366,3 +366,73 @@ def test_gemv_reference_identity(oracle):
     v44 = to_v44(qt, bi)
     for n in (0, 17, 95):
         assert abs(decode_v44_numpy(v44, x.astype(np.float64), n) - y[n]) <= 2e-3 * np.max(np.abs(y))
+
+
+# ----------------------------------------------- prefill GEMM operand (core_f16)
+
+def test_core_kat_degenerate_and_signed_zero(oracle):
+    # dmin == dmax = v: d = 0 so step = 1e-10f and rlo = fmaf(0, k1, v) = v; w = v + lv*1e-10
+    # is within 6.3e-9 of v, below half an fp16 ulp for every normal v -> exactly v.  v = 0:
+    # w <= 6.3e-9 < 2^-25 rounds to +0.  v = -0: rlo = (+0 * k1) + -0 = +0 -> +0 (0x0000).
+    for v, exp in ((0.75, 0x3A00), (-3.5, 0xC300), (2.0 ** -14, 0x0400), (0.0, 0x0000), (-0.0, 0x0000)):
+        qt = _block_qt([v], [v], [0b11100100], np.tile(np.arange(32) * 2, (1, 1)), [0x7F])
+        got = oracle.core_f16(qt).view(np.uint16)[0]
+        assert np.all(got == exp), (v, got)
+
+
+def test_core_kat_level_zero_is_rlo(oracle):
+    # lo = -1, hi = 1: d = 2, q = 0.5 (exact); level 0 gives rlo = lo + q*k1 with
+    # k1 = 0, 0, 3, 1 for strategies 0..3 -> -1, -1, 0.5, -0.5.  A swapped k1 table
+    # (reference rhi offsets 3*(s==1) + (s==3) used for rlo) gives 0.5 for strategy 1.
+    qt = _block_qt([-1.0], [1.0], [0b11100100], np.zeros((1, 32)), [0])
+    got = oracle.core_f16(qt)[0]
+    for sb, v in enumerate([-1.0, -1.0, 0.5, -0.5]):
+        assert np.all(got[8 * sb:8 * sb + 8] == v)
+    # level 63 of strategy 0 with lo = 0, hi = 64: 63 * 64 * 0.015873f = 63.99994 -> 64
+    qt = _block_qt([0.0], [64.0], [0], np.full((1, 32), 63), [0])
+    assert np.all(oracle.core_f16(qt)[0] == 64.0)
+
+
+def test_core_matches_exact_rationals_and_discriminates(oracle):
+    # the C recipe against an independent exact-rational evaluation (every binary32
+    # operation correctly rounded) on finite fuzzed blocks and quantized blocks; the same
+    # evaluation with 1/63 for the 0.015873 constant or without the per-strategy range
+    # scaling disagrees with the oracle on some of the same weights
+    rng = np.random.default_rng(21)
+    qt, _ = _fuzz(rng, 60)
+    got = oracle.core_f16(qt).reshape(-1, 32)
+    lv = oracle.unpack_levels(qt["levels_hi"], qt["levels_lo"])
+    W = (rng.standard_normal((8, 256)) * 0.02).astype(np.float16)
+    qq, _ = oracle.quantize(W)
+    got_q = oracle.core_f16(qq).reshape(-1, 32)
+    lv_q = oracle.unpack_levels(qq["levels_hi"], qq["levels_lo"])
+    bad, diff63, diffscale, n = 0, 0, 0, 0
+    for (q_, g_, l_) in ((qt, got, lv), (qq, got_q, lv_q)):
+        ok = np.nonzero(np.isfinite(q_["dmin"].astype(np.float32)) & np.isfinite(q_["dmax"].astype(np.float32)))[0]
+        for bid in ok[::2]:
+            for t in range(0, 32, 2):
+                args = (q_["dmin"][bid], q_["dmax"][bid], int(q_["config"][bid]), int(l_[bid, t]), t)
+                e = oracle.core_exact_weight(*args)
+                bad += int(e.view(np.uint16) != g_[bid, t].view(np.uint16))
+                diff63 += int(oracle.core_exact_weight(*args, c_step=1 / 63).view(np.uint16) != e.view(np.uint16))
+                n += 1
+    assert n > 2000 and bad == 0
+    assert diff63 > 0
+    # range scaling: strategy 1 with a nonzero level must not decode like strategy 0
+    qt1 = _block_qt([0.0], [1.0], [0x55], np.full((1, 32), 40), [0])
+    qt0 = _block_qt([0.0], [1.0], [0x00], np.full((1, 32), 40), [0])
+    assert not np.array_equal(oracle.core_f16(qt1), oracle.core_f16(qt0))
+
+
+def test_core_is_within_one_ulp_of_r64_without_pca(oracle):
+    # the operand is the reference's float32 decode without PCA; against the canonical R64
+    # with zero PCA terms it may differ only in the last fp16 bit, and rarely
+    g = np.random.default_rng(22)
+    W = (g.standard_normal((256, 512)) * 0.02).astype(np.float16)
+    qt, bi = oracle.quantize(W)
+    zero = {"n_cb": bi["n_cb"], "data": np.zeros_like(bi["data"]), "scales": np.zeros_like(bi["scales"])}
+    a = oracle.core_f16(qt).view(np.uint16).astype(np.int32)
+    b = oracle.dequant_r64(qt, zero).view(np.uint16).astype(np.int32)
+    frac = np.count_nonzero(a != b) / a.size
+    assert np.max(np.abs(a - b)) <= 1
+    assert frac < 2e-3, frac

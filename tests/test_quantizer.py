@@ -1,6 +1,8 @@
-"""The product quantizer's deterministic half against the oracle (CPU), and its PCA half
-by invariants (the SVD/eigen signs and order are not bit-pinnable: they depend on the
-LAPACK / rocSOLVER build, scripts/quantize_qwen35_4b_sx8_v43_gpu.py:75-142)."""
+"""The product quantizer's deterministic half against the oracle (CPU); its PCA half
+(scripts/quantize_qwen35_4b_sx8_v43_gpu.py:75-142) by known answers -- residual slices
+whose principal directions, lower-median / 3 scales and coefficient bytes follow in
+closed form, up to the singular-vector sign the decomposition returns (that sign depends
+on the LAPACK / rocSOLVER build) -- and by invariants on quantized Gaussian weights."""
 import numpy as np
 import pytest
 import torch
@@ -64,6 +66,92 @@ def test_torch_v6_encode_matches_oracle(oracle):
     hi, lo = pack_levels_6bit(lv.numpy())
     ohi, olo = oracle.pack_levels(olv)
     assert np.array_equal(hi, ohi) and np.array_equal(lo, olo)
+
+
+# ------------------------------------------------------------- PCA known answers
+
+def _hadamard(n):
+    H = np.array([[1.0]])
+    while H.shape[0] < n:
+        H = np.block([[H, H], [H, -H]])
+    return H
+
+
+_PCA_K = np.array([1, -2, 3, -3, 4, -6, 9, 12])       # magnitudes k_w, w = 0..7
+_PCA_A = np.array([8.0, 4.0, 2.0, 1.0])               # component weights: distinct energies
+_PCA_TAU = 1.0 / 64
+_PCA_ROWS = {0: (1, 2, 3, 5), 1: (6, 9, 12, 17)}      # Walsh rows used as directions per kb
+
+
+def _pca_case():
+    """Two K blocks (n_cb = 2) of 32 rows each.  Row r = 8u + w of block kb holds the
+    residual sum_i c_i[r] V_i with V_i = Walsh row _PCA_ROWS[kb][i] / sqrt(32) (orthonormal)
+    and c_i[r] = a_i H4[i, u] k_w tau.  The c_i are mutually orthogonal (H4 rows), so
+    V_0..V_3 are the right singular vectors in order of a_i.  |c_i| takes the values
+    a_i tau |k_w| four times each: sorted, positions 8-15 hold 3 and 16-19 hold 4, so the
+    lower median (position 15 of 32) is 3 a_i tau and the scale a_i tau; c_i / scale =
+    H4[i, u] k_w exactly, clamped to [-8, 7].  dmin = dmax = 0, levels 0, config 0 make the
+    V6 reconstruction zero, so the residual equals the block values."""
+    H32, H4 = _hadamard(32) / np.sqrt(32.0), _hadamard(4)
+    n_rows, n_cb = 32, 2
+    blocks = np.zeros((n_rows, n_cb, 32))
+    for kb in range(n_cb):
+        V = H32[list(_PCA_ROWS[kb])]
+        for r in range(n_rows):
+            u, w = divmod(r, 8)
+            c = _PCA_A * H4[:, u] * _PCA_K[w] * _PCA_TAU
+            blocks[r, kb] = c @ V
+    n_blk = n_rows * n_cb
+    return (np.zeros((n_blk, 32), np.uint8), np.zeros(n_blk, np.float32), np.zeros(n_blk, np.float32),
+            np.zeros(n_blk, np.uint8), blocks.reshape(n_blk, 32).astype(np.float32), n_cb, H32, H4)
+
+
+def _check_pca_known_answers(coeff, data, scales):
+    _, _, _, _, _, n_cb, H32, H4 = _pca_case()
+    coeff = np.asarray(coeff).reshape(32, n_cb)
+    data = np.asarray(data, np.float64).reshape(n_cb, 2, 32)
+    scales = np.asarray(scales, np.float64).reshape(n_cb, 2)
+    for kb in range(n_cb):
+        V = H32[list(_PCA_ROWS[kb])]
+        cq = []
+        for i in range(2):
+            # the kept direction is +-V_i; its sign decides the coefficient signs
+            sgn = np.sign(data[kb, i] @ V[i])
+            assert np.allclose(data[kb, i], sgn * V[i], atol=1e-5), (kb, i)
+            assert abs(scales[kb, i] - _PCA_A[i] * _PCA_TAU) <= 1e-5 * _PCA_A[i] * _PCA_TAU, (kb, i)
+            cq.append(np.array([np.clip(sgn * H4[i, r // 8] * _PCA_K[r % 8], -8, 7) for r in range(32)]))
+        exp = (cq[0].astype(np.int64) & 0xF) | ((cq[1].astype(np.int64) & 0xF) << 4)
+        assert np.array_equal(coeff[:, kb].astype(np.int64), exp), kb
+
+
+def test_pca_known_answers_oracle(oracle):
+    lv, dmin, dmax, cfg, blocks, n_cb, _, _ = _pca_case()
+    _check_pca_known_answers(*oracle.pca_correct(lv, dmin, dmax, cfg, blocks, n_cb))
+
+
+@pytest.mark.parametrize("plant", ["median/4", "upper_median", "vh1:3"])
+def test_pca_known_answers_catch_planted_mistakes(oracle, plant):
+    lv, dmin, dmax, cfg, blocks, n_cb, _, _ = _pca_case()
+    with pytest.raises(AssertionError):
+        _check_pca_known_answers(*oracle.pca_correct(lv, dmin, dmax, cfg, blocks, n_cb, _plant=plant))
+
+
+def _product_pca(method, device):
+    from quantize_sx8 import pca_correct
+    lv, dmin, dmax, cfg, blocks, n_cb, _, _ = _pca_case()
+    t = lambda a: torch.from_numpy(a).to(device)
+    return pca_correct(t(lv), t(dmin), t(dmax), t(cfg), t(blocks), n_cb, pca_method=method)
+
+
+@pytest.mark.parametrize("method", ["svd", "gram"])
+def test_pca_known_answers_product_cpu(method):
+    _check_pca_known_answers(*_product_pca(method, "cpu"))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("method", ["svd", "gram"])
+def test_pca_known_answers_product_gpu(hiplib, cuda, method):
+    _check_pca_known_answers(*_product_pca(method, cuda))
 
 
 def test_cpu_quantizer_pca_invariants():
