@@ -168,9 +168,10 @@ int32_t sx8_gemm_prefill_plan(int64_t M, int32_t n_mats, const int64_t* Ns, int6
                               int64_t* desc);
 
 /* Prefill GEMM Y (M, N) float32 = X (M, ldx) fp16 . W^T on the v4.4 layout.
- * The PCA-free core weights rlo + step*lv are decoded in float32 (the reference's
- * R32 form, cuda/sx8_fused_wmma.cu:70-94), rounded to fp16 and fed to
- * v_mfma_f32_32x32x16_f16 with float32 accumulation; the PCA term sum_kb c0 Z0 + c1 Z1 is
+ * The PCA-free core weights rlo + step*lv are decoded with the reference's float32
+ * range parameters (cuda/sx8_fused_wmma.cu:70-94), the multiply-add rounded once to fp16,
+ * and fed to v_mfma_f32_32x32x16_f16 with float32 accumulation; the PCA term
+ * sum_kb c0 Z0 + c1 Z1 is
  * added by extra MFMA k-steps over Z (split into fp16 hi + lo parts), which the call
  * computes first with the reference's summation tree.  The MFMA operands are therefore
  * not the canonical R64 fp16 weights (those come from sx8_dequant_f16); the product is

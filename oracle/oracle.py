@@ -361,11 +361,24 @@ def _rn32(fr: Fraction) -> Fraction:
     return Fraction(float(min(cands, key=key)))
 
 
-def core_exact_weight(dmin16, dmax16, cfg, lv, t, c_step=None):
+def _rn16(fr: Fraction) -> np.float16:
+    """Correctly rounded binary16 (RNE) of an exact rational, subnormals included."""
+    if fr == 0:
+        return np.float16(0.0)
+    x = np.float16(float(fr))
+    cands = [np.nextafter(x, np.float16(-np.inf)), x, np.nextafter(x, np.float16(np.inf))]
+
+    def key(c):
+        return abs(Fraction(float(c)) - fr), int(np.array(c, dtype=np.float16).view(np.uint16)) & 1
+    return min(cands, key=key)
+
+
+def core_exact_weight(dmin16, dmax16, cfg, lv, t, c_step=None, f32_store=False):
     """One operand value of ``core_f16`` from exact rationals: every binary32 operation
-    rounded once (a fused multiply-add rounds the exact a*b + c once), then fp16 RNE.
-    ``c_step`` overrides the 0.015873 constant (tests plant 1/63 here to show that the
-    checks discriminate).  Finite endpoints only."""
+    rounded once, and the final multiply-add step*lv + rlo rounded once to fp16 (what the
+    kernel's v_fma_mix does).  ``f32_store`` rounds it to binary32 first (the reference's
+    float w then __float2half); ``c_step`` overrides the 0.015873 constant.  Tests use
+    both knobs to show that the checks discriminate.  Finite endpoints only."""
     lo = Fraction(float(np.float16(dmin16)))
     hi = Fraction(float(np.float16(dmax16)))
     c = Fraction(float(np.float32(C_STEP))) if c_step is None else Fraction(c_step)
@@ -377,8 +390,8 @@ def core_exact_weight(dmin16, dmax16, cfg, lv, t, c_step=None):
     e = (0, 2, 2, 1)[s]
     rlo = _rn32(q * k1 + lo)
     step = m / (2 ** e) if d > 0 else Fraction(float(np.float32(STEP_FLOOR)))
-    w = _rn32(step * lv + rlo)
-    return np.float16(np.float32(float(w)))
+    w = step * lv + rlo
+    return _rn16(_rn32(w) if f32_store else w)
 
 
 def dequant_r64_numpy(qt, bases_info):

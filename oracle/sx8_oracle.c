@@ -22,7 +22,8 @@
  *   - R32-ggml, llama.cpp's no-PCA float32 dequant of GGUF block_sx8 records
  *     (llama-cpp-sx8.patch:746-767), with and without fused multiply-adds;
  *   - the prefill GEMM's fp16 MFMA operand (the PCA-free core of the reference's float32
- *     decode, cuda/sx8_fused_wmma.cu:70-94, in the HIP kernel's evaluation order);
+ *     decode, cuda/sx8_fused_wmma.cu:70-94, in the HIP kernel's evaluation order, the
+ *     final multiply-add rounded once to fp16);
  *   - float64-accumulated GEMV/GEMM references used as the 1e-3 yardstick
  *     (scripts/sx8_decode1_v3.py:131-133, scripts/sx8_fused_wmma.py:128-132);
  *   - the CPU dequant + fp32-accumulated GEMV that bench.py reports as its CPU
@@ -203,15 +204,46 @@ void sx8o_dequant_r32(int64_t n_blocks, int32_t n_cb,
 
 /* ------------------------------------------------- prefill GEMM operand (core) */
 
+/* binary64 -> binary16, round to nearest even, subnormals, overflow to infinity.  adj
+ * breaks an exact tie the other way when a lower-order part of the value is known:
+ * adj > 0 means the true value lies just above |x| in magnitude, adj < 0 just below. */
+static uint16_t sx8o_f64_to_f16_adj(double x, double adj) {
+    const uint16_t sign = signbit(x) ? 0x8000u : 0u;
+    if (isnan(x)) return (uint16_t)(sign | 0x7E00u);
+    const double ax = fabs(x);
+    if (isinf(x)) return (uint16_t)(sign | 0x7C00u);
+    if (ax == 0.0) return sign;
+    int e2;
+    (void)frexp(ax, &e2);                        /* ax = f 2^e2, f in [0.5, 1) */
+    int ue = e2 - 1 - 10;                        /* exponent of the fp16 ulp at ax */
+    if (ue < -24) ue = -24;                      /* subnormal range: ulp 2^-24 */
+    const double q = ldexp(ax, -ue);             /* exact: a power-of-two scaling */
+    double n = floor(q);
+    const double frac = q - n;
+    if (frac > 0.5 || (frac == 0.5 && (adj > 0 || (adj == 0 && fmod(n, 2.0) != 0)))) n += 1.0;
+    /* n counts ulps of 2^ue; a normal result has n in [1024, 2048] (2048 carries) */
+    uint32_t bits;
+    if (ue == -24) {
+        bits = (uint32_t)n;                      /* 1024 is the smallest normal, 0x0400 */
+    } else {
+        bits = ((uint32_t)(ue + 10 + 15) << 10) + ((uint32_t)n - 1024u);
+    }
+    if (bits >= 0x7C00u) bits = 0x7C00u;
+    return (uint16_t)(sign | bits);
+}
+
 /* The fp16 operand the prefill GEMM feeds to its MFMAs for weight t of a block: the
  * PCA-free core rlo + step*lv of the reference's float32 decode (cuda/sx8_fused_wmma.cu:
- * 70-94, whose WMMA tiles also hold float32 weights rounded with __float2half), evaluated
- * the way the HIP kernel does it (csrc/sx8_gemm.hip, sub_range / dec_pair):
+ * 70-94, whose WMMA tiles hold that float32 weight plus the per-weight PCA, rounded with
+ * __float2half), evaluated the way the HIP kernel does it (csrc/sx8_gemm.hip, sub_range /
+ * dec_pair):
  *   d = hi - lo, q = d * 0.25f, m = d * 0.015873f           (binary32, each rounded)
  *   s = strategy of sub-block t/8; k1 = {0, 0, 3, 1}[s], e = {0, 2, 2, 1}[s]
  *   rlo  = fmaf(q, k1, lo)                                  (= lo + q*(3*(s==2)+(s==3)))
  *   step = d > 0 ? m * 2^-e : 1e-10f    (the range rhi - rlo is d * {1, 1/4, 1/4, 1/2})
- *   w    = fmaf(step, lv, rlo), then binary32 -> fp16 (RNE).
+ *   w16  = fp16(step * lv + rlo), the exact value rounded once (RNE) -- the kernel's
+ *          v_fma_mix{lo,hi}_f16 evaluates the multiply-add at full precision and rounds
+ *          straight to fp16, with no binary32 intermediate.
  * The PCA term is not part of the operand (the kernel adds it through Z).  The reference
  * floors step at 1e-10 after scaling; for hi > lo the unfloored step is at least
  * 2.4e-10 (the smallest fp16 range times 0.015873 / 4), so the floor binds exactly when
@@ -232,8 +264,14 @@ void sx8o_core_f16(int64_t n_blocks, const uint16_t* dmin, const uint16_t* dmax,
             static const int et[4] = {0, 2, 2, 1};
             const float rlo = fmaf(q, k1t[s], lo_f);
             const float step = d > 0.f ? ldexpf(m, -et[s]) : 1e-10f;
-            const float lv = (float)sx8o_level(hi + bid * 16, lo + bid * 8, t);
-            out16[bid * 32 + t] = sx8o_f32_to_f16(fmaf(step, lv, rlo));
+            const double a = (double)step * (double)sx8o_level(hi + bid * 16, lo + bid * 8, t);  /* exact */
+            const double b = (double)rlo;
+            /* a + b = sum + err exactly (two-sum); a tie of the fp16 rounding of sum is
+             * broken by err, so the result is the exact value rounded once */
+            const double sum = a + b;
+            const double bb = sum - a;
+            const double err = (a - (sum - bb)) + (b - bb);
+            out16[bid * 32 + t] = sx8o_f64_to_f16_adj(sum, signbit(sum) ? -err : err);
         }
     }
 }

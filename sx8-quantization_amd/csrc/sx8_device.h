@@ -4,13 +4,19 @@
 // one row in 30 bytes -- dmin fp16, dmax fp16, config u8 (4 x 2-bit range strategy),
 // 16 B of high nibbles, 8 B of low quads, coeff u8 (two signed 4-bit PCA coefficients).
 //
-// Two decode recipes live here:
-//   * R64 (sx8_r64_subblock): the canonical dequant of scripts/kernel_sx8_v43.py:14-51
-//     under Numba typing -- binary32 hi-lo, binary64 everywhere else, binary32 store,
-//     RNE to fp16.  Every kernel that hands fp16 weights to a caller or to the MFMA
-//     units uses it, so those weights are bit-identical to the canonical dequant.
-//   * the fp32 GEMV decode in sx8_gemv.hip, which only feeds an fp32 dot product
-//     (tolerance 1e-3 relative, scripts/sx8_decode1_v3.py:131-133).
+// Decode recipes of this library:
+//   * R64 (sx8_r64_subblock, here): the canonical dequant of scripts/kernel_sx8_v43.py:
+//     14-51 under Numba typing -- binary32 hi-lo, binary64 everywhere else, binary32
+//     store, RNE to fp16.  The kernels that hand fp16 weights to a caller (full dequant,
+//     embedding gather) use it, so those weights are bit-identical to the canonical
+//     dequant.
+//   * the prefill GEMM's MFMA operand (sx8_gemm.hip): the PCA-free core rlo + step*lv
+//     with the reference's float32 range parameters (cuda/sx8_fused_wmma.cu:70-94), the
+//     multiply-add rounded once to fp16; PCA is added through Z.  Not R64: it differs
+//     from the R64 weights without PCA in the last fp16 bit on about 1e-4 of weights.
+//   * the fp32 GEMV decode in sx8_gemv.hip, which only feeds an fp32 dot product.
+//   The GEMV and GEMM products meet max|dY| / max|Y| <= 1e-3 against the float64 product
+//   of the R64 weights (scripts/sx8_decode1_v3.py:131-133).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>

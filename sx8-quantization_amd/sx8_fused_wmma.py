@@ -6,9 +6,9 @@ Interface of scripts/sx8_fused_wmma.py (reference): ``_get_module()`` (an object
 which builds the kb-major dict these functions consume.
 
 The kernel behind it is the same MFMA prefill as gemm_sx8_compact (sx8_gemm_prefill_
-split): the PCA-free core weights rlo + step*lv decoded in float32 (the reference's R32
-form), rounded to fp16 into v_mfma_f32_32x32x16_f16 operands, PCA added through Z as
-extra k-steps.  Like the reference's WMMA tiles (cuda/sx8_fused_wmma.cu:70-97) these
+split): the PCA-free core weights rlo + step*lv with the reference's float32 range
+parameters, each multiply-add rounded once to fp16, as v_mfma_f32_32x32x16_f16 operands;
+PCA added through Z as extra k-steps.  Like the reference's WMMA tiles (cuda/sx8_fused_wmma.cu:70-97) these
 operands are not the canonical R64 weights; the product meets the 1e-3 bar.
 ``make_tensors`` no longer builds the rlo/step fp16 tables of precompute_rlo_step.py: no
 kernel here reads them.

@@ -4,8 +4,8 @@ Interface of scripts/sx8_gemm_compact.py (reference): ``_ext()`` (an object with
 ``compute_z44_batch`` and ``gemm_compact``) and ``gemm_sx8_compact``.
 
 ``gemm_sx8_compact`` runs sx8_gemm_prefill: Z is computed inside the call, the core
-weights (rlo + step*lv) are decoded in float32, rounded to fp16 and fed to
-v_mfma_f32_32x32x16_f16, and the PCA term rides along as extra MFMA k-steps over Z.
+weights rlo + step*lv (float32 range parameters, the multiply-add rounded once to fp16)
+feed v_mfma_f32_32x32x16_f16, and the PCA term rides along as extra MFMA k-steps over Z.
 ``_ext().gemm_compact`` keeps the reference's caller-supplied-Z contract with the same
 kernel (sx8_gemm_prefill_z).  The library allocates nothing: each call takes its
 workspace (Z, packed X, split-K partials) from torch's caching allocator on the current

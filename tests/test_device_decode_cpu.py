@@ -1,6 +1,8 @@
 """Runs the product's R64 device decode (sx8_r64_subblock from csrc/sx8_device.h),
-compiled for the host, against the oracle: the same function the dequant, embedding
-and prefill kernels call must be bit-exact on the CPU before it reaches a GPU."""
+compiled for the host, against the oracle: the same function the dequant and embedding
+kernels call must be bit-exact on the CPU before it reaches a GPU.  (The prefill GEMM's
+operand decode is a different recipe, pinned on the GPU by
+tests/test_gpu_prefill.py::test_prefill_mfma_operand_bit_exact.)"""
 import ctypes
 import os
 import subprocess

@@ -1,9 +1,10 @@
 """GPU parity of the HIP hot path against the CPU oracle (run with -m gpu).
 
 Bars:
-  * dequantized fp16 weights (full-tensor dequant, embedding rows, and the MFMA
-    operand tiles of the prefill GEMM) are bit-exact to the canonical R64 dequant,
-    including the degenerate-block step = 1e-10 floor;
+  * dequantized fp16 weights (full-tensor dequant and embedding rows) are bit-exact to
+    the canonical R64 dequant, including the degenerate-block step = 1e-10 floor (the
+    prefill GEMM's MFMA operands follow the reference's float32 decode instead and are
+    pinned against their own oracle recipe in test_gpu_prefill.py);
   * GEMV / GEMM outputs are within max|dY| / max|Y_ref| <= 1e-3 of the float64-
     accumulated X . W16^T (the reference's metric, sx8_fused_wmma.py:132).
 """

@@ -139,8 +139,10 @@ def _operand_case(kind, cuda, oracle):
 def test_prefill_mfma_operand_bit_exact(hiplib, oracle, cuda, kind):
     """The fp16 operand the GEMM decodes for every weight, read back through the core-only
     GEMM with X = the identity (Y[k, n] = 1 * w(n, k) + zeros: exact in the float32
-    accumulators), against the oracle's core_f16 bit for bit (-0 reads back as +0).  Fuzz
-    blocks: every strategy and level, degenerate, reversed and subnormal ranges."""
+    accumulators), against the oracle's core_f16 bit for bit (-0 reads back as +0): the
+    reference's float32 range parameters (cuda/sx8_fused_wmma.cu:70-94), step*lv + rlo
+    rounded once to fp16.  Fuzz blocks: every strategy and level, degenerate, reversed and
+    subnormal ranges."""
     import torch
     import _sx8lib as L
     from prepare_v44 import to_v44_device
