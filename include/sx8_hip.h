@@ -186,6 +186,21 @@ int32_t sx8_gemm_prefill(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
                          const float* basis, const float* scales, int64_t N, int64_t n_cb,
                          float* Y, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* sx8_gemm_prefill without a workspace argument, for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  The call's scratch (Z, packed X, split-K partials) is a
+ * 64 MiB device array inside the library (one per device, held until the process ends);
+ * the call allocates, frees and synchronizes nothing.  Z plus the packed X must fit it,
+ * about 72 * M * n_cb bytes (M <= 3000 at K = 9728, M <= 11000 at K = 2560); a larger call
+ * returns SX8_ERR_UNSUPPORTED, and a split-K plan is used only if its partials fit the rest
+ * (otherwise an unsplit plan, same result up to the fp32 summation order).  All calls on a
+ * device share the array: calls that overlap in time on one device race (serialize them,
+ * e.g. on one stream).  Same output as sx8_gemm_prefill whenever both run the same plan. */
+int32_t sx8_gemm_prefill_static(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
+                                const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
+                                const float* basis, const float* scales, int64_t N, int64_t n_cb,
+                                float* Y, void* stream);
+
 /* Same GEMM from kb-major split arrays (dmin/dmax fp16, config, coeff, hi (n_blk*16),
  * lo (n_blk*8), all in bid = kb*N + n order).  Same workspace as sx8_gemm_prefill.
  * Replaces fused_forward (cuda/sx8_fused_wmma.cu:134-154, kernel :11-132). */

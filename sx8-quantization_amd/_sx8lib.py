@@ -50,6 +50,7 @@ SIGNATURES = [
     ("sx8_gemm_prefill_workspace_bytes", _I64, [_I64, _I32, _P, _I64]),
     ("sx8_gemm_prefill_plan", _I32, [_I64, _I32, _P, _I64, _P]),
     ("sx8_gemm_prefill", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _I64, _P]),
+    ("sx8_gemm_prefill_static", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P]),
     ("sx8_gemm_prefill_split", _I32,
      [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P]),
     ("sx8_gemm_prefill_z", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _I64, _I64, _P, _P, _I64, _P]),

@@ -21,6 +21,8 @@
 //   * tiles are dealt XCD by XCD in m-major order; shapes with fewer tiles than CUs
 //     split K into ranges of whole 4-block groups and add the partials in a fixed order.
 #include <algorithm>
+#include <climits>
+#include <mutex>
 
 #include "sx8_buffer.h"
 #include "sx8_device.h"
@@ -978,20 +980,20 @@ Plan plan_split(int64_t M, int64_t N, int64_t T, int64_t n_cb, int64_t S, int MF
 
 // Tiles of 128 MF rows over NB column tiles (N columns in all); the number of K ranges
 // (1..8, at most one per 4-block group) that the cost model prefers.
-Plan plan_k_gemm(int64_t M, int64_t N, int64_t NB, int64_t n_cb, int MF) {
+Plan plan_k_gemm(int64_t M, int64_t N, int64_t NB, int64_t n_cb, int MF, int64_t part_cap) {
     const int64_t T = ((M + 128 * MF - 1) / (128 * MF)) * NB;
     const int64_t groups = (n_cb + 3) / 4;
     Plan best = plan_split(M, N, T, n_cb, 1, MF);
     for (int64_t S = 2; S <= std::min<int64_t>(8, groups); ++S) {
         const Plan p = plan_split(M, N, T, n_cb, S, MF);
-        if (p.cost < best.cost) best = p;
+        if (p.cost < best.cost && (int64_t)(p.S - 1) * M * N * 4 <= part_cap) best = p;
     }
     return best;
 }
 
 // 512-row tiles: Tf = 0 (every tile split St ways) or the whole rounds of 256 tiles with
 // the remainder split; St from 1 to 8.
-Plan plan_w1(int64_t M, int64_t NB, int64_t n_cb) {
+Plan plan_w1(int64_t M, int64_t NB, int64_t n_cb, int64_t part_cap) {
     const int64_t T = ((M + kW1BM - 1) / kW1BM) * NB;
     const int64_t groups = (n_cb + 3) / 4;
     Plan best{};
@@ -1011,7 +1013,7 @@ Plan plan_w1(int64_t M, int64_t NB, int64_t n_cb) {
             p.cost = (double)(Tf / 256) * n_cb * kW1Cost +
                      (double)((rem * p.St + 255) / 256) * p.kbs * kW1Cost +
                      (p.St > 1 ? (double)rem * (p.St + 1) * tile_bytes * 2.0 / kBytesPerUnit : 0.0);
-            if (p.cost < best.cost) best = p;
+            if (p.cost < best.cost && p.n_split * (p.St - 1) * kW1BM * kBN * 4 <= part_cap) best = p;
             if (rem == 0) break;
         }
     }
@@ -1020,14 +1022,15 @@ Plan plan_w1(int64_t M, int64_t NB, int64_t n_cb) {
 
 // N columns in NB column tiles (a group pads every matrix to whole tiles).
 // SX8_GEMM_TILE=256 or 512 forces a tile height (tuning); otherwise the cheaper plan.
-Plan plan_gemm(int64_t M, int64_t N, int64_t NB, int64_t n_cb) {
+// part_cap bounds the split-K partial bytes (the unsplit plans need none).
+Plan plan_gemm(int64_t M, int64_t N, int64_t NB, int64_t n_cb, int64_t part_cap = INT64_MAX) {
     const int MF = M > 128 ? 2 : 1;
-    const Plan p256 = plan_k_gemm(M, N, NB, n_cb, MF);
+    const Plan p256 = plan_k_gemm(M, N, NB, n_cb, MF, part_cap);
     // k_gemm_w1 addresses rows up to the next multiple of 512 with 31-bit offsets
     const int64_t Mp = (M + kW1BM - 1) / kW1BM * kW1BM;
     const bool w1_ok = M > 256 && Mp / 32 * n_cb * 2048 <= 0x7FFFFFFF && Mp * n_cb * 8 <= 0x7FFFFFFF;
     if (!w1_ok) return p256;
-    const Plan p512 = plan_w1(M, NB, n_cb);
+    const Plan p512 = plan_w1(M, NB, n_cb, part_cap);
     const char* e = getenv("SX8_GEMM_TILE");
     const int forced = e ? atoi(e) : 0;
     if (forced == 256) return p256;
@@ -1097,11 +1100,12 @@ int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, in
                  const WeightSrc* ws_in, int32_t hdr_bytes, ZMode zm, const float* const* bases,
                  const float* const* scales, const float* Z, const int64_t* Ns, int64_t n_cb,
                  float* const* Ys, void* workspace, int64_t workspace_bytes, hipStream_t st,
-                 const float* silu_g = nullptr, const float* silu_u = nullptr) {
+                 const float* silu_g = nullptr, const float* silu_u = nullptr,
+                 int64_t part_cap = INT64_MAX) {
     using namespace sx8;
     int64_t Ntot = 0, NB = 0;
     if (!group_width(n_mats, Ns, Ntot, NB)) return fail(SX8_ERR_UNSUPPORTED, "%s: group too wide", what);
-    const Plan p = plan_gemm(M, Ntot, NB, n_cb);
+    const Plan p = plan_gemm(M, Ntot, NB, n_cb, part_cap);
     if (p.G > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "%s: grid too large", what);
     const WsLayout lay = ws_layout(p, M, Ntot, n_cb, n_mats, zm != ZMode::kNone);
     if (!workspace || workspace_bytes < lay.total || !aligned(workspace, 256))
@@ -1228,6 +1232,83 @@ extern "C" int32_t sx8_gemm_prefill(const uint16_t* X, int64_t M, int64_t ldx, i
     w.levels = levels;
     return run_gemm<false>("sx8_gemm_prefill", X, M, ldx, K, 1, &w, hdr_bytes, ZMode::kBasis, &basis,
                            &scales, nullptr, &N, n_cb, &Y, workspace, workspace_bytes, as_stream(stream));
+}
+
+// ------------------------------------------------- the no-allocation prefill entry point
+//
+// sx8_gemm_prefill_static: sx8_gemm_prefill for callers that cannot allocate (code under
+// HIP graph capture, serving loops, harnesses that forbid hipMalloc).  Its workspace is
+// `scratch`, a file-scope device array of kScratchBytes that every device running this
+// library holds until the process ends.  In host code `scratch` names a host-side stand-in,
+// not device memory: its device address is looked up once per device with
+// hipGetSymbolAddress (on the entry point's first call on that device, with the device
+// current) and only that address is passed to kernels.  Calls on one device share the
+// array: calls that overlap in time on one device race.  Nothing in it needs clearing:
+// every byte a call reads was written earlier in the same call (Zhl and the packed X by
+// the Z pass, partial tiles by the split-K work-groups; rows past M read zero through the
+// buffer loads' range checks).
+
+constexpr int64_t kScratchBytes = int64_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_dev[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device (looked up once per device).
+int32_t scratch_address(void** out) {
+    using namespace sx8;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(SX8_ERR_HIP, "sx8_gemm_prefill_static: hipGetDevice failed");
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return fail(SX8_ERR_UNSUPPORTED, "sx8_gemm_prefill_static: device %d beyond %d", dev, kMaxScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(SX8_ERR_HIP, "sx8_gemm_prefill_static: hipGetSymbolAddress(scratch) failed: %s",
+                        hipGetErrorString(e));
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return SX8_OK;
+}
+}  // namespace
+
+extern "C" int32_t sx8_gemm_prefill_static(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
+                                           const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
+                                           const float* basis, const float* scales, int64_t N,
+                                           int64_t n_cb, float* Y, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_gemm_prefill_static";
+    if (!X || !hdr || !levels || !basis || !scales || !Y) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (hdr_bytes != 6 && hdr_bytes != 8)
+        return fail(SX8_ERR_INVALID, "%s: hdr_bytes must be 6 or 8, got %d", what, hdr_bytes);
+    if (!aligned(hdr, hdr_bytes == 8 ? 8 : 2) || !aligned(levels, 8) || !aligned(X, 2) ||
+        !aligned(Y, 4) || !aligned(basis, 16) || !aligned(scales, 8))
+        return fail(SX8_ERR_INVALID, "%s: misaligned pointer", what);
+    int32_t rc = check_shape(what, M, ldx, K, N, n_cb);
+    if (rc != SX8_OK) return rc;
+    // Zhl and the packed X must fit; split-K partials only in what is left of the array
+    Plan unsplit{};
+    unsplit.S = 1;
+    const int64_t fixed = ws_layout(unsplit, M, N, n_cb, 1, true).total;
+    if (fixed > kScratchBytes)
+        return fail(SX8_ERR_UNSUPPORTED,
+                    "%s: M=%lld n_cb=%lld needs %lld scratch bytes, the static scratch holds %lld "
+                    "(use sx8_gemm_prefill with a workspace)",
+                    what, (long long)M, (long long)n_cb, (long long)fixed, (long long)kScratchBytes);
+    void* ws = nullptr;
+    rc = scratch_address(&ws);
+    if (rc != SX8_OK) return rc;
+    WeightSrc w{};
+    w.hdr = hdr;
+    w.levels = levels;
+    return run_gemm<false>(what, X, M, ldx, K, 1, &w, hdr_bytes, ZMode::kBasis, &basis, &scales, nullptr, &N,
+                           n_cb, &Y, ws, kScratchBytes, as_stream(stream), nullptr, nullptr,
+                           kScratchBytes - fixed);
 }
 
 extern "C" int32_t sx8_dec_gemm_silu(const float* g, const float* u, int64_t M, int64_t K,
