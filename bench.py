@@ -58,8 +58,13 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|vocab|container|quantizer|e2e|copy "
-                    "(copy: the 512 MiB device copy that calibrates the HBM byte counters)")
+    ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|vocab|container|quantizer|e2e|copy|"
+                    "gemm-one (copy: the 512 MiB device copy that calibrates the HBM byte counters; "
+                    "gemm-one: --iters calls of one prefill shape, the counter workload)")
+    ap.add_argument("--shape", default="gate_proj", help="gemm-one: layer shape name")
+    ap.add_argument("--m", type=int, default=2048, help="gemm-one: rows of X")
+    ap.add_argument("--iters", type=int, default=200,
+                    help="calls per duration distribution (median/p10/p90), at least 200")
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--e2e-prompt", type=int, default=512)
     ap.add_argument("--e2e-new", type=int, default=256)
@@ -134,6 +139,29 @@ class HipEvents:
             self.hip.hipEventDestroy(e)
 
 
+def quantiles(us):
+    """median, p10, p90 (and the sample count) of a list of durations in us."""
+    a = np.asarray(us, dtype=np.float64)
+    p10, p50, p90 = np.percentile(a, [10, 50, 90])
+    return {"median_us": float(p50), "p10_us": float(p10), "p90_us": float(p90), "n": int(a.size)}
+
+
+def call_series(torch, st, fn, n, delay_ms=10):
+    """Durations (us) of n back-to-back calls fn(i): one HIP event (no system fence) on the
+    launch stream before the first call and after each one, so call i's duration is the
+    time between the events around it, the event packet included."""
+    ev = HipEvents(n + 1, st)
+    gpu_delay(torch, delay_ms)
+    ev.record(0)
+    for i in range(n):
+        fn(i)
+        ev.record(i + 1)
+    torch.cuda.synchronize()
+    out = [ev.ms(i, i + 1) * 1e3 for i in range(n)]
+    ev.close()
+    return out
+
+
 def bench_gemv(torch, L, layer, args):
     import ctypes
     dev = torch.device("cuda:0")
@@ -161,24 +189,19 @@ def bench_gemv(torch, L, layer, args):
     log(f"gemv: {R} copies x {step_bytes / 1e6:.1f} MB = {R * step_bytes / 1e9:.2f} GB resident")
     nL = len(layer)
     K = args.steps
-    ev = HipEvents(2 + 2 * nL * K, st)
+    ev = HipEvents(2, st)
 
-    def run_step(s, pairs=False):
-        for i, a in enumerate(calls[s % R]):
-            if pairs:
-                ev.record(2 + 2 * (s * nL + i))
+    def run_step(s):
+        for a in calls[s % R]:
             rc = fn(*a)
             if rc != 0:
                 raise RuntimeError(L.lib().sx8_last_error().decode())
-            if pairs:
-                ev.record(3 + 2 * (s * nL + i))
 
     for s in range(args.warmup):
         run_step(s)
     torch.cuda.synchronize()
 
-    # timed region: K steps back to back, bracketed by two events (no per-launch events)
-    torch.cuda.synchronize()
+    # timed region: K steps back to back, bracketed by two events (nothing in between)
     gpu_delay(torch, 50)                     # keep the GPU busy while the host enqueues
     ev.record(0)
     for s in range(K):
@@ -187,17 +210,21 @@ def bench_gemv(torch, L, layer, args):
     torch.cuda.synchronize()
     total_ms = ev.ms(0, 1)
 
-    # kernel-duration pass: the same K steps with an event pair around every launch
-    gpu_delay(torch, 50)
-    for s in range(K):
-        run_step(s, pairs=True)
-    torch.cuda.synchronize()
-    per_shape_ms = [0.0] * nL
-    for s in range(K):
-        for i in range(nL):
-            b = 2 + 2 * (s * nL + i)
-            per_shape_ms[i] += ev.ms(b, b + 1)
-    kern_ms = sum(per_shape_ms)
+    # distributions: args.iters steps with an event after each, and args.iters launches of
+    # each shape alone (rotating copies) with an event after each
+    nd = max(200, args.iters)
+    step_us = call_series(torch, st, run_step, nd, delay_ms=50)
+    per_shape = {}
+    for i, t in enumerate(layer):
+        def one(r, i=i):
+            rc = fn(*calls[r % R][i])
+            if rc != 0:
+                raise RuntimeError(L.lib().sx8_last_error().decode())
+        q = quantiles(call_series(torch, st, one, nd))
+        q["gbs_at_median"] = packed_bytes(t["N"], t["K"]) / (q["median_us"] * 1e-6) / 1e9
+        per_shape[t["name"]] = q
+    step_q = quantiles(step_us)
+    step_q["gbs_at_median"] = sum(packed_bytes(t["N"], t["K"]) for t in layer) / (step_q["median_us"] * 1e-6) / 1e9
 
     # the same layer as a decoder step runs it: q/k/v and gate/up share their input and
     # go out as one launch each (sx8_gemv_group), o and down alone -> 4 launches per step
@@ -238,8 +265,9 @@ def bench_gemv(torch, L, layer, args):
     torch.cuda.synchronize()
     g_ms = ev.ms(0, 1)
     ev.close()
+    gq = quantiles(call_series(torch, st, run_group_step, nd, delay_ms=50))
     grouped = {"launches_per_step": len(gcalls[0]), "ms_per_step": g_ms / K,
-               "gbs": step_bytes * K / (g_ms * 1e-3) / 1e9,
+               "gbs": step_bytes * K / (g_ms * 1e-3) / 1e9, "step_us": gq,
                "groups": [g for g in groups]}
 
     # the same seven launches per step, replayed from a HIP graph (how a decode loop that
@@ -273,15 +301,12 @@ def bench_gemv(torch, L, layer, args):
     out = {
         "ms_per_step": total_ms / K,
         "value_gbs": step_bytes * K / (total_ms * 1e-3) / 1e9,
-        "kernel_ms_total": kern_ms,
         "launches": K * nL,
-        "avg_launch_us": kern_ms * 1e3 / (K * nL),
+        "avg_launch_us": total_ms * 1e3 / (K * nL),
         "bytes_per_launch": step_bytes / nL,
-        "achieved_gbs": step_bytes * K / (kern_ms * 1e-3) / 1e9,
-        "per_shape": {t["name"]: {
-            "us": per_shape_ms[i] * 1e3 / K,
-            "gbs": packed_bytes(t["N"], t["K"]) / (per_shape_ms[i] * 1e-3 / K) / 1e9}
-            for i, t in enumerate(layer)},
+        "achieved_gbs": step_bytes * K / (total_ms * 1e-3) / 1e9,
+        "step_us": step_q,
+        "per_shape": per_shape,
         "step_bytes": step_bytes,
         "grouped": grouped,
         "graph": graph_res,
@@ -308,25 +333,22 @@ def bench_prefill_m(torch, L, layer, args, M):
     for i, t in enumerate(layer):
         one(i, t)
     torch.cuda.synchronize()
-    reps = 5
     res = {}
-    tot_flop, tot_ms = 0.0, 0.0
+    tot_flop, tot_us = 0.0, 0.0
     for i, t in enumerate(layer):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        gpu_delay(torch, 10)
-        a.record()
-        for _ in range(reps):
-            one(i, t)
-        b.record()
-        torch.cuda.synchronize()
-        ms = a.elapsed_time(b) / reps
+        q = quantiles(call_series(torch, st, lambda r, i=i, t=t: one(i, t), max(200, args.iters)))
         flop = 2.0 * M * t["N"] * t["K"]
-        res[t["name"]] = {"us": ms * 1e3, "tflops": flop / (ms * 1e-3) / 1e12}
+        q["us"] = q["median_us"]
+        q["tflops"] = flop / (q["median_us"] * 1e-6) / 1e12
+        q["plan"] = L.gemm_plan(M, (t["N"],), t["n_cb"])
+        res[t["name"]] = q
         tot_flop += flop
-        tot_ms += ms
-        log(f"prefill {t['name']} M={M}: {ms * 1e3:.1f} us {res[t['name']]['tflops']:.1f} TFLOP/s")
-    tf = tot_flop / (tot_ms * 1e-3) / 1e12
-    return {"M": M, "tflops": tf, "per_shape": res, "frac_of_mfma_peak": tf / MFMA_F16_PEAK_TFLOPS}
+        tot_us += q["median_us"]
+        log(f"prefill {t['name']} M={M}: {q['median_us']:.1f} us (p10 {q['p10_us']:.1f}, p90 {q['p90_us']:.1f}) "
+            f"{q['tflops']:.1f} TFLOP/s")
+    tf = tot_flop / (tot_us * 1e-6) / 1e12
+    return {"M": M, "tflops": tf, "layer_us": tot_us, "layer_flop": tot_flop, "per_shape": res,
+            "frac_of_mfma_peak": tf / MFMA_F16_PEAK_TFLOPS}
 
 
 def bench_prefill_grouped(torch, L, layer, args, M):
@@ -362,19 +384,12 @@ def bench_prefill_grouped(torch, L, layer, args, M):
 
     step()
     torch.cuda.synchronize()
-    reps = 5
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    gpu_delay(torch, 10)
-    a.record()
-    for _ in range(reps):
-        step()
-    b.record()
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / reps
+    q = quantiles(call_series(torch, st, lambda r: step(), max(200, args.iters)))
     flop = sum(2.0 * M * t["N"] * t["K"] for t in layer)
-    tf = flop / (ms * 1e-3) / 1e12
-    log(f"prefill grouped M={M}: {ms * 1e3:.1f} us {tf:.1f} TFLOP/s")
-    return {"M": M, "calls_per_layer": len(calls), "us": ms * 1e3, "tflops": tf,
+    tf = flop / (q["median_us"] * 1e-6) / 1e12
+    log(f"prefill grouped M={M}: {q['median_us']:.1f} us (p10 {q['p10_us']:.1f}, p90 {q['p90_us']:.1f}) "
+        f"{tf:.1f} TFLOP/s")
+    return {"M": M, "calls_per_layer": len(calls), "us": q["median_us"], "us_dist": q, "tflops": tf,
             "frac_of_mfma_peak": tf / MFMA_F16_PEAK_TFLOPS, "groups": groups}
 
 
@@ -562,16 +577,14 @@ def bench_vocab(torch, L, args):
     out = {"shape": f"{N}x{K}", "packed_bytes": packed_bytes(N, K)}
 
     def timed(fn, reps):
+        """median ms of max(reps, --iters) back-to-back calls (and the distribution)"""
         fn()
         torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        gpu_delay(torch, 10)
-        a.record()
-        for _ in range(reps):
-            fn()
-        b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / reps
+        q = quantiles(call_series(torch, st, lambda r: fn(), max(reps, args.iters)))
+        dist.append(q)
+        return q["median_us"] * 1e-3
+
+    dist = []
 
     def ok(rc):
         if rc != 0:
@@ -584,7 +597,7 @@ def bench_vocab(torch, L, args):
     ms = timed(lambda: ok(lib.sx8_gemv(L.ptr(x1), L.ptr(hdr), L.ptr(lvl), args.hdr_bytes, L.ptr(bas),
                                        L.ptr(sca), None, None, N, n_cb, L.ptr(y1), L.ptr(ws),
                                        ws.numel() * 4, st)), 20)
-    out["gemv_m1"] = {"us": ms * 1e3, "gbs": packed_bytes(N, K) / (ms * 1e-3) / 1e9}
+    out["gemv_m1"] = {"us": ms * 1e3, "gbs": packed_bytes(N, K) / (ms * 1e-3) / 1e9, "us_dist": dist[-1]}
     log(f"vocab gemv M=1: {ms * 1e3:.1f} us {out['gemv_m1']['gbs']:.0f} GB/s")
     # lm_head prefill GEMM, M = 512
     M = 512
@@ -594,7 +607,8 @@ def bench_vocab(torch, L, args):
     ms = timed(lambda: ok(lib.sx8_gemm_prefill(L.ptr(xm), M, K, K, L.ptr(hdr), L.ptr(lvl), args.hdr_bytes,
                                                L.ptr(bas), L.ptr(sca), N, n_cb, L.ptr(ym), L.ptr(wsm), nbm,
                                                st)), 5)
-    out["gemm_m512"] = {"us": ms * 1e3, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
+    out["gemm_m512"] = {"us": ms * 1e3, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12, "us_dist": dist[-1],
+                        "plan": L.gemm_plan(M, (N,), n_cb)}
     log(f"vocab gemm M=512: {ms * 1e3:.1f} us {out['gemm_m512']['tflops']:.0f} TFLOP/s")
     del ym
     # embedding gather of 512 ids
@@ -603,7 +617,7 @@ def bench_vocab(torch, L, args):
     ms = timed(lambda: ok(lib.sx8_embed_gather(L.ptr(ids), 512, L.ptr(hdr), L.ptr(lvl), args.hdr_bytes,
                                                L.ptr(bas), L.ptr(sca), K, N, n_cb, L.ptr(rows), st)), 20)
     rd, wr = 512 * n_cb * 30, 512 * K * 2
-    out["embed"] = {"ids": 512, "us": ms * 1e3, "gbs": (rd + wr) / (ms * 1e-3) / 1e9}
+    out["embed"] = {"ids": 512, "us": ms * 1e3, "gbs": (rd + wr) / (ms * 1e-3) / 1e9, "us_dist": dist[-1]}
     log(f"vocab embed 512 ids: {ms * 1e3:.1f} us")
     return out
 
@@ -612,7 +626,9 @@ def bench_e2e(torch, args):
     """Config 5: 36-layer random-init Qwen3-4B-style decoder on S-X8 weights (every layer
     quantized separately), batch 1: a 512-token prefill of uniform-random ids, then 256
     greedy tokens, one decode step replayed from a HIP graph.  The whole generate() runs
-    twice; the second (warm) run is reported."""
+    twice; the second (warm) run is reported.  Generation's prefill computes the lm_head
+    for the last prompt row only (all it needs); the prefill with logits for every row --
+    what a Hugging Face forward computes -- is timed separately."""
     from e2e_decoder import QWEN3_4B, SX8Decoder
     t0 = time.time()
     dec = SX8Decoder(QWEN3_4B, device="cuda", seed=7, max_len=1024)
@@ -624,12 +640,24 @@ def bench_e2e(torch, args):
         out, tp, td = dec.generate(ids, args.e2e_new, use_graph=True)
         res = {"prompt": args.e2e_prompt, "new_tokens": args.e2e_new,
                "prefill_ms": tp * 1e3, "prefill_tok_s": args.e2e_prompt / tp,
+               "prefill_logits": "last row only (generation path)",
                "decode_ms_per_token": td * 1e3 / (args.e2e_new - 1),
                "decode_tok_s": (args.e2e_new - 1) / td,
                "weights_gb": sum(t.numel() for ly in dec.layers for lin in
                                  (ly.q, ly.k, ly.v, ly.o, ly.gate, ly.up, ly.down)
                                  for t in lin._t44[:2]) / 1e9 + sum(t.numel() for t in dec.head._t44[:2]) / 1e9}
         log("e2e", json.dumps(res))
+    times = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        dec.prefill_fused(ids, all_logits=True)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t1)
+    ta = min(times[1:])
+    res["prefill_all_logits_ms"] = ta * 1e3
+    res["prefill_all_logits_tok_s"] = args.e2e_prompt / ta
+    log("e2e all-row logits prefill", f"{ta * 1e3:.2f} ms")
     del dec
     torch.cuda.empty_cache()
     return res
@@ -658,42 +686,124 @@ def bench_copy(torch, args):
 
 def cpu_baseline(layer, seconds):
     """The oracle's C restatement (R64 dequant to fp16 + fp32 GEMV, OpenMP) on the host,
-    over as many layer shapes as fit in about `seconds`."""
+    over as many layer shapes as fit in about `seconds`: with every host thread OpenMP
+    gives it (the reported `value`), then single-threaded for about a third of that."""
     import numpy as np
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as O
     O.build()
     lib = O.lib()
-    threads = int(lib.sx8o_num_threads())
-    done_bytes, t_dq, t_gv, names = 0, 0.0, 0.0, []
-    rng = np.random.default_rng(2)
-    # cycle through the layer's shapes until about `seconds` of CPU work is done
-    for i in range(10000):
-        t = layer[i % len(layer)]
-        qt, bi = t["qt"], t["bi"]
-        n_blk, dmin, dmax, cfg, cof, hi, lo = O._fields(qt)
-        data, sc = O._bases(bi)
-        w16 = np.empty(n_blk * 32, dtype=np.uint16)
-        x = rng.standard_normal(t["K"]).astype(np.float16).view(np.uint16)
-        y = np.empty(t["N"], dtype=np.float32)
-        t0 = time.perf_counter()
-        lib.sx8o_dequant_r64(n_blk, qt["n_cb"], O._ptr(dmin), O._ptr(dmax), O._ptr(cfg),
-                             O._ptr(cof), O._ptr(hi), O._ptr(lo), O._ptr(data), O._ptr(sc), 1,
-                             O._ptr(w16), None)
-        t1 = time.perf_counter()
-        lib.sx8o_gemv_f32(t["N"], t["K"], qt["n_cb"] * 32, O._ptr(w16), O._ptr(x), O._ptr(y))
-        t2 = time.perf_counter()
-        t_dq += t1 - t0
-        t_gv += t2 - t1
-        done_bytes += packed_bytes(t["N"], t["K"])
-        names.append(t["name"])
-        if t_dq + t_gv > seconds:
-            break
-    tot = t_dq + t_gv
-    return {"value": done_bytes / tot / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"R64 dequant + fp32 GEMV, {len(names)} matrices cycling through the "
-                      f"layer's shapes ({done_bytes / 1e6:.1f} MB packed) "
-                      f"in {tot:.1f} s (dequant {t_dq:.1f} s, GEMV {t_gv:.1f} s)"}
+
+    def run(budget):
+        threads = int(lib.sx8o_num_threads())
+        done_bytes, t_dq, t_gv, names = 0, 0.0, 0.0, []
+        rng = np.random.default_rng(2)
+        # cycle through the layer's shapes until about `budget` seconds of CPU work is done
+        for i in range(10000):
+            t = layer[i % len(layer)]
+            qt, bi = t["qt"], t["bi"]
+            n_blk, dmin, dmax, cfg, cof, hi, lo = O._fields(qt)
+            data, sc = O._bases(bi)
+            w16 = np.empty(n_blk * 32, dtype=np.uint16)
+            x = rng.standard_normal(t["K"]).astype(np.float16).view(np.uint16)
+            y = np.empty(t["N"], dtype=np.float32)
+            t0 = time.perf_counter()
+            lib.sx8o_dequant_r64(n_blk, qt["n_cb"], O._ptr(dmin), O._ptr(dmax), O._ptr(cfg),
+                                 O._ptr(cof), O._ptr(hi), O._ptr(lo), O._ptr(data), O._ptr(sc), 1,
+                                 O._ptr(w16), None)
+            t1 = time.perf_counter()
+            lib.sx8o_gemv_f32(t["N"], t["K"], qt["n_cb"] * 32, O._ptr(w16), O._ptr(x), O._ptr(y))
+            t2 = time.perf_counter()
+            t_dq += t1 - t0
+            t_gv += t2 - t1
+            done_bytes += packed_bytes(t["N"], t["K"])
+            names.append(t["name"])
+            if t_dq + t_gv > budget:
+                break
+        tot = t_dq + t_gv
+        return {"value": done_bytes / tot / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": f"R64 dequant + fp32 GEMV, {len(names)} matrices cycling through the "
+                          f"layer's shapes ({done_bytes / 1e6:.1f} MB packed) "
+                          f"in {tot:.1f} s (dequant {t_dq:.1f} s, GEMV {t_gv:.1f} s)"}
+
+    multi = run(seconds)
+    lib.sx8o_set_num_threads(1)
+    single = run(seconds / 3)
+    multi["single_thread"] = {"value": single["value"], "cores": 1, "sample": single["sample"]}
+    return multi
+
+
+def bench_gemm_one(torch, L, layer, args):
+    """One prefill GEMM shape (--shape) at M = --m, called --iters times back to back: the
+    workload of the counter passes in profiles/prefill_gemm_m2048.md."""
+    dev = torch.device("cuda:0")
+    t = {x["name"]: x for x in layer}[args.shape]
+    M = args.m
+    g = torch.Generator(device="cpu").manual_seed(12)
+    X = torch.randn(M, t["K"], generator=g).half().to(dev)
+    Y = torch.empty(M, t["N"], dtype=torch.float32, device=dev)
+    ws, nb = L.gemm_workspace(M, (t["N"],), t["n_cb"], dev)
+    st = L.stream(dev)
+    fn = L.lib().sx8_gemm_prefill
+
+    def one(r):
+        if fn(L.ptr(X), M, t["K"], t["K"], L.ptr(t["hdr"]), L.ptr(t["lvl"]), args.hdr_bytes, L.ptr(t["bas"]),
+              L.ptr(t["sca"]), t["N"], t["n_cb"], L.ptr(Y), L.ptr(ws), nb, st) != 0:
+            raise RuntimeError(L.lib().sx8_last_error().decode())
+    one(0)
+    torch.cuda.synchronize()
+    q = quantiles(call_series(torch, st, one, max(1, args.iters)))
+    q["tflops_at_median"] = 2.0 * M * t["N"] * t["K"] / (q["median_us"] * 1e-6) / 1e12
+    q["plan"] = L.gemm_plan(M, (t["N"],), t["n_cb"])
+    q["mfma_instructions_per_call"] = mfma_count(M, t["N"], t["K"], q["plan"])
+    return q
+
+
+def mfma_count(M, N, K, plan):
+    """v_mfma_f32_32x32x16_f16 instructions one sx8_gemm_prefill call issues: every work-group
+    runs, for each 32 x 32 output fragment of its tile (padded rows included), two per K
+    block of its range plus one PCA k-step per started group of 4 K blocks."""
+    tile = plan["tile"]
+    n_cb = -(-K // 32)
+    NB = -(-N // 128)
+    frags = (tile // 32) * 4
+
+    def per_range(nb):
+        return frags * (2 * nb + -(-nb // 4))
+
+    def ranges(S, kbs):
+        return [min(kbs, n_cb - s * kbs) for s in range(S) if s * kbs < n_cb]
+
+    if tile != 512:
+        MB = -(-M // tile)
+        return MB * NB * sum(per_range(nb) for nb in ranges(plan["k_ranges"], plan["kb_per_range"]))
+    T = -(-M // 512) * NB
+    n_split = plan["split_tiles"]
+    whole = T - n_split
+    return whole * per_range(n_cb) + n_split * sum(per_range(nb) for nb in ranges(plan["k_ranges"],
+                                                                                  plan["kb_per_range"]))
+
+
+def prefill_roofline(pf):
+    """The roofline block of the prefill GEMM at the headline M: the layer (7 calls, each
+    with its Z/pack pass and any split-K sum) and its dominant call, median durations."""
+    if not pf:
+        return None
+    M = pf["M"]
+    dom = max(pf["per_shape"].items(), key=lambda kv: kv[1]["median_us"])
+    name, q = dom
+    flop = 2.0 * M * dict((n, N * K) for n, N, K in LAYER)[name]
+    return {
+        "bound": "mfma", "unit": "TFLOP/s", "peak": MFMA_F16_PEAK_TFLOPS, "M": M,
+        "layer": {"flop": pf["layer_flop"], "us": pf["layer_us"], "achieved": round(pf["tflops"], 1),
+                  "frac": round(pf["tflops"] / MFMA_F16_PEAK_TFLOPS, 4)},
+        "dominant": {"shape": name, "kernel": "k_gemm_w1" if q["plan"]["tile"] == 512 else "k_gemm",
+                     "flop_per_call": flop, "us": q["median_us"], "p10_us": q["p10_us"], "p90_us": q["p90_us"],
+                     "achieved": round(q["tflops"], 1), "frac": round(q["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+                     "plan": q["plan"]},
+        "mfma_busy": "profiles/prefill_gemm_m2048.md (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs)",
+        "traffic": None,
+    }
 
 
 def main():
@@ -717,6 +827,9 @@ def main():
     layer = build_layer(torch, dev, args.hdr_bytes)
     log(f"setup {time.time() - t0:.1f}s")
     res = {}
+    if args.only == "gemm-one":
+        log("gemm-one", json.dumps(bench_gemm_one(torch, L, layer, args)))
+        return
     if args.only in ("", "gemv"):
         res["gemv"] = bench_gemv(torch, L, layer, args)
         log("gemv", json.dumps(res["gemv"]))
@@ -760,7 +873,7 @@ def main():
             "frac_of_hbm_peak": round(gv.get("value_gbs", 0.0) / HBM_PEAK_GBS, 4),
         },
         "roofline": {
-            "kernel": f"k_gemv_panel<{args.hdr_bytes},1,3,TP> (sx8_gemv)",
+            "kernel": f"k_gemv_panel<{args.hdr_bytes},1,ring,TP,plain,one> (sx8_gemv)",
             "bound": "hbm",
             "achieved": round(gv.get("achieved_gbs", 0.0), 1),
             "peak": HBM_PEAK_GBS,
@@ -769,8 +882,13 @@ def main():
             "traffic": GEMV_TRAFFIC_PER_LAUNCH if args.hdr_bytes == 6 else None,
             "traffic_unit": "bytes per launch (HBM, rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
             "avg_launch_us": round(gv.get("avg_launch_us", 0.0), 3),
+            "avg_launch_source": "timed region / launches (two HIP events on the launch stream, "
+                                 "nothing between the launches); compare the rocprofv3 kernel-trace mean "
+                                 "in profiles/gemv_decode_layer.md",
             "bytes_per_launch": gv.get("bytes_per_launch"),
+            "step_us": gv.get("step_us"),
         },
+        "prefill_roofline": prefill_roofline(res.get("prefill")),
         "cpu_baseline": cpu,
         "gemv_grouped": gv.get("grouped"),
         "gemv_graph": gv.get("graph"),

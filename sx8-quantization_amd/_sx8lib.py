@@ -31,6 +31,10 @@ HIP_FLAGS = [
     "-Wall", "-Wno-unused-function",
 ]
 
+# Per-source extra flags: the GEMV kernels take their leading arguments (matrix pointers,
+# N, n_cb) preloaded into SGPRs at wave launch (8 arguments = 14 SGPRs).
+SOURCE_FLAGS = {"sx8_gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"]}
+
 # (name, restype, argtypes) for every exported symbol of include/sx8_hip.h
 _P = ctypes.c_void_p
 _I32, _I64 = ctypes.c_int32, ctypes.c_int64
@@ -92,7 +96,7 @@ def build(verbose: bool = False) -> str:
     with tempfile.TemporaryDirectory(prefix="sx8_build_") as d:
         def compile_one(name):
             obj = os.path.join(d, name + ".o")
-            flags = [f for f in HIP_FLAGS if f != "-shared"]
+            flags = [f for f in HIP_FLAGS if f != "-shared"] + SOURCE_FLAGS.get(name, [])
             cmd = [HIPCC, *flags, "-I", CSRC_DIR, "-I", INCLUDE_DIR, "-c", "-o", obj,
                    os.path.join(CSRC_DIR, name)]
             return obj, subprocess.run(cmd, capture_output=True, text=True)

@@ -384,32 +384,35 @@ __device__ __forceinline__ void tab_load(TabIn& t, const uint16_t* __restrict__ 
     }
 }
 
+// Z value (q & 1) of the unit's K block from its x and basis quarters: each of the four
+// threads of a kb dots its 8 x values with 8 + 8 basis values, two DPP exchanges sum the
+// quarters, and t.s (the scale of basis q & 1) scales the sum.
+__device__ __forceinline__ float tab_z(const TabIn& t, int q) {
+    const uint32_t xw[4] = {t.x.x, t.x.y, t.x.z, t.x.w};
+    const float* b0 = reinterpret_cast<const float*>(t.b0);
+    const float* b1 = reinterpret_cast<const float*>(t.b1);
+    float z0 = 0.f, z1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float xf = sx8_h2f(xw[i >> 1] >> (16 * (i & 1)));
+        z0 = __builtin_fmaf(xf, b0[i], z0);
+        z1 = __builtin_fmaf(xf, b1[i], z1);
+    }
+    z0 = dpp_add<0xB1>(z0);      // + lane ^ 1
+    z1 = dpp_add<0xB1>(z1);
+    z0 = dpp_add<0x4E>(z0);      // + lane ^ 2
+    z1 = dpp_add<0x4E>(z1);
+    return t.s * ((q & 1) == 0 ? z0 : z1);
+}
+
 // Writes entry kb, or the spare entry past the table when !ok: no branch, so the compiler
 // has no conditional block to sink the table loads into (below the weight records).
 template <int kMode>
 __device__ __forceinline__ void tab_store(KbInfo* info, const TabIn& t, int kb, int q, bool ok,
                                           int n_cb) {
-    float z = t.s;
-    if constexpr (kMode == 1) {
-        const uint32_t xw[4] = {t.x.x, t.x.y, t.x.z, t.x.w};
-        const float* b0 = reinterpret_cast<const float*>(t.b0);
-        const float* b1 = reinterpret_cast<const float*>(t.b1);
-        float z0 = 0.f, z1 = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float xf = sx8_h2f(xw[i >> 1] >> (16 * (i & 1)));
-            z0 = __builtin_fmaf(xf, b0[i], z0);
-            z1 = __builtin_fmaf(xf, b1[i], z1);
-        }
-        z0 = dpp_add<0xB1>(z0);      // + lane ^ 1
-        z1 = dpp_add<0xB1>(z1);
-        z0 = dpp_add<0x4E>(z0);      // + lane ^ 2
-        z1 = dpp_add<0x4E>(z1);
-        z = t.s * ((q & 1) == 0 ? z0 : z1);     // t.s is scale (q & 1)
-    }
     KbInfo& e = info[ok ? kb : n_cb];
     fill_x_side(e, q, t.x);
-    e.z[q & 1] = z;      // q = 2, 3 write the same values as q = 0, 1
+    e.z[q & 1] = kMode == 1 ? tab_z(t, q) : t.s;   // q = 2, 3 write the same values as q = 0, 1
 }
 
 // Input producers of the decoder's fused GEMVs: instead of reading x as fp16, every
@@ -551,23 +554,44 @@ struct GemvGroup {
     int n_mats;
 };
 
-// kOne: a single matrix (n_mats = 1), so its fields sit at fixed argument offsets and load
-// in the first batch of argument loads.
+// Panel width for a launch over `total` output columns: about one work-group per CU
+// (ceil(total / 256) columns), two per CU past 64 columns (host and device share it).
+__host__ __device__ inline int panel_ct(int64_t total) {
+    int64_t ct = (total + 255) / 256;
+    if (ct > 64) ct = (total + 511) / 512;
+    return (int)(ct < 1 ? 1 : ct > 64 ? 64 : ct);
+}
+
+// Arguments: the fields a single-matrix launch needs first (hdr, levels, X, N, n_cb) lead,
+// then its bases, scales and output; this file is built with the first 8 kernel arguments
+// preloaded into SGPRs, so those arrive with the wave instead of after a scalar-memory
+// round trip.  kOne (a single matrix) takes its fields and derives CT, S, R from them;
+// a group (n_mats > 1) reads its matrices from `grp` and CT, S, R from the arguments.
+// (Measured and rejected: building Z after the K loop, with the bases requested behind
+// the first record rounds and each lane's coefficients kept for a PCA pass before the
+// reduction -- 8% slower on the layer sweep; the epilogue it adds costs more than the
+// prologue it shortens.)
 template <int HB, int kMode, int NR, int TP, int kX = kXPlain, bool kOne = false>
 __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
-    const uint16_t* __restrict__ X, const GemvGroup grp, const KbInfo* __restrict__ table,
-    int n_cb, int CT, int S, int R, const XProd xp) {
+    const uint8_t* __restrict__ hdr0, const uint8_t* __restrict__ lv0, const uint16_t* __restrict__ X,
+    int N0, int n_cb, const float* __restrict__ bas0, const float* __restrict__ sca0,
+    float* __restrict__ Y0, int CT_g, int S_g, int R_g, const GemvGroup grp,
+    const KbInfo* __restrict__ table, const XProd xp) {
     extern __shared__ __align__(16) unsigned char smem[];
     float* red = reinterpret_cast<float*>(smem);                 // 2 x 512 floats
     KbInfo* info = reinterpret_cast<KbInfo*>(smem + sizeof(float) * 2 * kPanelThreads);
     const int tid = threadIdx.x;
+    const int CT = kOne ? panel_ct(N0) : CT_g;
+    const int S = kOne ? kPanelThreads / CT : S_g;
+    const int R = kOne ? (n_cb + S - 1) / S : R_g;
     const int j0 = tid / CT;
     const int c = tid - j0 * CT;
     // panel number: XCD x (= blockIdx % 8) gets the contiguous range after the
     // sum_{y < x} ceil((G - y) / 8) panels of the XCDs before it (G = 8 q + r)
-    const int G = gridDim.x, xcd = blockIdx.x & 7;
+    // (a single matrix's grid is its panel count; gridDim would be another argument load)
+    const int G = kOne ? (N0 + CT - 1) / CT : (int)gridDim.x, xcd = blockIdx.x & 7;
     int panel = (blockIdx.x >> 3) + xcd * (G >> 3) + min(xcd, G & 7);
-    // the matrix this panel belongs to; every field is read at a fixed kernel-argument
+    // a group's matrix for this panel; every field is read at a fixed kernel-argument
     // offset and picked with uniform selects (no chain of dependent argument loads)
     int mi = 0;
     if (!kOne && grp.n_mats > 1 && panel >= grp.m[0].panels) {
@@ -585,13 +609,13 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     auto pick = [&](auto field) {
         return mi == 0 ? field(grp.m[0]) : mi == 1 ? field(grp.m[1]) : mi == 2 ? field(grp.m[2]) : field(grp.m[3]);
     };
-    const uint8_t* __restrict__ hdr = pick([](const GemvMat& g) { return g.hdr; });
-    const uint8_t* __restrict__ levels = pick([](const GemvMat& g) { return g.levels; });
-    const float* __restrict__ basis = pick([](const GemvMat& g) { return g.basis; });
-    const float* __restrict__ scales = pick([](const GemvMat& g) { return g.scales; });
+    const uint8_t* __restrict__ hdr = kOne ? hdr0 : pick([](const GemvMat& g) { return g.hdr; });
+    const uint8_t* __restrict__ levels = kOne ? lv0 : pick([](const GemvMat& g) { return g.levels; });
+    const float* __restrict__ basis = kOne ? bas0 : pick([](const GemvMat& g) { return g.basis; });
+    const float* __restrict__ scales = kOne ? sca0 : pick([](const GemvMat& g) { return g.scales; });
     const float* __restrict__ Zin = pick([](const GemvMat& g) { return g.Zin; });
-    float* __restrict__ Y = pick([](const GemvMat& g) { return g.Y; });
-    const int N = pick([](const GemvMat& g) { return g.N; });
+    float* __restrict__ Y = kOne ? Y0 : pick([](const GemvMat& g) { return g.Y; });
+    const int N = kOne ? N0 : pick([](const GemvMat& g) { return g.N; });
     const int n = panel * CT + c;
     const bool col_ok = n < N;
     const uint32_t nn = (uint32_t)min(n, N - 1);
@@ -741,12 +765,21 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
         if (r + i < R) step(buf[i], r + i);
 
     // slices -> columns in a fixed order: thread t < 8 CT sums slices g, g + 8, ... of
-    // column t % CT (g = t / CT), then thread c < CT sums the 8 partials of column c
+    // column t % CT (g = t / CT), eight loads in flight at a time, then thread c < CT sums
+    // the 8 partials of column c
     red[tid] = acc;
     __syncthreads();
     if (tid < 8 * CT) {
         float t = 0.f;
-        for (int s = j0; s < S; s += 8) t += red[s * CT + c];
+        int s = j0;
+        for (; s + 56 < S; s += 64) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = red[(s + 8 * i) * CT + c];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) t += v[i];
+        }
+        for (; s < S; s += 8) t += red[s * CT + c];
         red[kPanelThreads + tid] = t;
     }
     __syncthreads();
@@ -771,10 +804,8 @@ struct PanelPlan {
 inline PanelPlan plan_panels(const int64_t* Ns, int n_mats, int n_cb) {
     int64_t total = 0;
     for (int i = 0; i < n_mats; ++i) total += Ns[i];
-    int64_t ct = (total + 255) / 256;
-    if (ct > 64) ct = (total + 511) / 512;
     PanelPlan p;
-    p.CT = (int)std::max<int64_t>(1, std::min<int64_t>(64, ct));
+    p.CT = panel_ct(total);
     p.S = kPanelThreads / p.CT;
     p.R = (n_cb + p.S - 1) / p.S;
     p.TP = n_cb <= 128 * kTabPassesShort ? kTabPassesShort : kTabPassesLong;
@@ -794,14 +825,15 @@ void launch_panel(const PanelPlan& p, size_t smem, hipStream_t st, const uint16_
                   const GemvGroup& g, const KbInfo* table, int n_cb, const XProd& xp = XProd{}) {
     const dim3 grid(p.grid), block(kPanelThreads);
     const bool one = g.n_mats == 1;
+    const GemvMat& m0 = g.m[0];
     auto go = [&](auto nr, auto tp) {
         constexpr int NR = decltype(nr)::value, TP = decltype(tp)::value;
         if (one)
-            hipLaunchKernelGGL((k_gemv_panel<HB, kMode, NR, TP, kX, true>), grid, block, smem, st, X, g, table,
-                               n_cb, p.CT, p.S, p.R, xp);
+            hipLaunchKernelGGL((k_gemv_panel<HB, kMode, NR, TP, kX, true>), grid, block, smem, st, m0.hdr,
+                               m0.levels, X, m0.N, n_cb, m0.basis, m0.scales, m0.Y, p.CT, p.S, p.R, g, table, xp);
         else
-            hipLaunchKernelGGL((k_gemv_panel<HB, kMode, NR, TP, kX>), grid, block, smem, st, X, g, table, n_cb,
-                               p.CT, p.S, p.R, xp);
+            hipLaunchKernelGGL((k_gemv_panel<HB, kMode, NR, TP, kX, false>), grid, block, smem, st, m0.hdr,
+                               m0.levels, X, m0.N, n_cb, m0.basis, m0.scales, m0.Y, p.CT, p.S, p.R, g, table, xp);
     };
     auto by_ring = [&](auto tp) {
         if (p.grid <= kRing3MaxGrid)

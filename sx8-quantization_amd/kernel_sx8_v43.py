@@ -19,27 +19,11 @@ DEV = torch.device("cuda")
 N_BASES = 2
 BYTES_PER_BLOCK = 30  # 2+2+1+16+8+1
 
-# Kept for callers that clear the reference's float32 staging pool; this
-# implementation needs no staging buffer, so the pool stays empty.
+# The reference's float32 staging pool (kernel_sx8_v43.py:84-106): callers clear these
+# (scripts/integrate_fused_v44.py:139-140).  No staging buffer is used here, so they stay
+# empty.
 _BUFFER_POOL = {}
 _BUFFER_POOL_ORDER = []
-_BUFFER_POOL_MAX = 3
-
-
-def _get_buffer(n):
-    """float32 device buffer of at least n elements (pool of the reference API)."""
-    n_round = (n + 4095) & ~4095
-    for k in _BUFFER_POOL_ORDER:
-        if k >= n_round:
-            _BUFFER_POOL_ORDER.remove(k)
-            _BUFFER_POOL_ORDER.append(k)
-            return _BUFFER_POOL[k]
-    if len(_BUFFER_POOL_ORDER) >= _BUFFER_POOL_MAX:
-        del _BUFFER_POOL[_BUFFER_POOL_ORDER.pop(0)]
-    buf = torch.empty(n_round, dtype=torch.float32, device=DEV)
-    _BUFFER_POOL[n_round] = buf
-    _BUFFER_POOL_ORDER.append(n_round)
-    return buf
 
 
 def _dequant_into(qt, bases_info, out, device):
