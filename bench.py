@@ -38,7 +38,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
 # HBM bytes per k_gemv_panel launch on this workload (hdr_bytes=6), measured with two
 # rocprofv3 passes (FETCH_SIZE, WRITE_SIZE) scaled by what the counters read for a 512 MiB
 # copy (fetch x2.000, write x1.000); passes and calibration: profiles/gemv_decode_layer.md
-GEMV_TRAFFIC_PER_LAUNCH = 13.96e6
+GEMV_TRAFFIC_PER_LAUNCH = 13.98e6
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, vendor figure
 
 
