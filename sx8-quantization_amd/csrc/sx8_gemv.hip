@@ -366,14 +366,34 @@ struct TabIn {
     float s;
 };
 
+// Global-memory views: a pointer that went through an SGPR pin (see k_gemv_panel) is a
+// generic pointer to the compiler, whose loads would be flat loads (counted on the LDS /
+// scalar counter as well, so any wait for a scalar load would also wait for them).
+// (The attribute applies to the device pass only; the host pass parses these bodies but
+// never emits them.)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define SX8_GLOBAL_AS __attribute__((address_space(1)))
+#else
+#define SX8_GLOBAL_AS
+#endif
+typedef const float4 SX8_GLOBAL_AS g_float4;
+typedef const uint4 SX8_GLOBAL_AS g_uint4;
+typedef const float SX8_GLOBAL_AS g_float;
+typedef const uint16_t SX8_GLOBAL_AS g_u16;
+
+template <typename T>
+__device__ __forceinline__ const T SX8_GLOBAL_AS* to_global(const T* p) {
+    return (const T SX8_GLOBAL_AS*)p;
+}
+
 template <int kMode, bool kLoadX = true>
-__device__ __forceinline__ void tab_load(TabIn& t, const uint16_t* __restrict__ X,
-                                         const float* __restrict__ basis,
-                                         const float* __restrict__ scales,
-                                         const float* __restrict__ Zin, int kb, int q) {
-    if constexpr (kLoadX) t.x = *reinterpret_cast<const uint4*>(X + (int64_t)kb * 32 + 8 * q);
+__device__ __forceinline__ void tab_load(TabIn& t, const g_u16* __restrict__ X,
+                                         const g_float* __restrict__ basis,
+                                         const g_float* __restrict__ scales,
+                                         const g_float* __restrict__ Zin, int kb, int q) {
+    if constexpr (kLoadX) t.x = *(const g_uint4*)(X + (int64_t)kb * 32 + 8 * q);
     if constexpr (kMode == 1) {
-        const float4* b = reinterpret_cast<const float4*>(basis + (int64_t)kb * 64 + 8 * q);
+        const g_float4* b = (const g_float4*)(basis + (int64_t)kb * 64 + 8 * q);
         t.b0[0] = b[0];
         t.b0[1] = b[1];
         t.b1[0] = b[8];
@@ -575,45 +595,83 @@ template <int HB, int kMode, int NR, int TP, int kX = kXPlain, bool kOne = false
 __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     const uint8_t* __restrict__ hdr0, const uint8_t* __restrict__ lv0, const uint16_t* __restrict__ X,
     int N0, int n_cb, const float* __restrict__ bas0, const float* __restrict__ sca0,
-    float* __restrict__ Y0, int CT_g, int S_g, int R_g, const GemvGroup grp,
+    float* __restrict__ Y0, const GemvGroup grp,
     const KbInfo* __restrict__ table, const XProd xp) {
     extern __shared__ __align__(16) unsigned char smem[];
     float* red = reinterpret_cast<float*>(smem);                 // 2 x 512 floats
     KbInfo* info = reinterpret_cast<KbInfo*>(smem + sizeof(float) * 2 * kPanelThreads);
     const int tid = threadIdx.x;
-    const int CT = kOne ? panel_ct(N0) : CT_g;
-    const int S = kOne ? kPanelThreads / CT : S_g;
-    const int R = kOne ? (n_cb + S - 1) / S : R_g;
-    const int j0 = tid / CT;
-    const int c = tid - j0 * CT;
     // panel number: XCD x (= blockIdx % 8) gets the contiguous range after the
     // sum_{y < x} ceil((G - y) / 8) panels of the XCDs before it (G = 8 q + r)
-    // (a single matrix's grid is its panel count; gridDim would be another argument load)
-    const int G = kOne ? (N0 + CT - 1) / CT : (int)gridDim.x, xcd = blockIdx.x & 7;
-    int panel = (blockIdx.x >> 3) + xcd * (G >> 3) + min(xcd, G & 7);
+    const int xcd = blockIdx.x & 7;
+    auto panel_of = [&](int G) { return (int)(blockIdx.x >> 3) + xcd * (G >> 3) + min(xcd, G & 7); };
     // a group's matrix for this panel; every field is read at a fixed kernel-argument
-    // offset and picked with uniform selects (no chain of dependent argument loads)
-    int mi = 0;
-    if (!kOne && grp.n_mats > 1 && panel >= grp.m[0].panels) {
-        panel -= grp.m[0].panels;
-        mi = 1;
-        if (grp.n_mats > 2 && panel >= grp.m[1].panels) {
-            panel -= grp.m[1].panels;
-            mi = 2;
-            if (grp.n_mats > 3 && panel >= grp.m[2].panels) {
-                panel -= grp.m[2].panels;
-                mi = 3;
-            }
+    // offset and picked with uniform selects, without branches, so the argument loads go
+    // out together (no chain of dependent loads).  A group's grid is its panel count, so
+    // the matrix is known before any division.
+    int panel = 0, mi = 0;
+    if constexpr (!kOne) {
+        panel = panel_of((int)gridDim.x);
+        const int nm = grp.n_mats;
+        const int e0 = grp.m[0].panels, e1 = e0 + grp.m[1].panels, e2 = e1 + grp.m[2].panels;
+        mi = (nm > 1 && panel >= e0) + (nm > 2 && panel >= e1) + (nm > 3 && panel >= e2);
+        panel -= mi == 0 ? 0 : mi == 1 ? e0 : mi == 2 ? e1 : e2;
+    }
+    // field of the group's matrix mi: the four candidates are loaded (pinned in SGPRs, so
+    // the compiler cannot turn the select into a load from a selected address) and picked
+    auto pick = [&](auto field) {
+        auto f0 = field(grp.m[0]), f1 = field(grp.m[1]), f2 = field(grp.m[2]), f3 = field(grp.m[3]);
+        asm volatile("" : "+s"(f0), "+s"(f1), "+s"(f2), "+s"(f3));
+        return mi == 0 ? f0 : mi == 1 ? f1 : mi == 2 ? f2 : f3;
+    };
+    const g_float* __restrict__ basis = to_global(kOne ? bas0 : pick([](const GemvMat& g) { return g.basis; }));
+    const g_float* __restrict__ scales = to_global(kOne ? sca0 : pick([](const GemvMat& g) { return g.scales; }));
+    const g_float* __restrict__ Zin = to_global(
+        kMode != 2 ? nullptr : kOne ? grp.m[0].Zin : pick([](const GemvMat& g) { return g.Zin; }));
+    // (X laundered through an empty asm: a load from the read-only argument itself could be
+    // moved past the ordering point below, behind the divisions)
+    const uint16_t* xa = X;
+    asm volatile("" : "+s"(xa));
+    const g_u16* __restrict__ Xg = to_global(xa);
+
+    // The table inputs go out first, ahead of the panel geometry (integer divisions) and
+    // the weight records: the table build gates the first decode, and its inputs depend
+    // on nothing but the thread index and n_cb (6% on the layer sweep against issuing
+    // them after the geometry).
+    const int n_units = n_cb * 4;
+    TabIn tin[TP];
+    XRaw xr[kX == kXPlain ? 1 : TP];
+    if constexpr (kMode == 1 || kMode == 2) {
+        XRsrc xs;
+        if constexpr (kX != kXPlain) xs = xraw_rsrc<kX>(xp, n_cb * 32);
+#pragma unroll
+        for (int p = 0; p < TP; ++p) {
+            const int u = min(p * kPanelThreads + tid, n_units - 1);
+            tab_load<kMode, kX == kXPlain>(tin[p], Xg, basis, scales, Zin, u >> 2, u & 3);
+            if constexpr (kX != kXPlain) xraw_load<kX>(xr[p], xs, u >> 2, u & 3);
         }
     }
-    auto pick = [&](auto field) {
-        return mi == 0 ? field(grp.m[0]) : mi == 1 ? field(grp.m[1]) : mi == 2 ? field(grp.m[2]) : field(grp.m[3]);
-    };
+    // issue order = wait order (the memory counter retires loads in order): table
+    // inputs, then round 0, 1, ...  (the clobber keeps the compiler from sinking a
+    // table load below the geometry or the record loads, which would make the table
+    // wait for them)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+
+    // panel geometry from the launch's total width (the host's plan_panels does the same);
+    // the width passes through an empty asm so that the divisions below cannot be hoisted
+    // above the table loads
+    int64_t width = kOne ? (int64_t)N0 : (int64_t)grp.m[0].N + grp.m[1].N + grp.m[2].N + grp.m[3].N;
+    asm volatile("" : "+s"(width));
+    const int CT = panel_ct(width);
+    const int S = kPanelThreads / CT;
+    const int R = (n_cb + S - 1) / S;
+    const int j0 = tid / CT;
+    const int c = tid - j0 * CT;
+    // a single matrix's grid is its panel count (gridDim would be another argument load)
+    if constexpr (kOne) panel = panel_of((N0 + CT - 1) / CT);
     const uint8_t* __restrict__ hdr = kOne ? hdr0 : pick([](const GemvMat& g) { return g.hdr; });
     const uint8_t* __restrict__ levels = kOne ? lv0 : pick([](const GemvMat& g) { return g.levels; });
-    const float* __restrict__ basis = kOne ? bas0 : pick([](const GemvMat& g) { return g.basis; });
-    const float* __restrict__ scales = kOne ? sca0 : pick([](const GemvMat& g) { return g.scales; });
-    const float* __restrict__ Zin = pick([](const GemvMat& g) { return g.Zin; });
     float* __restrict__ Y = kOne ? Y0 : pick([](const GemvMat& g) { return g.Y; });
     const int N = kOne ? N0 : pick([](const GemvMat& g) { return g.N; });
     const int n = panel * CT + c;
@@ -630,24 +688,6 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     const uint32_t dbid = lane_ok ? (uint32_t)S * (uint32_t)N : 0u;
     auto load = [&](BlockRec& o, int r) { load_rec<HB>(o, rh, rl, bid0 + (uint32_t)r * dbid); };
 
-    const int n_units = n_cb * 4;
-    TabIn tin[TP];
-    XRaw xr[kX == kXPlain ? 1 : TP];
-    if constexpr (kMode == 1 || kMode == 2) {
-        XRsrc xs;
-        if constexpr (kX != kXPlain) xs = xraw_rsrc<kX>(xp, n_cb * 32);
-#pragma unroll
-        for (int p = 0; p < TP; ++p) {
-            const int u = min(p * kPanelThreads + tid, n_units - 1);
-            tab_load<kMode, kX == kXPlain>(tin[p], X, basis, scales, Zin, u >> 2, u & 3);
-            if constexpr (kX != kXPlain) xraw_load<kX>(xr[p], xs, u >> 2, u & 3);
-        }
-    }
-    // issue order = wait order (the memory counter retires loads in order): table
-    // inputs, then round 0, 1, ...  (the clobber keeps the compiler from sinking a
-    // table load below the record loads, which would make the table wait for them)
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
     // the first kNR0 rounds go out before the table build, the rest of the ring after it
     constexpr int kNR0 = NR < 2 ? NR : 2;
     BlockRec buf[NR];
@@ -723,7 +763,7 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
         if constexpr (kX == kXPlain) {
             for (int u0 = TP * kPanelThreads; u0 < n_units; u0 += kPanelThreads) {
                 const int u = min(u0 + tid, n_units - 1);
-                tab_load<kMode>(tin[0], X, basis, scales, Zin, u >> 2, u & 3);
+                tab_load<kMode>(tin[0], Xg, basis, scales, Zin, u >> 2, u & 3);
                 tab_store<kMode>(info, tin[0], u >> 2, u & 3, u0 + tid < n_units, n_cb);
             }
         }
@@ -787,7 +827,7 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
         float t = 0.f;
 #pragma unroll
         for (int g = 0; g < 8; ++g) t += red[kPanelThreads + g * CT + tid];
-        Y[n] = t;
+        *(float SX8_GLOBAL_AS*)(Y + n) = t;
     }
 }
 
@@ -830,10 +870,10 @@ void launch_panel(const PanelPlan& p, size_t smem, hipStream_t st, const uint16_
         constexpr int NR = decltype(nr)::value, TP = decltype(tp)::value;
         if (one)
             hipLaunchKernelGGL((k_gemv_panel<HB, kMode, NR, TP, kX, true>), grid, block, smem, st, m0.hdr,
-                               m0.levels, X, m0.N, n_cb, m0.basis, m0.scales, m0.Y, p.CT, p.S, p.R, g, table, xp);
+                               m0.levels, X, m0.N, n_cb, m0.basis, m0.scales, m0.Y, g, table, xp);
         else
             hipLaunchKernelGGL((k_gemv_panel<HB, kMode, NR, TP, kX, false>), grid, block, smem, st, m0.hdr,
-                               m0.levels, X, m0.N, n_cb, m0.basis, m0.scales, m0.Y, p.CT, p.S, p.R, g, table, xp);
+                               m0.levels, X, m0.N, n_cb, m0.basis, m0.scales, m0.Y, g, table, xp);
     };
     auto by_ring = [&](auto tp) {
         if (p.grid <= kRing3MaxGrid)
