@@ -277,38 +277,81 @@ struct RopeIn {
     float eps;
 };
 
-// RMSNorm over one head row of HD values held 8 per lane by the CH = HD / 8 lanes of a
-// lane group (lane c: dims 8c .. 8c + 7), fp16 rounding, then rotate-half RoPE at row
-// `pos` of the tables: dim d < HD / 2 pairs with d + HD / 2, i.e. lane c with c ^ (CH / 2).
-// Returns the fp16-rounded results (as k_qk_rope_cache stores them) in o.
+// Lane-group helpers.  A lane group is CH = HD / 8 consecutive lanes (16 for HD 128: one
+// DPP row; 8 for HD 64: half a row), lane c holding dims 8c .. 8c + 7 of a head row.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF,
+                                                                 false));
+}
+
+// Sum over the lanes of a lane group, the same value in every lane: DPP quad swaps, then
+// the half-row mirror and (CH = 16) the row mirror -- VALU operations, no LDS round trips.
+template <int CH>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp_f<0xB1>(v);                              // quad_perm [1, 0, 3, 2]
+    v += dpp_f<0x4E>(v);                              // quad_perm [2, 3, 0, 1]
+    v += dpp_f<0x141>(v);                             // row_half_mirror
+    if constexpr (CH == 16) v += dpp_f<0x140>(v);     // row_mirror
+    return v;
+}
+
+// The value of lane c ^ (CH / 2) of the lane group (the RoPE partner of lane c).
+template <int CH>
+__device__ __forceinline__ float group_partner(float v) {
+    if constexpr (CH == 16) return dpp_f<0x128>(v);   // row_ror:8 (= lane ^ 8 within the row)
+    else return __shfl_xor(v, CH / 2, CH);
+}
+
+// One head row's inputs for RMSNorm + RoPE (8 values per lane): the row, the norm weight
+// and the cos / sin entries at the table row, all requested together.
+struct RopeRow {
+    float4 a, b;
+    sx8_u32x4 w;
+    float4 c0, c1, s0, s1;
+};
+
 template <int HD>
-__device__ __forceinline__ void norm_rope8(const float* __restrict__ src, const uint16_t* __restrict__ w,
-                                           const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-                                           int64_t pos, int c, float eps, float o[8]) {
+__device__ __forceinline__ void rope_load(RopeRow& r, const float* __restrict__ src,
+                                          const uint16_t* __restrict__ w, const float* __restrict__ cos_t,
+                                          const float* __restrict__ sin_t, int64_t pos, int c) {
     constexpr int CH = HD / 8, half = HD / 2;
-    const float4 a = *reinterpret_cast<const float4*>(src + 8 * c);
-    const float4 b = *reinterpret_cast<const float4*>(src + 8 * c + 4);
-    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    r.a = *reinterpret_cast<const float4*>(src + 8 * c);
+    r.b = *reinterpret_cast<const float4*>(src + 8 * c + 4);
+    r.w = *reinterpret_cast<const sx8_u32x4*>(w + 8 * c);
+    const int d0 = c < CH / 2 ? 8 * c : 8 * c - half;
+    r.c0 = *reinterpret_cast<const float4*>(cos_t + pos * half + d0);
+    r.c1 = *reinterpret_cast<const float4*>(cos_t + pos * half + d0 + 4);
+    r.s0 = *reinterpret_cast<const float4*>(sin_t + pos * half + d0);
+    r.s1 = *reinterpret_cast<const float4*>(sin_t + pos * half + d0 + 4);
+}
+
+// RMSNorm over the head row (sum of squares over the lane group), fp16 rounding, then
+// rotate-half RoPE: dim d < HD / 2 pairs with d + HD / 2, i.e. lane c with c ^ (CH / 2).
+// The results are fp16-rounded (as the caches and k_qk_rope_cache hold them), packed in
+// pairs: o[e] = (dim 8c + 2e, dim 8c + 2e + 1).
+template <int HD>
+__device__ __forceinline__ void rope_apply(const RopeRow& r, int c, float eps, uint32_t o[4]) {
+    constexpr int CH = HD / 8;
+    const float x[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+    const float cs[8] = {r.c0.x, r.c0.y, r.c0.z, r.c0.w, r.c1.x, r.c1.y, r.c1.z, r.c1.w};
+    const float sn[8] = {r.s0.x, r.s0.y, r.s0.z, r.s0.w, r.s1.x, r.s1.y, r.s1.z, r.s1.w};
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-#pragma unroll
-    for (int m = CH / 2; m > 0; m >>= 1) ss += __shfl_xor(ss, m, CH);
+    ss = group_sum<CH>(ss);
     const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
-    const sx8_u32x4 wv = *reinterpret_cast<const sx8_u32x4*>(w + 8 * c);
-    float nv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-        nv[e] = h2f(f2h(x[e] * inv * h2f((uint16_t)(wv[e >> 1] >> (16 * (e & 1))))));
     const bool lo = c < CH / 2;
-    const int d0 = (lo ? 8 * c : 8 * c - half);
+    float res[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const float other = __shfl_xor(nv[e], CH / 2, CH);
-        const float cs = cos_t[pos * half + d0 + e], sn = sin_t[pos * half + d0 + e];
+        const float nv = h2f(f2h(x[e] * inv * h2f((uint16_t)(r.w[e >> 1] >> (16 * (e & 1))))));
+        const float other = group_partner<CH>(nv);
         // first half: n1 c - n2 s; second half: n2 c + n1 s (own value is n2, partner n1)
-        o[e] = h2f(f2h(lo ? nv[e] * cs - other * sn : nv[e] * cs + other * sn));
+        res[e] = lo ? nv * cs[e] - other * sn[e] : nv * cs[e] + other * sn[e];
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = (uint32_t)f2h(res[2 * e]) | ((uint32_t)f2h(res[2 * e + 1]) << 16);
 }
 
 template <int HD, int G, bool kRope = false>
@@ -321,53 +364,97 @@ __global__ __launch_bounds__(256) void k_attn_split(const uint16_t* __restrict__
     constexpr int CH = HD / 8;
     constexpr int PG = 256 / CH;
     constexpr int kU = 4;
+    // kRope rows by wave: waves 0 .. kQw - 1 the G q rows (one lane group each), wave kQw the
+    // new k row, wave kQw + 1 the new v row -- one pointer per wave, picked with scalar
+    // selects (a per-lane pick of a kernel-argument field becomes a vector load of it)
+    constexpr int kGpw = 64 / CH, kQw = (G + kGpw - 1) / kGpw;
+    static_assert(!kRope || kQw + 2 <= 4, "k_attn_split: waves for the q, k and v rows");
     __shared__ float sm[PG][G], sl[PG][G];
     __shared__ float sacc[PG][G][HD + 4];
+    __shared__ uint32_t rq[kRope ? G : 1][HD / 2], rk[HD / 2], rv[HD / 2];   // RoPE'd rows (fp16 pairs)
     const int kv = blockIdx.x / kAttnChunks, chunk = blockIdx.x % kAttnChunks;
     const int64_t pos = *pos_p;
     const int n = (int)min(max(pos, (int64_t)0) + 1, (int64_t)L);
     const int T = (n + kAttnChunks - 1) / kAttnChunks;
     const int jb = chunk * T, je = min(jb + T, n);
     const int tid = threadIdx.x, c = tid % CH, pg = tid / CH;
-    float qv[G][8];
     // kRope: the new position's row (pos inside the cache and inside this chunk) comes from
-    // registers, not from the cache this launch is writing
+    // LDS, not from the cache this launch is writing
     const bool own_new = kRope && pos >= 0 && pos < L && pos >= jb && pos < je;
+    const int64_t pr = min(max(pos, (int64_t)0), (int64_t)L - 1);   // RoPE table row
+
+    // (1) kRope: the inputs of this lane group's row -- q head kv G + pg in the q waves, the
+    // new k row in wave kQw, the new v row in wave kQw + 1 (every lane group of a wave loads
+    // its row; the idle ones repeat a valid one) -- requested first, without branches (rows
+    // merged from branches would be register copies that wait for their loads)
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    RopeRow rr;
+    if constexpr (kRope) {
+        const float* src = wv < kQw ? ri.q_raw + (int64_t)(kv * G + min(pg, G - 1)) * HD
+                                    : (wv == kQw ? ri.k_raw : ri.v_raw) + (int64_t)kv * HD;
+        rope_load<HD>(rr, src, wv < kQw ? ri.qn : ri.kn, ri.cos_t, ri.sin_t, pr, c);
+    }
+    // (2) then the chunk's first kU K and V rows of this lane group (past the chunk: a valid
+    // row, its score is -inf), behind the row inputs: the memory counter retires loads in
+    // order, so the RoPE math waits only for what was issued before these
+    asm volatile("" ::: "memory");
+    const uint16_t* kc = k_cache + (int64_t)kv * L * HD;
+    const uint16_t* vc = v_cache + (int64_t)kv * L * HD;
+    sx8_u32x4 kr[kU], vr[kU];
+    auto load_rows = [&](int j0) {
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+            kr[u] = *reinterpret_cast<const sx8_u32x4*>(kc + (int64_t)min(j0 + u * PG, je - 1) * HD + 8 * c);
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+            vr[u] = *reinterpret_cast<const sx8_u32x4*>(vc + (int64_t)min(j0 + u * PG, je - 1) * HD + 8 * c);
+    };
+    load_rows(jb + pg);
+    __builtin_amdgcn_sched_barrier(0);       // no RoPE math (which waits for its rows) above here
+
+    // (3) kRope: norm + RoPE of the G q rows and the new k row in parallel (one lane group
+    // each), the new rows into the caches (the chunk holding *pos), all of them into LDS
+    uint32_t qv[G][4];
     sx8_u32x4 knew = sx8_u32x4{0u, 0u, 0u, 0u}, vnew = knew;
     if constexpr (kRope) {
-        const int64_t pr = min(max(pos, (int64_t)0), (int64_t)L - 1);   // table row
+        uint32_t o[4];
+        rope_apply<HD>(rr, c, ri.eps, o);          // every lane group (the v row's result is unused)
+        const bool first = pg == wv * kGpw;       // the first lane group of its wave
+        if (wv < kQw) {
+            if (pg < G)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) rq[pg][4 * c + e] = o[e];
+        } else if (wv == kQw && first && own_new) {
+            const sx8_u32x4 w = sx8_u32x4{o[0], o[1], o[2], o[3]};
+            *reinterpret_cast<sx8_u32x4*>(&rk[4 * c]) = w;
+            *reinterpret_cast<sx8_u32x4*>(ri.k_out + ((int64_t)kv * L + pos) * HD + 8 * c) = w;
+        } else if (wv == kQw + 1 && first && own_new) {
+            const float f[8] = {rr.a.x, rr.a.y, rr.a.z, rr.a.w, rr.b.x, rr.b.y, rr.b.z, rr.b.w};
+            sx8_u32x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = (uint32_t)f2h(f[2 * e]) | ((uint32_t)f2h(f[2 * e + 1]) << 16);
+            *reinterpret_cast<sx8_u32x4*>(&rv[4 * c]) = w;
+            *reinterpret_cast<sx8_u32x4*>(ri.v_out + ((int64_t)kv * L + pos) * HD + 8 * c) = w;
+        }
+        __syncthreads();
 #pragma unroll
         for (int g = 0; g < G; ++g)
-            norm_rope8<HD>(ri.q_raw + (kv * G + g) * HD, ri.qn, ri.cos_t, ri.sin_t, pr, c, ri.eps, qv[g]);
-        if (own_new) {
-            float kf[8];
-            norm_rope8<HD>(ri.k_raw + kv * HD, ri.kn, ri.cos_t, ri.sin_t, pr, c, ri.eps, kf);
-            const float4 va = *reinterpret_cast<const float4*>(ri.v_raw + kv * HD + 8 * c);
-            const float4 vb = *reinterpret_cast<const float4*>(ri.v_raw + kv * HD + 8 * c + 4);
-            const float vf8[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                knew[e] = (uint32_t)f2h(kf[2 * e]) | ((uint32_t)f2h(kf[2 * e + 1]) << 16);
-                vnew[e] = (uint32_t)f2h(vf8[2 * e]) | ((uint32_t)f2h(vf8[2 * e + 1]) << 16);
-            }
-            if (pg == 0) {
-                *reinterpret_cast<sx8_u32x4*>(ri.k_out + ((int64_t)kv * L + pos) * HD + 8 * c) = knew;
-                *reinterpret_cast<sx8_u32x4*>(ri.v_out + ((int64_t)kv * L + pos) * HD + 8 * c) = vnew;
-            }
+            for (int e = 0; e < 4; ++e) qv[g][e] = rq[g][4 * c + e];
+        if (own_new) {
+            knew = *reinterpret_cast<const sx8_u32x4*>(&rk[4 * c]);
+            vnew = *reinterpret_cast<const sx8_u32x4*>(&rv[4 * c]);
         }
     } else {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const sx8_u32x4 x = *reinterpret_cast<const sx8_u32x4*>(q + (kv * G + g) * HD + 8 * c);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                qv[g][2 * e] = h2f(x[e] & 0xFFFFu);
-                qv[g][2 * e + 1] = h2f(x[e] >> 16);
-            }
+            for (int e = 0; e < 4; ++e) qv[g][e] = x[e];
         }
     }
-    const uint16_t* kc = k_cache + (int64_t)kv * L * HD;
-    const uint16_t* vc = v_cache + (int64_t)kv * L * HD;
+
+    // (4) online softmax over the lane group's positions pg, pg + PG, ... of the chunk
     float m[G], l[G], a[G][8];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -376,45 +463,32 @@ __global__ __launch_bounds__(256) void k_attn_split(const uint16_t* __restrict__
 #pragma unroll
         for (int e = 0; e < 8; ++e) a[g][e] = 0.f;
     }
-    for (int j0 = jb + pg; j0 < je; j0 += kU * PG) {
-        sx8_u32x4 kr[kU], vr[kU];
-#pragma unroll
-        for (int u = 0; u < kU; ++u)      // past the chunk: a valid row, its score is -inf
-            kr[u] = *reinterpret_cast<const sx8_u32x4*>(kc + (int64_t)min(j0 + u * PG, je - 1) * HD + 8 * c);
-#pragma unroll
-        for (int u = 0; u < kU; ++u)
-            vr[u] = *reinterpret_cast<const sx8_u32x4*>(vc + (int64_t)min(j0 + u * PG, je - 1) * HD + 8 * c);
-        if constexpr (kRope) {
-            if (own_new) {
-#pragma unroll
-                for (int u = 0; u < kU; ++u)
-                    if (min(j0 + u * PG, je - 1) == pos) {
-                        kr[u] = knew;
-                        vr[u] = vnew;
-                    }
-            }
-        }
+    for (int j0 = jb + pg; j0 < je;) {
         float s[kU][G];
+        float vf[kU][8];
 #pragma unroll
-        for (int u = 0; u < kU; ++u)
+        for (int u = 0; u < kU; ++u) {
+            const bool is_new = own_new && min(j0 + u * PG, je - 1) == pos;
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 float sc = 0.f;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    sc += qv[g][2 * e] * h2f(kr[u][e] & 0xFFFFu) + qv[g][2 * e + 1] * h2f(kr[u][e] >> 16);
-#pragma unroll
-                for (int o = CH / 2; o > 0; o >>= 1) sc += __shfl_xor(sc, o, 64);
+                for (int e = 0; e < 4; ++e) {
+                    // (through a scalar: a bit_cast of a vector-element lvalue reads element 0)
+                    const uint32_t kw = is_new ? knew[e] : kr[u][e];
+                    sc = __builtin_amdgcn_fdot2(__builtin_bit_cast(sx8_half2, qv[g][e]),
+                                                __builtin_bit_cast(sx8_half2, kw), sc, false);
+                }
+                sc = group_sum<CH>(sc);
                 s[u][g] = j0 + u * PG < je ? sc * scale : -INFINITY;
             }
-        float vf[kU][8];
-#pragma unroll
-        for (int u = 0; u < kU; ++u)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                vf[u][2 * e] = h2f(vr[u][e] & 0xFFFFu);
-                vf[u][2 * e + 1] = h2f(vr[u][e] >> 16);
+                const uint32_t vw = is_new ? vnew[e] : vr[u][e];
+                vf[u][2 * e] = h2f((uint16_t)(vw & 0xFFFFu));
+                vf[u][2 * e + 1] = h2f((uint16_t)(vw >> 16));
             }
+        }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float mx = m[g];
@@ -433,6 +507,8 @@ __global__ __launch_bounds__(256) void k_attn_split(const uint16_t* __restrict__
             }
             m[g] = mx;
         }
+        j0 += kU * PG;
+        if (j0 < je) load_rows(j0);
     }
     if (c == 0)
 #pragma unroll

@@ -286,6 +286,7 @@ def test_argmax_advance(hiplib, cuda, n, offset):
     (8, 4, 64, 64, [0, 63]),
     (32, 8, 128, 1500, [0, 700, 1499]),
     (16, 2, 128, 400, [0, 399]),                   # G = 8
+    (8, 2, 128, 3000, [0, 2047, 2999]),            # a longer cache (94 positions per chunk)
 ])
 def test_attn_rope_matches_two_calls(hiplib, cuda, nh, nk, hd, L, positions):
     """sx8_dec_attn_rope against sx8_dec_qk_rope_cache + sx8_dec_attn_split: the new k/v rows
