@@ -117,7 +117,11 @@ int32_t sx8_dec_silu_mul(const float* g, const float* u, uint16_t* out, int64_t 
  * W_i . x for the n_mats matrices, as sx8_gemv_group.  When resid_out is not NULL it
  * receives h; it must not alias resid or delta.  State vectors 16-byte aligned.
  * sx8_dec_gemv_silu: the same with x = fp16(silu(g) * u) (as sx8_dec_silu_mul).
- * Both need n_cb <= 384 and take bases/scales (no caller Z). */
+ * sx8_dec_gemv_silu_add / sx8_dec_gemv_add: x = fp16(silu(g) * u), or x given (fp16, 16-byte
+ * aligned), and Ys[i] = adds[i] + W_i . x: the residual add of the decoder layer in the
+ * GEMV's final store (each element read and written by one thread, so adds[i] may be
+ * Ys[i]: the residual stream updated in place).
+ * All need n_cb <= 384 and take bases/scales (no caller Z). */
 int32_t sx8_dec_gemv_rmsnorm(const float* resid, const uint16_t* init, const float* delta,
                              const uint16_t* norm_w, float eps, float* resid_out, int32_t n_mats,
                              const uint8_t* const* hdrs, const uint8_t* const* levels,
@@ -128,6 +132,15 @@ int32_t sx8_dec_gemv_silu(const float* g, const float* u, int32_t n_mats,
                           const uint8_t* const* hdrs, const uint8_t* const* levels,
                           int32_t hdr_bytes, const float* const* bases, const float* const* scales,
                           const int64_t* Ns, int64_t n_cb, float* const* Ys, void* stream);
+int32_t sx8_dec_gemv_silu_add(const float* g, const float* u, int32_t n_mats,
+                              const uint8_t* const* hdrs, const uint8_t* const* levels,
+                              int32_t hdr_bytes, const float* const* bases, const float* const* scales,
+                              const int64_t* Ns, int64_t n_cb, const float* const* adds,
+                              float* const* Ys, void* stream);
+int32_t sx8_dec_gemv_add(const uint16_t* x, int32_t n_mats, const uint8_t* const* hdrs,
+                         const uint8_t* const* levels, int32_t hdr_bytes, const float* const* bases,
+                         const float* const* scales, const int64_t* Ns, int64_t n_cb,
+                         const float* const* adds, float* const* Ys, void* stream);
 
 /* *tok = argmax(logits[0..n)) (first index among equal maxima), then *pos += 1. */
 int32_t sx8_dec_argmax_advance(const float* logits, int64_t n, int64_t* tok, int64_t* pos,

@@ -567,6 +567,7 @@ struct GemvMat {
     const float* scales;
     const float* Zin;
     float* Y;
+    const float* add;   // Y = add + W x when set (may be Y itself: the residual updated in place)
     int N, panels;
 };
 struct GemvGroup {
@@ -827,6 +828,9 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
         float t = 0.f;
 #pragma unroll
         for (int g = 0; g < 8; ++g) t += red[kPanelThreads + g * CT + tid];
+        // residual epilogue: h = resid + W x, each element read and written by this thread
+        const float* __restrict__ add = kOne ? grp.m[0].add : pick([](const GemvMat& g) { return g.add; });
+        if (add) t = *(const g_float*)(add + n) + t;
         *(float SX8_GLOBAL_AS*)(Y + n) = t;
     }
 }
@@ -912,7 +916,7 @@ int32_t launch_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels
                     (long long)N, (long long)n_cb);
     GemvGroup g{};
     g.n_mats = 1;
-    g.m[0] = GemvMat{hdr, levels, basis, scales, Zin, Y, N, (int)p.grid};
+    g.m[0] = GemvMat{hdr, levels, basis, scales, Zin, Y, nullptr, N, (int)p.grid};
     const bool lds = n_cb <= kLdsMaxKb;
     const size_t smem = panel_smem(n_cb, lds);
     if (!Zout && lds) {   // single launch: the table is built inside every work-group
@@ -952,7 +956,7 @@ int32_t launch_gemv_group(const uint16_t* X, int n_mats, const uint8_t* const* h
             return fail(SX8_ERR_UNSUPPORTED, "sx8_gemv_group: %lld x %lld blocks exceed 32-bit offsets",
                         (long long)Ns[i], (long long)n_cb);
         g.m[i] = GemvMat{hdrs[i], levels[i], bases ? bases[i] : nullptr,
-                         scales ? scales[i] : nullptr, Zins ? Zins[i] : nullptr, Ys[i],
+                         scales ? scales[i] : nullptr, Zins ? Zins[i] : nullptr, Ys[i], nullptr,
                          (int)Ns[i], (int)((Ns[i] + p.CT - 1) / p.CT)};
     }
     const size_t smem = panel_smem(n_cb, true);
@@ -1151,7 +1155,7 @@ template <int kX>
 int32_t launch_fused(const char* what, const XProd& xp, int32_t n_mats, const uint8_t* const* hdrs,
                      const uint8_t* const* levels, int32_t hdr_bytes, const float* const* bases,
                      const float* const* scales, const int64_t* Ns, int64_t n_cb, float* const* Ys,
-                     hipStream_t st) {
+                     hipStream_t st, const uint16_t* X = nullptr, const float* const* adds = nullptr) {
     using namespace sx8;
     PanelPlan p = plan_panels(Ns, n_mats, (int)n_cb);
     GemvGroup g{};
@@ -1160,14 +1164,14 @@ int32_t launch_fused(const char* what, const XProd& xp, int32_t n_mats, const ui
         if (!offsets_fit(p, Ns[i], n_cb))
             return fail(SX8_ERR_UNSUPPORTED, "%s: %lld x %lld blocks exceed 32-bit offsets", what,
                         (long long)Ns[i], (long long)n_cb);
-        g.m[i] = GemvMat{hdrs[i], levels[i], bases[i], scales[i], nullptr, Ys[i], (int)Ns[i],
-                         (int)((Ns[i] + p.CT - 1) / p.CT)};
+        g.m[i] = GemvMat{hdrs[i], levels[i], bases[i], scales[i], nullptr, Ys[i], adds ? adds[i] : nullptr,
+                         (int)Ns[i], (int)((Ns[i] + p.CT - 1) / p.CT)};
     }
     const size_t smem = panel_smem((int)n_cb, true);
     if (hdr_bytes == 8)
-        launch_panel<8, 1, kX>(p, smem, st, nullptr, g, nullptr, (int)n_cb, xp);
+        launch_panel<8, 1, kX>(p, smem, st, X, g, nullptr, (int)n_cb, xp);
     else
-        launch_panel<6, 1, kX>(p, smem, st, nullptr, g, nullptr, (int)n_cb, xp);
+        launch_panel<6, 1, kX>(p, smem, st, X, g, nullptr, (int)n_cb, xp);
     return check_launch(what);
 }
 
@@ -1217,4 +1221,50 @@ extern "C" int32_t sx8_dec_gemv_silu(const float* g, const float* u, int32_t n_m
     xp.u = u;
     return launch_fused<kXSilu>(what, xp, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys,
                                 as_stream(stream));
+}
+
+// Residual checks of the *_add entry points: adds[i] is either Ys[i] (updated in place) or
+// a separate 16-byte aligned vector of Ns[i] floats.
+static int32_t check_adds(const char* what, int32_t n_mats, const float* const* adds, float* const* Ys) {
+    using namespace sx8;
+    if (!adds) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    for (int i = 0; i < n_mats; ++i)
+        if (!adds[i] || !aligned(adds[i], 4))
+            return fail(SX8_ERR_INVALID, "%s: bad residual pointer (matrix %d)", what, i);
+    (void)Ys;
+    return SX8_OK;
+}
+
+extern "C" int32_t sx8_dec_gemv_silu_add(const float* g, const float* u, int32_t n_mats,
+                                         const uint8_t* const* hdrs, const uint8_t* const* levels,
+                                         int32_t hdr_bytes, const float* const* bases,
+                                         const float* const* scales, const int64_t* Ns, int64_t n_cb,
+                                         const float* const* adds, float* const* Ys, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_dec_gemv_silu_add";
+    if (!g || !u) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (!aligned(g, 16) || !aligned(u, 16)) return fail(SX8_ERR_INVALID, "%s: g and u must be 16-byte aligned", what);
+    int32_t rc = check_fused_group(what, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys);
+    if (rc == SX8_OK) rc = check_adds(what, n_mats, adds, Ys);
+    if (rc != SX8_OK) return rc;
+    XProd xp{};
+    xp.g = g;
+    xp.u = u;
+    return launch_fused<kXSilu>(what, xp, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys,
+                                as_stream(stream), nullptr, adds);
+}
+
+extern "C" int32_t sx8_dec_gemv_add(const uint16_t* x, int32_t n_mats, const uint8_t* const* hdrs,
+                                    const uint8_t* const* levels, int32_t hdr_bytes, const float* const* bases,
+                                    const float* const* scales, const int64_t* Ns, int64_t n_cb,
+                                    const float* const* adds, float* const* Ys, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_dec_gemv_add";
+    if (!x) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (!aligned(x, 16)) return fail(SX8_ERR_INVALID, "%s: x must be 16-byte aligned", what);
+    int32_t rc = check_fused_group(what, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys);
+    if (rc == SX8_OK) rc = check_adds(what, n_mats, adds, Ys);
+    if (rc != SX8_OK) return rc;
+    return launch_fused<kXPlain>(what, XProd{}, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys,
+                                 as_stream(stream), x, adds);
 }

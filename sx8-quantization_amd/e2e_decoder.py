@@ -300,24 +300,21 @@ class SX8Decoder(nn.Module):
                                cfg["inter"], cfg["vocab"])
         f32 = dict(dtype=torch.float32, device=dev)
         f16 = dict(dtype=torch.float16, device=dev)
-        z = {"resid": torch.zeros(1, H, **f32), "h": torch.zeros(H, **f16),
-             "ra": torch.zeros(H, **f32), "rb": torch.zeros(H, **f32),
+        z = {"ra": torch.zeros(H, **f32),
              "q": torch.zeros(nh * hd, **f32), "k": torch.zeros(nk * hd, **f32),
-             "v": torch.zeros(nk * hd, **f32), "qh": torch.zeros(nh * hd, **f16),
-             "a": torch.zeros(nh * hd, **f16), "o": torch.zeros(H, **f32),
-             "g": torch.zeros(I, **f32), "u": torch.zeros(I, **f32), "m": torch.zeros(I, **f16),
-             "d": torch.zeros(H, **f32), "logits": torch.zeros(V, **f32)}
-        n_cb_max = max(lin.qt["n_cb"] for ly in self.layers for lin in (ly.q, ly.o, ly.down))
-        ws_bytes = int(_L.lib().sx8_gemv_workspace_bytes(max(n_cb_max, self.head.qt["n_cb"])))
-        z["ws"] = torch.zeros((ws_bytes + 3) // 4 + 64, **f32)
+             "v": torch.zeros(nk * hd, **f32), "a": torch.zeros(nh * hd, **f16),
+             "g": torch.zeros(I, **f32), "u": torch.zeros(I, **f32), "logits": torch.zeros(V, **f32)}
         z["attn_ws"] = torch.zeros(int(_L.lib().sx8_dec_attn_workspace_bytes(nh, hd)) // 4 + 64, **f32)
-        # grouped GEMV arguments (q/k/v and gate/up share their input): ctypes arrays
-        # of device pointers, built once per layer
+        # grouped GEMV arguments (q/k/v and gate/up share their input): ctypes arrays of
+        # device pointers, built once per layer; the o and down GEMVs add their output to
+        # the residual stream ra in place
         z["groups"] = []
         for ly in self.layers:
             z["groups"].append((self._group_args((ly.q, ly.k, ly.v), (z["q"], z["k"], z["v"])),
                                 self._group_args((ly.gate, ly.up), (z["g"], z["u"])),
-                                self._group_args((ly.down,), (z["d"],))))
+                                self._group_args((ly.down,), (z["ra"],)),
+                                self._group_args((ly.o,), (z["ra"],))))
+        z["resid_adds"] = (ctypes.c_void_p * 1)(z["ra"].data_ptr())
         z["head_group"] = self._group_args((self.head,), (z["logits"],))
         self._fz = z
         return z
@@ -351,21 +348,29 @@ class SX8Decoder(nn.Module):
         n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
         _L.call("sx8_dec_gemv_silu", _L.ptr(g), _L.ptr(u), n, hdrs, lvls, 6, bas, sca, ns, n_cb, ys, st)
 
-    def _gemv(self, lin, x, y, st):
-        z = self._fz
-        hdr, lvl, bas, sca = lin._t44
-        _L.call("sx8_gemv", _L.ptr(x), _L.ptr(hdr), _L.ptr(lvl), 6, _L.ptr(bas), _L.ptr(sca), None,
-                None, lin.out_f, lin.qt["n_cb"], _L.ptr(y), _L.ptr(z["ws"]), z["ws"].numel() * 4, st)
+    @staticmethod
+    def _gemv_silu_add(args, g, u, adds, st):
+        """Ys = adds + W silu(g) * u (the residual add in the GEMV's store)."""
+        n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
+        _L.call("sx8_dec_gemv_silu_add", _L.ptr(g), _L.ptr(u), n, hdrs, lvls, 6, bas, sca, ns, n_cb, adds,
+                ys, st)
+
+    @staticmethod
+    def _gemv_add(args, x, adds, st):
+        """Ys = adds + W x."""
+        n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
+        _L.call("sx8_dec_gemv_add", _L.ptr(x), n, hdrs, lvls, 6, bas, sca, ns, n_cb, adds, ys, st)
 
     @torch.no_grad()
     def decode_step_fused(self, tok, pos):
         """decode_step with the per-token ops as single HIP launches (sx8_decoder.h) and the
         GEMVs called through the C ABI; the residual stream is float32.  Each RMSNorm runs
-        inside the GEMV that consumes it (sx8_dec_gemv_rmsnorm: q/k/v, gate/up, lm_head)
-        and SiLU * up inside the down GEMV (sx8_dec_gemv_silu); q/k norm + RoPE + KV-cache
-        write inside attention (sx8_dec_attn_rope): per layer one launch each for q/k/v,
-        attention (two: chunks, combine), o, gate/up and down.  The residual
-        ping-pongs between ra and rb (a fused GEMV reads one and writes the other)."""
+        inside the GEMV that consumes it (sx8_dec_gemv_rmsnorm: q/k/v, gate/up, lm_head),
+        SiLU * up inside the down GEMV, and both residual adds inside the GEMVs that produce
+        them (sx8_dec_gemv_add for o, sx8_dec_gemv_silu_add for down: the stream ra is
+        updated in place); q/k norm + RoPE + KV-cache write inside attention
+        (sx8_dec_attn_rope): per layer one launch each for q/k/v, attention (two: chunks,
+        combine), o, gate/up and down."""
         cfg = self.cfg
         nh, nk, hd, eps = cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["eps"]
         z = self._fused_setup()
@@ -373,22 +378,22 @@ class SX8Decoder(nn.Module):
         P = _L.ptr
         emb = self.embed(tok)                                       # (1, H) fp16
         L = self.max_len
-        ra, rb = z["ra"], z["rb"]
+        r, adds = z["ra"], z["resid_adds"]
         for li, ly in enumerate(self.layers):
-            g_qkv, g_gu, g_dn = z["groups"][li]
-            if li == 0:                                             # h = embedding row
-                self._gemv_rms(g_qkv, None, emb, None, ly.in_norm, rb, eps, st)
-            else:                                                   # h = ra + down output
-                self._gemv_rms(g_qkv, ra, None, z["d"], ly.in_norm, rb, eps, st)
+            g_qkv, g_gu, g_dn, g_o = z["groups"][li]
+            if li == 0:                                             # h = embedding row -> r
+                self._gemv_rms(g_qkv, None, emb, None, ly.in_norm, r, eps, st)
+            else:                                                   # h = r
+                self._gemv_rms(g_qkv, r, None, None, ly.in_norm, None, eps, st)
             # q/k norm + RoPE + KV-cache write inside the attention pass
             _L.call("sx8_dec_attn_rope", P(z["q"]), P(z["k"]), P(z["v"]), P(ly.q_norm), P(ly.k_norm),
                     P(self.cos), P(self.sin), P(pos), P(self.k_cache[li]), P(self.v_cache[li]),
                     P(z["a"]), nh, nk, hd, L, 1.0 / math.sqrt(hd), eps, P(z["attn_ws"]),
                     z["attn_ws"].numel() * 4, st)
-            self._gemv(ly.o, z["a"], z["o"], st)
-            self._gemv_rms(g_gu, rb, None, z["o"], ly.post_norm, ra, eps, st)   # h = rb + o
-            self._gemv_silu(g_dn, z["g"], z["u"], st)
-        self._gemv_rms(z["head_group"], ra, None, z["d"], self.final_norm, None, eps, st)
+            self._gemv_add(g_o, z["a"], adds, st)                   # r += W_o a
+            self._gemv_rms(g_gu, r, None, None, ly.post_norm, None, eps, st)
+            self._gemv_silu_add(g_dn, z["g"], z["u"], adds, st)    # r += W_down silu(g) u
+        self._gemv_rms(z["head_group"], r, None, None, self.final_norm, None, eps, st)
         _L.call("sx8_dec_argmax_advance", P(z["logits"]), cfg["vocab"], P(tok), P(pos), st)
         return tok
 

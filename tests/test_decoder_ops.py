@@ -1,5 +1,6 @@
 """The per-token decoder ops of include/sx8_decoder.h on the GPU against float32 torch
 references (the same math as the decode loop of scripts/infer_sx8.py:109-173)."""
+import ctypes
 import math
 
 import numpy as np
@@ -231,6 +232,58 @@ def test_fused_gemv_silu(hiplib, cuda):
     # more K blocks than the up-front table passes hold: refused
     with pytest.raises(RuntimeError, match="n_cb"):
         _L.call("sx8_dec_gemv_silu", P(a), P(b), n, hd, lv, 6, bs, sc, ns, 385, ys, st)
+
+
+def test_fused_gemv_residual_add(hiplib, cuda):
+    """sx8_dec_gemv_add and sx8_dec_gemv_silu_add: Ys[i] = adds[i] + W_i x bit for bit against
+    sx8_gemv_group (resp. sx8_dec_silu_mul + sx8_gemv_group) plus a float32 add, both with a
+    separate residual and with the residual updated in place (adds[i] = Ys[i])."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    g = torch.Generator().manual_seed(12)
+    # o-like group of one matrix and a q/k/v-like group of three, plain x
+    for K, Ns in ((4096, [2560]), (2560, [4096, 1024, 1024])):
+        ts = _mats(cuda, Ns, K, 70 + len(Ns))
+        x = torch.randn(K, generator=g).half().to(cuda)
+        res = [torch.randn(N, generator=g).to(cuda) for N in Ns]
+        y_ref = [torch.empty(N, device=cuda) for N in Ns]
+        n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y_ref)
+        _L.call("sx8_gemv_group", P(x), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, None, 0, st)
+        exp = [yr + r for yr, r in zip(y_ref, res)]
+        y = [torch.empty(N, device=cuda) for N in Ns]
+        n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y)
+        adds = (ctypes.c_void_p * n)(*[r.data_ptr() for r in res])
+        _L.call("sx8_dec_gemv_add", P(x), n, hd, lv, 6, bs, sc, ns, n_cb, adds, ys, st)
+        inplace = [r.clone() for r in res]
+        n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, inplace)
+        adds2 = (ctypes.c_void_p * n)(*[r.data_ptr() for r in inplace])
+        _L.call("sx8_dec_gemv_add", P(x), n, hd, lv, 6, bs, sc, ns, n_cb, adds2, ys, st)
+        torch.cuda.synchronize()
+        for i in range(n):
+            assert torch.equal(y[i].cpu(), exp[i].cpu()), (K, i)
+            assert torch.equal(inplace[i].cpu(), exp[i].cpu()), (K, i)
+    # down-like: x = silu(g) * u, residual updated in place
+    K, Ns = 9728, [2560]
+    ts = _mats(cuda, Ns, K, 61)
+    a = torch.randn(K, generator=g).to(cuda)
+    b = torch.randn(K, generator=g).to(cuda)
+    m = torch.empty(K, dtype=torch.float16, device=cuda)
+    _L.call("sx8_dec_silu_mul", P(a), P(b), P(m), K, st)
+    y_ref = [torch.empty(N, device=cuda) for N in Ns]
+    n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y_ref)
+    _L.call("sx8_gemv_group", P(m), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, None, 0, st)
+    res = torch.randn(Ns[0], generator=g).to(cuda)
+    exp = y_ref[0] + res
+    n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, [res])
+    adds = (ctypes.c_void_p * 1)(res.data_ptr())
+    _L.call("sx8_dec_gemv_silu_add", P(a), P(b), n, hd, lv, 6, bs, sc, ns, n_cb, adds, ys, st)
+    torch.cuda.synchronize()
+    assert torch.equal(res.cpu(), exp.cpu())
+    with pytest.raises(RuntimeError, match="residual"):
+        bad = (ctypes.c_void_p * 1)(None)
+        _L.call("sx8_dec_gemv_silu_add", P(a), P(b), n, hd, lv, 6, bs, sc, ns, n_cb, bad, ys, st)
 
 
 @pytest.mark.parametrize("M,K,N", [(512, 9728, 2560), (77, 9728, 300), (40, 1000, 130)])
