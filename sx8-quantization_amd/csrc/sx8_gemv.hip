@@ -573,6 +573,7 @@ struct GemvMat {
 struct GemvGroup {
     GemvMat m[kMaxGroup];
     int n_mats;
+    int ct;   // panel width of a group launch (plan_panels)
 };
 
 // Panel width for a launch over `total` output columns: about one work-group per CU
@@ -659,12 +660,12 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 
-    // panel geometry from the launch's total width (the host's plan_panels does the same);
-    // the width passes through an empty asm so that the divisions below cannot be hoisted
-    // above the table loads
-    int64_t width = kOne ? (int64_t)N0 : (int64_t)grp.m[0].N + grp.m[1].N + grp.m[2].N + grp.m[3].N;
-    asm volatile("" : "+s"(width));
-    const int CT = panel_ct(width);
+    // panel geometry: a single matrix derives it from N (as the host's plan_panels does; N
+    // passes through an empty asm so that the divisions below cannot be hoisted above the
+    // table loads), a group reads it with its matrix fields
+    int n_one = N0;
+    asm volatile("" : "+s"(n_one));
+    const int CT = kOne ? panel_ct(n_one) : grp.ct;
     const int S = kPanelThreads / CT;
     const int R = (n_cb + S - 1) / S;
     const int j0 = tid / CT;
@@ -850,12 +851,21 @@ inline PanelPlan plan_panels(const int64_t* Ns, int n_mats, int n_cb) {
     for (int i = 0; i < n_mats; ++i) total += Ns[i];
     PanelPlan p;
     p.CT = panel_ct(total);
+    // a group rounds every matrix up to whole panels: widen the panels until the grid is
+    // back within one (two) work-groups per CU -- one more work-group than CUs puts two on
+    // one CU, and the launch waits for that CU (q/k/v 4096 + 1024 + 1024: CT 24 gives 257
+    // panels, CT 25 gives 246)
+    const int64_t cap = total > 64 * 256 ? 512 : 256;
+    auto panels = [&](int ct) {
+        int64_t g = 0;
+        for (int i = 0; i < n_mats; ++i) g += (Ns[i] + ct - 1) / ct;
+        return g;
+    };
+    while (p.CT < 64 && panels(p.CT) > cap) ++p.CT;
     p.S = kPanelThreads / p.CT;
     p.R = (n_cb + p.S - 1) / p.S;
     p.TP = n_cb <= 128 * kTabPassesShort ? kTabPassesShort : kTabPassesLong;
-    int64_t grid = 0;
-    for (int i = 0; i < n_mats; ++i) grid += (Ns[i] + p.CT - 1) / p.CT;
-    p.grid = (unsigned)grid;
+    p.grid = (unsigned)panels(p.CT);
     return p;
 }
 
@@ -916,6 +926,7 @@ int32_t launch_gemv(const uint16_t* X, const uint8_t* hdr, const uint8_t* levels
                     (long long)N, (long long)n_cb);
     GemvGroup g{};
     g.n_mats = 1;
+    g.ct = p.CT;
     g.m[0] = GemvMat{hdr, levels, basis, scales, Zin, Y, nullptr, N, (int)p.grid};
     const bool lds = n_cb <= kLdsMaxKb;
     const size_t smem = panel_smem(n_cb, lds);
@@ -951,6 +962,7 @@ int32_t launch_gemv_group(const uint16_t* X, int n_mats, const uint8_t* const* h
     const PanelPlan p = plan_panels(Ns, n_mats, n_cb);
     GemvGroup g{};
     g.n_mats = n_mats;
+    g.ct = p.CT;
     for (int i = 0; i < n_mats; ++i) {
         if (!offsets_fit(p, Ns[i], n_cb))
             return fail(SX8_ERR_UNSUPPORTED, "sx8_gemv_group: %lld x %lld blocks exceed 32-bit offsets",
@@ -1160,6 +1172,7 @@ int32_t launch_fused(const char* what, const XProd& xp, int32_t n_mats, const ui
     PanelPlan p = plan_panels(Ns, n_mats, (int)n_cb);
     GemvGroup g{};
     g.n_mats = n_mats;
+    g.ct = p.CT;
     for (int i = 0; i < n_mats; ++i) {
         if (!offsets_fit(p, Ns[i], n_cb))
             return fail(SX8_ERR_UNSUPPORTED, "%s: %lld x %lld blocks exceed 32-bit offsets", what,
