@@ -484,21 +484,44 @@ __device__ __forceinline__ XRsrc xraw_rsrc(const XProd& xp, int K) {
     return r;
 }
 
+// The same from the preloaded argument slots (kPre): kXRms reads h = resid (no init, no
+// delta) from the x slot and the norm weight from the header slot; kXSilu reads g from the
+// x slot and u from g + K (the two vectors adjacent in memory).
+template <int kX>
+__device__ __forceinline__ XRsrc xraw_rsrc_pre(const void* xs, const void* hs, int K) {
+    XRsrc r;
+    if constexpr (kX == kXRms) {
+        r.a = make_rsrc(xs, (int64_t)K * 4);
+        r.b = make_rsrc(nullptr, 0);
+        r.h16 = make_rsrc(nullptr, 0);
+        r.w = make_rsrc(hs, (int64_t)K * 2);
+    } else {
+        r.a = make_rsrc(xs, (int64_t)K * 4);
+        r.b = make_rsrc(static_cast<const float*>(xs) + K, (int64_t)K * 4);
+    }
+    return r;
+}
+
 __device__ __forceinline__ float4 ld_f4(sx8_rsrc r, uint32_t off) {
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
-template <int kX>
+template <int kX, bool kPre = false>
 __device__ __forceinline__ void xraw_load(XRaw& r, const XRsrc& rs, int kb, int q) {
     const uint32_t e = (uint32_t)(kb * 32 + 8 * q);
     r.a0 = ld_f4(rs.a, e * 4);
     r.a1 = ld_f4(rs.a, e * 4 + 16);
-    r.b0 = ld_f4(rs.b, e * 4);
-    r.b1 = ld_f4(rs.b, e * 4 + 16);
-    if constexpr (kX == kXRms) {
-        r.h16 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.h16, e * 2, 0, 0));
-        r.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, e * 2, 0, 0));
+    if (kX == kXRms && kPre) {           // no delta, no init
+        r.b0 = r.b1 = make_float4(0.f, 0.f, 0.f, 0.f);
+        r.h16 = make_uint4(0u, 0u, 0u, 0u);
+    } else {
+        r.b0 = ld_f4(rs.b, e * 4);
+        r.b1 = ld_f4(rs.b, e * 4 + 16);
+        if constexpr (kX == kXRms)
+            r.h16 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.h16, e * 2, 0, 0));
     }
+    if constexpr (kX == kXRms)
+        r.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.w, e * 2, 0, 0));
 }
 
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
@@ -593,7 +616,14 @@ __host__ __device__ inline int panel_ct(int64_t total) {
 // the first record rounds and each lane's coefficients kept for a PCA pass before the
 // reduction -- 8% slower on the layer sweep; the epilogue it adds costs more than the
 // prologue it shortens.)
-template <int HB, int kMode, int NR, int TP, int kX = kXPlain, bool kOne = false>
+// kPre: the producer's inputs sit in the argument slots that arrive preloaded (see
+// xraw_rsrc_pre): a group's header slot is free (its matrices come from grp), so a
+// grouped RMSNorm takes h and the norm weight from there; a single-matrix SiLU takes g
+// (u = g + K).  kResY (single matrix): Y = Y + W x, the residual read from the preloaded
+// output slot right after the first records are requested (not at the end, where a load
+// would add a memory round trip to every work-group's finish).
+template <int HB, int kMode, int NR, int TP, int kX = kXPlain, bool kOne = false, bool kPre = false,
+          bool kResY = false>
 __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     const uint8_t* __restrict__ hdr0, const uint8_t* __restrict__ lv0, const uint16_t* __restrict__ X,
     int N0, int n_cb, const float* __restrict__ bas0, const float* __restrict__ sca0,
@@ -603,6 +633,20 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     float* red = reinterpret_cast<float*>(smem);                 // 2 x 512 floats
     KbInfo* info = reinterpret_cast<KbInfo*>(smem + sizeof(float) * 2 * kPanelThreads);
     const int tid = threadIdx.x;
+    // The producer's inputs go out before anything else: with kPre they need no argument
+    // load (a group's matrix fields are a memory round trip away).
+    XRaw xr[kX == kXPlain ? 1 : TP];
+    if constexpr ((kMode == 1 || kMode == 2) && kX != kXPlain) {
+        XRsrc xs;
+        if constexpr (kPre) xs = xraw_rsrc_pre<kX>(X, hdr0, n_cb * 32);
+        else xs = xraw_rsrc<kX>(xp, n_cb * 32);
+#pragma unroll
+        for (int p = 0; p < TP; ++p) {
+            const int u = min(p * kPanelThreads + tid, n_cb * 4 - 1);
+            xraw_load<kX, kPre>(xr[p], xs, u >> 2, u & 3);
+        }
+        asm volatile("" ::: "memory");
+    }
     // panel number: XCD x (= blockIdx % 8) gets the contiguous range after the
     // sum_{y < x} ceil((G - y) / 8) panels of the XCDs before it (G = 8 q + r)
     const int xcd = blockIdx.x & 7;
@@ -642,15 +686,11 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     // them after the geometry).
     const int n_units = n_cb * 4;
     TabIn tin[TP];
-    XRaw xr[kX == kXPlain ? 1 : TP];
     if constexpr (kMode == 1 || kMode == 2) {
-        XRsrc xs;
-        if constexpr (kX != kXPlain) xs = xraw_rsrc<kX>(xp, n_cb * 32);
 #pragma unroll
         for (int p = 0; p < TP; ++p) {
             const int u = min(p * kPanelThreads + tid, n_units - 1);
             tab_load<kMode, kX == kXPlain>(tin[p], Xg, basis, scales, Zin, u >> 2, u & 3);
-            if constexpr (kX != kXPlain) xraw_load<kX>(xr[p], xs, u >> 2, u & 3);
         }
     }
     // issue order = wait order (the memory counter retires loads in order): table
@@ -698,6 +738,10 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
         load(buf[i], i);
         __builtin_amdgcn_sched_barrier(0);
     }
+    float yres = 0.f;                        // kResY: this column's residual, read early
+    if constexpr (kResY) {
+        if (tid < CT && col_ok) yres = *(const g_float*)(Y0 + n);
+    }
     if constexpr (kMode == 0) {
         const uint4* src = reinterpret_cast<const uint4*>(table);
         uint4* dst = reinterpret_cast<uint4*>(info);
@@ -725,7 +769,7 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
 #pragma unroll
             for (int wv = 0; wv < kPanelThreads / 64; ++wv) tot += red[wv];
             const float inv = 1.0f / sqrtf(tot / (float)(n_cb * 32) + xp.eps);
-            const bool writer = blockIdx.x == 0 && xp.resid_out != nullptr;
+            const bool writer = !kPre && blockIdx.x == 0 && xp.resid_out != nullptr;
 #pragma unroll
             for (int p = 0; p < TP; ++p) {
                 const uint32_t ww[4] = {xr[p].w.x, xr[p].w.y, xr[p].w.z, xr[p].w.w};
@@ -830,8 +874,12 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
 #pragma unroll
         for (int g = 0; g < 8; ++g) t += red[kPanelThreads + g * CT + tid];
         // residual epilogue: h = resid + W x, each element read and written by this thread
-        const float* __restrict__ add = kOne ? grp.m[0].add : pick([](const GemvMat& g) { return g.add; });
-        if (add) t = *(const g_float*)(add + n) + t;
+        if constexpr (kResY) {
+            t = yres + t;
+        } else {
+            const float* __restrict__ add = kOne ? grp.m[0].add : pick([](const GemvMat& g) { return g.add; });
+            if (add) t = *(const g_float*)(add + n) + t;
+        }
         *(float SX8_GLOBAL_AS*)(Y + n) = t;
     }
 }
@@ -874,20 +922,31 @@ constexpr int kRing = 3;   // record buffers per lane (at most)
 // work-group's prologue amortized) run with two record buffers, which measured faster there.
 constexpr unsigned kRing3MaxGrid = 1024;
 
-template <int HB, int kMode, int kX = kXPlain>
+// kPre / kResY: see k_gemv_panel.  A group (kPre, kXRms) passes h in the x slot and the
+// norm weight in the header slot; a single matrix (kPre, kXSilu) passes g in the x slot.
+template <int HB, int kMode, int kX = kXPlain, bool kPre = false, bool kResY = false>
 void launch_panel(const PanelPlan& p, size_t smem, hipStream_t st, const uint16_t* X,
                   const GemvGroup& g, const KbInfo* table, int n_cb, const XProd& xp = XProd{}) {
     const dim3 grid(p.grid), block(kPanelThreads);
     const bool one = g.n_mats == 1;
     const GemvMat& m0 = g.m[0];
+    // instantiated forms: kPre with kXRms only for groups, kPre with kXSilu and kResY only
+    // for single matrices
+    constexpr bool kAllowOne = !(kPre && kX == kXRms);
+    constexpr bool kAllowGroup = !(kPre && kX == kXSilu) && !kResY;
+    const uint8_t* h0 = (kPre && kX == kXRms) ? reinterpret_cast<const uint8_t*>(xp.w) : m0.hdr;
     auto go = [&](auto nr, auto tp) {
         constexpr int NR = decltype(nr)::value, TP = decltype(tp)::value;
-        if (one)
-            hipLaunchKernelGGL((k_gemv_panel<HB, kMode, NR, TP, kX, true>), grid, block, smem, st, m0.hdr,
-                               m0.levels, X, m0.N, n_cb, m0.basis, m0.scales, m0.Y, g, table, xp);
-        else
-            hipLaunchKernelGGL((k_gemv_panel<HB, kMode, NR, TP, kX, false>), grid, block, smem, st, m0.hdr,
-                               m0.levels, X, m0.N, n_cb, m0.basis, m0.scales, m0.Y, g, table, xp);
+        if constexpr (kAllowOne) {
+            if (one) {
+                hipLaunchKernelGGL((k_gemv_panel<HB, kMode, NR, TP, kX, true, kPre, kResY>), grid, block, smem, st,
+                                   h0, m0.levels, X, m0.N, n_cb, m0.basis, m0.scales, m0.Y, g, table, xp);
+                return;
+            }
+        }
+        if constexpr (kAllowGroup)
+            hipLaunchKernelGGL((k_gemv_panel<HB, kMode, NR, TP, kX, false, kPre, kResY>), grid, block, smem, st,
+                               h0, m0.levels, X, m0.N, n_cb, m0.basis, m0.scales, m0.Y, g, table, xp);
     };
     auto by_ring = [&](auto tp) {
         if (p.grid <= kRing3MaxGrid)
@@ -1181,10 +1240,35 @@ int32_t launch_fused(const char* what, const XProd& xp, int32_t n_mats, const ui
                          (int)Ns[i], (int)((Ns[i] + p.CT - 1) / p.CT)};
     }
     const size_t smem = panel_smem((int)n_cb, true);
+    const int64_t K = n_cb * 32;
+    // preloaded producer inputs (see k_gemv_panel): a grouped RMSNorm of the residual alone,
+    // or a single-matrix SiLU whose u follows g
+    const bool pre = kX == kXRms ? (n_mats > 1 && xp.resid && !xp.init && !xp.delta && !xp.resid_out)
+                     : kX == kXSilu ? (n_mats == 1 && xp.u == xp.g + K)
+                                    : false;
+    // the residual updated in place by a single matrix: read from the preloaded output slot
+    // (kResY forms: plain x, or the preloaded SiLU; the others add through the descriptor)
+    const bool resy = n_mats == 1 && adds && adds[0] == Ys[0] && (kX == kXPlain || (kX == kXSilu && pre));
+    if (resy) g.m[0].add = nullptr;
+    const uint16_t* xs = pre ? reinterpret_cast<const uint16_t*>(kX == kXRms ? xp.resid : xp.g) : X;
+    auto run = [&](auto hb) {
+        constexpr int HB = decltype(hb)::value;
+        if constexpr (kX == kXRms) {
+            if (pre) launch_panel<HB, 1, kX, true>(p, smem, st, xs, g, nullptr, (int)n_cb, xp);
+            else launch_panel<HB, 1, kX>(p, smem, st, xs, g, nullptr, (int)n_cb, xp);
+        } else if constexpr (kX == kXSilu) {
+            if (pre && resy) launch_panel<HB, 1, kX, true, true>(p, smem, st, xs, g, nullptr, (int)n_cb, xp);
+            else if (pre) launch_panel<HB, 1, kX, true>(p, smem, st, xs, g, nullptr, (int)n_cb, xp);
+            else launch_panel<HB, 1, kX>(p, smem, st, xs, g, nullptr, (int)n_cb, xp);
+        } else {
+            if (resy) launch_panel<HB, 1, kX, false, true>(p, smem, st, xs, g, nullptr, (int)n_cb, xp);
+            else launch_panel<HB, 1, kX>(p, smem, st, xs, g, nullptr, (int)n_cb, xp);
+        }
+    };
     if (hdr_bytes == 8)
-        launch_panel<8, 1, kX>(p, smem, st, X, g, nullptr, (int)n_cb, xp);
+        run(std::integral_constant<int, 8>{});
     else
-        launch_panel<6, 1, kX>(p, smem, st, X, g, nullptr, (int)n_cb, xp);
+        run(std::integral_constant<int, 6>{});
     return check_launch(what);
 }
 

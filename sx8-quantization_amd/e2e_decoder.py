@@ -303,7 +303,11 @@ class SX8Decoder(nn.Module):
         z = {"ra": torch.zeros(H, **f32),
              "q": torch.zeros(nh * hd, **f32), "k": torch.zeros(nk * hd, **f32),
              "v": torch.zeros(nk * hd, **f32), "a": torch.zeros(nh * hd, **f16),
-             "g": torch.zeros(I, **f32), "u": torch.zeros(I, **f32), "logits": torch.zeros(V, **f32)}
+             "logits": torch.zeros(V, **f32)}
+        # gate and up outputs adjacent (u = g + I): the down GEMV then takes both from one
+        # preloaded kernel argument
+        gu = torch.zeros(2, I, **f32)
+        z["g"], z["u"] = gu[0], gu[1]
         z["attn_ws"] = torch.zeros(int(_L.lib().sx8_dec_attn_workspace_bytes(nh, hd)) // 4 + 64, **f32)
         # grouped GEMV arguments (q/k/v and gate/up share their input): ctypes arrays of
         # device pointers, built once per layer; the o and down GEMVs add their output to

@@ -201,6 +201,22 @@ def test_fused_gemv_rmsnorm(hiplib, cuda):
         for a, b in zip(y, y_ref):
             rel = (a - b).abs().max().item() / b.abs().max().item()
             assert rel <= 1e-5, rel
+    # the residual alone (no delta, no init, no resid_out): the group takes h and the norm
+    # weight from its preloaded argument slots; the same x, so the same outputs as the
+    # two-launch path with delta = 0
+    r_ref = resid.cpu().clone().view(1, K).to(cuda)
+    h16 = torch.empty(1, K, dtype=torch.float16, device=cuda)
+    _L.call("sx8_dec_add_rmsnorm", P(r_ref), None, None, P(w), P(h16), 1, K, eps, st)
+    y_ref = [torch.empty(N, device=cuda) for N in Ns]
+    n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y_ref)
+    _L.call("sx8_gemv_group", P(h16), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, None, 0, st)
+    y = [torch.empty(N, device=cuda) for N in Ns]
+    n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y)
+    _L.call("sx8_dec_gemv_rmsnorm", P(resid), None, None, P(w), eps, None, n, hd, lv, 6, bs, sc, ns, n_cb, ys, st)
+    torch.cuda.synchronize()
+    for a, b in zip(y, y_ref):
+        rel = (a - b).abs().max().item() / b.abs().max().item()
+        assert rel <= 1e-5, rel
     # resid_out may not alias an input still being read by other work-groups
     with pytest.raises(RuntimeError, match="alias"):
         _L.call("sx8_dec_gemv_rmsnorm", P(resid), None, P(delta), P(w), eps, P(resid), n, hd, lv, 6, bs,
@@ -264,11 +280,12 @@ def test_fused_gemv_residual_add(hiplib, cuda):
         for i in range(n):
             assert torch.equal(y[i].cpu(), exp[i].cpu()), (K, i)
             assert torch.equal(inplace[i].cpu(), exp[i].cpu()), (K, i)
-    # down-like: x = silu(g) * u, residual updated in place
+    # down-like: x = silu(g) * u, residual updated in place; g and u adjacent (u = g + K:
+    # both from one preloaded argument), then apart
     K, Ns = 9728, [2560]
     ts = _mats(cuda, Ns, K, 61)
-    a = torch.randn(K, generator=g).to(cuda)
-    b = torch.randn(K, generator=g).to(cuda)
+    ab = torch.randn(2, K, generator=g).to(cuda)
+    a, b = ab[0], ab[1]
     m = torch.empty(K, dtype=torch.float16, device=cuda)
     _L.call("sx8_dec_silu_mul", P(a), P(b), P(m), K, st)
     y_ref = [torch.empty(N, device=cuda) for N in Ns]
@@ -276,11 +293,18 @@ def test_fused_gemv_residual_add(hiplib, cuda):
     _L.call("sx8_gemv_group", P(m), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, None, 0, st)
     res = torch.randn(Ns[0], generator=g).to(cuda)
     exp = y_ref[0] + res
+    res0 = res.clone()
     n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, [res])
     adds = (ctypes.c_void_p * 1)(res.data_ptr())
     _L.call("sx8_dec_gemv_silu_add", P(a), P(b), n, hd, lv, 6, bs, sc, ns, n_cb, adds, ys, st)
+    b2 = b.clone()                                          # u no longer at g + K
+    res2 = res0.clone()
+    n, hd, lv, bs, sc, ns, n_cb, ys2 = _group(ts, Ns, K // 32, [res2])
+    adds2 = (ctypes.c_void_p * 1)(res2.data_ptr())
+    _L.call("sx8_dec_gemv_silu_add", P(a), P(b2), n, hd, lv, 6, bs, sc, ns, n_cb, adds2, ys2, st)
     torch.cuda.synchronize()
     assert torch.equal(res.cpu(), exp.cpu())
+    assert torch.equal(res2.cpu(), exp.cpu())
     with pytest.raises(RuntimeError, match="residual"):
         bad = (ctypes.c_void_p * 1)(None)
         _L.call("sx8_dec_gemv_silu_add", P(a), P(b), n, hd, lv, 6, bs, sc, ns, n_cb, bad, ys, st)
