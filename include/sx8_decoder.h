@@ -142,6 +142,25 @@ int32_t sx8_dec_gemv_add(const uint16_t* x, int32_t n_mats, const uint8_t* const
                          const float* const* scales, const int64_t* Ns, int64_t n_cb,
                          const float* const* adds, float* const* Ys, void* stream);
 
+/* The decoder MLP as two launches (no reference counterpart: the reference runs the gate,
+ * up and down linears of the Hugging Face MLP separately, scripts/infer_sx8.py:109-173).
+ * sx8_dec_gemv_rmsnorm_pair: x = fp16(resid * rsqrt(mean(resid^2) + eps) * norm_w) (as
+ * sx8_dec_gemv_rmsnorm with the residual alone), g = W_gate x and u = W_up x in one
+ * launch, m = fp16(silu(g) * u) (as sx8_dec_silu_mul) to m, and zp = the down projection's
+ * PCA sums of m per K block in two partial slots, (N / 32, 2, 2) floats.  The up matrix's
+ * headers, levels, bases and scales must follow the gate matrix's in memory (hdr, levels,
+ * bases, scales point at the gate's; each array holds both); N a multiple of 32 in
+ * 32..16384 (the down projection's K); down_bases its (N / 32, 64) bases.
+ * sx8_dec_gemv_zp_add: Y = add + W_down m with the PCA term from zp (Z = (zp[kb][0][c] +
+ * zp[kb][1][c]) * scales[kb][c]); add may be Y (the residual updated in place). */
+int32_t sx8_dec_gemv_rmsnorm_pair(const float* resid, const uint16_t* norm_w, float eps,
+                                  const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
+                                  const float* bases, const float* scales, int64_t N, int64_t n_cb,
+                                  const float* down_bases, uint16_t* m, float* zp, void* stream);
+int32_t sx8_dec_gemv_zp_add(const uint16_t* m, const uint8_t* hdr, const uint8_t* levels,
+                            int32_t hdr_bytes, const float* zp, const float* scales, int64_t N,
+                            int64_t n_cb, const float* add, float* Y, void* stream);
+
 /* *tok = argmax(logits[0..n)) (first index among equal maxima), then *pos += 1. */
 int32_t sx8_dec_argmax_advance(const float* logits, int64_t n, int64_t* tok, int64_t* pos,
                                void* stream);

@@ -83,6 +83,8 @@ SIGNATURES = [
     ("sx8_dec_gemv_silu", _I32, [_P, _P, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P]),
     ("sx8_dec_gemv_silu_add", _I32, [_P, _P, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P, _P]),
     ("sx8_dec_gemv_add", _I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P, _P]),
+    ("sx8_dec_gemv_rmsnorm_pair", _I32, [_P, _P, ctypes.c_float, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _P, _P]),
+    ("sx8_dec_gemv_zp_add", _I32, [_P, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _P]),
 ]
 ABI_VERSION = 2
 

@@ -313,7 +313,8 @@ __device__ __forceinline__ void load_rec(BlockRec& o, sx8_rsrc hdr, sx8_rsrc lv,
 // range is <= 0, so step = 1e-10 throughout (m = 1e-10, e = 0); NaN endpoints make rlo
 // NaN as in the reference.  The four strategies are moved into the bytes of `sel` so
 // that one v_perm_b32 per table looks k1 and e up for all sub-blocks at once.
-__device__ __forceinline__ float block_dot(const BlockRec& o, const KbInfo& ki, const SpliceK& k) {
+__device__ __forceinline__ float block_dot_z(const BlockRec& o, const KbInfo& ki, float z0, float z1,
+                                             const SpliceK& k) {
     const float lo = sx8_h2f(o.lohi), hi = sx8_h2f(o.lohi >> 16);
     const float d = hi - lo;
     const float q = d * 0.25f;
@@ -324,7 +325,7 @@ __device__ __forceinline__ float block_dot(const BlockRec& o, const KbInfo& ki, 
     const uint32_t eb = d > 0.f ? __builtin_amdgcn_perm(0u, 0xFFFEFE00u, sel) : 0u;  // e[s]
     const float m = d > 0.f ? d * 0.015873f : 1e-10f;
     const uint32_t cf = o.cc >> 8;
-    float acc = (float)sx8_sext4(cf) * ki.z[0] + (float)sx8_sext4(cf >> 4) * ki.z[1];
+    float acc = (float)sx8_sext4(cf) * z0 + (float)sx8_sext4(cf >> 4) * z1;
     float T = 0.f;
     const uint32_t H[4] = {o.a.x, o.a.y, o.a.z, o.a.w};
 #pragma unroll
@@ -347,6 +348,10 @@ __device__ __forceinline__ float block_dot(const BlockRec& o, const KbInfo& ki, 
         T += __builtin_ldexpf(t, __builtin_amdgcn_sbfe((int)eb, 8 * sb, 8));
     }
     return __builtin_fmaf(m, T, acc);
+}
+
+__device__ __forceinline__ float block_dot(const BlockRec& o, const KbInfo& ki, const SpliceK& k) {
+    return block_dot_z(o, ki, ki.z[0], ki.z[1], k);
 }
 
 // v + (v of another lane), the lane picked by a DPP control (quad_perm, row mirrors).
@@ -399,6 +404,11 @@ __device__ __forceinline__ void tab_load(TabIn& t, const g_u16* __restrict__ X,
         t.b1[0] = b[8];
         t.b1[1] = b[9];
         t.s = scales[2 * kb + (q & 1)];
+    } else if constexpr (kMode == 4) {
+        // Z from two partial sums per K block and basis (laid out [kb][slot][basis], in
+        // the basis argument), then the scale: Z = (P0 + P1) * scale
+        const int c = q & 1;
+        t.s = (basis[(int64_t)kb * 4 + c] + basis[(int64_t)kb * 4 + 2 + c]) * scales[2 * kb + c];
     } else {
         t.s = Zin[2 * kb + (q & 1)];
     }
@@ -553,6 +563,42 @@ __device__ __forceinline__ void xraw_h(const XRaw& r, float h[8]) {
     for (int i = 0; i < 8; ++i) h[i] = (sx8_h2f(hw[i >> 1] >> (16 * (i & 1))) + a[i]) + d[i];
 }
 
+// RMSNorm scale of the work-group's h (every unit within the TP passes): h per unit, the
+// sum of h^2 over the work-group in a fixed order (so every work-group gets the same
+// value), 1 / sqrt(mean + eps).  One s_barrier; the LDS-only wait leaves the records in
+// flight.  red[0 .. 8) is used.
+template <int TP>
+__device__ __forceinline__ float rms_inv(const XRaw (&xr)[TP], float (&h)[TP][8], float* red, int n_units,
+                                         int K, float eps, int tid) {
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < TP; ++p) {
+        xraw_h(xr[p], h[p]);
+        if (p * kPanelThreads + tid < n_units) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(h[p][i], h[p][i], ss);
+        }
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __builtin_amdgcn_s_waitcnt(0xC07F);       // lgkmcnt(0): LDS only, records stay in flight
+    asm volatile("s_barrier" ::: "memory");
+    float tot = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < kPanelThreads / 64; ++wv) tot += red[wv];
+    return 1.0f / sqrtf(tot / (float)K + eps);
+}
+
+// x = fp16(h * inv * w) of one unit, as fp16 pairs
+__device__ __forceinline__ uint4 rms_x(const float (&h)[8], const uint4 w, float inv) {
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    uint32_t xw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        xw[i] = pack_h2(h[2 * i] * inv * sx8_h2f(ww[i]), h[2 * i + 1] * inv * sx8_h2f(ww[i] >> 16));
+    return make_uint4(xw[0], xw[1], xw[2], xw[3]);
+}
+
 // Table passes whose inputs are loaded before the weight records (the rest, for
 // n_cb > kTabPasses * 128, load after them).
 constexpr int kTabPassesShort = 1;   // n_cb <= 128
@@ -577,7 +623,9 @@ constexpr int kTabPassesLong = 3;    // n_cb <= 384
 // decode after it.
 //
 // kMode: 0 = copy the table k_kbinfo wrote into LDS; 1 = build it computing Z; 2 = build
-// it with Z from Zin; 3 = read k_kbinfo's table from global memory (n_cb > kLdsMaxKb).
+// it with Z from Zin; 3 = read k_kbinfo's table from global memory (n_cb > kLdsMaxKb);
+// 4 = build it with Z from two partial sums per K block (in the basis argument) and the
+// scales (the down projection after k_gemv_pair).
 // Work-groups go to the 8 XCDs round-robin by block index; panels are renumbered so each
 // XCD gets a contiguous column range and neighbouring panels share cache lines in one L2.
 // Weight matrices of one launch: every matrix multiplies the same x (same K); matrix m
@@ -636,7 +684,8 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     // The producer's inputs go out before anything else: with kPre they need no argument
     // load (a group's matrix fields are a memory round trip away).
     XRaw xr[kX == kXPlain ? 1 : TP];
-    if constexpr ((kMode == 1 || kMode == 2) && kX != kXPlain) {
+    constexpr bool kBuild = kMode == 1 || kMode == 2 || kMode == 4;   // table built in-kernel
+    if constexpr (kBuild && kX != kXPlain) {
         XRsrc xs;
         if constexpr (kPre) xs = xraw_rsrc_pre<kX>(X, hdr0, n_cb * 32);
         else xs = xraw_rsrc<kX>(xp, n_cb * 32);
@@ -686,7 +735,7 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     // them after the geometry).
     const int n_units = n_cb * 4;
     TabIn tin[TP];
-    if constexpr (kMode == 1 || kMode == 2) {
+    if constexpr (kBuild) {
 #pragma unroll
         for (int p = 0; p < TP; ++p) {
             const int u = min(p * kPanelThreads + tid, n_units - 1);
@@ -746,39 +795,17 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
         const uint4* src = reinterpret_cast<const uint4*>(table);
         uint4* dst = reinterpret_cast<uint4*>(info);
         for (int i = tid; i < n_cb * 7; i += kPanelThreads) dst[i] = src[i];
-    } else if constexpr (kMode == 1 || kMode == 2) {
+    } else if constexpr (kBuild) {
         if constexpr (kX == kXRms) {
             // every unit fits the TP passes (checked by the host): sum h^2 over the
             // work-group, then normalize; the sum's order is fixed, so every work-group
             // produces the same x
             float h[TP][8];
-            float ss = 0.f;
-#pragma unroll
-            for (int p = 0; p < TP; ++p) {
-                xraw_h(xr[p], h[p]);
-                if (p * kPanelThreads + tid < n_units) {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(h[p][i], h[p][i], ss);
-                }
-            }
-            ss = wave_sum(ss);
-            if ((tid & 63) == 0) red[tid >> 6] = ss;
-            __builtin_amdgcn_s_waitcnt(0xC07F);       // lgkmcnt(0): LDS only, records stay in flight
-            asm volatile("s_barrier" ::: "memory");
-            float tot = 0.f;
-#pragma unroll
-            for (int wv = 0; wv < kPanelThreads / 64; ++wv) tot += red[wv];
-            const float inv = 1.0f / sqrtf(tot / (float)(n_cb * 32) + xp.eps);
+            const float inv = rms_inv<TP>(xr, h, red, n_units, n_cb * 32, xp.eps, tid);
             const bool writer = !kPre && blockIdx.x == 0 && xp.resid_out != nullptr;
 #pragma unroll
             for (int p = 0; p < TP; ++p) {
-                const uint32_t ww[4] = {xr[p].w.x, xr[p].w.y, xr[p].w.z, xr[p].w.w};
-                uint32_t xw[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    xw[i] = pack_h2(h[p][2 * i] * inv * sx8_h2f(ww[i]),
-                                    h[p][2 * i + 1] * inv * sx8_h2f(ww[i] >> 16));
-                tin[p].x = make_uint4(xw[0], xw[1], xw[2], xw[3]);
+                tin[p].x = rms_x(h[p], xr[p].w, inv);
                 const int u = p * kPanelThreads + tid;
                 if (writer && u < n_units) {
                     float4* ro = reinterpret_cast<float4*>(xp.resid_out + (int64_t)u * 8);
@@ -954,7 +981,7 @@ void launch_panel(const PanelPlan& p, size_t smem, hipStream_t st, const uint16_
         else
             go(std::integral_constant<int, 2>{}, tp);
     };
-    if constexpr (kMode == 1 || kMode == 2) {
+    if constexpr (kMode == 1 || kMode == 2 || kMode == 4) {
         if (p.TP == kTabPassesLong) {
             by_ring(std::integral_constant<int, kTabPassesLong>{});
             return;
@@ -1364,4 +1391,292 @@ extern "C" int32_t sx8_dec_gemv_add(const uint16_t* x, int32_t n_mats, const uin
     if (rc != SX8_OK) return rc;
     return launch_fused<kXPlain>(what, XProd{}, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys,
                                  as_stream(stream), x, adds);
+}
+
+// ------------------------------------------------------------------ gate / up pairs
+
+namespace {
+
+// k_gemv_pair: the decoder MLP's gate and up GEMVs over one RMSNorm'd input in a single
+// launch, each work-group computing both for the same CTp columns (lanes alternate: even
+// lanes gate, odd lanes up).  The epilogue emits m = fp16(silu(g) u) (the arithmetic of
+// sx8_dec_silu_mul) and, for the down projection whose K blocks are these columns, the
+// partial PCA sums P[kb][slot][c] = sum_j m_j basis_d[kb][c][j % 32] over the panel's
+// columns j of block kb: with CTp >= 32 a block spans at most two panels, slot 0 comes
+// from the panel holding the block's first column and slot 1 from the next one (zero when
+// the block ends in the first).  The down GEMV then reads m and Z = (P0 + P1) scale
+// (kMode 4) instead of g, u and its bases.
+// Layout (checked by the host): the up matrix's headers, levels, bases and scales follow
+// the gate matrix's in memory, so one pointer per field, preloaded, covers both; h and
+// the norm weight are preloaded too.  Everything else is read late from PairArgs.
+struct PairArgs {
+    uint16_t* m;           // (N) fp16
+    const float* bas_d;    // down bases (N / 32, 64)
+    float* zp;             // (N / 32, 2, 2) partial sums
+    float eps;
+};
+
+template <int HB, int NR, int TP>
+__global__ __launch_bounds__(kPanelThreads) void k_gemv_pair(
+    const uint8_t* __restrict__ hdr, const uint8_t* __restrict__ lv, const float* __restrict__ resid, int N,
+    int n_cb, const uint16_t* __restrict__ nw, const float* __restrict__ bas, const float* __restrict__ sca,
+    const PairArgs pa) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* red = reinterpret_cast<float*>(smem);                 // 2 x 512 floats
+    KbInfo* info = reinterpret_cast<KbInfo*>(smem + sizeof(float) * 2 * kPanelThreads);
+    const int tid = threadIdx.x;
+    const int n_units = n_cb * 4;
+    // (1) h and the norm weight (preloaded pointers), then the bases of both matrices
+    XRaw xr[TP];
+    {
+        const XRsrc xs = xraw_rsrc_pre<kXRms>(resid, nw, n_cb * 32);
+#pragma unroll
+        for (int p = 0; p < TP; ++p) {
+            const int u = min(p * kPanelThreads + tid, n_units - 1);
+            xraw_load<kXRms, true>(xr[p], xs, u >> 2, u & 3);
+        }
+    }
+    asm volatile("" ::: "memory");
+    TabIn tg[TP], tu[TP];
+    const g_float* __restrict__ bg = to_global(bas);
+    const g_float* __restrict__ sg = to_global(sca);
+#pragma unroll
+    for (int p = 0; p < TP; ++p) {
+        const int u = min(p * kPanelThreads + tid, n_units - 1);
+        tab_load<1, false>(tg[p], nullptr, bg, sg, nullptr, u >> 2, u & 3);
+        tab_load<1, false>(tu[p], nullptr, bg + (int64_t)n_cb * 64, sg + (int64_t)n_cb * 2, nullptr, u >> 2, u & 3);
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+
+    // (2) geometry: CTp = 32..64 column pairs per panel (N <= 16384), CT = 2 CTp lanes per
+    // slice
+    int n_one = N;
+    asm volatile("" : "+s"(n_one));
+    const int CTp = max((n_one + 255) / 256, 32), CT = 2 * CTp;
+    const int S = kPanelThreads / CT, R = (n_cb + S - 1) / S;
+    const int j0 = tid / CT, c = tid - j0 * CT;
+    const int G = (n_one + CTp - 1) / CTp, xcd = blockIdx.x & 7;
+    const int panel = (int)(blockIdx.x >> 3) + xcd * (G >> 3) + min(xcd, G & 7);
+    const int mat = c & 1;
+    const int col = panel * CTp + (c >> 1);
+    const bool col_ok = col < N;
+    const uint32_t nn = (uint32_t)min(col, N - 1);
+    const bool lane_ok = j0 < S;
+    const int j = lane_ok ? j0 : n_cb;
+    const uint32_t n_blk = (uint32_t)n_cb * (uint32_t)N;
+    const sx8_rsrc rh = make_rsrc(hdr, (int64_t)n_blk * 2 * HB);
+    const sx8_rsrc rl = make_rsrc(lv, (int64_t)n_blk * 2 * 24);
+    const uint32_t bid0 = lane_ok ? (uint32_t)j * (uint32_t)N + nn + (mat ? n_blk : 0u) : 2 * n_blk;
+    const uint32_t dbid = lane_ok ? (uint32_t)S * (uint32_t)N : 0u;
+    auto load = [&](BlockRec& o, int r) { load_rec<HB>(o, rh, rl, bid0 + (uint32_t)r * dbid); };
+    constexpr int kNR0 = NR < 2 ? NR : 2;
+    BlockRec buf[NR];
+#pragma unroll
+    for (int i = 0; i < kNR0; ++i) {
+        load(buf[i], i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // (3) the table: x = RMSNorm(h), Z of the gate bases in z, of the up bases in pad
+    {
+        float h[TP][8];
+        const float inv = rms_inv<TP>(xr, h, red, n_units, n_cb * 32, pa.eps, tid);
+#pragma unroll
+        for (int p = 0; p < TP; ++p) {
+            const uint4 x = rms_x(h[p], xr[p].w, inv);
+            tg[p].x = x;
+            tu[p].x = x;
+            const int u = p * kPanelThreads + tid;
+            const int q = u & 3;
+            KbInfo& e = info[u < n_units ? u >> 2 : n_cb];
+            fill_x_side(e, q, x);
+            e.z[q & 1] = tab_z(tg[p], q);
+            e.pad[q & 1] = tab_z(tu[p], q);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = kNR0; i < NR; ++i) load(buf[i], i);
+    // the down bases of this lane's column, for the epilogue: requested now (the argument
+    // load behind pa.bas_d has arrived during the table build), used after the K loop
+    float bd0 = 0.f, bd1 = 0.f;
+    if (tid < CT && mat == 0 && col_ok) {
+        const int kb = col >> 5, jj = col & 31;
+        bd0 = pa.bas_d[(int64_t)kb * 64 + jj];
+        bd1 = pa.bas_d[(int64_t)kb * 64 + 32 + jj];
+    }
+
+    // (4) the K loop (as k_gemv_panel), each lane with its matrix's Z pair
+    const SpliceK sk = splice_consts();
+    float acc = 0.f;
+    auto step = [&](const BlockRec& rec, int r) {
+        BlockRec o = rec;
+        if constexpr (HB == 8) {
+            asm volatile("" : "+v"(o.lohi), "+v"(o.cc));
+        } else {
+            asm volatile("" : "+v"(o.lohi), "+v"(o.cc16));
+            o.cc = o.cc16;
+        }
+        asm volatile("" : "+v"(o.a.x), "+v"(o.a.y), "+v"(o.a.z), "+v"(o.a.w), "+v"(o.b.x), "+v"(o.b.y));
+        const int kb = j + r * S;
+        const KbInfo& ki = info[min(kb, n_cb - 1)];
+        const float4 zz = *reinterpret_cast<const float4*>(&ki.z[0]);   // z[0], z[1], pad[0], pad[1]
+        const float v = block_dot_z(o, ki, mat ? zz.z : zz.x, mat ? zz.w : zz.y, sk);
+        acc += (col_ok && kb < n_cb) ? v : 0.f;
+    };
+    int r = 0;
+    for (; r + NR < R; r += NR) {
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            step(buf[i], r + i);
+            __builtin_amdgcn_sched_barrier(0);
+            load(buf[i], r + NR + i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+        if (r + i < R) step(buf[i], r + i);
+
+    // (5) slices -> lanes in a fixed order (NG partial groups: 4 when CT > 64)
+    red[tid] = acc;
+    __syncthreads();
+    const int NG = CT > 64 ? 4 : 8;
+    if (tid < NG * CT) {
+        float t = 0.f;
+        int s = j0;
+        for (; s + 7 * NG < S; s += 8 * NG) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = red[(s + NG * i) * CT + c];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) t += v[i];
+        }
+        for (; s < S; s += NG) t += red[s * CT + c];
+        red[kPanelThreads + tid] = t;
+    }
+    __syncthreads();
+    float y = 0.f;
+    if (tid < CT)
+        for (int g = 0; g < NG; ++g) y += red[kPanelThreads + g * CT + tid];
+    // lane pairs (2i, 2i + 1) = (gate, up) of column i sit in one wave (64 is even)
+    const float yo = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, y), 0xB1,
+                                                                           0xF, 0xF, false));
+    // (6) m and the down projection's contributions m_j basis_d[kb][c][j % 32]
+    float* contrib = red;                  // [CTp][2] (the first half of red is free again)
+    if (tid < CT && mat == 0) {
+        float mv = 0.f;
+        if (col_ok) {
+            const uint16_t mh = __builtin_bit_cast(uint16_t, (_Float16)(y / (1.0f + __expf(-y)) * yo));
+            *(uint16_t SX8_GLOBAL_AS*)(pa.m + col) = mh;
+            mv = sx8_h2f(mh);
+        }
+        contrib[2 * (c >> 1)] = mv * bd0;
+        contrib[2 * (c >> 1) + 1] = mv * bd1;
+    }
+    __syncthreads();
+    const int c0 = panel * CTp, c1 = min(c0 + CTp, N);
+    if (c0 < c1) {
+        const int kbf = c0 >> 5, kbl = (c1 - 1) >> 5;
+        if (tid < 2 * (kbl - kbf + 1)) {
+            const int kb = kbf + (tid >> 1), cc = tid & 1;
+            const int lo = max(32 * kb, c0), hi = min(32 * kb + 32, c1);
+            float sum = 0.f;
+            for (int q = lo; q < hi; ++q) sum += contrib[2 * (q - c0) + cc];
+            const int slot = 32 * kb >= c0 ? 0 : 1;
+            pa.zp[((int64_t)kb * 2 + slot) * 2 + cc] = sum;
+            // the block ends in this panel: nobody else writes its slot 1
+            if (slot == 0 && min(32 * kb + 32, N) <= c1) pa.zp[((int64_t)kb * 2 + 1) * 2 + cc] = 0.f;
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" int32_t sx8_dec_gemv_rmsnorm_pair(const float* resid, const uint16_t* norm_w, float eps,
+                                             const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
+                                             const float* bases, const float* scales, int64_t N, int64_t n_cb,
+                                             const float* down_bases, uint16_t* m, float* zp, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_dec_gemv_rmsnorm_pair";
+    if (!resid || !norm_w || !hdr || !levels || !bases || !scales || !down_bases || !m || !zp)
+        return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (hdr_bytes != 6 && hdr_bytes != 8)
+        return fail(SX8_ERR_INVALID, "%s: hdr_bytes must be 6 or 8, got %d", what, hdr_bytes);
+    // panels of 32..64 column pairs (a K block of the down projection spans at most two)
+    if (N < 32 || N > 16384 || N % 32)
+        return fail(SX8_ERR_UNSUPPORTED, "%s: N must be a multiple of 32 in 32..16384, got %lld", what,
+                    (long long)N);
+    if (n_cb <= 0 || n_cb * 4 > (int64_t)kTabPassesLong * kPanelThreads)
+        return fail(SX8_ERR_UNSUPPORTED, "%s: n_cb %lld outside 1..%d", what, (long long)n_cb,
+                    kTabPassesLong * kPanelThreads / 4);
+    if (!aligned(resid, 16) || !aligned(norm_w, 16) || !aligned(hdr, hdr_bytes == 8 ? 8 : 2) ||
+        !aligned(levels, 8) || !aligned(bases, 16) || !aligned(scales, 4) || !aligned(down_bases, 4) ||
+        !aligned(m, 2) || !aligned(zp, 4))
+        return fail(SX8_ERR_INVALID, "%s: misaligned pointer", what);
+    const int64_t n_blk = N * n_cb;
+    if ((n_cb + (int64_t)(kRing + 1) * kPanelThreads) * N * 24 * 2 >= ((int64_t)1 << 31))
+        return fail(SX8_ERR_UNSUPPORTED, "%s: %lld x %lld blocks exceed 32-bit offsets", what, (long long)N,
+                    (long long)n_cb);
+    (void)n_blk;
+    const int CTp = std::max((int)((N + 255) / 256), 32);
+    const unsigned grid = (unsigned)((N + CTp - 1) / CTp);
+    const int TP = n_cb <= 128 * kTabPassesShort ? kTabPassesShort : kTabPassesLong;
+    const size_t smem = panel_smem((int)n_cb, true);
+    const PairArgs pa{m, down_bases, zp, eps};
+    const hipStream_t st = as_stream(stream);
+    auto go = [&](auto hb, auto tp) {
+        constexpr int HB = decltype(hb)::value, TPv = decltype(tp)::value;
+        hipLaunchKernelGGL((k_gemv_pair<HB, kRing, TPv>), dim3(grid), dim3(kPanelThreads), smem, st, hdr, levels,
+                           resid, (int)N, (int)n_cb, norm_w, bases, scales, pa);
+    };
+    auto by_tp = [&](auto hb) {
+        if (TP == kTabPassesLong) go(hb, std::integral_constant<int, kTabPassesLong>{});
+        else go(hb, std::integral_constant<int, kTabPassesShort>{});
+    };
+    if (hdr_bytes == 8) by_tp(std::integral_constant<int, 8>{});
+    else by_tp(std::integral_constant<int, 6>{});
+    return check_launch(what);
+}
+
+// The down projection after sx8_dec_gemv_rmsnorm_pair: Y = adds + W_down m with Z from the
+// pair's partial sums (kMode 4); a residual updated in place (adds == Y) is read from the
+// preloaded output slot.
+extern "C" int32_t sx8_dec_gemv_zp_add(const uint16_t* m, const uint8_t* hdr, const uint8_t* levels,
+                                       int32_t hdr_bytes, const float* zp, const float* scales, int64_t N,
+                                       int64_t n_cb, const float* add, float* Y, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_dec_gemv_zp_add";
+    if (!m || !hdr || !levels || !zp || !scales || !add || !Y) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (hdr_bytes != 6 && hdr_bytes != 8)
+        return fail(SX8_ERR_INVALID, "%s: hdr_bytes must be 6 or 8, got %d", what, hdr_bytes);
+    if (N <= 0 || N > 0x7FFFFFFF / 2) return fail(SX8_ERR_INVALID, "%s: bad N %lld", what, (long long)N);
+    if (n_cb <= 0 || n_cb * 4 > (int64_t)kTabPassesLong * kPanelThreads)
+        return fail(SX8_ERR_UNSUPPORTED, "%s: n_cb %lld outside 1..%d", what, (long long)n_cb,
+                    kTabPassesLong * kPanelThreads / 4);
+    if (!aligned(m, 16) || !aligned(hdr, hdr_bytes == 8 ? 8 : 2) || !aligned(levels, 8) || !aligned(zp, 4) ||
+        !aligned(scales, 4) || !aligned(add, 4) || !aligned(Y, 4))
+        return fail(SX8_ERR_INVALID, "%s: misaligned pointer", what);
+    const int64_t N64 = N;
+    const PanelPlan p = plan_panels(&N64, 1, (int)n_cb);
+    if (!offsets_fit(p, N, n_cb))
+        return fail(SX8_ERR_UNSUPPORTED, "%s: %lld x %lld blocks exceed 32-bit offsets", what, (long long)N,
+                    (long long)n_cb);
+    GemvGroup g{};
+    g.n_mats = 1;
+    g.ct = p.CT;
+    const bool resy = add == Y;
+    // the partial sums travel in the basis slot (kMode 4)
+    g.m[0] = GemvMat{hdr, levels, zp, scales, nullptr, Y, resy ? nullptr : add, (int)N, (int)p.grid};
+    const size_t smem = panel_smem((int)n_cb, true);
+    const hipStream_t st = as_stream(stream);
+    auto run = [&](auto hb) {
+        constexpr int HB = decltype(hb)::value;
+        if (resy) launch_panel<HB, 4, kXPlain, false, true>(p, smem, st, m, g, nullptr, (int)n_cb);
+        else launch_panel<HB, 4, kXPlain>(p, smem, st, m, g, nullptr, (int)n_cb);
+    };
+    if (hdr_bytes == 8) run(std::integral_constant<int, 8>{});
+    else run(std::integral_constant<int, 6>{});
+    return check_launch(what);
 }

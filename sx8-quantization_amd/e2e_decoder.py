@@ -55,6 +55,18 @@ def clone_linear(lin):
     return new
 
 
+def pair_storage(a, b):
+    """Move the device tensors of `a` and `b` into one allocation per field, b's right after
+    a's (both keep views of it): sx8_dec_gemv_rmsnorm_pair addresses a matrix pair through
+    the first matrix's pointers."""
+    ta, tb = [], []
+    for x, y in zip(a._t44, b._t44):
+        buf = torch.cat([x.reshape(-1), y.reshape(-1)])
+        ta.append(buf[:x.numel()].view(x.shape))
+        tb.append(buf[x.numel():].view(y.shape))
+    a._t44, b._t44 = tuple(ta), tuple(tb)
+
+
 class Layer(nn.Module):
     def __init__(self, cfg, lins, device):
         super().__init__()
@@ -95,6 +107,7 @@ class SX8Decoder(nn.Module):
             src = base[i % n_distinct]
             lins = src if i < n_distinct else [clone_linear(l) for l in src]
             layers.append(Layer(cfg, lins, device))
+            pair_storage(layers[-1].gate, layers[-1].up)
         self.layers = layers
         self.head = sx8_linear(cfg["vocab"], H, gen, device)      # tied lm_head / embedding
         self.embed = SX8EmbeddingV44(self.head.qt, self.head.bases_info, hdr_bytes=6)
@@ -304,10 +317,10 @@ class SX8Decoder(nn.Module):
              "q": torch.zeros(nh * hd, **f32), "k": torch.zeros(nk * hd, **f32),
              "v": torch.zeros(nk * hd, **f32), "a": torch.zeros(nh * hd, **f16),
              "logits": torch.zeros(V, **f32)}
-        # gate and up outputs adjacent (u = g + I): the down GEMV then takes both from one
-        # preloaded kernel argument
-        gu = torch.zeros(2, I, **f32)
-        z["g"], z["u"] = gu[0], gu[1]
+        # the MLP in two launches: m = silu(W_gate x) * W_up x and the down projection's
+        # partial PCA sums zp from the gate/up pair, then the down GEMV from m and zp
+        z["m"] = torch.zeros(I, **f16)
+        z["zp"] = torch.zeros(I // 32, 2, 2, **f32)
         z["attn_ws"] = torch.zeros(int(_L.lib().sx8_dec_attn_workspace_bytes(nh, hd)) // 4 + 64, **f32)
         # grouped GEMV arguments (q/k/v and gate/up share their input): ctypes arrays of
         # device pointers, built once per layer; the o and down GEMVs add their output to
@@ -315,8 +328,6 @@ class SX8Decoder(nn.Module):
         z["groups"] = []
         for ly in self.layers:
             z["groups"].append((self._group_args((ly.q, ly.k, ly.v), (z["q"], z["k"], z["v"])),
-                                self._group_args((ly.gate, ly.up), (z["g"], z["u"])),
-                                self._group_args((ly.down,), (z["ra"],)),
                                 self._group_args((ly.o,), (z["ra"],))))
         z["resid_adds"] = (ctypes.c_void_p * 1)(z["ra"].data_ptr())
         z["head_group"] = self._group_args((self.head,), (z["logits"],))
@@ -333,11 +344,6 @@ class SX8Decoder(nn.Module):
                 P(*[y.data_ptr() for y in ys]))
 
     @staticmethod
-    def _gemv_group(args, x, st):
-        n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
-        _L.call("sx8_gemv_group", _L.ptr(x), n, hdrs, lvls, 6, bas, sca, None, ns, n_cb, ys, None, 0, st)
-
-    @staticmethod
     def _gemv_rms(args, resid, init, delta, w, resid_out, eps, st):
         """GEMVs of `args` on RMSNorm((init or resid) + delta) * w, the sum to resid_out."""
         n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
@@ -347,17 +353,15 @@ class SX8Decoder(nn.Module):
                 P(w), eps, P(resid_out) if resid_out is not None else None, n, hdrs, lvls, 6, bas,
                 sca, ns, n_cb, ys, st)
 
-    @staticmethod
-    def _gemv_silu(args, g, u, st):
-        n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
-        _L.call("sx8_dec_gemv_silu", _L.ptr(g), _L.ptr(u), n, hdrs, lvls, 6, bas, sca, ns, n_cb, ys, st)
-
-    @staticmethod
-    def _gemv_silu_add(args, g, u, adds, st):
-        """Ys = adds + W silu(g) * u (the residual add in the GEMV's store)."""
-        n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
-        _L.call("sx8_dec_gemv_silu_add", _L.ptr(g), _L.ptr(u), n, hdrs, lvls, 6, bas, sca, ns, n_cb, adds,
-                ys, st)
+    def _mlp_fused(self, ly, r, eps, st):
+        """r += W_down (silu(W_gate x) * W_up x), x = RMSNorm(r) * post_norm, in two launches."""
+        z, P = self._fz, _L.ptr
+        gh, gl, gb, gs = ly.gate._t44
+        dh, dl, db, ds = ly.down._t44
+        _L.call("sx8_dec_gemv_rmsnorm_pair", P(r), P(ly.post_norm), eps, P(gh), P(gl), 6, P(gb), P(gs),
+                ly.gate.out_f, ly.gate.qt["n_cb"], P(db), P(z["m"]), P(z["zp"]), st)
+        _L.call("sx8_dec_gemv_zp_add", P(z["m"]), P(dh), P(dl), 6, P(z["zp"]), P(ds), ly.down.out_f,
+                ly.down.qt["n_cb"], P(r), P(r), st)
 
     @staticmethod
     def _gemv_add(args, x, adds, st):
@@ -369,9 +373,10 @@ class SX8Decoder(nn.Module):
     def decode_step_fused(self, tok, pos):
         """decode_step with the per-token ops as single HIP launches (sx8_decoder.h) and the
         GEMVs called through the C ABI; the residual stream is float32.  Each RMSNorm runs
-        inside the GEMV that consumes it (sx8_dec_gemv_rmsnorm: q/k/v, gate/up, lm_head),
-        SiLU * up inside the down GEMV, and both residual adds inside the GEMVs that produce
-        them (sx8_dec_gemv_add for o, sx8_dec_gemv_silu_add for down: the stream ra is
+        inside the GEMV that consumes it (sx8_dec_gemv_rmsnorm: q/k/v, lm_head;
+        sx8_dec_gemv_rmsnorm_pair: gate/up, whose epilogue also forms silu(g) * u and the
+        down projection's PCA sums), and both residual adds inside the GEMVs that produce
+        them (sx8_dec_gemv_add for o, sx8_dec_gemv_zp_add for down: the stream ra is
         updated in place); q/k norm + RoPE + KV-cache write inside attention
         (sx8_dec_attn_rope): per layer one launch each for q/k/v, attention (two: chunks,
         combine), o, gate/up and down."""
@@ -384,7 +389,7 @@ class SX8Decoder(nn.Module):
         L = self.max_len
         r, adds = z["ra"], z["resid_adds"]
         for li, ly in enumerate(self.layers):
-            g_qkv, g_gu, g_dn, g_o = z["groups"][li]
+            g_qkv, g_o = z["groups"][li]
             if li == 0:                                             # h = embedding row -> r
                 self._gemv_rms(g_qkv, None, emb, None, ly.in_norm, r, eps, st)
             else:                                                   # h = r
@@ -395,8 +400,7 @@ class SX8Decoder(nn.Module):
                     P(z["a"]), nh, nk, hd, L, 1.0 / math.sqrt(hd), eps, P(z["attn_ws"]),
                     z["attn_ws"].numel() * 4, st)
             self._gemv_add(g_o, z["a"], adds, st)                   # r += W_o a
-            self._gemv_rms(g_gu, r, None, None, ly.post_norm, None, eps, st)
-            self._gemv_silu_add(g_dn, z["g"], z["u"], adds, st)    # r += W_down silu(g) u
+            self._mlp_fused(ly, r, eps, st)                         # r += W_down silu(g) u
         self._gemv_rms(z["head_group"], r, None, None, self.final_norm, None, eps, st)
         _L.call("sx8_dec_argmax_advance", P(z["logits"]), cfg["vocab"], P(tok), P(pos), st)
         return tok

@@ -413,3 +413,68 @@ def test_attn_rope_matches_two_calls(hiplib, cuda, nh, nk, hd, L, positions):
         assert dk <= 2e-3 * kc1[:, p].float().abs().max().item(), dk
         o1, o2 = out1.cpu().float(), out2.cpu().float()
         assert (o1 - o2).abs().max().item() <= 5e-3 * o1.abs().max().item()
+
+
+@pytest.mark.parametrize("H,I", [(2560, 9728), (1024, 8224), (512, 1056)])
+def test_gemv_pair_and_zp_down(hiplib, cuda, H, I):
+    """sx8_dec_gemv_rmsnorm_pair + sx8_dec_gemv_zp_add against the three-launch MLP
+    (sx8_dec_gemv_rmsnorm over gate and up as a group, sx8_dec_silu_mul, sx8_dec_gemv_add):
+    m within one fp16 step (g and u are summed in another order), the partial sums' Z
+    against sx8_compute_z on the same m, and the down GEMV from the partial sums against
+    sx8_dec_gemv_add on the same m.  I = 8224 leaves the last panel partly empty; I = 1056
+    runs at the 32-pair minimum panel width."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    eps = 1e-6
+    gu = _mats(cuda, [I, I], H, 80 + H)
+    (dh, dl, db, ds), = _mats(cuda, [H], I, 90 + H)
+    # the up matrix's arrays right behind the gate matrix's
+    cat = [torch.cat([gu[0][f].reshape(-1), gu[1][f].reshape(-1)]) for f in range(4)]
+    g = torch.Generator().manual_seed(H)
+    resid = torch.randn(H, generator=g).to(cuda)
+    w = (torch.rand(H, generator=g) + 0.5).half().to(cuda)
+    y_gu = torch.empty(2, I, device=cuda)
+    n, hd, lv, bs, sc, ns, n_cb, ys = _group(gu, [I, I], H // 32, [y_gu[0], y_gu[1]])
+    _L.call("sx8_dec_gemv_rmsnorm", P(resid), None, None, P(w), eps, None, n, hd, lv, 6, bs, sc, ns, n_cb,
+            ys, st)
+    m_ref = torch.empty(I, dtype=torch.float16, device=cuda)
+    _L.call("sx8_dec_silu_mul", P(y_gu[0]), P(y_gu[1]), P(m_ref), I, st)
+    m = torch.full((I,), float("nan"), dtype=torch.float16, device=cuda)
+    zp = torch.full((I // 32, 2, 2), float("nan"), device=cuda)
+    _L.call("sx8_dec_gemv_rmsnorm_pair", P(resid), P(w), eps, P(cat[0]), P(cat[1]), 6, P(cat[2]), P(cat[3]),
+            I, H // 32, P(db), P(m), P(zp), st)
+    torch.cuda.synchronize()
+    mf, mr = m.cpu().float(), m_ref.cpu().float()
+    assert torch.isfinite(mf).all()
+    step = torch.where(mr.abs() < 2.0 ** -14, torch.full_like(mr, 2.0 ** -24),
+                       2.0 ** (torch.floor(torch.log2(mr.abs().clamp_min(2.0 ** -14))) - 10))
+    assert ((mf - mr).abs() <= step).all()
+    assert (mf == mr).float().mean().item() > 0.99
+    # Z from the partial sums against sx8_compute_z on the pair's own m
+    z_ref = torch.empty(I // 32, 2, device=cuda)
+    _L.call("sx8_compute_z", P(m), 1, I, P(db), P(ds), I // 32, P(z_ref), st)
+    torch.cuda.synchronize()
+    zpc = zp.cpu()
+    assert torch.isfinite(zpc).all()
+    z = (zpc[:, 0, :] + zpc[:, 1, :]) * ds.cpu().view(I // 32, 2)
+    zr = z_ref.cpu()
+    assert (z - zr).abs().max().item() <= 1e-5 * zr.abs().max().item()
+    # the down GEMV: partial sums vs its own Z, separate output and in place
+    res = torch.randn(H, generator=g).to(cuda)
+    y_ref = res.clone()
+    n, hd, lv, bs, sc, ns, n_cb, ys = _group([(dh, dl, db, ds)], [H], I // 32, [y_ref])
+    adds = (ctypes.c_void_p * 1)(y_ref.data_ptr())
+    _L.call("sx8_dec_gemv_add", P(m), n, hd, lv, 6, bs, sc, ns, n_cb, adds, ys, st)
+    y = torch.full((H,), float("nan"), device=cuda)
+    _L.call("sx8_dec_gemv_zp_add", P(m), P(dh), P(dl), 6, P(zp), P(ds), H, I // 32, P(res), P(y), st)
+    y_in = res.clone()
+    _L.call("sx8_dec_gemv_zp_add", P(m), P(dh), P(dl), 6, P(zp), P(ds), H, I // 32, P(y_in), P(y_in), st)
+    torch.cuda.synchronize()
+    scale = (y_ref - res).abs().max().item()
+    for out in (y, y_in):
+        assert (out - y_ref).abs().max().item() <= 1e-5 * scale
+    with pytest.raises(RuntimeError, match="multiple of 32"):
+        _L.call("sx8_dec_gemv_rmsnorm_pair", P(resid), P(w), eps, P(cat[0]), P(cat[1]), 6, P(cat[2]),
+                P(cat[3]), I - 16, H // 32, P(db), P(m), P(zp), st)
