@@ -22,6 +22,8 @@
 //     split K into ranges of whole 4-block groups and add the partials in a fixed order.
 #include <algorithm>
 #include <climits>
+#include <cstdio>
+#include <cstdlib>
 #include <mutex>
 
 #include "sx8_buffer.h"
@@ -991,44 +993,71 @@ Plan plan_k_gemm(int64_t M, int64_t N, int64_t NB, int64_t n_cb, int MF, int64_t
     return best;
 }
 
-// 512-row tiles: Tf = 0 (every tile split St ways) or the whole rounds of 256 tiles with
-// the remainder split; St from 1 to 8.
+// 512-row tiles, the first Tf (0 or whole rounds of 256) over the whole K and the rest in
+// St K ranges.
+Plan make_w1(int64_t M, int64_t NB, int64_t n_cb, int64_t Tf, int64_t St) {
+    const int64_t T = ((M + kW1BM - 1) / kW1BM) * NB;
+    const int64_t groups = (n_cb + 3) / 4;
+    const int64_t rem = T - Tf;
+    Plan p{};
+    p.w1 = true;
+    p.MF = kW1MF;
+    p.Tf = (int)Tf;
+    p.kbs = (int)(4 * ((groups + St - 1) / St));
+    p.St = (int)((n_cb + p.kbs - 1) / p.kbs);
+    p.n_split = p.St > 1 ? rem : 0;
+    p.G = Tf + rem * p.St;
+    const double tile_bytes = (double)kW1BM * kBN * 4.0;
+    p.cost = (double)(Tf / 256) * n_cb * kW1Cost + (double)((rem * p.St + 255) / 256) * p.kbs * kW1Cost +
+             (p.St > 1 ? (double)rem * (p.St + 1) * tile_bytes * 2.0 / kBytesPerUnit : 0.0);
+    return p;
+}
+
+// Tf = 0 (every tile split St ways) or the whole rounds of 256 tiles with the remainder
+// split; St from 1 to 8.
 Plan plan_w1(int64_t M, int64_t NB, int64_t n_cb, int64_t part_cap) {
     const int64_t T = ((M + kW1BM - 1) / kW1BM) * NB;
     const int64_t groups = (n_cb + 3) / 4;
     Plan best{};
     best.cost = 1e300;
     for (int64_t Tf : {int64_t(0), T / 256 * 256}) {
-        const int64_t rem = T - Tf;
         for (int64_t St = 1; St <= std::min<int64_t>(8, groups); ++St) {
-            Plan p{};
-            p.w1 = true;
-            p.MF = kW1MF;
-            p.Tf = (int)Tf;
-            p.kbs = (int)(4 * ((groups + St - 1) / St));
-            p.St = (int)((n_cb + p.kbs - 1) / p.kbs);
-            p.n_split = p.St > 1 ? rem : 0;
-            p.G = Tf + rem * p.St;
-            const double tile_bytes = (double)kW1BM * kBN * 4.0;
-            p.cost = (double)(Tf / 256) * n_cb * kW1Cost +
-                     (double)((rem * p.St + 255) / 256) * p.kbs * kW1Cost +
-                     (p.St > 1 ? (double)rem * (p.St + 1) * tile_bytes * 2.0 / kBytesPerUnit : 0.0);
+            const Plan p = make_w1(M, NB, n_cb, Tf, St);
             if (p.cost < best.cost && p.n_split * (p.St - 1) * kW1BM * kBN * 4 <= part_cap) best = p;
-            if (rem == 0) break;
+            if (Tf == T) break;
         }
     }
     return best;
 }
 
 // N columns in NB column tiles (a group pads every matrix to whole tiles).
-// SX8_GEMM_TILE=256 or 512 forces a tile height (tuning); otherwise the cheaper plan.
-// part_cap bounds the split-K partial bytes (the unsplit plans need none).
+// Tuning knobs: SX8_GEMM_TILE=256 or 512 forces a tile height; SX8_GEMM_PLAN forces one plan,
+// "k<MF>:<S>" (128 MF-row tiles in S K ranges) or "w<0|1>:<St>" (512-row tiles, 1: whole
+// rounds first, St K ranges for the rest); otherwise the cheaper plan.  part_cap bounds the
+// split-K partial bytes (the unsplit plans need none).
 Plan plan_gemm(int64_t M, int64_t N, int64_t NB, int64_t n_cb, int64_t part_cap = INT64_MAX) {
     const int MF = M > 128 ? 2 : 1;
-    const Plan p256 = plan_k_gemm(M, N, NB, n_cb, MF, part_cap);
     // k_gemm_w1 addresses rows up to the next multiple of 512 with 31-bit offsets
     const int64_t Mp = (M + kW1BM - 1) / kW1BM * kW1BM;
     const bool w1_ok = M > 256 && Mp / 32 * n_cb * 2048 <= 0x7FFFFFFF && Mp * n_cb * 8 <= 0x7FFFFFFF;
+    if (const char* f = getenv("SX8_GEMM_PLAN")) {
+        char kind = 0;
+        int a = 0, b = 0;
+        const int64_t groups = (n_cb + 3) / 4;
+        if (sscanf(f, "%c%d:%d", &kind, &a, &b) == 3 && b >= 1 && b <= std::min<int64_t>(8, groups)) {
+            if (kind == 'k' && (a == 1 || a == 2)) {
+                const int64_t T = ((M + 128 * a - 1) / (128 * a)) * NB;
+                const Plan p = plan_split(M, N, T, n_cb, b, a);
+                if ((int64_t)(p.S - 1) * M * N * 4 <= part_cap) return p;
+            }
+            if (kind == 'w' && (a == 0 || a == 1) && w1_ok) {
+                const int64_t T = ((M + kW1BM - 1) / kW1BM) * NB;
+                const Plan p = make_w1(M, NB, n_cb, a ? T / 256 * 256 : 0, b);
+                if (p.n_split * (p.St - 1) * kW1BM * kBN * 4 <= part_cap) return p;
+            }
+        }
+    }
+    const Plan p256 = plan_k_gemm(M, N, NB, n_cb, MF, part_cap);
     if (!w1_ok) return p256;
     const Plan p512 = plan_w1(M, NB, n_cb, part_cap);
     const char* e = getenv("SX8_GEMM_TILE");
