@@ -721,8 +721,9 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     };
     const g_float* __restrict__ basis = to_global(kOne ? bas0 : pick([](const GemvMat& g) { return g.basis; }));
     const g_float* __restrict__ scales = to_global(kOne ? sca0 : pick([](const GemvMat& g) { return g.scales; }));
+    // (a single matrix's Z arrives in the preloaded basis slot)
     const g_float* __restrict__ Zin = to_global(
-        kMode != 2 ? nullptr : kOne ? grp.m[0].Zin : pick([](const GemvMat& g) { return g.Zin; }));
+        kMode != 2 ? nullptr : kOne ? bas0 : pick([](const GemvMat& g) { return g.Zin; }));
     // (X laundered through an empty asm: a load from the read-only argument itself could be
     // moved past the ordering point below, behind the divisions)
     const uint16_t* xa = X;
@@ -962,12 +963,14 @@ void launch_panel(const PanelPlan& p, size_t smem, hipStream_t st, const uint16_
     constexpr bool kAllowOne = !(kPre && kX == kXRms);
     constexpr bool kAllowGroup = !(kPre && kX == kXSilu) && !kResY;
     const uint8_t* h0 = (kPre && kX == kXRms) ? reinterpret_cast<const uint8_t*>(xp.w) : m0.hdr;
+    // a single matrix with Z given (kMode 2) takes Z in the basis slot, which is preloaded
+    const float* b0 = kMode == 2 ? m0.Zin : m0.basis;
     auto go = [&](auto nr, auto tp) {
         constexpr int NR = decltype(nr)::value, TP = decltype(tp)::value;
         if constexpr (kAllowOne) {
             if (one) {
                 hipLaunchKernelGGL((k_gemv_panel<HB, kMode, NR, TP, kX, true, kPre, kResY>), grid, block, smem, st,
-                                   h0, m0.levels, X, m0.N, n_cb, m0.basis, m0.scales, m0.Y, g, table, xp);
+                                   h0, m0.levels, X, m0.N, n_cb, b0, m0.scales, m0.Y, g, table, xp);
                 return;
             }
         }
@@ -1576,18 +1579,23 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_pair(
         contrib[2 * (c >> 1) + 1] = mv * bd1;
     }
     __syncthreads();
+    // per (block, basis) 32 lanes, lane t holding column 32 kb + t's contribution (zero
+    // outside the panel), summed by an xor tree (a fixed order)
     const int c0 = panel * CTp, c1 = min(c0 + CTp, N);
     if (c0 < c1) {
         const int kbf = c0 >> 5, kbl = (c1 - 1) >> 5;
-        if (tid < 2 * (kbl - kbf + 1)) {
-            const int kb = kbf + (tid >> 1), cc = tid & 1;
-            const int lo = max(32 * kb, c0), hi = min(32 * kb + 32, c1);
-            float sum = 0.f;
-            for (int q = lo; q < hi; ++q) sum += contrib[2 * (q - c0) + cc];
-            const int slot = 32 * kb >= c0 ? 0 : 1;
-            pa.zp[((int64_t)kb * 2 + slot) * 2 + cc] = sum;
-            // the block ends in this panel: nobody else writes its slot 1
-            if (slot == 0 && min(32 * kb + 32, N) <= c1) pa.zp[((int64_t)kb * 2 + 1) * 2 + cc] = 0.f;
+        if (tid < 64 * (kbl - kbf + 1)) {             // whole 32-lane groups
+            const int t = tid & 31, cc = (tid >> 5) & 1, kb = kbf + (tid >> 6);
+            const int q = 32 * kb + t;
+            float sum = q >= c0 && q < c1 ? contrib[2 * (q - c0) + cc] : 0.f;
+#pragma unroll
+            for (int off = 16; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 32);
+            if (t == 0) {
+                const int slot = 32 * kb >= c0 ? 0 : 1;
+                pa.zp[((int64_t)kb * 2 + slot) * 2 + cc] = sum;
+                // the block ends in this panel: nobody else writes its slot 1
+                if (slot == 0 && min(32 * kb + 32, N) <= c1) pa.zp[((int64_t)kb * 2 + 1) * 2 + cc] = 0.f;
+            }
         }
     }
 }
