@@ -161,6 +161,20 @@ int32_t sx8_dec_gemv_zp_add(const uint16_t* m, const uint8_t* hdr, const uint8_t
                             int32_t hdr_bytes, const float* zp, const float* scales, int64_t N,
                             int64_t n_cb, const float* add, float* Y, void* stream);
 
+/* The lm_head step of a decode: logits = W · fp16(resid · rsqrt(mean(resid^2) + eps) · norm_w)
+ * (sx8_dec_gemv_rmsnorm on one matrix), then *tok = argmax(logits) (first index among
+ * equal maxima, as sx8_dec_argmax_advance) and *pos += 1.  Each GEMV work-group also
+ * writes the best of its own columns to parts (sx8_dec_argmax_parts_bytes(N, n_cb) bytes,
+ * 8-byte aligned), so the argmax launch scans those instead of the N logits.  No
+ * reference counterpart (the reference takes torch.argmax of the Hugging Face logits,
+ * scripts/infer_sx8.py). */
+int64_t sx8_dec_argmax_parts_bytes(int64_t N, int64_t n_cb);
+int32_t sx8_dec_gemv_rmsnorm_argmax(const float* resid, const uint16_t* norm_w, float eps,
+                                    const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
+                                    const float* bases, const float* scales, int64_t N, int64_t n_cb,
+                                    float* logits, void* parts, int64_t parts_bytes, int64_t* tok,
+                                    int64_t* pos, void* stream);
+
 /* *tok = argmax(logits[0..n)) (first index among equal maxima), then *pos += 1. */
 int32_t sx8_dec_argmax_advance(const float* logits, int64_t n, int64_t* tok, int64_t* pos,
                                void* stream);

@@ -78,6 +78,9 @@ SIGNATURES = [
                                  ctypes.c_float, ctypes.c_float, _P, _I64, _P]),
     ("sx8_dec_silu_mul", _I32, [_P, _P, _P, _I64, _P]),
     ("sx8_dec_argmax_advance", _I32, [_P, _I64, _P, _P, _P]),
+    ("sx8_dec_argmax_parts_bytes", _I64, [_I64, _I64]),
+    ("sx8_dec_gemv_rmsnorm_argmax", _I32, [_P, _P, ctypes.c_float, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P,
+                                           _I64, _P, _P, _P]),
     ("sx8_dec_gemv_rmsnorm", _I32, [_P, _P, _P, _P, ctypes.c_float, _P, _I32, _P, _P, _I32, _P, _P, _P,
                                     _I64, _P, _P]),
     ("sx8_dec_gemv_silu", _I32, [_P, _P, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P]),

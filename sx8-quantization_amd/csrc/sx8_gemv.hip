@@ -23,6 +23,7 @@
 //     loads that read zeros past the end) and panels are renumbered per XCD (see
 //     k_gemv_panel).
 #include <algorithm>
+#include <climits>
 #include <type_traits>
 
 #include "sx8_buffer.h"
@@ -462,6 +463,7 @@ struct XProd {
     const float* g;
     const float* u;
     float eps;
+    uint32_t* amax;   // kXRms, one matrix: per panel (max bits, first index of the max), or null
 };
 
 // Raw producer inputs of one table unit (kb, q): 8 consecutive elements 32 kb + 8 q.
@@ -897,6 +899,7 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
         red[kPanelThreads + tid] = t;
     }
     __syncthreads();
+    float yv = -INFINITY;
     if (tid < CT && col_ok) {
         float t = 0.f;
 #pragma unroll
@@ -909,6 +912,67 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
             if (add) t = *(const g_float*)(add + n) + t;
         }
         *(float SX8_GLOBAL_AS*)(Y + n) = t;
+        yv = t;
+    }
+    // argmax partials (lm_head): the panel's best column -- larger value, or equal value and
+    // lower index, so the maxima of the panels give the first index of the overall maximum;
+    // a NaN never wins -- from the CT <= 64 columns of wave 0
+    if constexpr (kX == kXRms && kOne) {
+        if (xp.amax != nullptr && tid < 64) {
+            const bool mine = tid < CT && col_ok;
+            float v = mine ? yv : -INFINITY;
+            int idx = mine ? n : INT_MAX;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(v, o);
+                const int oi = __shfl_xor(idx, o);
+                if (ov > v || (ov == v && oi < idx)) {
+                    v = ov;
+                    idx = oi;
+                }
+            }
+            if (tid == 0) {
+                xp.amax[2 * panel] = __builtin_bit_cast(uint32_t, v);
+                xp.amax[2 * panel + 1] = (uint32_t)idx;
+            }
+        }
+    }
+}
+
+// The argmax over the panel partials of a lm_head launch: *tok = first index of the
+// maximum (INT64_MAX if no value compares, e.g. all NaN, as a scan of the logits gives),
+// then *pos += 1.  One 256-thread work-group.
+__global__ __launch_bounds__(256) void k_argmax_parts(const uint32_t* __restrict__ parts, int n_parts,
+                                                      int64_t* __restrict__ tok, int64_t* __restrict__ pos) {
+    __shared__ float bv[4];
+    __shared__ int64_t bi[4];
+    auto better = [](float x, int64_t i, float& v, int64_t& idx) {
+        if (x > v || (x == v && i < idx)) {
+            v = x;
+            idx = i;
+        }
+    };
+    float v = -INFINITY;
+    int64_t idx = INT64_MAX;
+    for (int i = threadIdx.x; i < n_parts; i += 256) {
+        const uint32_t pi = parts[2 * i + 1];
+        better(__builtin_bit_cast(float, parts[2 * i]), pi == (uint32_t)INT_MAX ? INT64_MAX : (int64_t)pi, v, idx);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o, 64);
+        const int64_t oi = __shfl_xor(idx, o, 64);
+        better(ov, oi, v, idx);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        bv[threadIdx.x >> 6] = v;
+        bi[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) better(bv[w], bi[w], v, idx);
+        tok[0] = idx;
+        pos[0] += 1;
     }
 }
 
@@ -1330,6 +1394,46 @@ extern "C" int32_t sx8_dec_gemv_rmsnorm(const float* resid, const uint16_t* init
     xp.eps = eps;
     return launch_fused<kXRms>(what, xp, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys,
                                as_stream(stream));
+}
+
+extern "C" int64_t sx8_dec_argmax_parts_bytes(int64_t N, int64_t n_cb) {
+    if (N <= 0 || n_cb <= 0) return -1;
+    const int64_t N64 = N;
+    return 8 * (int64_t)plan_panels(&N64, 1, (int)n_cb).grid;
+}
+
+extern "C" int32_t sx8_dec_gemv_rmsnorm_argmax(const float* resid, const uint16_t* norm_w, float eps,
+                                               const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
+                                               const float* bases, const float* scales, int64_t N, int64_t n_cb,
+                                               float* logits, void* parts, int64_t parts_bytes, int64_t* tok,
+                                               int64_t* pos, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_dec_gemv_rmsnorm_argmax";
+    if (!resid || !norm_w || !parts || !tok || !pos) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (!aligned(resid, 16) || !aligned(norm_w, 16) || !aligned(parts, 8))
+        return fail(SX8_ERR_INVALID, "%s: resid and norm_w must be 16-byte aligned, parts 8-byte aligned", what);
+    const int64_t need = sx8_dec_argmax_parts_bytes(N, n_cb);
+    if (need < 0 || parts_bytes < need)
+        return fail(SX8_ERR_INVALID, "%s: parts needs %lld bytes (sx8_dec_argmax_parts_bytes), got %lld", what,
+                    (long long)need, (long long)parts_bytes);
+    const uint8_t* const hdrs[1] = {hdr};
+    const uint8_t* const lvls[1] = {levels};
+    const float* const bas[1] = {bases};
+    const float* const sca[1] = {scales};
+    float* const ys[1] = {logits};
+    const int32_t rc = check_fused_group(what, 1, hdrs, lvls, hdr_bytes, bas, sca, &N, n_cb, ys);
+    if (rc != SX8_OK) return rc;
+    XProd xp{};
+    xp.resid = resid;
+    xp.w = norm_w;
+    xp.eps = eps;
+    xp.amax = reinterpret_cast<uint32_t*>(parts);
+    const int32_t r2 = launch_fused<kXRms>(what, xp, 1, hdrs, lvls, hdr_bytes, bas, sca, &N, n_cb, ys,
+                                           as_stream(stream));
+    if (r2 != SX8_OK) return r2;
+    hipLaunchKernelGGL(k_argmax_parts, dim3(1), dim3(256), 0, as_stream(stream),
+                       reinterpret_cast<const uint32_t*>(parts), (int)(need / 8), tok, pos);
+    return check_launch(what);
 }
 
 extern "C" int32_t sx8_dec_gemv_silu(const float* g, const float* u, int32_t n_mats,

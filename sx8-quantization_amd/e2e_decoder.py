@@ -331,6 +331,9 @@ class SX8Decoder(nn.Module):
                                 self._group_args((ly.o,), (z["ra"],))))
         z["resid_adds"] = (ctypes.c_void_p * 1)(z["ra"].data_ptr())
         z["head_group"] = self._group_args((self.head,), (z["logits"],))
+        # per-work-group argmax partials of the lm_head GEMV
+        nb = int(_L.lib().sx8_dec_argmax_parts_bytes(V, self.head.qt["n_cb"]))
+        z["head_parts"] = torch.zeros(max(nb, 8) // 4, dtype=torch.int32, device=dev)
         self._fz = z
         return z
 
@@ -401,8 +404,11 @@ class SX8Decoder(nn.Module):
                     z["attn_ws"].numel() * 4, st)
             self._gemv_add(g_o, z["a"], adds, st)                   # r += W_o a
             self._mlp_fused(ly, r, eps, st)                         # r += W_down silu(g) u
-        self._gemv_rms(z["head_group"], r, None, None, self.final_norm, None, eps, st)
-        _L.call("sx8_dec_argmax_advance", P(z["logits"]), cfg["vocab"], P(tok), P(pos), st)
+        # final norm + lm_head GEMV, whose work-groups leave argmax partials; argmax + pos += 1
+        hh, hl, hb, hs = self.head._t44
+        _L.call("sx8_dec_gemv_rmsnorm_argmax", P(r), P(self.final_norm), eps, P(hh), P(hl), 6, P(hb), P(hs),
+                cfg["vocab"], self.head.qt["n_cb"], P(z["logits"]), P(z["head_parts"]),
+                z["head_parts"].numel() * 4, P(tok), P(pos), st)
         return tok
 
     # ---------------------------------------------------------------- generation
