@@ -55,6 +55,8 @@ struct WeightSrc {
 // operand and output.  poff: offset (floats) of this matrix's (M, N) block inside a
 // k_gemm split-K partial slice (slices hold the whole group, M * Ntot floats).
 constexpr int kMaxGemmGroup = 4;
+// K ranges of a split plan: at most 8, so at most 7 partial slices or tiles to add
+constexpr int kMaxSplitParts = 7;
 struct GemmMat {
     WeightSrc w;
     const uint32_t* Zhl;
@@ -866,11 +868,28 @@ __global__ __launch_bounds__(256) void k_reduce_tiles(const GemmGroup g, const f
     if (m >= M || n >= N) return;
     const float* p = part + (int64_t)ts * (St - 1) * (kW1BM * kBN) + e;
     float* y = g.m[mi].Y + (int64_t)m * N + n;
+    // every partial (at most kMaxSplitParts) requested before the first add: the loads are
+    // unconditional (a clamped index), so they all go out together
+    sx8_float4 pv[kMaxSplitParts];
+#pragma unroll
+    for (int s = 0; s < kMaxSplitParts; ++s)
+        pv[s] = *reinterpret_cast<const sx8_float4*>(p + (int64_t)min(s, St - 2) * (kW1BM * kBN));
+    const bool vec = n + 3 < N && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
     const int ne = min(4, N - n);
     sx8_float4 v = sx8_float4{0.f, 0.f, 0.f, 0.f};
-    for (int c = 0; c < ne; ++c) v[c] = y[c];
-    for (int s = 0; s < St - 1; ++s) v += *reinterpret_cast<const sx8_float4*>(p + (int64_t)s * (kW1BM * kBN));
-    for (int c = 0; c < ne; ++c) y[c] = v[c];
+    if (vec) {
+        v = *reinterpret_cast<const sx8_float4*>(y);
+    } else {
+        for (int c = 0; c < ne; ++c) v[c] = y[c];
+    }
+#pragma unroll
+    for (int s = 0; s < kMaxSplitParts; ++s)
+        if (s < St - 1) v += pv[s];
+    if (vec) {
+        *reinterpret_cast<sx8_float4*>(y) = v;
+    } else {
+        for (int c = 0; c < ne; ++c) y[c] = v[c];
+    }
 }
 
 // Y_i += partial slices 0 .. S - 2 of every matrix of the group, in slice order
@@ -886,13 +905,26 @@ __global__ __launch_bounds__(256) void k_reduce(const GemmGroup g, const float* 
     int mi = 0;
     while (mi + 1 < g.n_mats && e >= g.m[mi + 1].poff) ++mi;
     float* Y = g.m[mi].Y + (e - g.m[mi].poff);
+    // every partial (at most kMaxSplitParts) requested before the first add (clamped,
+    // unconditional loads)
     if constexpr (kVec) {
+        sx8_float4 pv[kMaxSplitParts];
+#pragma unroll
+        for (int p = 0; p < kMaxSplitParts; ++p)
+            pv[p] = *reinterpret_cast<const sx8_float4*>(part + (int64_t)min(p, nparts - 1) * MNtot + e);
         sx8_float4 y = *reinterpret_cast<const sx8_float4*>(Y);
-        for (int p = 0; p < nparts; ++p) y += *reinterpret_cast<const sx8_float4*>(part + p * MNtot + e);
+#pragma unroll
+        for (int p = 0; p < kMaxSplitParts; ++p)
+            if (p < nparts) y += pv[p];
         *reinterpret_cast<sx8_float4*>(Y) = y;
     } else {
+        float pv[kMaxSplitParts];
+#pragma unroll
+        for (int p = 0; p < kMaxSplitParts; ++p) pv[p] = part[(int64_t)min(p, nparts - 1) * MNtot + e];
         float y = *Y;
-        for (int p = 0; p < nparts; ++p) y += part[p * MNtot + e];
+#pragma unroll
+        for (int p = 0; p < kMaxSplitParts; ++p)
+            if (p < nparts) y += pv[p];
         *Y = y;
     }
 }

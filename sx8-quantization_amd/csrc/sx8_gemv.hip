@@ -101,27 +101,33 @@ __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ 
     // once in LDS; otherwise kb runs fastest, which keeps every lane busy for the M = 1
     // callers
     __shared__ float4 bsh[kPack && kZ ? sx8::kMaxZSets : 1][8][16];
-    if constexpr (kPack && kZ) {
-        const int64_t rest0 = (int64_t)blockIdx.x * 8, nrest = rows / 32 * n_cb;
-        for (int t = threadIdx.x; t < zs.n * 128; t += 256) {
-            const int si = t >> 7, i = (t >> 4) & 7, q = t & 15;
-            const int64_t r = min(rest0 + i, nrest - 1);
-            bsh[si][i][q] = reinterpret_cast<const float4*>(zs.basis[si] + (r % n_cb) * 64)[q];
-        }
-        __syncthreads();
-    }
-    if (gid >= rows * n_cb) return;
+    // the X loads go out first, the basis staging (global -> LDS -> barrier) after them, so
+    // the two round trips overlap; threads past the end load a valid element and stop after
+    // the barrier
+    const bool live = gid < rows * n_cb;
+    const int64_t gq = live ? gid : rows * n_cb - 1;
     int64_t m, kb;
     if constexpr (kPack) {
-        const int64_t rest = gid >> 5;
+        const int64_t rest = gq >> 5;
         kb = rest % n_cb;
-        m = (rest / n_cb) * 32 + (gid & 31);
+        m = (rest / n_cb) * 32 + (gq & 31);
     } else {
-        m = gid / n_cb;
-        kb = gid - m * n_cb;
+        m = gq / n_cb;
+        kb = gq - m * n_cb;
     }
     const bool row_ok = m < M;
     const int kmax = row_ok ? (int)min((int64_t)32, K - kb * 32) : 0;
+    auto stage_basis = [&]() {
+        if constexpr (kPack && kZ) {
+            const int64_t rest0 = (int64_t)blockIdx.x * 8, nrest = rows / 32 * n_cb;
+            for (int t = threadIdx.x; t < zs.n * 128; t += 256) {
+                const int si = t >> 7, i = (t >> 4) & 7, q = t & 15;
+                const int64_t r = min(rest0 + i, nrest - 1);
+                bsh[si][i][q] = reinterpret_cast<const float4*>(zs.basis[si] + (r % n_cb) * 64)[q];
+            }
+            __syncthreads();
+        }
+    };
     uint32_t xw[16];
     if constexpr (kSilu) {
         const int64_t off = min(m, M - 1) * ldx + kb * 32;
@@ -141,6 +147,7 @@ __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ 
                 uv[t] = t < kmax ? su[off + t] : 0.f;
             }
         }
+        stage_basis();
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
             const float x0 = gv[2 * t] / (1.0f + __expf(-gv[2 * t])) * uv[2 * t];
@@ -164,7 +171,9 @@ __global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ 
             xw[t] = a | (b << 16);
         }
     }
+    stage_basis();
     }
+    if (!live) return;
     if constexpr (kPack) {
         const int64_t G = m >> 5;
         const int r = (int)(m & 31);
