@@ -850,6 +850,308 @@ __global__ __launch_bounds__(kW1Threads) __attribute__((amdgpu_waves_per_eu(1, 1
     }
 }
 
+// k_gemm_w2: the 512 x 128 tile of k_gemm_w1 with two waves per SIMD.  Eight waves, wave w
+// owning rows 64 w .. 64 w + 63 (2 m-fragments x 4 n-fragments: 128 accumulator registers,
+// so two waves fit a SIMD), each lane decoding one 8-weight sub-block per K block (thread
+// t: column t % 128, sub-block t / 128).  Waves w and w + 4 share a SIMD: the decode VALU
+// work of one issues while the matrix core runs the other's MFMAs, where k_gemm_w1 has to
+// interleave both in one wave.  Same ring, record lead, plan, partial tiles and reduction
+// as k_gemm_w1.
+constexpr int kW2Threads = 512;
+constexpr int kW2MF = 2;
+
+// The part of a block one decoding thread of k_gemm_w2 needs: endpoints / config /
+// coefficients as in LaneRec, the hi-nibble word and the lo-quad half-word of its sub-block.
+struct LaneRec1 {
+    uint32_t lohi, hi16, cc, cf;
+    uint32_t qh, ql;
+};
+
+template <bool kSplit, int HB>
+__device__ __forceinline__ void load_rec1(LaneRec1& r, const LoopSrc<kW2MF>& ls, int N, int kb, int sb) {
+    const int nn = ls.nn;
+    const int rowb = sx8_uniform(kb * N);
+    if constexpr (kSplit) {
+        r.lohi = __builtin_amdgcn_raw_buffer_load_b16(ls.dmin, nn * 2, rowb * 2, 0);
+        r.hi16 = __builtin_amdgcn_raw_buffer_load_b16(ls.dmax, nn * 2, rowb * 2, 0);
+        r.cc = __builtin_amdgcn_raw_buffer_load_b8(ls.cfg, nn, rowb, 0);
+        r.cf = __builtin_amdgcn_raw_buffer_load_b8(ls.cf, nn, rowb, 0);
+        r.qh = __builtin_amdgcn_raw_buffer_load_b32(ls.hi, nn * 16 + 4 * sb, rowb * 16, 0);
+        r.ql = __builtin_amdgcn_raw_buffer_load_b16(ls.lo, nn * 8 + 2 * sb, rowb * 8, 0);
+    } else {
+        if constexpr (HB == 8) {
+            const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ls.hdr, nn * 8, rowb * 8, 0));
+            r.lohi = v.x;
+            r.cc = v.y;
+        } else {
+            r.lohi = __builtin_amdgcn_raw_buffer_load_b32(ls.hdr, nn * 6, rowb * 6, 0);
+            r.cc = __builtin_amdgcn_raw_buffer_load_b16(ls.hdr, nn * 6 + 4, rowb * 6, 0);
+        }
+        r.hi16 = r.cf = 0;
+        r.qh = __builtin_amdgcn_raw_buffer_load_b32(ls.lv, nn * 24 + 4 * sb, rowb * 24, 0);
+        r.ql = __builtin_amdgcn_raw_buffer_load_b16(ls.lv, nn * 24 + 16 + 2 * sb, rowb * 24, 0);
+    }
+}
+
+// One sub-block's range, levels and (for the first sub-block of a pair) PCA coefficient,
+// the arithmetic of dec_prep
+struct DecPrep1 {
+    float rlo, step;
+    uint32_t le, lv;
+    uint32_t cpair;
+};
+
+template <bool kSplit>
+__device__ __forceinline__ DecPrep1 dec1_prep(const LaneRec1& rec, int sb) {
+    const uint32_t lohi = kSplit ? ((rec.lohi & 0xFFFFu) | (rec.hi16 << 16)) : rec.lohi;
+    const uint32_t cfg = rec.cc & 0xFFu;
+    const float lo = sx8_h2f(lohi), hi = sx8_h2f(lohi >> 16);
+    const float d = hi - lo;
+    DecPrep1 p;
+    sub_range(lo, d, d * 0.25f, d * 0.015873f, cfg, sb, p.rlo, p.step);
+    dec_unpack(rec.qh, rec.ql, p.le, p.lv);
+    const uint32_t cf = kSplit ? rec.cf : (rec.cc >> 8);
+    p.cpair = coeff_pair_f16(sx8_sext4(cf >> (4 * (sb >> 1))));
+    return p;
+}
+
+// the sub-block's 8 weights into buffer b, slot (n-fragment c / 32, k-step sb & 1, lane
+// 32 (sb / 2) + c % 32); the even sub-block of a pair stores the coefficient pair
+template <bool kPca>
+__device__ __forceinline__ void dec1_finish(GemmSmem& sm, const DecPrep1& p, int kb, int b, int c, int sb) {
+    sm.wt[b][c >> 5][sb & 1][32 * (sb >> 1) + (c & 31)] =
+        sx8_u32x4{dec_pair(p.le, p.lv, 0, p.rlo, p.step), dec_pair(p.le, p.lv, 1, p.rlo, p.step),
+                  dec_pair(p.le, p.lv, 2, p.rlo, p.step), dec_pair(p.le, p.lv, 3, p.rlo, p.step)};
+    if constexpr (kPca) {
+        if ((sb & 1) == 0) {
+            const int t4 = kb & 3;
+            uint32_t* dst = reinterpret_cast<uint32_t*>(&sm.pt[(kb >> 2) & 1][c >> 5][(t4 >> 1) * 32 + (c & 31)]);
+            dst[2 * (t4 & 1) + (sb >> 1)] = p.cpair;
+        }
+    }
+}
+
+template <bool kSplit, int HB, bool kPca>
+__global__ __launch_bounds__(kW2Threads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_w2(
+    const uint16_t* __restrict__ Xp, int M, const GemmGroup g, int n_cb, int Tf, int St, int kbs,
+    float* __restrict__ part) {
+    constexpr int MF = kW2MF;
+    __shared__ GemmSmem sm;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int NB = g.NB;
+    const int b = blockIdx.x;
+    int t, ks = 0, kb0 = 0, kb1 = n_cb;
+    if (b < Tf) {
+        t = xcd_order(b, Tf);
+    } else {
+        // Tf is a multiple of 8, so work-group b still runs on XCD b % 8
+        const int o = xcd_order(b - Tf, gridDim.x - Tf);
+        t = Tf + o / St;
+        ks = o % St;
+        kb0 = ks * kbs;
+        kb1 = min(n_cb, kb0 + kbs);
+    }
+    int nb = t % NB;
+    const int mb = t / NB;
+    const int mi = group_mat(g, nb);
+    const WeightSrc w = g.m[mi].w;
+    const uint32_t* __restrict__ Zhl = g.m[mi].Zhl;
+    float* __restrict__ Y = g.m[mi].Y;
+    const int N = g.m[mi].N;
+    const int m0 = mb * kW1BM;
+    const int n0 = nb * kBN;
+    const int hf = lane >> 5, r = lane & 31;
+    const int dc = tid & 127, dsb = tid >> 7;    // decode: column and sub-block
+
+    if constexpr (kPca) {
+        // coefficient slots of blocks past n_cb are never written: start them at zero (each
+        // thread clears one slot of the 512; the barrier of the prologue orders the clears
+        // before every coefficient store, which comes after it)
+        reinterpret_cast<sx8_u32x4*>(&sm.pt[0][0][0])[tid] = sx8_u32x4{0u, 0u, 0u, 0u};
+        lds_barrier();
+    }
+
+    LoopSrc<MF> ls;
+    const int64_t n_blk = (int64_t)N * n_cb;
+    if constexpr (kSplit) {
+        ls.dmin = make_rsrc(w.dmin, n_blk * 2);
+        ls.dmax = make_rsrc(w.dmax, n_blk * 2);
+        ls.cfg = make_rsrc(w.config, n_blk);
+        ls.cf = make_rsrc(w.coeff, n_blk);
+        ls.hi = make_rsrc(w.hi, n_blk * 16);
+        ls.lo = make_rsrc(w.lo, n_blk * 8);
+    } else {
+        ls.hdr = make_rsrc(w.hdr, n_blk * HB);
+        ls.lv = make_rsrc(w.levels, n_blk * 24);
+    }
+    ls.nn = min(n0 + dc, N - 1);
+    ls.h = 0;
+    ls.x = make_rsrc(Xp, (int64_t)((M + 31) / 32) * n_cb * 2048);
+    if constexpr (kPca) ls.z = make_rsrc(Zhl, (int64_t)M * n_cb * 8);
+#pragma unroll
+    for (int f = 0; f < MF; ++f) {
+        const int g32 = (m0 >> 5) + wave * MF + f;
+        ls.a_off[f] = (int)((int64_t)g32 * n_cb * 2048) + lane * 16;
+        const int row = m0 + wave * 32 * MF + 32 * f + r;
+        ls.z_off[f] = (int)(((int64_t)row * n_cb + 2 * hf) * 8);
+    }
+
+    sx8_float16v acc[MF][4];
+#pragma unroll
+    for (int f = 0; f < MF; ++f)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[f][j][i] = 0.f;
+
+    // prologue (as k_gemm_w1): blocks kb0, kb0 + 1 decoded, block kb0 + 2 prepared, records
+    // of kb0 + 3 .. kb0 + 6 and A of kb0, kb0 + 1 in flight
+    LaneRec1 R[4];
+    DecPrep1 P[2];
+    sx8_u32x4 A[2][MF][2];
+    sx8_u32x4 za[MF];
+    {
+        LaneRec1 r0, r1, r2;
+        load_rec1<kSplit, HB>(r0, ls, N, kb0, dsb);
+        load_rec1<kSplit, HB>(r1, ls, N, min(kb0 + 1, kb1 - 1), dsb);
+        load_rec1<kSplit, HB>(r2, ls, N, min(kb0 + 2, kb1 - 1), dsb);
+        load_a<MF>(A[0], ls, kb0);
+        load_a_step<MF>(A[1], ls, min(kb0 + 1, kb1 - 1), 0);
+        if constexpr (kPca) load_za<MF>(za, ls, kb0 >> 2);
+        load_rec1<kSplit, HB>(R[3], ls, N, min(kb0 + 3, kb1 - 1), dsb);
+        load_rec1<kSplit, HB>(R[0], ls, N, min(kb0 + 4, kb1 - 1), dsb);
+        load_rec1<kSplit, HB>(R[1], ls, N, min(kb0 + 5, kb1 - 1), dsb);
+        load_rec1<kSplit, HB>(R[2], ls, N, min(kb0 + 6, kb1 - 1), dsb);
+        dec1_finish<kPca>(sm, dec1_prep<kSplit>(r0, dsb), kb0, kb0 % 3, dc, dsb);
+        dec1_finish<kPca>(sm, dec1_prep<kSplit>(r1, dsb), kb0 + 1, (kb0 + 1) % 3, dc, dsb);
+        P[0] = dec1_prep<kSplit>(r2, dsb);
+        lds_barrier();
+    }
+    const uint8_t* wbase = reinterpret_cast<const uint8_t*>(&sm.wt[0][0][0][lane]);
+    sx8_u32x4 bw[4][2];
+    auto read_b = [&](int kb, int st) __attribute__((always_inline)) {
+        const uint8_t* src = wbase + (kb % 3) * kWtBufBytes;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            bw[j][st] = *reinterpret_cast<const sx8_u32x4*>(src + (j * 2 + st) * 1024);
+    };
+    read_b(kb0, 0);
+
+    // iteration kb (as k_gemm_w1 with 8 MFMAs per k-step): k-step 0 prepares block kb + 3,
+    // k-step 1 finishes block kb + 2 into the ring; PCA k-step at the end of a 4-block group
+    auto body = [&](int kb, sx8_u32x4 (&acur)[MF][2], sx8_u32x4 (&aprev)[MF][2], LaneRec1& rx,
+                    const DecPrep1& pcur, DecPrep1& pnext, const bool pca) __attribute__((always_inline)) {
+        const int ka = min(kb + 2, kb1 - 1);
+        const int kp = min(kb + 1, kb1 - 1);
+        pnext = dec1_prep<kSplit>(rx, dsb);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int f = 0; f < MF; ++f)
+                acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                    __builtin_bit_cast(sx8_half8, bw[j][0]),
+                    __builtin_bit_cast(sx8_half8, acur[f][0]), acc[f][j], 0, 0, 0);
+        load_a_step<MF>(aprev, ls, kp, 1);
+        read_b(kb, 1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // up to four VALU
+            if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);           // a B read
+            else if (i < 6) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);      // an A load
+        }
+        SX8_SCHED_FENCE();
+        dec1_finish<kPca>(sm, pcur, kb + 2, (kb + 2) % 3, dc, dsb);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int f = 0; f < MF; ++f)
+                acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                    __builtin_bit_cast(sx8_half8, bw[j][1]),
+                    __builtin_bit_cast(sx8_half8, acur[f][1]), acc[f][j], 0, 0, 0);
+        load_a_step<MF>(acur, ls, ka, 0);
+        load_rec1<kSplit, HB>(rx, ls, N, min(kb + 7, kb1 - 1), dsb);
+        read_b(kb + 1, 0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // up to three VALU
+            if (i < 2) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);           // ring writes
+            else if (i < 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);      // A / record loads
+            if (i >= 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // B reads
+        }
+        SX8_SCHED_FENCE();
+        if constexpr (kPca) {
+            if (pca) {
+                const int gq = kb >> 2;
+                sx8_half8 zh[MF];
+#pragma unroll
+                for (int f = 0; f < MF; ++f) zh[f] = mask_za(za[f], n_cb, gq, hf);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const sx8_half8 cq = __builtin_bit_cast(sx8_half8, sm.pt[gq & 1][j][lane]);
+#pragma unroll
+                    for (int f = 0; f < MF; ++f)
+                        acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cq, zh[f], acc[f][j], 0, 0, 0);
+                }
+                load_za<MF>(za, ls, min(gq + 1, (kb1 - 1) >> 2));
+            }
+        }
+        lds_barrier();
+    };
+    int kb = kb0;   // a multiple of 4
+    for (; kb + 4 <= kb1; kb += 4) {
+        body(kb, A[0], A[1], R[3], P[0], P[1], false);
+        body(kb + 1, A[1], A[0], R[0], P[1], P[0], false);
+        body(kb + 2, A[0], A[1], R[1], P[0], P[1], false);
+        body(kb + 3, A[1], A[0], R[2], P[1], P[0], true);
+    }
+    if (kb < kb1) body(kb, A[0], A[1], R[3], P[0], P[1], kb + 1 == kb1);
+    if (kb + 1 < kb1) body(kb + 1, A[1], A[0], R[0], P[1], P[0], kb + 2 == kb1);
+    if (kb + 2 < kb1) body(kb + 2, A[0], A[1], R[1], P[0], P[1], true);
+
+    // epilogue (as k_gemm_w1): partial tiles dense 512 x 128, else Y with bounds
+    if (ks > 0) {
+        float* pt = part + ((int64_t)(t - Tf) * (St - 1) + ks - 1) * (kW1BM * kBN);
+#pragma unroll
+        for (int f = 0; f < MF; ++f) {
+            float* row = pt + (wave * 32 * MF + 32 * f + r) * kBN;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<sx8_float4*>(row + 32 * j + 8 * q + 4 * hf) =
+                        sx8_float4{acc[f][j][4 * q], acc[f][j][4 * q + 1], acc[f][j][4 * q + 2],
+                                   acc[f][j][4 * q + 3]};
+        }
+        return;
+    }
+    const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+#pragma unroll
+    for (int f = 0; f < MF; ++f) {
+        const int m = m0 + wave * 32 * MF + 32 * f + r;
+        if (m >= M) continue;
+        float* row = Y + (int64_t)m * N;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + 32 * j + 8 * q + 4 * hf;
+                const sx8_float4 v = {acc[f][j][4 * q], acc[f][j][4 * q + 1], acc[f][j][4 * q + 2],
+                                      acc[f][j][4 * q + 3]};
+                if (vec && n + 3 < N) {
+                    *reinterpret_cast<sx8_float4*>(row + n) = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < N) row[n + e] = v[e];
+                }
+            }
+    }
+}
+
 // Y += the St - 1 partial tiles of each split tile Tf .. T - 1 of k_gemm_w1, in range order
 // (deterministic).  One thread per 4 consecutive columns of a tile row.
 __global__ __launch_bounds__(256) void k_reduce_tiles(const GemmGroup g, const float* __restrict__ part,
@@ -1113,7 +1415,13 @@ void launch_mf(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, con
 template <bool kSplit, bool kPca, int HB>
 void launch_hb(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, const GemmGroup& g,
                int64_t n_cb, float* part) {
-    if (p.w1)
+    // 512-row plans run k_gemm_w2 (two waves per SIMD, measured 2-4% faster than k_gemm_w1
+    // on the layer's 512-row shapes); SX8_GEMM_W2=0 selects k_gemm_w1 (tuning)
+    static const bool w2 = !(getenv("SX8_GEMM_W2") && atoi(getenv("SX8_GEMM_W2")) == 0);
+    if (p.w1 && w2)
+        hipLaunchKernelGGL((k_gemm_w2<kSplit, HB, kPca>), dim3((unsigned)p.G), dim3(kW2Threads), 0, st,
+                           Xp, (int)M, g, (int)n_cb, p.Tf, p.St, p.kbs, part);
+    else if (p.w1)
         hipLaunchKernelGGL((k_gemm_w1<kSplit, HB, kPca>), dim3((unsigned)p.G), dim3(kW1Threads), 0, st,
                            Xp, (int)M, g, (int)n_cb, p.Tf, p.St, p.kbs, part);
     else if (p.MF == 2)
