@@ -797,7 +797,9 @@ def prefill_roofline(pf):
         "bound": "mfma", "unit": "TFLOP/s", "peak": MFMA_F16_PEAK_TFLOPS, "M": M,
         "layer": {"flop": pf["layer_flop"], "us": pf["layer_us"], "achieved": round(pf["tflops"], 1),
                   "frac": round(pf["tflops"] / MFMA_F16_PEAK_TFLOPS, 4)},
-        "dominant": {"shape": name, "kernel": "k_gemm_w1" if q["plan"]["tile"] == 512 else "k_gemm",
+        "dominant": {"shape": name,
+                     "kernel": ("k_gemm_w1" if os.environ.get("SX8_GEMM_W2") == "0" else "k_gemm_w2")
+                     if q["plan"]["tile"] == 512 else "k_gemm",
                      "flop_per_call": flop, "us": q["median_us"], "p10_us": q["p10_us"], "p90_us": q["p90_us"],
                      "achieved": round(q["tflops"], 1), "frac": round(q["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                      "plan": q["plan"]},

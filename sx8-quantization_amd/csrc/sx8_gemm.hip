@@ -1417,7 +1417,8 @@ void launch_hb(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, con
                int64_t n_cb, float* part) {
     // 512-row plans run k_gemm_w2 (two waves per SIMD, measured 2-4% faster than k_gemm_w1
     // on the layer's 512-row shapes); SX8_GEMM_W2=0 selects k_gemm_w1 (tuning)
-    static const bool w2 = !(getenv("SX8_GEMM_W2") && atoi(getenv("SX8_GEMM_W2")) == 0);
+    const char* e2 = getenv("SX8_GEMM_W2");
+    const bool w2 = !(e2 && atoi(e2) == 0);
     if (p.w1 && w2)
         hipLaunchKernelGGL((k_gemm_w2<kSplit, HB, kPca>), dim3((unsigned)p.G), dim3(kW2Threads), 0, st,
                            Xp, (int)M, g, (int)n_cb, p.Tf, p.St, p.kbs, part);

@@ -308,7 +308,7 @@ PREFILL_CASES = [
     ("q_proj", 4096, 2560, 128, "auto"), ("k_proj", 1024, 2560, 512, "auto"),
     ("down", 2560, 9728, 130, "auto"), ("odd", 1000, 2560, 7, "auto"), ("tiny", 64, 96, 1, "auto"),
     ("ragged_K", 300, 80, 33, "auto"),
-    # the 512-row tile kernel (k_gemm_w1), forced: ragged M and N, split K, long K, the
+    # the 512-row tile kernel (k_gemm_w2; k_gemm_w1 with SX8_GEMM_W2=0), forced: ragged M and N, split K, long K, the
     # 256-row kernel on the same shape for comparison
     ("w1_ragged", 1000, 2560, 700, "512"), ("w1_ragged_256", 1000, 2560, 700, "256"),
     ("w1_q", 4096, 2560, 1024, "512"), ("w1_long_k", 640, 9728, 600, "512"),
@@ -316,13 +316,19 @@ PREFILL_CASES = [
     # 272 tiles of 512 x 128: one full round of 256, the other 16 split over K (partial tiles
     # added by the tile reducer)
     ("w1_tail", 17408, 640, 600, "512"),
+    # the one-wave-per-SIMD 512-row kernel (k_gemm_w1, SX8_GEMM_W2=0) on the same kinds of case
+    ("w1only_ragged", 1000, 2560, 700, "512w1"), ("w1only_long_k", 640, 9728, 600, "512w1"),
+    ("w1only_tail", 17408, 640, 600, "512w1"),
 ]
 
 
 @pytest.mark.parametrize("name,N,K,M,tile", PREFILL_CASES)
 def test_prefill_gemm(hiplib, oracle, cuda, monkeypatch, name, N, K, M, tile):
     import torch
-    if tile != "auto":
+    if tile == "512w1":
+        monkeypatch.setenv("SX8_GEMM_TILE", "512")
+        monkeypatch.setenv("SX8_GEMM_W2", "0")
+    elif tile != "auto":
         monkeypatch.setenv("SX8_GEMM_TILE", tile)
     from sx8_decode1_v3 import make_tensors_v44
     from sx8_gemm_compact import _ext, gemm_sx8_compact
@@ -454,7 +460,10 @@ def test_prefill_gemm_group(hiplib, oracle, cuda, monkeypatch, name, Ns, K, M, t
     import torch
     import _sx8lib as L
     from sx8_decode1_v3 import make_tensors_v44
-    if tile != "auto":
+    if tile == "512w1":
+        monkeypatch.setenv("SX8_GEMM_TILE", "512")
+        monkeypatch.setenv("SX8_GEMM_W2", "0")
+    elif tile != "auto":
         monkeypatch.setenv("SX8_GEMM_TILE", tile)
     _say("prefill group", name, Ns, K, M)
     mats = [_quantized(N, K, 500 + i, cuda) for i, N in enumerate(Ns)]
