@@ -1153,9 +1153,13 @@ __global__ __launch_bounds__(kW2Threads) __attribute__((amdgpu_waves_per_eu(2, 2
 }
 
 // Y += the St - 1 partial tiles of each split tile Tf .. T - 1 of k_gemm_w1, in range order
-// (deterministic).  One thread per 4 consecutive columns of a tile row.
+// (deterministic).  One thread per 4 consecutive columns of a tile row.  NP = St - 1 is a
+// template argument: every partial is requested before the first add, and exactly NP
+// loads go out (clamped copies of the last partial would cost memory-pipeline cycles).
+template <int NP>
 __global__ __launch_bounds__(256) void k_reduce_tiles(const GemmGroup g, const float* __restrict__ part,
-                                                      int M, int Tf, int n_split, int St) {
+                                                      int M, int Tf, int n_split) {
+    constexpr int St = NP + 1;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;     // float4 index
     constexpr int kQ = kW1BM * kBN / 4;                            // float4s per tile
     if (i >= (int64_t)n_split * kQ) return;
@@ -1170,12 +1174,9 @@ __global__ __launch_bounds__(256) void k_reduce_tiles(const GemmGroup g, const f
     if (m >= M || n >= N) return;
     const float* p = part + (int64_t)ts * (St - 1) * (kW1BM * kBN) + e;
     float* y = g.m[mi].Y + (int64_t)m * N + n;
-    // every partial (at most kMaxSplitParts) requested before the first add: the loads are
-    // unconditional (a clamped index), so they all go out together
-    sx8_float4 pv[kMaxSplitParts];
+    sx8_float4 pv[NP];
 #pragma unroll
-    for (int s = 0; s < kMaxSplitParts; ++s)
-        pv[s] = *reinterpret_cast<const sx8_float4*>(p + (int64_t)min(s, St - 2) * (kW1BM * kBN));
+    for (int s = 0; s < NP; ++s) pv[s] = *reinterpret_cast<const sx8_float4*>(p + (int64_t)s * (kW1BM * kBN));
     const bool vec = n + 3 < N && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
     const int ne = min(4, N - n);
     sx8_float4 v = sx8_float4{0.f, 0.f, 0.f, 0.f};
@@ -1185,8 +1186,7 @@ __global__ __launch_bounds__(256) void k_reduce_tiles(const GemmGroup g, const f
         for (int c = 0; c < ne; ++c) v[c] = y[c];
     }
 #pragma unroll
-    for (int s = 0; s < kMaxSplitParts; ++s)
-        if (s < St - 1) v += pv[s];
+    for (int s = 0; s < NP; ++s) v += pv[s];
     if (vec) {
         *reinterpret_cast<sx8_float4*>(y) = v;
     } else {
@@ -1198,35 +1198,31 @@ __global__ __launch_bounds__(256) void k_reduce_tiles(const GemmGroup g, const f
 // (deterministic).  Slice s holds the group's M x Ntot partials, matrix i's M x N_i block at
 // poff_i; one launch covers all matrices.  kVec (every Y_i 16-byte aligned, every M N_i a
 // multiple of 4): 4 floats per thread, never straddling two matrices; otherwise one.
-template <bool kVec>
+// NP = S - 1 partials, all requested before the first add (exactly NP loads).
+template <bool kVec, int NP>
 __global__ __launch_bounds__(256) void k_reduce(const GemmGroup g, const float* __restrict__ part,
-                                                int64_t MNtot, int nparts) {
+                                                int64_t MNtot) {
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t e = kVec ? t * 4 : t;
     if (e >= MNtot) return;
     int mi = 0;
     while (mi + 1 < g.n_mats && e >= g.m[mi + 1].poff) ++mi;
     float* Y = g.m[mi].Y + (e - g.m[mi].poff);
-    // every partial (at most kMaxSplitParts) requested before the first add (clamped,
-    // unconditional loads)
     if constexpr (kVec) {
-        sx8_float4 pv[kMaxSplitParts];
+        sx8_float4 pv[NP];
 #pragma unroll
-        for (int p = 0; p < kMaxSplitParts; ++p)
-            pv[p] = *reinterpret_cast<const sx8_float4*>(part + (int64_t)min(p, nparts - 1) * MNtot + e);
+        for (int p = 0; p < NP; ++p) pv[p] = *reinterpret_cast<const sx8_float4*>(part + (int64_t)p * MNtot + e);
         sx8_float4 y = *reinterpret_cast<const sx8_float4*>(Y);
 #pragma unroll
-        for (int p = 0; p < kMaxSplitParts; ++p)
-            if (p < nparts) y += pv[p];
+        for (int p = 0; p < NP; ++p) y += pv[p];
         *reinterpret_cast<sx8_float4*>(Y) = y;
     } else {
-        float pv[kMaxSplitParts];
+        float pv[NP];
 #pragma unroll
-        for (int p = 0; p < kMaxSplitParts; ++p) pv[p] = part[(int64_t)min(p, nparts - 1) * MNtot + e];
+        for (int p = 0; p < NP; ++p) pv[p] = part[(int64_t)p * MNtot + e];
         float y = *Y;
 #pragma unroll
-        for (int p = 0; p < kMaxSplitParts; ++p)
-            if (p < nparts) y += pv[p];
+        for (int p = 0; p < NP; ++p) y += pv[p];
         *Y = y;
     }
 }
@@ -1532,20 +1528,38 @@ int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, in
         else
             launch_hb<false, true, 6>(p, st, Xp, M, g, n_cb, part);
     }
+    // the partial sums, instantiated per partial count (1 .. kMaxSplitParts)
+    auto by_np = [](int np, auto&& f) {
+        switch (np) {
+            case 1: f(std::integral_constant<int, 1>{}); break;
+            case 2: f(std::integral_constant<int, 2>{}); break;
+            case 3: f(std::integral_constant<int, 3>{}); break;
+            case 4: f(std::integral_constant<int, 4>{}); break;
+            case 5: f(std::integral_constant<int, 5>{}); break;
+            case 6: f(std::integral_constant<int, 6>{}); break;
+            default: f(std::integral_constant<int, 7>{}); break;
+        }
+    };
+    static_assert(kMaxSplitParts == 7, "by_np covers 1 .. kMaxSplitParts partials");
     if (p.w1 && p.n_split > 0) {
         const int64_t n4 = p.n_split * (kW1BM * kBN / 4);
-        hipLaunchKernelGGL(k_reduce_tiles, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, g, part,
-                           (int)M, p.Tf, (int)p.n_split, p.St);
+        by_np(p.St - 1, [&](auto np) {
+            hipLaunchKernelGGL((k_reduce_tiles<decltype(np)::value>), dim3((unsigned)((n4 + 255) / 256)),
+                               dim3(256), 0, st, g, part, (int)M, p.Tf, (int)p.n_split);
+        });
     } else if (!p.w1 && p.S > 1) {
         bool vec = true;
         for (int i = 0; i < n_mats; ++i) vec = vec && aligned(Ys[i], 16) && (M * Ns[i]) % 4 == 0;
         const int64_t MN = M * Ntot;
-        if (vec)
-            hipLaunchKernelGGL(k_reduce<true>, dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0, st, g,
-                               part, MN, p.S - 1);
-        else
-            hipLaunchKernelGGL(k_reduce<false>, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, st, g,
-                               part, MN, p.S - 1);
+        by_np(p.S - 1, [&](auto np) {
+            constexpr int NP = decltype(np)::value;
+            if (vec)
+                hipLaunchKernelGGL((k_reduce<true, NP>), dim3((unsigned)((MN / 4 + 255) / 256)), dim3(256), 0,
+                                   st, g, part, MN);
+            else
+                hipLaunchKernelGGL((k_reduce<false, NP>), dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, st,
+                                   g, part, MN);
+        });
     }
     return check_launch(what);
 }

@@ -480,7 +480,12 @@ def test_gemv_pair_and_zp_down(hiplib, cuda, H, I):
                 P(cat[3]), I - 16, H // 32, P(db), P(m), P(zp), st)
 
 
-def test_head_argmax_partials(hiplib, cuda):
+@pytest.mark.parametrize("K,N,hb", [
+    (2560, 20000, 6),      # fewer panels than co-resident work-groups: one panel each
+    (256, 100000, 6),      # several panels per work-group, one K round per panel (R < ring)
+    (2560, 151936, 8),     # the vocab-sized lm_head, 8-byte headers
+])
+def test_head_argmax_partials(hiplib, cuda, K, N, hb):
     """sx8_dec_gemv_rmsnorm_argmax: logits bit for bit those of sx8_dec_gemv_rmsnorm, and the
     token that sx8_dec_argmax_advance picks from them -- with three equal maxima (rows 5, 6
     in one panel and 17000 in another, identical weights give identical logits) the first
@@ -491,14 +496,16 @@ def test_head_argmax_partials(hiplib, cuda):
     from sx8_decode1_v3 import make_tensors_v44
     P = _L.ptr
     st = _L.stream(cuda)
-    K, N, eps = 2560, 20000, 1e-6
+    eps = 1e-6
+    print("head argmax", K, N, hb, flush=True)
     g = torch.Generator().manual_seed(31)
     resids = [torch.randn(K, generator=g) for _ in range(2)]
     W = torch.randn(N, K, generator=g) * 0.02
     top = torch.sign(resids[0]) * 0.05           # the largest logit for the first residual
     W[5], W[6], W[17000] = top, top, top
     qt, bi = quantize_tensor(W.half(), device=cuda, degenerate_frac=0.0, seed=32)   # equal rows stay equal
-    hdr, lvl, bas, sca = make_tensors_v44(qt, bi)
+    hdr, lvl, bas, sca = make_tensors_v44(qt, bi, hdr_aligned=hb == 8)
+    assert hdr.shape[-1] == hb
     w = (torch.rand(K, generator=g) + 0.5).half().to(cuda)
     nb = int(_L.lib().sx8_dec_argmax_parts_bytes(N, K // 32))
     assert nb > 0
@@ -507,14 +514,14 @@ def test_head_argmax_partials(hiplib, cuda):
         rd = r.to(cuda)
         ref = torch.empty(N, device=cuda)
         n, hd, lv, bs, sc, ns, n_cb, ys = _group([(hdr, lvl, bas, sca)], [N], K // 32, [ref])
-        _L.call("sx8_dec_gemv_rmsnorm", P(rd), None, None, P(w), eps, None, n, hd, lv, 6, bs, sc, ns, n_cb, ys, st)
+        _L.call("sx8_dec_gemv_rmsnorm", P(rd), None, None, P(w), eps, None, n, hd, lv, hb, bs, sc, ns, n_cb, ys, st)
         tok_ref = torch.zeros(1, dtype=torch.int64, device=cuda)
         pos_ref = torch.full((1,), 40, dtype=torch.int64, device=cuda)
         _L.call("sx8_dec_argmax_advance", P(ref), N, P(tok_ref), P(pos_ref), st)
         logits = torch.full((N,), float("nan"), device=cuda)
         tok = torch.full((1,), -1, dtype=torch.int64, device=cuda)
         pos = torch.full((1,), 40, dtype=torch.int64, device=cuda)
-        _L.call("sx8_dec_gemv_rmsnorm_argmax", P(rd), P(w), eps, P(hdr), P(lvl), 6, P(bas), P(sca), N, K // 32,
+        _L.call("sx8_dec_gemv_rmsnorm_argmax", P(rd), P(w), eps, P(hdr), P(lvl), hb, P(bas), P(sca), N, K // 32,
                 P(logits), P(parts), nb, P(tok), P(pos), st)
         torch.cuda.synchronize()
         assert torch.equal(logits.cpu(), ref.cpu()), k
@@ -522,5 +529,5 @@ def test_head_argmax_partials(hiplib, cuda):
         if k == 0:
             assert tok.item() == 5 and ref[5].item() == ref[17000].item() == ref.max().item()
     with pytest.raises(RuntimeError, match="parts"):
-        _L.call("sx8_dec_gemv_rmsnorm_argmax", P(rd), P(w), eps, P(hdr), P(lvl), 6, P(bas), P(sca), N, K // 32,
+        _L.call("sx8_dec_gemv_rmsnorm_argmax", P(rd), P(w), eps, P(hdr), P(lvl), hb, P(bas), P(sca), N, K // 32,
                 P(logits), P(parts), nb - 8, P(tok), P(pos), st)
