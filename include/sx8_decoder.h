@@ -52,7 +52,7 @@ int32_t sx8_dec_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
                      const int64_t* pos, uint16_t* out, int32_t nh, int32_t nk, int32_t hd,
                      int64_t L, float scale, void* stream);
 
-/* The same attention split over cache positions: two launches, n_kv x 32 work-groups each
+/* The same attention split over cache positions: two launches, n_kv x 16 work-groups each
  * taking one KV head's share of positions for all nh/nk query heads that share it (nh/nk
  * in {1, 2, 4, 8}), then a combine of the per-chunk partial softmax sums in fixed order.
  * `workspace` (16-byte aligned, >= sx8_dec_attn_workspace_bytes(nh, hd)) holds the

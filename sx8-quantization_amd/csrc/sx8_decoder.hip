@@ -256,9 +256,13 @@ __global__ __launch_bounds__(256) void k_attn_decode(const uint16_t* __restrict_
 // chunk's (m, l, acc[hd]) per head goes to the workspace.  k_attn_combine: per head and
 // dim, out = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c over the chunks in order
 // (deterministic; an empty chunk has m = -inf, l = 0 and weighs nothing).
-// kAttnChunks x n_kv work-groups fill the GPU where one work-group per query head
-// (k_attn_decode) leaves most CUs idle and waits on the cache latency round after round.
-constexpr int kAttnChunks = 32;
+// kAttnChunks x n_kv work-groups spread the cache reads where one work-group per query head
+// (k_attn_decode) waits on the cache latency round after round.  The combine reads every
+// chunk's partials, so fewer chunks shorten it; 36-layer decode at 513..767 positions,
+// ms per token on one box: 8 chunks 1.589, 12 1.534, 16 1.534, 24 1.557, 32 1.569.  (A
+// chunk count derived from *pos on the device was slower, 1.66: the combine's loads then
+// wait for that read.)
+constexpr int kAttnChunks = 16;
 constexpr int64_t kAttnSplitMaxL = (int64_t)1 << 20;
 
 // Inputs of the RoPE-fused form (kRope): the raw f32 projections and what
