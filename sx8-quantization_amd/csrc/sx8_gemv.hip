@@ -950,37 +950,48 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
 
 // The argmax over the panel partials of a lm_head launch: *tok = first index of the
 // maximum (INT64_MAX if no value compares, e.g. all NaN, as a scan of the logits gives),
-// then *pos += 1.  One 256-thread work-group.
+// then *pos += 1.  One 256-thread work-group; each thread requests its kPer partials
+// together before comparing (a loop that compares as it loads waits a memory round trip
+// per partial).  The comparison -- larger value, or equal value and lower index; NaN never
+// wins -- does not depend on the order, so any reduction tree gives the same token.
+// Indices stay 32-bit (a panel's column, INT_MAX for none) until the store.
 __global__ __launch_bounds__(256) void k_argmax_parts(const uint32_t* __restrict__ parts, int n_parts,
                                                       int64_t* __restrict__ tok, int64_t* __restrict__ pos) {
-    __shared__ float bv[4];
-    __shared__ int64_t bi[4];
-    auto better = [](float x, int64_t i, float& v, int64_t& idx) {
+    constexpr int kThreads = 256, kPer = 10;
+    __shared__ float bv[kThreads / 64];
+    __shared__ int bi[kThreads / 64];
+    auto better = [](float x, int i, float& v, int& idx) {
         if (x > v || (x == v && i < idx)) {
             v = x;
             idx = i;
         }
     };
+    const uint2* p2 = reinterpret_cast<const uint2*>(parts);
+    const int t = (int)threadIdx.x;
     float v = -INFINITY;
-    int64_t idx = INT64_MAX;
-    for (int i = threadIdx.x; i < n_parts; i += 256) {
-        const uint32_t pi = parts[2 * i + 1];
-        better(__builtin_bit_cast(float, parts[2 * i]), pi == (uint32_t)INT_MAX ? INT64_MAX : (int64_t)pi, v, idx);
+    int idx = INT_MAX;
+    for (int base = 0; base < n_parts; base += kThreads * kPer) {
+        uint2 w[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) w[k] = p2[min(base + k * kThreads + t, n_parts - 1)];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k)
+            if (base + k * kThreads + t < n_parts) better(__builtin_bit_cast(float, w[k].x), (int)w[k].y, v, idx);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(v, o, 64);
-        const int64_t oi = __shfl_xor(idx, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
         better(ov, oi, v, idx);
     }
-    if ((threadIdx.x & 63) == 0) {
-        bv[threadIdx.x >> 6] = v;
-        bi[threadIdx.x >> 6] = idx;
+    if ((t & 63) == 0) {
+        bv[t >> 6] = v;
+        bi[t >> 6] = idx;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w) better(bv[w], bi[w], v, idx);
-        tok[0] = idx;
+    if (t == 0) {
+        for (int w = 1; w < kThreads / 64; ++w) better(bv[w], bi[w], v, idx);
+        tok[0] = idx == INT_MAX ? INT64_MAX : (int64_t)idx;
         pos[0] += 1;
     }
 }
