@@ -37,15 +37,59 @@ __device__ __forceinline__ float block_max256(float v, float* red) {
 
 // Row r: resid = (init ? fp16 init : resid) + (delta ? delta : 0) in f32; out = fp16(resid *
 // rsqrt(mean(resid^2) + eps) * w).  Rows of up to 256 * kRmsPer values stay in registers
-// (every load of the row is issued before the reduction); longer rows loop.
-constexpr int kRmsPer = 16;
+// (every load of the row is issued before the reduction); longer rows loop.  vec (H % 4 ==
+// 0, 16-byte aligned f32 rows, 8-byte aligned fp16 rows): 4 consecutive values per load,
+// rows of up to 256 * 4 * kRmsPer4 values.
+constexpr int kRmsPer = 16, kRmsPer4 = 4;
+
+__device__ __forceinline__ float4 h4f(uint2 v) {
+    return make_float4(h2f((uint16_t)(v.x & 0xFFFFu)), h2f((uint16_t)(v.x >> 16)), h2f((uint16_t)(v.y & 0xFFFFu)),
+                       h2f((uint16_t)(v.y >> 16)));
+}
 
 __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ resid, const float* __restrict__ delta,
                                                      const uint16_t* __restrict__ init,
                                                      const uint16_t* __restrict__ w,
-                                                     uint16_t* __restrict__ out, int H, float eps) {
+                                                     uint16_t* __restrict__ out, int H, float eps, bool vec) {
     __shared__ float red[4];
     const int64_t base = (int64_t)blockIdx.x * H;
+    if (vec && H <= 256 * 4 * kRmsPer4) {
+        const int H4 = H >> 2;
+        float4* r4 = reinterpret_cast<float4*>(resid + base);
+        const float4* d4 = reinterpret_cast<const float4*>(delta + (delta ? base : 0));
+        const uint2* i4 = reinterpret_cast<const uint2*>(init + (init ? base : 0));
+        const uint2* w4 = reinterpret_cast<const uint2*>(w);
+        float4 v[kRmsPer4];
+        uint2 wv[kRmsPer4];
+#pragma unroll
+        for (int u = 0; u < kRmsPer4; ++u) {       // every load of the row before the reduction
+            const int i = threadIdx.x + 256 * u;
+            const int ic = min(i, H4 - 1);
+            float4 x = init ? h4f(i4[ic]) : r4[ic];
+            if (delta) {
+                const float4 dd = d4[ic];
+                x = make_float4(x.x + dd.x, x.y + dd.y, x.z + dd.z, x.w + dd.w);
+            }
+            v[u] = i < H4 ? x : make_float4(0.f, 0.f, 0.f, 0.f);
+            wv[u] = w4[ic];
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < kRmsPer4; ++u) ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
+        const float inv = 1.0f / sqrtf(block_sum256(ss, red) / (float)H + eps);
+        uint2* o4 = reinterpret_cast<uint2*>(out + base);
+#pragma unroll
+        for (int u = 0; u < kRmsPer4; ++u) {
+            const int i = threadIdx.x + 256 * u;
+            if (i < H4) {
+                r4[i] = v[u];
+                const float4 wf = h4f(wv[u]);
+                o4[i] = make_uint2((uint32_t)f2h(v[u].x * inv * wf.x) | ((uint32_t)f2h(v[u].y * inv * wf.y) << 16),
+                                   (uint32_t)f2h(v[u].z * inv * wf.z) | ((uint32_t)f2h(v[u].w * inv * wf.w) << 16));
+            }
+        }
+        return;
+    }
     if (H <= 256 * kRmsPer) {
         float v[kRmsPer], wv[kRmsPer];
 #pragma unroll
@@ -82,11 +126,16 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ resid, 
     for (int i = threadIdx.x; i < H; i += 256) out[base + i] = f2h(resid[base + i] * inv * h2f(w[i]));
 }
 
-// One block per head (nh query heads, then nk key heads, then nk value heads) of
-// 64 * ceil(hd / 128) threads, thread d < hd / 2 owning the pair (d, d + hd / 2): q/k RMSNorm
-// over the head, RoPE (rotate-half) at position *pos, q to q_out, k into k_cache and v into
-// v_cache (both (nk, L, hd)).
-__global__ __launch_bounds__(128) void k_qk_rope_cache(const float* __restrict__ q_raw,
+// Heads per 256-thread block: nh query heads, then nk key heads, then nk value heads, TPH =
+// 64 ceil(hd / 128) threads per head (256 / TPH heads per block, blockIdx.x numbering head
+// groups), thread d < hd / 2 owning the pair (d, d + hd / 2): q/k RMSNorm over the head,
+// RoPE (rotate-half) at position *pos, q to q_out, k into k_cache and v into v_cache (both
+// (nk, L, hd)).  A multi-row call takes kRopeRows tokens per block (blockIdx.y) and requests
+// every row's inputs before the first norm: a block per (head, token) leaves tens of
+// thousands of one-wave work-groups that each wait two memory round trips.
+constexpr int kRopeRows = 4;
+
+__global__ __launch_bounds__(256) void k_qk_rope_cache(const float* __restrict__ q_raw,
                                                        const float* __restrict__ k_raw,
                                                        const float* __restrict__ v_raw,
                                                        const uint16_t* __restrict__ qn,
@@ -97,50 +146,67 @@ __global__ __launch_bounds__(128) void k_qk_rope_cache(const float* __restrict__
                                                        uint16_t* __restrict__ q_out,
                                                        uint16_t* __restrict__ k_cache,
                                                        uint16_t* __restrict__ v_cache, int nh,
-                                                       int nk, int hd, int L, float eps) {
-    __shared__ float red[2];
-    // row y of a multi-row call: token y at position *pos + y, inputs and q_out offset by y rows
-    const int y = blockIdx.y;
-    const int64_t pos = *pos_p + y;
-    if (pos < 0 || pos >= L) return;         // position outside the cache: nothing to write
-    q_raw += (int64_t)y * nh * hd;
-    k_raw += (int64_t)y * nk * hd;
-    v_raw += (int64_t)y * nk * hd;
-    q_out += (int64_t)y * nh * hd;
+                                                       int nk, int hd, int L, float eps, int rows) {
+    __shared__ float red[kRopeRows][4][2];
     const int half = hd >> 1;
-    const int d = threadIdx.x;
-    const int b = blockIdx.x;
-    if (b >= nh + nk) {                      // value head: copy into the cache
-        const int h = b - nh - nk;
-        for (int e = d; e < hd; e += blockDim.x) v_cache[((int64_t)h * L + pos) * hd + e] = f2h(v_raw[h * hd + e]);
-        return;
-    }
+    const int tph = hd > 128 ? 128 : 64;
+    const int lh = (int)threadIdx.x / tph, d = (int)threadIdx.x - lh * tph;
+    const int b = (int)blockIdx.x * (256 / tph) + lh;
+    const bool is_v = b >= nh + nk && b < nh + 2 * nk;
+    const bool is_qk = b < nh + nk;
     const bool is_q = b < nh;
-    const int h = is_q ? b : b - nh;
-    const float* src = is_q ? q_raw + h * hd : k_raw + h * hd;
-    const uint16_t* nw = is_q ? qn : kn;
-    const bool act = d < half;
-    const float x1 = act ? src[d] : 0.f, x2 = act ? src[d + half] : 0.f;
-    float ss = x1 * x1 + x2 * x2;
+    const int h = is_q ? b : is_qk ? b - nh : b - nh - nk;
+    const bool act = is_qk && d < half;
+    const int y0 = (int)blockIdx.y * kRopeRows;
+    const int64_t pos0 = *pos_p;
+    // (1) every row's q/k pair (and its value-head elements) requested together
+    float x1[kRopeRows], x2[kRopeRows], va[kRopeRows], vb[kRopeRows];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    if (blockDim.x > 64) {
-        if ((d & 63) == 0) red[d >> 6] = ss;
-        __syncthreads();
-        ss = red[0] + red[1];
+    for (int r = 0; r < kRopeRows; ++r) {
+        const int y = min(y0 + r, rows - 1);
+        const float* src = (is_q ? q_raw + (int64_t)y * nh * hd : k_raw + (int64_t)y * nk * hd) + h * hd;
+        x1[r] = act ? src[d] : 0.f;
+        x2[r] = act ? src[d + half] : 0.f;
+        const float* vs = v_raw + (int64_t)y * nk * hd + h * hd;
+        va[r] = is_v && d < hd ? vs[d] : 0.f;
+        vb[r] = is_v && d + tph < hd ? vs[d + tph] : 0.f;
     }
-    if (!act) return;
-    const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
-    // round to fp16 after the norm, as the fp16 activations of the model do
-    const float n1 = h2f(f2h(x1 * inv * h2f(nw[d]))), n2 = h2f(f2h(x2 * inv * h2f(nw[d + half])));
-    const float c = cos_t[pos * half + d], s = sin_t[pos * half + d];
-    const float o1 = n1 * c - n2 * s, o2 = n2 * c + n1 * s;
-    if (is_q) {
-        q_out[h * hd + d] = f2h(o1);
-        q_out[h * hd + d + half] = f2h(o2);
-    } else {
-        k_cache[((int64_t)h * L + pos) * hd + d] = f2h(o1);
-        k_cache[((int64_t)h * L + pos) * hd + d + half] = f2h(o2);
+    // (2) per row: RMSNorm, RoPE at *pos + y, stores (rows outside the cache write nothing)
+#pragma unroll
+    for (int r = 0; r < kRopeRows; ++r) {
+        const int y = y0 + r;
+        const int64_t pos = pos0 + y;
+        const bool row_ok = y < rows && pos >= 0 && pos < L;
+        if (row_ok && is_v) {
+            uint16_t* vd = v_cache + ((int64_t)h * L + pos) * hd;
+            if (d < hd) vd[d] = f2h(va[r]);
+            if (d + tph < hd) vd[d + tph] = f2h(vb[r]);
+            for (int e = d + 2 * tph; e < hd; e += tph) vd[e] = f2h(v_raw[(int64_t)y * nk * hd + h * hd + e]);
+        }
+        float ss = x1[r] * x1[r] + x2[r] * x2[r];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if (tph > 64) {                      // two waves per head (every thread reaches the barrier)
+            if ((d & 63) == 0) red[r][lh][d >> 6] = ss;
+            __syncthreads();
+            ss = red[r][lh][0] + red[r][lh][1];
+        }
+        if (!act || !row_ok) continue;
+        const uint16_t* nw = is_q ? qn : kn;
+        const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+        // round to fp16 after the norm, as the fp16 activations of the model do
+        const float n1 = h2f(f2h(x1[r] * inv * h2f(nw[d]))), n2 = h2f(f2h(x2[r] * inv * h2f(nw[d + half])));
+        const float c = cos_t[pos * half + d], s = sin_t[pos * half + d];
+        const float o1 = n1 * c - n2 * s, o2 = n2 * c + n1 * s;
+        if (is_q) {
+            uint16_t* qo = q_out + (int64_t)y * nh * hd + h * hd;
+            qo[d] = f2h(o1);
+            qo[d + half] = f2h(o2);
+        } else {
+            uint16_t* kd = k_cache + ((int64_t)h * L + pos) * hd;
+            kd[d] = f2h(o1);
+            kd[d + half] = f2h(o2);
+        }
     }
 }
 
@@ -915,8 +981,10 @@ extern "C" int32_t sx8_dec_add_rmsnorm(float* resid, const float* delta, const u
     if (!resid || !w || !out) return fail(SX8_ERR_INVALID, "sx8_dec_add_rmsnorm: null pointer");
     if (M <= 0 || H <= 0 || M > 0x7FFFFFFF || H > 0x7FFFFFFF)
         return fail(SX8_ERR_INVALID, "sx8_dec_add_rmsnorm: bad shape");
+    const bool vec = H % 4 == 0 && aligned(resid, 16) && (!delta || aligned(delta, 16)) &&
+                     (!init || aligned(init, 8)) && aligned(w, 8) && aligned(out, 8);
     hipLaunchKernelGGL(k_add_rmsnorm, dim3((unsigned)M), dim3(256), 0, as_stream(stream), resid, delta,
-                       init, w, out, (int)H, eps);
+                       init, w, out, (int)H, eps, vec);
     return check_launch("sx8_dec_add_rmsnorm");
 }
 
@@ -932,9 +1000,10 @@ extern "C" int32_t sx8_dec_qk_rope_cache(const float* q_raw, const float* k_raw,
         return fail(SX8_ERR_INVALID, "sx8_dec_qk_rope_cache: null pointer");
     if (nh <= 0 || nk <= 0 || nh % nk || hd <= 0 || (hd & 1) || hd > 256 || L <= 0 || L > 0x7FFFFFFF)
         return fail(SX8_ERR_INVALID, "sx8_dec_qk_rope_cache: bad shape (hd even, <= 256)");
-    hipLaunchKernelGGL(k_qk_rope_cache, dim3((unsigned)(nh + 2 * nk)), dim3(hd > 128 ? 128 : 64), 0,
+    const unsigned hpb = hd > 128 ? 2u : 4u;     // heads per 256-thread block
+    hipLaunchKernelGGL(k_qk_rope_cache, dim3(((unsigned)(nh + 2 * nk) + hpb - 1) / hpb), dim3(256), 0,
                        as_stream(stream), q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, pos,
-                       q_out, k_cache, v_cache, nh, nk, hd, (int)L, eps);
+                       q_out, k_cache, v_cache, nh, nk, hd, (int)L, eps, 1);
     return check_launch("sx8_dec_qk_rope_cache");
 }
 
@@ -951,9 +1020,11 @@ extern "C" int32_t sx8_dec_qk_rope_cache_rows(const float* q_raw, const float* k
     if (nh <= 0 || nk <= 0 || nh % nk || hd <= 0 || (hd & 1) || hd > 256 || L <= 0 || L > 0x7FFFFFFF ||
         rows <= 0 || rows > 65535)
         return fail(SX8_ERR_INVALID, "sx8_dec_qk_rope_cache_rows: bad shape (hd even, <= 256, rows 1..65535)");
-    hipLaunchKernelGGL(k_qk_rope_cache, dim3((unsigned)(nh + 2 * nk), (unsigned)rows), dim3(hd > 128 ? 128 : 64),
+    const unsigned hpb = hd > 128 ? 2u : 4u;     // heads per 256-thread block
+    const unsigned yb = (unsigned)((rows + kRopeRows - 1) / kRopeRows);
+    hipLaunchKernelGGL(k_qk_rope_cache, dim3(((unsigned)(nh + 2 * nk) + hpb - 1) / hpb, yb), dim3(256),
                        0, as_stream(stream), q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, pos,
-                       q_out, k_cache, v_cache, nh, nk, hd, (int)L, eps);
+                       q_out, k_cache, v_cache, nh, nk, hd, (int)L, eps, (int)rows);
     return check_launch("sx8_dec_qk_rope_cache_rows");
 }
 
