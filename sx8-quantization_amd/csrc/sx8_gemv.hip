@@ -1585,16 +1585,25 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_pair(
     const int j0 = tid / CT, c = tid - j0 * CT;
     const int G = (n_one + CTp - 1) / CTp, xcd = blockIdx.x & 7;
     const int panel = (int)(blockIdx.x >> 3) + xcd * (G >> 3) + min(xcd, G & 7);
-    const int mat = c & 1;
+    const int mat = c & 1;                       // (epilogue mapping: thread tid)
     const int col = panel * CTp + (c >> 1);
     const bool col_ok = col < N;
-    const uint32_t nn = (uint32_t)min(col, N - 1);
-    const bool lane_ok = j0 < S;
-    const int j = lane_ok ? j0 : n_cb;
+    // K-loop mapping: the S CT active lanes spread evenly over the eight waves (lane i < A
+    // of wave w is virtual lane w A + i = slice * CT + column), so no SIMD carries more
+    // of them than another (S CT = 456 for CT = 76 would otherwise leave wave 7 with 8)
+    const int nact = S * CT, A = (nact + 7) / 8;
+    const int va = (tid >> 6) * A + (tid & 63);
+    const bool lane_ok = (tid & 63) < A && va < nact;
+    const int jv = va / CT, cv = va - jv * CT;
+    const int matk = cv & 1;
+    const int colk = panel * CTp + (cv >> 1);
+    const bool col_okk = colk < N;
+    const uint32_t nn = (uint32_t)min(colk, N - 1);
+    const int j = lane_ok ? jv : n_cb;
     const uint32_t n_blk = (uint32_t)n_cb * (uint32_t)N;
     const sx8_rsrc rh = make_rsrc(hdr, (int64_t)n_blk * 2 * HB);
     const sx8_rsrc rl = make_rsrc(lv, (int64_t)n_blk * 2 * 24);
-    const uint32_t bid0 = lane_ok ? (uint32_t)j * (uint32_t)N + nn + (mat ? n_blk : 0u) : 2 * n_blk;
+    const uint32_t bid0 = lane_ok ? (uint32_t)j * (uint32_t)N + nn + (matk ? n_blk : 0u) : 2 * n_blk;
     const uint32_t dbid = lane_ok ? (uint32_t)S * (uint32_t)N : 0u;
     auto load = [&](BlockRec& o, int r) { load_rec<HB>(o, rh, rl, bid0 + (uint32_t)r * dbid); };
     constexpr int kNR0 = NR < 2 ? NR : 2;
@@ -1649,8 +1658,8 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_pair(
         const int kb = j + r * S;
         const KbInfo& ki = info[min(kb, n_cb - 1)];
         const float4 zz = *reinterpret_cast<const float4*>(&ki.z[0]);   // z[0], z[1], pad[0], pad[1]
-        const float v = block_dot_z(o, ki, mat ? zz.z : zz.x, mat ? zz.w : zz.y, sk);
-        acc += (col_ok && kb < n_cb) ? v : 0.f;
+        const float v = block_dot_z(o, ki, matk ? zz.z : zz.x, matk ? zz.w : zz.y, sk);
+        acc += (col_okk && kb < n_cb) ? v : 0.f;
     };
     int r = 0;
     for (; r + NR < R; r += NR) {
@@ -1666,8 +1675,9 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_pair(
     for (int i = 0; i < NR; ++i)
         if (r + i < R) step(buf[i], r + i);
 
-    // (5) slices -> lanes in a fixed order (NG partial groups: 4 when CT > 64)
-    red[tid] = acc;
+    // (5) slices -> lanes in a fixed order (NG partial groups: 4 when CT > 64), from the
+    // virtual lanes' sums
+    if (lane_ok) red[va] = acc;
     __syncthreads();
     const int NG = CT > 64 ? 4 : 8;
     if (tid < NG * CT) {

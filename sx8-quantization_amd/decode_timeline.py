@@ -95,9 +95,9 @@ def instrument(src):
     sub("    red[tid] = acc;\n    __syncthreads();\n    if (tid < 8 * CT) {",
         "    asm volatile(\"\" :: \"v\"(acc));\n    TS(6);\n    red[tid] = acc;\n    __syncthreads();\n    TS(9);\n"
         "    if (tid < 8 * CT) {")
-    sub("    red[tid] = acc;\n    __syncthreads();\n    const int NG = CT > 64 ? 4 : 8;",
-        "    asm volatile(\"\" :: \"v\"(acc));\n    TS(6);\n    red[tid] = acc;\n    __syncthreads();\n    TS(9);\n"
-        "    const int NG = CT > 64 ? 4 : 8;")
+    sub("    if (lane_ok) red[va] = acc;\n    __syncthreads();\n    const int NG = CT > 64 ? 4 : 8;",
+        "    asm volatile(\"\" :: \"v\"(acc));\n    TS(6);\n    if (lane_ok) red[va] = acc;\n    __syncthreads();\n"
+        "    TS(9);\n    const int NG = CT > 64 ? 4 : 8;")
     # end of k_gemv_panel (after the argmax partials) and of k_gemv_pair
     sub("                xp.amax[2 * panel + 1] = (uint32_t)idx;\n            }\n        }\n    }\n}\n",
         "                xp.amax[2 * panel + 1] = (uint32_t)idx;\n            }\n        }\n    }\n"
