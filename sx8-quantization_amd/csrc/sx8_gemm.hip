@@ -1291,8 +1291,9 @@ struct Plan {
 
 // Costs are in units of one 256-row tile iteration (~0.5 us): rounds of work-groups over the
 // 256 CUs times the K blocks per work-group (a 512-row iteration costs kW1Cost of them, a
-// 128-row one kMF1Cost), plus partial sums written and read once at about 10 KB per CU per
-// unit.
+// 128-row one kMF1Cost), plus the traffic a split adds at about 10 KB per CU per unit: for
+// S K ranges of a tile, S - 1 partial tiles written and read back, and Y read and written
+// again by the sum -- 2 S tile-sized transfers, for both kernels.
 constexpr double kW1Cost = 1.60, kMF1Cost = 0.62;
 constexpr double kBytesPerUnit = 256.0 * 10240.0;
 
@@ -1306,7 +1307,7 @@ Plan plan_split(int64_t M, int64_t N, int64_t T, int64_t n_cb, int64_t S, int MF
     p.G = T * p.S;
     const double rounds = (double)((p.G + 255) / 256);
     p.cost = rounds * p.kb_per_split * (MF == 2 ? 1.0 : kMF1Cost) +
-             (double)(p.S - 1) * M * N * 8.0 / kBytesPerUnit;
+             (p.S > 1 ? 2.0 * p.S * M * N * 4.0 / kBytesPerUnit : 0.0);
     return p;
 }
 
@@ -1339,7 +1340,7 @@ Plan make_w1(int64_t M, int64_t NB, int64_t n_cb, int64_t Tf, int64_t St) {
     p.G = Tf + rem * p.St;
     const double tile_bytes = (double)kW1BM * kBN * 4.0;
     p.cost = (double)(Tf / 256) * n_cb * kW1Cost + (double)((rem * p.St + 255) / 256) * p.kbs * kW1Cost +
-             (p.St > 1 ? (double)rem * (p.St + 1) * tile_bytes * 2.0 / kBytesPerUnit : 0.0);
+             (p.St > 1 ? (double)rem * 2.0 * p.St * tile_bytes / kBytesPerUnit : 0.0);
     return p;
 }
 
