@@ -85,9 +85,12 @@ constexpr int kLdsMaxKb = 640;     // activation table staged in LDS up to this 
 // kSilu: x is not read from X but produced from two float32 matrices (g, u with row
 // stride ldx) as fp16(silu(g) * u) = fp16(g / (1 + exp(-g)) * u), the arithmetic of
 // sx8_dec_silu_mul, so the prefill GEMM of the MLP's down projection takes the gate / up
-// outputs directly.
+// outputs directly.  The plain-x forms are held to 80 VGPRs (six waves per SIMD, no spills;
+// 103 unbounded, four waves): the pass is latency-bound, and the larger grids (K = 9728,
+// 2432 work-groups at M = 2048) run in fewer rounds (down at M = 2048 147.7 -> 145.2 us per
+// prefill call, A/B).
 template <bool kZ, bool kPack, bool kSilu = false>
-__global__ __launch_bounds__(256) void k_compute_z(const uint16_t* __restrict__ X, int64_t M,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSilu ? 1 : 6, 8))) void k_compute_z(const uint16_t* __restrict__ X, int64_t M,
                                                    int64_t ldx, int64_t K, const sx8::ZSets zs,
                                                    int64_t n_cb, bool x_vec, bool hl,
                                                    uint16_t* __restrict__ Xp,
