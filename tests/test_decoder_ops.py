@@ -146,6 +146,42 @@ def test_add_rmsnorm_and_silu_mul(hiplib, cuda):
     assert (o.cpu().float() - refm).abs().max().item() <= 2e-3 * refm.abs().max().item()
 
 
+@pytest.mark.parametrize("M,H,use_init,use_delta,shift", [
+    (3, 2560, True, True, 0),     # four-wide loads, residual from the fp16 embedding rows
+    (2, 4096, False, True, 0),    # four-wide, the longest such row
+    (2, 2562, True, False, 0),    # H % 4 != 0: one value per load
+    (2, 2560, False, True, 1),    # a residual one float past 16-byte alignment
+    (2, 5000, True, True, 0),     # longer than the unrolled forms hold
+    (1, 7, False, False, 0),      # a row shorter than a wave
+])
+def test_add_rmsnorm_forms(hiplib, cuda, M, H, use_init, use_delta, shift):
+    """sx8_dec_add_rmsnorm in each of its load forms against float32 torch: resid written
+    back exactly (init, when given, replacing resid before delta is added) and the fp16
+    normed rows within half-precision rounding."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    g = torch.Generator().manual_seed(M * H + shift)
+    resid = torch.randn(M, H, generator=g)
+    delta = torch.randn(M, H, generator=g)
+    init = torch.randn(M, H, generator=g).half()
+    w = (torch.rand(H, generator=g) + 0.5).half()
+    rbuf = torch.zeros(M * H + shift, device=cuda)
+    rbuf[shift:] = resid.flatten().to(cuda)
+    rd = rbuf[shift:]
+    dd, idd, wd = delta.to(cuda), init.to(cuda), w.to(cuda)
+    out = torch.empty(M, H, dtype=torch.float16, device=cuda)
+    print("add_rmsnorm", M, H, use_init, use_delta, shift, flush=True)
+    _L.call("sx8_dec_add_rmsnorm", P(rd), P(dd) if use_delta else None, P(idd) if use_init else None, P(wd),
+            P(out), M, H, 1e-6, _L.stream(cuda))
+    x = init.float() if use_init else resid.clone()
+    if use_delta:
+        x = x + delta
+    ref = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + 1e-6) * w.float()
+    assert torch.equal(rd.cpu().view(M, H), x)
+    assert bool(((out.cpu().float() - ref).abs() <= 2.0 ** -9 * ref.abs() + 1e-4).all())
+
+
 def _group(lins_t, Ns, n_cb, ys):
     import ctypes
     n = len(lins_t)
@@ -413,6 +449,82 @@ def test_attn_rope_matches_two_calls(hiplib, cuda, nh, nk, hd, L, positions):
         assert dk <= 2e-3 * kc1[:, p].float().abs().max().item(), dk
         o1, o2 = out1.cpu().float(), out2.cpu().float()
         assert (o1 - o2).abs().max().item() <= 5e-3 * o1.abs().max().item()
+
+
+def _qk_rope_ref(x, w, cos_row, sin_row, eps):
+    """One head's RMSNorm (fp16-rounded, as the model's fp16 activations are) and rotate-half
+    RoPE in float32; x (hd,) float32, w (hd,) fp16, cos_row / sin_row (hd/2,)."""
+    import torch
+    half = x.numel() // 2
+    n = (x * torch.rsqrt((x * x).mean() + eps) * w.float()).half().float()
+    n1, n2 = n[:half], n[half:]
+    return torch.cat([n1 * cos_row - n2 * sin_row, n2 * cos_row + n1 * sin_row])
+
+
+@pytest.mark.parametrize("nh,nk,hd,L,rows,pos0", [
+    (32, 8, 128, 64, 9, 3),      # the decoder's heads, a ragged last block of rows
+    (4, 2, 256, 40, 7, 36),      # hd 256 (two waves per head); rows 4..6 fall past the cache
+    (6, 2, 96, 32, 5, 0),        # hd 96; 10 heads in blocks of 4
+    (3, 1, 160, 16, 4, 0),       # hd 160: a value head's upper elements at d + 128
+    (8, 8, 64, 20, 1, 19),       # one row at the last cache position
+    (2, 1, 200, 8, 3, -1),       # the first row before the cache writes nothing
+])
+def test_qk_rope_cache_rows(hiplib, cuda, nh, nk, hd, L, rows, pos0):
+    """sx8_dec_qk_rope_cache_rows against a float32 per-head reference (q, the cache rows it
+    writes, every other cache row and every out-of-cache q row untouched), and bit for bit
+    against one sx8_dec_qk_rope_cache call per row."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    eps = 1e-6
+    g = torch.Generator().manual_seed(hd * 31 + rows)
+    half = hd // 2
+    inv = 1.0 / (1e6 ** (torch.arange(half, dtype=torch.float32) / half))
+    ang = torch.arange(L, dtype=torch.float32)[:, None] * inv[None]
+    cos, sin = ang.cos(), ang.sin()
+    qn = (torch.rand(hd, generator=g) + 0.5).half()
+    kn = (torch.rand(hd, generator=g) + 0.5).half()
+    q = torch.randn(rows, nh * hd, generator=g)
+    k = torch.randn(rows, nk * hd, generator=g) * 3.0
+    v = torch.randn(rows, nk * hd, generator=g)
+    base_k = torch.randn(nk, L, hd, generator=g).half()
+    base_v = torch.randn(nk, L, hd, generator=g).half()
+    sentinel = torch.full((rows, nh * hd), 7.0).half()
+    d = {n: t.to(cuda) for n, t in dict(q=q, k=k, v=v, qn=qn, kn=kn, cos=cos, sin=sin).items()}
+    print("qk_rope_rows", nh, nk, hd, L, rows, pos0, flush=True)
+    # the rows form
+    qo, kc, vc = sentinel.to(cuda), base_k.to(cuda), base_v.to(cuda)
+    pos = torch.tensor([pos0], dtype=torch.int64, device=cuda)
+    _L.call("sx8_dec_qk_rope_cache_rows", P(d["q"]), P(d["k"]), P(d["v"]), P(d["qn"]), P(d["kn"]),
+            P(d["cos"]), P(d["sin"]), P(pos), rows, P(qo), P(kc), P(vc), nh, nk, hd, L, eps, st)
+    # one single-token call per row
+    qo1, kc1, vc1 = sentinel.to(cuda), base_k.to(cuda), base_v.to(cuda)
+    for y in range(rows):
+        py = torch.tensor([pos0 + y], dtype=torch.int64, device=cuda)
+        _L.call("sx8_dec_qk_rope_cache", P(d["q"][y]), P(d["k"][y]), P(d["v"][y]), P(d["qn"]), P(d["kn"]),
+                P(d["cos"]), P(d["sin"]), P(py), P(qo1[y]), P(kc1), P(vc1), nh, nk, hd, L, eps, st)
+    torch.cuda.synchronize()
+    qo, kc, vc = qo.cpu(), kc.cpu(), vc.cpu()
+    assert torch.equal(qo, qo1.cpu()) and torch.equal(kc, kc1.cpu()) and torch.equal(vc, vc1.cpu())
+    ref_k, ref_v = base_k.clone(), base_v.clone()
+    ref_q = sentinel.clone().float()
+    for y in range(rows):
+        p = pos0 + y
+        if not 0 <= p < L:
+            continue
+        for h in range(nh):
+            ref_q[y, h * hd:(h + 1) * hd] = _qk_rope_ref(q[y, h * hd:(h + 1) * hd], qn, cos[p], sin[p], eps)
+        for h in range(nk):
+            ref_k[h, p] = _qk_rope_ref(k[y, h * hd:(h + 1) * hd], kn, cos[p], sin[p], eps).half()
+            ref_v[h, p] = v[y, h * hd:(h + 1) * hd].half()
+    assert torch.equal(vc, ref_v)
+    # fp16 outputs: the output's own rounding, plus one fp16 step of a normed value below 8
+    # (the reference's norm sum, in another order, can round a normed element the other way)
+    def close(a, r):
+        return bool(((a.float() - r).abs() <= 2.0 ** -10 * r.abs() + 2.0 ** -7).all())
+    assert close(qo, ref_q), (qo.float() - ref_q).abs().max().item()
+    assert close(kc, ref_k.float()), (kc.float() - ref_k.float()).abs().max().item()
 
 
 @pytest.mark.parametrize("H,I", [(2560, 9728), (1024, 8224), (512, 1056)])
