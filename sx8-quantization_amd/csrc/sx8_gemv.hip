@@ -68,6 +68,26 @@ __device__ __forceinline__ void fill_x_side(KbInfo& out, int sb, const uint4 xv)
                                                                        dot2(p0, kNegSplice[0], 0.f))));
 }
 
+// Global-memory views: a pointer that went through an SGPR pin (see k_gemv_panel) is a
+// generic pointer to the compiler, whose loads would be flat loads (counted on the LDS /
+// scalar counter as well, so any wait for a scalar load would also wait for them).
+// (The attribute applies to the device pass only; the host pass parses these bodies but
+// never emits them.)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define SX8_GLOBAL_AS __attribute__((address_space(1)))
+#else
+#define SX8_GLOBAL_AS
+#endif
+typedef const float4 SX8_GLOBAL_AS g_float4;
+typedef const uint4 SX8_GLOBAL_AS g_uint4;
+typedef const float SX8_GLOBAL_AS g_float;
+typedef const uint16_t SX8_GLOBAL_AS g_u16;
+
+template <typename T>
+__device__ __forceinline__ const T SX8_GLOBAL_AS* to_global(const T* p) {
+    return (const T SX8_GLOBAL_AS*)p;
+}
+
 constexpr int kPanelThreads = 512;
 constexpr int kLdsMaxKb = 640;     // activation table staged in LDS up to this many K blocks
 
@@ -85,55 +105,91 @@ constexpr int kLdsMaxKb = 640;     // activation table staged in LDS up to this 
 // kSilu: x is not read from X but produced from two float32 matrices (g, u with row
 // stride ldx) as fp16(silu(g) * u) = fp16(g / (1 + exp(-g)) * u), the arithmetic of
 // sx8_dec_silu_mul, so the prefill GEMM of the MLP's down projection takes the gate / up
-// outputs directly.  The plain-x forms are held to 80 VGPRs (six waves per SIMD, no spills;
-// 103 unbounded, four waves): the pass is latency-bound, and the larger grids (K = 9728,
-// 2432 work-groups at M = 2048) run in fewer rounds (down at M = 2048 147.7 -> 145.2 us per
-// prefill call, A/B).
+// outputs directly.  The packing plain-x forms are held to 80 VGPRs (six waves per SIMD, no
+// spills; 103 unbounded, four waves): the pass is latency-bound, and the larger grids (K =
+// 9728, 2432 work-groups at M = 2048) run in fewer rounds (down at M = 2048 147.7 -> 145.2
+// us per prefill call, A/B).
 template <bool kZ, bool kPack, bool kSilu = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSilu ? 1 : 6, 8))) void k_compute_z(const uint16_t* __restrict__ X, int64_t M,
-                                                   int64_t ldx, int64_t K, const sx8::ZSets zs,
-                                                   int64_t n_cb, bool x_vec, bool hl,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSilu || !kPack ? 1 : 6, 8))) void k_compute_z(const uint16_t* __restrict__ X, int M,
+                                                   int64_t ldx, int K, const sx8::ZSets zs,
+                                                   int n_cb, bool x_vec, bool hl,
                                                    uint16_t* __restrict__ Xp,
                                                    const float* __restrict__ sg,
                                                    const float* __restrict__ su) {
 #pragma clang fp contract(off)
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t rows = kPack ? (M + 31) / 32 * 32 : M;
+    // 32-bit index arithmetic: the host keeps rows * n_cb below 2^31 (a 64-bit division
+    // is a ~120-instruction sequence ahead of the first load)
+    const int gid = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    const int rows = kPack ? (M + 31) / 32 * 32 : M;
+    const int total = rows * n_cb;
     // packing: the row within its 32-row group runs fastest (whole 512-byte runs of packed
     // stores), so a work-group covers 8 (row group, kb) pairs and its basis rows are staged
     // once in LDS; otherwise kb runs fastest, which keeps every lane busy for the M = 1
     // callers
     __shared__ float4 bsh[kPack && kZ ? sx8::kMaxZSets : 1][8][16];
-    // the X loads go out first, the basis staging (global -> LDS -> barrier) after them, so
-    // the two round trips overlap; threads past the end load a valid element and stop after
-    // the barrier
-    const bool live = gid < rows * n_cb;
-    const int64_t gq = live ? gid : rows * n_cb - 1;
-    int64_t m, kb;
+    // the X loads go out first, then the scales and the basis staging (global -> LDS ->
+    // barrier), so the round trips overlap; threads past the end load a valid element and
+    // stop after the barrier
+    const bool live = gid < total;
+    const int gq = live ? gid : total - 1;
+    int m, kb;
     if constexpr (kPack) {
-        const int64_t rest = gq >> 5;
-        kb = rest % n_cb;
-        m = (rest / n_cb) * 32 + (gq & 31);
+        const int rest = gq >> 5;
+        const int grp = (int)((unsigned)rest / (unsigned)n_cb);
+        kb = rest - grp * n_cb;
+        m = grp * 32 + (gq & 31);
     } else {
-        m = gq / n_cb;
+        m = (int)((unsigned)gq / (unsigned)n_cb);
         kb = gq - m * n_cb;
     }
     const bool row_ok = m < M;
-    const int kmax = row_ok ? (int)min((int64_t)32, K - kb * 32) : 0;
+    const int kmax = row_ok ? min(32, K - kb * 32) : 0;
+    // every set's two scales of this kb, requested with the X loads (the Z products below
+    // would otherwise wait a round trip per set)
+    // (sets past zs.n read set 0's rows, which a Z launch always has, so that no load sits
+    // behind a branch; the set pointers are pinned in SGPRs, so a select between them is
+    // not turned into a load from a selected argument address)
+    float sc[sx8::kMaxZSets][2];
+    auto set_ptr = [&](const float* const* a, int s) {
+        const float* p = a[s];
+        const float* p0 = a[0];
+        asm volatile("" : "+s"(p), "+s"(p0));
+        return to_global(s < zs.n ? p : p0);
+    };
+    auto load_scales = [&]() {
+        if constexpr (kZ) {
+#pragma unroll
+            for (int s = 0; s < sx8::kMaxZSets; ++s) {
+                const g_float* p = set_ptr(zs.scales, s) + kb * 2;
+                sc[s][0] = p[0];
+                sc[s][1] = p[1];
+            }
+        }
+    };
+    // the work-group's basis rows: 16 float4 per (set, kb) for its 8 kb, at most 512
+    // float4, two per thread, both requested before either is written; a wave's 64
+    // entries share one set (t >> 7)
     auto stage_basis = [&]() {
         if constexpr (kPack && kZ) {
-            const int64_t rest0 = (int64_t)blockIdx.x * 8, nrest = rows / 32 * n_cb;
-            for (int t = threadIdx.x; t < zs.n * 128; t += 256) {
-                const int si = t >> 7, i = (t >> 4) & 7, q = t & 15;
-                const int64_t r = min(rest0 + i, nrest - 1);
-                bsh[si][i][q] = reinterpret_cast<const float4*>(zs.basis[si] + (r % n_cb) * 64)[q];
-            }
+            const int nrest = rows / 32 * n_cb;
+            const int i = ((int)threadIdx.x >> 4) & 7, q = (int)threadIdx.x & 15;
+            const int r = min((int)blockIdx.x * 8 + i, nrest - 1);
+            const int row = (int)((unsigned)r % (unsigned)n_cb) * 64;
+            const int s0 = (int)threadIdx.x >> 7, s1 = s0 + 2;
+            const g_float* p0 = set_ptr(zs.basis, 0);
+            const g_float* p1 = set_ptr(zs.basis, 1);
+            const g_float* p2 = set_ptr(zs.basis, 2);
+            const g_float* p3 = set_ptr(zs.basis, 3);
+            const float4 v0 = reinterpret_cast<g_float4*>((s0 == 0 ? p0 : p1) + row)[q];
+            const float4 v1 = reinterpret_cast<g_float4*>((s1 == 2 ? p2 : p3) + row)[q];
+            if (s0 < zs.n) bsh[s0][i][q] = v0;
+            if (s1 < zs.n) bsh[s1][i][q] = v1;
             __syncthreads();
         }
     };
     uint32_t xw[16];
     if constexpr (kSilu) {
-        const int64_t off = min(m, M - 1) * ldx + kb * 32;
+        const int64_t off = (int64_t)min(m, M - 1) * ldx + kb * 32;
         float gv[32], uv[32];
         if (x_vec && kmax == 32) {
 #pragma unroll
@@ -150,6 +206,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSilu ? 1 :
                 uv[t] = t < kmax ? su[off + t] : 0.f;
             }
         }
+        load_scales();
         stage_basis();
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
@@ -159,7 +216,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSilu ? 1 :
                     ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x1) << 16);
         }
     } else {
-    const uint16_t* x = X + min(m, M - 1) * ldx + kb * 32;
+    const uint16_t* x = X + (int64_t)min(m, M - 1) * ldx + kb * 32;
     if (x_vec && kmax == 32) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -174,44 +231,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSilu ? 1 :
             xw[t] = a | (b << 16);
         }
     }
+    load_scales();
     stage_basis();
     }
     if (!live) return;
     if constexpr (kPack) {
-        const int64_t G = m >> 5;
-        const int r = (int)(m & 31);
+        const int G = m >> 5;
+        const int r = m & 31;
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
-                uint4* dst = reinterpret_cast<uint4*>(Xp + ((G * n_cb + kb) * 2 + st) * 512 + (hf * 32 + r) * 8);
+                uint4* dst = reinterpret_cast<uint4*>(Xp + (((int64_t)G * n_cb + kb) * 2 + st) * 512 + (hf * 32 + r) * 8);
                 const int q = 8 * hf + 4 * st;
                 *dst = make_uint4(xw[q], xw[q + 1], xw[q + 2], xw[q + 3]);
             }
     }
     if constexpr (kZ) {
         if (!row_ok) return;
-        const int64_t zi = m * n_cb + kb;
-        for (int s = 0; s < zs.n; ++s) {
+        const int64_t zi = (int64_t)m * n_cb + kb;
+        auto xf = [&](int t) { return sx8_h2f(xw[t >> 1] >> (16 * (t & 1))); };
+#pragma unroll
+        for (int s = 0; s < sx8::kMaxZSets; ++s) {
+            if (s >= zs.n) break;
             const float4* bv = kPack ? &bsh[s][threadIdx.x >> 5][0]
                                      : reinterpret_cast<const float4*>(zs.basis[s] + kb * 64);
             float z[2];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                float p[32];
+                // products x_t * b_t, then the tree: level 16 as each pair (t, t + 16)
+                // arrives (float4 q and q + 4), then offsets 8, 4, 2, 1
+                float p[16];
 #pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const float4 b = bv[8 * j + q];
-                    p[4 * q] = sx8_h2f(xw[2 * q]) * b.x;
-                    p[4 * q + 1] = sx8_h2f(xw[2 * q] >> 16) * b.y;
-                    p[4 * q + 2] = sx8_h2f(xw[2 * q + 1]) * b.z;
-                    p[4 * q + 3] = sx8_h2f(xw[2 * q + 1] >> 16) * b.w;
+                for (int q = 0; q < 4; ++q) {
+                    const float4 lo = bv[8 * j + q], hi = bv[8 * j + q + 4];
+                    p[4 * q] = xf(4 * q) * lo.x + xf(4 * q + 16) * hi.x;
+                    p[4 * q + 1] = xf(4 * q + 1) * lo.y + xf(4 * q + 17) * hi.y;
+                    p[4 * q + 2] = xf(4 * q + 2) * lo.z + xf(4 * q + 18) * hi.z;
+                    p[4 * q + 3] = xf(4 * q + 3) * lo.w + xf(4 * q + 19) * hi.w;
                 }
 #pragma unroll
-                for (int off = 16; off > 0; off >>= 1)
+                for (int off = 8; off > 0; off >>= 1)
 #pragma unroll
                     for (int t = 0; t < off; ++t) p[t] = p[t] + p[t + off];
-                z[j] = zs.scales[s][kb * 2 + j] * p[0];
+                z[j] = sc[s][j] * p[0];
             }
             float* Z = zs.Z[s];
             if (hl)
@@ -383,26 +446,6 @@ struct TabIn {
     float4 b0[2], b1[2];
     float s;
 };
-
-// Global-memory views: a pointer that went through an SGPR pin (see k_gemv_panel) is a
-// generic pointer to the compiler, whose loads would be flat loads (counted on the LDS /
-// scalar counter as well, so any wait for a scalar load would also wait for them).
-// (The attribute applies to the device pass only; the host pass parses these bodies but
-// never emits them.)
-#if defined(__HIP_DEVICE_COMPILE__)
-#define SX8_GLOBAL_AS __attribute__((address_space(1)))
-#else
-#define SX8_GLOBAL_AS
-#endif
-typedef const float4 SX8_GLOBAL_AS g_float4;
-typedef const uint4 SX8_GLOBAL_AS g_uint4;
-typedef const float SX8_GLOBAL_AS g_float;
-typedef const uint16_t SX8_GLOBAL_AS g_u16;
-
-template <typename T>
-__device__ __forceinline__ const T SX8_GLOBAL_AS* to_global(const T* p) {
-    return (const T SX8_GLOBAL_AS*)p;
-}
 
 template <int kMode, bool kLoadX = true>
 __device__ __forceinline__ void tab_load(TabIn& t, const g_u16* __restrict__ X,
@@ -1164,33 +1207,37 @@ extern "C" int64_t sx8_gemv_workspace_bytes(int64_t n_cb) {
 int32_t sx8::compute_z_sets(const uint16_t* X, int64_t M, int64_t ldx, int64_t K, const ZSets& zs,
                            int64_t n_cb, bool hl, uint16_t* xpack, hipStream_t st) {
     const int64_t rows = xpack ? (M + 31) / 32 * 32 : M;
+    if (rows * n_cb > 0x7FFFFFFF - 255 || K > n_cb * 32)
+        return fail(SX8_ERR_UNSUPPORTED, "compute_z: %lld rows x %lld K blocks exceed 2^31", (long long)rows,
+                    (long long)n_cb);
     const int64_t grid = (rows * n_cb + 255) / 256;
-    if (grid > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "compute_z: too large");
     const bool x_vec = aligned(X, 16) && ldx % 8 == 0;
     if (zs.n > 0 && xpack)
-        hipLaunchKernelGGL((k_compute_z<true, true>), dim3((unsigned)grid), dim3(256), 0, st, X, M, ldx,
-                           K, zs, n_cb, x_vec, hl, xpack, nullptr, nullptr);
+        hipLaunchKernelGGL((k_compute_z<true, true>), dim3((unsigned)grid), dim3(256), 0, st, X, (int)M, ldx,
+                           (int)K, zs, (int)n_cb, x_vec, hl, xpack, nullptr, nullptr);
     else if (zs.n > 0)
-        hipLaunchKernelGGL((k_compute_z<true, false>), dim3((unsigned)grid), dim3(256), 0, st, X, M,
-                           ldx, K, zs, n_cb, x_vec, hl, xpack, nullptr, nullptr);
+        hipLaunchKernelGGL((k_compute_z<true, false>), dim3((unsigned)grid), dim3(256), 0, st, X, (int)M,
+                           ldx, (int)K, zs, (int)n_cb, x_vec, hl, xpack, nullptr, nullptr);
     else if (xpack)
-        hipLaunchKernelGGL((k_compute_z<false, true>), dim3((unsigned)grid), dim3(256), 0, st, X, M,
-                           ldx, K, zs, n_cb, x_vec, hl, xpack, nullptr, nullptr);
+        hipLaunchKernelGGL((k_compute_z<false, true>), dim3((unsigned)grid), dim3(256), 0, st, X, (int)M,
+                           ldx, (int)K, zs, (int)n_cb, x_vec, hl, xpack, nullptr, nullptr);
     return check_launch("compute_z");
 }
 
 int32_t sx8::compute_z_silu(const float* g, const float* u, int64_t M, int64_t ld, int64_t K,
                            const ZSets& zs, int64_t n_cb, uint16_t* xpack, hipStream_t st) {
     const int64_t rows = (M + 31) / 32 * 32;
+    if (rows * n_cb > 0x7FFFFFFF - 255 || K > n_cb * 32)
+        return fail(SX8_ERR_UNSUPPORTED, "compute_z: %lld rows x %lld K blocks exceed 2^31", (long long)rows,
+                    (long long)n_cb);
     const int64_t grid = (rows * n_cb + 255) / 256;
-    if (grid > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "compute_z: too large");
     const bool vec = aligned(g, 16) && aligned(u, 16) && ld % 4 == 0;
     if (zs.n > 0)
-        hipLaunchKernelGGL((k_compute_z<true, true, true>), dim3((unsigned)grid), dim3(256), 0, st, nullptr, M,
-                           ld, K, zs, n_cb, vec, true, xpack, g, u);
+        hipLaunchKernelGGL((k_compute_z<true, true, true>), dim3((unsigned)grid), dim3(256), 0, st, nullptr, (int)M,
+                           ld, (int)K, zs, (int)n_cb, vec, true, xpack, g, u);
     else
-        hipLaunchKernelGGL((k_compute_z<false, true, true>), dim3((unsigned)grid), dim3(256), 0, st, nullptr, M,
-                           ld, K, zs, n_cb, vec, true, xpack, g, u);
+        hipLaunchKernelGGL((k_compute_z<false, true, true>), dim3((unsigned)grid), dim3(256), 0, st, nullptr, (int)M,
+                           ld, (int)K, zs, (int)n_cb, vec, true, xpack, g, u);
     return check_launch("compute_z");
 }
 
