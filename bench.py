@@ -812,7 +812,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
-              "multi-GPU path (see DESIGN.md, 'sharding')", file=sys.stderr)
+              "multi-GPU path: the value is one GPU's throughput", file=sys.stderr)
         sys.exit(2)
     import torch
     import _sx8lib as L
