@@ -626,7 +626,8 @@ def bench_e2e(torch, args):
     """Config 5: 36-layer random-init Qwen3-4B-style decoder on S-X8 weights (every layer
     quantized separately), batch 1: a 512-token prefill of uniform-random ids, then 256
     greedy tokens, one decode step replayed from a HIP graph.  The whole generate() runs
-    twice; the second (warm) run is reported.  Generation's prefill computes the lm_head
+    twice; the second (warm) run is reported, then once more with every decode step launched
+    from the host (no graph).  Generation's prefill computes the lm_head
     for the last prompt row only (all it needs); the prefill with logits for every row --
     what a Hugging Face forward computes -- is timed separately."""
     from e2e_decoder import QWEN3_4B, SX8Decoder
@@ -636,6 +637,7 @@ def bench_e2e(torch, args):
     g = torch.Generator(device="cpu").manual_seed(11)
     ids = torch.randint(0, QWEN3_4B["vocab"], (args.e2e_prompt,), generator=g).cuda()
     res = None
+    out = None
     for _ in range(2):
         out, tp, td = dec.generate(ids, args.e2e_new, use_graph=True)
         res = {"prompt": args.e2e_prompt, "new_tokens": args.e2e_new,
@@ -647,6 +649,14 @@ def bench_e2e(torch, args):
                                  (ly.q, ly.k, ly.v, ly.o, ly.gate, ly.up, ly.down)
                                  for t in lin._t44[:2]) / 1e9 + sum(t.numel() for t in dec.head._t44[:2]) / 1e9}
         log("e2e", json.dumps(res))
+    # the same decode without the graph: every step's launches issued from the host (the
+    # same kernels; the greedy tokens must not change)
+    out_e, _, td_e = dec.generate(ids, args.e2e_new, use_graph=False)
+    res["decode_eager_ms_per_token"] = td_e * 1e3 / (args.e2e_new - 1)
+    res["decode_eager_tok_s"] = (args.e2e_new - 1) / td_e
+    res["eager_tokens_equal_graph"] = bool(torch.equal(out_e, out))
+    log("e2e eager decode", f"{res['decode_eager_ms_per_token']:.3f} ms/token, tokens equal: "
+        f"{res['eager_tokens_equal_graph']}")
     times = []
     for _ in range(3):
         torch.cuda.synchronize()
