@@ -113,7 +113,7 @@ int32_t sx8_v6_encode(const uint16_t* W, int64_t out_f, int64_t in_f, int64_t ld
  * Replaces compute_z44 (cuda/sx8_decode1_v3.cu:185-195, kernel :44-65) for M = 1 and
  * compute_z44_batch (cuda/sx8_gemm_compact.cu:157-169, kernel :28-50) for M > 1.
  * X is (M, ldx) fp16 with ldx >= n_cb*32.  Z is (M, n_cb, 2) float32 (8-byte aligned);
- * basis 16-byte aligned. */
+ * basis 16-byte aligned.  M * n_cb below 2^31 (SX8_ERR_UNSUPPORTED otherwise). */
 int32_t sx8_compute_z(const uint16_t* X, int64_t M, int64_t ldx, const float* basis,
                       const float* scales, int64_t n_cb, float* Z, void* stream);
 

@@ -60,6 +60,8 @@ def test_invalid_arguments_rejected_on_host(hiplib):
     assert L.sx8_gemm_prefill(p, 4, 32, 64, p, p, 6, p, p, 64, 2, p, p, 1 << 20, NULL) == 1   # ldx < K
     assert L.sx8_embed_gather(p, 4, p, p, 5, p, p, 64, 10, 2, p, NULL) == 1
     assert L.sx8_compute_z(p, 1, 16, p, p, 1, p, NULL) == 1                      # ldx < 32
+    assert L.sx8_compute_z(p, 1 << 26, 2048, p, p, 64, p, NULL) == 3             # M n_cb >= 2^31
+    assert "2^31" in _err(L)
     assert L.sx8_gemm_pca_z(NULL, 1, p, 6, 64, 2, p, NULL) == 1
     assert L.sx8_gemm_prefill_z(p, 4, 64, 64, p, p, 6, NULL, 64, 2, p, p, 1 << 20, NULL) == 1   # Z missing
     assert L.sx8_gemm_prefill_z(p, 4, 64, 64, p, p, 6, p, 64, 3, p, p, 1 << 20, NULL) == 1      # n_cb != K/32
