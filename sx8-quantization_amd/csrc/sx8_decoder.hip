@@ -709,7 +709,9 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict
 // head), two sets of G waves (one for G = 8): wave g of set s takes query head kvh * G + g
 // and the key blocks s, s + 2, s + 4, ... (two waves per SIMD, each with half of the
 // tile's serial chain; the sets merge their softmax states at the end).  The G heads of a set share
-// the staged K and V of its block.  Per 32-key block a wave computes S^T = K Q^T: keys
+// the staged K and V of its block.  A work-group may instead take GW of the G heads (G / GW
+// work-groups per KV head and tile) in NS sets of GW waves, set s taking blocks s, s + NS,
+// ... (the host uses GW = 2, NS = 4 when G = 4 and the plain grid is short of the CUs).  Per 32-key block a wave computes S^T = K Q^T: keys
 // are the MFMA rows and the tile's 32 queries the columns, so lane l = 32 h + c owns query
 // c (keys 8 g + 4 h + r of the block in accumulator 4 g + r) and the online softmax is
 // lane-local (one exchange with lane l ^ 32 for the other 16 keys).  Then O^T += V^T P^T:
@@ -734,38 +736,40 @@ __device__ __forceinline__ float lane_swap32(float v) {
 template <int G>
 constexpr int ap_sets() { return G <= 4 ? 2 : 1; }
 
-template <int HD, int G>
+template <int HD, int GW, int NS>
 struct ApLds {
-    static constexpr int NS = ap_sets<G>();
     static constexpr int kK = 32 * kApKRow * 2;                 // bytes of one staged K block
     static constexpr int kV = HD * kApVRow * 2;                 // bytes of one staged V^T block
     static constexpr int kStage = 2 * NS * (kK + kV);           // [buffer][set]
-    static constexpr int kMerge = NS > 1 ? G * 64 * (2 + 16 * (HD / 32)) * 4 : 0;
+    static constexpr int kMerge = (NS - 1) * GW * 64 * (2 + 16 * (HD / 32)) * 4;   // sets 1 .. NS - 1
     static constexpr int kBytes = kStage > kMerge ? kStage : kMerge;
 };
 
-template <int HD, int G>
-__global__ __launch_bounds__(64 * G * ap_sets<G>()) void k_attn_prefill(const uint16_t* __restrict__ q,
+// GW of the G query heads of a KV head per work-group (G / GW work-groups per KV head and
+// query tile), NS sets of GW waves: set s takes key blocks s, s + NS, s + 2 NS, ...
+template <int HD, int G, int GW, int NS>
+__global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* __restrict__ q,
                                                           const uint16_t* __restrict__ k_cache,
                                                           const uint16_t* __restrict__ v_cache,
                                                           uint16_t* __restrict__ out, int T, int start,
                                                           int nh, int L, float scale_log2) {
     typedef float f32x16 __attribute__((ext_vector_type(16)));
     typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-    using Lds = ApLds<HD, G>;
-    constexpr int NS = Lds::NS;
+    using Lds = ApLds<HD, GW, NS>;
+    static_assert(G % GW == 0 && NS >= 1 && NS <= 4, "k_attn_prefill: head split / sets");
     constexpr int KS = HD / 16;                 // k-steps of S^T over the head dimension
     constexpr int NT = HD / 32;                 // 32-row tiles of O^T
     constexpr int CPR = HD / 8;                 // 16-byte chunks per key row
-    constexpr int ST = 64 * G;                  // threads per set
+    constexpr int ST = 64 * GW;                 // threads per set
     constexpr int KCH = 32 * CPR / ST;          // K chunks staged per thread and block
     static_assert(KCH >= 1 && KCH * ST == 32 * CPR, "K staging split");
     constexpr int VPT = (16 * CPR + ST - 1) / ST;   // V key-pair tasks per thread
     __shared__ __align__(16) unsigned char lds[Lds::kBytes];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int set = w / G, g = w % G, ts = tid % ST;
+    const int set = w / GW, g = w % GW, ts = tid % ST;
     const int c = lane & 31, h = lane >> 5;
-    const int kvh = blockIdx.y, head = kvh * G + g;
+    constexpr int R = G / GW;
+    const int kvh = blockIdx.y / R, head = kvh * G + (blockIdx.y % R) * GW + g;
     const int q0 = blockIdx.x * 32, qi = q0 + c;
     const int ktot = start + T;                                 // keys in the cache
     const int nblk = (start + min(q0 + 32, T) + 31) / 32;       // key blocks this tile needs
@@ -925,9 +929,9 @@ __global__ __launch_bounds__(64 * G * ap_sets<G>()) void k_attn_prefill(const ui
         for (int i = 0; i < kPf; ++i)
             if (j + i < nstep) body(j + i, kreg[i], vreg[i]);
     }
-    // merge: set 1 hands (m, lsum, O^T) to its partner wave of set 0 through LDS (the
-    // staging buffers are free after the last barrier); lane-contiguous rows
-    float* mg = reinterpret_cast<float*>(lds) + g * 64 * (2 + 16 * NT);
+    // merge: sets 1 .. NS - 1 hand (m, lsum, O^T) to their partner wave of set 0 through LDS
+    // (the staging buffers are free after the last barrier); lane-contiguous rows
+    constexpr int kMg = 64 * (2 + 16 * NT);                    // floats per handed-over state
     if (NS == 1) {
         if (qi >= T) return;
         const float inv = 1.0f / lsum;
@@ -943,7 +947,8 @@ __global__ __launch_bounds__(64 * G * ap_sets<G>()) void k_attn_prefill(const ui
             }
         return;
     }
-    if (set == 1) {
+    if (set > 0) {
+        float* mg = reinterpret_cast<float*>(lds) + ((set - 1) * GW + g) * kMg;
         mg[lane] = m;
         mg[64 + lane] = lsum;
 #pragma unroll
@@ -952,13 +957,31 @@ __global__ __launch_bounds__(64 * G * ap_sets<G>()) void k_attn_prefill(const ui
             for (int r = 0; r < 16; ++r) mg[(2 + 16 * n + r) * 64 + lane] = o[n][r];
     }
     __syncthreads();
-    if (set == 1 || qi >= T) return;
-    const float m1 = mg[lane], l1 = mg[64 + lane];
-    const float mm = fmaxf(m, m1);                    // m is finite: set 0 owns block 0
-    const float f0 = __builtin_amdgcn_exp2f(m - mm);
-    const float f1 = m1 == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
-    const float inv = 1.0f / (lsum * f0 + l1 * f1);
-    const float a0 = f0 * inv, a1 = f1 * inv;
+    if (set > 0 || qi >= T) return;
+    // set s's state weighs 2^(m_s - max m); an empty set (m = -inf) weighs nothing, and m is
+    // finite in set 0, which owns block 0
+    const float* mg1 = reinterpret_cast<const float*>(lds) + g * kMg;
+    float ms[NS], ls[NS], f[NS];
+    ms[0] = m;
+    ls[0] = lsum;
+#pragma unroll
+    for (int t = 1; t < NS; ++t) {
+        ms[t] = mg1[(t - 1) * GW * kMg + lane];
+        ls[t] = mg1[(t - 1) * GW * kMg + 64 + lane];
+    }
+    float mm = ms[0];
+#pragma unroll
+    for (int t = 1; t < NS; ++t) mm = fmaxf(mm, ms[t]);
+    f[0] = __builtin_amdgcn_exp2f(m - mm);
+#pragma unroll
+    for (int t = 1; t < NS; ++t) f[t] = ms[t] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(ms[t] - mm);
+    float den = ls[0] * f[0];
+#pragma unroll
+    for (int t = 1; t < NS; ++t) den += ls[t] * f[t];
+    const float inv = 1.0f / den;
+    float wgt[NS];
+#pragma unroll
+    for (int t = 0; t < NS; ++t) wgt[t] = f[t] * inv;
     uint16_t* orow = out + ((int64_t)qi * nh + head) * HD;
 #pragma unroll
     for (int n = 0; n < NT; ++n)
@@ -966,7 +989,11 @@ __global__ __launch_bounds__(64 * G * ap_sets<G>()) void k_attn_prefill(const ui
         for (int gq = 0; gq < 4; ++gq) {
             float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = o[n][4 * gq + e] * a0 + mg[(2 + 16 * n + 4 * gq + e) * 64 + lane] * a1;
+            for (int e = 0; e < 4; ++e) {
+                v[e] = o[n][4 * gq + e] * wgt[0];
+#pragma unroll
+                for (int t = 1; t < NS; ++t) v[e] += mg1[(t - 1) * GW * kMg + (2 + 16 * n + 4 * gq + e) * 64 + lane] * wgt[t];
+            }
             const int d = 32 * n + 8 * gq + 4 * h;
             const uint32_t lo = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
             const uint32_t hi = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
@@ -1063,10 +1090,17 @@ extern "C" int32_t sx8_dec_attn_prefill(const uint16_t* q, const uint16_t* k_cac
     const float sl2 = scale * 1.4426950408889634f;
     const dim3 grid((unsigned)((T + 31) / 32), (unsigned)nk);
 #define SX8_AP(HD_, G_)                                                                                      \
-    hipLaunchKernelGGL((k_attn_prefill<HD_, G_>), grid, dim3(64 * G_ * ap_sets<G_>()), 0, as_stream(stream), q, \
-                       k_cache, v_cache, out, (int)T, (int)start, nh, (int)L, sl2)
+    hipLaunchKernelGGL((k_attn_prefill<HD_, G_, G_, ap_sets<G_>()>), grid, dim3(64 * G_ * ap_sets<G_>()), 0,     \
+                       as_stream(stream), q, k_cache, v_cache, out, (int)T, (int)start, nh, (int)L, sl2)
     if (hd == 128) {
-        if (G == 1) SX8_AP(128, 1); else if (G == 2) SX8_AP(128, 2); else if (G == 4) SX8_AP(128, 4); else SX8_AP(128, 8);
+        if (G == 4 && (int64_t)grid.x * grid.y < 256) {
+            // a grid short of one work-group per CU: two work-groups per KV head and tile (two
+            // heads each) with four sets of two waves, so the longest (last) tiles' chain of key
+            // blocks is half as long (T = 512: 18.3 -> 16.6 us).  Past that the heads share
+            // the staging of four per work-group (T = 2048: 90 us against 117 for this form).
+            hipLaunchKernelGGL((k_attn_prefill<128, 4, 2, 4>), dim3(grid.x, 2 * grid.y), dim3(512), 0,
+                               as_stream(stream), q, k_cache, v_cache, out, (int)T, (int)start, nh, (int)L, sl2);
+        } else if (G == 4) SX8_AP(128, 4); else if (G == 1) SX8_AP(128, 1); else if (G == 2) SX8_AP(128, 2); else SX8_AP(128, 8);
     } else {
         if (G == 1) SX8_AP(64, 1); else if (G == 2) SX8_AP(64, 2); else SX8_AP(64, 4);
     }

@@ -65,6 +65,7 @@ def test_decode_attention_split_and_single(hiplib, cuda, nh, nk, hd, L, position
     (32, 8, 128, 128, 1, 77),       # one row after 77 cached positions
     (2, 1, 128, 160, 40, 5),        # G = 2 at hd 128
     (8, 8, 128, 256, 100, 0),       # G = 1 at hd 128
+    (32, 8, 128, 1200, 1100, 50),   # G = 4 on a grid of 280 work-groups (four heads per group)
 ])
 def test_prefill_attention(hiplib, cuda, nh, nk, hd, L, T, start):
     """sx8_dec_attn_prefill against float32 causal attention; cache rows past start + T
