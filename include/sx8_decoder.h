@@ -120,7 +120,8 @@ int32_t sx8_dec_silu_mul(const float* g, const float* u, uint16_t* out, int64_t 
  * sx8_dec_gemv_silu_add / sx8_dec_gemv_add: x = fp16(silu(g) * u), or x given (fp16, 16-byte
  * aligned), and Ys[i] = adds[i] + W_i . x: the residual add of the decoder layer in the
  * GEMV's final store (each element read and written by one thread, so adds[i] may be
- * Ys[i]: the residual stream updated in place).
+ * Ys[i]: the residual stream updated in place).  adds[i] is 4-byte aligned and either
+ * equals Ys[i] or overlaps no output vector; any other overlap is refused.
  * All need n_cb <= 384 and take bases/scales (no caller Z). */
 int32_t sx8_dec_gemv_rmsnorm(const float* resid, const uint16_t* init, const float* delta,
                              const uint16_t* norm_w, float eps, float* resid_out, int32_t n_mats,
@@ -148,14 +149,18 @@ int32_t sx8_dec_gemv_add(const uint16_t* x, int32_t n_mats, const uint8_t* const
  * sx8_dec_gemv_rmsnorm with the residual alone), g = W_gate x and u = W_up x in one
  * launch, m = fp16(silu(g) * u) (as sx8_dec_silu_mul) to m, and zp = the down projection's
  * PCA sums of m per K block in two partial slots, (N / 32, 2, 2) floats.  The up matrix's
- * headers, levels, bases and scales must follow the gate matrix's in memory (hdr, levels,
- * bases, scales point at the gate's; each array holds both); N a multiple of 32 in
- * 32..16384 (the down projection's K); down_bases its (N / 32, 64) bases.
+ * headers, levels, bases and scales (up_*) must follow the gate matrix's in memory
+ * (up_hdr = hdr + N * n_cb * hdr_bytes, up_levels = levels + N * n_cb * 24, up_bases =
+ * bases + n_cb * 64, up_scales = scales + n_cb * 2: one allocation per field holding both),
+ * otherwise SX8_ERR_INVALID; N a multiple of 32 in 32..12288 (the down projection's K, as
+ * sx8_dec_gemv_zp_add accepts); down_bases its (N / 32, 64) bases.
  * sx8_dec_gemv_zp_add: Y = add + W_down m with the PCA term from zp (Z = (zp[kb][0][c] +
  * zp[kb][1][c]) * scales[kb][c]); add may be Y (the residual updated in place). */
 int32_t sx8_dec_gemv_rmsnorm_pair(const float* resid, const uint16_t* norm_w, float eps,
                                   const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
-                                  const float* bases, const float* scales, int64_t N, int64_t n_cb,
+                                  const float* bases, const float* scales, const uint8_t* up_hdr,
+                                  const uint8_t* up_levels, const float* up_bases,
+                                  const float* up_scales, int64_t N, int64_t n_cb,
                                   const float* down_bases, uint16_t* m, float* zp, void* stream);
 int32_t sx8_dec_gemv_zp_add(const uint16_t* m, const uint8_t* hdr, const uint8_t* levels,
                             int32_t hdr_bytes, const float* zp, const float* scales, int64_t N,

@@ -155,10 +155,21 @@ int64_t sx8_gemv_workspace_bytes(int64_t n_cb);
  * packed copy of X and the split-K partials of the plan the call will run.  The same value
  * serves sx8_gemm_prefill, _split, _z, _core (n_mats = 1) and _group; sx8_dec_gemm_silu
  * (K = its inner size).  -1 for an invalid shape.  The plan depends only on (M, sum Ns,
- * the group's column tiles, n_cb) and on the SX8_GEMM_TILE environment variable at the
- * time of the call.  No counterpart in the reference, whose wrappers allocate outputs and
- * Z with torch inside each call (cuda/sx8_gemm_compact.cu:157-194). */
+ * the group's column tiles, n_cb) and on the tuning variables SX8_GEMM_TILE, SX8_GEMM_PLAN
+ * and SX8_GEMM_W2 as the library last read them (see sx8_gemm_reload_tuning), so a size
+ * returned here stays valid for later calls with the same sizes.  No counterpart in the
+ * reference, whose wrappers allocate outputs and Z with torch inside each call
+ * (cuda/sx8_gemm_compact.cu:157-194). */
 int64_t sx8_gemm_prefill_workspace_bytes(int64_t M, int32_t n_mats, const int64_t* Ns, int64_t n_cb);
+
+/* Prefill tuning variables (for tuning runs and tests; a default run sets none):
+ * SX8_GEMM_TILE=256|512 forces the tile height, SX8_GEMM_PLAN=k<1|2>:<S> (128- or 256-row
+ * tiles in S K ranges) or w<0|1>:<St> (512-row tiles; 1: whole rounds of 256 tiles first,
+ * St K ranges for the rest) forces one plan when it is valid for the shape, SX8_GEMM_W2=0
+ * runs 512-row plans on the one-wave-per-SIMD kernel.  The library reads them once, at the
+ * first prefill call or query; this call reads them again.  Not to be called while prefill
+ * calls or queries run on other threads.  No counterpart in the reference. */
+int32_t sx8_gemm_reload_tuning(void);
 
 /* The plan a prefill call with these sizes runs (for logs and tests): desc[0] tile rows
  * (128, 256 or 512), desc[1] work-groups, desc[2] K ranges, desc[3] K blocks per range,

@@ -53,6 +53,7 @@ SIGNATURES = [
     ("sx8_gemv_workspace_bytes", _I64, [_I64]),
     ("sx8_gemm_prefill_workspace_bytes", _I64, [_I64, _I32, _P, _I64]),
     ("sx8_gemm_prefill_plan", _I32, [_I64, _I32, _P, _I64, _P]),
+    ("sx8_gemm_reload_tuning", _I32, []),
     ("sx8_gemm_prefill", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _I64, _P]),
     ("sx8_gemm_prefill_static", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P]),
     ("sx8_gemm_prefill_split", _I32,
@@ -86,7 +87,8 @@ SIGNATURES = [
     ("sx8_dec_gemv_silu", _I32, [_P, _P, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P]),
     ("sx8_dec_gemv_silu_add", _I32, [_P, _P, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P, _P]),
     ("sx8_dec_gemv_add", _I32, [_P, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P, _P]),
-    ("sx8_dec_gemv_rmsnorm_pair", _I32, [_P, _P, ctypes.c_float, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _P, _P]),
+    ("sx8_dec_gemv_rmsnorm_pair", _I32, [_P, _P, ctypes.c_float, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _I64, _I64,
+                                         _P, _P, _P, _P]),
     ("sx8_dec_gemv_zp_add", _I32, [_P, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _P]),
 ]
 ABI_VERSION = 2
@@ -214,6 +216,37 @@ def gemm_plan(M, Ns, n_cb):
     call("sx8_gemm_prefill_plan", int(M), n, (ctypes.c_int64 * n)(*[int(v) for v in Ns]), int(n_cb), desc)
     keys = ("tile", "groups", "k_ranges", "kb_per_range", "whole_tiles", "split_tiles", "workspace")
     return dict(zip(keys, (int(v) for v in desc[:7])))
+
+
+GEMM_TUNING_VARS = ("SX8_GEMM_TILE", "SX8_GEMM_PLAN", "SX8_GEMM_W2")
+
+
+class GemmTuning:
+    """Prefill tuning variables set from Python (tuning runs and tests).  The library reads
+    SX8_GEMM_TILE / SX8_GEMM_PLAN / SX8_GEMM_W2 once; set() changes them and makes the
+    library read them again (sx8_gemm_reload_tuning), restore() puts back what was there."""
+
+    def __init__(self):
+        self._saved = {k: os.environ.get(k) for k in GEMM_TUNING_VARS}
+
+    def set(self, **kv):
+        for k, v in kv.items():
+            name = "SX8_GEMM_" + k.upper()
+            if name not in GEMM_TUNING_VARS:
+                raise KeyError(name)
+            if v is None:
+                os.environ.pop(name, None)
+            else:
+                os.environ[name] = str(v)
+        call("sx8_gemm_reload_tuning")
+
+    def restore(self):
+        for k, v in self._saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+        call("sx8_gemm_reload_tuning")
 
 
 def as_device(a, np_dtype, device):

@@ -1361,21 +1361,55 @@ Plan plan_w1(int64_t M, int64_t NB, int64_t n_cb, int64_t part_cap) {
     return best;
 }
 
-// N columns in NB column tiles (a group pads every matrix to whole tiles).
-// Tuning knobs: SX8_GEMM_TILE=256 or 512 forces a tile height; SX8_GEMM_PLAN forces one plan,
-// "k<MF>:<S>" (128 MF-row tiles in S K ranges) or "w<0|1>:<St>" (512-row tiles, 1: whole
-// rounds first, St K ranges for the rest); otherwise the cheaper plan.  part_cap bounds the
-// split-K partial bytes (the unsplit plans need none).
+// Tuning knobs, read from the environment once (at the first prefill call or plan query) and
+// again only by sx8_gemm_reload_tuning, so a workspace sized for a call stays valid for it:
+// SX8_GEMM_TILE=256 or 512 forces a tile height; SX8_GEMM_PLAN forces one plan, "k<MF>:<S>"
+// (128 MF-row tiles in S K ranges) or "w<0|1>:<St>" (512-row tiles, 1: whole rounds first,
+// St K ranges for the rest); SX8_GEMM_W2=0 runs 512-row plans on k_gemm_w1.
+struct Tuning {
+    int tile = 0;          // 0: the planner's choice
+    bool w2 = true;
+    bool plan = false;     // SX8_GEMM_PLAN parsed
+    char kind = 0;
+    int a = 0, b = 0;
+};
+
+Tuning read_tuning() {
+    Tuning t;
+    if (const char* e = getenv("SX8_GEMM_TILE")) t.tile = atoi(e);
+    if (const char* e = getenv("SX8_GEMM_W2")) t.w2 = atoi(e) != 0;
+    if (const char* f = getenv("SX8_GEMM_PLAN"))
+        t.plan = sscanf(f, "%c%d:%d", &t.kind, &t.a, &t.b) == 3;
+    return t;
+}
+
+std::mutex g_tuning_mu;
+Tuning g_tuning;
+bool g_tuning_read = false;
+
+Tuning tuning() {
+    std::lock_guard<std::mutex> lk(g_tuning_mu);
+    if (!g_tuning_read) {
+        g_tuning = read_tuning();
+        g_tuning_read = true;
+    }
+    return g_tuning;
+}
+
+// N columns in NB column tiles (a group pads every matrix to whole tiles).  The plan forced
+// by SX8_GEMM_PLAN if it is valid for the shape, else SX8_GEMM_TILE's tile height, else the
+// cheaper plan.  part_cap bounds the split-K partial bytes (the unsplit plans need none).
 Plan plan_gemm(int64_t M, int64_t N, int64_t NB, int64_t n_cb, int64_t part_cap = INT64_MAX) {
     const int MF = M > 128 ? 2 : 1;
     // k_gemm_w1 addresses rows up to the next multiple of 512 with 31-bit offsets
     const int64_t Mp = (M + kW1BM - 1) / kW1BM * kW1BM;
     const bool w1_ok = M > 256 && Mp / 32 * n_cb * 2048 <= 0x7FFFFFFF && Mp * n_cb * 8 <= 0x7FFFFFFF;
-    if (const char* f = getenv("SX8_GEMM_PLAN")) {
-        char kind = 0;
-        int a = 0, b = 0;
+    const Tuning tu = tuning();
+    if (tu.plan) {
+        const char kind = tu.kind;
+        const int a = tu.a, b = tu.b;
         const int64_t groups = (n_cb + 3) / 4;
-        if (sscanf(f, "%c%d:%d", &kind, &a, &b) == 3 && b >= 1 && b <= std::min<int64_t>(8, groups)) {
+        if (b >= 1 && b <= std::min<int64_t>(8, groups)) {
             if (kind == 'k' && (a == 1 || a == 2)) {
                 const int64_t T = ((M + 128 * a - 1) / (128 * a)) * NB;
                 const Plan p = plan_split(M, N, T, n_cb, b, a);
@@ -1391,8 +1425,7 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t NB, int64_t n_cb, int64_t part_cap 
     const Plan p256 = plan_k_gemm(M, N, NB, n_cb, MF, part_cap);
     if (!w1_ok) return p256;
     const Plan p512 = plan_w1(M, NB, n_cb, part_cap);
-    const char* e = getenv("SX8_GEMM_TILE");
-    const int forced = e ? atoi(e) : 0;
+    const int forced = tu.tile;
     if (forced == 256) return p256;
     if (forced == 512) return p512;
     return p512.cost < p256.cost ? p512 : p256;
@@ -1414,8 +1447,7 @@ void launch_hb(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, con
                int64_t n_cb, float* part) {
     // 512-row plans run k_gemm_w2 (two waves per SIMD, measured 2-4% faster than k_gemm_w1
     // on the layer's 512-row shapes); SX8_GEMM_W2=0 selects k_gemm_w1 (tuning)
-    const char* e2 = getenv("SX8_GEMM_W2");
-    const bool w2 = !(e2 && atoi(e2) == 0);
+    const bool w2 = tuning().w2;
     if (p.w1 && w2)
         hipLaunchKernelGGL((k_gemm_w2<kSplit, HB, kPca>), dim3((unsigned)p.G), dim3(kW2Threads), 0, st,
                            Xp, (int)M, g, (int)n_cb, p.Tf, p.St, p.kbs, part);
@@ -1576,6 +1608,14 @@ extern "C" int64_t sx8_gemm_prefill_workspace_bytes(int64_t M, int32_t n_mats, c
     if (!group_width(n_mats, Ns, Ntot, NB)) return -1;
     const Plan p = plan_gemm(M, Ntot, NB, n_cb);
     return ws_layout(p, M, Ntot, n_cb, n_mats, true).total;
+}
+
+extern "C" int32_t sx8_gemm_reload_tuning(void) {
+    const Tuning t = read_tuning();
+    std::lock_guard<std::mutex> lk(g_tuning_mu);
+    g_tuning = t;
+    g_tuning_read = true;
+    return SX8_OK;
 }
 
 extern "C" int32_t sx8_gemm_prefill_plan(int64_t M, int32_t n_mats, const int64_t* Ns, int64_t n_cb,

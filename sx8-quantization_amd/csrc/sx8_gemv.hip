@@ -974,7 +974,9 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     // a NaN never wins -- from the CT <= 64 columns of wave 0
     if constexpr (kX == kXRms && kOne) {
         if (xp.amax != nullptr && tid < 64) {
-            const bool mine = tid < CT && col_ok;
+            // a NaN logit never enters the butterfly: its lane starts empty (-inf, INT_MAX)
+            // and takes its partners' values like any other
+            const bool mine = tid < CT && col_ok && !__builtin_isnan(yv);
             float v = mine ? yv : -INFINITY;
             int idx = mine ? n : INT_MAX;
 #pragma unroll
@@ -1524,15 +1526,28 @@ extern "C" int32_t sx8_dec_gemv_silu(const float* g, const float* u, int32_t n_m
                                 as_stream(stream));
 }
 
-// Residual checks of the *_add entry points: adds[i] is either Ys[i] (updated in place) or
-// a separate 16-byte aligned vector of Ns[i] floats.
-static int32_t check_adds(const char* what, int32_t n_mats, const float* const* adds, float* const* Ys) {
+// Residual checks of the *_add entry points: adds[i] is either Ys[i] (updated in place: each
+// element is read and written by the one thread that stores it) or a separate 4-byte
+// aligned vector of Ns[i] floats that overlaps no output.  Any other overlap (a residual
+// partly over its own output, or over another matrix's output) would let one work-group
+// read an element another has already replaced, so it is refused.
+static int32_t check_adds(const char* what, int32_t n_mats, const float* const* adds, float* const* Ys,
+                          const int64_t* Ns) {
     using namespace sx8;
     if (!adds) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
-    for (int i = 0; i < n_mats; ++i)
+    auto overlap = [](const float* a, int64_t na, const float* b, int64_t nb) {
+        return (uintptr_t)a < (uintptr_t)(b + nb) && (uintptr_t)b < (uintptr_t)(a + na);
+    };
+    for (int i = 0; i < n_mats; ++i) {
         if (!adds[i] || !aligned(adds[i], 4))
             return fail(SX8_ERR_INVALID, "%s: bad residual pointer (matrix %d)", what, i);
-    (void)Ys;
+        for (int j = 0; j < n_mats; ++j) {
+            if (j == i && adds[i] == Ys[i]) continue;
+            if (overlap(adds[i], Ns[i], Ys[j], Ns[j]))
+                return fail(SX8_ERR_INVALID, "%s: residual %d overlaps output %d (only adds[i] == Ys[i] may alias)",
+                            what, i, j);
+        }
+    }
     return SX8_OK;
 }
 
@@ -1546,7 +1561,7 @@ extern "C" int32_t sx8_dec_gemv_silu_add(const float* g, const float* u, int32_t
     if (!g || !u) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
     if (!aligned(g, 16) || !aligned(u, 16)) return fail(SX8_ERR_INVALID, "%s: g and u must be 16-byte aligned", what);
     int32_t rc = check_fused_group(what, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys);
-    if (rc == SX8_OK) rc = check_adds(what, n_mats, adds, Ys);
+    if (rc == SX8_OK) rc = check_adds(what, n_mats, adds, Ys, Ns);
     if (rc != SX8_OK) return rc;
     XProd xp{};
     xp.g = g;
@@ -1564,7 +1579,7 @@ extern "C" int32_t sx8_dec_gemv_add(const uint16_t* x, int32_t n_mats, const uin
     if (!x) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
     if (!aligned(x, 16)) return fail(SX8_ERR_INVALID, "%s: x must be 16-byte aligned", what);
     int32_t rc = check_fused_group(what, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys);
-    if (rc == SX8_OK) rc = check_adds(what, n_mats, adds, Ys);
+    if (rc == SX8_OK) rc = check_adds(what, n_mats, adds, Ys, Ns);
     if (rc != SX8_OK) return rc;
     return launch_fused<kXPlain>(what, XProd{}, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb, Ys,
                                  as_stream(stream), x, adds);
@@ -1788,18 +1803,23 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_pair(
 
 extern "C" int32_t sx8_dec_gemv_rmsnorm_pair(const float* resid, const uint16_t* norm_w, float eps,
                                              const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
-                                             const float* bases, const float* scales, int64_t N, int64_t n_cb,
+                                             const float* bases, const float* scales, const uint8_t* up_hdr,
+                                             const uint8_t* up_levels, const float* up_bases,
+                                             const float* up_scales, int64_t N, int64_t n_cb,
                                              const float* down_bases, uint16_t* m, float* zp, void* stream) {
     using namespace sx8;
     const char* what = "sx8_dec_gemv_rmsnorm_pair";
-    if (!resid || !norm_w || !hdr || !levels || !bases || !scales || !down_bases || !m || !zp)
+    if (!resid || !norm_w || !hdr || !levels || !bases || !scales || !up_hdr || !up_levels || !up_bases ||
+        !up_scales || !down_bases || !m || !zp)
         return fail(SX8_ERR_INVALID, "%s: null pointer", what);
     if (hdr_bytes != 6 && hdr_bytes != 8)
         return fail(SX8_ERR_INVALID, "%s: hdr_bytes must be 6 or 8, got %d", what, hdr_bytes);
-    // panels of 32..64 column pairs (a K block of the down projection spans at most two)
-    if (N < 32 || N > 16384 || N % 32)
-        return fail(SX8_ERR_UNSUPPORTED, "%s: N must be a multiple of 32 in 32..16384, got %lld", what,
-                    (long long)N);
+    // panels of 32..64 column pairs (a K block of the down projection spans at most two);
+    // N is the down projection's K, so its limit is sx8_dec_gemv_zp_add's n_cb limit x 32
+    const int64_t n_max = (int64_t)kTabPassesLong * kPanelThreads / 4 * 32;
+    if (N < 32 || N > n_max || N % 32)
+        return fail(SX8_ERR_UNSUPPORTED, "%s: N must be a multiple of 32 in 32..%lld, got %lld", what,
+                    (long long)n_max, (long long)N);
     if (n_cb <= 0 || n_cb * 4 > (int64_t)kTabPassesLong * kPanelThreads)
         return fail(SX8_ERR_UNSUPPORTED, "%s: n_cb %lld outside 1..%d", what, (long long)n_cb,
                     kTabPassesLong * kPanelThreads / 4);
@@ -1808,10 +1828,16 @@ extern "C" int32_t sx8_dec_gemv_rmsnorm_pair(const float* resid, const uint16_t*
         !aligned(m, 2) || !aligned(zp, 4))
         return fail(SX8_ERR_INVALID, "%s: misaligned pointer", what);
     const int64_t n_blk = N * n_cb;
+    // the kernel reads both matrices through the gate's pointers (one buffer resource per
+    // field): the up matrix's arrays must start where the gate's end
+    if (up_hdr != hdr + n_blk * hdr_bytes || up_levels != levels + n_blk * 24 || up_bases != bases + n_cb * 64 ||
+        up_scales != scales + n_cb * 2)
+        return fail(SX8_ERR_INVALID,
+                    "%s: the up matrix's headers, levels, bases and scales must follow the gate matrix's "
+                    "in memory (one allocation per field holding both)", what);
     if ((n_cb + (int64_t)(kRing + 1) * kPanelThreads) * N * 24 * 2 >= ((int64_t)1 << 31))
         return fail(SX8_ERR_UNSUPPORTED, "%s: %lld x %lld blocks exceed 32-bit offsets", what, (long long)N,
                     (long long)n_cb);
-    (void)n_blk;
     const int CTp = std::max((int)((N + 255) / 256), 32);
     const unsigned grid = (unsigned)((N + CTp - 1) / CTp);
     const int TP = n_cb <= 128 * kTabPassesShort ? kTabPassesShort : kTabPassesLong;

@@ -57,8 +57,8 @@ def clone_linear(lin):
 
 def pair_storage(a, b):
     """Move the device tensors of `a` and `b` into one allocation per field, b's right after
-    a's (both keep views of it): sx8_dec_gemv_rmsnorm_pair addresses a matrix pair through
-    the first matrix's pointers."""
+    a's (both keep views of it): sx8_dec_gemv_rmsnorm_pair reads a matrix pair through the
+    first matrix's pointers and refuses a pair stored apart."""
     ta, tb = [], []
     for x, y in zip(a._t44, b._t44):
         buf = torch.cat([x.reshape(-1), y.reshape(-1)])
@@ -360,9 +360,10 @@ class SX8Decoder(nn.Module):
         """r += W_down (silu(W_gate x) * W_up x), x = RMSNorm(r) * post_norm, in two launches."""
         z, P = self._fz, _L.ptr
         gh, gl, gb, gs = ly.gate._t44
+        uh, ul, ub, us = ly.up._t44
         dh, dl, db, ds = ly.down._t44
         _L.call("sx8_dec_gemv_rmsnorm_pair", P(r), P(ly.post_norm), eps, P(gh), P(gl), 6, P(gb), P(gs),
-                ly.gate.out_f, ly.gate.qt["n_cb"], P(db), P(z["m"]), P(z["zp"]), st)
+                P(uh), P(ul), P(ub), P(us), ly.gate.out_f, ly.gate.qt["n_cb"], P(db), P(z["m"]), P(z["zp"]), st)
         _L.call("sx8_dec_gemv_zp_add", P(z["m"]), P(dh), P(dl), 6, P(z["zp"]), P(ds), ly.down.out_f,
                 ly.down.qt["n_cb"], P(r), P(r), st)
 
@@ -413,17 +414,25 @@ class SX8Decoder(nn.Module):
 
     # ---------------------------------------------------------------- generation
     @torch.no_grad()
-    def generate(self, ids, n_new, use_graph=True, fused=True):
+    def generate(self, ids, n_new, use_graph=True, fused=True, return_logits=False):
         """Prefill `ids`, then greedily decode `n_new` tokens.  Returns (tokens (n_new,)
-        on the device, prefill seconds, decode seconds)."""
+        on the device, prefill seconds, decode seconds); with return_logits (fused path
+        only) also the (n_new, vocab) float32 logits each token was picked from: row 0 the
+        prefill's last row, row i the i-th decode step's (copied after each step, outside
+        the timed figures' meaning: the copies add to the decode time)."""
         dev = self.device
         T = ids.shape[0]
         assert T + n_new <= self.max_len
+        if return_logits and not fused:
+            raise ValueError("return_logits needs the fused path")
+        lg = torch.empty(n_new, self.cfg["vocab"], dtype=torch.float32, device=dev) if return_logits else None
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         first = self.prefill_fused(ids) if fused else self.prefill(ids)
         torch.cuda.synchronize()
         t_prefill = time.perf_counter() - t0
+        if lg is not None:
+            lg[0].copy_(self._pb["logits"])
         tok = first.clone()
         pos = torch.full((1,), T, dtype=torch.int64, device=dev)
         out = torch.empty(n_new, dtype=torch.int64, device=dev)
@@ -449,6 +458,8 @@ class SX8Decoder(nn.Module):
             for i in range(1, n_new):
                 g.replay()
                 out[i:i + 1].copy_(tok)
+                if lg is not None:
+                    lg[i].copy_(self._fz["logits"])
             torch.cuda.synchronize()
             t_decode = time.perf_counter() - t1
         else:
@@ -457,6 +468,10 @@ class SX8Decoder(nn.Module):
             for i in range(1, n_new):
                 step(tok, pos)
                 out[i:i + 1].copy_(tok)
+                if lg is not None:
+                    lg[i].copy_(self._fz["logits"])
             torch.cuda.synchronize()
             t_decode = time.perf_counter() - t1
+        if lg is not None:
+            return out, t_prefill, t_decode, lg
         return out, t_prefill, t_decode

@@ -41,3 +41,13 @@ def cuda():
     if not torch.cuda.is_available():
         pytest.skip("no GPU visible")
     return torch.device("cuda:0")
+
+
+@pytest.fixture
+def gemm_tuning(hiplib):
+    """Setter for the prefill tuning variables (TILE=, PLAN=, W2=) during one test; the
+    library reads them once, so the setter and the teardown make it read them again."""
+    import _sx8lib
+    t = _sx8lib.GemmTuning()
+    yield t.set
+    t.restore()

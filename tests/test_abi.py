@@ -142,3 +142,37 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setenv("SX8_HIP_LIB", str(tmp_path / "nope.so"))
     with pytest.raises(RuntimeError, match="not found"):
         _sx8lib.lib()
+
+
+def test_decoder_pair_and_residual_refusals_on_host(hiplib):
+    """sx8_dec_gemv_rmsnorm_pair reads the up matrix at the gate's pointers plus the gate's
+    size: up arrays stored anywhere else are refused before any launch, as is an N the
+    down GEMV (sx8_dec_gemv_zp_add) would refuse; the *_add GEMVs refuse a residual that
+    overlaps an output without being it."""
+    L = hiplib
+    N, n_cb, hb = 9728, 80, 6
+    n_blk = N * n_cb
+    hdr, lvl, bas, sca = 1 << 28, 2 << 28, 3 << 28, 4 << 28
+    up = [hdr + n_blk * hb, lvl + n_blk * 24, bas + n_cb * 64 * 4, sca + n_cb * 2 * 4]
+    p = ctypes.c_void_p(4096)
+    V = ctypes.c_void_p
+
+    def pair(ups, Ncols=N, nc=n_cb):
+        return L.sx8_dec_gemv_rmsnorm_pair(p, p, ctypes.c_float(1e-6), V(hdr), V(lvl), hb, V(bas), V(sca),
+                                           *[V(u) for u in ups], Ncols, nc, p, p, p, NULL)
+
+    for f in range(4):
+        bad = list(up)
+        bad[f] += 256
+        assert pair(bad) == 1, f
+        assert "follow the gate" in _err(L)
+    assert pair(up, 12288 + 32) == 3 and "multiple of 32" in _err(L)
+    assert pair(up, 16384) == 3
+    # residual add: adds[0] 8 floats into Ys[0], and adds[1] == Ys[0] (another matrix's output)
+    P2 = ctypes.c_void_p * 2
+    ns = (ctypes.c_int64 * 2)(1024, 1024)
+    ptrs = P2(1 << 20, 2 << 20)
+    ys = P2(5 << 20, 6 << 20)
+    for adds in (P2((5 << 20) + 32, 7 << 20), P2(7 << 20, 5 << 20)):
+        assert L.sx8_dec_gemv_add(p, 2, ptrs, ptrs, 6, ptrs, ptrs, ns, 80, adds, ys, NULL) == 1
+        assert "overlaps" in _err(L)

@@ -192,7 +192,7 @@ def _group(lins_t, Ns, n_cb, ys):
             (ctypes.c_int64 * n)(*Ns), n_cb, P(*[y.data_ptr() for y in ys]))
 
 
-def _mats(cuda, Ns, K, seed):
+def _mats(cuda, Ns, K, seed, hb=6):
     import torch
     from quantize_sx8 import quantize_tensor
     from sx8_decode1_v3 import make_tensors_v44
@@ -201,18 +201,21 @@ def _mats(cuda, Ns, K, seed):
         g = torch.Generator().manual_seed(seed + i)
         W = (torch.randn(N, K, generator=g) * 0.02).half()
         qt, bi = quantize_tensor(W, device=cuda, degenerate_frac=0.01, seed=seed + 100 + i)
-        out.append(make_tensors_v44(qt, bi))
+        t = make_tensors_v44(qt, bi, hdr_aligned=hb == 8)
+        assert t[0].shape[-1] == hb
+        out.append(t)
     return out
 
 
-def test_fused_gemv_rmsnorm(hiplib, cuda):
+@pytest.mark.parametrize("hb", [6, 8])
+def test_fused_gemv_rmsnorm(hiplib, cuda, hb):
     """sx8_dec_gemv_rmsnorm against sx8_dec_add_rmsnorm + sx8_gemv_group (q/k/v-like group)."""
     import torch
     import _sx8lib as _L
     P = _L.ptr
     st = _L.stream(cuda)
     K, Ns, eps = 2560, [1024, 512, 300], 1e-6
-    ts = _mats(cuda, Ns, K, 40)
+    ts = _mats(cuda, Ns, K, 40, hb)
     g = torch.Generator().manual_seed(7)
     resid = torch.randn(K, generator=g).to(cuda)
     delta = torch.randn(K, generator=g).to(cuda)
@@ -226,13 +229,13 @@ def test_fused_gemv_rmsnorm(hiplib, cuda):
                 P(init) if use_init else None, P(w), P(h16), 1, K, eps, st)
         y_ref = [torch.empty(N, device=cuda) for N in Ns]
         n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y_ref)
-        _L.call("sx8_gemv_group", P(h16), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, None, 0, st)
+        _L.call("sx8_gemv_group", P(h16), n, hd, lv, hb, bs, sc, None, ns, n_cb, ys, None, 0, st)
         # fused
         r_out = torch.full((K,), float("nan"), device=cuda)
         y = [torch.empty(N, device=cuda) for N in Ns]
         n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y)
         _L.call("sx8_dec_gemv_rmsnorm", None if use_init else P(resid), P(init) if use_init else None,
-                None if use_init else P(delta), P(w), eps, P(r_out), n, hd, lv, 6, bs, sc, ns, n_cb, ys, st)
+                None if use_init else P(delta), P(w), eps, P(r_out), n, hd, lv, hb, bs, sc, ns, n_cb, ys, st)
         torch.cuda.synchronize()
         assert torch.equal(r_out.cpu(), r_ref.cpu().view(K))        # h = resid + delta, exact
         for a, b in zip(y, y_ref):
@@ -246,17 +249,17 @@ def test_fused_gemv_rmsnorm(hiplib, cuda):
     _L.call("sx8_dec_add_rmsnorm", P(r_ref), None, None, P(w), P(h16), 1, K, eps, st)
     y_ref = [torch.empty(N, device=cuda) for N in Ns]
     n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y_ref)
-    _L.call("sx8_gemv_group", P(h16), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, None, 0, st)
+    _L.call("sx8_gemv_group", P(h16), n, hd, lv, hb, bs, sc, None, ns, n_cb, ys, None, 0, st)
     y = [torch.empty(N, device=cuda) for N in Ns]
     n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y)
-    _L.call("sx8_dec_gemv_rmsnorm", P(resid), None, None, P(w), eps, None, n, hd, lv, 6, bs, sc, ns, n_cb, ys, st)
+    _L.call("sx8_dec_gemv_rmsnorm", P(resid), None, None, P(w), eps, None, n, hd, lv, hb, bs, sc, ns, n_cb, ys, st)
     torch.cuda.synchronize()
     for a, b in zip(y, y_ref):
         rel = (a - b).abs().max().item() / b.abs().max().item()
         assert rel <= 1e-5, rel
     # resid_out may not alias an input still being read by other work-groups
     with pytest.raises(RuntimeError, match="alias"):
-        _L.call("sx8_dec_gemv_rmsnorm", P(resid), None, P(delta), P(w), eps, P(resid), n, hd, lv, 6, bs,
+        _L.call("sx8_dec_gemv_rmsnorm", P(resid), None, P(delta), P(w), eps, P(resid), n, hd, lv, hb, bs,
                 sc, ns, n_cb, ys, st)
 
 
@@ -287,10 +290,12 @@ def test_fused_gemv_silu(hiplib, cuda):
         _L.call("sx8_dec_gemv_silu", P(a), P(b), n, hd, lv, 6, bs, sc, ns, 385, ys, st)
 
 
-def test_fused_gemv_residual_add(hiplib, cuda):
+@pytest.mark.parametrize("hb", [6, 8])
+def test_fused_gemv_residual_add(hiplib, cuda, hb):
     """sx8_dec_gemv_add and sx8_dec_gemv_silu_add: Ys[i] = adds[i] + W_i x bit for bit against
     sx8_gemv_group (resp. sx8_dec_silu_mul + sx8_gemv_group) plus a float32 add, both with a
-    separate residual and with the residual updated in place (adds[i] = Ys[i])."""
+    separate residual and with the residual updated in place (adds[i] = Ys[i]), with 6- and
+    8-byte headers; a residual that partly overlaps an output is refused."""
     import torch
     import _sx8lib as _L
     P = _L.ptr
@@ -298,21 +303,21 @@ def test_fused_gemv_residual_add(hiplib, cuda):
     g = torch.Generator().manual_seed(12)
     # o-like group of one matrix and a q/k/v-like group of three, plain x
     for K, Ns in ((4096, [2560]), (2560, [4096, 1024, 1024])):
-        ts = _mats(cuda, Ns, K, 70 + len(Ns))
+        ts = _mats(cuda, Ns, K, 70 + len(Ns), hb)
         x = torch.randn(K, generator=g).half().to(cuda)
         res = [torch.randn(N, generator=g).to(cuda) for N in Ns]
         y_ref = [torch.empty(N, device=cuda) for N in Ns]
         n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y_ref)
-        _L.call("sx8_gemv_group", P(x), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, None, 0, st)
+        _L.call("sx8_gemv_group", P(x), n, hd, lv, hb, bs, sc, None, ns, n_cb, ys, None, 0, st)
         exp = [yr + r for yr, r in zip(y_ref, res)]
         y = [torch.empty(N, device=cuda) for N in Ns]
         n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y)
         adds = (ctypes.c_void_p * n)(*[r.data_ptr() for r in res])
-        _L.call("sx8_dec_gemv_add", P(x), n, hd, lv, 6, bs, sc, ns, n_cb, adds, ys, st)
+        _L.call("sx8_dec_gemv_add", P(x), n, hd, lv, hb, bs, sc, ns, n_cb, adds, ys, st)
         inplace = [r.clone() for r in res]
         n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, inplace)
         adds2 = (ctypes.c_void_p * n)(*[r.data_ptr() for r in inplace])
-        _L.call("sx8_dec_gemv_add", P(x), n, hd, lv, 6, bs, sc, ns, n_cb, adds2, ys, st)
+        _L.call("sx8_dec_gemv_add", P(x), n, hd, lv, hb, bs, sc, ns, n_cb, adds2, ys, st)
         torch.cuda.synchronize()
         for i in range(n):
             assert torch.equal(y[i].cpu(), exp[i].cpu()), (K, i)
@@ -320,42 +325,57 @@ def test_fused_gemv_residual_add(hiplib, cuda):
     # down-like: x = silu(g) * u, residual updated in place; g and u adjacent (u = g + K:
     # both from one preloaded argument), then apart
     K, Ns = 9728, [2560]
-    ts = _mats(cuda, Ns, K, 61)
+    ts = _mats(cuda, Ns, K, 61, hb)
     ab = torch.randn(2, K, generator=g).to(cuda)
     a, b = ab[0], ab[1]
     m = torch.empty(K, dtype=torch.float16, device=cuda)
     _L.call("sx8_dec_silu_mul", P(a), P(b), P(m), K, st)
     y_ref = [torch.empty(N, device=cuda) for N in Ns]
     n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, y_ref)
-    _L.call("sx8_gemv_group", P(m), n, hd, lv, 6, bs, sc, None, ns, n_cb, ys, None, 0, st)
+    _L.call("sx8_gemv_group", P(m), n, hd, lv, hb, bs, sc, None, ns, n_cb, ys, None, 0, st)
     res = torch.randn(Ns[0], generator=g).to(cuda)
     exp = y_ref[0] + res
     res0 = res.clone()
     n, hd, lv, bs, sc, ns, n_cb, ys = _group(ts, Ns, K // 32, [res])
     adds = (ctypes.c_void_p * 1)(res.data_ptr())
-    _L.call("sx8_dec_gemv_silu_add", P(a), P(b), n, hd, lv, 6, bs, sc, ns, n_cb, adds, ys, st)
+    _L.call("sx8_dec_gemv_silu_add", P(a), P(b), n, hd, lv, hb, bs, sc, ns, n_cb, adds, ys, st)
     b2 = b.clone()                                          # u no longer at g + K
     res2 = res0.clone()
     n, hd, lv, bs, sc, ns, n_cb, ys2 = _group(ts, Ns, K // 32, [res2])
     adds2 = (ctypes.c_void_p * 1)(res2.data_ptr())
-    _L.call("sx8_dec_gemv_silu_add", P(a), P(b2), n, hd, lv, 6, bs, sc, ns, n_cb, adds2, ys2, st)
+    _L.call("sx8_dec_gemv_silu_add", P(a), P(b2), n, hd, lv, hb, bs, sc, ns, n_cb, adds2, ys2, st)
+    # u = g + K (one preloaded argument for both) with a separate residual: Ys = adds + W x
+    res3 = res0.clone()
+    out3 = torch.full((Ns[0],), float("nan"), device=cuda)
+    n, hd, lv, bs, sc, ns, n_cb, ys3 = _group(ts, Ns, K // 32, [out3])
+    adds3 = (ctypes.c_void_p * 1)(res3.data_ptr())
+    _L.call("sx8_dec_gemv_silu_add", P(a), P(b), n, hd, lv, hb, bs, sc, ns, n_cb, adds3, ys3, st)
     torch.cuda.synchronize()
     assert torch.equal(res.cpu(), exp.cpu())
     assert torch.equal(res2.cpu(), exp.cpu())
+    assert torch.equal(out3.cpu(), exp.cpu())
+    assert torch.equal(res3.cpu(), res0.cpu())              # the separate residual is only read
+    # a residual that overlaps its output without being it: refused before any launch
+    big = torch.zeros(Ns[0] + 8, device=cuda)
+    n, hd, lv, bs, sc, ns, n_cb, ysb = _group(ts, Ns, K // 32, [big[8:]])
+    with pytest.raises(RuntimeError, match="overlaps"):
+        _L.call("sx8_dec_gemv_silu_add", P(a), P(b), n, hd, lv, hb, bs, sc, ns, n_cb,
+                (ctypes.c_void_p * 1)(big.data_ptr()), ysb, st)
     with pytest.raises(RuntimeError, match="residual"):
         bad = (ctypes.c_void_p * 1)(None)
-        _L.call("sx8_dec_gemv_silu_add", P(a), P(b), n, hd, lv, 6, bs, sc, ns, n_cb, bad, ys, st)
+        _L.call("sx8_dec_gemv_silu_add", P(a), P(b), n, hd, lv, hb, bs, sc, ns, n_cb, bad, ys, st)
 
 
-@pytest.mark.parametrize("M,K,N", [(512, 9728, 2560), (77, 9728, 300), (40, 1000, 130)])
-def test_gemm_silu_matches_two_calls(hiplib, cuda, M, K, N):
+@pytest.mark.parametrize("M,K,N,hb", [(512, 9728, 2560, 6), (512, 9728, 2560, 8), (77, 9728, 300, 6),
+                                      (40, 1000, 130, 8)])
+def test_gemm_silu_matches_two_calls(hiplib, cuda, M, K, N, hb):
     """sx8_dec_gemm_silu equals sx8_dec_silu_mul + sx8_gemm_prefill bit for bit (the pack
     pass forms the same fp16 x); K = 1000 takes the unaligned, ragged-tail loads."""
     import torch
     import _sx8lib as _L
     P = _L.ptr
     st = _L.stream(cuda)
-    (hdr, lvl, bas, sca), = _mats(cuda, [N], K, 70 + M)
+    (hdr, lvl, bas, sca), = _mats(cuda, [N], K, 70 + M, hb)
     n_cb = (K + 31) // 32
     g = torch.Generator().manual_seed(M + K)
     a = (torch.randn(M, K, generator=g) * 3).to(cuda)
@@ -364,11 +384,11 @@ def test_gemm_silu_matches_two_calls(hiplib, cuda, M, K, N):
     _L.call("sx8_dec_silu_mul", P(a), P(b), P(m), M * K, st)
     y_ref = torch.empty(M, N, device=cuda)
     ws, nb = _L.gemm_workspace(M, (N,), n_cb, cuda)
-    _L.call("sx8_gemm_prefill", P(m), M, K, K, P(hdr), P(lvl), 6, P(bas), P(sca), N, n_cb, P(y_ref), P(ws), nb,
+    _L.call("sx8_gemm_prefill", P(m), M, K, K, P(hdr), P(lvl), hb, P(bas), P(sca), N, n_cb, P(y_ref), P(ws), nb,
             st)
     y = torch.empty(M, N, device=cuda)
-    print("gemm_silu", M, K, N, flush=True)
-    _L.call("sx8_dec_gemm_silu", P(a), P(b), M, K, P(hdr), P(lvl), 6, P(bas), P(sca), N, n_cb, P(y), P(ws), nb,
+    print("gemm_silu", M, K, N, hb, flush=True)
+    _L.call("sx8_dec_gemm_silu", P(a), P(b), M, K, P(hdr), P(lvl), hb, P(bas), P(sca), N, n_cb, P(y), P(ws), nb,
             st)
     torch.cuda.synchronize()
     assert torch.equal(y.cpu(), y_ref.cpu())
@@ -528,36 +548,38 @@ def test_qk_rope_cache_rows(hiplib, cuda, nh, nk, hd, L, rows, pos0):
     assert close(kc, ref_k.float()), (kc.float() - ref_k.float()).abs().max().item()
 
 
-@pytest.mark.parametrize("H,I", [(2560, 9728), (1024, 8224), (512, 1056)])
-def test_gemv_pair_and_zp_down(hiplib, cuda, H, I):
+@pytest.mark.parametrize("H,I,hb", [(2560, 9728, 6), (2560, 9728, 8), (1024, 8224, 6), (512, 1056, 8)])
+def test_gemv_pair_and_zp_down(hiplib, cuda, H, I, hb):
     """sx8_dec_gemv_rmsnorm_pair + sx8_dec_gemv_zp_add against the three-launch MLP
     (sx8_dec_gemv_rmsnorm over gate and up as a group, sx8_dec_silu_mul, sx8_dec_gemv_add):
     m within one fp16 step (g and u are summed in another order), the partial sums' Z
     against sx8_compute_z on the same m, and the down GEMV from the partial sums against
     sx8_dec_gemv_add on the same m.  I = 8224 leaves the last panel partly empty; I = 1056
-    runs at the 32-pair minimum panel width."""
+    runs at the 32-pair minimum panel width.  A pair stored apart, or an N the down GEMV
+    would refuse, is refused."""
     import torch
     import _sx8lib as _L
     P = _L.ptr
     st = _L.stream(cuda)
     eps = 1e-6
-    gu = _mats(cuda, [I, I], H, 80 + H)
-    (dh, dl, db, ds), = _mats(cuda, [H], I, 90 + H)
+    gu = _mats(cuda, [I, I], H, 80 + H, hb)
+    (dh, dl, db, ds), = _mats(cuda, [H], I, 90 + H, hb)
     # the up matrix's arrays right behind the gate matrix's
     cat = [torch.cat([gu[0][f].reshape(-1), gu[1][f].reshape(-1)]) for f in range(4)]
+    up = [c[gu[0][f].numel():] for f, c in enumerate(cat)]
     g = torch.Generator().manual_seed(H)
     resid = torch.randn(H, generator=g).to(cuda)
     w = (torch.rand(H, generator=g) + 0.5).half().to(cuda)
     y_gu = torch.empty(2, I, device=cuda)
     n, hd, lv, bs, sc, ns, n_cb, ys = _group(gu, [I, I], H // 32, [y_gu[0], y_gu[1]])
-    _L.call("sx8_dec_gemv_rmsnorm", P(resid), None, None, P(w), eps, None, n, hd, lv, 6, bs, sc, ns, n_cb,
+    _L.call("sx8_dec_gemv_rmsnorm", P(resid), None, None, P(w), eps, None, n, hd, lv, hb, bs, sc, ns, n_cb,
             ys, st)
     m_ref = torch.empty(I, dtype=torch.float16, device=cuda)
     _L.call("sx8_dec_silu_mul", P(y_gu[0]), P(y_gu[1]), P(m_ref), I, st)
     m = torch.full((I,), float("nan"), dtype=torch.float16, device=cuda)
     zp = torch.full((I // 32, 2, 2), float("nan"), device=cuda)
-    _L.call("sx8_dec_gemv_rmsnorm_pair", P(resid), P(w), eps, P(cat[0]), P(cat[1]), 6, P(cat[2]), P(cat[3]),
-            I, H // 32, P(db), P(m), P(zp), st)
+    _L.call("sx8_dec_gemv_rmsnorm_pair", P(resid), P(w), eps, P(cat[0]), P(cat[1]), hb, P(cat[2]), P(cat[3]),
+            *[P(u) for u in up], I, H // 32, P(db), P(m), P(zp), st)
     torch.cuda.synchronize()
     mf, mr = m.cpu().float(), m_ref.cpu().float()
     assert torch.isfinite(mf).all()
@@ -579,18 +601,30 @@ def test_gemv_pair_and_zp_down(hiplib, cuda, H, I):
     y_ref = res.clone()
     n, hd, lv, bs, sc, ns, n_cb, ys = _group([(dh, dl, db, ds)], [H], I // 32, [y_ref])
     adds = (ctypes.c_void_p * 1)(y_ref.data_ptr())
-    _L.call("sx8_dec_gemv_add", P(m), n, hd, lv, 6, bs, sc, ns, n_cb, adds, ys, st)
+    _L.call("sx8_dec_gemv_add", P(m), n, hd, lv, hb, bs, sc, ns, n_cb, adds, ys, st)
     y = torch.full((H,), float("nan"), device=cuda)
-    _L.call("sx8_dec_gemv_zp_add", P(m), P(dh), P(dl), 6, P(zp), P(ds), H, I // 32, P(res), P(y), st)
+    _L.call("sx8_dec_gemv_zp_add", P(m), P(dh), P(dl), hb, P(zp), P(ds), H, I // 32, P(res), P(y), st)
     y_in = res.clone()
-    _L.call("sx8_dec_gemv_zp_add", P(m), P(dh), P(dl), 6, P(zp), P(ds), H, I // 32, P(y_in), P(y_in), st)
+    _L.call("sx8_dec_gemv_zp_add", P(m), P(dh), P(dl), hb, P(zp), P(ds), H, I // 32, P(y_in), P(y_in), st)
     torch.cuda.synchronize()
     scale = (y_ref - res).abs().max().item()
     for out in (y, y_in):
         assert (out - y_ref).abs().max().item() <= 1e-5 * scale
+    def pair(ptrs, Ncols):
+        _L.call("sx8_dec_gemv_rmsnorm_pair", P(resid), P(w), eps, P(ptrs[0]), P(ptrs[1]), hb, P(ptrs[2]),
+                P(ptrs[3]), *[P(u) for u in ptrs[4:]], Ncols, H // 32, P(db), P(m), P(zp), st)
+
     with pytest.raises(RuntimeError, match="multiple of 32"):
-        _L.call("sx8_dec_gemv_rmsnorm_pair", P(resid), P(w), eps, P(cat[0]), P(cat[1]), 6, P(cat[2]),
-                P(cat[3]), I - 16, H // 32, P(db), P(m), P(zp), st)
+        pair(cat + up, I - 16)
+    # the up matrix in its own allocations (as to_v44_device makes them): refused on the host
+    for f in range(4):
+        apart = list(cat) + list(up)
+        apart[4 + f] = gu[1][f]
+        with pytest.raises(RuntimeError, match="follow the gate"):
+            pair(apart, I)
+    # N past what sx8_dec_gemv_zp_add accepts (n_cb <= 384, N <= 12288)
+    with pytest.raises(RuntimeError, match="multiple of 32"):
+        pair(cat + up, 12288 + 32)
 
 
 @pytest.mark.parametrize("K,N,hb", [
@@ -644,3 +678,46 @@ def test_head_argmax_partials(hiplib, cuda, K, N, hb):
     with pytest.raises(RuntimeError, match="parts"):
         _L.call("sx8_dec_gemv_rmsnorm_argmax", P(rd), P(w), eps, P(hdr), P(lvl), hb, P(bas), P(sca), N, K // 32,
                 P(logits), P(parts), nb - 8, P(tok), P(pos), st)
+
+
+def test_head_argmax_partials_nan_logit(hiplib, cuda):
+    """A NaN logit in a panel never hides the panel's other columns from the argmax: column
+    16's first header decodes a NaN range (dmin = fp16 NaN), column 48 -- in the same
+    64-column panel, its partner across the 32-lane step of the panel's butterfly -- holds
+    the largest logit.  sx8_dec_gemv_rmsnorm_argmax must pick 48, as sx8_dec_argmax_advance
+    does on the same logits."""
+    import torch
+    import _sx8lib as _L
+    from quantize_sx8 import quantize_tensor
+    from sx8_decode1_v3 import make_tensors_v44
+    P = _L.ptr
+    st = _L.stream(cuda)
+    K, N, eps = 2560, 16384, 1e-6           # 16384 columns: 64-column panels (256 of them)
+    g = torch.Generator().manual_seed(41)
+    resid = torch.randn(K, generator=g)
+    W = torch.randn(N, K, generator=g) * 0.02
+    W[48] = torch.sign(resid) * 0.05
+    qt, bi = quantize_tensor(W.half(), device=cuda, degenerate_frac=0.0, seed=42)
+    hdr, lvl, bas, sca = make_tensors_v44(qt, bi)
+    hdr.view(-1, 6)[16, 0:2] = torch.tensor([0x00, 0x7E], dtype=torch.uint8, device=cuda)  # kb 0, n 16
+    w = (torch.rand(K, generator=g) + 0.5).half().to(cuda)
+    rd = resid.to(cuda)
+    ref = torch.empty(N, device=cuda)
+    n, hd, lv, bs, sc, ns, n_cb, ys = _group([(hdr, lvl, bas, sca)], [N], K // 32, [ref])
+    _L.call("sx8_dec_gemv_rmsnorm", P(rd), None, None, P(w), eps, None, n, hd, lv, 6, bs, sc, ns, n_cb, ys, st)
+    tok_ref = torch.zeros(1, dtype=torch.int64, device=cuda)
+    pos_ref = torch.zeros(1, dtype=torch.int64, device=cuda)
+    _L.call("sx8_dec_argmax_advance", P(ref), N, P(tok_ref), P(pos_ref), st)
+    nb = int(_L.lib().sx8_dec_argmax_parts_bytes(N, K // 32))
+    parts = torch.empty(nb // 4, dtype=torch.int32, device=cuda)
+    logits = torch.empty(N, device=cuda)
+    tok = torch.full((1,), -1, dtype=torch.int64, device=cuda)
+    pos = torch.zeros(1, dtype=torch.int64, device=cuda)
+    _L.call("sx8_dec_gemv_rmsnorm_argmax", P(rd), P(w), eps, P(hdr), P(lvl), 6, P(bas), P(sca), N, K // 32,
+            P(logits), P(parts), nb, P(tok), P(pos), st)
+    torch.cuda.synchronize()
+    lr = ref.cpu()
+    assert torch.isnan(lr[16]) and torch.isnan(lr).sum().item() == 1
+    assert torch.equal(logits.cpu().view(torch.int32), lr.view(torch.int32))
+    assert tok_ref.item() == 48
+    assert tok.item() == 48 and pos.item() == 1

@@ -323,13 +323,12 @@ PREFILL_CASES = [
 
 
 @pytest.mark.parametrize("name,N,K,M,tile", PREFILL_CASES)
-def test_prefill_gemm(hiplib, oracle, cuda, monkeypatch, name, N, K, M, tile):
+def test_prefill_gemm(hiplib, oracle, cuda, gemm_tuning, name, N, K, M, tile):
     import torch
     if tile == "512w1":
-        monkeypatch.setenv("SX8_GEMM_TILE", "512")
-        monkeypatch.setenv("SX8_GEMM_W2", "0")
+        gemm_tuning(TILE="512", W2="0")
     elif tile != "auto":
-        monkeypatch.setenv("SX8_GEMM_TILE", tile)
+        gemm_tuning(TILE=tile)
     from sx8_decode1_v3 import make_tensors_v44
     from sx8_gemm_compact import _ext, gemm_sx8_compact
     from sx8_fused_wmma import gemm_sx8_wmma_cached, make_tensors, to_kbmajor
@@ -453,7 +452,7 @@ def test_clone_model_replaces_linears(hiplib, cuda):
     ("gate_up_m700_w1", [1000, 1300], 2560, 700, "512"),
     ("ragged_four", [300, 64, 129, 700], 80, 33, "auto"),
 ])
-def test_prefill_gemm_group(hiplib, oracle, cuda, monkeypatch, name, Ns, K, M, tile):
+def test_prefill_gemm_group(hiplib, oracle, cuda, gemm_tuning, name, Ns, K, M, tile):
     """sx8_gemm_prefill_group against the oracle (1e-3) and against one sx8_gemm_prefill per
     matrix (the same kernel arithmetic; only the split-K summation order can differ)."""
     import ctypes
@@ -461,10 +460,9 @@ def test_prefill_gemm_group(hiplib, oracle, cuda, monkeypatch, name, Ns, K, M, t
     import _sx8lib as L
     from sx8_decode1_v3 import make_tensors_v44
     if tile == "512w1":
-        monkeypatch.setenv("SX8_GEMM_TILE", "512")
-        monkeypatch.setenv("SX8_GEMM_W2", "0")
+        gemm_tuning(TILE="512", W2="0")
     elif tile != "auto":
-        monkeypatch.setenv("SX8_GEMM_TILE", tile)
+        gemm_tuning(TILE=tile)
     _say("prefill group", name, Ns, K, M)
     mats = [_quantized(N, K, 500 + i, cuda) for i, N in enumerate(Ns)]
     ts = [make_tensors_v44(qt, bi) for qt, bi in mats]

@@ -193,3 +193,171 @@ def test_prefill_wrapper_graph_capture(hiplib, oracle, cuda):
         torch.cuda.synchronize()
         assert torch.equal(Yg, eager), i
         assert not torch.equal(other, eager)
+
+
+# ------------------------------------------------------------ 8-byte headers
+# The reference's compact GEMM is instantiated for 6- and 8-byte headers
+# (cuda/sx8_gemm_compact.cu:55, HDR template; scripts/sx8_decode1_v3.py:57-66 builds the
+# 8-byte form with hdr_aligned=True: two pad bytes after coeff).  The header width changes
+# only the record stride, so every 8-byte call must give the 6-byte call's output bit for
+# bit, besides meeting the float64 yardstick.
+
+_T8 = {}
+
+
+def _t8(name, cuda, oracle):
+    """The v4.4 tensors of a layer shape with 8-byte headers."""
+    if name not in _T8:
+        from prepare_v44 import to_v44_device
+        qt, bi, t6, _ = _weight(name, cuda, oracle)
+        t8 = to_v44_device(qt, bi, hdr_aligned=True, device=cuda)
+        h6 = t6[0].reshape(-1, 6)
+        h8 = t8[0].reshape(-1, 8)
+        assert h8.shape[0] == h6.shape[0]
+        assert np.array_equal(h8[:, :6].cpu().numpy(), h6.cpu().numpy())
+        assert int(h8[:, 6:].abs().sum()) == 0
+        assert np.array_equal(t8[1].cpu().numpy(), t6[1].cpu().numpy())
+        _T8[name] = t8
+    return _T8[name]
+
+
+@pytest.mark.parametrize("name,M", [("gate_proj", 2048), ("down_proj", 2048), ("o_proj", 512),
+                                    ("k_proj", 128)])
+def test_prefill_hdr8_layer_shapes(hiplib, oracle, cuda, name, M):
+    """gemm_sx8_compact(..., hdr_bytes=8) through the plan the library picks: within 1e-3
+    of the float64 yardstick and bit-identical to the 6-byte-header call."""
+    from sx8_gemm_compact import gemm_sx8_compact
+    import _sx8lib as L
+    qt, bi, t6, W16 = _weight(name, cuda, oracle)
+    t8 = _t8(name, cuda, oracle)
+    N, K = SHAPE[name]
+    _say("prefill hdr8", name, N, K, "M", M, "plan", L.gemm_plan(M, (N,), qt["n_cb"]))
+    X = _x(M, K, 21 + M, cuda)
+    Y8 = gemm_sx8_compact(X, qt, bi, *t8, hdr_bytes=8)
+    rel = _rel(Y8, _ref64(X, W16))
+    _say("   rel", rel)
+    assert rel <= TOL
+    Y6 = gemm_sx8_compact(X, qt, bi, *t6, hdr_bytes=6)
+    assert Y8.equal(Y6)
+
+
+def test_prefill_hdr8_ragged(hiplib, oracle, cuda):
+    """8-byte headers on a ragged shape: N not a multiple of the column tile, K not a
+    multiple of 32 (last K block partly past the end), M not a multiple of 32."""
+    import torch
+    from kernel_sx8_v43 import decode_tensor_gpu_fast
+    from prepare_v44 import to_v44_device
+    from quantize_sx8 import quantize_tensor
+    from sx8_gemm_compact import gemm_sx8_compact
+    N, K, M = 1000, 2600, 300
+    g = torch.Generator(device="cpu").manual_seed(77)
+    W = (torch.randn(N, K, generator=g) * 0.02).half()
+    qt, bi = quantize_tensor(W, device=cuda, degenerate_frac=0.02, seed=78)
+    W16 = decode_tensor_gpu_fast(qt, bi).to(cuda)
+    assert np.array_equal(W16.cpu().numpy().view(np.uint16), oracle.dequant_r64(qt, bi).view(np.uint16))
+    X = _x(M, K, 79, cuda)
+    t8 = to_v44_device(qt, bi, hdr_aligned=True, device=cuda)
+    t6 = to_v44_device(qt, bi, hdr_aligned=False, device=cuda)
+    Y8 = gemm_sx8_compact(X, qt, bi, *t8, hdr_bytes=8)
+    rel = _rel(Y8, _ref64(X, W16))
+    _say("prefill hdr8 ragged", N, K, M, "rel", rel)
+    assert rel <= TOL
+    assert Y8.equal(gemm_sx8_compact(X, qt, bi, *t6, hdr_bytes=6))
+
+
+@pytest.mark.parametrize("group", [("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj")])
+def test_prefill_hdr8_group_m2048(hiplib, oracle, cuda, group):
+    """sx8_gemm_prefill_group with 8-byte headers at M = 2048: every output within the bar
+    of the float64 yardstick and bit-identical to the 6-byte-header group call."""
+    import torch
+    import _sx8lib as L
+    M = 2048
+    mats = [_weight(n, cuda, oracle) for n in group]
+    t8s = [_t8(n, cuda, oracle) for n in group]
+    Ns = [SHAPE[n][0] for n in group]
+    K = SHAPE[group[0]][1]
+    n_cb = mats[0][0]["n_cb"]
+    _say("prefill hdr8 group", group, "M", M, "plan", L.gemm_plan(M, Ns, n_cb))
+    X = _x(M, K, 25, cuda)
+    n = len(group)
+    Pa = ctypes.c_void_p * n
+
+    def run(ts, hb):
+        ys = [torch.empty(M, N, device=cuda) for N in Ns]
+        ws, nb = L.gemm_workspace(M, Ns, n_cb, cuda)
+        L.call("sx8_gemm_prefill_group", L.ptr(X), M, K, K, n, Pa(*[t[0].data_ptr() for t in ts]),
+               Pa(*[t[1].data_ptr() for t in ts]), hb, Pa(*[t[2].data_ptr() for t in ts]),
+               Pa(*[t[3].data_ptr() for t in ts]), (ctypes.c_int64 * n)(*Ns), n_cb,
+               Pa(*[y.data_ptr() for y in ys]), L.ptr(ws), nb, L.stream(cuda))
+        return ys
+
+    y8 = run(t8s, 8)
+    y6 = run([m[2] for m in mats], 6)
+    for name, m, a, b in zip(group, mats, y8, y6):
+        rel = _rel(a, _ref64(X, m[3]))
+        _say("   ", name, "rel", rel)
+        assert rel <= TOL
+        assert a.equal(b), name
+
+
+def test_prefill_hdr8_z_core_and_pca_z(hiplib, oracle, cuda):
+    """The 8-byte-header forms of the caller-supplied-Z contract (gemm_compact ->
+    sx8_gemm_prefill_z) and of the two-pass form (sx8_gemm_prefill_core + sx8_gemm_pca_z):
+    each equal to its 6-byte-header call bit for bit and within the float64 yardstick."""
+    import torch
+    import _sx8lib as L
+    from sx8_gemm_compact import _ext
+    name, M = "q_proj", 512
+    qt, bi, t6, W16 = _weight(name, cuda, oracle)
+    t8 = _t8(name, cuda, oracle)
+    N, K = SHAPE[name]
+    n_cb = qt["n_cb"]
+    X = _x(M, K, 27, cuda)
+    Yref = _ref64(X, W16)
+    ext = _ext()
+    Z = ext.compute_z44_batch(X, t6[2], t6[3], n_cb)
+    Yz8 = ext.gemm_compact(X, t8[0], t8[1], Z, n_cb, 8)
+    Yz6 = ext.gemm_compact(X, t6[0], t6[1], Z, n_cb, 6)
+    assert _rel(Yz8, Yref) <= TOL
+    assert Yz8.equal(Yz6)
+
+    def two_pass(t, hb):
+        Yc = torch.empty(M, N, device=cuda)
+        ws, nb = L.gemm_workspace(M, (N,), n_cb, cuda)
+        L.call("sx8_gemm_prefill_core", L.ptr(X), M, K, K, L.ptr(t[0]), L.ptr(t[1]), hb, N, n_cb,
+               L.ptr(Yc), L.ptr(ws), nb, L.stream(cuda))
+        core = Yc.clone()
+        L.call("sx8_gemm_pca_z", L.ptr(Z), M, L.ptr(t[0]), hb, N, n_cb, L.ptr(Yc), L.stream(cuda))
+        return core, Yc
+
+    c8, y8 = two_pass(t8, 8)
+    c6, y6 = two_pass(t6, 6)
+    assert c8.equal(c6) and y8.equal(y6)
+    rel = _rel(y8, Yref)
+    _say("prefill hdr8 two-pass rel", rel)
+    assert rel <= TOL
+    # the PCA pass added something: the core alone misses the PCA term
+    assert not c8.equal(y8)
+
+
+def test_prefill_hdr8_mfma_operand_bit_exact(hiplib, oracle, cuda):
+    """The fp16 MFMA operand decoded from 8-byte headers, read back through the core-only
+    GEMM with X = the identity, against the oracle's core_f16 bit for bit (fuzz blocks:
+    every strategy and level, degenerate, reversed and subnormal ranges)."""
+    import torch
+    import _sx8lib as L
+    from prepare_v44 import to_v44_device
+    qt = _operand_case("fuzz", cuda, oracle)
+    N, K = qt["shape"]
+    n_cb = qt["n_cb"]
+    zero = {"n_cb": n_cb, "data": np.zeros((n_cb, 64), np.float32), "scales": np.zeros((n_cb, 2), np.float32)}
+    hdr, lvl, _, _ = to_v44_device(qt, zero, hdr_aligned=True, device=cuda)
+    X = torch.eye(K, dtype=torch.float16, device=cuda)
+    Y = torch.empty(K, N, dtype=torch.float32, device=cuda)
+    ws, nb = L.gemm_workspace(K, (N,), n_cb, cuda)
+    L.call("sx8_gemm_prefill_core", L.ptr(X), K, K, K, L.ptr(hdr), L.ptr(lvl), 8, N, n_cb, L.ptr(Y),
+           L.ptr(ws), nb, L.stream(cuda))
+    got = Y.T.contiguous().cpu().numpy()
+    exp = oracle.core_f16(qt).astype(np.float32)
+    exp[exp == 0] = 0.0
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))

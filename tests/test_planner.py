@@ -80,20 +80,20 @@ def test_plan_invariants_ragged(hiplib, n_cb):
 
 @pytest.mark.parametrize("force,tile,S", [("k1:3", 128, 3), ("k2:5", 256, 5), ("w0:2", 512, 2),
                                           ("w1:4", 512, 4)])
-def test_forced_plan(hiplib, monkeypatch, force, tile, S):
+def test_forced_plan(hiplib, gemm_tuning, force, tile, S):
     """SX8_GEMM_PLAN selects one plan (the tuning knob the parity tests use to reach every
     kernel form); w1 runs whole rounds of tiles first."""
-    monkeypatch.setenv("SX8_GEMM_PLAN", force)
+    gemm_tuning(PLAN=force)
     p = _check(2048, (9728, 9728), 80, forced=True)
     assert (p["tile"], p["k_ranges"]) == (tile, S), p
     T = 4 * 152
     assert p["whole_tiles"] == (T // 256 * 256 if force.startswith("w1") else 0), p
 
 
-def test_forced_plan_out_of_range_falls_back(hiplib, monkeypatch):
+def test_forced_plan_out_of_range_falls_back(hiplib, gemm_tuning):
     base = _plan(512, (2560,), 80)
     for bad in ("k2:9", "k3:2", "w2:1", "x1:1", "w0:0", "k1"):
-        monkeypatch.setenv("SX8_GEMM_PLAN", bad)
+        gemm_tuning(PLAN=bad)
         assert _plan(512, (2560,), 80) == base, bad
 
 
