@@ -20,8 +20,10 @@ the per-launch kernel duration used for the roofline.
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
@@ -35,11 +37,56 @@ LAYER = [  # (name, N, K)
     ("down_proj", 2560, 9728),
 ]
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
-# HBM bytes per k_gemv_panel launch on this workload (hdr_bytes=6), measured with two
-# rocprofv3 passes (FETCH_SIZE, WRITE_SIZE) scaled by what the counters read for a 512 MiB
-# copy (fetch x2.000, write x1.000); passes and calibration: profiles/gemv_decode_layer.md
-GEMV_TRAFFIC_PER_LAUNCH = 13.98e6
+# Counter figures measured with rocprofv3 on the GPU box (profiles/gemv_decode_layer.md,
+# profiles/prefill_gemm_m2048.md).  Each holds for the kernel source it was measured on
+# (sha256 prefix of the files listed in SRC_FILES for that kernel); with any other source
+# the bench line reports null for it instead of a stale figure.
+# HBM bytes per launch = FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 (KiB per dispatch, scaled by
+# what the two counters read for a 512 MiB device copy, bench.py --only copy).
+SRC_FILES = {"gemv": ("sx8_gemv.hip", "sx8_device.h", "sx8_buffer.h"),
+             "gemm": ("sx8_gemm.hip", "sx8_gemv.hip", "sx8_device.h", "sx8_buffer.h")}
+MEASURED = {
+    # k_gemv_panel over the layer sweep: mean 6812.6 KiB fetched, 17.1 KiB written per launch
+    "gemv_traffic": {"value": (6812.6 * 2.0 + 17.1) * 1024, "src": "gemv", "src_sha16": "41e63bced56438b7",
+                     "how": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, bench.py --only gemv --steps 10 "
+                            "--warmup 2, first 12 x 7 single-matrix dispatches"},
+    # rocprofv3 kernel-trace mean over the 140 timed k_gemv_panel dispatches (20 steps x 7);
+    # bench.py's own figure in that traced run: 6.215 us per launch (timed region / launches)
+    "gemv_traced_launch_us": {"value": 6.187, "src": "gemv", "src_sha16": "41e63bced56438b7",
+                              "how": "rocprofv3 --kernel-trace --stats, bench.py --only gemv --steps 20 "
+                                     "(same-run event figure under the tracer: 6.215 us)"},
+    # k_gemm_w2 on down_proj at M = 2048 (plan 80 tiles x 3 K ranges): 89774.3 KiB fetched,
+    # 61751.1 KiB written per dispatch (Y 21 MB + two partial tiles per split tile 42 MB)
+    "prefill_traffic": {"value": (89774.3 * 2.0 + 61751.1) * 1024, "src": "gemm", "src_sha16": "86fe77f14a62352c",
+                        "how": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, bench.py --only gemm-one "
+                               "--shape down_proj --m 2048 --iters 20, mean of 21 dispatches"},
+    # 100 x sum SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs)
+    "prefill_mfma_busy_pct": {"value": 47.9, "src": "gemm", "src_sha16": "86fe77f14a62352c",
+                              "how": "rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_F16 "
+                                     "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE, bench.py --only gemm-one "
+                                     "--shape down_proj --m 2048 --iters 50 (k_gemm_w2; gate: 43.0)"},
+}
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, vendor figure
+
+
+def src_sha16(kind):
+    """sha256 prefix of a kernel's source files (SRC_FILES[kind]): a change to them
+    invalidates a counter figure measured on the old source."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in SRC_FILES[kind]:
+        with open(os.path.join(PKG, "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def measured(key):
+    """(value or None, note) of a MEASURED counter figure for the source of this tree."""
+    m = MEASURED[key]
+    sha = src_sha16(m["src"])
+    if m["src_sha16"] == sha:
+        return m["value"], f"{m['how']} (source {sha})"
+    return None, f"not measured on this source ({sha})"
 
 
 def packed_bytes(N, K):
@@ -59,8 +106,12 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|vocab|container|quantizer|e2e|copy|"
-                    "gemm-one (copy: the 512 MiB device copy that calibrates the HBM byte counters; "
-                    "gemm-one: --iters calls of one prefill shape, the counter workload)")
+                    "library|gemm-one|timeline (copy: the 512 MiB device copy that calibrates the HBM byte "
+                    "counters; library: torch's fp16 GEMM/GEMV and the copy on the layer's shapes; gemm-one: "
+                    "--iters calls of one prefill shape, the counter workload; timeline: per-wave phases of the "
+                    "decode step's GEMV launches from an instrumented build)")
+    ap.add_argument("--no-library", action="store_true", help="skip the same-run library baseline")
+    ap.add_argument("--timeline-tokens", type=int, default=4, help="timeline: tokens generated per run")
     ap.add_argument("--shape", default="gate_proj", help="gemm-one: layer shape name")
     ap.add_argument("--m", type=int, default=2048, help="gemm-one: rows of X")
     ap.add_argument("--iters", type=int, default=200,
@@ -694,6 +745,240 @@ def bench_copy(torch, args):
             "gbs": 2 * nbytes / (us * 1e-6) / 1e9}
 
 
+def bench_library(torch, args):
+    """Same-run library baseline on the layer's shapes, without any dequant: torch's fp16
+    GEMM (hipBLASLt) Y (M, N) fp16 = X (M, K) . W^T at every M of --prefill-m (TFLOP/s per
+    shape and over the layer, median of --iters calls), torch's fp16 GEMV at M = 1 over the
+    layer with 6 rotated copies of the fp16 weights (1.2 GB, cold cache; GB/s of fp16 weight
+    bytes per 7-launch step), and the 512 MiB device copy (the streaming rate)."""
+    dev = torch.device("cuda:0")
+    import _sx8lib as L
+    st = L.stream(dev)
+    g = torch.Generator(device="cpu").manual_seed(99)
+    W = {name: (torch.randn(N, K, generator=g) * 0.02).half().to(dev) for name, N, K in LAYER}
+    out = {"gemm_f16": {}, "library": "torch.mm fp16 (hipBLASLt), fp32 accumulation, fp16 output"}
+    ms = [int(v) for v in str(args.prefill_m).split(",") if v.strip()]
+    for M in ms:
+        xs = {K: torch.randn(M, K, generator=g).half().to(dev) for K in {K for _, _, K in LAYER}}
+        per, tot_flop, tot_us = {}, 0.0, 0.0
+        for name, N, K in LAYER:
+            Y = torch.empty(M, N, dtype=torch.float16, device=dev)
+            Wt = W[name].t()
+            torch.mm(xs[K], Wt, out=Y)
+            torch.cuda.synchronize()
+            q = quantiles(call_series(torch, st, lambda r, X=xs[K], Wt=Wt, Y=Y: torch.mm(X, Wt, out=Y),
+                                      max(200, args.iters)))
+            flop = 2.0 * M * N * K
+            per[name] = {"us": q["median_us"], "p10_us": q["p10_us"], "p90_us": q["p90_us"],
+                         "tflops": flop / (q["median_us"] * 1e-6) / 1e12}
+            tot_flop += flop
+            tot_us += q["median_us"]
+        tf = tot_flop / (tot_us * 1e-6) / 1e12
+        out["gemm_f16"][str(M)] = {"layer_tflops": tf, "frac_of_mfma_peak": tf / MFMA_F16_PEAK_TFLOPS,
+                                   "layer_us": tot_us, "per_shape": per}
+        log(f"library fp16 GEMM M={M}: layer {tf:.1f} TFLOP/s ({tot_us:.1f} us); " +
+            ", ".join(f"{k} {v['tflops']:.0f}" for k, v in per.items()))
+    # fp16 GEMV at M = 1, cold weights: 6 copies of the layer rotated
+    copies = [{name: W[name].clone() for name, _, _ in LAYER} for _ in range(6)]
+    xs = {K: torch.randn(K, generator=g).half().to(dev) for K in {K for _, _, K in LAYER}}
+    ys = {name: torch.empty(N, dtype=torch.float16, device=dev) for name, N, _ in LAYER}
+
+    def step(r):
+        c = copies[r % len(copies)]
+        for name, N, K in LAYER:
+            torch.mv(c[name], xs[K], out=ys[name])
+
+    for r in range(len(copies)):
+        step(r)
+    torch.cuda.synchronize()
+    q = quantiles(call_series(torch, st, step, max(200, args.iters)))
+    wbytes = sum(2 * N * K for _, N, K in LAYER)
+    out["gemv_f16_m1"] = {"step_us": q, "weight_bytes": wbytes, "gbs": wbytes / (q["median_us"] * 1e-6) / 1e9,
+                          "launches_per_step": len(LAYER), "copies": len(copies)}
+    log(f"library fp16 GEMV M=1: {q['median_us']:.1f} us per layer step, "
+        f"{out['gemv_f16_m1']['gbs']:.0f} GB/s of fp16 weights")
+    del copies
+    out["copy_512MiB"] = bench_copy(torch, args)
+    log(f"device copy 512 MiB: {out['copy_512MiB']['gbs']:.0f} GB/s")
+    return out
+
+
+# ------------------------------------------------------------------ decode timeline
+# Per-wave timeline of the decode step's GEMV launches (bench.py --only timeline, GPU only).
+#
+# Builds an instrumented copy of csrc/sx8_gemv.hip into a temporary directory: wave 0 of every
+# work-group of every k_gemv_panel / k_gemv_pair launch stamps the shader clock (s_memtime)
+# at fixed points of the kernel and stores one record.  Then it replays decode steps of the
+# 36-layer decoder through that library (HIP graph, as bench.py's e2e) and prints, per launch
+# kind, the median work-group's phases in shader cycles:
+#
+#   pre-tab          kernel start -> activation-table loads issued
+#   tab->rec         -> first record rounds issued
+#   build(a)         -> table build (RMSNorm forms: up to the norm's barrier)
+#   rms->build(b)    RMSNorm forms: norm barrier -> rest of the table build
+#   barrier          table barrier
+#   loop             the K loop
+#   red-barrier      loop end -> reduction barrier passed (waiting for the slowest wave)
+#   reduce+store     reduction, epilogue, stores
+#
+# plus the launch span (first start to last end, 100 MHz clock), the median start skew and
+# the tail after the median work-group ends.  Usage: python3 bench.py --only timeline [--timeline-tokens T].
+# The instrumentation is anchored on the source text; it fails loudly when the kernel code
+# it expects has changed.
+TL_MAX_REC = 262144
+
+TL_HEADER = r'''
+__device__ unsigned long long g_rec[262144 * 16];
+__device__ unsigned int g_tick;
+#define TS(i) do { __builtin_amdgcn_sched_barrier(0); ts[i] = __builtin_amdgcn_s_memtime(); __builtin_amdgcn_sched_barrier(0); } while (0)
+extern "C" int sx8x_ts_reset() { unsigned int z = 0; return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_tick), &z, 4); }
+extern "C" int sx8x_ts_read(void* dst, size_t n, unsigned* tick) {
+    int r = (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_rec), n);
+    if (r) return r;
+    return (int)hipMemcpyFromSymbol(tick, HIP_SYMBOL(g_tick), 4);
+}
+'''
+
+
+def _tl_record(tag):
+    return f"""    TS(7);
+    ts[11] = __builtin_amdgcn_s_memrealtime();
+    if (tid < 64) {{
+        unsigned tk = 0;
+        if (tid == 0) tk = atomicAdd(&g_tick, 1u);
+        tk = __builtin_amdgcn_readfirstlane(tk);
+        if (tid == 0 && tk < 262144) {{
+            unsigned long long* o = g_rec + (size_t)tk * 16;
+            for (int i = 0; i < 12; ++i) o[i] = ts[i];
+            o[12] = gridDim.x;
+            o[13] = blockIdx.x;
+            o[14] = (unsigned long long)({tag});
+            o[15] = (unsigned long long)TP;
+        }}
+    }}
+"""
+
+
+def timeline_instrument(src):
+    """The GEMV source with the timeline stamps inserted (asserts every anchor)."""
+    def sub(old, new, count=1):
+        nonlocal src
+        if src.count(old) != count:
+            raise SystemExit(f"timeline: anchor found {src.count(old)} times, expected {count}: {old[:70]!r}")
+        src = src.replace(old, new)
+
+    sub("namespace {\n\nstruct KbInfo", TL_HEADER + "namespace {\n\nstruct KbInfo")
+    start = ("    extern __shared__ __align__(16) unsigned char smem[];\n"
+             "    float* red = reinterpret_cast<float*>(smem);                 // 2 x 512 floats\n"
+             "    KbInfo* info")
+    sub(start, "    unsigned long long ts[12] = {};\n    TS(0);\n    ts[10] = __builtin_amdgcn_s_memrealtime();\n"
+        + start, 2)
+    sub("    asm volatile(\"\" ::: \"memory\");\n    __builtin_amdgcn_sched_barrier(0);\n",
+        "    asm volatile(\"\" ::: \"memory\");\n    __builtin_amdgcn_sched_barrier(0);\n    TS(1);\n", 2)
+    sub("        load(buf[i], i);\n        __builtin_amdgcn_sched_barrier(0);\n    }\n",
+        "        load(buf[i], i);\n        __builtin_amdgcn_sched_barrier(0);\n    }\n    TS(2);\n", 2)
+    sub("            const float inv = rms_inv<TP>(xr, h, red, n_units, n_cb * 32, xp.eps, tid);\n",
+        "            const float inv = rms_inv<TP>(xr, h, red, n_units, n_cb * 32, xp.eps, tid);\n            TS(8);\n")
+    sub("        const float inv = rms_inv<TP>(xr, h, red, n_units, n_cb * 32, pa.eps, tid);\n",
+        "        const float inv = rms_inv<TP>(xr, h, red, n_units, n_cb * 32, pa.eps, tid);\n        TS(8);\n")
+    sub("    __syncthreads();\n#pragma unroll\n    for (int i = kNR0; i < NR; ++i) load(buf[i], i);",
+        "    TS(3);\n    __syncthreads();\n    TS(4);\n#pragma unroll\n    for (int i = kNR0; i < NR; ++i) load(buf[i], i);", 2)
+    sub("    red[tid] = acc;\n    __syncthreads();\n    if (tid < 8 * CT) {",
+        "    asm volatile(\"\" :: \"v\"(acc));\n    TS(6);\n    red[tid] = acc;\n    __syncthreads();\n    TS(9);\n"
+        "    if (tid < 8 * CT) {")
+    sub("    if (lane_ok) red[va] = acc;\n    __syncthreads();\n    const int NG = CT > 64 ? 4 : 8;",
+        "    asm volatile(\"\" :: \"v\"(acc));\n    TS(6);\n    if (lane_ok) red[va] = acc;\n    __syncthreads();\n"
+        "    TS(9);\n    const int NG = CT > 64 ? 4 : 8;")
+    # end of k_gemv_panel (after the argmax partials) and of k_gemv_pair
+    sub("                xp.amax[2 * panel + 1] = (uint32_t)idx;\n            }\n        }\n    }\n}\n",
+        "                xp.amax[2 * panel + 1] = (uint32_t)idx;\n            }\n        }\n    }\n"
+        + _tl_record("kX * 100 + kMode * 10 + (kOne ? 1 : 0) + (kPre ? 1000 : 0) + (kResY ? 2000 : 0)") + "}\n")
+    sub("                if (slot == 0 && min(32 * kb + 32, N) <= c1) pa.zp[((int64_t)kb * 2 + 1) * 2 + cc] = 0.f;\n"
+        "            }\n        }\n    }\n}\n",
+        "                if (slot == 0 && min(32 * kb + 32, N) <= c1) pa.zp[((int64_t)kb * 2 + 1) * 2 + cc] = 0.f;\n"
+        "            }\n        }\n    }\n" + _tl_record("9999") + "}\n")
+    return src
+
+
+def timeline_build(L, out_dir):
+    """libsx8_hip.so with the instrumented GEMV source, in out_dir."""
+    src = timeline_instrument(open(os.path.join(L.CSRC_DIR, "sx8_gemv.hip")).read())
+    gemv = os.path.join(out_dir, "sx8_gemv_ts.hip")
+    open(gemv, "w").write(src)
+    flags = [f for f in L.HIP_FLAGS if f != "-shared"]
+
+    def cc(name):
+        path = gemv if name == "sx8_gemv.hip" else os.path.join(L.CSRC_DIR, name)
+        obj = os.path.join(out_dir, name + ".o")
+        r = subprocess.run([L.HIPCC, *flags, *L.SOURCE_FLAGS.get(name, []), "-I", L.CSRC_DIR, "-I",
+                            L.INCLUDE_DIR, "-c", "-o", obj, path], capture_output=True, text=True)
+        if r.returncode:
+            raise SystemExit(r.stderr[-3000:])
+        return obj
+
+    with ThreadPoolExecutor(8) as ex:
+        objs = list(ex.map(cc, L.SOURCES))
+    lib = os.path.join(out_dir, "libsx8_hip.so")
+    subprocess.run([L.HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", lib, *objs], check=True)
+    return lib
+
+
+def bench_timeline(args):
+    """--only timeline: per-wave phases of the decode step's GEMV launches (the comment block above)."""
+    import collections
+    import ctypes
+    import tempfile
+    import _sx8lib as L
+    n_tok = args.timeline_tokens
+    with tempfile.TemporaryDirectory() as d:
+        lib = timeline_build(L, d)
+        print("built", lib, flush=True)
+        os.environ["SX8_HIP_LIB"] = lib
+        import torch
+        from e2e_decoder import QWEN3_4B, SX8Decoder
+        L.lib()
+        raw = ctypes.CDLL(L.lib_path())
+        raw.sx8x_ts_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        dec = SX8Decoder(QWEN3_4B, device="cuda", seed=7, max_len=1024)
+        g = torch.Generator(device="cpu").manual_seed(11)
+        ids = torch.randint(0, QWEN3_4B["vocab"], (512,), generator=g).cuda()
+        dec.generate(ids, n_tok, use_graph=True)           # capture and warm-up
+        torch.cuda.synchronize()
+        raw.sx8x_ts_reset()
+        dec.generate(ids, n_tok, use_graph=True)           # prefill + n_tok - 1 replays
+        torch.cuda.synchronize()
+        buf = np.zeros(TL_MAX_REC * 16, np.uint64)
+        tick = ctypes.c_uint(0)
+        assert raw.sx8x_ts_read(buf.ctypes.data, buf.nbytes, ctypes.byref(tick)) == 0
+    n = min(tick.value, TL_MAX_REC)
+    rec = buf.reshape(-1, 16)[:n].astype(np.int64)
+    launches, i = [], 0
+    while i < n:                                          # records of a launch are contiguous
+        G = int(rec[i, 12])
+        launches.append(rec[i:i + G])
+        i += G
+    print(f"records {n}, launches {len(launches)}")
+    stats = collections.defaultdict(list)
+    for lr in launches:
+        G, tag, tp = int(lr[0, 12]), int(lr[0, 14]), int(lr[0, 15])
+        kx = 1 if tag == 9999 else (tag % 1000) // 100
+        key = (f"pair grid {G}" if tag == 9999 else
+               f"grid {G} kX {kx} mode {(tag % 100) // 10} one {tag % 10} pre/resy {tag // 1000} TP {tp}")
+        t = lr[:, :12]
+        rt0, rt1 = t[:, 10], t[:, 11]
+        ph = lambda a, b: np.median(t[:, b] - t[:, a])  # noqa: E731
+        stats[key].append(((rt1.max() - rt0.min()) * 10 / 1e3, ph(0, 1), ph(1, 2),
+                           ph(2, 3) if kx != 1 else ph(2, 8), ph(8, 3) if kx == 1 else 0, ph(3, 4), ph(4, 6),
+                           ph(6, 9), ph(9, 7), np.median(t[:, 7] - t[:, 0]),
+                           (np.median(rt0) - rt0.min()) * 10 / 1e3, (rt1.max() - np.median(rt1)) * 10 / 1e3))
+    print("median work-group, wave 0, shader cycles: pre-tab | tab->rec | build(a) | rms->build(b) | barrier | "
+          "loop | red-barrier | reduce+store | total ; start skew us ; tail us")
+    for key, v in stats.items():
+        a = np.median(np.array(v), axis=0)
+        print(f"{key:44s} n={len(v):4d} span {a[0]:6.2f} us | " + " ".join(f"{x:.0f}" for x in a[1:10]) +
+              f" | {a[10]:.2f} {a[11]:.2f}")
+
+
 def cpu_baseline(layer, seconds):
     """The oracle's C restatement (R64 dequant to fp16 + fp32 GEMV, OpenMP) on the host,
     over as many layer shapes as fit in about `seconds`: with every host thread OpenMP
@@ -794,15 +1079,24 @@ def mfma_count(M, N, K, plan):
                                                                                   plan["kb_per_range"]))
 
 
-def prefill_roofline(pf):
+def prefill_roofline(pf, lib=None):
     """The roofline block of the prefill GEMM at the headline M: the layer (7 calls, each
-    with its Z/pack pass and any split-K sum) and its dominant call, median durations."""
+    with its Z/pack pass and any split-K sum) and its dominant call, median durations; the
+    dominant kernel's MFMA busy % and HBM bytes per launch from the counter passes when the
+    source and plan are the ones measured; the same-run library fp16 GEMM (no dequant) over
+    the layer at that M for comparison."""
     if not pf:
         return None
     M = pf["M"]
     dom = max(pf["per_shape"].items(), key=lambda kv: kv[1]["median_us"])
     name, q = dom
     flop = 2.0 * M * dict((n, N * K) for n, N, K in LAYER)[name]
+    same = name == "down_proj" and M == 2048 and q["plan"]["tile"] == 512 and os.environ.get("SX8_GEMM_W2") != "0"
+    busy, busy_src = measured("prefill_mfma_busy_pct") if same else (None, "measured for down_proj at M = 2048 only")
+    traffic, traffic_src = measured("prefill_traffic") if same else (None, "measured for down_proj at M = 2048 only")
+    lib_tf = None
+    if lib and str(M) in lib.get("gemm_f16", {}):
+        lib_tf = round(lib["gemm_f16"][str(M)]["layer_tflops"], 1)
     return {
         "bound": "mfma", "unit": "TFLOP/s", "peak": MFMA_F16_PEAK_TFLOPS, "M": M,
         "layer": {"flop": pf["layer_flop"], "us": pf["layer_us"], "achieved": round(pf["tflops"], 1),
@@ -813,8 +1107,14 @@ def prefill_roofline(pf):
                      "flop_per_call": flop, "us": q["median_us"], "p10_us": q["p10_us"], "p90_us": q["p90_us"],
                      "achieved": round(q["tflops"], 1), "frac": round(q["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                      "plan": q["plan"]},
-        "mfma_busy": "profiles/prefill_gemm_m2048.md (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs)",
-        "traffic": None,
+        "mfma_busy_pct": busy,
+        "mfma_busy_source": busy_src,
+        "traffic": traffic,
+        "traffic_unit": "HBM bytes per launch of the dominant call's GEMM kernel (FETCH_SIZE+WRITE_SIZE, "
+                        "copy-calibrated)",
+        "traffic_source": traffic_src,
+        "library_layer_tflops": lib_tf,
+        "vs_library": round(pf["tflops"] / lib_tf, 3) if lib_tf else None,
     }
 
 
@@ -829,6 +1129,9 @@ def main():
     if not torch.cuda.is_available():
         print("no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.only == "timeline":
+        bench_timeline(args)                               # loads its own instrumented build
+        return
     L.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -858,6 +1161,8 @@ def main():
         log("vocab", json.dumps(res["vocab"]))
     if args.only in ("", "e2e") and not args.no_e2e:
         res["e2e"] = bench_e2e(torch, args)
+    if args.only in ("", "library") and not args.no_library:
+        res["library"] = bench_library(torch, args)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(layer, args.cpu_seconds)
@@ -891,16 +1196,19 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gv.get("achieved_gbs", 0.0) / HBM_PEAK_GBS, 4),
-            "traffic": GEMV_TRAFFIC_PER_LAUNCH if args.hdr_bytes == 6 else None,
+            "traffic": measured("gemv_traffic")[0] if args.hdr_bytes == 6 else None,
             "traffic_unit": "bytes per launch (HBM, rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
+            "traffic_source": measured("gemv_traffic")[1] if args.hdr_bytes == 6 else "measured for hdr_bytes=6 only",
             "avg_launch_us": round(gv.get("avg_launch_us", 0.0), 3),
+            "traced_avg_launch_us": measured("gemv_traced_launch_us")[0] if args.hdr_bytes == 6 else None,
+            "traced_avg_launch_source": measured("gemv_traced_launch_us")[1],
             "avg_launch_source": "timed region / launches (two HIP events on the launch stream, "
-                                 "nothing between the launches); compare the rocprofv3 kernel-trace mean "
-                                 "in profiles/gemv_decode_layer.md",
+                                 "nothing between the launches); traced_avg_launch_us is the rocprofv3 "
+                                 "kernel-trace mean of the same launches (profiles/gemv_decode_layer.md)",
             "bytes_per_launch": gv.get("bytes_per_launch"),
             "step_us": gv.get("step_us"),
         },
-        "prefill_roofline": prefill_roofline(res.get("prefill")),
+        "prefill_roofline": prefill_roofline(res.get("prefill"), res.get("library")),
         "cpu_baseline": cpu,
         "gemv_grouped": gv.get("grouped"),
         "gemv_graph": gv.get("graph"),
@@ -909,6 +1217,7 @@ def main():
         "container": res.get("container"),
         "quantizer": res.get("quantizer"),
         "e2e": res.get("e2e"),
+        "library_baseline": res.get("library"),
     }
     print(json.dumps(line), flush=True)
 

@@ -36,7 +36,8 @@
 extern "C" {
 #endif
 
-#define SX8_ABI_VERSION 2
+/* 3: sx8_dec_gemv_rmsnorm_pair takes the up matrix's pointers; sx8_gemm_reload_tuning */
+#define SX8_ABI_VERSION 3
 
 #define SX8_OK 0
 #define SX8_ERR_INVALID 1      /* bad argument (null pointer, size, hdr_bytes, alignment) */

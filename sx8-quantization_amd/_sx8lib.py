@@ -91,7 +91,7 @@ SIGNATURES = [
                                          _P, _P, _P, _P]),
     ("sx8_dec_gemv_zp_add", _I32, [_P, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _P]),
 ]
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 _lock = threading.Lock()
