@@ -67,6 +67,9 @@ MEASURED = {
                                      "--shape down_proj --m 2048 --iters 50 (k_gemm_w2; gate: 43.0)"},
 }
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, vendor figure
+# The streaming-read rate measured on the GPU boxes (bench.py --only readbw: best of the
+# probe's grid sizes, 6.06-6.25 TB/s across runs): a second reference beside the vendor peak
+READ_CEILING_GBS = 6250.0
 
 
 def src_sha16(kind):
@@ -106,10 +109,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|vocab|container|quantizer|e2e|copy|"
-                    "library|gemm-one|timeline (copy: the 512 MiB device copy that calibrates the HBM byte "
+                    "library|gemm-one|timeline|readbw (copy: the 512 MiB device copy that calibrates the HBM byte "
                     "counters; library: torch's fp16 GEMM/GEMV and the copy on the layer's shapes; gemm-one: "
                     "--iters calls of one prefill shape, the counter workload; timeline: per-wave phases of the "
-                    "decode step's GEMV launches from an instrumented build)")
+                    "decode step's GEMV launches from an instrumented build; readbw: the streaming-read rate of "
+                    "the GPU, a 4 GiB buffer read by a hipcc-built probe)")
     ap.add_argument("--no-library", action="store_true", help="skip the same-run library baseline")
     ap.add_argument("--timeline-tokens", type=int, default=4, help="timeline: tokens generated per run")
     ap.add_argument("--shape", default="gate_proj", help="gemm-one: layer shape name")
@@ -979,6 +983,72 @@ def bench_timeline(args):
               f" | {a[10]:.2f} {a[11]:.2f}")
 
 
+# ------------------------------------------------------------------ read ceiling
+# The streaming-read rate of this GPU (bench.py --only readbw): a 4 GiB buffer read with
+# 16-byte loads by 256..4096 work-groups, each streaming a contiguous slice (8 loads in
+# flight per thread, one store per work-group), 10 launches per grid size.  The GEMV is a
+# read stream, so this -- not the 8 TB/s vendor figure, nor the read + write device copy --
+# is the practical ceiling its streaming phase is compared with.  Built with hipcc into a
+# temporary directory at run time.
+READBW_SRC = r'''
+#include <hip/hip_runtime.h>
+#include <cstdio>
+__global__ __launch_bounds__(256) void rd(const uint4* __restrict__ p, size_t n16, unsigned* out) {
+    const size_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const size_t b = (size_t)blockIdx.x * per, e = b + per < n16 ? b + per : n16;
+    unsigned acc = 0;
+    for (size_t i = b + threadIdx.x; i < e; i += 256 * 8) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) { size_t k = i + 256 * u; v[u] = k < e ? p[k] : make_uint4(0, 0, 0, 0); }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x12345678u) out[blockIdx.x] = acc;
+}
+int main() {
+    const size_t bytes = (size_t)4 << 30;
+    uint4* p; unsigned* o;
+    if (hipMalloc(&p, bytes) != hipSuccess || hipMalloc(&o, 1 << 20) != hipSuccess) return 1;
+    if (hipMemset(p, 1, bytes) != hipSuccess) return 1;
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) return 1;
+    for (int grid : {256, 512, 1024, 2048, 4096}) {
+        rd<<<grid, 256>>>(p, bytes / 16, o);
+        hipEventRecord(a);
+        for (int i = 0; i < 10; ++i) rd<<<grid, 256>>>(p, bytes / 16, o);
+        hipEventRecord(b);
+        if (hipEventSynchronize(b) != hipSuccess) return 1;
+        float ms = 0.f;
+        hipEventElapsedTime(&ms, a, b);
+        printf("{\"grid\": %d, \"gbs\": %.1f}\n", grid, bytes * 10.0 / (ms * 1e-3) / 1e9);
+    }
+    return hipFree(p) != hipSuccess || hipFree(o) != hipSuccess;
+}
+'''
+
+
+def bench_readbw():
+    """--only readbw: the streaming-read ceiling (the comment block above).  Runs the probe
+    as a child process (it makes its own HIP context) and returns its figures."""
+    import tempfile
+    sys.path.insert(0, PKG)
+    import _sx8lib as L
+    with tempfile.TemporaryDirectory() as d:
+        src, exe = os.path.join(d, "readbw.hip"), os.path.join(d, "readbw")
+        with open(src, "w") as f:
+            f.write(READBW_SRC)
+        r = subprocess.run([L.HIPCC, "--offload-arch=gfx950", "-O3", "-Xclang", "-target-feature", "-Xclang",
+                            "-packed-fp32-ops", "-o", exe, src], capture_output=True, text=True)
+        if r.returncode:
+            raise SystemExit(r.stderr[-2000:])
+        r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+        if r.returncode:
+            raise SystemExit(f"readbw probe failed ({r.returncode}): {r.stderr[-500:]}")
+    rows = [json.loads(l) for l in r.stdout.splitlines() if l.startswith("{")]
+    best = max(x["gbs"] for x in rows)
+    return {"per_grid": rows, "best_gbs": best, "frac_of_vendor_peak": best / HBM_PEAK_GBS}
+
 def cpu_baseline(layer, seconds):
     """The oracle's C restatement (R64 dequant to fp16 + fp32 GEMV, OpenMP) on the host,
     over as many layer shapes as fit in about `seconds`: with every host thread OpenMP
@@ -1132,6 +1202,9 @@ def main():
     if args.only == "timeline":
         bench_timeline(args)                               # loads its own instrumented build
         return
+    if args.only == "readbw":
+        print(json.dumps({"readbw": bench_readbw()}), flush=True)   # a child process of its own
+        return
     L.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -1196,6 +1269,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gv.get("achieved_gbs", 0.0) / HBM_PEAK_GBS, 4),
+            "read_ceiling_gbs": READ_CEILING_GBS,
+            "frac_of_read_ceiling": round(gv.get("achieved_gbs", 0.0) / READ_CEILING_GBS, 4),
+            "read_ceiling_source": "bench.py --only readbw (streaming 16-byte reads of 4 GiB)",
             "traffic": measured("gemv_traffic")[0] if args.hdr_bytes == 6 else None,
             "traffic_unit": "bytes per launch (HBM, rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
             "traffic_source": measured("gemv_traffic")[1] if args.hdr_bytes == 6 else "measured for hdr_bytes=6 only",
