@@ -43,28 +43,30 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
 # the bench line reports null for it instead of a stale figure.
 # HBM bytes per launch = FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 (KiB per dispatch, scaled by
 # what the two counters read for a 512 MiB device copy, bench.py --only copy).
+# (the prefill figures are k_gemm_w2's alone, which is built from sx8_gemm.hip and the device
+# headers; the Z/pack pass in sx8_gemv.hip is a kernel of its own)
 SRC_FILES = {"gemv": ("sx8_gemv.hip", "sx8_device.h", "sx8_buffer.h"),
-             "gemm": ("sx8_gemm.hip", "sx8_gemv.hip", "sx8_device.h", "sx8_buffer.h")}
+             "gemm": ("sx8_gemm.hip", "sx8_device.h", "sx8_buffer.h")}
 MEASURED = {
-    # k_gemv_panel over the layer sweep: mean 6812.6 KiB fetched, 17.1 KiB written per launch
-    "gemv_traffic": {"value": (6812.6 * 2.0 + 17.1) * 1024, "src": "gemv", "src_sha16": "41e63bced56438b7",
+    # k_gemv_panel over the layer sweep: mean 6820.7 KiB fetched, 17.1 KiB written per launch
+    "gemv_traffic": {"value": (6820.7 * 2.0 + 17.1) * 1024, "src": "gemv", "src_sha16": "9ba026f0ed6ce498",
                      "how": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, bench.py --only gemv --steps 10 "
                             "--warmup 2, first 12 x 7 single-matrix dispatches"},
     # rocprofv3 kernel-trace mean over the 140 timed k_gemv_panel dispatches (20 steps x 7);
-    # bench.py's own figure in that traced run: 6.215 us per launch (timed region / launches)
-    "gemv_traced_launch_us": {"value": 6.187, "src": "gemv", "src_sha16": "41e63bced56438b7",
+    # bench.py's own figure in that traced run: 6.143 us per launch (timed region / launches)
+    "gemv_traced_launch_us": {"value": 6.116, "src": "gemv", "src_sha16": "9ba026f0ed6ce498",
                               "how": "rocprofv3 --kernel-trace --stats, bench.py --only gemv --steps 20 "
-                                     "(same-run event figure under the tracer: 6.215 us)"},
-    # k_gemm_w2 on down_proj at M = 2048 (plan 80 tiles x 3 K ranges): 89774.3 KiB fetched,
-    # 61751.1 KiB written per dispatch (Y 21 MB + two partial tiles per split tile 42 MB)
-    "prefill_traffic": {"value": (89774.3 * 2.0 + 61751.1) * 1024, "src": "gemm", "src_sha16": "86fe77f14a62352c",
+                                     "(same-run event figure under the tracer: 6.143 us)"},
+    # k_gemm_w2 on down_proj at M = 2048 (plan 80 tiles x 3 K ranges): 89774.2 KiB fetched,
+    # 61699.2 KiB written per dispatch (Y 21 MB + two partial tiles per split tile 42 MB)
+    "prefill_traffic": {"value": (89774.2 * 2.0 + 61699.2) * 1024, "src": "gemm", "src_sha16": "ed75f6af399ae58c",
                         "how": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, bench.py --only gemm-one "
                                "--shape down_proj --m 2048 --iters 20, mean of 21 dispatches"},
     # 100 x sum SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs)
-    "prefill_mfma_busy_pct": {"value": 47.9, "src": "gemm", "src_sha16": "86fe77f14a62352c",
+    "prefill_mfma_busy_pct": {"value": 47.7, "src": "gemm", "src_sha16": "ed75f6af399ae58c",
                               "how": "rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_F16 "
                                      "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE, bench.py --only gemm-one "
-                                     "--shape down_proj --m 2048 --iters 50 (k_gemm_w2; gate: 43.0)"},
+                                     "--shape down_proj --m 2048 --iters 50 (k_gemm_w2; gate: 42.8)"},
 }
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, vendor figure
 # The streaming-read rate measured on the GPU boxes (bench.py --only readbw: best of the
@@ -214,6 +216,24 @@ def call_series(torch, st, fn, n, delay_ms=10):
     torch.cuda.synchronize()
     out = [ev.ms(i, i + 1) * 1e3 for i in range(n)]
     ev.close()
+    return out
+
+
+def region_series(torch, st, fn, n, reps=10, delay_ms=10):
+    """Per-call time (us) of n back-to-back calls fn(i) with one HIP event before the first
+    and one after the last (nothing between the calls: the GEMV headline's method), `reps`
+    such regions; returns the regions' per-call times."""
+    out = []
+    for _ in range(reps):
+        ev = HipEvents(2, st)
+        gpu_delay(torch, delay_ms)
+        ev.record(0)
+        for i in range(n):
+            fn(i)
+        ev.record(1)
+        torch.cuda.synchronize()
+        out.append(ev.ms(0, 1) * 1e3 / n)
+        ev.close()
     return out
 
 
@@ -632,14 +652,17 @@ def bench_vocab(torch, L, args):
     out = {"shape": f"{N}x{K}", "packed_bytes": packed_bytes(N, K)}
 
     def timed(fn, reps):
-        """median ms of max(reps, --iters) back-to-back calls (and the distribution)"""
+        """median ms of max(reps, --iters) back-to-back calls, an event after each (and the
+        distribution); `region` gets the per-call time of timed regions of `reps` calls with
+        events only around each region (the GEMV headline's method)"""
         fn()
         torch.cuda.synchronize()
         q = quantiles(call_series(torch, st, lambda r: fn(), max(reps, args.iters)))
         dist.append(q)
+        region.append(quantiles(region_series(torch, st, lambda r: fn(), reps)))
         return q["median_us"] * 1e-3
 
-    dist = []
+    dist, region = [], []
 
     def ok(rc):
         if rc != 0:
@@ -652,8 +675,14 @@ def bench_vocab(torch, L, args):
     ms = timed(lambda: ok(lib.sx8_gemv(L.ptr(x1), L.ptr(hdr), L.ptr(lvl), args.hdr_bytes, L.ptr(bas),
                                        L.ptr(sca), None, None, N, n_cb, L.ptr(y1), L.ptr(ws),
                                        ws.numel() * 4, st)), 20)
-    out["gemv_m1"] = {"us": ms * 1e3, "gbs": packed_bytes(N, K) / (ms * 1e-3) / 1e9, "us_dist": dist[-1]}
-    log(f"vocab gemv M=1: {ms * 1e3:.1f} us {out['gemv_m1']['gbs']:.0f} GB/s")
+    rus = region[-1]["median_us"]
+    out["gemv_m1"] = {"us": ms * 1e3, "gbs": packed_bytes(N, K) / (ms * 1e-3) / 1e9, "us_dist": dist[-1],
+                      "region_us": rus, "region_gbs": packed_bytes(N, K) / (rus * 1e-6) / 1e9,
+                      "region_dist": region[-1],
+                      "region_method": "median over 10 timed regions of 20 back-to-back calls, one event "
+                                       "before and one after each region (as the layer sweep's avg_launch_us)"}
+    log(f"vocab gemv M=1: {ms * 1e3:.1f} us {out['gemv_m1']['gbs']:.0f} GB/s (event after each call); "
+        f"{rus:.1f} us {out['gemv_m1']['region_gbs']:.0f} GB/s (timed regions)")
     # lm_head prefill GEMM, M = 512
     M = 512
     xm = torch.randn(M, K, generator=g).half().to(dev)
@@ -663,6 +692,8 @@ def bench_vocab(torch, L, args):
                                                L.ptr(bas), L.ptr(sca), N, n_cb, L.ptr(ym), L.ptr(wsm), nbm,
                                                st)), 5)
     out["gemm_m512"] = {"us": ms * 1e3, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12, "us_dist": dist[-1],
+                        "region_us": region[-1]["median_us"],
+                        "region_tflops": 2.0 * M * N * K / (region[-1]["median_us"] * 1e-6) / 1e12,
                         "plan": L.gemm_plan(M, (N,), n_cb)}
     log(f"vocab gemm M=512: {ms * 1e3:.1f} us {out['gemm_m512']['tflops']:.0f} TFLOP/s")
     del ym
@@ -672,7 +703,8 @@ def bench_vocab(torch, L, args):
     ms = timed(lambda: ok(lib.sx8_embed_gather(L.ptr(ids), 512, L.ptr(hdr), L.ptr(lvl), args.hdr_bytes,
                                                L.ptr(bas), L.ptr(sca), K, N, n_cb, L.ptr(rows), st)), 20)
     rd, wr = 512 * n_cb * 30, 512 * K * 2
-    out["embed"] = {"ids": 512, "us": ms * 1e3, "gbs": (rd + wr) / (ms * 1e-3) / 1e9, "us_dist": dist[-1]}
+    out["embed"] = {"ids": 512, "us": ms * 1e3, "gbs": (rd + wr) / (ms * 1e-3) / 1e9, "us_dist": dist[-1],
+                    "region_us": region[-1]["median_us"]}
     log(f"vocab embed 512 ids: {ms * 1e3:.1f} us")
     return out
 
@@ -887,9 +919,9 @@ def timeline_instrument(src):
         "        const float inv = rms_inv<TP>(xr, h, red, n_units, n_cb * 32, pa.eps, tid);\n        TS(8);\n")
     sub("    __syncthreads();\n#pragma unroll\n    for (int i = kNR0; i < NR; ++i) load(buf[i], i);",
         "    TS(3);\n    __syncthreads();\n    TS(4);\n#pragma unroll\n    for (int i = kNR0; i < NR; ++i) load(buf[i], i);", 2)
-    sub("    red[tid] = acc;\n    __syncthreads();\n    if (tid < 8 * CT) {",
+    sub("    red[tid] = acc;\n    __syncthreads();\n    const bool wide = CT > 64;",
         "    asm volatile(\"\" :: \"v\"(acc));\n    TS(6);\n    red[tid] = acc;\n    __syncthreads();\n    TS(9);\n"
-        "    if (tid < 8 * CT) {")
+        "    const bool wide = CT > 64;")
     sub("    if (lane_ok) red[va] = acc;\n    __syncthreads();\n    const int NG = CT > 64 ? 4 : 8;",
         "    asm volatile(\"\" :: \"v\"(acc));\n    TS(6);\n    if (lane_ok) red[va] = acc;\n    __syncthreads();\n"
         "    TS(9);\n    const int NG = CT > 64 ? 4 : 8;")

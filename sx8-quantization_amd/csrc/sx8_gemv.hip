@@ -705,8 +705,17 @@ struct GemvGroup {
 };
 
 // Panel width for a launch over `total` output columns: about one work-group per CU
-// (ceil(total / 256) columns), two per CU past 64 columns (host and device share it).
+// (ceil(total / 256) columns), two per CU past 64 columns, and 128 columns (4 slices, no
+// idle lanes) past 65536, where that still leaves two or more work-groups per CU and
+// halves the number of table builds (vocab-sized matrices; host and device share it).
+// Measured on the 151936 x 2560 lm_head (timed regions of 50 back-to-back launches, same
+// box): the RMSNorm + argmax-partials form 69.8-70.9 us against 72.4-72.7 us with 64
+// columns (half the norms and partials), the plain GEMV 65.0-66.0 against 65.5-67.6 us;
+// widths 96 and 160 (idle lanes) and 256 (too few work-groups) were slower than 64.
+constexpr int kMaxPanelCt = 128;
+static_assert(kPanelThreads % kMaxPanelCt == 0, "a 128-column panel has whole slices");
 __host__ __device__ inline int panel_ct(int64_t total) {
+    if (total > 65536) return kMaxPanelCt;
     int64_t ct = (total + 255) / 256;
     if (ct > 64) ct = (total + 511) / 512;
     return (int)(ct < 1 ? 1 : ct > 64 ? 64 : ct);
@@ -935,30 +944,40 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     for (int i = 0; i < NR; ++i)
         if (r + i < R) step(buf[i], r + i);
 
-    // slices -> columns in a fixed order: thread t < 8 CT sums slices g, g + 8, ... of
-    // column t % CT (g = t / CT), eight loads in flight at a time, then thread c < CT sums
-    // the 8 partials of column c
+    // slices -> columns in a fixed order.  CT <= 64 (S >= 8): thread t < 8 CT sums slices
+    // g, g + 8, ... of column t % CT (g = t / CT), eight loads in flight at a time, then
+    // thread c < CT sums the 8 partials of column c.  CT = kMaxPanelCt (S = 4, every lane a
+    // slice): thread c sums its column's 4 slices in slice order (the same order the
+    // two-step form gives with 4 groups of one slice each); red[kPanelThreads..) stays free.
     red[tid] = acc;
     __syncthreads();
-    if (tid < 8 * CT) {
-        float t = 0.f;
-        int s = j0;
-        for (; s + 56 < S; s += 64) {
-            float v[8];
+    const bool wide = CT > 64;   // CT is kMaxPanelCt (the host plans no width in 65..127)
+    if (!wide) {
+        if (tid < 8 * CT) {
+            float t = 0.f;
+            int s = j0;
+            for (; s + 56 < S; s += 64) {
+                float v[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = red[(s + 8 * i) * CT + c];
+                for (int i = 0; i < 8; ++i) v[i] = red[(s + 8 * i) * CT + c];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) t += v[i];
+                for (int i = 0; i < 8; ++i) t += v[i];
+            }
+            for (; s < S; s += 8) t += red[s * CT + c];
+            red[kPanelThreads + tid] = t;
         }
-        for (; s < S; s += 8) t += red[s * CT + c];
-        red[kPanelThreads + tid] = t;
+        __syncthreads();
     }
-    __syncthreads();
     float yv = -INFINITY;
     if (tid < CT && col_ok) {
         float t = 0.f;
+        if (wide) {
 #pragma unroll
-        for (int g = 0; g < 8; ++g) t += red[kPanelThreads + g * CT + tid];
+            for (int g = 0; g < kPanelThreads / kMaxPanelCt; ++g) t += red[g * kMaxPanelCt + tid];
+        } else {
+#pragma unroll
+            for (int g = 0; g < 8; ++g) t += red[kPanelThreads + g * CT + tid];
+        }
         // residual epilogue: h = resid + W x, each element read and written by this thread
         if constexpr (kResY) {
             t = yres + t;
@@ -971,21 +990,42 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
     }
     // argmax partials (lm_head): the panel's best column -- larger value, or equal value and
     // lower index, so the maxima of the panels give the first index of the overall maximum;
-    // a NaN never wins -- from the CT <= 64 columns of wave 0
+    // a NaN never wins -- from the CT columns of waves 0 (and 1 when CT > 64), wave 1's
+    // best passed to wave 0 through LDS
     if constexpr (kX == kXRms && kOne) {
-        if (xp.amax != nullptr && tid < 64) {
-            // a NaN logit never enters the butterfly: its lane starts empty (-inf, INT_MAX)
-            // and takes its partners' values like any other
-            const bool mine = tid < CT && col_ok && !__builtin_isnan(yv);
-            float v = mine ? yv : -INFINITY;
-            int idx = mine ? n : INT_MAX;
+        if (xp.amax != nullptr) {   // the same for every thread of the work-group
+            float v = -INFINITY;
+            int idx = INT_MAX;
+            if (tid < 128) {
+                // a NaN logit never enters the butterfly: its lane starts empty (-inf,
+                // INT_MAX) and takes its partners' values like any other
+                const bool mine = tid < CT && col_ok && !__builtin_isnan(yv);
+                v = mine ? yv : -INFINITY;
+                idx = mine ? n : INT_MAX;
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(v, o);
-                const int oi = __shfl_xor(idx, o);
-                if (ov > v || (ov == v && oi < idx)) {
-                    v = ov;
-                    idx = oi;
+                for (int o = 32; o > 0; o >>= 1) {
+                    const float ov = __shfl_xor(v, o);
+                    const int oi = __shfl_xor(idx, o);
+                    if (ov > v || (ov == v && oi < idx)) {
+                        v = ov;
+                        idx = oi;
+                    }
+                }
+            }
+            if (wide) {
+                // the 128-column sums leave red[kPanelThreads..) unused
+                if (tid == 64) {
+                    red[kPanelThreads] = v;
+                    red[kPanelThreads + 1] = __builtin_bit_cast(float, idx);
+                }
+                __syncthreads();
+                if (tid == 0) {
+                    const float ov = red[kPanelThreads];
+                    const int oi = __builtin_bit_cast(int, red[kPanelThreads + 1]);
+                    if (ov > v || (ov == v && oi < idx)) {
+                        v = ov;
+                        idx = oi;
+                    }
                 }
             }
             if (tid == 0) {
@@ -1044,9 +1084,9 @@ __global__ __launch_bounds__(256) void k_argmax_parts(const uint32_t* __restrict
     }
 }
 
-// Panel geometry: CT columns per panel (at most 64), from the group's total width:
-// ceil(sum N / 256) gives about one work-group per CU; wider groups take two per CU
-// (co-resident).  Three record buffers, two of them requested before the table build and
+// Panel geometry: CT columns per panel (at most 64, or 128 past 65536 columns), from the
+// group's total width: ceil(sum N / 256) gives about one work-group per CU; wider groups
+// take two per CU (co-resident).  Three record buffers, two of them requested before the table build and
 // the third right after it: more rounds ahead of the table lengthen the prologue, which is
 // where a launch loses most of its time (measured slower on MI355X).
 struct PanelPlan {

@@ -629,14 +629,15 @@ def test_gemv_pair_and_zp_down(hiplib, cuda, H, I, hb):
 
 @pytest.mark.parametrize("K,N,hb", [
     (2560, 20000, 6),      # fewer panels than co-resident work-groups: one panel each
-    (256, 100000, 6),      # several panels per work-group, one K round per panel (R < ring)
-    (2560, 151936, 8),     # the vocab-sized lm_head, 8-byte headers
+    (256, 100000, 6),      # 128-column panels, one K round per panel (R < ring)
+    (2560, 151936, 8),     # the vocab-sized lm_head (128-column panels), 8-byte headers
 ])
 def test_head_argmax_partials(hiplib, cuda, K, N, hb):
     """sx8_dec_gemv_rmsnorm_argmax: logits bit for bit those of sx8_dec_gemv_rmsnorm, and the
-    token that sx8_dec_argmax_advance picks from them -- with three equal maxima (rows 5, 6
-    in one panel and 17000 in another, identical weights give identical logits) the first
-    index wins -- and the position advanced."""
+    token that sx8_dec_argmax_advance picks from them -- with four equal maxima (rows 5, 6
+    and 70 in the first panel, 70 in the second wave of a 128-column panel, and 17000 in
+    another panel; identical weights give identical logits) the first index wins -- and
+    the position advanced."""
     import torch
     import _sx8lib as _L
     from quantize_sx8 import quantize_tensor
@@ -649,7 +650,7 @@ def test_head_argmax_partials(hiplib, cuda, K, N, hb):
     resids = [torch.randn(K, generator=g) for _ in range(2)]
     W = torch.randn(N, K, generator=g) * 0.02
     top = torch.sign(resids[0]) * 0.05           # the largest logit for the first residual
-    W[5], W[6], W[17000] = top, top, top
+    W[5], W[6], W[70], W[17000] = top, top, top, top
     qt, bi = quantize_tensor(W.half(), device=cuda, degenerate_frac=0.0, seed=32)   # equal rows stay equal
     hdr, lvl, bas, sca = make_tensors_v44(qt, bi, hdr_aligned=hb == 8)
     assert hdr.shape[-1] == hb
@@ -674,29 +675,33 @@ def test_head_argmax_partials(hiplib, cuda, K, N, hb):
         assert torch.equal(logits.cpu(), ref.cpu()), k
         assert tok.item() == tok_ref.item() and pos.item() == 41, (k, tok.item(), tok_ref.item())
         if k == 0:
-            assert tok.item() == 5 and ref[5].item() == ref[17000].item() == ref.max().item()
+            assert tok.item() == 5 and ref[5].item() == ref[70].item() == ref[17000].item() == ref.max().item()
     with pytest.raises(RuntimeError, match="parts"):
         _L.call("sx8_dec_gemv_rmsnorm_argmax", P(rd), P(w), eps, P(hdr), P(lvl), hb, P(bas), P(sca), N, K // 32,
                 P(logits), P(parts), nb - 8, P(tok), P(pos), st)
 
 
-def test_head_argmax_partials_nan_logit(hiplib, cuda):
+@pytest.mark.parametrize("N,top", [
+    (16384, 48),     # 64-column panels (256 of them): 48 is 16's partner across 32 lanes
+    (70000, 100),    # 128-column panels: 100 is in the panel's second wave
+])
+def test_head_argmax_partials_nan_logit(hiplib, cuda, N, top):
     """A NaN logit in a panel never hides the panel's other columns from the argmax: column
-    16's first header decodes a NaN range (dmin = fp16 NaN), column 48 -- in the same
-    64-column panel, its partner across the 32-lane step of the panel's butterfly -- holds
-    the largest logit.  sx8_dec_gemv_rmsnorm_argmax must pick 48, as sx8_dec_argmax_advance
-    does on the same logits."""
+    16's first header decodes a NaN range (dmin = fp16 NaN), column `top` -- in the same
+    panel, across the 32-lane step of the butterfly of 64-column panels, or in the second
+    wave of a 128-column panel -- holds the largest logit.  sx8_dec_gemv_rmsnorm_argmax must
+    pick `top`, as sx8_dec_argmax_advance does on the same logits."""
     import torch
     import _sx8lib as _L
     from quantize_sx8 import quantize_tensor
     from sx8_decode1_v3 import make_tensors_v44
     P = _L.ptr
     st = _L.stream(cuda)
-    K, N, eps = 2560, 16384, 1e-6           # 16384 columns: 64-column panels (256 of them)
+    K, eps = 2560, 1e-6
     g = torch.Generator().manual_seed(41)
     resid = torch.randn(K, generator=g)
     W = torch.randn(N, K, generator=g) * 0.02
-    W[48] = torch.sign(resid) * 0.05
+    W[top] = torch.sign(resid) * 0.05
     qt, bi = quantize_tensor(W.half(), device=cuda, degenerate_frac=0.0, seed=42)
     hdr, lvl, bas, sca = make_tensors_v44(qt, bi)
     hdr.view(-1, 6)[16, 0:2] = torch.tensor([0x00, 0x7E], dtype=torch.uint8, device=cuda)  # kb 0, n 16
@@ -719,5 +724,5 @@ def test_head_argmax_partials_nan_logit(hiplib, cuda):
     lr = ref.cpu()
     assert torch.isnan(lr[16]) and torch.isnan(lr).sum().item() == 1
     assert torch.equal(logits.cpu().view(torch.int32), lr.view(torch.int32))
-    assert tok_ref.item() == 48
-    assert tok.item() == 48 and pos.item() == 1
+    assert tok_ref.item() == top
+    assert tok.item() == top and pos.item() == 1
