@@ -111,11 +111,12 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|vocab|container|quantizer|e2e|copy|"
-                    "library|gemm-one|timeline|readbw (copy: the 512 MiB device copy that calibrates the HBM byte "
+                    "library|gemm-one|timeline|readbw|handoff (copy: the 512 MiB device copy that calibrates the HBM byte "
                     "counters; library: torch's fp16 GEMM/GEMV and the copy on the layer's shapes; gemm-one: "
                     "--iters calls of one prefill shape, the counter workload; timeline: per-wave phases of the "
                     "decode step's GEMV launches from an instrumented build; readbw: the streaming-read rate of "
-                    "the GPU, a 4 GiB buffer read by a hipcc-built probe)")
+                    "the GPU, a 4 GiB buffer read by a hipcc-built probe; handoff: an in-kernel producer-to-consumer "
+                    "handoff against a second launch, a hipcc-built probe)")
     ap.add_argument("--no-library", action="store_true", help="skip the same-run library baseline")
     ap.add_argument("--timeline-tokens", type=int, default=4, help="timeline: tokens generated per run")
     ap.add_argument("--shape", default="gate_proj", help="gemm-one: layer shape name")
@@ -1060,26 +1061,162 @@ int main() {
 '''
 
 
-def bench_readbw():
-    """--only readbw: the streaming-read ceiling (the comment block above).  Runs the probe
-    as a child process (it makes its own HIP context) and returns its figures."""
+def run_probe(name, source):
+    """Build a stand-alone HIP probe with hipcc into a temporary directory, run it as a child
+    process (it makes its own HIP context) and return the JSON objects it printed."""
     import tempfile
     sys.path.insert(0, PKG)
     import _sx8lib as L
     with tempfile.TemporaryDirectory() as d:
-        src, exe = os.path.join(d, "readbw.hip"), os.path.join(d, "readbw")
+        src, exe = os.path.join(d, name + ".hip"), os.path.join(d, name)
         with open(src, "w") as f:
-            f.write(READBW_SRC)
+            f.write(source)
         r = subprocess.run([L.HIPCC, "--offload-arch=gfx950", "-O3", "-Xclang", "-target-feature", "-Xclang",
                             "-packed-fp32-ops", "-o", exe, src], capture_output=True, text=True)
         if r.returncode:
             raise SystemExit(r.stderr[-2000:])
         r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
         if r.returncode:
-            raise SystemExit(f"readbw probe failed ({r.returncode}): {r.stderr[-500:]}")
-    rows = [json.loads(l) for l in r.stdout.splitlines() if l.startswith("{")]
+            raise SystemExit(f"{name} probe failed ({r.returncode}): {r.stderr[-500:]} {r.stdout[-500:]}")
+    return [json.loads(l) for l in r.stdout.splitlines() if l.startswith("{")]
+
+
+def bench_readbw():
+    """--only readbw: the streaming-read ceiling (the comment block above)."""
+    rows = run_probe("readbw", READBW_SRC)
     best = max(x["gbs"] for x in rows)
     return {"per_grid": rows, "best_gbs": best, "frac_of_vendor_peak": best / HBM_PEAK_GBS}
+
+
+# ------------------------------------------------------------------ handoff cost
+# What it costs to pass data from the work-groups of one kernel to a consumer inside the
+# same launch, against a second launch (bench.py --only handoff).  A producer of 256
+# work-groups (8 groups of 32) each streams 64 KB, reduces it and writes a 2 KB partial;
+# the 32 partials of a group are summed (fixed order) (a) by a second, 8-work-group launch;
+# (b) by the group's last work-group to arrive, the partials stored and loaded as
+# agent-scope relaxed atomics, each thread's stores acknowledged before one relaxed
+# agent-scope ticket per work-group (no fences); (c) as (b) with a release fence before
+# the ticket and an acquire fence in the last work-group.  Nothing waits on another
+# work-group (the last to arrive does the sum), so every form ends; the three outputs are
+# compared.  This is the pattern a fused decoder step would need between its phases.
+HANDOFF_SRC = r'''
+#include <hip/hip_runtime.h>
+#include <cstdio>
+#include <vector>
+constexpr int kG = 8, kC = 32, kP = 512;
+__device__ float part_sum(const float4* __restrict__ src, int wg, int t) {
+    const float4* p = src + (size_t)wg * 4096;
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { const float4 v = p[i * 256 + t]; a += (v.x + v.y) + (v.z + v.w); }
+    return a;
+}
+__device__ void group_sum(const float* part, float* out, int g, int t, bool atomic_loads) {
+    float s0 = 0.f, s1 = 0.f;
+    for (int c = 0; c < kC; ++c) {
+        const float* q = part + (size_t)(g * kC + c) * kP;
+        if (atomic_loads) {
+            s0 += __hip_atomic_load(q + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s1 += __hip_atomic_load(q + 256 + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            s0 += q[t];
+            s1 += q[256 + t];
+        }
+    }
+    out[g * kP + t] = s0;
+    out[g * kP + 256 + t] = s1;
+}
+__global__ __launch_bounds__(256) void k_produce(const float4* src, float* part) {
+    const float a = part_sum(src, blockIdx.x, threadIdx.x);
+    part[(size_t)blockIdx.x * kP + threadIdx.x] = a;
+    part[(size_t)blockIdx.x * kP + 256 + threadIdx.x] = 0.5f * a;
+}
+__global__ __launch_bounds__(256) void k_consume(const float* part, float* out) {
+    group_sum(part, out, blockIdx.x, threadIdx.x, false);
+}
+template <bool kFence>
+__global__ __launch_bounds__(256) void k_fused(const float4* src, float* part, float* out, unsigned* ticket) {
+    const int wg = blockIdx.x, t = threadIdx.x, g = wg / kC;
+    const float a = part_sum(src, wg, t);
+    float* pp = part + (size_t)wg * kP;
+    if (kFence) {
+        pp[t] = a;
+        pp[256 + t] = 0.5f * a;
+    } else {
+        __hip_atomic_store(pp + t, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pp + 256 + t, 0.5f * a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+    __shared__ unsigned last;
+    __syncthreads();
+    if (t == 0) {
+        const unsigned old = kFence
+            ? __hip_atomic_fetch_add(ticket + g, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT)
+            : __hip_atomic_fetch_add(ticket + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = old == kC - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    if (kFence) __atomic_thread_fence(__ATOMIC_ACQUIRE);
+    group_sum(part, out, g, t, !kFence);
+    if (t == 0) ticket[g] = 0u;
+}
+int main() {
+    const int nwg = kG * kC, kSlices = 16;
+    const size_t slice = (size_t)nwg * 4096;                     // float4s per launch (16 MB)
+    float4* src; float* part; float* out; unsigned* ticket;
+    if (hipMalloc(&src, kSlices * slice * sizeof(float4)) != hipSuccess || hipMalloc(&part, (size_t)nwg * kP * 4) != hipSuccess ||
+        hipMalloc(&out, 3 * kG * kP * 4) != hipSuccess || hipMalloc(&ticket, 64) != hipSuccess) return 1;
+    std::vector<float> h(kSlices * slice * 4);
+    for (size_t i = 0; i < h.size(); ++i) h[i] = (float)((i * 2654435761u) % 1000) * 1e-3f;
+    if (hipMemcpy(src, h.data(), h.size() * 4, hipMemcpyHostToDevice) != hipSuccess) return 1;
+    if (hipMemset(ticket, 0, 64) != hipSuccess) return 1;
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return 1;
+    auto run = [&](int form, const float4* s) {
+        if (form == 0) {
+            k_produce<<<nwg, 256>>>(s, part);
+            k_consume<<<kG, 256>>>(part, out);
+        } else if (form == 1) {
+            k_fused<false><<<nwg, 256>>>(s, part, out + kG * kP, ticket);
+        } else if (form == 2) {
+            k_fused<true><<<nwg, 256>>>(s, part, out + 2 * kG * kP, ticket);
+        } else {
+            k_produce<<<nwg, 256>>>(s, part);
+        }
+    };
+    const char* names[4] = {"two launches", "one launch, atomic data, no fences", "one launch, release/acquire fences",
+                            "producer alone"};
+    for (int form = 0; form < 4; ++form) {
+        for (int i = 0; i < 20; ++i) run(form, src + (i % kSlices) * slice);
+        if (hipDeviceSynchronize() != hipSuccess) return 1;
+        const int n = 200;
+        if (hipEventRecord(e0) != hipSuccess) return 1;
+        for (int i = 0; i < n; ++i) run(form, src + (i % kSlices) * slice);
+        if (hipEventRecord(e1) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) return 1;
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return 1;
+        run(form, src);
+        if (hipDeviceSynchronize() != hipSuccess) return 1;
+        printf("{\"form\": \"%s\", \"us\": %.2f}\n", names[form], ms * 1e3f / n);
+    }
+    std::vector<float> r(3 * kG * kP);
+    if (hipMemcpy(r.data(), out, r.size() * 4, hipMemcpyDeviceToHost) != hipSuccess) return 1;
+    int bad = 0;
+    for (int i = 0; i < kG * kP; ++i) bad += (r[i] != r[kG * kP + i]) + (r[i] != r[2 * kG * kP + i]);
+    printf("{\"mismatches\": %d}\n", bad);
+    return bad != 0;
+}
+'''
+
+
+def bench_handoff():
+    """--only handoff: one launch with an in-kernel handoff against two launches (the comment
+    block above)."""
+    rows = run_probe("handoff", HANDOFF_SRC)
+    out = {r["form"]: r["us"] for r in rows if "form" in r}
+    out["mismatches"] = next(r["mismatches"] for r in rows if "mismatches" in r)
+    return out
 
 def cpu_baseline(layer, seconds):
     """The oracle's C restatement (R64 dequant to fp16 + fp32 GEMV, OpenMP) on the host,
@@ -1236,6 +1373,9 @@ def main():
         return
     if args.only == "readbw":
         print(json.dumps({"readbw": bench_readbw()}), flush=True)   # a child process of its own
+        return
+    if args.only == "handoff":
+        print(json.dumps({"handoff": bench_handoff()}), flush=True)
         return
     L.lib()
     dev = torch.device("cuda:0")
