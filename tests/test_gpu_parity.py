@@ -143,7 +143,9 @@ GEMV_CASES = [("cpu_config", 2560, 2560, 0)] + [
     ("odd_N", 1000, 2560, 7), ("tiny", 65, 96, 8), ("ragged_K", 200, 80, 9),
     # n_cb = 512: table inputs beyond the three up-front passes; 64-column panels
     # with 10 rounds: the record-buffer ring
-    ("long_K", 300, 16384, 10), ("wide_N", 20000, 2560, 11)]
+    ("long_K", 300, 16384, 10), ("wide_N", 20000, 2560, 11),
+    # past 65536 columns: 128-column panels (four slices per column), the last one partial
+    ("wide_panels", 70001, 256, 12)]
 
 
 @pytest.mark.parametrize("hdr_bytes", [6, 8])
@@ -196,7 +198,9 @@ def test_gemv_deterministic_and_pool(hiplib, cuda):
 
 GROUP_CASES = [  # name, [N_i], K
     ("qkv", [4096, 1024, 1024], 2560), ("gate_up", [9728, 9728], 2560),
-    ("ragged", [1000, 65, 300, 7], 96), ("long_K", [64, 100], 20512)]
+    ("ragged", [1000, 65, 300, 7], 96), ("long_K", [64, 100], 20512),
+    # 70001 columns in all: a group on 128-column panels, each matrix ending in a partial one
+    ("wide_group", [40000, 30001], 256)]
 
 
 @pytest.mark.parametrize("name,Ns,K", GROUP_CASES)
