@@ -1323,12 +1323,17 @@ def prefill_roofline(pf, lib=None):
     with its Z/pack pass and any split-K sum) and its dominant call, median durations; the
     dominant kernel's MFMA busy % and HBM bytes per launch from the counter passes when the
     source and plan are the ones measured; the same-run library fp16 GEMM (no dequant) over
-    the layer at that M for comparison."""
+    the layer at that M for comparison.  The dominant call is the one with the most flops:
+    gate, up and down tie (and run within a few microseconds of each other, in either order
+    from run to run), so down -- the shape of the counter passes -- is taken; the run's
+    slowest call is reported beside it."""
     if not pf:
         return None
     M = pf["M"]
-    dom = max(pf["per_shape"].items(), key=lambda kv: kv[1]["median_us"])
-    name, q = dom
+    fl = dict((n, N * K) for n, N, K in LAYER)
+    name = max(pf["per_shape"], key=lambda n: (fl[n], n == "down_proj"))
+    q = pf["per_shape"][name]
+    slowest = max(pf["per_shape"].items(), key=lambda kv: kv[1]["median_us"])
     flop = 2.0 * M * dict((n, N * K) for n, N, K in LAYER)[name]
     same = name == "down_proj" and M == 2048 and q["plan"]["tile"] == 512 and os.environ.get("SX8_GEMM_W2") != "0"
     busy, busy_src = measured("prefill_mfma_busy_pct") if same else (None, "measured for down_proj at M = 2048 only")
@@ -1346,6 +1351,7 @@ def prefill_roofline(pf, lib=None):
                      "flop_per_call": flop, "us": q["median_us"], "p10_us": q["p10_us"], "p90_us": q["p90_us"],
                      "achieved": round(q["tflops"], 1), "frac": round(q["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                      "plan": q["plan"]},
+        "slowest": {"shape": slowest[0], "us": slowest[1]["median_us"]},
         "mfma_busy_pct": busy,
         "mfma_busy_source": busy_src,
         "traffic": traffic,
