@@ -1098,7 +1098,10 @@ def bench_readbw():
 # agent-scope ticket per work-group (no fences); (c) as (b) with a release fence before
 # the ticket and an acquire fence in the last work-group.  Nothing waits on another
 # work-group (the last to arrive does the sum), so every form ends; the three outputs are
-# compared.  This is the pattern a fused decoder step would need between its phases.
+# compared.  This is the pattern a fused decoder step would need between its phases.  Form
+# (b) leans on the hardware (a store acknowledged at agent scope is visible to agent-scope
+# loads) rather than on the language's memory model, which asks for (c)'s fences; it is
+# timed as the cheapest handoff there could be, and checked against the other two outputs.
 HANDOFF_SRC = r'''
 #include <hip/hip_runtime.h>
 #include <cstdio>
