@@ -1422,7 +1422,17 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t NB, int64_t n_cb, int64_t part_cap 
             }
         }
     }
-    const Plan p256 = plan_k_gemm(M, N, NB, n_cb, MF, part_cap);
+    Plan p256 = plan_k_gemm(M, N, NB, n_cb, MF, part_cap);
+    // past 128 rows, 128-row tiles only where the 256-row plan leaves more than half the
+    // CUs idle (the cost model prices them too cheaply for fuller grids).  Plan sweep at M =
+    // 512 (every plan of each call, same box): k 1024 x 2560 26.0 us on 128-row tiles in 5
+    // K ranges against 28.8 on 256-row tiles in 7 (112 work-groups); q, o and the q/k/v
+    // group ran 1-5 us slower on 128-row tiles than on their 256-row plans (256, 160, 192
+    // work-groups)
+    if (MF == 2 && p256.G < 128 && tu.tile != 256) {
+        const Plan p128 = plan_k_gemm(M, N, NB, n_cb, 1, part_cap);
+        if (p128.cost < p256.cost) p256 = p128;
+    }
     if (!w1_ok) return p256;
     const Plan p512 = plan_w1(M, NB, n_cb, part_cap);
     const int forced = tu.tile;

@@ -50,8 +50,9 @@ def _check(M, Ns, n_cb, forced=False):
         assert G == (T if S == 1 else Tf + n_split * S), ctx
         part = n_split * (S - 1) * W_ROWS * BN * 4
     else:
-        # 256-row tiles past 128 rows unless a plan is forced
-        assert tile in (128, 256) and (forced or tile == (256 if M > 128 else 128)), ctx
+        # 128-row tiles up to 128 rows; past that 256-row tiles, or 128-row ones when the
+        # 256-row plan would leave more than half the CUs idle (or a plan is forced)
+        assert tile in (128, 256) and (forced or M > 128 or tile == 128), ctx
         assert p["whole_tiles"] == 0 and p["split_tiles"] == 0, ctx
         assert G == _ceil(M, tile) * NB * S, ctx
         part = (S - 1) * M * Ntot * 4
@@ -110,6 +111,8 @@ def test_forced_plan_out_of_range_falls_back(hiplib, gemm_tuning):
     (512, (2560,), 128, (256, 160, 4, 0, 0)),                  # o at M = 512
     (512, (9728, 9728), 80, (512, 152, 1, 0, 0)),              # gate/up group at M = 512
     (512, (2560,), 304, (256, 240, 6, 0, 0)),                  # down at M = 512
+    (512, (1024,), 80, (128, 160, 5, 0, 0)),                   # k, v at M = 512: 128-row tiles
+    (512, (4096,), 80, (256, 256, 4, 0, 0)),                   # q at M = 512
 ])
 def test_layer_plans(hiplib, M, Ns, n_cb, want):
     """The planner's choices for the layer's calls (a change here moves the measured
