@@ -23,6 +23,14 @@ int32_t sx8_dec_add_rmsnorm(float* resid, const float* delta, const uint16_t* in
                             const uint16_t* w, uint16_t* out, int64_t M, int64_t H, float eps,
                             void* stream);
 
+/* sx8_dec_add_rmsnorm where delta is a deferred split-K GEMM output (the *_deferred prefill
+ * calls): each delta element is first summed with its n_parts (0..7) partial slices at
+ * parts + s * slice, in slice order, the sum the GEMM would have written.  delta must be
+ * given when n_parts > 0; parts 4-byte aligned, slice >= M * H. */
+int32_t sx8_dec_add_rmsnorm_parts(float* resid, const float* delta, const uint16_t* init,
+                                  const uint16_t* w, uint16_t* out, int64_t M, int64_t H, float eps,
+                                  const float* parts, int32_t n_parts, int64_t slice, void* stream);
+
 /* One token at position *pos: per query/key head RMSNorm (q_norm/k_norm weights, over hd),
  * fp16 rounding, rotate-half RoPE with cos_t/sin_t rows (L, hd/2) float32; q into q_out
  * (nh*hd fp16), k and v into row *pos of k_cache / v_cache ((nk, L, hd) fp16 each).  A
@@ -43,6 +51,19 @@ int32_t sx8_dec_qk_rope_cache_rows(const float* q_raw, const float* k_raw, const
                                    int64_t rows, uint16_t* q_out, uint16_t* k_cache,
                                    uint16_t* v_cache, int32_t nh, int32_t nk, int32_t hd,
                                    int64_t L, float eps, void* stream);
+
+/* sx8_dec_qk_rope_cache_rows on the deferred output of the q/k/v group GEMM
+ * (sx8_gemm_prefill_group_deferred with matrices q, k, v and M = rows): every value read is
+ * summed with its n_parts (0..7) partial slices first, in slice order (q's block of slice s
+ * at parts + s * slice, k's at + rows*nh*hd, v's at + rows*(nh+nk)*hd).  parts 4-byte
+ * aligned, slice >= rows * (nh + 2 nk) * hd. */
+int32_t sx8_dec_qk_rope_cache_rows_parts(const float* q_raw, const float* k_raw, const float* v_raw,
+                                         const uint16_t* q_norm, const uint16_t* k_norm,
+                                         const float* cos_t, const float* sin_t, const int64_t* pos,
+                                         int64_t rows, uint16_t* q_out, uint16_t* k_cache,
+                                         uint16_t* v_cache, int32_t nh, int32_t nk, int32_t hd,
+                                         int64_t L, float eps, const float* parts, int32_t n_parts,
+                                         int64_t slice, void* stream);
 
 /* Decode attention of one token: for each of nh query heads (kv head = h / (nh/nk)),
  * softmax(scale * q . K[0..*pos]) . V[0..*pos] over the caches written by
@@ -88,6 +109,14 @@ int32_t sx8_dec_gemm_silu(const float* g, const float* u, int64_t M, int64_t K, 
                           const uint8_t* levels, int32_t hdr_bytes, const float* basis,
                           const float* scales, int64_t N, int64_t n_cb, float* Y, void* workspace,
                           int64_t workspace_bytes, void* stream);
+
+/* sx8_dec_gemm_silu with the split-K sum left to the caller, as
+ * sx8_gemm_prefill_group_deferred (one matrix: slice s at parts + s * slice). */
+int32_t sx8_dec_gemm_silu_deferred(const float* g, const float* u, int64_t M, int64_t K,
+                                   const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
+                                   const float* basis, const float* scales, int64_t N, int64_t n_cb,
+                                   float* Y, void* workspace, int64_t workspace_bytes, float** parts,
+                                   int32_t* n_parts, int64_t* slice, void* stream);
 
 /* Causal attention of T prompt rows (prefill): q (T, nh, hd) fp16 (normalized and
  * rotated, as sx8_dec_qk_rope_cache_rows writes it), caches (nk, L, hd) fp16 holding

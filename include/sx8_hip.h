@@ -36,8 +36,10 @@
 extern "C" {
 #endif
 
-/* 3: sx8_dec_gemv_rmsnorm_pair takes the up matrix's pointers; sx8_gemm_reload_tuning */
-#define SX8_ABI_VERSION 3
+/* 3: sx8_dec_gemv_rmsnorm_pair takes the up matrix's pointers; sx8_gemm_reload_tuning.
+ * 4: deferred split-K sums: sx8_gemm_prefill_group_deferred, sx8_dec_gemm_silu_deferred and
+ *    the consumers sx8_dec_add_rmsnorm_parts, sx8_dec_qk_rope_cache_rows_parts */
+#define SX8_ABI_VERSION 4
 
 #define SX8_OK 0
 #define SX8_ERR_INVALID 1      /* bad argument (null pointer, size, hdr_bytes, alignment) */
@@ -248,6 +250,24 @@ int32_t sx8_gemm_prefill_group(const uint16_t* X, int64_t M, int64_t ldx, int64_
                                const float* const* scales, const int64_t* Ns, int64_t n_cb,
                                float* const* Ys, void* workspace, int64_t workspace_bytes,
                                void* stream);
+
+/* sx8_gemm_prefill_group with its split-K sum left to the caller.  When the plan splits K
+ * into S ranges on 128- or 256-row tiles, Ys[i] receive the first range's products only and
+ * the other S - 1 ranges' partial products stay in the workspace: *n_parts = S - 1, *parts =
+ * the first partial slice (a device pointer into the workspace), *slice = floats per slice
+ * (M * sum N_i); matrix i's (M, N_i) block of slice s starts at parts + s * slice +
+ * M * (N_0 + .. + N_{i-1}).  Ys[i] + slice 0 + .. + slice S-2, added in that order, is what
+ * sx8_gemm_prefill_group writes, bit for bit (sx8_dec_add_rmsnorm_parts and
+ * sx8_dec_qk_rope_cache_rows_parts add them where they read Y).  Any other plan sums as
+ * usual and reports *n_parts = 0.  The slices live until the workspace is used again.  No
+ * counterpart in the reference (its prefill GEMM does not split K). */
+int32_t sx8_gemm_prefill_group_deferred(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
+                                        int32_t n_mats, const uint8_t* const* hdrs,
+                                        const uint8_t* const* levels, int32_t hdr_bytes,
+                                        const float* const* bases, const float* const* scales,
+                                        const int64_t* Ns, int64_t n_cb, float* const* Ys,
+                                        void* workspace, int64_t workspace_bytes, float** parts,
+                                        int32_t* n_parts, int64_t* slice, void* stream);
 
 /* Output-side PCA: Y[m, n] += sum_kb c0(kb,n) Z[m,kb,0] + c1(kb,n) Z[m,kb,1], c0/c1 the
  * signed nibbles of the coeff byte in the v4.4 header (float32 FMAs, one thread per

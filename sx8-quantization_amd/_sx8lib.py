@@ -61,16 +61,23 @@ SIGNATURES = [
     ("sx8_gemm_prefill_z", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _P, _I64, _I64, _P, _P, _I64, _P]),
     ("sx8_gemm_prefill_group", _I32,
      [_P, _I64, _I64, _I64, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P, _I64, _P]),
+    ("sx8_gemm_prefill_group_deferred", _I32,
+     [_P, _I64, _I64, _I64, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _P]),
     ("sx8_gemm_pca_z", _I32, [_P, _I64, _P, _I32, _I64, _I64, _P, _P]),
     ("sx8_gemm_prefill_core", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _I64, _I64, _P, _P, _I64, _P]),
     # include/sx8_decoder.h
     ("sx8_dec_add_rmsnorm", _I32, [_P, _P, _P, _P, _P, _I64, _I64, ctypes.c_float, _P]),
+    ("sx8_dec_add_rmsnorm_parts", _I32, [_P, _P, _P, _P, _P, _I64, _I64, ctypes.c_float, _P, _I32, _I64, _P]),
     ("sx8_dec_qk_rope_cache", _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
                                      _I64, ctypes.c_float, _P]),
     ("sx8_dec_qk_rope_cache_rows", _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _I32, _I32,
                                           _I32, _I64, ctypes.c_float, _P]),
+    ("sx8_dec_qk_rope_cache_rows_parts", _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _I32, _I32,
+                                                _I32, _I64, ctypes.c_float, _P, _I32, _I64, _P]),
     ("sx8_dec_attn", _I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I64, ctypes.c_float, _P]),
     ("sx8_dec_gemm_silu", _I32, [_P, _P, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _I64, _P]),
+    ("sx8_dec_gemm_silu_deferred", _I32,
+     [_P, _P, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P, _P]),
     ("sx8_dec_attn_prefill", _I32, [_P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _I64, ctypes.c_float, _P]),
     ("sx8_dec_attn_split", _I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I64, ctypes.c_float, _P, _I64,
                                   _P]),
@@ -91,7 +98,7 @@ SIGNATURES = [
                                          _P, _P, _P, _P]),
     ("sx8_dec_gemv_zp_add", _I32, [_P, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _P]),
 ]
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib = None
 _lock = threading.Lock()

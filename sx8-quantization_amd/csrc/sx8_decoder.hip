@@ -47,12 +47,29 @@ __device__ __forceinline__ float4 h4f(uint2 v) {
                        h2f((uint16_t)(v.y >> 16)));
 }
 
+// NP > 0: delta is the first K range of a split GEMM whose other NP ranges' partial products
+// sit at parts + s * slice (same row-major layout); each element is delta + part 0 + ... +
+// part NP-1 in that order (the split-K sum of the GEMM, bit for bit) before it is added.
+template <int NP = 0>
 __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ resid, const float* __restrict__ delta,
                                                      const uint16_t* __restrict__ init,
                                                      const uint16_t* __restrict__ w,
-                                                     uint16_t* __restrict__ out, int H, float eps, bool vec) {
+                                                     uint16_t* __restrict__ out, int H, float eps, bool vec,
+                                                     const float* __restrict__ parts = nullptr,
+                                                     int64_t slice = 0) {
     __shared__ float red[4];
     const int64_t base = (int64_t)blockIdx.x * H;
+    auto dsum = [&](int64_t e) {         // delta (plus its pending partial sums) at element e
+        float dd = delta[e];
+        if constexpr (NP > 0) {
+            float pv[NP];
+#pragma unroll
+            for (int s2 = 0; s2 < NP; ++s2) pv[s2] = parts[s2 * slice + e];
+#pragma unroll
+            for (int s2 = 0; s2 < NP; ++s2) dd += pv[s2];
+        }
+        return dd;
+    };
     if (vec && H <= 256 * 4 * kRmsPer4) {
         const int H4 = H >> 2;
         float4* r4 = reinterpret_cast<float4*>(resid + base);
@@ -67,7 +84,16 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ resid, 
             const int ic = min(i, H4 - 1);
             float4 x = init ? h4f(i4[ic]) : r4[ic];
             if (delta) {
-                const float4 dd = d4[ic];
+                float4 dd = d4[ic];
+                if constexpr (NP > 0) {
+                    float4 pv[NP];
+#pragma unroll
+                    for (int s2 = 0; s2 < NP; ++s2)
+                        pv[s2] = reinterpret_cast<const float4*>(parts + s2 * slice + base)[ic];
+#pragma unroll
+                    for (int s2 = 0; s2 < NP; ++s2)
+                        dd = make_float4(dd.x + pv[s2].x, dd.y + pv[s2].y, dd.z + pv[s2].z, dd.w + pv[s2].w);
+                }
                 x = make_float4(x.x + dd.x, x.y + dd.y, x.z + dd.z, x.w + dd.w);
             }
             v[u] = i < H4 ? x : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -97,7 +123,7 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ resid, 
             const int i = threadIdx.x + 256 * u;
             const int ic = min(i, H - 1);
             float x = init ? h2f(init[base + ic]) : resid[base + ic];
-            if (delta) x += delta[base + ic];
+            if (delta) x += dsum(base + ic);
             v[u] = i < H ? x : 0.f;
             wv[u] = h2f(w[ic]);
         }
@@ -118,7 +144,7 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ resid, 
     float ss = 0.f;
     for (int i = threadIdx.x; i < H; i += 256) {
         float x = init ? h2f(init[base + i]) : resid[base + i];
-        if (delta) x += delta[base + i];
+        if (delta) x += dsum(base + i);
         resid[base + i] = x;
         ss += x * x;
     }
@@ -135,6 +161,10 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ resid, 
 // thousands of one-wave work-groups that each wait two memory round trips.
 constexpr int kRopeRows = 4;
 
+// NP > 0: q_raw, k_raw, v_raw hold the first K range of a split GEMM whose other NP ranges'
+// partial products sit at q_part / k_part / v_part + s * slice (same layout); every value
+// read is raw + part 0 + ... + part NP-1 in that order (the split-K sum, bit for bit).
+template <int NP = 0>
 __global__ __launch_bounds__(256) void k_qk_rope_cache(const float* __restrict__ q_raw,
                                                        const float* __restrict__ k_raw,
                                                        const float* __restrict__ v_raw,
@@ -146,7 +176,11 @@ __global__ __launch_bounds__(256) void k_qk_rope_cache(const float* __restrict__
                                                        uint16_t* __restrict__ q_out,
                                                        uint16_t* __restrict__ k_cache,
                                                        uint16_t* __restrict__ v_cache, int nh,
-                                                       int nk, int hd, int L, float eps, int rows) {
+                                                       int nk, int hd, int L, float eps, int rows,
+                                                       const float* __restrict__ q_part = nullptr,
+                                                       const float* __restrict__ k_part = nullptr,
+                                                       const float* __restrict__ v_part = nullptr,
+                                                       int64_t slice = 0) {
     __shared__ float red[kRopeRows][4][2];
     const int half = hd >> 1;
     const int tph = hd > 128 ? 128 : 64;
@@ -159,17 +193,44 @@ __global__ __launch_bounds__(256) void k_qk_rope_cache(const float* __restrict__
     const bool act = is_qk && d < half;
     const int y0 = (int)blockIdx.y * kRopeRows;
     const int64_t pos0 = *pos_p;
-    // (1) every row's q/k pair (and its value-head elements) requested together
+    // (1) every row's q/k pair (and its value-head elements) requested together, with the
+    // pending partial sums of each value (NP > 0) behind them
     float x1[kRopeRows], x2[kRopeRows], va[kRopeRows], vb[kRopeRows];
+    constexpr int kP = NP > 0 ? NP : 1;
+    float p1[kRopeRows][kP], p2[kRopeRows][kP], pa[kRopeRows][kP], pb[kRopeRows][kP];
 #pragma unroll
     for (int r = 0; r < kRopeRows; ++r) {
         const int y = min(y0 + r, rows - 1);
-        const float* src = (is_q ? q_raw + (int64_t)y * nh * hd : k_raw + (int64_t)y * nk * hd) + h * hd;
+        const int64_t qko = (is_q ? (int64_t)y * nh * hd : (int64_t)y * nk * hd) + h * hd;
+        const float* src = (is_q ? q_raw : k_raw) + qko;
         x1[r] = act ? src[d] : 0.f;
         x2[r] = act ? src[d + half] : 0.f;
-        const float* vs = v_raw + (int64_t)y * nk * hd + h * hd;
+        const int64_t vo = (int64_t)y * nk * hd + h * hd;
+        const float* vs = v_raw + vo;
         va[r] = is_v && d < hd ? vs[d] : 0.f;
         vb[r] = is_v && d + tph < hd ? vs[d + tph] : 0.f;
+        if constexpr (NP > 0) {
+            const float* ps = (is_q ? q_part : k_part) + qko;
+            const float* pv = v_part + vo;
+#pragma unroll
+            for (int s2 = 0; s2 < NP; ++s2) {
+                p1[r][s2] = act ? ps[s2 * slice + d] : 0.f;
+                p2[r][s2] = act ? ps[s2 * slice + d + half] : 0.f;
+                pa[r][s2] = is_v && d < hd ? pv[s2 * slice + d] : 0.f;
+                pb[r][s2] = is_v && d + tph < hd ? pv[s2 * slice + d + tph] : 0.f;
+            }
+        }
+    }
+    if constexpr (NP > 0) {
+#pragma unroll
+        for (int r = 0; r < kRopeRows; ++r)
+#pragma unroll
+            for (int s2 = 0; s2 < NP; ++s2) {
+                x1[r] += p1[r][s2];
+                x2[r] += p2[r][s2];
+                va[r] += pa[r][s2];
+                vb[r] += pb[r][s2];
+            }
     }
     // (2) per row: RMSNorm, RoPE at *pos + y, stores (rows outside the cache write nothing)
 #pragma unroll
@@ -181,7 +242,15 @@ __global__ __launch_bounds__(256) void k_qk_rope_cache(const float* __restrict__
             uint16_t* vd = v_cache + ((int64_t)h * L + pos) * hd;
             if (d < hd) vd[d] = f2h(va[r]);
             if (d + tph < hd) vd[d + tph] = f2h(vb[r]);
-            for (int e = d + 2 * tph; e < hd; e += tph) vd[e] = f2h(v_raw[(int64_t)y * nk * hd + h * hd + e]);
+            for (int e = d + 2 * tph; e < hd; e += tph) {
+                const int64_t vo = (int64_t)y * nk * hd + h * hd + e;
+                float ve = v_raw[vo];
+                if constexpr (NP > 0) {
+#pragma unroll
+                    for (int s2 = 0; s2 < NP; ++s2) ve += v_part[s2 * slice + vo];
+                }
+                vd[e] = f2h(ve);
+            }
         }
         float ss = x1[r] * x1[r] + x2[r] * x2[r];
 #pragma unroll
@@ -1001,18 +1070,72 @@ __global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* _
         }
 }
 
+namespace {
+
+// Checks of the pending split-K sums a *_parts entry point takes: n_parts in 0 ..
+// kMaxPendingParts, and with n_parts > 0 a 4-byte aligned parts pointer and a slice that
+// covers `need` floats.
+constexpr int kMaxPendingParts = 7;
+
+int32_t check_parts(const char* what, const float* parts, int32_t n_parts, int64_t slice, int64_t need) {
+    using namespace sx8;
+    if (n_parts < 0 || n_parts > kMaxPendingParts)
+        return fail(SX8_ERR_INVALID, "%s: n_parts must be 0..%d, got %d", what, kMaxPendingParts, n_parts);
+    if (n_parts > 0 && (!parts || !aligned(parts, 4) || slice < need))
+        return fail(SX8_ERR_INVALID, "%s: parts must be a 4-byte aligned pointer and slice >= %lld floats",
+                    what, (long long)need);
+    return SX8_OK;
+}
+
+// f(std::integral_constant<int, np>) for np = 0 .. kMaxPendingParts
+template <class F>
+void by_parts(int np, F&& f) {
+    switch (np) {
+        case 0: f(std::integral_constant<int, 0>{}); break;
+        case 1: f(std::integral_constant<int, 1>{}); break;
+        case 2: f(std::integral_constant<int, 2>{}); break;
+        case 3: f(std::integral_constant<int, 3>{}); break;
+        case 4: f(std::integral_constant<int, 4>{}); break;
+        case 5: f(std::integral_constant<int, 5>{}); break;
+        case 6: f(std::integral_constant<int, 6>{}); break;
+        default: f(std::integral_constant<int, 7>{}); break;
+    }
+}
+
+int32_t add_rmsnorm_impl(const char* what, float* resid, const float* delta, const uint16_t* init,
+                         const uint16_t* w, uint16_t* out, int64_t M, int64_t H, float eps,
+                         const float* parts, int32_t n_parts, int64_t slice, void* stream) {
+    using namespace sx8;
+    if (!resid || !w || !out) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (M <= 0 || H <= 0 || M > 0x7FFFFFFF || H > 0x7FFFFFFF) return fail(SX8_ERR_INVALID, "%s: bad shape", what);
+    if (n_parts > 0 && !delta) return fail(SX8_ERR_INVALID, "%s: partial sums need delta", what);
+    const int32_t rc = check_parts(what, parts, n_parts, slice, M * H);
+    if (rc != SX8_OK) return rc;
+    const bool vec = H % 4 == 0 && aligned(resid, 16) && (!delta || aligned(delta, 16)) &&
+                     (!init || aligned(init, 8)) && aligned(w, 8) && aligned(out, 8) &&
+                     (n_parts == 0 || (aligned(parts, 16) && slice % 4 == 0));
+    by_parts(n_parts, [&](auto np) {
+        hipLaunchKernelGGL((k_add_rmsnorm<decltype(np)::value>), dim3((unsigned)M), dim3(256), 0,
+                           as_stream(stream), resid, delta, init, w, out, (int)H, eps, vec, parts, slice);
+    });
+    return check_launch(what);
+}
+
+}  // namespace
+
 extern "C" int32_t sx8_dec_add_rmsnorm(float* resid, const float* delta, const uint16_t* init,
                                        const uint16_t* w, uint16_t* out, int64_t M, int64_t H,
                                        float eps, void* stream) {
-    using namespace sx8;
-    if (!resid || !w || !out) return fail(SX8_ERR_INVALID, "sx8_dec_add_rmsnorm: null pointer");
-    if (M <= 0 || H <= 0 || M > 0x7FFFFFFF || H > 0x7FFFFFFF)
-        return fail(SX8_ERR_INVALID, "sx8_dec_add_rmsnorm: bad shape");
-    const bool vec = H % 4 == 0 && aligned(resid, 16) && (!delta || aligned(delta, 16)) &&
-                     (!init || aligned(init, 8)) && aligned(w, 8) && aligned(out, 8);
-    hipLaunchKernelGGL(k_add_rmsnorm, dim3((unsigned)M), dim3(256), 0, as_stream(stream), resid, delta,
-                       init, w, out, (int)H, eps, vec);
-    return check_launch("sx8_dec_add_rmsnorm");
+    return add_rmsnorm_impl("sx8_dec_add_rmsnorm", resid, delta, init, w, out, M, H, eps, nullptr, 0, 0,
+                            stream);
+}
+
+extern "C" int32_t sx8_dec_add_rmsnorm_parts(float* resid, const float* delta, const uint16_t* init,
+                                             const uint16_t* w, uint16_t* out, int64_t M, int64_t H,
+                                             float eps, const float* parts, int32_t n_parts, int64_t slice,
+                                             void* stream) {
+    return add_rmsnorm_impl("sx8_dec_add_rmsnorm_parts", resid, delta, init, w, out, M, H, eps, parts, n_parts,
+                            slice, stream);
 }
 
 extern "C" int32_t sx8_dec_qk_rope_cache(const float* q_raw, const float* k_raw, const float* v_raw,
@@ -1028,11 +1151,44 @@ extern "C" int32_t sx8_dec_qk_rope_cache(const float* q_raw, const float* k_raw,
     if (nh <= 0 || nk <= 0 || nh % nk || hd <= 0 || (hd & 1) || hd > 256 || L <= 0 || L > 0x7FFFFFFF)
         return fail(SX8_ERR_INVALID, "sx8_dec_qk_rope_cache: bad shape (hd even, <= 256)");
     const unsigned hpb = hd > 128 ? 2u : 4u;     // heads per 256-thread block
-    hipLaunchKernelGGL(k_qk_rope_cache, dim3(((unsigned)(nh + 2 * nk) + hpb - 1) / hpb), dim3(256), 0,
+    hipLaunchKernelGGL(k_qk_rope_cache<0>, dim3(((unsigned)(nh + 2 * nk) + hpb - 1) / hpb), dim3(256), 0,
                        as_stream(stream), q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, pos,
                        q_out, k_cache, v_cache, nh, nk, hd, (int)L, eps, 1);
     return check_launch("sx8_dec_qk_rope_cache");
 }
+
+namespace {
+
+int32_t rope_rows_impl(const char* what, const float* q_raw, const float* k_raw, const float* v_raw,
+                       const uint16_t* q_norm, const uint16_t* k_norm, const float* cos_t, const float* sin_t,
+                       const int64_t* pos, int64_t rows, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+                       int32_t nh, int32_t nk, int32_t hd, int64_t L, float eps, const float* parts,
+                       int32_t n_parts, int64_t slice, void* stream) {
+    using namespace sx8;
+    if (!q_raw || !k_raw || !v_raw || !q_norm || !k_norm || !cos_t || !sin_t || !pos || !q_out ||
+        !k_cache || !v_cache)
+        return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (nh <= 0 || nk <= 0 || nh % nk || hd <= 0 || (hd & 1) || hd > 256 || L <= 0 || L > 0x7FFFFFFF ||
+        rows <= 0 || rows > 65535)
+        return fail(SX8_ERR_INVALID, "%s: bad shape (hd even, <= 256, rows 1..65535)", what);
+    // the q/k/v group's partial slices: q block first, then k, then v (rows x width each)
+    const int64_t qn = rows * nh * hd, kvn = rows * nk * hd;
+    const int32_t rc = check_parts(what, parts, n_parts, slice, qn + 2 * kvn);
+    if (rc != SX8_OK) return rc;
+    const float* qp = n_parts ? parts : nullptr;
+    const float* kp = n_parts ? parts + qn : nullptr;
+    const float* vp = n_parts ? parts + qn + kvn : nullptr;
+    const unsigned hpb = hd > 128 ? 2u : 4u;     // heads per 256-thread block
+    const unsigned yb = (unsigned)((rows + kRopeRows - 1) / kRopeRows);
+    by_parts(n_parts, [&](auto np) {
+        hipLaunchKernelGGL((k_qk_rope_cache<decltype(np)::value>), dim3(((unsigned)(nh + 2 * nk) + hpb - 1) / hpb, yb),
+                           dim3(256), 0, as_stream(stream), q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t,
+                           pos, q_out, k_cache, v_cache, nh, nk, hd, (int)L, eps, (int)rows, qp, kp, vp, slice);
+    });
+    return check_launch(what);
+}
+
+}  // namespace
 
 extern "C" int32_t sx8_dec_qk_rope_cache_rows(const float* q_raw, const float* k_raw, const float* v_raw,
                                               const uint16_t* q_norm, const uint16_t* k_norm,
@@ -1040,19 +1196,19 @@ extern "C" int32_t sx8_dec_qk_rope_cache_rows(const float* q_raw, const float* k
                                               int64_t rows, uint16_t* q_out, uint16_t* k_cache,
                                               uint16_t* v_cache, int32_t nh, int32_t nk, int32_t hd,
                                               int64_t L, float eps, void* stream) {
-    using namespace sx8;
-    if (!q_raw || !k_raw || !v_raw || !q_norm || !k_norm || !cos_t || !sin_t || !pos || !q_out ||
-        !k_cache || !v_cache)
-        return fail(SX8_ERR_INVALID, "sx8_dec_qk_rope_cache_rows: null pointer");
-    if (nh <= 0 || nk <= 0 || nh % nk || hd <= 0 || (hd & 1) || hd > 256 || L <= 0 || L > 0x7FFFFFFF ||
-        rows <= 0 || rows > 65535)
-        return fail(SX8_ERR_INVALID, "sx8_dec_qk_rope_cache_rows: bad shape (hd even, <= 256, rows 1..65535)");
-    const unsigned hpb = hd > 128 ? 2u : 4u;     // heads per 256-thread block
-    const unsigned yb = (unsigned)((rows + kRopeRows - 1) / kRopeRows);
-    hipLaunchKernelGGL(k_qk_rope_cache, dim3(((unsigned)(nh + 2 * nk) + hpb - 1) / hpb, yb), dim3(256),
-                       0, as_stream(stream), q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, pos,
-                       q_out, k_cache, v_cache, nh, nk, hd, (int)L, eps, (int)rows);
-    return check_launch("sx8_dec_qk_rope_cache_rows");
+    return rope_rows_impl("sx8_dec_qk_rope_cache_rows", q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, pos,
+                          rows, q_out, k_cache, v_cache, nh, nk, hd, L, eps, nullptr, 0, 0, stream);
+}
+
+extern "C" int32_t sx8_dec_qk_rope_cache_rows_parts(const float* q_raw, const float* k_raw, const float* v_raw,
+                                                    const uint16_t* q_norm, const uint16_t* k_norm,
+                                                    const float* cos_t, const float* sin_t, const int64_t* pos,
+                                                    int64_t rows, uint16_t* q_out, uint16_t* k_cache,
+                                                    uint16_t* v_cache, int32_t nh, int32_t nk, int32_t hd,
+                                                    int64_t L, float eps, const float* parts, int32_t n_parts,
+                                                    int64_t slice, void* stream) {
+    return rope_rows_impl("sx8_dec_qk_rope_cache_rows_parts", q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t,
+                          pos, rows, q_out, k_cache, v_cache, nh, nk, hd, L, eps, parts, n_parts, slice, stream);
 }
 
 extern "C" int32_t sx8_dec_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,

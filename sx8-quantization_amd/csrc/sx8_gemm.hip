@@ -1504,14 +1504,23 @@ bool group_width(int n_mats, const int64_t* Ns, int64_t& Ntot, int64_t& NB) {
 // matrix's Zhl operand) followed by the split-K partials; run the GEMM and, for a split
 // plan, the fixed-order partial sums.  Nothing is allocated and nothing synchronizes: the
 // call only enqueues kernels on `st`.
+// Split-K sums a caller takes over (the *_deferred entry points): the plan's S - 1 partial
+// slices in the workspace, slice s of matrix i at part + s * slice + M * (N_0 + .. + N_{i-1}).
+struct PendingSums {
+    float* part;
+    int np;
+    int64_t slice;
+};
+
 template <bool kSplit>
 int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, int64_t K, int n_mats,
                  const WeightSrc* ws_in, int32_t hdr_bytes, ZMode zm, const float* const* bases,
                  const float* const* scales, const float* Z, const int64_t* Ns, int64_t n_cb,
                  float* const* Ys, void* workspace, int64_t workspace_bytes, hipStream_t st,
                  const float* silu_g = nullptr, const float* silu_u = nullptr,
-                 int64_t part_cap = INT64_MAX) {
+                 int64_t part_cap = INT64_MAX, PendingSums* defer = nullptr) {
     using namespace sx8;
+    if (defer) *defer = PendingSums{nullptr, 0, 0};
     int64_t Ntot = 0, NB = 0;
     if (!group_width(n_mats, Ns, Ntot, NB)) return fail(SX8_ERR_UNSUPPORTED, "%s: group too wide", what);
     const Plan p = plan_gemm(M, Ntot, NB, n_cb, part_cap);
@@ -1590,6 +1599,9 @@ int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, in
             hipLaunchKernelGGL((k_reduce_tiles<decltype(np)::value>), dim3((unsigned)((n4 + 255) / 256)),
                                dim3(256), 0, st, g, part, (int)M, p.Tf, (int)p.n_split);
         });
+    } else if (!p.w1 && p.S > 1 && defer) {
+        // the caller adds the slices (in slice order, as k_reduce does) where it reads Y
+        *defer = PendingSums{part, p.S - 1, M * Ntot};
     } else if (!p.w1 && p.S > 1) {
         bool vec = true;
         for (int i = 0; i < n_mats; ++i) vec = vec && aligned(Ys[i], 16) && (M * Ns[i]) % 4 == 0;
@@ -1746,25 +1758,62 @@ extern "C" int32_t sx8_gemm_prefill_static(const uint16_t* X, int64_t M, int64_t
                            kScratchBytes - fixed);
 }
 
-extern "C" int32_t sx8_dec_gemm_silu(const float* g, const float* u, int64_t M, int64_t K,
-                                     const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
-                                     const float* basis, const float* scales, int64_t N, int64_t n_cb,
-                                     float* Y, void* workspace, int64_t workspace_bytes, void* stream) {
+namespace {
+
+// Hands the pending sums to the caller's out-parameters (all three must be given).
+int32_t report_pending(const char* what, const PendingSums& pend, float** parts, int32_t* n_parts,
+                       int64_t* slice) {
+    *parts = pend.part;
+    *n_parts = pend.np;
+    *slice = pend.slice;
+    return sx8::check_launch(what);
+}
+
+int32_t gemm_silu_impl(const char* what, const float* g, const float* u, int64_t M, int64_t K,
+                       const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes, const float* basis,
+                       const float* scales, int64_t N, int64_t n_cb, float* Y, void* workspace,
+                       int64_t workspace_bytes, void* stream, PendingSums* defer) {
     using namespace sx8;
     if (!g || !u || !hdr || !levels || !basis || !scales || !Y)
-        return fail(SX8_ERR_INVALID, "sx8_dec_gemm_silu: null pointer");
+        return fail(SX8_ERR_INVALID, "%s: null pointer", what);
     if (hdr_bytes != 6 && hdr_bytes != 8)
-        return fail(SX8_ERR_INVALID, "sx8_dec_gemm_silu: hdr_bytes must be 6 or 8, got %d", hdr_bytes);
+        return fail(SX8_ERR_INVALID, "%s: hdr_bytes must be 6 or 8, got %d", what, hdr_bytes);
     if (!aligned(hdr, hdr_bytes == 8 ? 8 : 2) || !aligned(levels, 8) || !aligned(g, 4) || !aligned(u, 4) ||
         !aligned(Y, 4) || !aligned(basis, 16) || !aligned(scales, 8))
-        return fail(SX8_ERR_INVALID, "sx8_dec_gemm_silu: misaligned pointer");
-    const int32_t rc = check_shape("sx8_dec_gemm_silu", M, K, K, N, n_cb);
+        return fail(SX8_ERR_INVALID, "%s: misaligned pointer", what);
+    const int32_t rc = check_shape(what, M, K, K, N, n_cb);
     if (rc != SX8_OK) return rc;
     WeightSrc w{};
     w.hdr = hdr;
     w.levels = levels;
-    return run_gemm<false>("sx8_dec_gemm_silu", nullptr, M, K, K, 1, &w, hdr_bytes, ZMode::kBasis, &basis,
-                           &scales, nullptr, &N, n_cb, &Y, workspace, workspace_bytes, as_stream(stream), g, u);
+    return run_gemm<false>(what, nullptr, M, K, K, 1, &w, hdr_bytes, ZMode::kBasis, &basis, &scales, nullptr,
+                           &N, n_cb, &Y, workspace, workspace_bytes, as_stream(stream), g, u, INT64_MAX, defer);
+}
+
+}  // namespace
+
+extern "C" int32_t sx8_dec_gemm_silu(const float* g, const float* u, int64_t M, int64_t K,
+                                     const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
+                                     const float* basis, const float* scales, int64_t N, int64_t n_cb,
+                                     float* Y, void* workspace, int64_t workspace_bytes, void* stream) {
+    return gemm_silu_impl("sx8_dec_gemm_silu", g, u, M, K, hdr, levels, hdr_bytes, basis, scales, N, n_cb, Y,
+                          workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int32_t sx8_dec_gemm_silu_deferred(const float* g, const float* u, int64_t M, int64_t K,
+                                              const uint8_t* hdr, const uint8_t* levels, int32_t hdr_bytes,
+                                              const float* basis, const float* scales, int64_t N,
+                                              int64_t n_cb, float* Y, void* workspace,
+                                              int64_t workspace_bytes, float** parts, int32_t* n_parts,
+                                              int64_t* slice, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_dec_gemm_silu_deferred";
+    if (!parts || !n_parts || !slice) return fail(SX8_ERR_INVALID, "%s: null out-parameter", what);
+    PendingSums pend{};
+    const int32_t rc = gemm_silu_impl(what, g, u, M, K, hdr, levels, hdr_bytes, basis, scales, N, n_cb, Y,
+                                      workspace, workspace_bytes, stream, &pend);
+    if (rc != SX8_OK) return rc;
+    return report_pending(what, pend, parts, n_parts, slice);
 }
 
 extern "C" int32_t sx8_gemm_prefill_split(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
@@ -1834,14 +1883,14 @@ extern "C" int32_t sx8_gemm_prefill_core(const uint16_t* X, int64_t M, int64_t l
                            as_stream(stream));
 }
 
-extern "C" int32_t sx8_gemm_prefill_group(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
-                                          int32_t n_mats, const uint8_t* const* hdrs,
-                                          const uint8_t* const* levels, int32_t hdr_bytes,
-                                          const float* const* bases, const float* const* scales,
-                                          const int64_t* Ns, int64_t n_cb, float* const* Ys,
-                                          void* workspace, int64_t workspace_bytes, void* stream) {
+namespace {
+
+int32_t group_impl(const char* what, const uint16_t* X, int64_t M, int64_t ldx, int64_t K, int32_t n_mats,
+                   const uint8_t* const* hdrs, const uint8_t* const* levels, int32_t hdr_bytes,
+                   const float* const* bases, const float* const* scales, const int64_t* Ns, int64_t n_cb,
+                   float* const* Ys, void* workspace, int64_t workspace_bytes, void* stream,
+                   PendingSums* defer) {
     using namespace sx8;
-    const char* what = "sx8_gemm_prefill_group";
     if (!X || !hdrs || !levels || !bases || !scales || !Ns || !Ys) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
     if (n_mats < 1 || n_mats > kMaxGemmGroup)
         return fail(SX8_ERR_INVALID, "%s: n_mats must be 1..%d, got %d", what, kMaxGemmGroup, n_mats);
@@ -1861,7 +1910,37 @@ extern "C" int32_t sx8_gemm_prefill_group(const uint16_t* X, int64_t M, int64_t 
         w[i].levels = levels[i];
     }
     return run_gemm<false>(what, X, M, ldx, K, n_mats, w, hdr_bytes, ZMode::kBasis, bases, scales, nullptr,
-                           Ns, n_cb, Ys, workspace, workspace_bytes, as_stream(stream));
+                           Ns, n_cb, Ys, workspace, workspace_bytes, as_stream(stream), nullptr, nullptr,
+                           INT64_MAX, defer);
+}
+
+}  // namespace
+
+extern "C" int32_t sx8_gemm_prefill_group(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
+                                          int32_t n_mats, const uint8_t* const* hdrs,
+                                          const uint8_t* const* levels, int32_t hdr_bytes,
+                                          const float* const* bases, const float* const* scales,
+                                          const int64_t* Ns, int64_t n_cb, float* const* Ys,
+                                          void* workspace, int64_t workspace_bytes, void* stream) {
+    return group_impl("sx8_gemm_prefill_group", X, M, ldx, K, n_mats, hdrs, levels, hdr_bytes, bases, scales,
+                      Ns, n_cb, Ys, workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int32_t sx8_gemm_prefill_group_deferred(const uint16_t* X, int64_t M, int64_t ldx, int64_t K,
+                                                   int32_t n_mats, const uint8_t* const* hdrs,
+                                                   const uint8_t* const* levels, int32_t hdr_bytes,
+                                                   const float* const* bases, const float* const* scales,
+                                                   const int64_t* Ns, int64_t n_cb, float* const* Ys,
+                                                   void* workspace, int64_t workspace_bytes, float** parts,
+                                                   int32_t* n_parts, int64_t* slice, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_gemm_prefill_group_deferred";
+    if (!parts || !n_parts || !slice) return fail(SX8_ERR_INVALID, "%s: null out-parameter", what);
+    PendingSums pend{};
+    const int32_t rc = group_impl(what, X, M, ldx, K, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb,
+                                  Ys, workspace, workspace_bytes, stream, &pend);
+    if (rc != SX8_OK) return rc;
+    return report_pending(what, pend, parts, n_parts, slice);
 }
 
 extern "C" int32_t sx8_gemm_pca_z(const float* Z, int64_t M, const uint8_t* hdr, int32_t hdr_bytes,

@@ -199,7 +199,8 @@ class SX8Decoder(nn.Module):
                                     ((ly0.down.out_f,), ly0.down.qt["n_cb"])))
         pb["ws"] = torch.empty(need, dtype=torch.uint8, device=dev)
         pb["groups"] = [(self._group_args((ly.q, ly.k, ly.v), (pb["q"], pb["k"], pb["v"])),
-                         self._group_args((ly.gate, ly.up), (pb["g"], pb["u"]))) for ly in self.layers]
+                         self._group_args((ly.gate, ly.up), (pb["g"], pb["u"])),
+                         self._group_args((ly.o,), (pb["o"],))) for ly in self.layers]
         self._pb = pb
         return pb
 
@@ -210,6 +211,19 @@ class SX8Decoder(nn.Module):
         M, K = X.shape
         _L.call("sx8_gemm_prefill_group", _L.ptr(X), M, K, K, n, hdrs, lvls, 6, bas, sca, ns, n_cb, ys,
                 _L.ptr(ws), ws.numel(), st)
+
+    @staticmethod
+    def _gemm_group_deferred(args, X, ws, st):
+        """_gemm_group with the split-K sum left to the consumer
+        (sx8_gemm_prefill_group_deferred): returns (parts, n_parts, slice), n_parts = 0 when
+        the outputs are complete."""
+        n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
+        M, K = X.shape
+        parts, n_parts, slc = ctypes.c_void_p(), ctypes.c_int32(), ctypes.c_int64()
+        _L.call("sx8_gemm_prefill_group_deferred", _L.ptr(X), M, K, K, n, hdrs, lvls, 6, bas, sca, ns, n_cb, ys,
+                _L.ptr(ws), ws.numel(), ctypes.addressof(parts), ctypes.addressof(n_parts), ctypes.addressof(slc),
+                st)
+        return parts.value, n_parts.value, slc.value
 
     @staticmethod
     def _gemm(lin, X, Y, ws, st):
@@ -225,8 +239,10 @@ class SX8Decoder(nn.Module):
         (sx8_dec_add_rmsnorm, M = T), the prefill GEMMs into preallocated buffers, q/k
         norm + RoPE + KV-cache write (sx8_dec_qk_rope_cache_rows), causal attention over
         the cache rows (sx8_dec_attn_prefill), SiLU * up inside the down GEMM
-        (sx8_dec_gemm_silu) and the final norm inside the lm_head GEMV.  The residual
-        stream is float32.  Returns the next token (1,); generation only needs the last
+        (sx8_dec_gemm_silu) and the final norm inside the lm_head GEMV.  The split-K sums
+        of the q/k/v, o and down GEMMs (all but the last layer's) are added by the kernels
+        that read those outputs (the *_deferred GEMM calls and the *_parts consumers), the
+        same sums in the same order.  The residual stream is float32.  Returns the next token (1,); generation only needs the last
         row's logits, so that is all the lm_head computes.  all_logits=True instead runs
         the final norm over every row and the lm_head as a prefill GEMM (M = T), as a
         Hugging Face forward does (scripts/integrate_fused_v44.py:119-167 compares those
@@ -238,26 +254,40 @@ class SX8Decoder(nn.Module):
         st = _L.stream(self.device)
         P = _L.ptr
         emb = self.embed(ids)                                      # (T, H) fp16
+        # split-K sums are left to the kernel that reads the GEMM output (the *_deferred
+        # calls and the *_parts consumers; the same sums in the same order): q/k/v into the
+        # RoPE pass, o into the second add + RMSNorm, down into the next layer's first
+        pend = (None, 0, 0)                                        # down's, for the next layer
+        last = len(self.layers) - 1
         for li, ly in enumerate(self.layers):
             if li == 0:
                 _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), None, P(emb), P(ly.in_norm), P(pb["h"]), T, H,
                         eps, st)
             else:
-                _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["d"]), None, P(ly.in_norm), P(pb["h"]), T,
-                        H, eps, st)
-            self._gemm_group(pb["groups"][li][0], pb["h"], pb["ws"], st)      # q, k, v: one call
-            _L.call("sx8_dec_qk_rope_cache_rows", P(pb["q"]), P(pb["k"]), P(pb["v"]), P(ly.q_norm),
+                _L.call("sx8_dec_add_rmsnorm_parts", P(pb["resid"]), P(pb["d"]), None, P(ly.in_norm), P(pb["h"]),
+                        T, H, eps, pend[0], pend[1], pend[2], st)
+            qp = self._gemm_group_deferred(pb["groups"][li][0], pb["h"], pb["ws"], st)     # q, k, v
+            _L.call("sx8_dec_qk_rope_cache_rows_parts", P(pb["q"]), P(pb["k"]), P(pb["v"]), P(ly.q_norm),
                     P(ly.k_norm), P(self.cos), P(self.sin), P(pb["pos0"]), T, P(pb["qh"]),
-                    P(self.k_cache[li]), P(self.v_cache[li]), nh, nk, hd, self.max_len, eps, st)
+                    P(self.k_cache[li]), P(self.v_cache[li]), nh, nk, hd, self.max_len, eps, qp[0], qp[1], qp[2],
+                    st)
             _L.call("sx8_dec_attn_prefill", P(pb["qh"]), P(self.k_cache[li]), P(self.v_cache[li]), P(pb["a"]),
                     T, 0, nh, nk, hd, self.max_len, 1.0 / math.sqrt(hd), st)
-            self._gemm(ly.o, pb["a"], pb["o"], pb["ws"], st)
-            _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["o"]), None, P(ly.post_norm), P(pb["h"]), T,
-                    H, eps, st)
+            op = self._gemm_group_deferred(pb["groups"][li][2], pb["a"], pb["ws"], st)     # o
+            _L.call("sx8_dec_add_rmsnorm_parts", P(pb["resid"]), P(pb["o"]), None, P(ly.post_norm), P(pb["h"]), T,
+                    H, eps, op[0], op[1], op[2], st)
             self._gemm_group(pb["groups"][li][1], pb["h"], pb["ws"], st)      # gate, up: one call
             hdr, lvl, bas, sca = ly.down._t44                       # SiLU * up inside the down GEMM
-            _L.call("sx8_dec_gemm_silu", P(pb["g"]), P(pb["u"]), T, cfg["inter"], P(hdr), P(lvl), 6, P(bas),
-                    P(sca), ly.down.out_f, ly.down.qt["n_cb"], P(pb["d"]), P(pb["ws"]), pb["ws"].numel(), st)
+            args = (P(pb["g"]), P(pb["u"]), T, cfg["inter"], P(hdr), P(lvl), 6, P(bas), P(sca), ly.down.out_f,
+                    ly.down.qt["n_cb"], P(pb["d"]), P(pb["ws"]), pb["ws"].numel())
+            if li < last:
+                parts, n_parts, slc = ctypes.c_void_p(), ctypes.c_int32(), ctypes.c_int64()
+                _L.call("sx8_dec_gemm_silu_deferred", *args, ctypes.addressof(parts), ctypes.addressof(n_parts),
+                        ctypes.addressof(slc), st)
+                pend = (parts.value, n_parts.value, slc.value)
+            else:
+                # the last layer's output feeds the final norm and the lm_head whole
+                _L.call("sx8_dec_gemm_silu", *args, st)
         if all_logits:
             # every row: residual + down output, final norm, lm_head GEMM over T rows
             _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["d"]), None, P(self.final_norm), P(pb["h"]),

@@ -176,3 +176,42 @@ def test_decoder_pair_and_residual_refusals_on_host(hiplib):
     for adds in (P2((5 << 20) + 32, 7 << 20), P2(7 << 20, 5 << 20)):
         assert L.sx8_dec_gemv_add(p, 2, ptrs, ptrs, 6, ptrs, ptrs, ns, 80, adds, ys, NULL) == 1
         assert "overlaps" in _err(L)
+
+
+def test_deferred_sum_refusals_on_host(hiplib):
+    """The deferred-sum entry points refuse bad arguments before any launch: missing
+    out-parameters, a partial count outside 0..7, partial sums without delta or parts, a
+    slice shorter than the rows it must cover, misaligned parts."""
+    L = hiplib
+    V = ctypes.c_void_p
+    p = V(1 << 24)
+    M, H = 512, 2560
+    # out-parameters of the deferred GEMMs
+    P1 = ctypes.c_void_p * 1
+    ns = (ctypes.c_int64 * 1)(2560)
+    ptrs = P1(1 << 20)
+    assert L.sx8_gemm_prefill_group_deferred(p, M, 4096, 4096, 1, ptrs, ptrs, 6, ptrs, ptrs, ns, 128, ptrs,
+                                             p, 1 << 30, NULL, NULL, NULL, NULL) == 1
+    assert "out-parameter" in _err(L)
+    assert L.sx8_dec_gemm_silu_deferred(p, p, M, 9728, p, p, 6, p, p, 2560, 304, p, p, 1 << 30,
+                                        NULL, NULL, NULL, NULL) == 1
+    assert "out-parameter" in _err(L)
+
+    def add(delta, parts, n, slc):
+        return L.sx8_dec_add_rmsnorm_parts(p, delta, NULL, p, p, M, H, ctypes.c_float(1e-6), parts, n, slc, NULL)
+
+    assert add(p, p, 8, M * H) == 1 and "n_parts" in _err(L)
+    assert add(p, p, -1, M * H) == 1 and "n_parts" in _err(L)
+    assert add(NULL, p, 1, M * H) == 1 and "need delta" in _err(L)
+    assert add(p, NULL, 1, M * H) == 1 and "parts" in _err(L)
+    assert add(p, p, 1, M * H - 1) == 1 and "slice" in _err(L)
+    assert add(p, V((1 << 24) + 2), 1, M * H) == 1 and "aligned" in _err(L)
+
+    def rope(parts, n, slc):
+        return L.sx8_dec_qk_rope_cache_rows_parts(p, p, p, p, p, p, p, p, M, p, p, p, 32, 8, 128, 1024,
+                                                  ctypes.c_float(1e-6), parts, n, slc, NULL)
+
+    need = M * (32 + 2 * 8) * 128
+    assert rope(p, 8, need) == 1 and "n_parts" in _err(L)
+    assert rope(NULL, 1, need) == 1
+    assert rope(p, 2, need - 1) == 1 and "slice" in _err(L)

@@ -726,3 +726,144 @@ def test_head_argmax_partials_nan_logit(hiplib, cuda, N, top):
     assert torch.equal(logits.cpu().view(torch.int32), lr.view(torch.int32))
     assert tok_ref.item() == top
     assert tok.item() == top and pos.item() == 1
+
+
+def _deferred(name, *args):
+    """Call a *_deferred entry point; returns (parts, n_parts, slice)."""
+    import ctypes
+    import _sx8lib as _L
+    parts, n_parts, slc = ctypes.c_void_p(), ctypes.c_int32(), ctypes.c_int64()
+    _L.call(name, *args[:-1], ctypes.addressof(parts), ctypes.addressof(n_parts), ctypes.addressof(slc), args[-1])
+    return parts.value, n_parts.value, slc.value
+
+
+@pytest.mark.parametrize("M,K,Ns,hb,want_np", [
+    (512, 4096, [2560], 6, 3),          # o at M = 512: 4 K ranges
+    (512, 4096, [2560], 8, 3),
+    (300, 2600, [1001], 6, None),       # ragged N (H % 4 != 0: the scalar add path)
+    (512, 2560, [9728, 9728], 6, 0),    # gate/up at M = 512: unsplit 512-row tiles
+    (2048, 2560, [9728], 6, 0),         # gate at M = 2048: split tiles, summed as usual
+])
+def test_gemm_deferred_sums_into_add_rmsnorm(hiplib, cuda, M, K, Ns, hb, want_np):
+    """sx8_gemm_prefill_group_deferred + sx8_dec_add_rmsnorm_parts give the residual and the
+    normalized rows of sx8_gemm_prefill_group + sx8_dec_add_rmsnorm bit for bit (the
+    partial slices are added in the order the split-K sum adds them); plans without K
+    slices report no parts and write the full sums."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    ts = _mats(cuda, Ns, K, 300 + M, hb)
+    n_cb = (K + 31) // 32
+    g = torch.Generator().manual_seed(M + K)
+    X = torch.randn(M, K, generator=g).half().to(cuda)
+    H = Ns[0]
+    resid0 = torch.randn(M, H, generator=g).to(cuda)
+    w = (torch.rand(H, generator=g) + 0.5).half().to(cuda)
+    ws, nb = _L.gemm_workspace(M, Ns, n_cb, cuda)
+    print("deferred gemm", M, K, Ns, hb, flush=True)
+    ya = [torch.empty(M, N, device=cuda) for N in Ns]
+    ga = _group(ts, Ns, n_cb, ya)
+    _L.call("sx8_gemm_prefill_group", P(X), M, K, K, ga[0], ga[1], ga[2], hb, ga[3], ga[4], ga[5], ga[6], ga[7],
+            P(ws), nb, st)
+    ra, ha = resid0.clone(), torch.empty(M, H, dtype=torch.float16, device=cuda)
+    _L.call("sx8_dec_add_rmsnorm", P(ra), P(ya[0]), None, P(w), P(ha), M, H, 1e-6, st)
+    yb = [torch.empty(M, N, device=cuda) for N in Ns]
+    grp = _group(ts, Ns, n_cb, yb)
+    parts, n_parts, slc = _deferred("sx8_gemm_prefill_group_deferred", P(X), M, K, K, grp[0], grp[1], grp[2], hb,
+                                    grp[3], grp[4], grp[5], grp[6], grp[7], P(ws), nb, st)
+    rb, hb16 = resid0.clone(), torch.empty(M, H, dtype=torch.float16, device=cuda)
+    _L.call("sx8_dec_add_rmsnorm_parts", P(rb), P(yb[0]), None, P(w), P(hb16), M, H, 1e-6, parts, n_parts, slc, st)
+    torch.cuda.synchronize()
+    plan = _L.gemm_plan(M, Ns, n_cb)
+    print("   plan", plan, "n_parts", n_parts, flush=True)
+    if want_np is not None:
+        assert n_parts == want_np
+    assert n_parts == (plan["k_ranges"] - 1 if plan["tile"] != 512 else 0)
+    if n_parts:
+        assert slc == M * sum(Ns)
+    else:
+        for a, b in zip(ya, yb):
+            assert torch.equal(a.cpu(), b.cpu())
+    assert torch.equal(rb.cpu(), ra.cpu())
+    assert torch.equal(hb16.cpu().view(torch.int16), ha.cpu().view(torch.int16))
+
+
+@pytest.mark.parametrize("T", [512, 13])
+def test_qkv_deferred_sums_into_rope(hiplib, cuda, T):
+    """The q/k/v group deferred + sx8_dec_qk_rope_cache_rows_parts write the q rows and the
+    K/V cache rows of the group call + sx8_dec_qk_rope_cache_rows bit for bit (32/8 heads of
+    128, K = 2560: two K ranges at T = 512)."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    nh, nk, hd, L, K, eps = 32, 8, 128, 600, 2560, 1e-6
+    Ns = [nh * hd, nk * hd, nk * hd]
+    ts = _mats(cuda, Ns, K, 500 + T)
+    n_cb = K // 32
+    g = torch.Generator().manual_seed(T)
+    X = torch.randn(T, K, generator=g).half().to(cuda)
+    qn = (torch.rand(hd, generator=g) + 0.5).half().to(cuda)
+    kn = (torch.rand(hd, generator=g) + 0.5).half().to(cuda)
+    ang = torch.rand(L, hd // 2, generator=g) * 6.0
+    cos, sin = ang.cos().to(cuda), ang.sin().to(cuda)
+    pos0 = torch.full((1,), 7, dtype=torch.int64, device=cuda)
+    ws, nb = _L.gemm_workspace(T, Ns, n_cb, cuda)
+    out = []
+    print("deferred qkv", T, flush=True)
+    for deferred in (False, True):
+        ys = [torch.empty(T, N, device=cuda) for N in Ns]
+        grp = _group(ts, Ns, n_cb, ys)
+        qh = torch.zeros(T, nh, hd, dtype=torch.float16, device=cuda)
+        kc = torch.zeros(nk, L, hd, dtype=torch.float16, device=cuda)
+        vc = torch.zeros(nk, L, hd, dtype=torch.float16, device=cuda)
+        common = (P(ys[0]), P(ys[1]), P(ys[2]), P(qn), P(kn), P(cos), P(sin), P(pos0), T, P(qh), P(kc), P(vc),
+                  nh, nk, hd, L, eps)
+        if deferred:
+            parts, n_parts, slc = _deferred("sx8_gemm_prefill_group_deferred", P(X), T, K, K, grp[0], grp[1],
+                                            grp[2], 6, grp[3], grp[4], grp[5], grp[6], grp[7], P(ws), nb, st)
+            _L.call("sx8_dec_qk_rope_cache_rows_parts", *common, parts, n_parts, slc, st)
+            print("   n_parts", n_parts, flush=True)
+            if T == 512:
+                assert n_parts == 1
+        else:
+            _L.call("sx8_gemm_prefill_group", P(X), T, K, K, grp[0], grp[1], grp[2], 6, grp[3], grp[4], grp[5],
+                    grp[6], grp[7], P(ws), nb, st)
+            _L.call("sx8_dec_qk_rope_cache_rows", *common, st)
+        torch.cuda.synchronize()
+        out.append((qh.cpu(), kc.cpu(), vc.cpu()))
+    for a, b in zip(*out):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_gemm_silu_deferred_sums_into_add_rmsnorm(hiplib, cuda):
+    """sx8_dec_gemm_silu_deferred (down at M = 512: 6 K ranges) + sx8_dec_add_rmsnorm_parts
+    equal sx8_dec_gemm_silu + sx8_dec_add_rmsnorm bit for bit."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    M, K, N = 512, 9728, 2560
+    (hdr, lvl, bas, sca), = _mats(cuda, [N], K, 77)
+    n_cb = K // 32
+    g = torch.Generator().manual_seed(5)
+    a = (torch.randn(M, K, generator=g) * 3).to(cuda)
+    b = torch.randn(M, K, generator=g).to(cuda)
+    resid0 = torch.randn(M, N, generator=g).to(cuda)
+    w = (torch.rand(N, generator=g) + 0.5).half().to(cuda)
+    ws, nb = _L.gemm_workspace(M, (N,), n_cb, cuda)
+    args = (P(a), P(b), M, K, P(hdr), P(lvl), 6, P(bas), P(sca), N, n_cb)
+    y = torch.empty(M, N, device=cuda)
+    _L.call("sx8_dec_gemm_silu", *args, P(y), P(ws), nb, st)
+    ra, ha = resid0.clone(), torch.empty(M, N, dtype=torch.float16, device=cuda)
+    _L.call("sx8_dec_add_rmsnorm", P(ra), P(y), None, P(w), P(ha), M, N, 1e-6, st)
+    y2 = torch.empty(M, N, device=cuda)
+    parts, n_parts, slc = _deferred("sx8_dec_gemm_silu_deferred", *args, P(y2), P(ws), nb, st)
+    rb, hb16 = resid0.clone(), torch.empty(M, N, dtype=torch.float16, device=cuda)
+    _L.call("sx8_dec_add_rmsnorm_parts", P(rb), P(y2), None, P(w), P(hb16), M, N, 1e-6, parts, n_parts, slc, st)
+    torch.cuda.synchronize()
+    print("deferred silu n_parts", n_parts, flush=True)
+    assert n_parts == 5 and slc == M * N
+    assert torch.equal(rb.cpu(), ra.cpu())
+    assert torch.equal(hb16.cpu().view(torch.int16), ha.cpu().view(torch.int16))
