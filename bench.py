@@ -57,16 +57,16 @@ MEASURED = {
     "gemv_traced_launch_us": {"value": 6.116, "src": "gemv", "src_sha16": "9ba026f0ed6ce498",
                               "how": "rocprofv3 --kernel-trace --stats, bench.py --only gemv --steps 20 "
                                      "(same-run event figure under the tracer: 6.143 us)"},
-    # k_gemm_w2 on down_proj at M = 2048 (plan 80 tiles x 3 K ranges): 89774.7 KiB fetched,
-    # 61698.2 KiB written per dispatch (Y 21 MB + two partial tiles per split tile 42 MB)
-    "prefill_traffic": {"value": (89774.7 * 2.0 + 61698.2) * 1024, "src": "gemm", "src_sha16": "68f51277e1c0657f",
+    # k_gemm_w2 on down_proj at M = 2048 (plan 80 tiles x 3 K ranges): 89776.0 KiB fetched,
+    # 61705.1 KiB written per dispatch (Y 21 MB + two partial tiles per split tile 42 MB)
+    "prefill_traffic": {"value": (89776.0 * 2.0 + 61705.1) * 1024, "src": "gemm", "src_sha16": "8e45d8246051e308",
                         "how": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, bench.py --only gemm-one "
                                "--shape down_proj --m 2048 --iters 20, mean of 21 dispatches"},
     # 100 x sum SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs)
-    "prefill_mfma_busy_pct": {"value": 47.9, "src": "gemm", "src_sha16": "68f51277e1c0657f",
+    "prefill_mfma_busy_pct": {"value": 47.0, "src": "gemm", "src_sha16": "8e45d8246051e308",
                               "how": "rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_F16 "
                                      "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE, bench.py --only gemm-one "
-                                     "--shape down_proj --m 2048 --iters 50 (k_gemm_w2; gate: 42.9)"},
+                                     "--shape down_proj --m 2048 --iters 50 (k_gemm_w2; gate: 42.3; 47.0-47.9 on down across boxes)"},
 }
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, vendor figure
 # The streaming-read rate measured on the GPU boxes (bench.py --only readbw: best of the
