@@ -129,6 +129,18 @@ int32_t sx8_dec_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const u
                              uint16_t* out, int64_t T, int64_t start, int32_t nh, int32_t nk, int32_t hd,
                              int64_t L, float scale, void* stream);
 
+/* sx8_dec_attn_prefill writing its output as the o projection's prefill-GEMM operands
+ * (sx8_gemm_prefill_packed) instead of (T, nh * hd) fp16: Xp, the packed X of the T rows
+ * (ceil(T / 32) * n_cb * 2048 bytes), and Zhl, the o projection's PCA operand (T * n_cb * 8
+ * bytes), with n_cb = nh * hd / 32 and basis (n_cb, 2, 32) / scales (n_cb, 2) that
+ * projection's.  Bit for bit what sx8_dec_attn_prefill followed by the prefill GEMM's own
+ * pass over its output gives; the separate pass (one launch, X read and written) is gone.
+ * basis, Xp and Zhl 16-byte aligned, scales 8-byte.  No reference counterpart. */
+int32_t sx8_dec_attn_prefill_packed(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                    int64_t T, int64_t start, int32_t nh, int32_t nk, int32_t hd, int64_t L,
+                                    float scale, const float* basis, const float* scales, uint16_t* Xp,
+                                    uint32_t* Zhl, void* stream);
+
 /* Workspace bytes of sx8_dec_attn_split. */
 int64_t sx8_dec_attn_workspace_bytes(int32_t nh, int32_t hd);
 

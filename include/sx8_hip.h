@@ -38,8 +38,10 @@ extern "C" {
 
 /* 3: sx8_dec_gemv_rmsnorm_pair takes the up matrix's pointers; sx8_gemm_reload_tuning.
  * 4: deferred split-K sums: sx8_gemm_prefill_group_deferred, sx8_dec_gemm_silu_deferred and
- *    the consumers sx8_dec_add_rmsnorm_parts, sx8_dec_qk_rope_cache_rows_parts */
-#define SX8_ABI_VERSION 4
+ *    the consumers sx8_dec_add_rmsnorm_parts, sx8_dec_qk_rope_cache_rows_parts
+ * 5: producer-written GEMM operands: sx8_gemm_prefill_packed(_workspace_bytes),
+ *    sx8_dec_attn_prefill_packed */
+#define SX8_ABI_VERSION 5
 
 #define SX8_OK 0
 #define SX8_ERR_INVALID 1      /* bad argument (null pointer, size, hdr_bytes, alignment) */
@@ -268,6 +270,31 @@ int32_t sx8_gemm_prefill_group_deferred(const uint16_t* X, int64_t M, int64_t ld
                                         const int64_t* Ns, int64_t n_cb, float* const* Ys,
                                         void* workspace, int64_t workspace_bytes, float** parts,
                                         int32_t* n_parts, int64_t* slice, void* stream);
+
+/* sx8_gemm_prefill_group on operands a producer kernel already wrote, so the call runs no
+ * pass over X (it launches the GEMM and, for a split plan, the partial sums only):
+ *   Xp  -- the packed X of the M rows: for each 32-row group G (rows past M zero) and K
+ *          block kb a 2 KB chunk at byte (G * n_cb + kb) * 2048, laid out [k-step st 0..1]
+ *          [lane l = 32 hf + r, hf 0..1, r 0..31][8 fp16] holding X[32 G + r][32 kb + 16 hf
+ *          + 8 st .. + 8]; ceil(M / 32) * n_cb * 2048 bytes, 16-byte aligned;
+ *   Zhl[i] -- matrix i's PCA operand, (M, n_cb) entries of 8 bytes: Z0, Z1 of the row's K
+ *          block (scale_j * sum_t x_t basis_j[t], the reference's tree order) each as fp16
+ *          (hi, lo) with hi = fp16(z), lo = fp16(z - hi); M * n_cb * 8 bytes, 16-byte aligned.
+ * sx8_dec_attn_prefill_packed writes both for the attention output.  The workspace holds
+ * only the split-K partials (sx8_gemm_prefill_packed_workspace_bytes; NULL when that is 0).
+ * parts / n_parts / slice: all NULL -- the call adds its split-K partials itself; all given
+ * -- the partial slices are left to the caller as in sx8_gemm_prefill_group_deferred.  Same
+ * outputs, bit for bit, as sx8_gemm_prefill_group on the X those operands came from.  No
+ * counterpart in the reference (its prefill GEMM reads X as given). */
+int32_t sx8_gemm_prefill_packed(const uint16_t* Xp, const uint32_t* const* Zhl, int64_t M, int64_t K,
+                                int32_t n_mats, const uint8_t* const* hdrs, const uint8_t* const* levels,
+                                int32_t hdr_bytes, const int64_t* Ns, int64_t n_cb, float* const* Ys,
+                                void* workspace, int64_t workspace_bytes, float** parts, int32_t* n_parts,
+                                int64_t* slice, void* stream);
+
+/* Workspace bytes of sx8_gemm_prefill_packed (the plan's split-K partials; 0 when the plan
+ * does not split K), or -1 for bad arguments. */
+int64_t sx8_gemm_prefill_packed_workspace_bytes(int64_t M, int32_t n_mats, const int64_t* Ns, int64_t n_cb);
 
 /* Output-side PCA: Y[m, n] += sum_kb c0(kb,n) Z[m,kb,0] + c1(kb,n) Z[m,kb,1], c0/c1 the
  * signed nibbles of the coeff byte in the v4.4 header (float32 FMAs, one thread per

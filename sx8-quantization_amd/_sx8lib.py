@@ -63,6 +63,9 @@ SIGNATURES = [
      [_P, _I64, _I64, _I64, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P, _I64, _P]),
     ("sx8_gemm_prefill_group_deferred", _I32,
      [_P, _I64, _I64, _I64, _I32, _P, _P, _I32, _P, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _P]),
+    ("sx8_gemm_prefill_packed", _I32,
+     [_P, _P, _I64, _I64, _I32, _P, _P, _I32, _P, _I64, _P, _P, _I64, _P, _P, _P, _P]),
+    ("sx8_gemm_prefill_packed_workspace_bytes", _I64, [_I64, _I32, _P, _I64]),
     ("sx8_gemm_pca_z", _I32, [_P, _I64, _P, _I32, _I64, _I64, _P, _P]),
     ("sx8_gemm_prefill_core", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _I64, _I64, _P, _P, _I64, _P]),
     # include/sx8_decoder.h
@@ -79,6 +82,8 @@ SIGNATURES = [
     ("sx8_dec_gemm_silu_deferred", _I32,
      [_P, _P, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _I64, _P, _P, _P, _P]),
     ("sx8_dec_attn_prefill", _I32, [_P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _I64, ctypes.c_float, _P]),
+    ("sx8_dec_attn_prefill_packed", _I32,
+     [_P, _P, _P, _I64, _I64, _I32, _I32, _I32, _I64, ctypes.c_float, _P, _P, _P, _P, _P]),
     ("sx8_dec_attn_split", _I32, [_P, _P, _P, _P, _P, _I32, _I32, _I32, _I64, ctypes.c_float, _P, _I64,
                                   _P]),
     ("sx8_dec_attn_workspace_bytes", _I64, [_I32, _I32]),
@@ -98,7 +103,7 @@ SIGNATURES = [
                                          _P, _P, _P, _P]),
     ("sx8_dec_gemv_zp_add", _I32, [_P, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _P]),
 ]
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib = None
 _lock = threading.Lock()

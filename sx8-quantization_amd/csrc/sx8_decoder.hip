@@ -805,23 +805,93 @@ __device__ __forceinline__ float lane_swap32(float v) {
 template <int G>
 constexpr int ap_sets() { return G <= 4 ? 2 : 1; }
 
+// Where the packed form of k_attn_prefill puts its output: the o projection's prefill-GEMM
+// operands (the packed X and Zhl of sx8_gemm_prefill_packed) for that projection's PCA
+// basis rows and scales; n_cb = nh * HD / 32.
+struct ApPack {
+    const float* basis;
+    const float* scales;
+    uint16_t* Xp;
+    uint32_t* Zhl;
+    int n_cb;
+};
+
+// The packed operands of one 32-dim fragment of a query row's attention output, bit for
+// bit what k_compute_z<true, true> writes from the fp16 output row: x = fp16(v) into the
+// packed X chunk of (row group, K block) (k-step st, MFMA lane 32 hf + r, 8 values
+// X[r][32 kb + 16 hf + 8 st ..]; rows past T as zeros), and the row's Z0, Z1 of the K block
+// in the reference's tree order -- products x_t b_t, pairs (t, t + 16), then offsets 8, 4,
+// 2, 1 (cuda/sx8_decode1_v3.cu:53-63) -- times the scales, as split fp16 hi / lo pairs.  The
+// lane holds t = 8 gq + 4 h + e (gq, e < 4), so offsets 16 and 8 stay in the lane and
+// offset 4 is one swap with lane ^ 32.  bl: the block's 64 basis values (LDS).
+__device__ __forceinline__ void ap_pack_fragment(const float (&v)[16], bool row_ok, int c, int h, const float* bl,
+                                                 float2 sc, uint16_t* xdst, uint32_t* zdst) {
+#pragma clang fp contract(off)
+    uint32_t xw[8];
+    float xf[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint16_t lo = row_ok ? f2h(v[2 * i]) : (uint16_t)0, hi = row_ok ? f2h(v[2 * i + 1]) : (uint16_t)0;
+        xw[i] = (uint32_t)lo | ((uint32_t)hi << 16);
+        xf[2 * i] = h2f(lo);
+        xf[2 * i + 1] = h2f(hi);
+    }
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq)
+        *reinterpret_cast<uint2*>(xdst + (gq & 1) * 512 + ((gq >> 1) * 32 + c) * 8 + 4 * h) =
+            make_uint2(xw[2 * gq], xw[2 * gq + 1]);
+    float z[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const float4* b = reinterpret_cast<const float4*>(bl + 32 * j + 4 * h);
+        float pr[16];
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+            const float4 bb = b[2 * gq];
+            pr[4 * gq] = xf[4 * gq] * bb.x;
+            pr[4 * gq + 1] = xf[4 * gq + 1] * bb.y;
+            pr[4 * gq + 2] = xf[4 * gq + 2] * bb.z;
+            pr[4 * gq + 3] = xf[4 * gq + 3] * bb.w;
+        }
+        float p[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float t16 = pr[e] + pr[8 + e];          // t = 4 h + e, with t + 16
+            const float u16 = pr[4 + e] + pr[12 + e];     // t + 8, with t + 24
+            p[e] = t16 + u16;                             // offset 8
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[e] = p[e] + lane_swap32(p[e]);   // offset 4 (h = 0: t = e)
+        p[0] = p[0] + p[2];
+        p[1] = p[1] + p[3];
+        z[j] = (j ? sc.y : sc.x) * (p[0] + p[1]);
+        // z is rounded to float32 before its fp16 split, as in k_compute_z: without the pin
+        // the compiler folds the product into the conversion (one v_fma_mixlo_f16, a single
+        // rounding of scale * sum to fp16), which differs on ties
+        asm volatile("" : "+v"(z[j]));
+    }
+    if (row_ok && h == 0) *reinterpret_cast<uint2*>(zdst) = make_uint2(sx8_split_hl(z[0]), sx8_split_hl(z[1]));
+}
+
 template <int HD, int GW, int NS>
 struct ApLds {
     static constexpr int kK = 32 * kApKRow * 2;                 // bytes of one staged K block
     static constexpr int kV = HD * kApVRow * 2;                 // bytes of one staged V^T block
     static constexpr int kStage = 2 * NS * (kK + kV);           // [buffer][set]
-    static constexpr int kMerge = (NS - 1) * GW * 64 * (2 + 16 * (HD / 32)) * 4;   // sets 1 .. NS - 1
+    // merge: every set's (m, lsum) and the O^T fragments it does not own (NT - NT / NS of them)
+    static constexpr int kMerge = NS > 1 ? NS * GW * 64 * (2 + 16 * (HD / 32 - HD / 32 / NS)) * 4 : 0;
     static constexpr int kBytes = kStage > kMerge ? kStage : kMerge;
 };
 
 // GW of the G query heads of a KV head per work-group (G / GW work-groups per KV head and
 // query tile), NS sets of GW waves: set s takes key blocks s, s + NS, s + 2 NS, ...
-template <int HD, int G, int GW, int NS>
+// kPack: the output goes out as the o projection's packed GEMM operands (ApPack) instead.
+template <int HD, int G, int GW, int NS, bool kPack = false>
 __global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* __restrict__ q,
                                                           const uint16_t* __restrict__ k_cache,
                                                           const uint16_t* __restrict__ v_cache,
                                                           uint16_t* __restrict__ out, int T, int start,
-                                                          int nh, int L, float scale_log2) {
+                                                          int nh, int L, float scale_log2, const ApPack pk) {
     typedef float f32x16 __attribute__((ext_vector_type(16)));
     typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
     using Lds = ApLds<HD, GW, NS>;
@@ -854,6 +924,19 @@ __global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* _
 #pragma unroll
         for (int st = 0; st < KS; ++st)
             qb[st] = qi < T ? *reinterpret_cast<const sx8_u32x4*>(qr + 16 * st) : zero4;
+    }
+    // kPack: the basis rows and scales of the work-group's GW heads' K blocks (one float4
+    // per thread), staged in LDS with the first key block
+    constexpr int kPkF4 = kPack ? GW * NT * 16 : 1;
+    static_assert(!kPack || kPkF4 <= 64 * GW * NS, "one basis float4 per thread");
+    __shared__ float4 apb[kPkF4];
+    __shared__ float2 aps[kPack ? GW * NT : 1];
+    const int kbw = (head - g) * NT;                            // first K block of the work-group
+    float4 bpre = make_float4(0.f, 0.f, 0.f, 0.f);
+    float2 spre = make_float2(0.f, 0.f);
+    if constexpr (kPack) {
+        if (tid < kPkF4) bpre = reinterpret_cast<const float4*>(pk.basis + (int64_t)kbw * 64)[tid];
+        if (tid < GW * NT) spre = reinterpret_cast<const float2*>(pk.scales + (int64_t)kbw * 2)[tid];
     }
     const uint16_t* kbase = k_cache + (int64_t)kvh * L * HD;
     const uint16_t* vbase = v_cache + (int64_t)kvh * L * HD;
@@ -991,6 +1074,10 @@ __global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* _
         for (int i = 0; i < kPf; ++i)
             if (NS * (i + 1) + set < nblk) load_blk(kreg[i], vreg[i], NS * (i + 1) + set);
         if (set < nblk) stage(0, k0, v0);
+        if constexpr (kPack) {
+            if (tid < kPkF4) apb[tid] = bpre;
+            if (tid < GW * NT) aps[tid] = spre;
+        }
         __syncthreads();
     }
     for (int j = 0; j < nstep; j += kPf) {
@@ -998,50 +1085,75 @@ __global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* _
         for (int i = 0; i < kPf; ++i)
             if (j + i < nstep) body(j + i, kreg[i], vreg[i]);
     }
-    // merge: sets 1 .. NS - 1 hand (m, lsum, O^T) to their partner wave of set 0 through LDS
-    // (the staging buffers are free after the last barrier); lane-contiguous rows
-    constexpr int kMg = 64 * (2 + 16 * NT);                    // floats per handed-over state
-    if (NS == 1) {
-        if (qi >= T) return;
-        const float inv = 1.0f / lsum;
-        uint16_t* orow = out + ((int64_t)qi * nh + head) * HD;
-#pragma unroll
-        for (int n = 0; n < NT; ++n)
+    // kPack: fragment n of the row (16 values, dims 32 n + 8 gq + 4 h + e) as packed operands;
+    // every lane of the wave takes part (the Z tree swaps lane halves), rows past T pack zeros
+    auto emit_packed = [&](int n, const float (&v)[16]) {
+        const int kb = kbw + g * NT + n;
+        ap_pack_fragment(v, qi < T, c, h, reinterpret_cast<const float*>(apb) + (g * NT + n) * 64, aps[g * NT + n],
+                         pk.Xp + ((int64_t)blockIdx.x * pk.n_cb + kb) * 1024,
+                         pk.Zhl + ((int64_t)qi * pk.n_cb + kb) * 2);
+    };
+    auto emit = [&](int n, const float (&v)[16]) {
+        if constexpr (kPack) {
+            emit_packed(n, v);
+        } else {
+            uint16_t* orow = out + ((int64_t)qi * nh + head) * HD;
 #pragma unroll
             for (int gq = 0; gq < 4; ++gq) {
-                const int d = 32 * n + 8 * gq + 4 * h;
-                const uint32_t lo = (uint32_t)f2h(o[n][4 * gq] * inv) | ((uint32_t)f2h(o[n][4 * gq + 1] * inv) << 16);
-                const uint32_t hi = (uint32_t)f2h(o[n][4 * gq + 2] * inv) | ((uint32_t)f2h(o[n][4 * gq + 3] * inv) << 16);
-                *reinterpret_cast<uint2*>(orow + d) = make_uint2(lo, hi);
+                const uint32_t lo = (uint32_t)f2h(v[4 * gq]) | ((uint32_t)f2h(v[4 * gq + 1]) << 16);
+                const uint32_t hi = (uint32_t)f2h(v[4 * gq + 2]) | ((uint32_t)f2h(v[4 * gq + 3]) << 16);
+                *reinterpret_cast<uint2*>(orow + 32 * n + 8 * gq + 4 * h) = make_uint2(lo, hi);
             }
+        }
+    };
+    if (NS == 1) {
+        if (!kPack && qi >= T) return;
+        const float inv = 1.0f / lsum;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                v[r] = o[n][r] * inv;
+                asm volatile("" : "+v"(v[r]));    // rounded to float32, then to fp16 (see below)
+            }
+            emit(n, v);
+        }
         return;
     }
-    if (set > 0) {
-        float* mg = reinterpret_cast<float*>(lds) + ((set - 1) * GW + g) * kMg;
-        mg[lane] = m;
-        mg[64 + lane] = lsum;
+    // merge: set s finishes the fragments n = s, s + NS, ... of its wave's head.  Every set
+    // hands its (m, lsum) and the O^T fragments it does not own to the others through LDS (the
+    // staging buffers are free after the last barrier; lane-contiguous rows), then merges its
+    // own fragments over all sets in set order -- the arithmetic one merging set would do --
+    // so the epilogue work is spread over the NS sets
+    static_assert(NT % NS == 0, "whole fragments per set");
+    constexpr int NX = NT - NT / NS;                            // fragments a set hands over
+    float* ml = reinterpret_cast<float*>(lds);                  // [set][g][m, lsum][64]
+    float* ob = ml + NS * GW * 128;                             // [set][slot < NX][g][16][64]
+    auto slot = [](int t, int n) { return n - n / NS - (n % NS > t ? 1 : 0); };   // n % NS != t
+    ml[(set * GW + g) * 128 + lane] = m;
+    ml[(set * GW + g) * 128 + 64 + lane] = lsum;
 #pragma unroll
-        for (int n = 0; n < NT; ++n)
+    for (int n = 0; n < NT; ++n) {
+        if (n % NS == set) continue;
+        float* dst = ob + ((set * NX + slot(set, n)) * GW + g) * 1024 + lane;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) mg[(2 + 16 * n + r) * 64 + lane] = o[n][r];
+        for (int r = 0; r < 16; ++r) dst[r * 64] = o[n][r];
     }
     __syncthreads();
-    if (set > 0 || qi >= T) return;
-    // set s's state weighs 2^(m_s - max m); an empty set (m = -inf) weighs nothing, and m is
+    if (!kPack && qi >= T) return;
+    // set t's state weighs 2^(m_t - max m); an empty set (m = -inf) weighs nothing, and m is
     // finite in set 0, which owns block 0
-    const float* mg1 = reinterpret_cast<const float*>(lds) + g * kMg;
     float ms[NS], ls[NS], f[NS];
-    ms[0] = m;
-    ls[0] = lsum;
 #pragma unroll
-    for (int t = 1; t < NS; ++t) {
-        ms[t] = mg1[(t - 1) * GW * kMg + lane];
-        ls[t] = mg1[(t - 1) * GW * kMg + 64 + lane];
+    for (int t = 0; t < NS; ++t) {
+        ms[t] = ml[(t * GW + g) * 128 + lane];
+        ls[t] = ml[(t * GW + g) * 128 + 64 + lane];
     }
     float mm = ms[0];
 #pragma unroll
     for (int t = 1; t < NS; ++t) mm = fmaxf(mm, ms[t]);
-    f[0] = __builtin_amdgcn_exp2f(m - mm);
+    f[0] = __builtin_amdgcn_exp2f(ms[0] - mm);
 #pragma unroll
     for (int t = 1; t < NS; ++t) f[t] = ms[t] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(ms[t] - mm);
     float den = ls[0] * f[0];
@@ -1051,23 +1163,29 @@ __global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* _
     float wgt[NS];
 #pragma unroll
     for (int t = 0; t < NS; ++t) wgt[t] = f[t] * inv;
-    uint16_t* orow = out + ((int64_t)qi * nh + head) * HD;
 #pragma unroll
-    for (int n = 0; n < NT; ++n)
+    for (int n = 0; n < NT; ++n) {
+        if (n % NS != set) continue;
+        float v[16];
 #pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-            float v[4];
+        for (int r = 0; r < 16; ++r) {
+            // set t's value: this wave's own accumulator for t = set, else the LDS copy
+            // (slot 0 stands in for t = set, so the address stays inside the handed-over block)
+            auto val = [&](int t) {
+                const int sl = t == set ? 0 : slot(t, n);
+                return t == set ? o[n][r] : ob[((t * NX + sl) * GW + g) * 1024 + r * 64 + lane];
+            };
+            // explicit fmas, and the float32 result pinned before its fp16 conversion: the
+            // compiler would otherwise pick which product to fuse and fold the last one into
+            // the conversion (v_fma_mixlo_f16), so the plain and packed outputs could differ
+            float acc = val(0) * wgt[0];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v[e] = o[n][4 * gq + e] * wgt[0];
-#pragma unroll
-                for (int t = 1; t < NS; ++t) v[e] += mg1[(t - 1) * GW * kMg + (2 + 16 * n + 4 * gq + e) * 64 + lane] * wgt[t];
-            }
-            const int d = 32 * n + 8 * gq + 4 * h;
-            const uint32_t lo = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
-            const uint32_t hi = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
-            *reinterpret_cast<uint2*>(orow + d) = make_uint2(lo, hi);
+            for (int t = 1; t < NS; ++t) acc = __builtin_fmaf(val(t), wgt[t], acc);
+            asm volatile("" : "+v"(acc));
+            v[r] = acc;
         }
+        emit(n, v);
+    }
 }
 
 namespace {
@@ -1230,38 +1348,83 @@ extern "C" int32_t sx8_dec_attn(const uint16_t* q, const uint16_t* k_cache, cons
     return check_launch("sx8_dec_attn");
 }
 
-extern "C" int32_t sx8_dec_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
-                                        uint16_t* out, int64_t T, int64_t start, int32_t nh, int32_t nk,
-                                        int32_t hd, int64_t L, float scale, void* stream) {
-    using namespace sx8;
-    if (!q || !k_cache || !v_cache || !out) return fail(SX8_ERR_INVALID, "sx8_dec_attn_prefill: null pointer");
-    const int G = nk > 0 ? nh / nk : 0;
-    if (nh <= 0 || nk <= 0 || nh % nk || (G != 1 && G != 2 && G != 4 && G != 8) || (hd != 64 && hd != 128) ||
-        16 * G > hd || T <= 0 || start < 0 || L <= 0 || start + T > L || L * (int64_t)hd > 0x7FFFFFFF ||
-        (T + 31) / 32 > 0x7FFFFFFF)
-        return fail(SX8_ERR_INVALID, "sx8_dec_attn_prefill: bad shape (nh / nk in {1, 2, 4, 8} with 16 nh / nk "
-                    "<= hd, hd 64 or 128, 0 <= start, start + T <= L)");
-    if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(out, 8))
-        return fail(SX8_ERR_INVALID, "sx8_dec_attn_prefill: q and caches must be 16-byte aligned, out 8-byte");
+namespace {
+
+// The prompt attention's kernel choice (shape checked by the caller).
+template <bool kPack>
+void launch_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
+                         int64_t T, int64_t start, int32_t nh, int32_t nk, int32_t hd, int64_t L, float scale,
+                         const ApPack& pk, hipStream_t st) {
+    const int G = nh / nk;
     const float sl2 = scale * 1.4426950408889634f;
     const dim3 grid((unsigned)((T + 31) / 32), (unsigned)nk);
 #define SX8_AP(HD_, G_)                                                                                      \
-    hipLaunchKernelGGL((k_attn_prefill<HD_, G_, G_, ap_sets<G_>()>), grid, dim3(64 * G_ * ap_sets<G_>()), 0,     \
-                       as_stream(stream), q, k_cache, v_cache, out, (int)T, (int)start, nh, (int)L, sl2)
+    hipLaunchKernelGGL((k_attn_prefill<HD_, G_, G_, ap_sets<G_>(), kPack>), grid, dim3(64 * G_ * ap_sets<G_>()), \
+                       0, st, q, k_cache, v_cache, out, (int)T, (int)start, nh, (int)L, sl2, pk)
     if (hd == 128) {
         if (G == 4 && (int64_t)grid.x * grid.y < 256) {
             // a grid short of one work-group per CU: two work-groups per KV head and tile (two
             // heads each) with four sets of two waves, so the longest (last) tiles' chain of key
             // blocks is half as long (T = 512: 18.3 -> 16.6 us).  Past that the heads share
             // the staging of four per work-group (T = 2048: 90 us against 117 for this form).
-            hipLaunchKernelGGL((k_attn_prefill<128, 4, 2, 4>), dim3(grid.x, 2 * grid.y), dim3(512), 0,
-                               as_stream(stream), q, k_cache, v_cache, out, (int)T, (int)start, nh, (int)L, sl2);
+            hipLaunchKernelGGL((k_attn_prefill<128, 4, 2, 4, kPack>), dim3(grid.x, 2 * grid.y), dim3(512), 0, st, q,
+                               k_cache, v_cache, out, (int)T, (int)start, nh, (int)L, sl2, pk);
         } else if (G == 4) SX8_AP(128, 4); else if (G == 1) SX8_AP(128, 1); else if (G == 2) SX8_AP(128, 2); else SX8_AP(128, 8);
     } else {
         if (G == 1) SX8_AP(64, 1); else if (G == 2) SX8_AP(64, 2); else SX8_AP(64, 4);
     }
 #undef SX8_AP
-    return check_launch("sx8_dec_attn_prefill");
+}
+
+int32_t check_attn_prefill(const char* what, const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                           int64_t T, int64_t start, int32_t nh, int32_t nk, int32_t hd, int64_t L) {
+    using namespace sx8;
+    if (!q || !k_cache || !v_cache) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    const int G = nk > 0 ? nh / nk : 0;
+    if (nh <= 0 || nk <= 0 || nh % nk || (G != 1 && G != 2 && G != 4 && G != 8) || (hd != 64 && hd != 128) ||
+        16 * G > hd || T <= 0 || start < 0 || L <= 0 || start + T > L || L * (int64_t)hd > 0x7FFFFFFF ||
+        (T + 31) / 32 > 0x7FFFFFFF)
+        return fail(SX8_ERR_INVALID, "%s: bad shape (nh / nk in {1, 2, 4, 8} with 16 nh / nk "
+                    "<= hd, hd 64 or 128, 0 <= start, start + T <= L)", what);
+    if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
+        return fail(SX8_ERR_INVALID, "%s: q and caches must be 16-byte aligned", what);
+    return SX8_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t sx8_dec_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                        uint16_t* out, int64_t T, int64_t start, int32_t nh, int32_t nk,
+                                        int32_t hd, int64_t L, float scale, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_dec_attn_prefill";
+    const int32_t rc = check_attn_prefill(what, q, k_cache, v_cache, T, start, nh, nk, hd, L);
+    if (rc != SX8_OK) return rc;
+    if (!out) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (!aligned(out, 8)) return fail(SX8_ERR_INVALID, "%s: out must be 8-byte aligned", what);
+    launch_attn_prefill<false>(q, k_cache, v_cache, out, T, start, nh, nk, hd, L, scale, ApPack{},
+                               as_stream(stream));
+    return check_launch(what);
+}
+
+extern "C" int32_t sx8_dec_attn_prefill_packed(const uint16_t* q, const uint16_t* k_cache,
+                                               const uint16_t* v_cache, int64_t T, int64_t start, int32_t nh,
+                                               int32_t nk, int32_t hd, int64_t L, float scale,
+                                               const float* basis, const float* scales, uint16_t* Xp,
+                                               uint32_t* Zhl, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_dec_attn_prefill_packed";
+    const int32_t rc = check_attn_prefill(what, q, k_cache, v_cache, T, start, nh, nk, hd, L);
+    if (rc != SX8_OK) return rc;
+    if (!basis || !scales || !Xp || !Zhl) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (!aligned(basis, 16) || !aligned(scales, 8) || !aligned(Xp, 16) || !aligned(Zhl, 16))
+        return fail(SX8_ERR_INVALID, "%s: basis, Xp and Zhl must be 16-byte aligned, scales 8-byte", what);
+    const int64_t n_cb = (int64_t)nh * hd / 32;
+    if ((T + 31) / 32 * n_cb * 2048 > 0x7FFFFFFF || T * n_cb * 8 > 0x7FFFFFFF)
+        return fail(SX8_ERR_UNSUPPORTED, "%s: operands beyond 2 GiB", what);
+    const ApPack pk{basis, scales, Xp, Zhl, (int)n_cb};
+    launch_attn_prefill<true>(q, k_cache, v_cache, nullptr, T, start, nh, nk, hd, L, scale, pk, as_stream(stream));
+    return check_launch(what);
 }
 
 extern "C" int64_t sx8_dec_attn_workspace_bytes(int32_t nh, int32_t hd) {

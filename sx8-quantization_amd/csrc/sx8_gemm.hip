@@ -1442,8 +1442,9 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t NB, int64_t n_cb, int64_t part_cap 
 }
 
 // How the PCA operand reaches the kernel: none (core weights only), computed here from
-// basis/scales, or converted from a caller's f32 Z.
-enum class ZMode { kNone, kBasis, kGiven };
+// basis/scales, converted from a caller's f32 Z, or written by the caller's producer kernel
+// together with the packed X (kPacked: nothing is staged in the workspace).
+enum class ZMode { kNone, kBasis, kGiven, kPacked };
 
 template <bool kSplit, bool kPca, int HB, int MF>
 void launch_mf(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, const GemmGroup& g,
@@ -1480,10 +1481,11 @@ struct WsLayout {
     int64_t total;
 };
 
-WsLayout ws_layout(const Plan& p, int64_t M, int64_t Ntot, int64_t n_cb, int n_mats, bool with_z) {
+WsLayout ws_layout(const Plan& p, int64_t M, int64_t Ntot, int64_t n_cb, int n_mats, bool with_z,
+                   bool staged = true) {
     WsLayout l;
-    l.z_bytes = with_z ? ((M * n_cb * 8 + 255) & ~int64_t(255)) : 0;
-    l.xp_bytes = ((M + 31) / 32 * n_cb * 2048 + 255) & ~int64_t(255);
+    l.z_bytes = with_z && staged ? ((M * n_cb * 8 + 255) & ~int64_t(255)) : 0;
+    l.xp_bytes = staged ? ((M + 31) / 32 * n_cb * 2048 + 255) & ~int64_t(255) : 0;
     l.part_bytes = p.w1 ? p.n_split * (p.St - 1) * kW1BM * kBN * 4 : (int64_t)(p.S - 1) * M * Ntot * 4;
     l.total = l.z_bytes * n_mats + l.xp_bytes + l.part_bytes;
     return l;
@@ -1512,28 +1514,38 @@ struct PendingSums {
     int64_t slice;
 };
 
+// The operands a producer kernel wrote (ZMode::kPacked): the packed X and every matrix's Zhl.
+struct PackedIn {
+    const uint16_t* Xp;
+    const uint32_t* const* Zhl;
+};
+
 template <bool kSplit>
 int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, int64_t K, int n_mats,
                  const WeightSrc* ws_in, int32_t hdr_bytes, ZMode zm, const float* const* bases,
                  const float* const* scales, const float* Z, const int64_t* Ns, int64_t n_cb,
                  float* const* Ys, void* workspace, int64_t workspace_bytes, hipStream_t st,
                  const float* silu_g = nullptr, const float* silu_u = nullptr,
-                 int64_t part_cap = INT64_MAX, PendingSums* defer = nullptr) {
+                 int64_t part_cap = INT64_MAX, PendingSums* defer = nullptr, const PackedIn* packed = nullptr) {
     using namespace sx8;
     if (defer) *defer = PendingSums{nullptr, 0, 0};
     int64_t Ntot = 0, NB = 0;
     if (!group_width(n_mats, Ns, Ntot, NB)) return fail(SX8_ERR_UNSUPPORTED, "%s: group too wide", what);
     const Plan p = plan_gemm(M, Ntot, NB, n_cb, part_cap);
     if (p.G > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "%s: grid too large", what);
-    const WsLayout lay = ws_layout(p, M, Ntot, n_cb, n_mats, zm != ZMode::kNone);
-    if (!workspace || workspace_bytes < lay.total || !aligned(workspace, 256))
+    const bool staged = zm != ZMode::kPacked;
+    const WsLayout lay = ws_layout(p, M, Ntot, n_cb, n_mats, zm != ZMode::kNone, staged);
+    // (a packed call whose plan does not split K needs no workspace at all)
+    if (lay.total > 0 && (!workspace || workspace_bytes < lay.total || !aligned(workspace, 256)))
         return fail(SX8_ERR_INVALID,
                     "%s: needs a 256-byte aligned workspace of %lld bytes "
-                    "(sx8_gemm_prefill_workspace_bytes), got %lld bytes at %p",
-                    what, (long long)lay.total, (long long)workspace_bytes, workspace);
+                    "(%s), got %lld bytes at %p",
+                    what, (long long)lay.total,
+                    staged ? "sx8_gemm_prefill_workspace_bytes" : "sx8_gemm_prefill_packed_workspace_bytes",
+                    (long long)workspace_bytes, workspace);
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
     const int64_t z_bytes = lay.z_bytes;
-    uint16_t* Xp = reinterpret_cast<uint16_t*>(ws + z_bytes * n_mats);
+    const uint16_t* Xp = staged ? reinterpret_cast<uint16_t*>(ws + z_bytes * n_mats) : packed->Xp;
     float* part = reinterpret_cast<float*>(ws + z_bytes * n_mats + lay.xp_bytes);
     GemmGroup g{};
     g.n_mats = n_mats;
@@ -1542,7 +1554,7 @@ int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, in
     for (int i = 0; i < n_mats; ++i) {
         GemmMat& m = g.m[i];
         m.w = ws_in[i];
-        m.Zhl = reinterpret_cast<const uint32_t*>(ws + z_bytes * i);
+        m.Zhl = staged ? reinterpret_cast<const uint32_t*>(ws + z_bytes * i) : packed->Zhl[i];
         m.Y = Ys[i];
         m.N = (int)Ns[i];
         m.nb = (int)((Ns[i] + kBN - 1) / kBN);
@@ -1564,9 +1576,12 @@ int32_t run_gemm(const char* what, const uint16_t* X, int64_t M, int64_t ldx, in
         hipLaunchKernelGGL(k_z_hl, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, Z, n,
                            reinterpret_cast<uint32_t*>(ws));
     }
-    int32_t rc = silu_g ? compute_z_silu(silu_g, silu_u, M, ldx, K, zs, n_cb, Xp, st)
-                        : compute_z_sets(X, M, ldx, K, zs, n_cb, true, Xp, st);
-    if (rc != SX8_OK) return rc;
+    if (staged) {
+        uint16_t* xp_ws = reinterpret_cast<uint16_t*>(ws + z_bytes * n_mats);
+        const int32_t rc = silu_g ? compute_z_silu(silu_g, silu_u, M, ldx, K, zs, n_cb, xp_ws, st)
+                                  : compute_z_sets(X, M, ldx, K, zs, n_cb, true, xp_ws, st);
+        if (rc != SX8_OK) return rc;
+    }
     if constexpr (kSplit) {
         launch_hb<true, true, 6>(p, st, Xp, M, g, n_cb, part);
     } else if (zm == ZMode::kNone) {
@@ -1940,6 +1955,56 @@ extern "C" int32_t sx8_gemm_prefill_group_deferred(const uint16_t* X, int64_t M,
     const int32_t rc = group_impl(what, X, M, ldx, K, n_mats, hdrs, levels, hdr_bytes, bases, scales, Ns, n_cb,
                                   Ys, workspace, workspace_bytes, stream, &pend);
     if (rc != SX8_OK) return rc;
+    return report_pending(what, pend, parts, n_parts, slice);
+}
+
+extern "C" int64_t sx8_gemm_prefill_packed_workspace_bytes(int64_t M, int32_t n_mats, const int64_t* Ns,
+                                                           int64_t n_cb) {
+    if (M <= 0 || n_cb <= 0 || !Ns || n_mats < 1 || n_mats > kMaxGemmGroup || M > 0x7FFFFFFF) return -1;
+    for (int i = 0; i < n_mats; ++i)
+        if (Ns[i] <= 0) return -1;
+    int64_t Ntot = 0, NB = 0;
+    if (!group_width(n_mats, Ns, Ntot, NB)) return -1;
+    const Plan p = plan_gemm(M, Ntot, NB, n_cb);
+    return ws_layout(p, M, Ntot, n_cb, n_mats, true, false).total;
+}
+
+extern "C" int32_t sx8_gemm_prefill_packed(const uint16_t* Xp, const uint32_t* const* Zhl, int64_t M, int64_t K,
+                                           int32_t n_mats, const uint8_t* const* hdrs,
+                                           const uint8_t* const* levels, int32_t hdr_bytes, const int64_t* Ns,
+                                           int64_t n_cb, float* const* Ys, void* workspace,
+                                           int64_t workspace_bytes, float** parts, int32_t* n_parts,
+                                           int64_t* slice, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_gemm_prefill_packed";
+    if (!Xp || !Zhl || !hdrs || !levels || !Ns || !Ys) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    const int n_out = (parts != nullptr) + (n_parts != nullptr) + (slice != nullptr);
+    if (n_out != 0 && n_out != 3)
+        return fail(SX8_ERR_INVALID, "%s: give all three of parts, n_parts, slice or none", what);
+    if (n_mats < 1 || n_mats > kMaxGemmGroup)
+        return fail(SX8_ERR_INVALID, "%s: n_mats must be 1..%d, got %d", what, kMaxGemmGroup, n_mats);
+    if (hdr_bytes != 6 && hdr_bytes != 8)
+        return fail(SX8_ERR_INVALID, "%s: hdr_bytes must be 6 or 8, got %d", what, hdr_bytes);
+    if (!aligned(Xp, 16)) return fail(SX8_ERR_INVALID, "%s: Xp must be 16-byte aligned", what);
+    WeightSrc w[kMaxGemmGroup]{};
+    for (int i = 0; i < n_mats; ++i) {
+        if (!hdrs[i] || !levels[i] || !Zhl[i] || !Ys[i])
+            return fail(SX8_ERR_INVALID, "%s: null pointer in matrix %d", what, i);
+        if (!aligned(hdrs[i], hdr_bytes == 8 ? 8 : 2) || !aligned(levels[i], 8) || !aligned(Ys[i], 4) ||
+            !aligned(Zhl[i], 16))
+            return fail(SX8_ERR_INVALID, "%s: misaligned pointer in matrix %d", what, i);
+        const int32_t rc = check_shape(what, M, K, K, Ns[i], n_cb);
+        if (rc != SX8_OK) return rc;
+        w[i].hdr = hdrs[i];
+        w[i].levels = levels[i];
+    }
+    const PackedIn in{Xp, Zhl};
+    PendingSums pend{};
+    const int32_t rc = run_gemm<false>(what, nullptr, M, K, K, n_mats, w, hdr_bytes, ZMode::kPacked, nullptr,
+                                       nullptr, nullptr, Ns, n_cb, Ys, workspace, workspace_bytes,
+                                       as_stream(stream), nullptr, nullptr, INT64_MAX, n_out ? &pend : nullptr,
+                                       &in);
+    if (rc != SX8_OK || !n_out) return rc;
     return report_pending(what, pend, parts, n_parts, slice);
 }
 

@@ -181,7 +181,9 @@ class SX8Decoder(nn.Module):
         pb = {"T": T, "resid": torch.empty(T, H, **f32), "h": torch.empty(T, H, **f16),
               "q": torch.empty(T, nh * hd, **f32), "k": torch.empty(T, nk * hd, **f32),
               "v": torch.empty(T, nk * hd, **f32), "qh": torch.empty(T, nh, hd, **f16),
-              "a": torch.empty(T, nh * hd, **f16),
+              # the attention output as the o projection's packed GEMM operands
+              "xp": torch.empty((T + 31) // 32 * (nh * hd // 32) * 1024, dtype=torch.int16, device=dev),
+              "zhl": torch.empty(T * (nh * hd // 32) * 4, dtype=torch.int16, device=dev),
               "o": torch.empty(T, H, **f32), "g": torch.empty(T, I, **f32), "u": torch.empty(T, I, **f32),
               "d": torch.empty(T, H, **f32),
               "pos0": torch.zeros(1, dtype=torch.int64, device=dev),
@@ -226,6 +228,17 @@ class SX8Decoder(nn.Module):
         return parts.value, n_parts.value, slc.value
 
     @staticmethod
+    def _gemm_packed_deferred(args, Xp, Zhl, M, K, ws, st):
+        """The prefill GEMM of one matrix on the packed X and Zhl its producer wrote
+        (sx8_gemm_prefill_packed), the split-K sum left to the consumer: (parts, n_parts, slice)."""
+        n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
+        parts, n_parts, slc = ctypes.c_void_p(), ctypes.c_int32(), ctypes.c_int64()
+        _L.call("sx8_gemm_prefill_packed", _L.ptr(Xp), (ctypes.c_void_p * 1)(Zhl.data_ptr()), M, K, n, hdrs, lvls, 6,
+                ns, n_cb, ys, _L.ptr(ws), ws.numel(), ctypes.addressof(parts), ctypes.addressof(n_parts),
+                ctypes.addressof(slc), st)
+        return parts.value, n_parts.value, slc.value
+
+    @staticmethod
     def _gemm(lin, X, Y, ws, st):
         """Y (M, N) f32 = X (M, K) fp16 . W^T through sx8_gemm_prefill."""
         hdr, lvl, bas, sca = lin._t44
@@ -238,7 +251,8 @@ class SX8Decoder(nn.Module):
         """prefill() with the library ops over the T prompt rows: add + RMSNorm
         (sx8_dec_add_rmsnorm, M = T), the prefill GEMMs into preallocated buffers, q/k
         norm + RoPE + KV-cache write (sx8_dec_qk_rope_cache_rows), causal attention over
-        the cache rows (sx8_dec_attn_prefill), SiLU * up inside the down GEMM
+        the cache rows writing the o projection's packed GEMM operands
+        (sx8_dec_attn_prefill_packed, sx8_gemm_prefill_packed), SiLU * up inside the down GEMM
         (sx8_dec_gemm_silu) and the final norm inside the lm_head GEMV.  The split-K sums
         of the q/k/v, o and down GEMMs (all but the last layer's) are added by the kernels
         that read those outputs (the *_deferred GEMM calls and the *_parts consumers), the
@@ -271,9 +285,11 @@ class SX8Decoder(nn.Module):
                     P(ly.k_norm), P(self.cos), P(self.sin), P(pb["pos0"]), T, P(pb["qh"]),
                     P(self.k_cache[li]), P(self.v_cache[li]), nh, nk, hd, self.max_len, eps, qp[0], qp[1], qp[2],
                     st)
-            _L.call("sx8_dec_attn_prefill", P(pb["qh"]), P(self.k_cache[li]), P(self.v_cache[li]), P(pb["a"]),
-                    T, 0, nh, nk, hd, self.max_len, 1.0 / math.sqrt(hd), st)
-            op = self._gemm_group_deferred(pb["groups"][li][2], pb["a"], pb["ws"], st)     # o
+            # attention writes the o projection's packed X and Zhl itself (no pass over its output)
+            _, _, obas, osca = ly.o._t44
+            _L.call("sx8_dec_attn_prefill_packed", P(pb["qh"]), P(self.k_cache[li]), P(self.v_cache[li]), T, 0, nh,
+                    nk, hd, self.max_len, 1.0 / math.sqrt(hd), P(obas), P(osca), P(pb["xp"]), P(pb["zhl"]), st)
+            op = self._gemm_packed_deferred(pb["groups"][li][2], pb["xp"], pb["zhl"], T, nh * hd, pb["ws"], st)
             _L.call("sx8_dec_add_rmsnorm_parts", P(pb["resid"]), P(pb["o"]), None, P(ly.post_norm), P(pb["h"]), T,
                     H, eps, op[0], op[1], op[2], st)
             self._gemm_group(pb["groups"][li][1], pb["h"], pb["ws"], st)      # gate, up: one call

@@ -215,3 +215,46 @@ def test_deferred_sum_refusals_on_host(hiplib):
     assert rope(p, 8, need) == 1 and "n_parts" in _err(L)
     assert rope(NULL, 1, need) == 1
     assert rope(p, 2, need - 1) == 1 and "slice" in _err(L)
+
+
+def test_packed_operand_refusals_on_host(hiplib):
+    """sx8_gemm_prefill_packed and sx8_dec_attn_prefill_packed refuse bad arguments before any
+    launch; the packed workspace holds the split-K partials only (none for an unsplit plan)."""
+    L = hiplib
+    V = ctypes.c_void_p
+    p = V(1 << 24)
+    M, K = 512, 4096
+    P1 = ctypes.c_void_p * 1
+    ns = (ctypes.c_int64 * 1)(2560)
+    ptrs = P1(1 << 20)
+    n_out = ctypes.c_int32()
+
+    def gemm(xp, ws, nbytes, parts, n_parts, slc, Ns=ns, n_mats=1, hb=6):
+        return L.sx8_gemm_prefill_packed(xp, ptrs, M, K, n_mats, ptrs, ptrs, hb, Ns, 128, ptrs, ws, nbytes,
+                                         parts, n_parts, slc, NULL)
+
+    assert gemm(p, p, 1 << 30, p, NULL, NULL) == 1 and "all three" in _err(L)
+    assert gemm(p, p, 1 << 30, NULL, ctypes.addressof(n_out), NULL) == 1 and "all three" in _err(L)
+    assert gemm(V((1 << 24) + 8), p, 1 << 30, NULL, NULL, NULL) == 1 and "aligned" in _err(L)
+    assert gemm(NULL, p, 1 << 30, NULL, NULL, NULL) == 1 and "null" in _err(L)
+    assert gemm(p, p, 1 << 30, NULL, NULL, NULL, n_mats=5) == 1 and "n_mats" in _err(L)
+    assert gemm(p, p, 1 << 30, NULL, NULL, NULL, hb=7) == 1 and "hdr_bytes" in _err(L)
+    # o at M = 512 splits K into 4 ranges: 3 partial slices of M x N floats
+    need = L.sx8_gemm_prefill_packed_workspace_bytes(M, 1, ns, 128)
+    assert need == 3 * M * 2560 * 4
+    assert gemm(p, NULL, 0, NULL, NULL, NULL) == 1 and "workspace" in _err(L)
+    assert gemm(p, p, need - 256, NULL, NULL, NULL) == 1 and "workspace" in _err(L)
+    gu = (ctypes.c_int64 * 2)(9728, 9728)     # gate/up at M = 512: unsplit 512-row tiles
+    assert L.sx8_gemm_prefill_packed_workspace_bytes(M, 2, gu, 80) == 0
+    assert L.sx8_gemm_prefill_packed_workspace_bytes(0, 1, ns, 128) == -1
+    assert L.sx8_gemm_prefill_packed_workspace_bytes(M, 1, ns, 128) <= L.sx8_gemm_prefill_workspace_bytes(
+        M, 1, ns, 128)
+
+    def attn(basis, xp, T=512, start=0, nh=32, nk=8, hd=128):
+        return L.sx8_dec_attn_prefill_packed(p, p, p, T, start, nh, nk, hd, 1024, ctypes.c_float(0.088), basis, p,
+                                             xp, p, NULL)
+
+    assert attn(NULL, p) == 1 and "null" in _err(L)
+    assert attn(p, V((1 << 24) + 4)) == 1 and "aligned" in _err(L)
+    assert attn(p, p, T=1000, start=100) == 1 and "bad shape" in _err(L)
+    assert attn(p, p, nh=24, nk=8) == 1 and "bad shape" in _err(L)

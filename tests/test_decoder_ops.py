@@ -867,3 +867,94 @@ def test_gemm_silu_deferred_sums_into_add_rmsnorm(hiplib, cuda):
     assert n_parts == 5 and slc == M * N
     assert torch.equal(rb.cpu(), ra.cpu())
     assert torch.equal(hb16.cpu().view(torch.int16), ha.cpu().view(torch.int16))
+
+
+def _packed_operands_ref(x16, Zf, n_cb):
+    """The packed X and Zhl (include/sx8_hip.h, sx8_gemm_prefill_packed) of an fp16 (T, 32 n_cb)
+    matrix given as uint16 and its float32 Z (T, n_cb, 2), built in numpy: X[32 G + r][32 kb +
+    16 hf + 8 st + i] at chunk (G, kb), k-step st, lane 32 hf + r, value i (rows past T
+    zero); Z as (fp16(z), fp16(z - fp16(z)))."""
+    T = x16.shape[0]
+    Gs = (T + 31) // 32
+    X = np.zeros((Gs * 32, n_cb * 32), np.uint16)
+    X[:T] = x16
+    Xp = X.reshape(Gs, 32, n_cb, 2, 2, 8).transpose(0, 2, 4, 3, 1, 5)   # G, kb, st, hf, r, i
+    hi = Zf.astype(np.float16)
+    lo = (Zf - hi.astype(np.float32)).astype(np.float16)
+    return np.ascontiguousarray(Xp).ravel(), np.stack([hi, lo], -1).view(np.uint16).ravel()
+
+
+@pytest.mark.parametrize("nh,nk,hd,L,T,start,N,hb", [
+    (32, 8, 128, 1024, 512, 0, 2560, 6),   # the decoder's prompt pass: o at T = 512 (4 K ranges)
+    (32, 8, 128, 1200, 1100, 50, 640, 8),  # G = 4 with four heads per work-group, ragged tile
+    (8, 1, 128, 200, 70, 3, 300, 6),       # G = 8 (one wave set)
+    (16, 16, 64, 300, 33, 0, 96, 8),       # G = 1 at hd 64
+    (2, 1, 128, 160, 40, 5, 1001, 6),      # G = 2 at hd 128
+    (32, 8, 128, 64, 1, 0, 256, 6),        # one row
+])
+def test_attention_packed_operands(hiplib, cuda, nh, nk, hd, L, T, start, N, hb):
+    """sx8_dec_attn_prefill_packed writes, bit for bit, the packed X and Zhl that the prefill
+    GEMM's own pass makes from sx8_dec_attn_prefill's output (packed rows padded with zeros,
+    Z in the reference's tree order: sx8_compute_z), every byte of both buffers; and
+    sx8_gemm_prefill_packed on them gives sx8_gemm_prefill_group's output bit for bit, with
+    the split-K sum inside the call and left to the caller."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    K = nh * hd
+    n_cb = K // 32
+    g = torch.Generator().manual_seed(nh * 17 + T + start)
+    q = torch.randn(T, nh, hd, generator=g).half().to(cuda)
+    kc = torch.full((nk, L, hd), float("nan")).half()
+    vc = torch.full((nk, L, hd), float("nan")).half()
+    kc[:, :start + T] = torch.randn(nk, start + T, hd, generator=g).half()
+    vc[:, :start + T] = torch.randn(nk, start + T, hd, generator=g).half()
+    kd, vd = kc.to(cuda), vc.to(cuda)
+    ts = _mats(cuda, [N], K, 900 + T, hb)
+    hdr, lvl, bas, sca = ts[0]
+    scale = 1.0 / math.sqrt(hd)
+    print("attn packed", nh, nk, hd, L, T, start, N, hb, flush=True)
+    out = torch.empty(T, K, dtype=torch.float16, device=cuda)
+    _L.call("sx8_dec_attn_prefill", P(q), P(kd), P(vd), P(out), T, start, nh, nk, hd, L, scale, st)
+    Gs = (T + 31) // 32
+    Xp = torch.full((Gs * n_cb * 1024,), 0x7E7E, dtype=torch.int16, device=cuda)   # sentinel bytes
+    Zhl = torch.full((T * n_cb * 4,), 0x7E7E, dtype=torch.int16, device=cuda)
+    _L.call("sx8_dec_attn_prefill_packed", P(q), P(kd), P(vd), T, start, nh, nk, hd, L, scale, P(bas), P(sca),
+            P(Xp), P(Zhl), st)
+    Zf = torch.empty(T, n_cb, 2, device=cuda)
+    _L.call("sx8_compute_z", P(out), T, K, P(bas), P(sca), n_cb, P(Zf), st)
+    torch.cuda.synchronize()
+    xp_ref, zhl_ref = _packed_operands_ref(out.cpu().view(torch.int16).numpy().view(np.uint16),
+                                           Zf.cpu().numpy(), n_cb)
+    assert np.array_equal(Xp.cpu().numpy().view(np.uint16), xp_ref)
+    assert np.array_equal(Zhl.cpu().numpy().view(np.uint16), zhl_ref)
+    # the GEMM on the producer's operands
+    ws, nb = _L.gemm_workspace(T, [N], n_cb, cuda)
+    ya = torch.empty(T, N, device=cuda)
+    ga = _group(ts, [N], n_cb, [ya])
+    _L.call("sx8_gemm_prefill_group", P(out), T, K, K, ga[0], ga[1], ga[2], hb, ga[3], ga[4], ga[5], ga[6], ga[7],
+            P(ws), nb, st)
+    nbp = int(_L.lib().sx8_gemm_prefill_packed_workspace_bytes(T, 1, (ctypes.c_int64 * 1)(N), n_cb))
+    assert 0 <= nbp <= nb
+    wsp = torch.empty(max(nbp, 256), dtype=torch.uint8, device=cuda)
+    zp = (ctypes.c_void_p * 1)(Zhl.data_ptr())
+    yb = torch.empty(T, N, device=cuda)
+    gb = _group(ts, [N], n_cb, [yb])
+    _L.call("sx8_gemm_prefill_packed", P(Xp), zp, T, K, 1, gb[1], gb[2], hb, gb[5], n_cb, gb[7],
+            P(wsp) if nbp else None, nbp, None, None, None, st)
+    yc = torch.empty(T, N, device=cuda)
+    gc = _group(ts, [N], n_cb, [yc])
+    parts, n_parts, slc = _deferred("sx8_gemm_prefill_packed", P(Xp), zp, T, K, 1, gc[1], gc[2], hb, gc[5], n_cb,
+                                    gc[7], P(wsp) if nbp else None, nbp, st)
+    yd = yc.clone()
+    if n_parts:                        # the slices sit in the workspace; added in slice order
+        assert slc == T * N
+        off = (parts - wsp.data_ptr()) // 4
+        f = wsp.view(torch.float32)
+        for s in range(n_parts):
+            yd += f[off + s * slc:off + s * slc + T * N].view(T, N)
+    torch.cuda.synchronize()
+    print("   plan", _L.gemm_plan(T, [N], n_cb), "n_parts", n_parts, flush=True)
+    assert torch.equal(ya.cpu(), yb.cpu())
+    assert torch.equal(ya.cpu(), yd.cpu())
