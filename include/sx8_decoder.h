@@ -118,6 +118,27 @@ int32_t sx8_dec_gemm_silu_deferred(const float* g, const float* u, int64_t M, in
                                    float* Y, void* workspace, int64_t workspace_bytes, float** parts,
                                    int32_t* n_parts, int64_t* slice, void* stream);
 
+/* The prompt pass's MLP up to the down projection's input: the gate and up prefill GEMMs
+ * of X (M, K) fp16 (hdrs / levels / bases / scales: [gate, up], N output columns each,
+ * n_cb K blocks) and x = fp16(silu(g) * u), written straight as the down projection's
+ * packed prefill-GEMM operands (sx8_gemm_prefill_packed): Xp (ceil(M / 32) * ceil(N / 32)
+ * * 2048 bytes) and Zhl (M * ceil(N / 32) * 8 bytes) for the down projection's basis
+ * (ceil(N / 32), 2, 32) and scales.  When the plan runs whole 512-row tiles, one GEMM
+ * launch takes 64 gate and the same 64 up columns per tile and its epilogue writes the
+ * operands (no float32 g and u in memory); otherwise the group GEMM writes g and u into the
+ * workspace and a pack pass reads them back.  Both forms give the same bits, the bits of
+ * sx8_gemm_prefill_group + sx8_dec_silu_mul + the down GEMM's own pass over x.  Workspace:
+ * sx8_dec_gemm_gateup_silu_workspace_bytes.  No reference counterpart (the reference's MLP
+ * runs gate, up, SiLU * up and down as separate torch ops, scripts/infer_sx8.py). */
+int32_t sx8_dec_gemm_gateup_silu(const uint16_t* X, int64_t M, int64_t K, const uint8_t* const* hdrs,
+                                 const uint8_t* const* levels, int32_t hdr_bytes, const float* const* bases,
+                                 const float* const* scales, int64_t N, int64_t n_cb, const float* down_basis,
+                                 const float* down_scales, uint16_t* Xp, uint32_t* Zhl, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of sx8_dec_gemm_gateup_silu, or -1 for bad arguments. */
+int64_t sx8_dec_gemm_gateup_silu_workspace_bytes(int64_t M, int64_t N, int64_t n_cb);
+
 /* Causal attention of T prompt rows (prefill): q (T, nh, hd) fp16 (normalized and
  * rotated, as sx8_dec_qk_rope_cache_rows writes it), caches (nk, L, hd) fp16 holding
  * keys/values 0 .. start + T - 1; row i (position start + i) attends keys 0 .. start + i.

@@ -40,7 +40,7 @@ extern "C" {
  * 4: deferred split-K sums: sx8_gemm_prefill_group_deferred, sx8_dec_gemm_silu_deferred and
  *    the consumers sx8_dec_add_rmsnorm_parts, sx8_dec_qk_rope_cache_rows_parts
  * 5: producer-written GEMM operands: sx8_gemm_prefill_packed(_workspace_bytes),
- *    sx8_dec_attn_prefill_packed */
+ *    sx8_dec_attn_prefill_packed, sx8_dec_gemm_gateup_silu(_workspace_bytes) */
 #define SX8_ABI_VERSION 5
 
 #define SX8_OK 0

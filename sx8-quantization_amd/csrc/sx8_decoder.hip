@@ -714,7 +714,7 @@ __global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ g, c
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
     const float x = g[i];
-    out[i] = f2h(x / (1.0f + __expf(-x)) * u[i]);
+    out[i] = f2h(sx8_silu_mul(x, u[i]));
 }
 
 // tok = argmax(logits) (first index among equal maxima; NaN entries are skipped), *pos += 1.
@@ -795,11 +795,7 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float* __restrict
 constexpr int kApVRow = 40;      // halves per LDS row of V^T: 32 keys + 8 pad (conflict-free reads)
 constexpr int kApKRow = 136;     // halves per LDS row of K: up to 128 + 8 pad (conflict-free reads)
 
-__device__ __forceinline__ float lane_swap32(float v) {
-    const uint32_t u = __builtin_bit_cast(uint32_t, v);
-    const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    return __builtin_bit_cast(float, (threadIdx.x & 32) ? sw[0] : sw[1]);
-}
+__device__ __forceinline__ float lane_swap32(float v) { return sx8_lane_swap32(v); }
 
 // Wave sets per work-group: two while 2 G waves (two per SIMD) keep their registers.
 template <int G>
@@ -815,63 +811,6 @@ struct ApPack {
     uint32_t* Zhl;
     int n_cb;
 };
-
-// The packed operands of one 32-dim fragment of a query row's attention output, bit for
-// bit what k_compute_z<true, true> writes from the fp16 output row: x = fp16(v) into the
-// packed X chunk of (row group, K block) (k-step st, MFMA lane 32 hf + r, 8 values
-// X[r][32 kb + 16 hf + 8 st ..]; rows past T as zeros), and the row's Z0, Z1 of the K block
-// in the reference's tree order -- products x_t b_t, pairs (t, t + 16), then offsets 8, 4,
-// 2, 1 (cuda/sx8_decode1_v3.cu:53-63) -- times the scales, as split fp16 hi / lo pairs.  The
-// lane holds t = 8 gq + 4 h + e (gq, e < 4), so offsets 16 and 8 stay in the lane and
-// offset 4 is one swap with lane ^ 32.  bl: the block's 64 basis values (LDS).
-__device__ __forceinline__ void ap_pack_fragment(const float (&v)[16], bool row_ok, int c, int h, const float* bl,
-                                                 float2 sc, uint16_t* xdst, uint32_t* zdst) {
-#pragma clang fp contract(off)
-    uint32_t xw[8];
-    float xf[16];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint16_t lo = row_ok ? f2h(v[2 * i]) : (uint16_t)0, hi = row_ok ? f2h(v[2 * i + 1]) : (uint16_t)0;
-        xw[i] = (uint32_t)lo | ((uint32_t)hi << 16);
-        xf[2 * i] = h2f(lo);
-        xf[2 * i + 1] = h2f(hi);
-    }
-#pragma unroll
-    for (int gq = 0; gq < 4; ++gq)
-        *reinterpret_cast<uint2*>(xdst + (gq & 1) * 512 + ((gq >> 1) * 32 + c) * 8 + 4 * h) =
-            make_uint2(xw[2 * gq], xw[2 * gq + 1]);
-    float z[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const float4* b = reinterpret_cast<const float4*>(bl + 32 * j + 4 * h);
-        float pr[16];
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-            const float4 bb = b[2 * gq];
-            pr[4 * gq] = xf[4 * gq] * bb.x;
-            pr[4 * gq + 1] = xf[4 * gq + 1] * bb.y;
-            pr[4 * gq + 2] = xf[4 * gq + 2] * bb.z;
-            pr[4 * gq + 3] = xf[4 * gq + 3] * bb.w;
-        }
-        float p[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float t16 = pr[e] + pr[8 + e];          // t = 4 h + e, with t + 16
-            const float u16 = pr[4 + e] + pr[12 + e];     // t + 8, with t + 24
-            p[e] = t16 + u16;                             // offset 8
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) p[e] = p[e] + lane_swap32(p[e]);   // offset 4 (h = 0: t = e)
-        p[0] = p[0] + p[2];
-        p[1] = p[1] + p[3];
-        z[j] = (j ? sc.y : sc.x) * (p[0] + p[1]);
-        // z is rounded to float32 before its fp16 split, as in k_compute_z: without the pin
-        // the compiler folds the product into the conversion (one v_fma_mixlo_f16, a single
-        // rounding of scale * sum to fp16), which differs on ties
-        asm volatile("" : "+v"(z[j]));
-    }
-    if (row_ok && h == 0) *reinterpret_cast<uint2*>(zdst) = make_uint2(sx8_split_hl(z[0]), sx8_split_hl(z[1]));
-}
 
 template <int HD, int GW, int NS>
 struct ApLds {
@@ -1089,7 +1028,7 @@ __global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* _
     // every lane of the wave takes part (the Z tree swaps lane halves), rows past T pack zeros
     auto emit_packed = [&](int n, const float (&v)[16]) {
         const int kb = kbw + g * NT + n;
-        ap_pack_fragment(v, qi < T, c, h, reinterpret_cast<const float*>(apb) + (g * NT + n) * 64, aps[g * NT + n],
+        sx8_pack_fragment(v, qi < T, c, h, reinterpret_cast<const float*>(apb) + (g * NT + n) * 64, aps[g * NT + n],
                          pk.Xp + ((int64_t)blockIdx.x * pk.n_cb + kb) * 1024,
                          pk.Zhl + ((int64_t)qi * pk.n_cb + kb) * 2);
     };

@@ -128,3 +128,84 @@ __device__ __forceinline__ void sx8_load_hdr(const uint8_t* __restrict__ hdr, in
         coeff = cc >> 8;
     }
 }
+
+// x = silu(g) * u = g * rcp(1 + e^-g) * u in float32 (v_exp_f32, v_rcp_f32: the reciprocal
+// is within 1 ulp, where a correctly rounded division costs nine more instructions; x is
+// rounded to fp16 afterwards, 13 bits coarser), the product rounded to float32 before any
+// fp16 conversion: the pin keeps the compiler from folding it into the conversion (one
+// v_fma_mixlo_f16, a single rounding), which it does in some kernels and not in others.
+// Every producer of the MLP's fp16 input -- the SiLU launch, the GEMV table build, the pair
+// GEMV's epilogue, the prefill pack pass and the prefill GEMM's gate/up epilogue -- goes
+// through here, so they give the same bits.
+__device__ __forceinline__ float sx8_silu_mul(float g, float u) {
+    float x = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+// v with lanes 0-31 and 32-63 swapped (v_permlane32_swap).
+__device__ __forceinline__ float sx8_lane_swap32(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto sw = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 32) ? sw[0] : sw[1]);
+}
+
+// The prefill GEMM's packed operands (packed X and Zhl, the layouts of
+// sx8_gemm_prefill_packed) of one 32-value K block of one row, from a 32 x 32 MFMA output
+// fragment's lane layout: lane 32 h + c holds the row's values t = 8 gq + 4 h + e (gq, e <
+// 4) in v[4 gq + e].  x = fp16(v) (zeros for rows past the end) goes into the packed chunk
+// (k-step st, lane 32 hf + c, 8 values X[c][16 hf + 8 st ..]), and Z0, Z1 of the block in
+// the reference's tree order -- products x_t b_t, pairs (t, t + 16), then offsets 8, 4, 2,
+// 1 (cuda/sx8_decode1_v3.cu:53-63) -- times the scales, as split fp16 hi / lo pairs (lane h
+// = 0 stores).  Offsets 16 and 8 stay in the lane, offset 4 is one swap of lane halves, so
+// every lane of the wave must take part.  Bit for bit what k_compute_z<true, true> writes
+// from the fp16 row.  bl: the block's 64 basis values (both vectors), sc: its two scales;
+// xdst: the (row group, K block) chunk; zdst: the row's Zhl entry of the block.
+__device__ __forceinline__ void sx8_pack_fragment(const float (&v)[16], bool row_ok, int c, int h,
+                                                  const float* bl, float2 sc, uint16_t* xdst, uint32_t* zdst) {
+#pragma clang fp contract(off)
+    uint32_t xw[8];
+    float xf[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint16_t lo = row_ok ? __builtin_bit_cast(uint16_t, (_Float16)v[2 * i]) : (uint16_t)0;
+        const uint16_t hi = row_ok ? __builtin_bit_cast(uint16_t, (_Float16)v[2 * i + 1]) : (uint16_t)0;
+        xw[i] = (uint32_t)lo | ((uint32_t)hi << 16);
+        xf[2 * i] = sx8_h2f(lo);
+        xf[2 * i + 1] = sx8_h2f(hi);
+    }
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq)
+        *reinterpret_cast<uint2*>(xdst + (gq & 1) * 512 + ((gq >> 1) * 32 + c) * 8 + 4 * h) =
+            make_uint2(xw[2 * gq], xw[2 * gq + 1]);
+    float z[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const float4* b = reinterpret_cast<const float4*>(bl + 32 * j + 4 * h);
+        float pr[16];
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+            const float4 bb = b[2 * gq];
+            pr[4 * gq] = xf[4 * gq] * bb.x;
+            pr[4 * gq + 1] = xf[4 * gq + 1] * bb.y;
+            pr[4 * gq + 2] = xf[4 * gq + 2] * bb.z;
+            pr[4 * gq + 3] = xf[4 * gq + 3] * bb.w;
+        }
+        float p[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float t16 = pr[e] + pr[8 + e];          // t = 4 h + e, with t + 16
+            const float u16 = pr[4 + e] + pr[12 + e];     // t + 8, with t + 24
+            p[e] = t16 + u16;                             // offset 8
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) p[e] = p[e] + sx8_lane_swap32(p[e]);   // offset 4 (h = 0: t = e)
+        p[0] = p[0] + p[2];
+        p[1] = p[1] + p[3];
+        z[j] = (j ? sc.y : sc.x) * (p[0] + p[1]);
+        // z rounded to float32 before its fp16 split, as in k_compute_z (see sx8_silu_mul)
+        asm volatile("" : "+v"(z[j]));
+    }
+    if (row_ok && h == 0) *reinterpret_cast<uint2*>(zdst) = make_uint2(sx8_split_hl(z[0]), sx8_split_hl(z[1]));
+}
+

@@ -931,10 +931,25 @@ __device__ __forceinline__ void dec1_finish(GemmSmem& sm, const DecPrep1& p, int
     }
 }
 
-template <bool kSplit, int HB, bool kPca>
+// kPair (the MLP's gate and up projections, g.m[0] and g.m[1], N columns each): a tile's
+// 128 columns are 64 gate columns and the same 64 up columns (tile p: intermediate indices
+// 64 p .. 64 p + 63; fragments 0, 1 gate, 2, 3 up), so each lane holds g and u of the same
+// (row, index) and the epilogue writes x = fp16(silu(g) u) straight into the down
+// projection's packed operands (SiluOut: the packed X and Zhl of sx8_gemm_prefill_packed for
+// the down projection's basis rows and scales, n_cb = its K blocks).  Whole tiles only (no
+// K split).  Waves of even index decode gate columns, odd ones up columns.
+struct SiluOut {
+    const float* basis;
+    const float* scales;
+    uint16_t* Xp;
+    uint32_t* Zhl;
+    int n_cb;
+};
+
+template <bool kSplit, int HB, bool kPca, bool kPair = false>
 __global__ __launch_bounds__(kW2Threads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_w2(
     const uint16_t* __restrict__ Xp, int M, const GemmGroup g, int n_cb, int Tf, int St, int kbs,
-    float* __restrict__ part) {
+    float* __restrict__ part, const SiluOut so) {
     constexpr int MF = kW2MF;
     __shared__ GemmSmem sm;
     const int tid = threadIdx.x;
@@ -955,13 +970,17 @@ __global__ __launch_bounds__(kW2Threads) __attribute__((amdgpu_waves_per_eu(2, 2
     }
     int nb = t % NB;
     const int mb = t / NB;
-    const int mi = group_mat(g, nb);
-    const WeightSrc w = g.m[mi].w;
+    const int mi = kPair ? 0 : group_mat(g, nb);
+    // kPair: this wave decodes columns of the gate (even waves) or up (odd) matrix
+    // (wave-uniform, but the compiler cannot tell from the thread index: readfirstlane keeps
+    // the weight pointers, and so the buffer resources, in scalar registers)
+    const int wm = kPair ? sx8_uniform(wave & 1) : mi;
+    const WeightSrc w = g.m[wm].w;
     const uint32_t* __restrict__ Zhl = g.m[mi].Zhl;
     float* __restrict__ Y = g.m[mi].Y;
     const int N = g.m[mi].N;
     const int m0 = mb * kW1BM;
-    const int n0 = nb * kBN;
+    const int n0 = nb * (kPair ? kBN / 2 : kBN);   // kPair: first intermediate index
     const int hf = lane >> 5, r = lane & 31;
     const int dc = tid & 127, dsb = tid >> 7;    // decode: column and sub-block
 
@@ -986,10 +1005,12 @@ __global__ __launch_bounds__(kW2Threads) __attribute__((amdgpu_waves_per_eu(2, 2
         ls.hdr = make_rsrc(w.hdr, n_blk * HB);
         ls.lv = make_rsrc(w.levels, n_blk * 24);
     }
-    ls.nn = min(n0 + dc, N - 1);
+    ls.nn = min(n0 + (kPair ? (dc & 63) : dc), N - 1);
     ls.h = 0;
     ls.x = make_rsrc(Xp, (int64_t)((M + 31) / 32) * n_cb * 2048);
     if constexpr (kPca) ls.z = make_rsrc(Zhl, (int64_t)M * n_cb * 8);
+    // kPair: the up matrix's Zhl (fragments 2, 3)
+    const sx8_rsrc z_up = make_rsrc(kPair ? g.m[1].Zhl : Zhl, kPca && kPair ? (int64_t)M * n_cb * 8 : 0);
 #pragma unroll
     for (int f = 0; f < MF; ++f) {
         const int g32 = (m0 >> 5) + wave * MF + f;
@@ -997,6 +1018,23 @@ __global__ __launch_bounds__(kW2Threads) __attribute__((amdgpu_waves_per_eu(2, 2
         const int row = m0 + wave * 32 * MF + 32 * f + r;
         ls.z_off[f] = (int)(((int64_t)row * n_cb + 2 * hf) * 8);
     }
+    // kPair: the down projection's basis rows and scales of this tile's two K blocks, staged
+    // in LDS with the prologue's barrier for the epilogue (threads 0-31 one float4 each)
+    __shared__ float4 dbas[kPair ? 32 : 1];
+    __shared__ float2 dsca[kPair ? 2 : 1];
+    float4 dbv = make_float4(0.f, 0.f, 0.f, 0.f);
+    float2 dsv = make_float2(0.f, 0.f);
+    if constexpr (kPair) {
+        const int kbd = min((n0 >> 5) + (tid >> 4), so.n_cb - 1);      // (blocks past n_cb: unused)
+        if (tid < 32) dbv = reinterpret_cast<const float4*>(so.basis + (int64_t)kbd * 64)[tid & 15];
+        if (tid < 2) dsv = reinterpret_cast<const float2*>(so.scales)[min((n0 >> 5) + tid, so.n_cb - 1)];
+    }
+    auto load_za_up = [&](sx8_u32x4 (&zu)[MF], int gq) __attribute__((always_inline)) {
+#pragma unroll
+        for (int f = 0; f < MF; ++f)
+            zu[f] = __builtin_bit_cast(sx8_u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      z_up, ls.z_off[f] + gq * 32, 0, 0));
+    };
 
     sx8_float16v acc[MF][4];
 #pragma unroll
@@ -1012,6 +1050,7 @@ __global__ __launch_bounds__(kW2Threads) __attribute__((amdgpu_waves_per_eu(2, 2
     DecPrep1 P[2];
     sx8_u32x4 A[2][MF][2];
     sx8_u32x4 za[MF];
+    sx8_u32x4 zu[kPair ? MF : 1];
     {
         LaneRec1 r0, r1, r2;
         load_rec1<kSplit, HB>(r0, ls, N, kb0, dsb);
@@ -1020,6 +1059,7 @@ __global__ __launch_bounds__(kW2Threads) __attribute__((amdgpu_waves_per_eu(2, 2
         load_a<MF>(A[0], ls, kb0);
         load_a_step<MF>(A[1], ls, min(kb0 + 1, kb1 - 1), 0);
         if constexpr (kPca) load_za<MF>(za, ls, kb0 >> 2);
+        if constexpr (kPca && kPair) load_za_up(zu, kb0 >> 2);
         load_rec1<kSplit, HB>(R[3], ls, N, min(kb0 + 3, kb1 - 1), dsb);
         load_rec1<kSplit, HB>(R[0], ls, N, min(kb0 + 4, kb1 - 1), dsb);
         load_rec1<kSplit, HB>(R[1], ls, N, min(kb0 + 5, kb1 - 1), dsb);
@@ -1027,6 +1067,10 @@ __global__ __launch_bounds__(kW2Threads) __attribute__((amdgpu_waves_per_eu(2, 2
         dec1_finish<kPca>(sm, dec1_prep<kSplit>(r0, dsb), kb0, kb0 % 3, dc, dsb);
         dec1_finish<kPca>(sm, dec1_prep<kSplit>(r1, dsb), kb0 + 1, (kb0 + 1) % 3, dc, dsb);
         P[0] = dec1_prep<kSplit>(r2, dsb);
+        if constexpr (kPair) {
+            if (tid < 32) dbas[tid] = dbv;
+            if (tid < 2) dsca[tid] = dsv;
+        }
         lds_barrier();
     }
     const uint8_t* wbase = reinterpret_cast<const uint8_t*>(&sm.wt[0][0][0][lane]);
@@ -1086,17 +1130,23 @@ __global__ __launch_bounds__(kW2Threads) __attribute__((amdgpu_waves_per_eu(2, 2
         if constexpr (kPca) {
             if (pca) {
                 const int gq = kb >> 2;
-                sx8_half8 zh[MF];
+                sx8_half8 zh[MF], zh2[kPair ? MF : 1];
 #pragma unroll
                 for (int f = 0; f < MF; ++f) zh[f] = mask_za(za[f], n_cb, gq, hf);
+                if constexpr (kPair) {
+#pragma unroll
+                    for (int f = 0; f < MF; ++f) zh2[f] = mask_za(zu[f], n_cb, gq, hf);
+                }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const sx8_half8 cq = __builtin_bit_cast(sx8_half8, sm.pt[gq & 1][j][lane]);
 #pragma unroll
                     for (int f = 0; f < MF; ++f)
-                        acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cq, zh[f], acc[f][j], 0, 0, 0);
+                        acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(cq, kPair && j >= 2 ? zh2[f] : zh[f],
+                                                                           acc[f][j], 0, 0, 0);
                 }
                 load_za<MF>(za, ls, min(gq + 1, (kb1 - 1) >> 2));
+                if constexpr (kPair) load_za_up(zu, min(gq + 1, (kb1 - 1) >> 2));
             }
         }
         lds_barrier();
@@ -1112,6 +1162,33 @@ __global__ __launch_bounds__(kW2Threads) __attribute__((amdgpu_waves_per_eu(2, 2
     if (kb + 1 < kb1) body(kb + 1, A[1], A[0], R[0], P[1], P[0], kb + 2 == kb1);
     if (kb + 2 < kb1) body(kb + 2, A[0], A[1], R[1], P[0], P[1], true);
 
+    if constexpr (kPair) {
+        // x = fp16(silu(g) u) of rows m0 + 64 wave + 32 f + r and intermediate indices n0 +
+        // 32 jj + t: the down projection's K block n0 / 32 + jj, as its packed operands
+        // (indices past N pack zeros; row groups past the packed rows are not written)
+        const int Gs = (M + 31) >> 5;
+#pragma unroll
+        for (int f = 0; f < MF; ++f) {
+            const int G = (m0 >> 5) + wave * MF + f;
+            if (G >= Gs) continue;                       // uniform across the wave
+            const int row = 32 * G + r;
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int kb = (n0 >> 5) + jj;
+                if (kb >= so.n_cb) continue;             // uniform
+                float v[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int idx = n0 + 32 * jj + 8 * (i >> 2) + 4 * hf + (i & 3);
+                    v[i] = idx < N ? sx8_silu_mul(acc[f][jj][i], acc[f][jj + 2][i]) : 0.f;
+                }
+                sx8_pack_fragment(v, row < M, r, hf, reinterpret_cast<const float*>(dbas) + 64 * jj, dsca[jj],
+                                  so.Xp + ((int64_t)G * so.n_cb + kb) * 1024,
+                                  so.Zhl + ((int64_t)row * so.n_cb + kb) * 2);
+            }
+        }
+        return;
+    }
     // epilogue (as k_gemm_w1): partial tiles dense 512 x 128, else Y with bounds
     if (ks > 0) {
         float* pt = part + ((int64_t)(t - Tf) * (St - 1) + ks - 1) * (kW1BM * kBN);
@@ -1461,7 +1538,7 @@ void launch_hb(const Plan& p, hipStream_t st, const uint16_t* Xp, int64_t M, con
     const bool w2 = tuning().w2;
     if (p.w1 && w2)
         hipLaunchKernelGGL((k_gemm_w2<kSplit, HB, kPca>), dim3((unsigned)p.G), dim3(kW2Threads), 0, st,
-                           Xp, (int)M, g, (int)n_cb, p.Tf, p.St, p.kbs, part);
+                           Xp, (int)M, g, (int)n_cb, p.Tf, p.St, p.kbs, part, SiluOut{});
     else if (p.w1)
         hipLaunchKernelGGL((k_gemm_w1<kSplit, HB, kPca>), dim3((unsigned)p.G), dim3(kW1Threads), 0, st,
                            Xp, (int)M, g, (int)n_cb, p.Tf, p.St, p.kbs, part);
@@ -1956,6 +2033,132 @@ extern "C" int32_t sx8_gemm_prefill_group_deferred(const uint16_t* X, int64_t M,
                                   Ys, workspace, workspace_bytes, stream, &pend);
     if (rc != SX8_OK) return rc;
     return report_pending(what, pend, parts, n_parts, slice);
+}
+
+namespace {
+
+// The MLP's gate/up GEMM ending in the down projection's packed operands.  Fused form: a
+// plan of whole 512-row tiles over the paired tiling (ceil(N / 64) tiles of 64 gate + 64
+// up columns) runs k_gemm_w2<kPair>, whose epilogue writes x = fp16(silu(g) u) and its Zhl;
+// any other plan runs the gate/up group GEMM into float32 g, u in the workspace and the
+// SiLU pack pass over them (the same bits: both go through sx8_silu_mul and the
+// reference's Z tree).  Workspace: the fused form's Zhl of gate and up and packed X, or the
+// group call's workspace followed by g and u.
+struct GateUpPlan {
+    bool fused;
+    Plan p;              // fused: the paired plan; else the group plan
+    int64_t gu_off;      // fallback: byte offset of g (u follows at + M N 4)
+    int64_t total;
+};
+
+GateUpPlan gateup_plan(int64_t M, int64_t N, int64_t n_cb) {
+    GateUpPlan gp{};
+    const int64_t NBp = (N + kBN / 2 - 1) / (kBN / 2);
+    const Plan pp = plan_gemm(M, 2 * N, NBp, n_cb);
+    gp.fused = pp.w1 && pp.n_split == 0 && tuning().w2;
+    if (gp.fused) {
+        gp.p = pp;
+        gp.total = ws_layout(pp, M, 2 * N, n_cb, 2, true).total;
+    } else {
+        const int64_t NBg = 2 * ((N + kBN - 1) / kBN);
+        gp.p = plan_gemm(M, 2 * N, NBg, n_cb);
+        gp.gu_off = ws_layout(gp.p, M, 2 * N, n_cb, 2, true).total;
+        gp.total = gp.gu_off + ((2 * M * N * 4 + 255) & ~int64_t(255));
+    }
+    return gp;
+}
+
+}  // namespace
+
+extern "C" int64_t sx8_dec_gemm_gateup_silu_workspace_bytes(int64_t M, int64_t N, int64_t n_cb) {
+    if (M <= 0 || N <= 0 || n_cb <= 0 || M > 0x7FFFFFFF || N > 0x3FFFFFFF) return -1;
+    return gateup_plan(M, N, n_cb).total;
+}
+
+extern "C" int32_t sx8_dec_gemm_gateup_silu(const uint16_t* X, int64_t M, int64_t K, const uint8_t* const* hdrs,
+                                            const uint8_t* const* levels, int32_t hdr_bytes,
+                                            const float* const* bases, const float* const* scales, int64_t N,
+                                            int64_t n_cb, const float* down_basis, const float* down_scales,
+                                            uint16_t* Xp, uint32_t* Zhl, void* workspace,
+                                            int64_t workspace_bytes, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_dec_gemm_gateup_silu";
+    if (!X || !hdrs || !levels || !bases || !scales || !down_basis || !down_scales || !Xp || !Zhl)
+        return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (hdr_bytes != 6 && hdr_bytes != 8)
+        return fail(SX8_ERR_INVALID, "%s: hdr_bytes must be 6 or 8, got %d", what, hdr_bytes);
+    if (!aligned(X, 2) || !aligned(down_basis, 16) || !aligned(down_scales, 8) || !aligned(Xp, 16) ||
+        !aligned(Zhl, 16))
+        return fail(SX8_ERR_INVALID, "%s: misaligned X, down basis / scales, Xp or Zhl", what);
+    const int64_t n_cb_d = (N + 31) / 32;
+    if (N > 0x3FFFFFFF || (M + 31) / 32 * n_cb_d * 2048 > 0x7FFFFFFF || M * n_cb_d * 8 > 0x7FFFFFFF)
+        return fail(SX8_ERR_UNSUPPORTED, "%s: operands beyond 2 GiB", what);
+    WeightSrc w[2]{};
+    for (int i = 0; i < 2; ++i) {
+        if (!hdrs[i] || !levels[i] || !bases[i] || !scales[i])
+            return fail(SX8_ERR_INVALID, "%s: null pointer in matrix %d", what, i);
+        if (!aligned(hdrs[i], hdr_bytes == 8 ? 8 : 2) || !aligned(levels[i], 8) || !aligned(bases[i], 16) ||
+            !aligned(scales[i], 8))
+            return fail(SX8_ERR_INVALID, "%s: misaligned pointer in matrix %d", what, i);
+        w[i].hdr = hdrs[i];
+        w[i].levels = levels[i];
+    }
+    int32_t rc = check_shape(what, M, K, K, N, n_cb);
+    if (rc != SX8_OK) return rc;
+    const GateUpPlan gp = gateup_plan(M, N, n_cb);
+    if (!workspace || workspace_bytes < gp.total || !aligned(workspace, 256))
+        return fail(SX8_ERR_INVALID,
+                    "%s: needs a 256-byte aligned workspace of %lld bytes "
+                    "(sx8_dec_gemm_gateup_silu_workspace_bytes), got %lld bytes at %p",
+                    what, (long long)gp.total, (long long)workspace_bytes, workspace);
+    hipStream_t st = as_stream(stream);
+    uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+    ZSets zd{};                                  // the down projection's basis set
+    zd.n = 1;
+    zd.basis[0] = down_basis;
+    zd.scales[0] = down_scales;
+    zd.Z[0] = reinterpret_cast<float*>(Zhl);
+    if (!gp.fused) {
+        float* gu = reinterpret_cast<float*>(ws + gp.gu_off);
+        float* Ys[2] = {gu, gu + M * N};
+        const int64_t Ns[2] = {N, N};
+        rc = run_gemm<false>(what, X, M, K, K, 2, w, hdr_bytes, ZMode::kBasis, bases, scales, nullptr, Ns, n_cb, Ys,
+                             workspace, gp.gu_off, st);
+        if (rc != SX8_OK) return rc;
+        rc = compute_z_silu(Ys[0], Ys[1], M, N, N, zd, n_cb_d, Xp, st);
+        if (rc != SX8_OK) return rc;
+        return check_launch(what);
+    }
+    // fused: one pass over X (packed X, Zhl of gate and up), then the paired GEMM
+    const Plan& p = gp.p;
+    if (p.G > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "%s: grid too large", what);
+    const WsLayout lay = ws_layout(p, M, 2 * N, n_cb, 2, true);
+    uint16_t* xp_in = reinterpret_cast<uint16_t*>(ws + lay.z_bytes * 2);
+    ZSets zs{};
+    zs.n = 2;
+    GemmGroup g{};
+    g.n_mats = 2;
+    g.Ntot = 2 * N;
+    g.NB = (int)((N + kBN / 2 - 1) / (kBN / 2));
+    for (int i = 0; i < 2; ++i) {
+        zs.basis[i] = bases[i];
+        zs.scales[i] = scales[i];
+        zs.Z[i] = reinterpret_cast<float*>(ws + lay.z_bytes * i);
+        g.m[i].w = w[i];
+        g.m[i].Zhl = reinterpret_cast<const uint32_t*>(ws + lay.z_bytes * i);
+        g.m[i].N = (int)N;
+        g.m[i].nb = g.NB;
+    }
+    rc = compute_z_sets(X, M, K, K, zs, n_cb, true, xp_in, st);
+    if (rc != SX8_OK) return rc;
+    const SiluOut so{down_basis, down_scales, Xp, Zhl, (int)n_cb_d};
+    if (hdr_bytes == 8)
+        hipLaunchKernelGGL((k_gemm_w2<false, 8, true, true>), dim3((unsigned)p.G), dim3(kW2Threads), 0, st, xp_in,
+                           (int)M, g, (int)n_cb, p.Tf, p.St, p.kbs, nullptr, so);
+    else
+        hipLaunchKernelGGL((k_gemm_w2<false, 6, true, true>), dim3((unsigned)p.G), dim3(kW2Threads), 0, st, xp_in,
+                           (int)M, g, (int)n_cb, p.Tf, p.St, p.kbs, nullptr, so);
+    return check_launch(what);
 }
 
 extern "C" int64_t sx8_gemm_prefill_packed_workspace_bytes(int64_t M, int32_t n_mats, const int64_t* Ns,

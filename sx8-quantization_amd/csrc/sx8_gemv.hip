@@ -210,8 +210,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kSilu || !k
         stage_basis();
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
-            const float x0 = gv[2 * t] / (1.0f + __expf(-gv[2 * t])) * uv[2 * t];
-            const float x1 = gv[2 * t + 1] / (1.0f + __expf(-gv[2 * t + 1])) * uv[2 * t + 1];
+            const float x0 = sx8_silu_mul(gv[2 * t], uv[2 * t]);
+            const float x1 = sx8_silu_mul(gv[2 * t + 1], uv[2 * t + 1]);
             xw[t] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x0) |
                     ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x1) << 16);
         }
@@ -890,8 +890,7 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_panel(
                 uint32_t xw[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    xw[i] = pack_h2(g8[2 * i] / (1.0f + __expf(-g8[2 * i])) * u8[2 * i],
-                                    g8[2 * i + 1] / (1.0f + __expf(-g8[2 * i + 1])) * u8[2 * i + 1]);
+                    xw[i] = pack_h2(sx8_silu_mul(g8[2 * i], u8[2 * i]), sx8_silu_mul(g8[2 * i + 1], u8[2 * i + 1]));
                 tin[p].x = make_uint4(xw[0], xw[1], xw[2], xw[3]);
             }
         }
@@ -1810,7 +1809,7 @@ __global__ __launch_bounds__(kPanelThreads) void k_gemv_pair(
     if (tid < CT && mat == 0) {
         float mv = 0.f;
         if (col_ok) {
-            const uint16_t mh = __builtin_bit_cast(uint16_t, (_Float16)(y / (1.0f + __expf(-y)) * yo));
+            const uint16_t mh = __builtin_bit_cast(uint16_t, (_Float16)sx8_silu_mul(y, yo));
             *(uint16_t SX8_GLOBAL_AS*)(pa.m + col) = mh;
             mv = sx8_h2f(mh);
         }

@@ -184,7 +184,10 @@ class SX8Decoder(nn.Module):
               # the attention output as the o projection's packed GEMM operands
               "xp": torch.empty((T + 31) // 32 * (nh * hd // 32) * 1024, dtype=torch.int16, device=dev),
               "zhl": torch.empty(T * (nh * hd // 32) * 4, dtype=torch.int16, device=dev),
-              "o": torch.empty(T, H, **f32), "g": torch.empty(T, I, **f32), "u": torch.empty(T, I, **f32),
+              # x = fp16(silu(g) u) as the down projection's packed GEMM operands
+              "xpd": torch.empty((T + 31) // 32 * ((I + 31) // 32) * 1024, dtype=torch.int16, device=dev),
+              "zhld": torch.empty(T * ((I + 31) // 32) * 4, dtype=torch.int16, device=dev),
+              "o": torch.empty(T, H, **f32),
               "d": torch.empty(T, H, **f32),
               "pos0": torch.zeros(1, dtype=torch.int64, device=dev),
               "logits": torch.empty(cfg["vocab"], **f32), "tok": torch.zeros(1, dtype=torch.int64, device=dev),
@@ -199,10 +202,12 @@ class SX8Decoder(nn.Module):
                                     ((ly0.o.out_f,), ly0.o.qt["n_cb"]),
                                     ((ly0.gate.out_f, ly0.up.out_f), ly0.gate.qt["n_cb"]),
                                     ((ly0.down.out_f,), ly0.down.qt["n_cb"])))
+        need = max(need, int(_L.lib().sx8_dec_gemm_gateup_silu_workspace_bytes(T, I, ly0.gate.qt["n_cb"])))
         pb["ws"] = torch.empty(need, dtype=torch.uint8, device=dev)
         pb["groups"] = [(self._group_args((ly.q, ly.k, ly.v), (pb["q"], pb["k"], pb["v"])),
-                         self._group_args((ly.gate, ly.up), (pb["g"], pb["u"])),
-                         self._group_args((ly.o,), (pb["o"],))) for ly in self.layers]
+                         self._group_args((ly.gate, ly.up), ()),         # (no float32 outputs)
+                         self._group_args((ly.o,), (pb["o"],)),
+                         self._group_args((ly.down,), (pb["d"],))) for ly in self.layers]
         self._pb = pb
         return pb
 
@@ -228,15 +233,16 @@ class SX8Decoder(nn.Module):
         return parts.value, n_parts.value, slc.value
 
     @staticmethod
-    def _gemm_packed_deferred(args, Xp, Zhl, M, K, ws, st):
+    def _gemm_packed(args, Xp, Zhl, M, K, ws, st, defer=True):
         """The prefill GEMM of one matrix on the packed X and Zhl its producer wrote
-        (sx8_gemm_prefill_packed), the split-K sum left to the consumer: (parts, n_parts, slice)."""
+        (sx8_gemm_prefill_packed); with defer the split-K sum is left to the consumer and
+        (parts, n_parts, slice) is returned, else the output is complete."""
         n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
         parts, n_parts, slc = ctypes.c_void_p(), ctypes.c_int32(), ctypes.c_int64()
+        outs = (ctypes.addressof(parts), ctypes.addressof(n_parts), ctypes.addressof(slc)) if defer else (None,) * 3
         _L.call("sx8_gemm_prefill_packed", _L.ptr(Xp), (ctypes.c_void_p * 1)(Zhl.data_ptr()), M, K, n, hdrs, lvls, 6,
-                ns, n_cb, ys, _L.ptr(ws), ws.numel(), ctypes.addressof(parts), ctypes.addressof(n_parts),
-                ctypes.addressof(slc), st)
-        return parts.value, n_parts.value, slc.value
+                ns, n_cb, ys, _L.ptr(ws), ws.numel(), *outs, st)
+        return (parts.value, n_parts.value, slc.value) if defer else (None, 0, 0)
 
     @staticmethod
     def _gemm(lin, X, Y, ws, st):
@@ -252,8 +258,9 @@ class SX8Decoder(nn.Module):
         (sx8_dec_add_rmsnorm, M = T), the prefill GEMMs into preallocated buffers, q/k
         norm + RoPE + KV-cache write (sx8_dec_qk_rope_cache_rows), causal attention over
         the cache rows writing the o projection's packed GEMM operands
-        (sx8_dec_attn_prefill_packed, sx8_gemm_prefill_packed), SiLU * up inside the down GEMM
-        (sx8_dec_gemm_silu) and the final norm inside the lm_head GEMV.  The split-K sums
+        (sx8_dec_attn_prefill_packed, sx8_gemm_prefill_packed), the gate/up GEMM writing
+        fp16(SiLU(g) * u) as the down projection's packed operands
+        (sx8_dec_gemm_gateup_silu) and the final norm inside the lm_head GEMV.  The split-K sums
         of the q/k/v, o and down GEMMs (all but the last layer's) are added by the kernels
         that read those outputs (the *_deferred GEMM calls and the *_parts consumers), the
         same sums in the same order.  The residual stream is float32.  Returns the next token (1,); generation only needs the last
@@ -289,21 +296,17 @@ class SX8Decoder(nn.Module):
             _, _, obas, osca = ly.o._t44
             _L.call("sx8_dec_attn_prefill_packed", P(pb["qh"]), P(self.k_cache[li]), P(self.v_cache[li]), T, 0, nh,
                     nk, hd, self.max_len, 1.0 / math.sqrt(hd), P(obas), P(osca), P(pb["xp"]), P(pb["zhl"]), st)
-            op = self._gemm_packed_deferred(pb["groups"][li][2], pb["xp"], pb["zhl"], T, nh * hd, pb["ws"], st)
+            op = self._gemm_packed(pb["groups"][li][2], pb["xp"], pb["zhl"], T, nh * hd, pb["ws"], st)
             _L.call("sx8_dec_add_rmsnorm_parts", P(pb["resid"]), P(pb["o"]), None, P(ly.post_norm), P(pb["h"]), T,
                     H, eps, op[0], op[1], op[2], st)
-            self._gemm_group(pb["groups"][li][1], pb["h"], pb["ws"], st)      # gate, up: one call
-            hdr, lvl, bas, sca = ly.down._t44                       # SiLU * up inside the down GEMM
-            args = (P(pb["g"]), P(pb["u"]), T, cfg["inter"], P(hdr), P(lvl), 6, P(bas), P(sca), ly.down.out_f,
-                    ly.down.qt["n_cb"], P(pb["d"]), P(pb["ws"]), pb["ws"].numel())
-            if li < last:
-                parts, n_parts, slc = ctypes.c_void_p(), ctypes.c_int32(), ctypes.c_int64()
-                _L.call("sx8_dec_gemm_silu_deferred", *args, ctypes.addressof(parts), ctypes.addressof(n_parts),
-                        ctypes.addressof(slc), st)
-                pend = (parts.value, n_parts.value, slc.value)
-            else:
-                # the last layer's output feeds the final norm and the lm_head whole
-                _L.call("sx8_dec_gemm_silu", *args, st)
+            # gate/up GEMM ending in x = fp16(silu(g) u) as the down projection's packed operands
+            _, hdrs, lvls, bas, sca, _, gcb, _ = pb["groups"][li][1]
+            _, _, dbas, dsca = ly.down._t44
+            _L.call("sx8_dec_gemm_gateup_silu", P(pb["h"]), T, H, hdrs, lvls, 6, bas, sca, cfg["inter"], gcb, P(dbas),
+                    P(dsca), P(pb["xpd"]), P(pb["zhld"]), P(pb["ws"]), pb["ws"].numel(), st)
+            # down; the last layer's output feeds the final norm and the lm_head whole
+            pend = self._gemm_packed(pb["groups"][li][3], pb["xpd"], pb["zhld"], T, cfg["inter"], pb["ws"], st,
+                                     defer=li < last)
         if all_logits:
             # every row: residual + down output, final norm, lm_head GEMM over T rows
             _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), P(pb["d"]), None, P(self.final_norm), P(pb["h"]),
@@ -390,7 +393,7 @@ class SX8Decoder(nn.Module):
         return (n, P(*[l._t44[0].data_ptr() for l in lins]), P(*[l._t44[1].data_ptr() for l in lins]),
                 P(*[l._t44[2].data_ptr() for l in lins]), P(*[l._t44[3].data_ptr() for l in lins]),
                 (ctypes.c_int64 * n)(*[l.out_f for l in lins]), lins[0].qt["n_cb"],
-                P(*[y.data_ptr() for y in ys]))
+                P(*[y.data_ptr() for y in ys]) if ys else None)
 
     @staticmethod
     def _gemv_rms(args, resid, init, delta, w, resid_out, eps, st):

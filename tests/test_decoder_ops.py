@@ -958,3 +958,70 @@ def test_attention_packed_operands(hiplib, cuda, nh, nk, hd, L, T, start, N, hb)
     print("   plan", _L.gemm_plan(T, [N], n_cb), "n_parts", n_parts, flush=True)
     assert torch.equal(ya.cpu(), yb.cpu())
     assert torch.equal(ya.cpu(), yd.cpu())
+
+
+@pytest.mark.parametrize("M,K,N,hb", [
+    (512, 2560, 9728, 6),     # the prompt pass's gate/up at T = 512: whole 512-row tiles (fused)
+    (512, 2560, 9728, 8),
+    (700, 640, 1536, 6),      # ragged rows
+    (2048, 2560, 9728, 6),    # split tail tiles: the group GEMM + pack pass form
+    (96, 512, 1000, 6),       # small M, N not a multiple of 32
+])
+def test_gateup_silu_packed_operands(hiplib, cuda, monkeypatch, M, K, N, hb):
+    """sx8_dec_gemm_gateup_silu writes, bit for bit, the down projection's packed X and Zhl of
+    x = sx8_dec_silu_mul(gate X, up X) (sx8_gemm_prefill_group for g and u, sx8_compute_z for
+    Z), in both of its forms: the paired-tile GEMM with the SiLU epilogue and the group GEMM +
+    pack pass (SX8_GEMM_W2=0 takes the second); the down GEMM on them equals
+    sx8_gemm_prefill on x."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    n_cb = (K + 31) // 32
+    n_cb_d = (N + 31) // 32
+    ts = _mats(cuda, [N, N], K, 40 + M, hb)
+    dn = _mats(cuda, [256], N, 70 + M, hb)[0]                   # a down-like matrix: K = N
+    g = torch.Generator().manual_seed(M + N)
+    X = torch.randn(M, K, generator=g).half().to(cuda)
+    # reference: g, u by the group GEMM, x by the SiLU launch, Z by sx8_compute_z
+    ws, nb = _L.gemm_workspace(M, [N, N], n_cb, cuda)
+    gu = [torch.empty(M, N, device=cuda) for _ in range(2)]
+    ga = _group(ts, [N, N], n_cb, gu)
+    _L.call("sx8_gemm_prefill_group", P(X), M, K, K, ga[0], ga[1], ga[2], hb, ga[3], ga[4], ga[5], ga[6], ga[7],
+            P(ws), nb, st)
+    x = torch.zeros(M, n_cb_d * 32, dtype=torch.float16, device=cuda)
+    xs = torch.empty(M, N, dtype=torch.float16, device=cuda)
+    _L.call("sx8_dec_silu_mul", P(gu[0]), P(gu[1]), P(xs), M * N, st)
+    x[:, :N] = xs
+    Zf = torch.empty(M, n_cb_d, 2, device=cuda)
+    _L.call("sx8_compute_z", P(x), M, n_cb_d * 32, P(dn[2]), P(dn[3]), n_cb_d, P(Zf), st)
+    torch.cuda.synchronize()
+    xp_ref, zhl_ref = _packed_operands_ref(x.cpu().view(torch.int16).numpy().view(np.uint16), Zf.cpu().numpy(),
+                                           n_cb_d)
+    Gs = (M + 31) // 32
+    for w2 in ("1", "0"):
+        monkeypatch.setenv("SX8_GEMM_W2", w2)
+        _L.lib().sx8_gemm_reload_tuning()
+        print("gateup silu", M, K, N, hb, "w2", w2, flush=True)
+        need = int(_L.lib().sx8_dec_gemm_gateup_silu_workspace_bytes(M, N, n_cb))
+        wsg = torch.empty(need, dtype=torch.uint8, device=cuda)
+        Xp = torch.full((Gs * n_cb_d * 1024,), 0x7E7E, dtype=torch.int16, device=cuda)
+        Zhl = torch.full((M * n_cb_d * 4,), 0x7E7E, dtype=torch.int16, device=cuda)
+        _L.call("sx8_dec_gemm_gateup_silu", P(X), M, K, ga[1], ga[2], hb, ga[3], ga[4], N, n_cb, P(dn[2]), P(dn[3]),
+                P(Xp), P(Zhl), P(wsg), need, st)
+        torch.cuda.synchronize()
+        assert np.array_equal(Xp.cpu().numpy().view(np.uint16), xp_ref)
+        assert np.array_equal(Zhl.cpu().numpy().view(np.uint16), zhl_ref)
+    monkeypatch.delenv("SX8_GEMM_W2")
+    _L.lib().sx8_gemm_reload_tuning()
+    # the down GEMM on the packed operands against sx8_gemm_prefill on x
+    yd = torch.empty(M, 256, device=cuda)
+    wsd, nbd = _L.gemm_workspace(M, [256], n_cb_d, cuda)
+    _L.call("sx8_gemm_prefill", P(x), M, n_cb_d * 32, n_cb_d * 32, P(dn[0]), P(dn[1]), hb, P(dn[2]), P(dn[3]), 256,
+            n_cb_d, P(yd), P(wsd), nbd, st)
+    yp = torch.empty(M, 256, device=cuda)
+    gd = _group([dn], [256], n_cb_d, [yp])
+    _L.call("sx8_gemm_prefill_packed", P(Xp), (ctypes.c_void_p * 1)(Zhl.data_ptr()), M, N, 1, gd[1], gd[2], hb, gd[5],
+            n_cb_d, gd[7], P(wsd), nbd, None, None, None, st)
+    torch.cuda.synchronize()
+    assert torch.equal(yd.cpu(), yp.cpu())
