@@ -31,6 +31,18 @@ int32_t sx8_dec_add_rmsnorm_parts(float* resid, const float* delta, const uint16
                                   const uint16_t* w, uint16_t* out, int64_t M, int64_t H, float eps,
                                   const float* parts, int32_t n_parts, int64_t slice, void* stream);
 
+/* sx8_dec_add_rmsnorm_parts (the same h into resid, the same x, bit for bit) writing x not as
+ * fp16 rows but as the prefill-GEMM operands of the n_mats (1..4) matrices that multiply
+ * it (sx8_gemm_prefill_packed): Xp, the packed X (ceil(M / 32) * (H / 32) * 2048 bytes; rows
+ * past M pack zeros), and Zhl[i], matrix i's PCA operand for its basis (H / 32, 2, 32) and
+ * scales (M * (H / 32) * 8 bytes) -- what the GEMM's own pass over x writes, without that
+ * launch.  H a multiple of 32, at most 4096; resid, delta, parts and Xp 16-byte aligned,
+ * init and w 8-byte, bases 16-byte, scales and Zhl 8-byte.  No reference counterpart. */
+int32_t sx8_dec_add_rmsnorm_packed(float* resid, const float* delta, const uint16_t* init, const uint16_t* w,
+                                   int64_t M, int64_t H, float eps, const float* parts, int32_t n_parts,
+                                   int64_t slice, int32_t n_mats, const float* const* bases,
+                                   const float* const* scales, uint16_t* Xp, uint32_t* const* Zhl, void* stream);
+
 /* One token at position *pos: per query/key head RMSNorm (q_norm/k_norm weights, over hd),
  * fp16 rounding, rotate-half RoPE with cos_t/sin_t rows (L, hd/2) float32; q into q_out
  * (nh*hd fp16), k and v into row *pos of k_cache / v_cache ((nk, L, hd) fp16 each).  A
@@ -119,8 +131,10 @@ int32_t sx8_dec_gemm_silu_deferred(const float* g, const float* u, int64_t M, in
                                    int32_t* n_parts, int64_t* slice, void* stream);
 
 /* The prompt pass's MLP up to the down projection's input: the gate and up prefill GEMMs
- * of X (M, K) fp16 (hdrs / levels / bases / scales: [gate, up], N output columns each,
- * n_cb K blocks) and x = fp16(silu(g) * u), written straight as the down projection's
+ * of X (M, K) fp16 -- or of its packed operands Xp_in, Zhl_in[gate, up] (the layouts of
+ * sx8_gemm_prefill_packed, e.g. from sx8_dec_add_rmsnorm_packed; X NULL) -- (hdrs / levels /
+ * bases / scales: [gate, up], N output columns each, n_cb K blocks) and x = fp16(silu(g) *
+ * u), written straight as the down projection's
  * packed prefill-GEMM operands (sx8_gemm_prefill_packed): Xp (ceil(M / 32) * ceil(N / 32)
  * * 2048 bytes) and Zhl (M * ceil(N / 32) * 8 bytes) for the down projection's basis
  * (ceil(N / 32), 2, 32) and scales.  When the plan runs whole 512-row tiles, one GEMM
@@ -130,7 +144,8 @@ int32_t sx8_dec_gemm_silu_deferred(const float* g, const float* u, int64_t M, in
  * sx8_gemm_prefill_group + sx8_dec_silu_mul + the down GEMM's own pass over x.  Workspace:
  * sx8_dec_gemm_gateup_silu_workspace_bytes.  No reference counterpart (the reference's MLP
  * runs gate, up, SiLU * up and down as separate torch ops, scripts/infer_sx8.py). */
-int32_t sx8_dec_gemm_gateup_silu(const uint16_t* X, int64_t M, int64_t K, const uint8_t* const* hdrs,
+int32_t sx8_dec_gemm_gateup_silu(const uint16_t* X, const uint16_t* Xp_in, const uint32_t* const* Zhl_in,
+                                 int64_t M, int64_t K, const uint8_t* const* hdrs,
                                  const uint8_t* const* levels, int32_t hdr_bytes, const float* const* bases,
                                  const float* const* scales, int64_t N, int64_t n_cb, const float* down_basis,
                                  const float* down_scales, uint16_t* Xp, uint32_t* Zhl, void* workspace,

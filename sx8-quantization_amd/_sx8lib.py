@@ -67,7 +67,9 @@ SIGNATURES = [
      [_P, _P, _I64, _I64, _I32, _P, _P, _I32, _P, _I64, _P, _P, _I64, _P, _P, _P, _P]),
     ("sx8_gemm_prefill_packed_workspace_bytes", _I64, [_I64, _I32, _P, _I64]),
     ("sx8_dec_gemm_gateup_silu", _I32,
-     [_P, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P]),
+     [_P, _P, _P, _I64, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P]),
+    ("sx8_dec_add_rmsnorm_packed", _I32,
+     [_P, _P, _P, _P, _I64, _I64, ctypes.c_float, _P, _I32, _I64, _I32, _P, _P, _P, _P, _P]),
     ("sx8_dec_gemm_gateup_silu_workspace_bytes", _I64, [_I64, _I64, _I64]),
     ("sx8_gemm_pca_z", _I32, [_P, _I64, _P, _I32, _I64, _I64, _P, _P]),
     ("sx8_gemm_prefill_core", _I32, [_P, _I64, _I64, _I64, _P, _P, _I32, _I64, _I64, _P, _P, _I64, _P]),

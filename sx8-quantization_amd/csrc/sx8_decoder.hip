@@ -47,9 +47,69 @@ __device__ __forceinline__ float4 h4f(uint2 v) {
                        h2f((uint16_t)(v.y >> 16)));
 }
 
+// The vec path's row arithmetic, shared with k_add_rmsnorm_pack so both give the same bits:
+// thread t's values i = t + 256 u (float4 units) of h = (init ? fp16 init : resid) + delta
+// (+ pending partial slices), zero past the row; their squares summed with explicit fmas in
+// a fixed order; x = h * inv * w rounded to float32 (pinned) before its fp16 conversion.
 // NP > 0: delta is the first K range of a split GEMM whose other NP ranges' partial products
 // sit at parts + s * slice (same row-major layout); each element is delta + part 0 + ... +
 // part NP-1 in that order (the split-K sum of the GEMM, bit for bit) before it is added.
+template <int NP>
+__device__ __forceinline__ void rms_row_load(float4 (&v)[kRmsPer4], uint2 (&wv)[kRmsPer4], const float* resid,
+                                             const float* delta, const uint16_t* init, const uint16_t* w,
+                                             const float* parts, int64_t slice, int64_t base, int H4, int t) {
+    const float4* r4 = reinterpret_cast<const float4*>(resid + base);
+    const float4* d4 = reinterpret_cast<const float4*>(delta + (delta ? base : 0));
+    const uint2* i4 = reinterpret_cast<const uint2*>(init + (init ? base : 0));
+    const uint2* w4 = reinterpret_cast<const uint2*>(w);
+#pragma unroll
+    for (int u = 0; u < kRmsPer4; ++u) {       // every load of the row before the reduction
+        const int i = t + 256 * u;
+        const int ic = min(i, H4 - 1);
+        float4 x = init ? h4f(i4[ic]) : r4[ic];
+        if (delta) {
+            float4 dd = d4[ic];
+            if constexpr (NP > 0) {
+                float4 pv[NP];
+#pragma unroll
+                for (int s2 = 0; s2 < NP; ++s2)
+                    pv[s2] = reinterpret_cast<const float4*>(parts + s2 * slice + base)[ic];
+#pragma unroll
+                for (int s2 = 0; s2 < NP; ++s2)
+                    dd = make_float4(dd.x + pv[s2].x, dd.y + pv[s2].y, dd.z + pv[s2].z, dd.w + pv[s2].w);
+            }
+            x = make_float4(x.x + dd.x, x.y + dd.y, x.z + dd.z, x.w + dd.w);
+        }
+        v[u] = i < H4 ? x : make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[u] = w4[ic];
+    }
+}
+
+__device__ __forceinline__ float rms_row_ss(const float4 (&v)[kRmsPer4]) {
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < kRmsPer4; ++u) {
+        ss = __builtin_fmaf(v[u].x, v[u].x, ss);
+        ss = __builtin_fmaf(v[u].y, v[u].y, ss);
+        ss = __builtin_fmaf(v[u].z, v[u].z, ss);
+        ss = __builtin_fmaf(v[u].w, v[u].w, ss);
+    }
+    return ss;
+}
+
+__device__ __forceinline__ float rms_scale(float h, float inv, float w) {
+    float y = h * inv * w;
+    asm volatile("" : "+v"(y));
+    return y;
+}
+
+// (the row's 4 wave sums, added in wave order after the shuffle tree, as block_sum256)
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
 template <int NP = 0>
 __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ resid, const float* __restrict__ delta,
                                                      const uint16_t* __restrict__ init,
@@ -72,37 +132,11 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ resid, 
     };
     if (vec && H <= 256 * 4 * kRmsPer4) {
         const int H4 = H >> 2;
-        float4* r4 = reinterpret_cast<float4*>(resid + base);
-        const float4* d4 = reinterpret_cast<const float4*>(delta + (delta ? base : 0));
-        const uint2* i4 = reinterpret_cast<const uint2*>(init + (init ? base : 0));
-        const uint2* w4 = reinterpret_cast<const uint2*>(w);
         float4 v[kRmsPer4];
         uint2 wv[kRmsPer4];
-#pragma unroll
-        for (int u = 0; u < kRmsPer4; ++u) {       // every load of the row before the reduction
-            const int i = threadIdx.x + 256 * u;
-            const int ic = min(i, H4 - 1);
-            float4 x = init ? h4f(i4[ic]) : r4[ic];
-            if (delta) {
-                float4 dd = d4[ic];
-                if constexpr (NP > 0) {
-                    float4 pv[NP];
-#pragma unroll
-                    for (int s2 = 0; s2 < NP; ++s2)
-                        pv[s2] = reinterpret_cast<const float4*>(parts + s2 * slice + base)[ic];
-#pragma unroll
-                    for (int s2 = 0; s2 < NP; ++s2)
-                        dd = make_float4(dd.x + pv[s2].x, dd.y + pv[s2].y, dd.z + pv[s2].z, dd.w + pv[s2].w);
-                }
-                x = make_float4(x.x + dd.x, x.y + dd.y, x.z + dd.z, x.w + dd.w);
-            }
-            v[u] = i < H4 ? x : make_float4(0.f, 0.f, 0.f, 0.f);
-            wv[u] = w4[ic];
-        }
-        float ss = 0.f;
-#pragma unroll
-        for (int u = 0; u < kRmsPer4; ++u) ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
-        const float inv = 1.0f / sqrtf(block_sum256(ss, red) / (float)H + eps);
+        rms_row_load<NP>(v, wv, resid, delta, init, w, parts, slice, base, H4, threadIdx.x);
+        const float inv = 1.0f / sqrtf(block_sum256(rms_row_ss(v), red) / (float)H + eps);
+        float4* r4 = reinterpret_cast<float4*>(resid + base);
         uint2* o4 = reinterpret_cast<uint2*>(out + base);
 #pragma unroll
         for (int u = 0; u < kRmsPer4; ++u) {
@@ -110,8 +144,8 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ resid, 
             if (i < H4) {
                 r4[i] = v[u];
                 const float4 wf = h4f(wv[u]);
-                o4[i] = make_uint2((uint32_t)f2h(v[u].x * inv * wf.x) | ((uint32_t)f2h(v[u].y * inv * wf.y) << 16),
-                                   (uint32_t)f2h(v[u].z * inv * wf.z) | ((uint32_t)f2h(v[u].w * inv * wf.w) << 16));
+                o4[i] = make_uint2((uint32_t)f2h(rms_scale(v[u].x, inv, wf.x)) | ((uint32_t)f2h(rms_scale(v[u].y, inv, wf.y)) << 16),
+                                   (uint32_t)f2h(rms_scale(v[u].z, inv, wf.z)) | ((uint32_t)f2h(rms_scale(v[u].w, inv, wf.w)) << 16));
             }
         }
         return;
@@ -150,6 +184,129 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ resid, 
     }
     const float inv = 1.0f / sqrtf(block_sum256(ss, red) / (float)H + eps);
     for (int i = threadIdx.x; i < H; i += 256) out[base + i] = f2h(resid[base + i] * inv * h2f(w[i]));
+}
+
+// k_add_rmsnorm's vec path, bit for bit (rms_row_*), for two rows per 512-thread work-group,
+// whose normalized rows go out as the prefill GEMM's packed operands of the NS matrices that
+// multiply them (sx8_gemm_prefill_packed) instead of fp16 rows: x into the packed X (rows
+// past M up to the next multiple of 32 pack zeros) and, per matrix, Z0 / Z1 of every K
+// block of every row (the reference's tree order, split fp16 hi / lo) into its Zhl -- what
+// the GEMM's own pass over the fp16 rows writes.  Phase 1: the rows' values, sums and
+// stores, x kept in LDS; phase 2: thread d takes the dot products (matrix s, K block kb,
+// vector j) numbered d, d + 512, ..., for both rows at once (one basis read for two rows).
+// H % 32 == 0, H <= 4096.
+constexpr int kPackRows = 2;
+struct NormPack {
+    const float* basis[4];
+    const float* scales[4];
+    uint32_t* Zhl[4];
+    uint16_t* Xp;
+    int n_cb;
+};
+
+template <int NP, int NS>
+__global__ __launch_bounds__(256 * kPackRows) void k_add_rmsnorm_pack(float* __restrict__ resid,
+                                                                     const float* __restrict__ delta,
+                                                                     const uint16_t* __restrict__ init,
+                                                                     const uint16_t* __restrict__ w, int M, int H,
+                                                                     float eps, const float* __restrict__ parts,
+                                                                     int64_t slice, const NormPack pk) {
+    __shared__ float red[kPackRows][4];
+    __shared__ __align__(16) float xs[kPackRows][256 * 4 * kRmsPer4];
+    const int rl = threadIdx.x >> 8, t = threadIdx.x & 255;
+    const int row = blockIdx.x * kPackRows + rl;
+    const int H4 = H >> 2;
+    const int n_cb = pk.n_cb;
+    const bool live = row < M;
+    const int rowc = live ? row : M - 1;              // rows past M: loads of a valid row, unused
+    const int64_t base = (int64_t)rowc * H;
+    // the basis vector and scale of this thread's first dot product (phase 2), requested
+    // ahead of the rows so their round trip overlaps phase 1
+    const int nd = NS * n_cb * 2;
+    auto dot_of = [&](int d, int& s, int& kb, int& j) {
+        s = d / (2 * n_cb);
+        const int rem = d - s * 2 * n_cb;
+        kb = rem >> 1;
+        j = rem & 1;
+    };
+    auto set_ptr = [&](auto const (&a)[4], int s) { return s == 0 ? a[0] : s == 1 ? a[1] : s == 2 ? a[2] : a[3]; };
+    float4 b0[8];
+    float sc0 = 0.f;
+    {
+        int s, kb, j;
+        dot_of(min((int)threadIdx.x, nd - 1), s, kb, j);
+        const float4* b4 = reinterpret_cast<const float4*>(set_ptr(pk.basis, s) + (int64_t)kb * 64 + 32 * j);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) b0[q] = b4[q];
+        sc0 = set_ptr(pk.scales, s)[2 * kb + j];
+    }
+    float4 v[kRmsPer4];
+    uint2 wv[kRmsPer4];
+    rms_row_load<NP>(v, wv, resid, delta, init, w, parts, slice, base, H4, t);
+    const float ws = wave_sum64(rms_row_ss(v));
+    if ((t & 63) == 0) red[rl][t >> 6] = ws;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf((red[rl][0] + red[rl][1] + red[rl][2] + red[rl][3]) / (float)H + eps);
+    const int G = row >> 5, r = row & 31;
+    float4* r4 = reinterpret_cast<float4*>(resid + base);
+#pragma unroll
+    for (int u = 0; u < kRmsPer4; ++u) {
+        const int i = t + 256 * u;
+        if (i >= H4) continue;
+        uint32_t lo = 0u, hi = 0u;
+        if (live) {
+            r4[i] = v[u];
+            const float4 wf = h4f(wv[u]);
+            lo = (uint32_t)f2h(rms_scale(v[u].x, inv, wf.x)) | ((uint32_t)f2h(rms_scale(v[u].y, inv, wf.y)) << 16);
+            hi = (uint32_t)f2h(rms_scale(v[u].z, inv, wf.z)) | ((uint32_t)f2h(rms_scale(v[u].w, inv, wf.w)) << 16);
+        }
+        *reinterpret_cast<float4*>(&xs[rl][4 * i]) = h4f(make_uint2(lo, hi));
+        // element 4 i of the row: K block kb, chunk (hf, st), offset 0 or 4 within it
+        const int e0 = 4 * i, kb = e0 >> 5, tt = e0 & 31;
+        *reinterpret_cast<uint2*>(pk.Xp + (((int64_t)G * n_cb + kb) * 2 + ((tt >> 3) & 1)) * 512 +
+                                  ((tt >> 4) * 32 + r) * 8 + (tt & 7)) = make_uint2(lo, hi);
+    }
+    __syncthreads();
+    {
+#pragma clang fp contract(off)
+    for (int d = threadIdx.x; d < nd; d += 256 * kPackRows) {
+        int s, kb, j;
+        dot_of(d, s, kb, j);
+        uint32_t* zs = set_ptr(pk.Zhl, s);
+        float b[32];
+        float sc = sc0;
+        if (d == (int)threadIdx.x) {                    // the prefetched first dot product
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                b[4 * q] = b0[q].x; b[4 * q + 1] = b0[q].y; b[4 * q + 2] = b0[q].z; b[4 * q + 3] = b0[q].w;
+            }
+        } else {
+            const float4* b4 = reinterpret_cast<const float4*>(set_ptr(pk.basis, s) + (int64_t)kb * 64 + 32 * j);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 bb = b4[q];
+                b[4 * q] = bb.x; b[4 * q + 1] = bb.y; b[4 * q + 2] = bb.z; b[4 * q + 3] = bb.w;
+            }
+            sc = set_ptr(pk.scales, s)[2 * kb + j];
+        }
+#pragma unroll
+        for (int rr = 0; rr < kPackRows; ++rr) {
+            const int row2 = blockIdx.x * kPackRows + rr;
+            if (row2 >= M) break;
+            const float* x = &xs[rr][32 * kb];
+            float p[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) p[q] = x[q] * b[q] + x[q + 16] * b[q + 16];
+#pragma unroll
+            for (int off = 8; off > 0; off >>= 1)
+#pragma unroll
+                for (int q = 0; q < off; ++q) p[q] = p[q] + p[q + off];
+            float z = sc * p[0];
+            asm volatile("" : "+v"(z));
+            zs[((int64_t)row2 * n_cb + kb) * 2 + j] = sx8_split_hl(z);
+        }
+    }
+    }
 }
 
 // Heads per 256-thread block: nh query heads, then nk key heads, then nk value heads, TPH =
@@ -1193,6 +1350,56 @@ extern "C" int32_t sx8_dec_add_rmsnorm_parts(float* resid, const float* delta, c
                                              void* stream) {
     return add_rmsnorm_impl("sx8_dec_add_rmsnorm_parts", resid, delta, init, w, out, M, H, eps, parts, n_parts,
                             slice, stream);
+}
+
+extern "C" int32_t sx8_dec_add_rmsnorm_packed(float* resid, const float* delta, const uint16_t* init,
+                                              const uint16_t* w, int64_t M, int64_t H, float eps,
+                                              const float* parts, int32_t n_parts, int64_t slice, int32_t n_mats,
+                                              const float* const* bases, const float* const* scales,
+                                              uint16_t* Xp, uint32_t* const* Zhl, void* stream) {
+    using namespace sx8;
+    const char* what = "sx8_dec_add_rmsnorm_packed";
+    if (!resid || !w || !Xp || !bases || !scales || !Zhl) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
+    if (M <= 0 || H <= 0 || M > 0x7FFFFFFF - 64 || H % 32 != 0 || H > 256 * 4 * kRmsPer4)
+        return fail(SX8_ERR_INVALID, "%s: bad shape (H a multiple of 32, at most %d)", what, 256 * 4 * kRmsPer4);
+    if (n_mats < 1 || n_mats > 4) return fail(SX8_ERR_INVALID, "%s: n_mats must be 1..4, got %d", what, n_mats);
+    if (n_parts > 0 && !delta) return fail(SX8_ERR_INVALID, "%s: partial sums need delta", what);
+    int32_t rc = check_parts(what, parts, n_parts, slice, M * H);
+    if (rc != SX8_OK) return rc;
+    if (!aligned(resid, 16) || (delta && !aligned(delta, 16)) || (init && !aligned(init, 8)) || !aligned(w, 8) ||
+        !aligned(Xp, 16) || (n_parts > 0 && (!aligned(parts, 16) || slice % 4 != 0)))
+        return fail(SX8_ERR_INVALID, "%s: resid, delta, parts and Xp must be 16-byte aligned, init and w 8-byte "
+                    "(slice a multiple of 4)", what);
+    const int64_t n_cb = H / 32, Mp = (M + 31) / 32 * 32;
+    if (Mp / 32 * n_cb * 2048 > 0x7FFFFFFF || M * n_cb * 8 > 0x7FFFFFFF)
+        return fail(SX8_ERR_UNSUPPORTED, "%s: operands beyond 2 GiB", what);
+    NormPack pk{};
+    for (int i = 0; i < n_mats; ++i) {
+        if (!bases[i] || !scales[i] || !Zhl[i]) return fail(SX8_ERR_INVALID, "%s: null pointer in matrix %d", what, i);
+        if (!aligned(bases[i], 16) || !aligned(scales[i], 8) || !aligned(Zhl[i], 8))
+            return fail(SX8_ERR_INVALID, "%s: misaligned basis, scales or Zhl of matrix %d", what, i);
+        pk.basis[i] = bases[i];
+        pk.scales[i] = scales[i];
+        pk.Zhl[i] = Zhl[i];
+    }
+    pk.Xp = Xp;
+    pk.n_cb = (int)n_cb;
+    const dim3 grid((unsigned)(Mp / kPackRows));
+    hipStream_t st = as_stream(stream);
+    by_parts(n_parts, [&](auto np) {
+        constexpr int NP = decltype(np)::value;
+        switch (n_mats) {
+            case 1: hipLaunchKernelGGL((k_add_rmsnorm_pack<NP, 1>), grid, dim3(256 * kPackRows), 0, st, resid, delta,
+                                       init, w, (int)M, (int)H, eps, parts, slice, pk); break;
+            case 2: hipLaunchKernelGGL((k_add_rmsnorm_pack<NP, 2>), grid, dim3(256 * kPackRows), 0, st, resid, delta,
+                                       init, w, (int)M, (int)H, eps, parts, slice, pk); break;
+            case 3: hipLaunchKernelGGL((k_add_rmsnorm_pack<NP, 3>), grid, dim3(256 * kPackRows), 0, st, resid, delta,
+                                       init, w, (int)M, (int)H, eps, parts, slice, pk); break;
+            default: hipLaunchKernelGGL((k_add_rmsnorm_pack<NP, 4>), grid, dim3(256 * kPackRows), 0, st, resid, delta,
+                                        init, w, (int)M, (int)H, eps, parts, slice, pk); break;
+        }
+    });
+    return check_launch(what);
 }
 
 extern "C" int32_t sx8_dec_qk_rope_cache(const float* q_raw, const float* k_raw, const float* v_raw,

@@ -2075,7 +2075,8 @@ extern "C" int64_t sx8_dec_gemm_gateup_silu_workspace_bytes(int64_t M, int64_t N
     return gateup_plan(M, N, n_cb).total;
 }
 
-extern "C" int32_t sx8_dec_gemm_gateup_silu(const uint16_t* X, int64_t M, int64_t K, const uint8_t* const* hdrs,
+extern "C" int32_t sx8_dec_gemm_gateup_silu(const uint16_t* X, const uint16_t* Xp_in, const uint32_t* const* Zhl_in,
+                                            int64_t M, int64_t K, const uint8_t* const* hdrs,
                                             const uint8_t* const* levels, int32_t hdr_bytes,
                                             const float* const* bases, const float* const* scales, int64_t N,
                                             int64_t n_cb, const float* down_basis, const float* down_scales,
@@ -2083,13 +2084,17 @@ extern "C" int32_t sx8_dec_gemm_gateup_silu(const uint16_t* X, int64_t M, int64_
                                             int64_t workspace_bytes, void* stream) {
     using namespace sx8;
     const char* what = "sx8_dec_gemm_gateup_silu";
-    if (!X || !hdrs || !levels || !bases || !scales || !down_basis || !down_scales || !Xp || !Zhl)
+    const bool packed_in = Xp_in != nullptr;
+    if ((X != nullptr) == packed_in || (packed_in && (!Zhl_in || !Zhl_in[0] || !Zhl_in[1])))
+        return fail(SX8_ERR_INVALID, "%s: give X, or Xp_in and both Zhl_in (not both forms)", what);
+    if (!hdrs || !levels || !bases || !scales || !down_basis || !down_scales || !Xp || !Zhl)
         return fail(SX8_ERR_INVALID, "%s: null pointer", what);
     if (hdr_bytes != 6 && hdr_bytes != 8)
         return fail(SX8_ERR_INVALID, "%s: hdr_bytes must be 6 or 8, got %d", what, hdr_bytes);
-    if (!aligned(X, 2) || !aligned(down_basis, 16) || !aligned(down_scales, 8) || !aligned(Xp, 16) ||
-        !aligned(Zhl, 16))
-        return fail(SX8_ERR_INVALID, "%s: misaligned X, down basis / scales, Xp or Zhl", what);
+    if ((X && !aligned(X, 2)) || (packed_in && (!aligned(Xp_in, 16) || !aligned(Zhl_in[0], 16) ||
+                                                !aligned(Zhl_in[1], 16))) ||
+        !aligned(down_basis, 16) || !aligned(down_scales, 8) || !aligned(Xp, 16) || !aligned(Zhl, 16))
+        return fail(SX8_ERR_INVALID, "%s: misaligned X / Xp_in / Zhl_in, down basis / scales, Xp or Zhl", what);
     const int64_t n_cb_d = (N + 31) / 32;
     if (N > 0x3FFFFFFF || (M + 31) / 32 * n_cb_d * 2048 > 0x7FFFFFFF || M * n_cb_d * 8 > 0x7FFFFFFF)
         return fail(SX8_ERR_UNSUPPORTED, "%s: operands beyond 2 GiB", what);
@@ -2122,8 +2127,10 @@ extern "C" int32_t sx8_dec_gemm_gateup_silu(const uint16_t* X, int64_t M, int64_
         float* gu = reinterpret_cast<float*>(ws + gp.gu_off);
         float* Ys[2] = {gu, gu + M * N};
         const int64_t Ns[2] = {N, N};
-        rc = run_gemm<false>(what, X, M, K, K, 2, w, hdr_bytes, ZMode::kBasis, bases, scales, nullptr, Ns, n_cb, Ys,
-                             workspace, gp.gu_off, st);
+        const PackedIn in{Xp_in, Zhl_in};
+        rc = run_gemm<false>(what, X, M, K, K, 2, w, hdr_bytes, packed_in ? ZMode::kPacked : ZMode::kBasis, bases,
+                             scales, nullptr, Ns, n_cb, Ys, workspace, gp.gu_off, st, nullptr, nullptr, INT64_MAX,
+                             nullptr, packed_in ? &in : nullptr);
         if (rc != SX8_OK) return rc;
         rc = compute_z_silu(Ys[0], Ys[1], M, N, N, zd, n_cb_d, Xp, st);
         if (rc != SX8_OK) return rc;
@@ -2133,7 +2140,7 @@ extern "C" int32_t sx8_dec_gemm_gateup_silu(const uint16_t* X, int64_t M, int64_
     const Plan& p = gp.p;
     if (p.G > 0x7FFFFFFF) return fail(SX8_ERR_UNSUPPORTED, "%s: grid too large", what);
     const WsLayout lay = ws_layout(p, M, 2 * N, n_cb, 2, true);
-    uint16_t* xp_in = reinterpret_cast<uint16_t*>(ws + lay.z_bytes * 2);
+    const uint16_t* xp_in = packed_in ? Xp_in : reinterpret_cast<uint16_t*>(ws + lay.z_bytes * 2);
     ZSets zs{};
     zs.n = 2;
     GemmGroup g{};
@@ -2145,12 +2152,14 @@ extern "C" int32_t sx8_dec_gemm_gateup_silu(const uint16_t* X, int64_t M, int64_
         zs.scales[i] = scales[i];
         zs.Z[i] = reinterpret_cast<float*>(ws + lay.z_bytes * i);
         g.m[i].w = w[i];
-        g.m[i].Zhl = reinterpret_cast<const uint32_t*>(ws + lay.z_bytes * i);
+        g.m[i].Zhl = packed_in ? Zhl_in[i] : reinterpret_cast<const uint32_t*>(ws + lay.z_bytes * i);
         g.m[i].N = (int)N;
         g.m[i].nb = g.NB;
     }
-    rc = compute_z_sets(X, M, K, K, zs, n_cb, true, xp_in, st);
-    if (rc != SX8_OK) return rc;
+    if (!packed_in) {
+        rc = compute_z_sets(X, M, K, K, zs, n_cb, true, reinterpret_cast<uint16_t*>(ws + lay.z_bytes * 2), st);
+        if (rc != SX8_OK) return rc;
+    }
     const SiluOut so{down_basis, down_scales, Xp, Zhl, (int)n_cb_d};
     if (hdr_bytes == 8)
         hipLaunchKernelGGL((k_gemm_w2<false, 8, true, true>), dim3((unsigned)p.G), dim3(kW2Threads), 0, st, xp_in,

@@ -184,6 +184,10 @@ class SX8Decoder(nn.Module):
               # the attention output as the o projection's packed GEMM operands
               "xp": torch.empty((T + 31) // 32 * (nh * hd // 32) * 1024, dtype=torch.int16, device=dev),
               "zhl": torch.empty(T * (nh * hd // 32) * 4, dtype=torch.int16, device=dev),
+              # the normalized rows as the q/k/v or gate/up GEMM's packed operands (one packed X,
+              # up to four Zhl; each consumed by its GEMM before the next norm writes them)
+              "xn": torch.empty((T + 31) // 32 * (H // 32) * 1024, dtype=torch.int16, device=dev),
+              "zn": [torch.empty(T * (H // 32) * 4, dtype=torch.int16, device=dev) for _ in range(3)],
               # x = fp16(silu(g) u) as the down projection's packed GEMM operands
               "xpd": torch.empty((T + 31) // 32 * ((I + 31) // 32) * 1024, dtype=torch.int16, device=dev),
               "zhld": torch.empty(T * ((I + 31) // 32) * 4, dtype=torch.int16, device=dev),
@@ -233,16 +237,27 @@ class SX8Decoder(nn.Module):
         return parts.value, n_parts.value, slc.value
 
     @staticmethod
-    def _gemm_packed(args, Xp, Zhl, M, K, ws, st, defer=True):
-        """The prefill GEMM of one matrix on the packed X and Zhl its producer wrote
-        (sx8_gemm_prefill_packed); with defer the split-K sum is left to the consumer and
-        (parts, n_parts, slice) is returned, else the output is complete."""
+    def _gemm_packed(args, Xp, Zhls, M, K, ws, st, defer=True):
+        """The prefill GEMMs of `args` on the packed X and the Zhl per matrix their producer
+        wrote (sx8_gemm_prefill_packed); with defer the split-K sum is left to the consumer and
+        (parts, n_parts, slice) is returned, else the outputs are complete."""
         n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
         parts, n_parts, slc = ctypes.c_void_p(), ctypes.c_int32(), ctypes.c_int64()
         outs = (ctypes.addressof(parts), ctypes.addressof(n_parts), ctypes.addressof(slc)) if defer else (None,) * 3
-        _L.call("sx8_gemm_prefill_packed", _L.ptr(Xp), (ctypes.c_void_p * 1)(Zhl.data_ptr()), M, K, n, hdrs, lvls, 6,
-                ns, n_cb, ys, _L.ptr(ws), ws.numel(), *outs, st)
+        _L.call("sx8_gemm_prefill_packed", _L.ptr(Xp), (ctypes.c_void_p * n)(*[z.data_ptr() for z in Zhls[:n]]), M,
+                K, n, hdrs, lvls, 6, ns, n_cb, ys, _L.ptr(ws), ws.numel(), *outs, st)
         return (parts.value, n_parts.value, slc.value) if defer else (None, 0, 0)
+
+    @staticmethod
+    def _norm_packed(pb, args, resid, delta, init, w, parts, eps, st):
+        """add + RMSNorm of the T rows written as the packed GEMM operands of the matrices
+        of `args` (sx8_dec_add_rmsnorm_packed into pb's xn / zn)."""
+        n, hdrs, lvls, bas, sca, ns, n_cb, ys = args
+        T, H = resid.shape
+        P = _L.ptr
+        _L.call("sx8_dec_add_rmsnorm_packed", P(resid), P(delta) if delta is not None else None,
+                P(init) if init is not None else None, P(w), T, H, eps, parts[0], parts[1], parts[2], n, bas, sca,
+                P(pb["xn"]), (ctypes.c_void_p * n)(*[z.data_ptr() for z in pb["zn"][:n]]), st)
 
     @staticmethod
     def _gemm(lin, X, Y, ws, st):
@@ -254,8 +269,9 @@ class SX8Decoder(nn.Module):
 
     @torch.no_grad()
     def prefill_fused(self, ids, all_logits=False):
-        """prefill() with the library ops over the T prompt rows: add + RMSNorm
-        (sx8_dec_add_rmsnorm, M = T), the prefill GEMMs into preallocated buffers, q/k
+        """prefill() with the library ops over the T prompt rows: add + RMSNorm written
+        as the next GEMM's packed operands (sx8_dec_add_rmsnorm_packed, M = T), the prefill
+        GEMMs on producer-written operands (sx8_gemm_prefill_packed), q/k
         norm + RoPE + KV-cache write (sx8_dec_qk_rope_cache_rows), causal attention over
         the cache rows writing the o projection's packed GEMM operands
         (sx8_dec_attn_prefill_packed, sx8_gemm_prefill_packed), the gate/up GEMM writing
@@ -281,13 +297,12 @@ class SX8Decoder(nn.Module):
         pend = (None, 0, 0)                                        # down's, for the next layer
         last = len(self.layers) - 1
         for li, ly in enumerate(self.layers):
+            # add + RMSNorm written as the q/k/v GEMM's packed operands (no pass over its rows)
             if li == 0:
-                _L.call("sx8_dec_add_rmsnorm", P(pb["resid"]), None, P(emb), P(ly.in_norm), P(pb["h"]), T, H,
-                        eps, st)
+                self._norm_packed(pb, pb["groups"][li][0], pb["resid"], None, emb, ly.in_norm, (None, 0, 0), eps, st)
             else:
-                _L.call("sx8_dec_add_rmsnorm_parts", P(pb["resid"]), P(pb["d"]), None, P(ly.in_norm), P(pb["h"]),
-                        T, H, eps, pend[0], pend[1], pend[2], st)
-            qp = self._gemm_group_deferred(pb["groups"][li][0], pb["h"], pb["ws"], st)     # q, k, v
+                self._norm_packed(pb, pb["groups"][li][0], pb["resid"], pb["d"], None, ly.in_norm, pend, eps, st)
+            qp = self._gemm_packed(pb["groups"][li][0], pb["xn"], pb["zn"], T, H, pb["ws"], st)     # q, k, v
             _L.call("sx8_dec_qk_rope_cache_rows_parts", P(pb["q"]), P(pb["k"]), P(pb["v"]), P(ly.q_norm),
                     P(ly.k_norm), P(self.cos), P(self.sin), P(pb["pos0"]), T, P(pb["qh"]),
                     P(self.k_cache[li]), P(self.v_cache[li]), nh, nk, hd, self.max_len, eps, qp[0], qp[1], qp[2],
@@ -296,16 +311,16 @@ class SX8Decoder(nn.Module):
             _, _, obas, osca = ly.o._t44
             _L.call("sx8_dec_attn_prefill_packed", P(pb["qh"]), P(self.k_cache[li]), P(self.v_cache[li]), T, 0, nh,
                     nk, hd, self.max_len, 1.0 / math.sqrt(hd), P(obas), P(osca), P(pb["xp"]), P(pb["zhl"]), st)
-            op = self._gemm_packed(pb["groups"][li][2], pb["xp"], pb["zhl"], T, nh * hd, pb["ws"], st)
-            _L.call("sx8_dec_add_rmsnorm_parts", P(pb["resid"]), P(pb["o"]), None, P(ly.post_norm), P(pb["h"]), T,
-                    H, eps, op[0], op[1], op[2], st)
+            op = self._gemm_packed(pb["groups"][li][2], pb["xp"], [pb["zhl"]], T, nh * hd, pb["ws"], st)
+            self._norm_packed(pb, pb["groups"][li][1], pb["resid"], pb["o"], None, ly.post_norm, op, eps, st)
             # gate/up GEMM ending in x = fp16(silu(g) u) as the down projection's packed operands
             _, hdrs, lvls, bas, sca, _, gcb, _ = pb["groups"][li][1]
             _, _, dbas, dsca = ly.down._t44
-            _L.call("sx8_dec_gemm_gateup_silu", P(pb["h"]), T, H, hdrs, lvls, 6, bas, sca, cfg["inter"], gcb, P(dbas),
-                    P(dsca), P(pb["xpd"]), P(pb["zhld"]), P(pb["ws"]), pb["ws"].numel(), st)
+            _L.call("sx8_dec_gemm_gateup_silu", None, P(pb["xn"]), (ctypes.c_void_p * 2)(*[z.data_ptr() for z in pb["zn"][:2]]),
+                    T, H, hdrs, lvls, 6, bas, sca, cfg["inter"], gcb, P(dbas), P(dsca), P(pb["xpd"]), P(pb["zhld"]),
+                    P(pb["ws"]), pb["ws"].numel(), st)
             # down; the last layer's output feeds the final norm and the lm_head whole
-            pend = self._gemm_packed(pb["groups"][li][3], pb["xpd"], pb["zhld"], T, cfg["inter"], pb["ws"], st,
+            pend = self._gemm_packed(pb["groups"][li][3], pb["xpd"], [pb["zhld"]], T, cfg["inter"], pb["ws"], st,
                                      defer=li < last)
         if all_logits:
             # every row: residual + down output, final norm, lm_head GEMM over T rows

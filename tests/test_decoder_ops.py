@@ -1007,8 +1007,8 @@ def test_gateup_silu_packed_operands(hiplib, cuda, monkeypatch, M, K, N, hb):
         wsg = torch.empty(need, dtype=torch.uint8, device=cuda)
         Xp = torch.full((Gs * n_cb_d * 1024,), 0x7E7E, dtype=torch.int16, device=cuda)
         Zhl = torch.full((M * n_cb_d * 4,), 0x7E7E, dtype=torch.int16, device=cuda)
-        _L.call("sx8_dec_gemm_gateup_silu", P(X), M, K, ga[1], ga[2], hb, ga[3], ga[4], N, n_cb, P(dn[2]), P(dn[3]),
-                P(Xp), P(Zhl), P(wsg), need, st)
+        _L.call("sx8_dec_gemm_gateup_silu", P(X), None, None, M, K, ga[1], ga[2], hb, ga[3], ga[4], N, n_cb, P(dn[2]),
+                P(dn[3]), P(Xp), P(Zhl), P(wsg), need, st)
         torch.cuda.synchronize()
         assert np.array_equal(Xp.cpu().numpy().view(np.uint16), xp_ref)
         assert np.array_equal(Zhl.cpu().numpy().view(np.uint16), zhl_ref)
@@ -1025,3 +1025,94 @@ def test_gateup_silu_packed_operands(hiplib, cuda, monkeypatch, M, K, N, hb):
             n_cb_d, gd[7], P(wsd), nbd, None, None, None, st)
     torch.cuda.synchronize()
     assert torch.equal(yd.cpu(), yp.cpu())
+
+
+@pytest.mark.parametrize("M,H,n_mats,np_,form", [
+    (512, 2560, 3, 5, "delta"),     # q/k/v's producer: the previous down projection's 5 slices
+    (512, 2560, 2, 3, "delta"),     # gate/up's producer: o's 3 slices
+    (77, 640, 1, 0, "init"),        # layer 0 (fp16 init, no delta), ragged rows
+    (33, 4096, 4, 1, "delta"),      # the widest row, four matrices
+])
+def test_add_rmsnorm_packed_operands(hiplib, cuda, M, H, n_mats, np_, form):
+    """sx8_dec_add_rmsnorm_packed writes the residual of sx8_dec_add_rmsnorm_parts and the
+    packed X / Zhl of its fp16 rows (every byte, rows past M packed as zeros) bit for bit;
+    sx8_gemm_prefill_packed on them equals sx8_gemm_prefill_group on the rows, and
+    sx8_dec_gemm_gateup_silu takes them in place of X."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    n_cb = H // 32
+    Ns = [256 + 64 * i for i in range(n_mats)]
+    ts = _mats(cuda, Ns, H, 500 + M, 6)
+    g = torch.Generator().manual_seed(M * 3 + H)
+    resid0 = torch.randn(M, H, generator=g).to(cuda)
+    delta = torch.randn(M, H, generator=g).to(cuda)
+    init = torch.randn(M, H, generator=g).half().to(cuda)
+    parts = torch.randn(max(np_, 1), M * H + 8, generator=g).to(cuda)
+    slc = M * H + 8                                             # a slice longer than the rows
+    w = (torch.rand(H, generator=g) + 0.5).half().to(cuda)
+    d_arg, i_arg = (P(delta), None) if form == "delta" else (None, P(init))
+    pp = P(parts) if np_ else None
+    print("rmsnorm packed", M, H, n_mats, np_, form, flush=True)
+    ra, xa = resid0.clone(), torch.empty(M, H, dtype=torch.float16, device=cuda)
+    _L.call("sx8_dec_add_rmsnorm_parts", P(ra), d_arg, i_arg, P(w), P(xa), M, H, 1e-6, pp, np_, slc, st)
+    rb = resid0.clone()
+    Gs = (M + 31) // 32
+    Xp = torch.full((Gs * n_cb * 1024,), 0x7E7E, dtype=torch.int16, device=cuda)
+    Zs = [torch.full((M * n_cb * 4,), 0x7E7E, dtype=torch.int16, device=cuda) for _ in range(n_mats)]
+    V = ctypes.c_void_p * n_mats
+    _L.call("sx8_dec_add_rmsnorm_packed", P(rb), d_arg, i_arg, P(w), M, H, 1e-6, pp, np_, slc, n_mats,
+            V(*[t[2].data_ptr() for t in ts]), V(*[t[3].data_ptr() for t in ts]), P(Xp),
+            V(*[z.data_ptr() for z in Zs]), st)
+    torch.cuda.synchronize()
+    assert torch.equal(ra.cpu(), rb.cpu())
+    x16 = xa.cpu().view(torch.int16).numpy().view(np.uint16)
+    for i, t in enumerate(ts):
+        Zf = torch.empty(M, n_cb, 2, device=cuda)
+        _L.call("sx8_compute_z", P(xa), M, H, P(t[2]), P(t[3]), n_cb, P(Zf), st)
+        torch.cuda.synchronize()
+        xp_ref, zhl_ref = _packed_operands_ref(x16, Zf.cpu().numpy(), n_cb)
+        if i == 0:
+            assert np.array_equal(Xp.cpu().numpy().view(np.uint16), xp_ref)
+        assert np.array_equal(Zs[i].cpu().numpy().view(np.uint16), zhl_ref), i
+    # the GEMM on the operands
+    ws, nb = _L.gemm_workspace(M, Ns, n_cb, cuda)
+    ya = [torch.empty(M, N, device=cuda) for N in Ns]
+    ga = _group(ts, Ns, n_cb, ya)
+    _L.call("sx8_gemm_prefill_group", P(xa), M, H, H, ga[0], ga[1], ga[2], 6, ga[3], ga[4], ga[5], ga[6], ga[7],
+            P(ws), nb, st)
+    yb = [torch.empty(M, N, device=cuda) for N in Ns]
+    gb = _group(ts, Ns, n_cb, yb)
+    _L.call("sx8_gemm_prefill_packed", P(Xp), V(*[z.data_ptr() for z in Zs]), M, H, n_mats, gb[1], gb[2], 6, gb[5],
+            n_cb, gb[7], P(ws), nb, None, None, None, st)
+    torch.cuda.synchronize()
+    for a, b in zip(ya, yb):
+        assert torch.equal(a.cpu(), b.cpu())
+    if n_mats == 2:
+        # gate/up on the packed operands = gate/up on the rows
+        N = Ns[0]
+        t2 = _mats(cuda, [N, N], H, 600 + M, 6)
+        dn = _mats(cuda, [64], N, 700 + M, 6)[0]
+        Zg = [torch.empty(M * n_cb * 4, dtype=torch.int16, device=cuda) for _ in range(2)]
+        rc = resid0.clone()
+        _L.call("sx8_dec_add_rmsnorm_packed", P(rc), d_arg, i_arg, P(w), M, H, 1e-6, pp, np_, slc, 2,
+                (ctypes.c_void_p * 2)(*[t[2].data_ptr() for t in t2]), (ctypes.c_void_p * 2)(*[t[3].data_ptr() for t in t2]),
+                P(Xp), (ctypes.c_void_p * 2)(*[z.data_ptr() for z in Zg]), st)
+        n_cb_d = (N + 31) // 32
+        need = int(_L.lib().sx8_dec_gemm_gateup_silu_workspace_bytes(M, N, n_cb))
+        wsg = torch.empty(need, dtype=torch.uint8, device=cuda)
+        outs = []
+        for packed in (False, True):
+            XpD = torch.empty(Gs * n_cb_d * 1024, dtype=torch.int16, device=cuda)
+            ZD = torch.empty(M * n_cb_d * 4, dtype=torch.int16, device=cuda)
+            g2 = _group(t2, [N, N], n_cb, [])
+            if packed:
+                _L.call("sx8_dec_gemm_gateup_silu", None, P(Xp), (ctypes.c_void_p * 2)(*[z.data_ptr() for z in Zg]), M, H,
+                        g2[1], g2[2], 6, g2[3], g2[4], N, n_cb, P(dn[2]), P(dn[3]), P(XpD), P(ZD), P(wsg), need, st)
+            else:
+                _L.call("sx8_dec_gemm_gateup_silu", P(xa), None, None, M, H, g2[1], g2[2], 6, g2[3], g2[4], N, n_cb,
+                        P(dn[2]), P(dn[3]), P(XpD), P(ZD), P(wsg), need, st)
+            torch.cuda.synchronize()
+            outs.append((XpD.cpu(), ZD.cpu()))
+        assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
