@@ -48,25 +48,25 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
 SRC_FILES = {"gemv": ("sx8_gemv.hip", "sx8_device.h", "sx8_buffer.h"),
              "gemm": ("sx8_gemm.hip", "sx8_device.h", "sx8_buffer.h")}
 MEASURED = {
-    # k_gemv_panel over the layer sweep: mean 6820.7 KiB fetched, 17.1 KiB written per launch
-    "gemv_traffic": {"value": (6820.7 * 2.0 + 17.1) * 1024, "src": "gemv", "src_sha16": "9ba026f0ed6ce498",
+    # k_gemv_panel over the layer sweep: mean 6820.9 KiB fetched, 17.1 KiB written per launch
+    "gemv_traffic": {"value": (6820.9 * 2.0 + 17.1) * 1024, "src": "gemv", "src_sha16": "81981aeb00e8fc2a",
                      "how": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, bench.py --only gemv --steps 10 "
                             "--warmup 2, first 12 x 7 single-matrix dispatches"},
     # rocprofv3 kernel-trace mean over the 140 timed k_gemv_panel dispatches (20 steps x 7);
-    # bench.py's own figure in that traced run: 6.143 us per launch (timed region / launches)
-    "gemv_traced_launch_us": {"value": 6.116, "src": "gemv", "src_sha16": "9ba026f0ed6ce498",
+    # bench.py's own figure in that traced run: 6.244 us per launch (timed region / launches)
+    "gemv_traced_launch_us": {"value": 6.216, "src": "gemv", "src_sha16": "81981aeb00e8fc2a",
                               "how": "rocprofv3 --kernel-trace --stats, bench.py --only gemv --steps 20 "
-                                     "(same-run event figure under the tracer: 6.143 us)"},
-    # k_gemm_w2 on down_proj at M = 2048 (plan 80 tiles x 3 K ranges): 89776.0 KiB fetched,
-    # 61705.1 KiB written per dispatch (Y 21 MB + two partial tiles per split tile 42 MB)
-    "prefill_traffic": {"value": (89776.0 * 2.0 + 61705.1) * 1024, "src": "gemm", "src_sha16": "8e45d8246051e308",
+                                     "(same-run event figure under the tracer: 6.244 us)"},
+    # k_gemm_w2 on down_proj at M = 2048 (plan 80 tiles x 3 K ranges): 89776.6 KiB fetched,
+    # 61690.7 KiB written per dispatch (Y 21 MB + two partial tiles per split tile 42 MB)
+    "prefill_traffic": {"value": (89776.6 * 2.0 + 61690.7) * 1024, "src": "gemm", "src_sha16": "55cfed02a03c334a",
                         "how": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, bench.py --only gemm-one "
                                "--shape down_proj --m 2048 --iters 20, mean of 21 dispatches"},
     # 100 x sum SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs)
-    "prefill_mfma_busy_pct": {"value": 47.0, "src": "gemm", "src_sha16": "8e45d8246051e308",
+    "prefill_mfma_busy_pct": {"value": 48.1, "src": "gemm", "src_sha16": "55cfed02a03c334a",
                               "how": "rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_F16 "
                                      "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE, bench.py --only gemm-one "
-                                     "--shape down_proj --m 2048 --iters 50 (k_gemm_w2; gate: 42.3; 47.0-47.9 on down across boxes)"},
+                                     "--shape down_proj --m 2048 --iters 50 (k_gemm_w2; gate: 43.0; 47.0-48.1 on down across boxes and builds)"},
 }
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, vendor figure
 # The streaming-read rate measured on the GPU boxes (bench.py --only readbw: best of the
