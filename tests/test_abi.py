@@ -258,3 +258,41 @@ def test_packed_operand_refusals_on_host(hiplib):
     assert attn(p, V((1 << 24) + 4)) == 1 and "aligned" in _err(L)
     assert attn(p, p, T=1000, start=100) == 1 and "bad shape" in _err(L)
     assert attn(p, p, nh=24, nk=8) == 1 and "bad shape" in _err(L)
+
+
+def test_producer_operand_refusals_on_host(hiplib):
+    """sx8_dec_gemm_gateup_silu and sx8_dec_add_rmsnorm_packed refuse bad arguments before any
+    launch: both or neither of X and the packed input, n_mats outside 1..4, H not a multiple
+    of 32 or past 4096, misaligned operands, a short workspace."""
+    L = hiplib
+    V = ctypes.c_void_p
+    p = V(1 << 24)
+    P2 = ctypes.c_void_p * 2
+    two = P2(1 << 20, 1 << 21)
+    M, K, N = 512, 2560, 9728
+    need = L.sx8_dec_gemm_gateup_silu_workspace_bytes(M, N, K // 32)
+    assert need > 0 and L.sx8_dec_gemm_gateup_silu_workspace_bytes(0, N, 80) == -1
+
+    def gu(x, xp, zin, ws=p, nbytes=1 << 30, xpo=p):
+        return L.sx8_dec_gemm_gateup_silu(x, xp, zin, M, K, two, two, 6, two, two, N, K // 32, p, p, xpo, p, ws,
+                                          nbytes, NULL)
+
+    assert gu(p, p, two) == 1 and "not both" in _err(L)            # X and the packed input
+    assert gu(NULL, NULL, NULL) == 1 and "not both" in _err(L)     # neither
+    assert gu(NULL, p, NULL) == 1 and "Zhl_in" in _err(L)
+    assert gu(p, NULL, NULL, xpo=V((1 << 24) + 4)) == 1 and "misaligned" in _err(L)
+    assert gu(p, NULL, NULL, nbytes=need - 256) == 1 and "workspace" in _err(L)
+
+    def norm(n_mats=3, H=2560, xp=p, parts=NULL, n_parts=0, slc=0, delta=p):
+        return L.sx8_dec_add_rmsnorm_packed(p, delta, NULL, p, M, H, ctypes.c_float(1e-6), parts, n_parts, slc,
+                                            n_mats, (ctypes.c_void_p * 4)(*[1 << 20] * 4),
+                                            (ctypes.c_void_p * 4)(*[1 << 20] * 4), xp,
+                                            (ctypes.c_void_p * 4)(*[1 << 20] * 4), NULL)
+
+    assert norm(n_mats=0) == 1 and "n_mats" in _err(L)
+    assert norm(n_mats=5) == 1 and "n_mats" in _err(L)
+    assert norm(H=2570) == 1 and "bad shape" in _err(L)
+    assert norm(H=8192) == 1 and "bad shape" in _err(L)
+    assert norm(xp=V((1 << 24) + 8)) == 1 and "aligned" in _err(L)
+    assert norm(parts=p, n_parts=2, slc=M * 2560, delta=NULL) == 1 and "need delta" in _err(L)
+    assert norm(parts=p, n_parts=2, slc=M * 2560 - 1) == 1 and "slice" in _err(L)
