@@ -966,6 +966,7 @@ def test_attention_packed_operands(hiplib, cuda, nh, nk, hd, L, T, start, N, hb)
     (700, 640, 1536, 6),      # ragged rows
     (2048, 2560, 9728, 6),    # split tail tiles: the group GEMM + pack pass form
     (96, 512, 1000, 6),       # small M, N not a multiple of 32
+    (512, 2560, 9760, 6),     # whole tiles with a half-empty last paired tile (N = 152.5 x 64)
 ])
 def test_gateup_silu_packed_operands(hiplib, cuda, monkeypatch, M, K, N, hb):
     """sx8_dec_gemm_gateup_silu writes, bit for bit, the down projection's packed X and Zhl of
@@ -999,6 +1000,7 @@ def test_gateup_silu_packed_operands(hiplib, cuda, monkeypatch, M, K, N, hb):
     xp_ref, zhl_ref = _packed_operands_ref(x.cpu().view(torch.int16).numpy().view(np.uint16), Zf.cpu().numpy(),
                                            n_cb_d)
     Gs = (M + 31) // 32
+    print("gateup silu plan (group tiling)", _L.gemm_plan(M, [N, N], n_cb), flush=True)
     for w2 in ("1", "0"):
         monkeypatch.setenv("SX8_GEMM_W2", w2)
         _L.lib().sx8_gemm_reload_tuning()
