@@ -4,6 +4,7 @@
 // Hugging Face Qwen modules driven by scripts/infer_sx8.py:109-173.)  Each is one launch
 // that reads its position from device memory, so a whole decode step can be captured in
 // a HIP graph and replayed.
+#include "sx8_buffer.h"
 #include "sx8_device.h"
 #include "sx8_host.h"
 
@@ -13,6 +14,25 @@ __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_c
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
 typedef uint32_t sx8_u32x4 __attribute__((ext_vector_type(4)));
+
+// A read-only argument pinned in SGPRs through an empty asm, so that its loads keep their
+// place in the program (a load from the argument itself may be moved past barriers to its
+// first use), and cast back to the global address space: through the pinned (generic)
+// pointer the loads would be flat loads, counted on the LDS counter as well, so that every
+// LDS wait would also wait for them.  (The attribute applies to the device pass only.)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define SX8_DEC_GLOBAL __attribute__((address_space(1)))
+#else
+#define SX8_DEC_GLOBAL
+#endif
+template <typename T>
+__device__ __forceinline__ const T SX8_DEC_GLOBAL* pinned_global(const T* p) {
+    asm volatile("" : "+s"(p));
+    return (const T SX8_DEC_GLOBAL*)p;
+}
+__device__ __forceinline__ sx8_u32x4 ld_u32x4(const uint16_t SX8_DEC_GLOBAL* p) {
+    return *reinterpret_cast<const sx8_u32x4 SX8_DEC_GLOBAL*>(p);
+}
 
 // Sum over a 256-thread block (wave64 shuffles, then 4 partials through LDS).
 __device__ __forceinline__ float block_sum256(float v, float* red) {
@@ -1000,7 +1020,9 @@ __global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* _
     static_assert(KCH >= 1 && KCH * ST == 32 * CPR, "K staging split");
     constexpr int VPT = (16 * CPR + ST - 1) / ST;   // V key-pair tasks per thread
     __shared__ __align__(16) unsigned char lds[Lds::kBytes];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // (the wave index read as uniform, so that the set's block choices are scalar: a per-lane
+    // condition on a load's offset would split the load into two under complementary masks)
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int set = w / GW, g = w % GW, ts = tid % ST;
     const int c = lane & 31, h = lane >> 5;
     constexpr int R = G / GW;
@@ -1014,13 +1036,28 @@ __global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* _
         return reinterpret_cast<uint16_t*>(lds + 2 * NS * Lds::kK + (buf * NS + set) * Lds::kV);
     };
     const sx8_u32x4 zero4 = {0u, 0u, 0u, 0u};
-    sx8_u32x4 qb[KS];
+    // The query and basis are read through pinned_global: a load from a read-only argument
+    // is otherwise free to sink past the barriers to its first use, which would put it
+    // behind the first staging instead of in flight during it.  Their loads are issued
+    // unconditionally from clamped (valid) addresses and the values selected afterwards (a
+    // load under a condition becomes a branch, after which the compiler can only wait for
+    // every outstanding load).
+    // The query tile of the work-group's GW heads: every set needs all of it, so with NS > 1
+    // set s loads chunks s QC .. s QC + QC - 1 of its wave's head (QC = KS / NS) and the sets
+    // exchange them through the free second staging buffer (kQLds, where they fit), instead
+    // of every wave loading its head's whole tile from memory.
+    const uint16_t SX8_DEC_GLOBAL* qg = pinned_global(q);
+    constexpr bool kQLds = NS > 1 && KS % NS == 0 && GW * KS * 1024 <= NS * Lds::kK;
+    constexpr int QC = kQLds ? KS / NS : KS;      // query chunks this wave loads
+    sx8_u32x4 qb[KS], qpart[QC];
     {
-        const uint16_t* qr = q + ((int64_t)min(qi, T - 1) * nh + head) * HD + 8 * h;
+        const uint16_t SX8_DEC_GLOBAL* qr = qg + ((int64_t)min(qi, T - 1) * nh + head) * HD + 8 * h;
+        const int st0 = kQLds ? set * QC : 0;
 #pragma unroll
-        for (int st = 0; st < KS; ++st)
-            qb[st] = qi < T ? *reinterpret_cast<const sx8_u32x4*>(qr + 16 * st) : zero4;
+        for (int i = 0; i < QC; ++i) qpart[i] = ld_u32x4(qr + 16 * (st0 + i));
     }
+    // [g][st][lane] 16-byte chunks at the start of the second buffer's K blocks
+    sx8_u32x4* const qlds = reinterpret_cast<sx8_u32x4*>(lds + NS * Lds::kK);
     // kPack: the basis rows and scales of the work-group's GW heads' K blocks (one float4
     // per thread), staged in LDS with the first key block
     constexpr int kPkF4 = kPack ? GW * NT * 16 : 1;
@@ -1031,34 +1068,41 @@ __global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* _
     float4 bpre = make_float4(0.f, 0.f, 0.f, 0.f);
     float2 spre = make_float2(0.f, 0.f);
     if constexpr (kPack) {
-        if (tid < kPkF4) bpre = reinterpret_cast<const float4*>(pk.basis + (int64_t)kbw * 64)[tid];
-        if (tid < GW * NT) spre = reinterpret_cast<const float2*>(pk.scales + (int64_t)kbw * 2)[tid];
+        const float SX8_DEC_GLOBAL* bg = pinned_global(pk.basis) + (int64_t)kbw * 64;
+        const float SX8_DEC_GLOBAL* sg = pinned_global(pk.scales) + (int64_t)kbw * 2;
+        bpre = reinterpret_cast<const float4 SX8_DEC_GLOBAL*>(bg)[min(tid, kPkF4 - 1)];
+        spre = reinterpret_cast<const float2 SX8_DEC_GLOBAL*>(sg)[min(tid, GW * NT - 1)];
     }
-    const uint16_t* kbase = k_cache + (int64_t)kvh * L * HD;
-    const uint16_t* vbase = v_cache + (int64_t)kvh * L * HD;
+    // the keys the tile reads: the KV head's cached keys below min(ktot, 32 nblk), HD halves each
+    // (the host keeps a head's cache, plus the blocks read past it, below 2 GiB)
+    const int64_t kbytes = (int64_t)min(ktot, 32 * nblk) * HD * 2;
+    const sx8_rsrc krs = make_rsrc(k_cache + (int64_t)kvh * L * HD, kbytes);
+    const sx8_rsrc vrs = make_rsrc(v_cache + (int64_t)kvh * L * HD, kbytes);
     // Step j: set s computes block NS j + s from LDS buffer j & 1 and stages its block of
     // step j + 1 into the other buffer; its global loads run kPf steps ahead of the
     // staging (a ring of kPf register sets, the loop unrolled by kPf).  One barrier per
     // step.
     constexpr int kPf = 2;
     sx8_u32x4 kreg[kPf][KCH], vreg[kPf][2 * VPT];
+    // Block kb through raw buffer loads over the keys the tile reads (krs / vrs): a block past
+    // the tile's last (kb >= nblk) and keys past the cache lie past the buffer and load zeros
+    // without touching memory.  Every load is issued unconditionally, with no condition on its
+    // offset either (the compiler would split such a load in two behind a branch), so the wait
+    // counts stay static and the set's next blocks stay in flight while it stages.
     auto load_blk = [&](sx8_u32x4 (&kr)[KCH], sx8_u32x4 (&vr)[2 * VPT], int kb) {
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {          // K: coalesced 16-byte chunks of whole rows
             const int ch = ts + i * ST;
-            const int key = kb * 32 + ch / CPR;
-            kr[i] = key < ktot ? *reinterpret_cast<const sx8_u32x4*>(kbase + (int64_t)key * HD + 8 * (ch % CPR))
-                               : zero4;
+            const int off = (kb * 32 + ch / CPR) * (HD * 2) + 16 * (ch % CPR);
+            kr[i] = __builtin_bit_cast(sx8_u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
         }
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {          // V: keys 2 kp, 2 kp + 1 at columns d0 .. d0 + 7
-            const int t = ts + i * ST;
-            const int kp = t & 15, d0 = 8 * (t >> 4);
-            const int key = kb * 32 + 2 * kp;
-            const bool ok = t < 16 * CPR;
-            vr[2 * i] = ok && key < ktot ? *reinterpret_cast<const sx8_u32x4*>(vbase + (int64_t)key * HD + d0) : zero4;
-            vr[2 * i + 1] = ok && key + 1 < ktot
-                                ? *reinterpret_cast<const sx8_u32x4*>(vbase + (int64_t)(key + 1) * HD + d0) : zero4;
+            const int tc = min(ts + i * ST, 16 * CPR - 1);   // (past the V tasks: loaded, not staged)
+            const int kp = tc & 15, d0 = 8 * (tc >> 4);
+            const int off = (kb * 32 + 2 * kp) * (HD * 2) + 2 * d0;
+            vr[2 * i] = __builtin_bit_cast(sx8_u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
+            vr[2 * i + 1] = __builtin_bit_cast(sx8_u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, off + HD * 2, 0, 0));
         }
     };
     auto stage = [&](int buf, const sx8_u32x4 (&kr)[KCH], const sx8_u32x4 (&vr)[2 * VPT]) {
@@ -1099,10 +1143,8 @@ __global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* _
     const int qpos = start + qi;
     auto body = [&](int j, sx8_u32x4 (&kr)[KCH], sx8_u32x4 (&vr)[2 * VPT]) {
         const int b = j & 1, kb = NS * j + set;
-        if (kb + NS < nblk) {
-            stage(b ^ 1, kr, vr);
-            if (kb + NS * (1 + kPf) < nblk) load_blk(kr, vr, kb + NS * (1 + kPf));
-        }
+        if (kb + NS < nblk) stage(b ^ 1, kr, vr);
+        load_blk(kr, vr, kb + NS * (1 + kPf));
         if (kb < nblk) {
             const uint16_t* kd = kt(b);
             const uint16_t* vd = vt(b);
@@ -1163,23 +1205,38 @@ __global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* _
         __syncthreads();      // step j + 1 staged; step j's buffers free for step j + 2
     };
     // ring slot i holds the set's blocks of steps i + 1, i + 1 + kPf, ...; step 0 is staged first
+    // Only the query, block 0 and the first ring slot are requested before the first barrier:
+    // the work-group's loads share one address path, and the barrier waits for the slowest
+    // wave's block 0; the other slots are requested behind it.
     {
         sx8_u32x4 k0[KCH], v0[2 * VPT];
-        if (set < nblk) load_blk(k0, v0, set);
+        load_blk(k0, v0, set);
+        load_blk(kreg[0], vreg[0], NS + set);
+        stage(0, k0, v0);                        // (a set past the tile's blocks: zeros, unused)
 #pragma unroll
-        for (int i = 0; i < kPf; ++i)
-            if (NS * (i + 1) + set < nblk) load_blk(kreg[i], vreg[i], NS * (i + 1) + set);
-        if (set < nblk) stage(0, k0, v0);
-        if constexpr (kPack) {
-            if (tid < kPkF4) apb[tid] = bpre;
-            if (tid < GW * NT) aps[tid] = spre;
+        for (int i = 0; i < QC; ++i) {
+            const sx8_u32x4 v = qi < T ? qpart[i] : zero4;
+            if constexpr (kQLds) qlds[(g * KS + set * QC + i) * 64 + lane] = v;
+            else qb[i] = v;
+        }
+        if constexpr (kPack) {      // (threads past the end store the last entry's value again)
+            apb[min(tid, kPkF4 - 1)] = bpre;
+            aps[min(tid, GW * NT - 1)] = spre;
         }
         __syncthreads();
+#pragma unroll
+        for (int i = 1; i < kPf; ++i) load_blk(kreg[i], vreg[i], NS * (i + 1) + set);
+        if constexpr (kQLds) {
+#pragma unroll
+            for (int st = 0; st < KS; ++st) qb[st] = qlds[(g * KS + st) * 64 + lane];
+            __syncthreads();                     // the second buffer is free again for step 0
+        }
     }
+    // (whole rounds of kPf steps: a step past nstep only loads and passes its barrier, and
+    // no step is skipped behind a branch that would end the loads' static wait counts)
     for (int j = 0; j < nstep; j += kPf) {
 #pragma unroll
-        for (int i = 0; i < kPf; ++i)
-            if (j + i < nstep) body(j + i, kreg[i], vreg[i]);
+        for (int i = 0; i < kPf; ++i) body(j + i, kreg[i], vreg[i]);
     }
     // kPack: fragment n of the row (16 values, dims 32 n + 8 gq + 4 h + e) as packed operands;
     // every lane of the wave takes part (the Z tree swaps lane halves), rows past T pack zeros
@@ -1528,10 +1585,10 @@ int32_t check_attn_prefill(const char* what, const uint16_t* q, const uint16_t* 
     if (!q || !k_cache || !v_cache) return fail(SX8_ERR_INVALID, "%s: null pointer", what);
     const int G = nk > 0 ? nh / nk : 0;
     if (nh <= 0 || nk <= 0 || nh % nk || (G != 1 && G != 2 && G != 4 && G != 8) || (hd != 64 && hd != 128) ||
-        16 * G > hd || T <= 0 || start < 0 || L <= 0 || start + T > L || L * (int64_t)hd > 0x7FFFFFFF ||
+        16 * G > hd || T <= 0 || start < 0 || L <= 0 || start + T > L || L * (int64_t)hd * 2 > 0x7FF00000 ||
         (T + 31) / 32 > 0x7FFFFFFF)
         return fail(SX8_ERR_INVALID, "%s: bad shape (nh / nk in {1, 2, 4, 8} with 16 nh / nk "
-                    "<= hd, hd 64 or 128, 0 <= start, start + T <= L)", what);
+                    "<= hd, hd 64 or 128, 0 <= start, start + T <= L, a head's cache below 2 GiB)", what);
     if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
         return fail(SX8_ERR_INVALID, "%s: q and caches must be 16-byte aligned", what);
     return SX8_OK;
