@@ -338,6 +338,14 @@ __global__ __launch_bounds__(256 * kPackRows) void k_add_rmsnorm_pack(float* __r
 // thousands of one-wave work-groups that each wait two memory round trips.
 constexpr int kRopeRows = 4;
 
+// A float32 result pinned before its fp16 conversion: the compiler would otherwise fold the
+// last multiply or fma into the conversion (v_fma_mixlo_f16, one rounding instead of two)
+// in some kernels and unrolled copies and not in others.
+__device__ __forceinline__ float rope_pin(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 // NP > 0: q_raw, k_raw, v_raw hold the first K range of a split GEMM whose other NP ranges'
 // partial products sit at q_part / k_part / v_part + s * slice (same layout); every value
 // read is raw + part 0 + ... + part NP-1 in that order (the split-K sum, bit for bit).
@@ -417,8 +425,8 @@ __global__ __launch_bounds__(256) void k_qk_rope_cache(const float* __restrict__
         const bool row_ok = y < rows && pos >= 0 && pos < L;
         if (row_ok && is_v) {
             uint16_t* vd = v_cache + ((int64_t)h * L + pos) * hd;
-            if (d < hd) vd[d] = f2h(va[r]);
-            if (d + tph < hd) vd[d + tph] = f2h(vb[r]);
+            if (d < hd) vd[d] = f2h(rope_pin(va[r]));
+            if (d + tph < hd) vd[d + tph] = f2h(rope_pin(vb[r]));
             for (int e = d + 2 * tph; e < hd; e += tph) {
                 const int64_t vo = (int64_t)y * nk * hd + h * hd + e;
                 float ve = v_raw[vo];
@@ -426,10 +434,12 @@ __global__ __launch_bounds__(256) void k_qk_rope_cache(const float* __restrict__
 #pragma unroll
                     for (int s2 = 0; s2 < NP; ++s2) ve += v_part[s2 * slice + vo];
                 }
-                vd[e] = f2h(ve);
+                vd[e] = f2h(rope_pin(ve));
             }
         }
-        float ss = x1[r] * x1[r] + x2[r] * x2[r];
+        // (explicit fmas here and in the rotation: which product the compiler would fuse
+        // differs between kernels)
+        float ss = __builtin_fmaf(x1[r], x1[r], x2[r] * x2[r]);
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
         if (tph > 64) {                      // two waves per head (every thread reaches the barrier)
@@ -441,9 +451,10 @@ __global__ __launch_bounds__(256) void k_qk_rope_cache(const float* __restrict__
         const uint16_t* nw = is_q ? qn : kn;
         const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
         // round to fp16 after the norm, as the fp16 activations of the model do
-        const float n1 = h2f(f2h(x1[r] * inv * h2f(nw[d]))), n2 = h2f(f2h(x2[r] * inv * h2f(nw[d + half])));
+        const float n1 = h2f(f2h(rope_pin(x1[r] * inv * h2f(nw[d]))));
+        const float n2 = h2f(f2h(rope_pin(x2[r] * inv * h2f(nw[d + half]))));
         const float c = cos_t[pos * half + d], s = sin_t[pos * half + d];
-        const float o1 = n1 * c - n2 * s, o2 = n2 * c + n1 * s;
+        const float o1 = rope_pin(__builtin_fmaf(n1, c, -(n2 * s))), o2 = rope_pin(__builtin_fmaf(n2, c, n1 * s));
         if (is_q) {
             uint16_t* qo = q_out + (int64_t)y * nh * hd + h * hd;
             qo[d] = f2h(o1);
@@ -556,6 +567,116 @@ __global__ __launch_bounds__(256) void k_attn_decode(const uint16_t* __restrict_
         for (int g = 0; g < PG; ++g) t += acc[g][tid];
         out[h * HD + tid] = f2h(t / sum);
     }
+}
+
+// k_qk_rope_cache for HD = 128, bit for bit, with 16-byte accesses: 16 lanes per (row,
+// head), unit u = y (nh + 2 nk) + b of the 16 per 256-thread work-group (b numbering q, then
+// k, then v heads as k_qk_rope_cache does).  A q/k lane j holds dims 4 j .. 4 j + 3 and their
+// RoPE partners 64 + 4 j .. (the pair k_qk_rope_cache's thread d owns, four at a time); its
+// sum of squares follows k_qk_rope_cache's 64-lane butterfly exactly: dim bits 5, 4, 3, 2
+// are lane bits 3, 2, 1, 0 (shuffles over lanes j ^ 8, ^ 4, ^ 2, ^ 1, per dim), bits 1 and 0
+// the dim within the lane.  A v lane copies dims 8 j .. 8 j + 7.  Every load is issued
+// unconditionally (clamped to a valid unit and table row) ahead of any arithmetic.  Needs
+// 16-byte aligned rows, partial slices and caches, 8-byte aligned norm weights.
+template <int NP = 0>
+__global__ __launch_bounds__(256) void k_qk_rope128(const float* __restrict__ q_raw, const float* __restrict__ k_raw,
+                                                    const float* __restrict__ v_raw,
+                                                    const uint16_t* __restrict__ qn,
+                                                    const uint16_t* __restrict__ kn,
+                                                    const float* __restrict__ cos_t,
+                                                    const float* __restrict__ sin_t,
+                                                    const int64_t* __restrict__ pos_p,
+                                                    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
+                                                    uint16_t* __restrict__ v_cache, int nh, int nk, int hd, int L,
+                                                    float eps, int rows, const float* __restrict__ q_part,
+                                                    const float* __restrict__ k_part,
+                                                    const float* __restrict__ v_part, int64_t slice) {
+    constexpr int HD = 128, half = 64;
+    const int NH = nh + 2 * nk;
+    const int unit = (int)blockIdx.x * 16 + ((int)threadIdx.x >> 4), j = (int)threadIdx.x & 15;
+    const bool live = unit < rows * NH;
+    const int uc = min(unit, rows * NH - 1);
+    const int y = uc / NH, b = uc - y * NH;
+    const bool is_q = b < nh, is_v = b >= nh + nk;
+    const int h = is_q ? b : is_v ? b - nh - nk : b - nh;
+    const int width = is_q ? nh * HD : nk * HD;
+    const int64_t ro = (int64_t)y * width + h * HD;                 // the unit's row in its source
+    // (sources read through pinned_global and ordered by an empty asm below: a load from a
+    // read-only argument may otherwise sink behind the branches to its first use)
+    typedef const float SX8_DEC_GLOBAL* gf;
+    const gf qg = pinned_global(q_raw), kg = pinned_global(k_raw), vg = pinned_global(v_raw);
+    const gf qpg = pinned_global(q_part), kpg = pinned_global(k_part), vpg = pinned_global(v_part);
+    const gf src = is_q ? qg : is_v ? vg : kg;
+    const gf prt = is_q ? qpg : is_v ? vpg : kpg;
+    const int e1 = is_v ? 8 * j : 4 * j, e2 = is_v ? 8 * j + 4 : half + 4 * j;
+    const int64_t pos = *pos_p + y;
+    const int pr = (int)min(max(pos, (int64_t)0), (int64_t)L - 1);
+    const uint16_t SX8_DEC_GLOBAL* qng = pinned_global(qn);
+    const uint16_t SX8_DEC_GLOBAL* kng = pinned_global(kn);
+    const uint16_t SX8_DEC_GLOBAL* nw = is_q ? qng : kng;
+    const float SX8_DEC_GLOBAL* ct = pinned_global(cos_t);
+    const float SX8_DEC_GLOBAL* st = pinned_global(sin_t);
+    typedef const float4 SX8_DEC_GLOBAL* gf4;
+    typedef const uint2 SX8_DEC_GLOBAL* gu2;
+    float4 x1 = *(gf4)(src + ro + e1);
+    float4 x2 = *(gf4)(src + ro + e2);
+    constexpr int kP = NP > 0 ? NP : 1;
+    float4 p1[kP], p2[kP];
+#pragma unroll
+    for (int s2 = 0; s2 < NP; ++s2) {
+        p1[s2] = *(gf4)(prt + s2 * slice + ro + e1);
+        p2[s2] = *(gf4)(prt + s2 * slice + ro + e2);
+    }
+    const uint2 w1 = *(gu2)(nw + 4 * j);
+    const uint2 w2 = *(gu2)(nw + half + 4 * j);
+    const float4 cs = *(gf4)(ct + (int64_t)pr * half + 4 * j);
+    const float4 sn = *(gf4)(st + (int64_t)pr * half + 4 * j);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int s2 = 0; s2 < NP; ++s2) {
+        x1 = make_float4(x1.x + p1[s2].x, x1.y + p1[s2].y, x1.z + p1[s2].z, x1.w + p1[s2].w);
+        x2 = make_float4(x2.x + p2[s2].x, x2.y + p2[s2].y, x2.z + p2[s2].z, x2.w + p2[s2].w);
+    }
+    const float a1[4] = {x1.x, x1.y, x1.z, x1.w}, a2[4] = {x2.x, x2.y, x2.z, x2.w};
+    float ssd[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ssd[e] = __builtin_fmaf(a1[e], a1[e], a2[e] * a2[e]);
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ssd[e] += __shfl_xor(ssd[e], o, 16);
+    const float ss = (ssd[0] + ssd[2]) + (ssd[1] + ssd[3]);
+    // (every lane computes the q/k result, so that no load sinks behind a branch)
+    const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+    const float wf1[4] = {h2f((uint16_t)(w1.x & 0xFFFFu)), h2f((uint16_t)(w1.x >> 16)), h2f((uint16_t)(w1.y & 0xFFFFu)),
+                          h2f((uint16_t)(w1.y >> 16))};
+    const float wf2[4] = {h2f((uint16_t)(w2.x & 0xFFFFu)), h2f((uint16_t)(w2.x >> 16)), h2f((uint16_t)(w2.y & 0xFFFFu)),
+                          h2f((uint16_t)(w2.y >> 16))};
+    const float c4[4] = {cs.x, cs.y, cs.z, cs.w}, s4[4] = {sn.x, sn.y, sn.z, sn.w};
+    uint16_t o1h[4], o2h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        // round to fp16 after the norm, as the fp16 activations of the model do
+        const float n1 = h2f(f2h(rope_pin(a1[e] * inv * wf1[e]))), n2 = h2f(f2h(rope_pin(a2[e] * inv * wf2[e])));
+        const float c = c4[e], sv = s4[e];
+        o1h[e] = f2h(rope_pin(__builtin_fmaf(n1, c, -(n2 * sv))));
+        o2h[e] = f2h(rope_pin(__builtin_fmaf(n2, c, n1 * sv)));
+    }
+    const uint2 u1 = make_uint2((uint32_t)o1h[0] | ((uint32_t)o1h[1] << 16), (uint32_t)o1h[2] | ((uint32_t)o1h[3] << 16));
+    const uint2 u2 = make_uint2((uint32_t)o2h[0] | ((uint32_t)o2h[1] << 16), (uint32_t)o2h[2] | ((uint32_t)o2h[3] << 16));
+    // rows outside the cache write nothing
+    if (!(live && pos >= 0 && pos < L)) return;
+    if (is_v) {
+        auto hp = [](float a, float b) {
+            return (uint32_t)f2h(rope_pin(a)) | ((uint32_t)f2h(rope_pin(b)) << 16);
+        };
+        *reinterpret_cast<uint4*>(v_cache + ((int64_t)h * L + pos) * HD + 8 * j) =
+            make_uint4(hp(x1.x, x1.y), hp(x1.z, x1.w), hp(x2.x, x2.y), hp(x2.z, x2.w));
+        return;
+    }
+    uint16_t* dst = is_q ? q_out + (int64_t)y * nh * HD + h * HD : k_cache + ((int64_t)h * L + pos) * HD;
+    *reinterpret_cast<uint2*>(dst + 4 * j) = u1;
+    *reinterpret_cast<uint2*>(dst + half + 4 * j) = u2;
 }
 
 // Split decode attention, two launches.  k_attn_split: work-group (kv head, chunk) takes
@@ -1459,6 +1580,21 @@ extern "C" int32_t sx8_dec_add_rmsnorm_packed(float* resid, const float* delta, 
     return check_launch(what);
 }
 
+namespace {
+
+// k_qk_rope128 applies (head dim 128, its 16- and 8-byte accesses aligned); it gives
+// k_qk_rope_cache's results bit for bit, so the choice does not change them.
+bool rope128_ok(const float* q_raw, const float* k_raw, const float* v_raw, const uint16_t* q_norm,
+                const uint16_t* k_norm, const float* cos_t, const float* sin_t, const uint16_t* q_out,
+                const uint16_t* k_cache, const uint16_t* v_cache, const float* parts, int64_t slice, int32_t hd) {
+    using namespace sx8;
+    return hd == 128 && aligned(q_raw, 16) && aligned(k_raw, 16) && aligned(v_raw, 16) && aligned(cos_t, 16) &&
+           aligned(sin_t, 16) && aligned(q_norm, 8) && aligned(k_norm, 8) && aligned(q_out, 8) &&
+           aligned(k_cache, 16) && aligned(v_cache, 16) && (!parts || (aligned(parts, 16) && slice % 4 == 0));
+}
+
+}  // namespace
+
 extern "C" int32_t sx8_dec_qk_rope_cache(const float* q_raw, const float* k_raw, const float* v_raw,
                                          const uint16_t* q_norm, const uint16_t* k_norm,
                                          const float* cos_t, const float* sin_t, const int64_t* pos,
@@ -1471,6 +1607,12 @@ extern "C" int32_t sx8_dec_qk_rope_cache(const float* q_raw, const float* k_raw,
         return fail(SX8_ERR_INVALID, "sx8_dec_qk_rope_cache: null pointer");
     if (nh <= 0 || nk <= 0 || nh % nk || hd <= 0 || (hd & 1) || hd > 256 || L <= 0 || L > 0x7FFFFFFF)
         return fail(SX8_ERR_INVALID, "sx8_dec_qk_rope_cache: bad shape (hd even, <= 256)");
+    if (rope128_ok(q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, q_out, k_cache, v_cache, nullptr, 0, hd)) {
+        hipLaunchKernelGGL(k_qk_rope128<0>, dim3(((unsigned)(nh + 2 * nk) + 15) / 16), dim3(256), 0, as_stream(stream),
+                           q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, pos, q_out, k_cache, v_cache, nh, nk,
+                           hd, (int)L, eps, 1, nullptr, nullptr, nullptr, (int64_t)0);
+        return check_launch("sx8_dec_qk_rope_cache");
+    }
     const unsigned hpb = hd > 128 ? 2u : 4u;     // heads per 256-thread block
     hipLaunchKernelGGL(k_qk_rope_cache<0>, dim3(((unsigned)(nh + 2 * nk) + hpb - 1) / hpb), dim3(256), 0,
                        as_stream(stream), q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, pos,
@@ -1499,6 +1641,16 @@ int32_t rope_rows_impl(const char* what, const float* q_raw, const float* k_raw,
     const float* qp = n_parts ? parts : nullptr;
     const float* kp = n_parts ? parts + qn : nullptr;
     const float* vp = n_parts ? parts + qn + kvn : nullptr;
+    if (rope128_ok(q_raw, k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, q_out, k_cache, v_cache, parts, slice, hd) &&
+        rows * (nh + 2 * nk) <= 0x7FFFFFFF - 16) {
+        const unsigned nb = (unsigned)((rows * (nh + 2 * nk) + 15) / 16);
+        by_parts(n_parts, [&](auto np) {
+            hipLaunchKernelGGL((k_qk_rope128<decltype(np)::value>), dim3(nb), dim3(256), 0, as_stream(stream), q_raw,
+                               k_raw, v_raw, q_norm, k_norm, cos_t, sin_t, pos, q_out, k_cache, v_cache, nh, nk, hd,
+                               (int)L, eps, (int)rows, qp, kp, vp, slice);
+        });
+        return check_launch(what);
+    }
     const unsigned hpb = hd > 128 ? 2u : 4u;     // heads per 256-thread block
     const unsigned yb = (unsigned)((rows + kRopeRows - 1) / kRopeRows);
     by_parts(n_parts, [&](auto np) {

@@ -548,6 +548,58 @@ def test_qk_rope_cache_rows(hiplib, cuda, nh, nk, hd, L, rows, pos0):
     assert close(kc, ref_k.float()), (kc.float() - ref_k.float()).abs().max().item()
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("nh,nk,L,rows,pos0,n_parts", [
+    (32, 8, 2048, 512, 0, 1),      # the prompt pass's call: 512 rows, the q/k/v GEMM's one pending slice
+    (32, 8, 600, 77, 530, 1),      # rows past the cache's end write nothing
+    (16, 2, 400, 33, -2, 2),       # rows before the cache write nothing
+    (12, 4, 100, 5, 0, 3),         # 20 heads: work-groups' units straddle q, k and v heads and rows
+    (8, 8, 40, 1, 39, 0),          # one row at the last position
+])
+def test_qk_rope_cache_rows_vector_kernel(hiplib, cuda, nh, nk, L, rows, pos0, n_parts):
+    """Head dim 128 with aligned rows runs the 16-byte kernel (k_qk_rope128); a q buffer 4 bytes
+    off 16-byte alignment runs the general one (k_qk_rope_cache).  Both write the same q rows
+    and K/V cache rows bit for bit, with and without pending partial slices."""
+    import torch
+    import _sx8lib as _L
+    P = _L.ptr
+    st = _L.stream(cuda)
+    hd = 128
+    g = torch.Generator().manual_seed(nh * 5 + rows)
+    half = hd // 2
+    inv = 1.0 / (1e6 ** (torch.arange(half, dtype=torch.float32) / half))
+    ang = torch.arange(L, dtype=torch.float32)[:, None] * inv[None]
+    cos, sin = ang.cos().to(cuda), ang.sin().to(cuda)
+    qn = (torch.rand(hd, generator=g) + 0.5).half().to(cuda)
+    kn = (torch.rand(hd, generator=g) + 0.5).half().to(cuda)
+    q = torch.randn(rows, nh * hd, generator=g).to(cuda)
+    k = (torch.randn(rows, nk * hd, generator=g) * 3).to(cuda)
+    v = torch.randn(rows, nk * hd, generator=g).to(cuda)
+    slice_ = rows * (nh + 2 * nk) * hd + 32
+    parts = torch.randn(max(n_parts, 1) * slice_, generator=g).to(cuda)
+    pos = torch.tensor([pos0], dtype=torch.int64, device=cuda)
+    base_k = torch.randn(nk, L, hd, generator=g).half().to(cuda)
+    base_v = torch.randn(nk, L, hd, generator=g).half().to(cuda)
+    qbuf = torch.empty(rows * nh * hd + 1, device=cuda)
+    qbuf[1:] = q.reshape(-1)
+    print("qk_rope vector kernel", nh, nk, L, rows, pos0, n_parts, flush=True)
+    outs = []
+    for qsrc in (q, qbuf[1:]):
+        qo = torch.full((rows, nh * hd), 7.0, device=cuda).half()
+        kc, vc = base_k.clone(), base_v.clone()
+        _L.call("sx8_dec_qk_rope_cache_rows_parts", P(qsrc), P(k), P(v), P(qn), P(kn), P(cos), P(sin), P(pos), rows,
+                P(qo), P(kc), P(vc), nh, nk, hd, L, 1e-6, P(parts) if n_parts else None, n_parts,
+                slice_ if n_parts else 0, st)
+        outs.append((qo, kc, vc))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a.cpu().view(torch.int16), b.cpu().view(torch.int16))
+    # rows outside the cache leave q (sentinel) and the caches untouched
+    for y in range(rows):
+        if not 0 <= pos0 + y < L:
+            assert bool((outs[0][0][y] == 7.0).all())
+
+
 @pytest.mark.parametrize("H,I,hb", [(2560, 9728, 6), (2560, 9728, 8), (1024, 8224, 6), (512, 1056, 8)])
 def test_gemv_pair_and_zp_down(hiplib, cuda, H, I, hb):
     """sx8_dec_gemv_rmsnorm_pair + sx8_dec_gemv_zp_add against the three-launch MLP
