@@ -1243,12 +1243,12 @@ __global__ __launch_bounds__(64 * GW * NS) void k_attn_prefill(const uint16_t* _
                 const int col = (kl & ~12) | ((kl & 4) << 1) | ((kl & 8) >> 1);   // even; col + 1 is key kl + 1
                 const uint32_t a[4] = {vr[2 * i].x, vr[2 * i].y, vr[2 * i].z, vr[2 * i].w};
                 const uint32_t bb[4] = {vr[2 * i + 1].x, vr[2 * i + 1].y, vr[2 * i + 1].z, vr[2 * i + 1].w};
+                // dim d0 + e of both keys: half e & 1 of word e / 2 of each, one v_perm_b32
+                // (bytes 0-3 select from a, 4-7 from bb)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint32_t lo = (a[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-                    const uint32_t hi = (bb[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-                    *reinterpret_cast<uint32_t*>(vd + (d0 + e) * kApVRow + col) = lo | (hi << 16);
-                }
+                for (int e = 0; e < 8; ++e)
+                    *reinterpret_cast<uint32_t*>(vd + (d0 + e) * kApVRow + col) =
+                        __builtin_amdgcn_perm(bb[e >> 1], a[e >> 1], (e & 1) ? 0x07060302u : 0x05040100u);
             }
         }
     };
