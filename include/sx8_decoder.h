@@ -158,7 +158,8 @@ int64_t sx8_dec_gemm_gateup_silu_workspace_bytes(int64_t M, int64_t N, int64_t n
  * rotated, as sx8_dec_qk_rope_cache_rows writes it), caches (nk, L, hd) fp16 holding
  * keys/values 0 .. start + T - 1; row i (position start + i) attends keys 0 .. start + i.
  * out (T, nh * hd) fp16; scale = 1 / sqrt(hd).  nh / nk in {1, 2, 4, 8} with 16 nh / nk
- * <= hd, hd 64 or 128.  fp16 products on MFMA with fp32 accumulation and an fp32 online
+ * <= hd, hd 64 or 128, one KV head's cache (L * hd * 2 bytes) at most 0x7FF00000 bytes
+ * (it is read through 32-bit buffer offsets).  fp16 products on MFMA with fp32 accumulation and an fp32 online
  * softmax (probabilities rounded to fp16 for the second product).  No reference
  * counterpart: the Hugging Face attention of the prompt pass in scripts/infer_sx8.py. */
 int32_t sx8_dec_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
