@@ -250,14 +250,18 @@ def test_packed_operand_refusals_on_host(hiplib):
     assert L.sx8_gemm_prefill_packed_workspace_bytes(M, 1, ns, 128) <= L.sx8_gemm_prefill_workspace_bytes(
         M, 1, ns, 128)
 
-    def attn(basis, xp, T=512, start=0, nh=32, nk=8, hd=128):
-        return L.sx8_dec_attn_prefill_packed(p, p, p, T, start, nh, nk, hd, 1024, ctypes.c_float(0.088), basis, p,
+    def attn(basis, xp, T=512, start=0, nh=32, nk=8, hd=128, Lc=1024):
+        return L.sx8_dec_attn_prefill_packed(p, p, p, T, start, nh, nk, hd, Lc, ctypes.c_float(0.088), basis, p,
                                              xp, p, NULL)
 
     assert attn(NULL, p) == 1 and "null" in _err(L)
     assert attn(p, V((1 << 24) + 4)) == 1 and "aligned" in _err(L)
     assert attn(p, p, T=1000, start=100) == 1 and "bad shape" in _err(L)
     assert attn(p, p, nh=24, nk=8) == 1 and "bad shape" in _err(L)
+    # one KV head's cache is read through 32-bit buffer offsets: at most 0x7FF00000 bytes
+    assert attn(p, p, Lc=(0x7FF00000 // 256) + 1) == 1 and "2 GiB" in _err(L)
+    assert L.sx8_dec_attn_prefill(p, p, p, p, 512, 0, 32, 8, 128, 1 << 23, ctypes.c_float(0.088), NULL) == 1
+    assert "2 GiB" in _err(L)
 
 
 def test_producer_operand_refusals_on_host(hiplib):
