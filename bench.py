@@ -653,17 +653,22 @@ def bench_vocab(torch, L, args):
     out = {"shape": f"{N}x{K}", "packed_bytes": packed_bytes(N, K)}
 
     def timed(fn, reps):
-        """median ms of max(reps, --iters) back-to-back calls, an event after each (and the
-        distribution); `region` gets the per-call time of timed regions of `reps` calls with
-        events only around each region (the GEMV headline's method)"""
+        """median ms over 10 series of `reps` back-to-back calls, an event after each call and
+        the same pause before each series as before each timed region (and the distribution);
+        `region` gets the per-call time of timed regions of `reps` calls with events only
+        around each region (the GEMV headline's method); `sustained` the distribution of one
+        series of max(reps, --iters) calls.  (A long series of these 365 MB reads drifts: the
+        lm_head GEMV runs ~65 us per call in its first 20 calls, then 70-88 us once the GPU
+        has streamed from HBM for more than ~1.5 ms without a pause; the kernel is the same.)"""
         fn()
         torch.cuda.synchronize()
-        q = quantiles(call_series(torch, st, lambda r: fn(), max(reps, args.iters)))
+        q = quantiles([u for _ in range(10) for u in call_series(torch, st, lambda r: fn(), reps)])
         dist.append(q)
         region.append(quantiles(region_series(torch, st, lambda r: fn(), reps)))
+        sustained.append(quantiles(call_series(torch, st, lambda r: fn(), max(reps, args.iters))))
         return q["median_us"] * 1e-3
 
-    dist, region = [], []
+    dist, region, sustained = [], [], []
 
     def ok(rc):
         if rc != 0:
@@ -679,7 +684,9 @@ def bench_vocab(torch, L, args):
     rus = region[-1]["median_us"]
     out["gemv_m1"] = {"us": ms * 1e3, "gbs": packed_bytes(N, K) / (ms * 1e-3) / 1e9, "us_dist": dist[-1],
                       "region_us": rus, "region_gbs": packed_bytes(N, K) / (rus * 1e-6) / 1e9,
-                      "region_dist": region[-1],
+                      "region_dist": region[-1], "sustained_dist": sustained[-1],
+                      "method": "us: median over 10 series of 20 back-to-back calls with an event after each "
+                                "call; sustained_dist: one series of max(20, --iters) such calls",
                       "region_method": "median over 10 timed regions of 20 back-to-back calls, one event "
                                        "before and one after each region (as the layer sweep's avg_launch_us)"}
     log(f"vocab gemv M=1: {ms * 1e3:.1f} us {out['gemv_m1']['gbs']:.0f} GB/s (event after each call); "
@@ -695,6 +702,7 @@ def bench_vocab(torch, L, args):
     out["gemm_m512"] = {"us": ms * 1e3, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12, "us_dist": dist[-1],
                         "region_us": region[-1]["median_us"],
                         "region_tflops": 2.0 * M * N * K / (region[-1]["median_us"] * 1e-6) / 1e12,
+                        "sustained_dist": sustained[-1],
                         "plan": L.gemm_plan(M, (N,), n_cb)}
     log(f"vocab gemm M=512: {ms * 1e3:.1f} us {out['gemm_m512']['tflops']:.0f} TFLOP/s")
     del ym
@@ -705,7 +713,7 @@ def bench_vocab(torch, L, args):
                                                L.ptr(bas), L.ptr(sca), K, N, n_cb, L.ptr(rows), st)), 20)
     rd, wr = 512 * n_cb * 30, 512 * K * 2
     out["embed"] = {"ids": 512, "us": ms * 1e3, "gbs": (rd + wr) / (ms * 1e-3) / 1e9, "us_dist": dist[-1],
-                    "region_us": region[-1]["median_us"]}
+                    "region_us": region[-1]["median_us"], "sustained_dist": sustained[-1]}
     log(f"vocab embed 512 ids: {ms * 1e3:.1f} us")
     return out
 
