@@ -111,14 +111,16 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="", help="restrict to one part: gemv|prefill|vocab|container|quantizer|e2e|copy|"
-                    "library|gemm-one|timeline|readbw|handoff (copy: the 512 MiB device copy that calibrates the HBM byte "
+                    "library|gemm-one|timeline|attn-timeline|readbw|handoff (copy: the 512 MiB device copy that calibrates the HBM byte "
                     "counters; library: torch's fp16 GEMM/GEMV and the copy on the layer's shapes; gemm-one: "
                     "--iters calls of one prefill shape, the counter workload; timeline: per-wave phases of the "
-                    "decode step's GEMV launches from an instrumented build; readbw: the streaming-read rate of "
+                    "decode step's GEMV launches from an instrumented build; attn-timeline: per-tile phases of the prompt "
+                    "attention (--attn-t rows) from an instrumented build; readbw: the streaming-read rate of "
                     "the GPU, a 4 GiB buffer read by a hipcc-built probe; handoff: an in-kernel producer-to-consumer "
                     "handoff against a second launch, a hipcc-built probe)")
     ap.add_argument("--no-library", action="store_true", help="skip the same-run library baseline")
     ap.add_argument("--timeline-tokens", type=int, default=4, help="timeline: tokens generated per run")
+    ap.add_argument("--attn-t", type=int, default=512, help="attn-timeline: prompt rows")
     ap.add_argument("--shape", default="gate_proj", help="gemm-one: layer shape name")
     ap.add_argument("--m", type=int, default=2048, help="gemm-one: rows of X")
     ap.add_argument("--iters", type=int, default=200,
@@ -964,15 +966,17 @@ def timeline_instrument(src):
     return src
 
 
-def timeline_build(L, out_dir):
-    """libsx8_hip.so with the instrumented GEMV source, in out_dir."""
-    src = timeline_instrument(open(os.path.join(L.CSRC_DIR, "sx8_gemv.hip")).read())
-    gemv = os.path.join(out_dir, "sx8_gemv_ts.hip")
+def timeline_build(L, out_dir, source="sx8_gemv.hip", instrument=None):
+    """libsx8_hip.so in out_dir with `source` replaced by its instrumented copy (the GEMV's
+    timeline stamps unless `instrument` is given)."""
+    instrument = instrument or timeline_instrument
+    src = instrument(open(os.path.join(L.CSRC_DIR, source)).read())
+    gemv = os.path.join(out_dir, source.replace(".hip", "_ts.hip"))
     open(gemv, "w").write(src)
     flags = [f for f in L.HIP_FLAGS if f != "-shared"]
 
     def cc(name):
-        path = gemv if name == "sx8_gemv.hip" else os.path.join(L.CSRC_DIR, name)
+        path = gemv if name == source else os.path.join(L.CSRC_DIR, name)
         obj = os.path.join(out_dir, name + ".o")
         r = subprocess.run([L.HIPCC, *flags, *L.SOURCE_FLAGS.get(name, []), "-I", L.CSRC_DIR, "-I",
                             L.INCLUDE_DIR, "-c", "-o", obj, path], capture_output=True, text=True)
@@ -1041,6 +1045,129 @@ def bench_timeline(args):
         a = np.median(np.array(v), axis=0)
         print(f"{key:44s} n={len(v):4d} span {a[0]:6.2f} us | " + " ".join(f"{x:.0f}" for x in a[1:10]) +
               f" | {a[10]:.2f} {a[11]:.2f}")
+
+
+# ------------------------------------------------------------------ prompt-attention timeline
+# bench.py --only attn-timeline [--attn-t T]: an instrumented copy of sx8_decoder.hip (built
+# into a temporary directory, anchored on the source text; it refuses to run if the kernel
+# moved) in which wave 0 of every k_attn_prefill work-group stamps the shader clock
+# (s_memtime).  The packed prompt attention of 32/8 heads of 128 over T rows (synthetic
+# fp16 q, K, V; random o-projection basis and scales) runs a few times; per query tile the
+# median work-group's phases, shader cycles:
+#   issue        entry -> query, block 0 and the first ring slot requested
+#   stage0       -> block 0 staged (its loads waited for)
+#   bar0         -> the first barrier passed (the slowest wave's block 0)
+#   step0        -> step 0's barrier (query exchange, the second slot's request, step 0)
+#   steps1..     -> the last step's barrier
+#   ->merge-bar  -> the merge barrier
+#   merge+emit   -> the end (the sets' merge and the packed operands' stores)
+ATL_HEADER = r"""
+__device__ unsigned long long g_rec[65536 * 16];
+__device__ unsigned int g_tick;
+#define TSN() ({ __builtin_amdgcn_sched_barrier(0); unsigned long long _t = __builtin_amdgcn_s_memtime(); __builtin_amdgcn_sched_barrier(0); _t; })
+extern "C" int sx8x_ts_reset() { unsigned int z = 0; return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_tick), &z, 4); }
+extern "C" int sx8x_ts_read(void* dst, size_t n, unsigned* tick) {
+    int r = (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_rec), n);
+    if (r) return r;
+    return (int)hipMemcpyFromSymbol(tick, HIP_SYMBOL(g_tick), 4);
+}
+"""
+
+
+def attn_timeline_instrument(src):
+    """sx8_decoder.hip with k_attn_prefill's timeline stamps inserted (asserts every anchor)."""
+    def sub(old, new, count=1):
+        nonlocal src
+        if src.count(old) != count:
+            raise SystemExit(f"attn-timeline: anchor found {src.count(old)} times, expected {count}: {old[:70]!r}")
+        src = src.replace(old, new)
+
+    sub("constexpr int kApVRow = 40;", ATL_HEADER + "constexpr int kApVRow = 40;")
+    sub("    __shared__ __align__(16) unsigned char lds[Lds::kBytes];\n",
+        "    __shared__ __align__(16) unsigned char lds[Lds::kBytes];\n"
+        "    unsigned long long t0 = TSN(), t1 = 0, t2 = 0, t3 = 0, t4 = 0, t5 = 0, t6 = 0, t7 = 0;\n")
+    sub("        stage(0, k0, v0);                        // (a set past the tile's blocks: zeros, unused)\n",
+        "        t6 = TSN();\n        stage(0, k0, v0);\n        t7 = TSN();\n")
+    sub("            aps[min(tid, GW * NT - 1)] = spre;\n        }\n        __syncthreads();\n",
+        "            aps[min(tid, GW * NT - 1)] = spre;\n        }\n        __syncthreads();\n        t1 = TSN();\n")
+    sub("        __syncthreads();      // step j + 1 staged; step j's buffers free for step j + 2\n    };\n",
+        "        __syncthreads();      // step j + 1 staged; step j's buffers free for step j + 2\n"
+        "        { const unsigned long long tt = TSN(); if (j == 0) t2 = tt; if (j == nstep - 1) t3 = tt; }\n    };\n")
+    sub("    __syncthreads();\n    if (!kPack && qi >= T) return;\n    // set t's state",
+        "    __syncthreads();\n    t4 = TSN();\n    if (!kPack && qi >= T) return;\n    // set t's state")
+    sub("            v[r] = acc;\n        }\n        emit(n, v);\n    }\n}\n",
+        "            v[r] = acc;\n        }\n        emit(n, v);\n    }\n"
+        "    t5 = TSN();\n"
+        "    if (tid < 64) {\n        unsigned tk = 0;\n        if (tid == 0) tk = atomicAdd(&g_tick, 1u);\n"
+        "        tk = __builtin_amdgcn_readfirstlane(tk);\n        if (tid == 0 && tk < 65536) {\n"
+        "            unsigned long long* o = g_rec + (size_t)tk * 16;\n"
+        "            o[0] = t0; o[1] = t1; o[2] = t2; o[3] = t3; o[4] = t4; o[5] = t5; o[6] = t6; o[7] = t7;\n"
+        "            o[8] = blockIdx.x; o[9] = blockIdx.y; o[10] = nstep; o[11] = NS;\n"
+        "        }\n    }\n}\n")
+    return src
+
+
+def bench_attn_timeline(args):
+    """--only attn-timeline: per-tile phases of the packed prompt attention (the comment block above)."""
+    import ctypes
+    import math
+    import tempfile
+    import _sx8lib as L
+    T = args.attn_t
+    with tempfile.TemporaryDirectory() as d:
+        lib = timeline_build(L, d, "sx8_decoder.hip", attn_timeline_instrument)
+        print("built", lib, flush=True)
+        os.environ["SX8_HIP_LIB"] = lib
+        import torch
+        L.lib()
+        raw = ctypes.CDLL(L.lib_path())
+        raw.sx8x_ts_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        cuda = torch.device("cuda")
+        st = L.stream(cuda)
+        P = L.ptr
+        nh, nk, hd, Lc = 32, 8, 128, max(2048, T)
+        n_cb = nh * hd // 32
+        g = torch.Generator(device="cpu").manual_seed(5)
+        q = torch.randn(T, nh, hd, generator=g).half().to(cuda)
+        kc = torch.randn(nk, Lc, hd, generator=g).half().to(cuda)
+        vc = torch.randn(nk, Lc, hd, generator=g).half().to(cuda)
+        bas = (torch.randn(n_cb, 2, 32, generator=g) * 0.1).to(cuda)
+        sca = torch.rand(n_cb, 2, generator=g).to(cuda)
+        Xp = torch.empty((T + 31) // 32 * n_cb * 1024, dtype=torch.int16, device=cuda)
+        Zhl = torch.empty(T * n_cb * 4, dtype=torch.int16, device=cuda)
+
+        def run():
+            L.call("sx8_dec_attn_prefill_packed", P(q), P(kc), P(vc), T, 0, nh, nk, hd, Lc, 1.0 / math.sqrt(hd),
+                   P(bas), P(sca), P(Xp), P(Zhl), st)
+
+        for _ in range(20):
+            run()
+        torch.cuda.synchronize()
+        names = ["issue", "stage0", "bar0", "step0", "steps1..", "->merge-bar", "merge+emit", "total"]
+        rows = []
+        for _ in range(3):
+            run()
+            run()
+            torch.cuda.synchronize()
+            raw.sx8x_ts_reset()
+            run()
+            torch.cuda.synchronize()
+            buf = np.zeros(65536 * 16, dtype=np.uint64)
+            tick = ctypes.c_uint()
+            assert raw.sx8x_ts_read(buf.ctypes.data, buf.nbytes, ctypes.byref(tick)) == 0
+            r = buf[:tick.value * 16].reshape(-1, 16).astype(np.int64)
+            multi = r[:, 10] > 1
+            last = np.where(multi, r[:, 3], r[:, 2])
+            rows.append(np.stack([r[:, 8], r[:, 10], r[:, 6] - r[:, 0], r[:, 7] - r[:, 6], r[:, 1] - r[:, 7],
+                                  r[:, 2] - r[:, 1], np.where(multi, r[:, 3] - r[:, 2], 0), r[:, 4] - last,
+                                  r[:, 5] - r[:, 4], r[:, 5] - r[:, 0]], 1))
+        a = np.concatenate(rows)
+        print(f"T {T}: {len(a) // 3} work-groups per call, 3 calls; median work-group per query tile, wave 0, "
+              f"shader cycles: " + " | ".join(names))
+        for tile in sorted(set(a[:, 0].tolist())):
+            sel = a[a[:, 0] == tile]
+            print(f"tile {tile:3d} steps {int(sel[0, 1])}: " + " ".join(f"{np.median(sel[:, i]):7.0f}"
+                                                                   for i in range(2, 10)), flush=True)
 
 
 # ------------------------------------------------------------------ read ceiling
@@ -1406,6 +1533,9 @@ def main():
         sys.exit(1)
     if args.only == "timeline":
         bench_timeline(args)                               # loads its own instrumented build
+        return
+    if args.only == "attn-timeline":
+        bench_attn_timeline(args)                          # loads its own instrumented build
         return
     if args.only == "readbw":
         print(json.dumps({"readbw": bench_readbw()}), flush=True)   # a child process of its own
