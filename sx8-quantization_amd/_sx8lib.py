@@ -32,8 +32,11 @@ HIP_FLAGS = [
 ]
 
 # Per-source extra flags: the GEMV kernels take their leading arguments (matrix pointers,
-# N, n_cb) preloaded into SGPRs at wave launch (8 arguments = 14 SGPRs).
-SOURCE_FLAGS = {"sx8_gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"]}
+# N, n_cb) preloaded into SGPRs at wave launch (8 arguments = 14 SGPRs); so do the decoder
+# kernels (as many of their first eight arguments as fit: the decode attention gets its
+# cache pointers and the position pointer without a kernel-argument load).
+_PRELOAD8 = ["-mllvm", "-amdgpu-kernarg-preload-count=8"]
+SOURCE_FLAGS = {"sx8_gemv.hip": _PRELOAD8, "sx8_decoder.hip": _PRELOAD8}
 
 # (name, restype, argtypes) for every exported symbol of include/sx8_hip.h
 _P = ctypes.c_void_p
