@@ -74,34 +74,58 @@ __device__ __forceinline__ float4 h4f(uint2 v) {
 // NP > 0: delta is the first K range of a split GEMM whose other NP ranges' partial products
 // sit at parts + s * slice (same row-major layout); each element is delta + part 0 + ... +
 // part NP-1 in that order (the split-K sum of the GEMM, bit for bit) before it is added.
+// One form per (init, delta) pair, with every load of the row (all rounds u, the delta and
+// its partial slices) issued before the first sum: a null-pointer test inside the round loop
+// became a branch per round, after which the compiler waited for all of that round's loads
+// before issuing the next round's, one memory round trip per round.
+template <int NP, bool kInit, bool kDelta>
+__device__ __forceinline__ void rms_row_load_t(float4 (&v)[kRmsPer4], uint2 (&wv)[kRmsPer4], const float* resid,
+                                               const float* delta, const uint16_t* init, const uint16_t* w,
+                                               const float* parts, int64_t slice, int64_t base, int H4, int t) {
+    constexpr int kP = kDelta ? NP : 0;
+    const float4* r4 = reinterpret_cast<const float4*>(resid + base);
+    const float4* d4 = reinterpret_cast<const float4*>(delta + (kDelta ? base : 0));
+    const uint2* i4 = reinterpret_cast<const uint2*>(init + (kInit ? base : 0));
+    const uint2* w4 = reinterpret_cast<const uint2*>(w);
+    uint2 hi[kInit ? kRmsPer4 : 1];
+    float4 x0[kRmsPer4], dd[kDelta ? kRmsPer4 : 1], pv[kRmsPer4][kP > 0 ? kP : 1];
+#pragma unroll
+    for (int u = 0; u < kRmsPer4; ++u) {       // every load of the row before the reduction
+        const int ic = min(t + 256 * u, H4 - 1);
+        if constexpr (kInit) hi[u] = i4[ic];
+        else x0[u] = r4[ic];
+        if constexpr (kDelta) {
+            dd[u] = d4[ic];
+#pragma unroll
+            for (int s2 = 0; s2 < kP; ++s2) pv[u][s2] = reinterpret_cast<const float4*>(parts + s2 * slice + base)[ic];
+        }
+        wv[u] = w4[ic];
+    }
+#pragma unroll
+    for (int u = 0; u < kRmsPer4; ++u) {
+        const int i = t + 256 * u;
+        float4 x = kInit ? h4f(hi[u]) : x0[u];
+        if constexpr (kDelta) {
+            float4 d = dd[u];
+#pragma unroll
+            for (int s2 = 0; s2 < kP; ++s2)
+                d = make_float4(d.x + pv[u][s2].x, d.y + pv[u][s2].y, d.z + pv[u][s2].z, d.w + pv[u][s2].w);
+            x = make_float4(x.x + d.x, x.y + d.y, x.z + d.z, x.w + d.w);
+        }
+        v[u] = i < H4 ? x : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
 template <int NP>
 __device__ __forceinline__ void rms_row_load(float4 (&v)[kRmsPer4], uint2 (&wv)[kRmsPer4], const float* resid,
                                              const float* delta, const uint16_t* init, const uint16_t* w,
                                              const float* parts, int64_t slice, int64_t base, int H4, int t) {
-    const float4* r4 = reinterpret_cast<const float4*>(resid + base);
-    const float4* d4 = reinterpret_cast<const float4*>(delta + (delta ? base : 0));
-    const uint2* i4 = reinterpret_cast<const uint2*>(init + (init ? base : 0));
-    const uint2* w4 = reinterpret_cast<const uint2*>(w);
-#pragma unroll
-    for (int u = 0; u < kRmsPer4; ++u) {       // every load of the row before the reduction
-        const int i = t + 256 * u;
-        const int ic = min(i, H4 - 1);
-        float4 x = init ? h4f(i4[ic]) : r4[ic];
-        if (delta) {
-            float4 dd = d4[ic];
-            if constexpr (NP > 0) {
-                float4 pv[NP];
-#pragma unroll
-                for (int s2 = 0; s2 < NP; ++s2)
-                    pv[s2] = reinterpret_cast<const float4*>(parts + s2 * slice + base)[ic];
-#pragma unroll
-                for (int s2 = 0; s2 < NP; ++s2)
-                    dd = make_float4(dd.x + pv[s2].x, dd.y + pv[s2].y, dd.z + pv[s2].z, dd.w + pv[s2].w);
-            }
-            x = make_float4(x.x + dd.x, x.y + dd.y, x.z + dd.z, x.w + dd.w);
-        }
-        v[u] = i < H4 ? x : make_float4(0.f, 0.f, 0.f, 0.f);
-        wv[u] = w4[ic];
+    if (init) {
+        if (delta) rms_row_load_t<NP, true, true>(v, wv, resid, delta, init, w, parts, slice, base, H4, t);
+        else rms_row_load_t<NP, true, false>(v, wv, resid, delta, init, w, parts, slice, base, H4, t);
+    } else {
+        if (delta) rms_row_load_t<NP, false, true>(v, wv, resid, delta, init, w, parts, slice, base, H4, t);
+        else rms_row_load_t<NP, false, false>(v, wv, resid, delta, init, w, parts, slice, base, H4, t);
     }
 }
 
@@ -232,7 +256,11 @@ __global__ __launch_bounds__(256 * kPackRows) void k_add_rmsnorm_pack(float* __r
                                                                      float eps, const float* __restrict__ parts,
                                                                      int64_t slice, const NormPack pk) {
     __shared__ float red[kPackRows][4];
-    __shared__ __align__(16) float xs[kPackRows][256 * 4 * kRmsPer4];
+    // x in LDS, K block kb at 36 kb (4 floats of padding per block): phase 2 reads 32
+    // consecutive floats per lane with the K block varying across lanes, which at a
+    // 32-float stride would put every lane's 16-byte reads on the same banks
+    constexpr int kXsStride = 36;
+    __shared__ __align__(16) float xs[kPackRows][256 * 4 * kRmsPer4 / 32 * kXsStride];
     const int rl = threadIdx.x >> 8, t = threadIdx.x & 255;
     const int row = blockIdx.x * kPackRows + rl;
     const int H4 = H >> 2;
@@ -280,7 +308,7 @@ __global__ __launch_bounds__(256 * kPackRows) void k_add_rmsnorm_pack(float* __r
             lo = (uint32_t)f2h(rms_scale(v[u].x, inv, wf.x)) | ((uint32_t)f2h(rms_scale(v[u].y, inv, wf.y)) << 16);
             hi = (uint32_t)f2h(rms_scale(v[u].z, inv, wf.z)) | ((uint32_t)f2h(rms_scale(v[u].w, inv, wf.w)) << 16);
         }
-        *reinterpret_cast<float4*>(&xs[rl][4 * i]) = h4f(make_uint2(lo, hi));
+        *reinterpret_cast<float4*>(&xs[rl][kXsStride * (i >> 3) + 4 * (i & 7)]) = h4f(make_uint2(lo, hi));
         // element 4 i of the row: K block kb, chunk (hf, st), offset 0 or 4 within it
         const int e0 = 4 * i, kb = e0 >> 5, tt = e0 & 31;
         *reinterpret_cast<uint2*>(pk.Xp + (((int64_t)G * n_cb + kb) * 2 + ((tt >> 3) & 1)) * 512 +
@@ -313,7 +341,7 @@ __global__ __launch_bounds__(256 * kPackRows) void k_add_rmsnorm_pack(float* __r
         for (int rr = 0; rr < kPackRows; ++rr) {
             const int row2 = blockIdx.x * kPackRows + rr;
             if (row2 >= M) break;
-            const float* x = &xs[rr][32 * kb];
+            const float* x = &xs[rr][kXsStride * kb];
             float p[16];
 #pragma unroll
             for (int q = 0; q < 16; ++q) p[q] = x[q] * b[q] + x[q + 16] * b[q + 16];
