@@ -152,6 +152,8 @@ def test_add_rmsnorm_and_silu_mul(hiplib, cuda):
     (2, 4096, False, True, 0),    # four-wide, the longest such row
     (2, 2562, True, False, 0),    # H % 4 != 0: one value per load
     (2, 2560, False, True, 1),    # a residual one float past 16-byte alignment
+    (2, 2560, True, False, 0),    # four-wide, the fp16 rows alone
+    (3, 1024, False, False, 0),   # four-wide, the residual alone
     (2, 5000, True, True, 0),     # longer than the unrolled forms hold
     (1, 7, False, False, 0),      # a row shorter than a wave
 ])
@@ -1086,6 +1088,8 @@ def test_gateup_silu_packed_operands(hiplib, cuda, monkeypatch, M, K, N, hb):
     (512, 2560, 2, 3, "delta"),     # gate/up's producer: o's 3 slices
     (77, 640, 1, 0, "init"),        # layer 0 (fp16 init, no delta), ragged rows
     (33, 4096, 4, 1, "delta"),      # the widest row, four matrices
+    (64, 2560, 2, 2, "both"),       # fp16 init plus delta and its slices
+    (40, 1024, 3, 0, "none"),       # the residual alone
 ])
 def test_add_rmsnorm_packed_operands(hiplib, cuda, M, H, n_mats, np_, form):
     """sx8_dec_add_rmsnorm_packed writes the residual of sx8_dec_add_rmsnorm_parts and the
@@ -1106,7 +1110,8 @@ def test_add_rmsnorm_packed_operands(hiplib, cuda, M, H, n_mats, np_, form):
     parts = torch.randn(max(np_, 1), M * H + 8, generator=g).to(cuda)
     slc = M * H + 8                                             # a slice longer than the rows
     w = (torch.rand(H, generator=g) + 0.5).half().to(cuda)
-    d_arg, i_arg = (P(delta), None) if form == "delta" else (None, P(init))
+    d_arg = P(delta) if form in ("delta", "both") else None
+    i_arg = P(init) if form in ("init", "both") else None
     pp = P(parts) if np_ else None
     print("rmsnorm packed", M, H, n_mats, np_, form, flush=True)
     ra, xa = resid0.clone(), torch.empty(M, H, dtype=torch.float16, device=cuda)
